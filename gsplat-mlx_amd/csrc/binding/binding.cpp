@@ -1,0 +1,271 @@
+// Python module `_gsplat_core`: the reference binding's surface
+// (gsplat_core/binding/binding.cpp:447-534) -- same function names, dict
+// inputs, keyword defaults, output dict keys and "missing optional key ->
+// empty array" convention -- over torch tensors on a ROCm device. Built
+// with pybind11 (nanobind is not available in this toolchain).
+#include <torch/extension.h>
+
+#include <stdexcept>
+#include <string>
+#include <unordered_map>
+
+#include "gsplat_core.h"
+
+namespace py = pybind11;
+using TensorMap = std::unordered_map<std::string, at::Tensor>;
+
+namespace {
+
+// binding.cpp:26-35
+const at::Tensor& require_key(const TensorMap& inputs, const char* key) {
+  auto it = inputs.find(key);
+  if (it == inputs.end()) throw std::runtime_error(std::string("gsplat_core binding missing input: ") + key);
+  return it->second;
+}
+
+// binding.cpp:37-45: absent optional input -> empty float32 array
+at::Tensor get_or_empty(const TensorMap& inputs, const char* key) {
+  auto it = inputs.find(key);
+  if (it == inputs.end()) return at::empty({0}, at::TensorOptions().dtype(at::kFloat));
+  return it->second;
+}
+
+py::dict projection_ewa_3dgs_fused_forward(const TensorMap& inputs, int image_width, int image_height, float eps2d,
+                                           float near_plane, float far_plane, float radius_clip,
+                                           bool calc_compensations, int camera_model) {
+  gsplat_core::ProjectionEWA3DGSFusedInput in;
+  in.means = require_key(inputs, "means");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.covars = get_or_empty(inputs, "covars");
+  in.quats = get_or_empty(inputs, "quats");
+  in.scales = get_or_empty(inputs, "scales");
+  in.opacities = get_or_empty(inputs, "opacities");
+  in.viewspace_points = get_or_empty(inputs, "viewspace_points");
+  in.params = {image_width, image_height, eps2d, near_plane, far_plane, radius_clip, calc_compensations,
+               camera_model, in.covars.numel() != 0, in.opacities.numel() != 0};
+  auto out = gsplat_core::gsplat_projection_ewa_3dgs_fused(in);
+  py::dict r;
+  r["radii"] = out[gsplat_core::kRadii];
+  r["means2d"] = out[gsplat_core::kMeans2D];
+  r["depths"] = out[gsplat_core::kDepths];
+  r["conics"] = out[gsplat_core::kConics];
+  r["compensations"] = out[gsplat_core::kCompensations];
+  r["viewspace_points"] = in.viewspace_points;
+  return r;
+}
+
+// binding.cpp:119-186. The reference evaluates this entry point on the CPU;
+// here it runs the GPU kernel with the same fixed parameters.
+py::dict projection_ewa_3dgs_fused_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
+                                            const TensorMap& cotangents, int image_width, int image_height,
+                                            float eps2d, int camera_model, bool viewmats_requires_grad) {
+  gsplat_core::ProjectionEWA3DGSFusedBackwardInput in;
+  in.means = require_key(inputs, "means");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.covars = get_or_empty(inputs, "covars");
+  in.quats = get_or_empty(inputs, "quats");
+  in.scales = get_or_empty(inputs, "scales");
+  in.radii = require_key(forward_outputs, "radii");
+  in.conics = require_key(forward_outputs, "conics");
+  in.compensations = get_or_empty(forward_outputs, "compensations");
+  in.v_means2d = require_key(cotangents, "v_means2d");
+  in.v_depths = require_key(cotangents, "v_depths");
+  in.v_conics = require_key(cotangents, "v_conics");
+  in.v_compensations = get_or_empty(cotangents, "v_compensations");
+  const bool use_covars = in.covars.numel() != 0;
+  in.params = {image_width, image_height, eps2d, -1.0e20f, 1.0e20f, 0.0f, in.compensations.numel() != 0,
+               camera_model, use_covars, false};
+  in.viewmats_requires_grad = viewmats_requires_grad;
+  auto out = gsplat_core::gsplat_projection_ewa_3dgs_fused_backward(in);
+  py::dict r;
+  r["v_means"] = out[gsplat_core::kProjectionVMeans];
+  if (use_covars) {
+    r["v_covars"] = out[gsplat_core::kProjectionVCovars];
+  } else {
+    r["v_quats"] = out[gsplat_core::kProjectionVQuats];
+    r["v_scales"] = out[gsplat_core::kProjectionVScales];
+  }
+  if (viewmats_requires_grad) r["v_viewmats"] = out[gsplat_core::kProjectionVViewmats];
+  return r;
+}
+
+py::dict intersect_tile_forward(const TensorMap& inputs, int I, int tile_size, int tile_width, int tile_height,
+                                bool sort, bool segmented) {
+  gsplat_core::IntersectTileInput in;
+  in.means2d = require_key(inputs, "means2d");
+  in.radii = require_key(inputs, "radii");
+  in.depths = require_key(inputs, "depths");
+  in.conics = get_or_empty(inputs, "conics");
+  in.opacities = get_or_empty(inputs, "opacities");
+  in.image_ids = get_or_empty(inputs, "image_ids");
+  in.gaussian_ids = get_or_empty(inputs, "gaussian_ids");
+  in.params = {I,
+               tile_size,
+               tile_width,
+               tile_height,
+               sort,
+               segmented,
+               in.image_ids.numel() != 0 || in.gaussian_ids.numel() != 0,
+               in.conics.numel() != 0,
+               in.opacities.numel() != 0};
+  auto out = gsplat_core::gsplat_intersect_tile(in);
+  py::dict r;
+  r["tiles_per_gauss"] = out[gsplat_core::kTilesPerGauss];
+  r["isect_ids"] = out[gsplat_core::kIsectIds];
+  r["flatten_ids"] = out[gsplat_core::kFlattenIds];
+  return r;
+}
+
+at::Tensor intersect_offset_forward(const at::Tensor& isect_ids, int I, int tile_width, int tile_height) {
+  return gsplat_core::gsplat_intersect_offset(isect_ids, I, tile_width, tile_height);
+}
+
+py::dict rasterize_to_pixels_3dgs_forward(const TensorMap& inputs, int image_width, int image_height, int tile_size) {
+  gsplat_core::RasterizeToPixels3DGSInput in;
+  in.means2d = require_key(inputs, "means2d");
+  in.conics = require_key(inputs, "conics");
+  in.colors = require_key(inputs, "colors");
+  in.opacities = require_key(inputs, "opacities");
+  in.tile_offsets = require_key(inputs, "tile_offsets");
+  in.flatten_ids = require_key(inputs, "flatten_ids");
+  in.backgrounds = get_or_empty(inputs, "backgrounds");
+  in.masks = get_or_empty(inputs, "masks");
+  in.params = {image_width, image_height, tile_size, in.backgrounds.numel() != 0, in.masks.numel() != 0,
+               in.means2d.dim() == 2};
+  auto out = gsplat_core::gsplat_rasterize_to_pixels_3dgs(in);
+  py::dict r;
+  r["render_colors"] = out[gsplat_core::kRenderColors];
+  r["render_alphas"] = out[gsplat_core::kRenderAlphas];
+  r["last_ids"] = out[gsplat_core::kLastIds];
+  return r;
+}
+
+py::dict rasterize_to_pixels_3dgs_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
+                                           const TensorMap& cotangents, int image_width, int image_height,
+                                           int tile_size, bool absgrad) {
+  gsplat_core::RasterizeToPixels3DGSBackwardInput in;
+  in.means2d = require_key(inputs, "means2d");
+  in.conics = require_key(inputs, "conics");
+  in.colors = require_key(inputs, "colors");
+  in.opacities = require_key(inputs, "opacities");
+  in.tile_offsets = require_key(inputs, "tile_offsets");
+  in.flatten_ids = require_key(inputs, "flatten_ids");
+  in.render_alphas = require_key(forward_outputs, "render_alphas");
+  in.last_ids = require_key(forward_outputs, "last_ids");
+  in.v_render_colors = require_key(cotangents, "v_render_colors");
+  in.v_render_alphas = require_key(cotangents, "v_render_alphas");
+  in.backgrounds = get_or_empty(inputs, "backgrounds");
+  in.masks = get_or_empty(inputs, "masks");
+  in.params = {image_width, image_height, tile_size, in.backgrounds.numel() != 0, in.masks.numel() != 0,
+               in.means2d.dim() == 2};
+  in.absgrad = absgrad;
+  auto out = gsplat_core::gsplat_rasterize_to_pixels_3dgs_backward(in);
+  py::dict r;
+  if (absgrad) r["v_means2d_abs"] = out[gsplat_core::kRasterVMeans2DAbs];
+  r["v_means2d"] = out[gsplat_core::kRasterVMeans2D];
+  r["v_conics"] = out[gsplat_core::kRasterVConics];
+  r["v_colors"] = out[gsplat_core::kRasterVColors];
+  r["v_opacities"] = out[gsplat_core::kRasterVOpacities];
+  if (in.backgrounds.numel() != 0) r["v_backgrounds"] = out[gsplat_core::kRasterVBackgrounds];
+  return r;
+}
+
+at::Tensor spherical_harmonics_forward(int degrees_to_use, const TensorMap& inputs) {
+  gsplat_core::SphericalHarmonicsInput in;
+  in.degrees_to_use = degrees_to_use;
+  in.dirs = require_key(inputs, "dirs");
+  in.coeffs = require_key(inputs, "coeffs");
+  in.masks = get_or_empty(inputs, "masks");
+  in.use_masks = in.masks.numel() != 0;
+  return gsplat_core::gsplat_spherical_harmonics_forward(in);
+}
+
+py::dict spherical_harmonics_backward(int degrees_to_use, const TensorMap& inputs, const TensorMap& cotangents,
+                                      bool compute_v_dirs) {
+  gsplat_core::SphericalHarmonicsBackwardInput in;
+  in.degrees_to_use = degrees_to_use;
+  in.dirs = require_key(inputs, "dirs");
+  in.coeffs = require_key(inputs, "coeffs");
+  in.v_colors = require_key(cotangents, "v_colors");
+  in.masks = get_or_empty(inputs, "masks");
+  in.use_masks = in.masks.numel() != 0;
+  in.compute_v_dirs = compute_v_dirs;
+  auto out = gsplat_core::gsplat_spherical_harmonics_backward(in);
+  py::dict r;
+  if (compute_v_dirs) r["v_dirs"] = out[gsplat_core::kSHVDirs];
+  r["v_coeffs"] = out[gsplat_core::kSHVCoeffs];
+  return r;
+}
+
+py::dict quat_scale_to_covar_preci_forward(const TensorMap& inputs, bool compute_covar, bool compute_preci,
+                                           bool triu) {
+  gsplat_core::QuatScaleToCovarPreciInput in;
+  in.quats = require_key(inputs, "quats");
+  in.scales = require_key(inputs, "scales");
+  in.compute_covar = compute_covar;
+  in.compute_preci = compute_preci;
+  in.triu = triu;
+  auto out = gsplat_core::gsplat_quat_scale_to_covar_preci_forward(in);
+  py::dict r;
+  r["covars"] = out[gsplat_core::kCovars];
+  r["precis"] = out[gsplat_core::kPrecis];
+  return r;
+}
+
+py::dict quat_scale_to_covar_preci_backward(const TensorMap& inputs, const TensorMap& cotangents, bool triu) {
+  gsplat_core::QuatScaleToCovarPreciBackwardInput in;
+  in.quats = require_key(inputs, "quats");
+  in.scales = require_key(inputs, "scales");
+  in.v_covars = get_or_empty(cotangents, "v_covars");
+  in.v_precis = get_or_empty(cotangents, "v_precis");
+  in.triu = triu;
+  in.use_v_covars = in.v_covars.numel() != 0;
+  in.use_v_precis = in.v_precis.numel() != 0;
+  auto out = gsplat_core::gsplat_quat_scale_to_covar_preci_backward(in);
+  py::dict r;
+  r["v_quats"] = out[gsplat_core::kVQuats];
+  r["v_scales"] = out[gsplat_core::kVScales];
+  return r;
+}
+
+// Template smoke entries of the reference (gsplat_core/dummy.cpp:7-13).
+int dummy_add(int a, int b) { return a + b; }
+
+at::Tensor dummy_array_add(const py::dict& inputs) {
+  if (!inputs.contains("a") || !inputs.contains("b"))
+    throw std::runtime_error("dummy_array_add input is not an array: a/b");
+  return inputs["a"].cast<at::Tensor>() + inputs["b"].cast<at::Tensor>();
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_gsplat_core, m) {
+  m.doc() = "MI355X (gfx950) splatting operator chain with the gsplat_core binding surface.";
+  m.def("dummy_add", &dummy_add, py::arg("a"), py::arg("b"));
+  m.def("dummy_array_add", &dummy_array_add, py::arg("inputs"));
+  m.def("projection_ewa_3dgs_fused_forward", &projection_ewa_3dgs_fused_forward, py::arg("inputs"),
+        py::arg("image_width"), py::arg("image_height"), py::arg("eps2d") = 0.3f, py::arg("near_plane") = 0.01f,
+        py::arg("far_plane") = 1.0e10f, py::arg("radius_clip") = 0.0f, py::arg("calc_compensations") = false,
+        py::arg("camera_model") = 0);
+  m.def("projection_ewa_3dgs_fused_backward", &projection_ewa_3dgs_fused_backward, py::arg("inputs"),
+        py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
+        py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
+  m.def("intersect_tile_forward", &intersect_tile_forward, py::arg("inputs"), py::arg("I"), py::arg("tile_size"),
+        py::arg("tile_width"), py::arg("tile_height"), py::arg("sort") = true, py::arg("segmented") = false);
+  m.def("intersect_offset_forward", &intersect_offset_forward, py::arg("isect_ids"), py::arg("I"),
+        py::arg("tile_width"), py::arg("tile_height"));
+  m.def("rasterize_to_pixels_3dgs_forward", &rasterize_to_pixels_3dgs_forward, py::arg("inputs"),
+        py::arg("image_width"), py::arg("image_height"), py::arg("tile_size"));
+  m.def("rasterize_to_pixels_3dgs_backward", &rasterize_to_pixels_3dgs_backward, py::arg("inputs"),
+        py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
+        py::arg("tile_size"), py::arg("absgrad") = false);
+  m.def("spherical_harmonics_forward", &spherical_harmonics_forward, py::arg("degrees_to_use"), py::arg("inputs"));
+  m.def("spherical_harmonics_backward", &spherical_harmonics_backward, py::arg("degrees_to_use"), py::arg("inputs"),
+        py::arg("cotangents"), py::arg("compute_v_dirs") = true);
+  m.def("quat_scale_to_covar_preci_forward", &quat_scale_to_covar_preci_forward, py::arg("inputs"),
+        py::arg("compute_covar") = true, py::arg("compute_preci") = true, py::arg("triu") = true);
+  m.def("quat_scale_to_covar_preci_backward", &quat_scale_to_covar_preci_backward, py::arg("inputs"),
+        py::arg("cotangents"), py::arg("triu") = true);
+}

@@ -1,0 +1,244 @@
+// Tile intersection operator layer: validation, staging and the single
+// device-to-host read of the intersection count follow
+// gsplat_core/gsplat_intersect.cpp:60-307, 586-603 of the reference; compute
+// is the HIP C-ABI (fused count+scan, encode, radix sort, offsets).
+#include "gsplat_intersect.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <limits>
+
+#include "core_util.h"
+
+namespace gsplat_core {
+namespace {
+using namespace detail;
+
+int floor_log2_plus_one(int64_t value) {
+  if (value <= 0) throw std::runtime_error("intersect expects positive image/tile counts.");
+  return static_cast<int>(std::floor(std::log2(static_cast<float>(value)))) + 1;
+}
+
+int bit_length(uint64_t v) {
+  int b = 0;
+  while (v) {
+    ++b;
+    v >>= 1;
+  }
+  return b;
+}
+
+// gsplat_intersect.cpp:114-148
+void validate_intersect_tile_input(const IntersectTileInput& input) {
+  if (input.params.packed) throw std::runtime_error("intersect_tile packed path is not implemented yet.");
+  if (input.params.segmented) throw std::runtime_error("intersect_tile segmented sort is not implemented yet.");
+  if (input.params.use_conics || input.params.use_opacities)
+    throw std::runtime_error("intersect_tile AccuTile conics/opacities path is not implemented yet.");
+  if (input.means2d.dim() < 3 || input.means2d.size(-1) != 2)
+    throw std::runtime_error("means2d must have shape [..., N, 2].");
+  if (input.radii.dim() != input.means2d.dim() || input.radii.size(-1) != 2)
+    throw std::runtime_error("radii must have shape [..., N, 2].");
+  if (input.depths.dim() + 1 != input.means2d.dim()) throw std::runtime_error("depths must have shape [..., N].");
+  if (input.means2d.scalar_type() != at::kFloat || input.radii.scalar_type() != at::kInt ||
+      input.depths.scalar_type() != at::kFloat)
+    throw std::runtime_error("intersect_tile dense path expects float32 means2d/depths and int32 radii.");
+  require_device(input.means2d, "means2d");
+  require_device(input.radii, "radii");
+  require_device(input.depths, "depths");
+}
+
+void check_dense_size(const IntersectTileInput& input, const char* op) {
+  const int64_t n = input.means2d.size(-2);
+  const int64_t numel = input.depths.numel();
+  const int64_t I = input.params.I;
+  if (I <= 0 || numel % I != 0 || numel != I * n)
+    throw std::runtime_error(std::string(op) + " dense path expects depths size to equal I * N.");
+  if (input.means2d.numel() != numel * 2 || input.radii.numel() != numel * 2)
+    throw std::runtime_error(std::string(op) + " expects means2d and radii with two values per depth.");
+}
+
+// Workspace bytes from torch's caching allocator (no synchronisation).
+array workspace(size_t bytes, const array& ref) {
+  return at::empty({static_cast<int64_t>(bytes > 0 ? bytes : 1)}, u8_like(ref));
+}
+
+struct Counted {
+  array tiles_per_gauss;
+  array offsets;
+  array total;  // int64 [1] on device
+};
+
+Counted count_and_scan(const IntersectTileInput& input, void* stream) {
+  const array means2d = contig(input.means2d);
+  const array radii = contig(input.radii);
+  const int64_t numel = input.depths.numel();
+  Counted c;
+  c.tiles_per_gauss = at::empty(input.depths.sizes(), i32_like(means2d));
+  c.offsets = at::empty(input.depths.sizes(), i32_like(means2d));
+  c.total = at::empty({1}, i64_like(means2d));
+  const size_t ws_bytes = gsplat_hip_isect_count_scan_workspace_size(numel);
+  array ws = workspace(ws_bytes, means2d);
+  check(gsplat_hip_isect_count_scan(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), numel,
+                                    input.params.tile_size, input.params.tile_width, input.params.tile_height,
+                                    c.tiles_per_gauss.data_ptr<int32_t>(), c.offsets.data_ptr<int32_t>(),
+                                    c.total.data_ptr<int64_t>(), ws.data_ptr<uint8_t>(), ws_bytes, stream));
+  return c;
+}
+
+// The one device->host read of the chain (gsplat_intersect.cpp:155-170),
+// ordered after the count/scan kernels on their stream.
+int read_total(const array& total_dev, void* stream) {
+  int64_t total = 0;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err = hipMemcpyAsync(&total, total_dev.data_ptr<int64_t>(), sizeof(int64_t), hipMemcpyDeviceToHost, s);
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  if (err != hipSuccess)
+    throw std::runtime_error(std::string("intersect_tile: reading the intersection count failed: ") +
+                             hipGetErrorString(err));
+  if (total > static_cast<int64_t>(INT32_MAX))
+    throw std::runtime_error("intersect_tile: more than 2^31-1 intersections (int32 offsets overflow).");
+  return static_cast<int>(total);
+}
+
+std::vector<array> sort_pairs(const array& keys, const array& vals, int key_bits, void* stream) {
+  const int64_t n = keys.numel();
+  array ko = at::empty({n}, keys.options());
+  array vo = at::empty({n}, vals.options());
+  if (n == 0) return {ko, vo};
+  const size_t ws_bytes = gsplat_hip_isect_sort_workspace_size(n);
+  array ws = workspace(ws_bytes, keys);
+  check(gsplat_hip_isect_sort(keys.data_ptr<int64_t>(), vals.data_ptr<int32_t>(), n, key_bits,
+                              ko.data_ptr<int64_t>(), vo.data_ptr<int32_t>(), ws.data_ptr<uint8_t>(), ws_bytes,
+                              stream));
+  return {ko, vo};
+}
+
+// Largest key the encoder can produce for I images of n_tiles tiles: the sort
+// only needs that many low bits (higher bits are zero for every key).
+int encoded_key_bits(int64_t I, int64_t n_tiles) {
+  const int tile_bits = floor_log2_plus_one(n_tiles);
+  const uint64_t max_key = (static_cast<uint64_t>(I - 1) << (32 + tile_bits)) |
+                           (static_cast<uint64_t>(n_tiles - 1) << 32) | 0xFFFFFFFFull;
+  return bit_length(max_key);
+}
+
+}  // namespace
+
+array gsplat_intersect_tile_count(const IntersectTileInput& input) {
+  validate_intersect_tile_input(input);
+  check_dense_size(input, "intersect_tile_count");
+  const c10::DeviceGuard guard(input.means2d.device());
+  return count_and_scan(input, stream_for(input.s, input.means2d)).tiles_per_gauss;
+}
+
+array gsplat_intersect_tile_offsets(const array& tiles_per_gauss, StreamOrDevice s) {
+  if (tiles_per_gauss.scalar_type() != at::kInt)
+    throw std::runtime_error("intersect_tile_offsets expects int32 tiles_per_gauss.");
+  require_device(tiles_per_gauss, "tiles_per_gauss");
+  const c10::DeviceGuard guard(tiles_per_gauss.device());
+  const array counts = contig(tiles_per_gauss);
+  array out = at::empty(counts.sizes(), counts.options());
+  const int64_t n = counts.numel();
+  const size_t ws_bytes = gsplat_hip_exclusive_scan_i32_workspace_size(n);
+  array ws = workspace(ws_bytes, counts);
+  check(gsplat_hip_exclusive_scan_i32(counts.data_ptr<int32_t>(), out.data_ptr<int32_t>(), n, nullptr,
+                                      ws.data_ptr<uint8_t>(), ws_bytes, stream_for(s, counts)));
+  return out;
+}
+
+std::vector<array> gsplat_intersect_tile_encode(const IntersectTileInput& input, const array& tile_offsets,
+                                                int total_isects) {
+  validate_intersect_tile_input(input);
+  check_dense_size(input, "intersect_tile_encode");
+  if (total_isects < 0) throw std::runtime_error("intersect_tile_encode expects non-negative total_isects.");
+  if (tile_offsets.scalar_type() != at::kInt || tile_offsets.numel() != input.depths.numel())
+    throw std::runtime_error("intersect_tile_encode expects int32 tile_offsets with depths shape.");
+  require_device(tile_offsets, "tile_offsets");
+  const int64_t n_tiles = static_cast<int64_t>(input.params.tile_width) * input.params.tile_height;
+  if (floor_log2_plus_one(input.params.I) + floor_log2_plus_one(n_tiles) > 32)
+    throw std::runtime_error("intersect_tile_encode image id and tile id require more than 32 bits.");
+  const c10::DeviceGuard guard(input.means2d.device());
+  const array means2d = contig(input.means2d);
+  const array radii = contig(input.radii);
+  const array depths = contig(input.depths);
+  const array offsets = contig(tile_offsets);
+  array ids = at::empty({total_isects}, i64_like(means2d));
+  array flat = at::empty({total_isects}, i32_like(means2d));
+  check(gsplat_hip_isect_encode(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), depths.data_ptr<float>(),
+                                offsets.data_ptr<int32_t>(), input.params.I, depths.numel(), input.params.tile_size,
+                                input.params.tile_width, input.params.tile_height, total_isects,
+                                ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(),
+                                stream_for(input.s, means2d)));
+  return {ids, flat};
+}
+
+std::vector<array> gsplat_intersect_tile_sort(const array& isect_ids, const array& flatten_ids, StreamOrDevice s) {
+  if (isect_ids.scalar_type() != at::kLong) throw std::runtime_error("intersect_tile_sort expects int64 isect_ids.");
+  if (flatten_ids.scalar_type() != at::kInt)
+    throw std::runtime_error("intersect_tile_sort expects int32 flatten_ids.");
+  if (isect_ids.dim() != 1 || flatten_ids.dim() != 1 || isect_ids.numel() != flatten_ids.numel())
+    throw std::runtime_error("intersect_tile_sort expects matching 1D isect_ids and flatten_ids.");
+  require_device(isect_ids, "isect_ids");
+  require_device(flatten_ids, "flatten_ids");
+  const c10::DeviceGuard guard(isect_ids.device());
+  const array keys = contig(isect_ids);
+  const array vals = contig(flatten_ids);
+  if (keys.numel() == 0) return {keys.clone(), vals.clone()};
+  void* stream = stream_for(s, keys);
+  // Arbitrary int64 keys: flip the sign bit so the unsigned order equals the
+  // signed order, sort the significant bits, flip back.
+  const int64_t kmin = keys.min().item<int64_t>();
+  if (kmin >= 0) {
+    const int64_t kmax = keys.max().item<int64_t>();
+    return sort_pairs(keys, vals, bit_length(static_cast<uint64_t>(kmax)), stream);
+  }
+  const array flipped = at::bitwise_xor(keys, std::numeric_limits<int64_t>::min());
+  auto out = sort_pairs(flipped, vals, 64, stream);
+  out[0] = at::bitwise_xor(out[0], std::numeric_limits<int64_t>::min());
+  return out;
+}
+
+std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& input) {
+  validate_intersect_tile_input(input);
+  check_dense_size(input, "intersect_tile");
+  const int64_t n_tiles = static_cast<int64_t>(input.params.tile_width) * input.params.tile_height;
+  if (floor_log2_plus_one(input.params.I) + floor_log2_plus_one(n_tiles) > 32)
+    throw std::runtime_error("intersect_tile_encode image id and tile id require more than 32 bits.");
+  const c10::DeviceGuard guard(input.means2d.device());
+  void* stream = stream_for(input.s, input.means2d);
+  Counted c = count_and_scan(input, stream);
+  const int total = read_total(c.total, stream);
+  const array means2d = contig(input.means2d);
+  const array radii = contig(input.radii);
+  const array depths = contig(input.depths);
+  array ids = at::empty({total}, i64_like(means2d));
+  array flat = at::empty({total}, i32_like(means2d));
+  check(gsplat_hip_isect_encode(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), depths.data_ptr<float>(),
+                                c.offsets.data_ptr<int32_t>(), input.params.I, depths.numel(),
+                                input.params.tile_size, input.params.tile_width, input.params.tile_height, total,
+                                ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), stream));
+  if (!input.params.sort) return {c.tiles_per_gauss, ids, flat};
+  auto sorted = sort_pairs(ids, flat, encoded_key_bits(input.params.I, n_tiles), stream);
+  return {c.tiles_per_gauss, sorted[0], sorted[1]};
+}
+
+std::vector<array> gsplat_intersect_tile(const IntersectTileInput& input) {
+  validate_intersect_tile_input(input);
+  return gsplat_intersect_tile_gpu_staged(input);
+}
+
+array gsplat_intersect_offset(const array& isect_ids, int I, int tile_width, int tile_height, StreamOrDevice s) {
+  if (I <= 0 || tile_width <= 0 || tile_height <= 0)
+    throw std::runtime_error("intersect_offset expects positive image and tile dimensions.");
+  if (isect_ids.scalar_type() != at::kLong) throw std::runtime_error("intersect_offset expects int64 isect_ids.");
+  require_device(isect_ids, "isect_ids");
+  const c10::DeviceGuard guard(isect_ids.device());
+  const array ids = contig(isect_ids);
+  array out = at::empty({I, tile_height, tile_width}, i32_like(ids));
+  check(gsplat_hip_isect_offset(ids.data_ptr<int64_t>(), ids.numel(), I, tile_width, tile_height,
+                                out.data_ptr<int32_t>(), stream_for(s, ids)));
+  return out;
+}
+
+}  // namespace gsplat_core

@@ -1,0 +1,200 @@
+// Fused EWA projection operator layer: validation, output shapes and the
+// empty-output conventions follow gsplat_core/gsplat_projection.cpp:67-172,
+// 584-652 of the reference; compute is the HIP C-ABI.
+#include "gsplat_projection.h"
+
+#include "core_util.h"
+
+namespace gsplat_core {
+namespace {
+using namespace detail;
+
+std::vector<int64_t> projection_shape(const array& means, const array& viewmats, int64_t tail_a,
+                                      int64_t tail_b = -1) {
+  if (means.dim() < 2 || viewmats.dim() < 3)
+    throw std::runtime_error(
+        "projection_ewa_3dgs_fused_forward expects means [..., N, 3] and viewmats [..., C, 4, 4].");
+  std::vector<int64_t> shape(means.sizes().begin(), means.sizes().end() - 2);
+  shape.push_back(viewmats.size(-3));
+  shape.push_back(means.size(-2));
+  if (tail_a > 0) shape.push_back(tail_a);
+  if (tail_b > 0) shape.push_back(tail_b);
+  return shape;
+}
+
+std::vector<int64_t> projection_scalar_shape(const array& means, const array& viewmats) {
+  return projection_shape(means, viewmats, -1);
+}
+
+// gsplat_projection.cpp:114-142
+void validate_inputs(const ProjectionEWA3DGSFusedInput& in) {
+  if (in.means.dim() < 2 || in.means.size(-1) != 3) throw std::runtime_error("means must have shape [..., N, 3].");
+  if (in.viewmats.dim() < 3 || in.viewmats.size(-1) != 4 || in.viewmats.size(-2) != 4)
+    throw std::runtime_error("viewmats must have shape [..., C, 4, 4].");
+  if (in.Ks.dim() < 3 || in.Ks.size(-1) != 3 || in.Ks.size(-2) != 3)
+    throw std::runtime_error("Ks must have shape [..., C, 3, 3].");
+  if (!in.params.use_covars && (is_empty(in.quats) || is_empty(in.scales)))
+    throw std::runtime_error("projection_ewa_3dgs_fused_forward expects covars or quats+scales.");
+  if (!is_empty(in.viewspace_points) &&
+      in.viewspace_points.sizes().vec() != projection_shape(in.means, in.viewmats, 2))
+    throw std::runtime_error("viewspace_points must have shape [..., C, N, 2].");
+}
+
+struct Dims {
+  int64_t B, C, N;
+};
+
+Dims dims_of(const array& means, const array& viewmats, const array& Ks) {
+  Dims d;
+  d.N = means.size(-2);
+  d.C = viewmats.size(-3);
+  int64_t b = 1;
+  for (int64_t i = 0; i < means.dim() - 2; ++i) b *= means.size(i);
+  d.B = b;
+  // The kernels index one [4,4] view matrix and one [3,3] K per (batch, camera).
+  if (viewmats.numel() != d.B * d.C * 16 || Ks.numel() != d.B * d.C * 9)
+    throw std::runtime_error("viewmats and Ks must hold one matrix per (batch, camera) of means' batch prefix.");
+  return d;
+}
+
+void check_gaussian_params(const array& means, const array& covars, const array& quats, const array& scales,
+                           bool use_covars, int64_t BN) {
+  require_dtype(means, at::kFloat, "projection_ewa_3dgs_fused expects float32 means.");
+  if (use_covars) {
+    require_device(covars, "covars");
+    require_dtype(covars, at::kFloat, "projection_ewa_3dgs_fused expects float32 covars.");
+    if (covars.numel() != BN * 6) throw std::runtime_error("covars must have shape [..., N, 6].");
+  } else {
+    require_device(quats, "quats");
+    require_device(scales, "scales");
+    require_dtype(quats, at::kFloat, "projection_ewa_3dgs_fused expects float32 quats.");
+    require_dtype(scales, at::kFloat, "projection_ewa_3dgs_fused expects float32 scales.");
+    if (quats.numel() != BN * 4 || scales.numel() != BN * 3)
+      throw std::runtime_error("quats/scales must have shapes [..., N, 4] / [..., N, 3].");
+  }
+}
+
+gsplat_projection_params to_c(const ProjectionEWA3DGSFusedParams& p) {
+  gsplat_projection_params c;
+  c.image_width = p.image_width;
+  c.image_height = p.image_height;
+  c.eps2d = p.eps2d;
+  c.near_plane = p.near_plane;
+  c.far_plane = p.far_plane;
+  c.radius_clip = p.radius_clip;
+  c.calc_compensations = p.calc_compensations;
+  c.camera_model = p.camera_model;
+  c.use_covars = p.use_covars;
+  c.use_opacities = p.use_opacities;
+  return c;
+}
+
+}  // namespace
+
+std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFusedInput& input) {
+  validate_inputs(input);
+  require_device(input.means, "means");
+  require_device(input.viewmats, "viewmats");
+  require_device(input.Ks, "Ks");
+  const Dims d = dims_of(input.means, input.viewmats, input.Ks);
+  const auto& p = input.params;
+  check_gaussian_params(input.means, input.covars, input.quats, input.scales, p.use_covars, d.B * d.N);
+  if (p.use_opacities) {
+    require_device(input.opacities, "opacities");
+    require_dtype(input.opacities, at::kFloat, "projection_ewa_3dgs_fused expects float32 opacities.");
+    if (input.opacities.numel() != d.B * d.N) throw std::runtime_error("opacities must have shape [..., N].");
+  }
+  const c10::DeviceGuard guard(input.means.device());
+  const array means = contig(input.means);
+  const array covars = p.use_covars ? contig(input.covars) : array();
+  const array quats = p.use_covars ? array() : contig(input.quats);
+  const array scales = p.use_covars ? array() : contig(input.scales);
+  const array opac = p.use_opacities ? contig(input.opacities) : array();
+  const array viewmats = contig(input.viewmats.to(at::kFloat));
+  const array Ks = contig(input.Ks.to(at::kFloat));
+  const auto scalar_shape = projection_scalar_shape(means, viewmats);
+  array means2d = at::empty(projection_shape(means, viewmats, 2), f32_like(means));
+  array depths = at::empty(scalar_shape, f32_like(means));
+  array conics = at::empty(projection_shape(means, viewmats, 3), f32_like(means));
+  array comps = p.calc_compensations ? at::empty(scalar_shape, f32_like(means)) : at::empty({0}, f32_like(means));
+  array radii = at::empty(projection_shape(means, viewmats, 2), i32_like(means));
+  const gsplat_projection_params cp = to_c(p);
+  check(gsplat_hip_projection_fwd(means.data_ptr<float>(), p.use_covars ? covars.data_ptr<float>() : nullptr,
+                                  p.use_covars ? nullptr : quats.data_ptr<float>(),
+                                  p.use_covars ? nullptr : scales.data_ptr<float>(),
+                                  p.use_opacities ? opac.data_ptr<float>() : nullptr, viewmats.data_ptr<float>(),
+                                  Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, radii.data_ptr<int32_t>(),
+                                  means2d.data_ptr<float>(), depths.data_ptr<float>(), conics.data_ptr<float>(),
+                                  p.calc_compensations ? comps.data_ptr<float>() : nullptr,
+                                  stream_for(input.s, means)));
+  return {means2d, depths, conics, comps, radii};
+}
+
+std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA3DGSFusedBackwardInput& input) {
+  // gsplat_projection.cpp:144-172
+  ProjectionEWA3DGSFusedInput fwd;
+  fwd.means = input.means;
+  fwd.covars = input.covars;
+  fwd.quats = input.quats;
+  fwd.scales = input.scales;
+  fwd.viewmats = input.viewmats;
+  fwd.Ks = input.Ks;
+  fwd.params = input.params;
+  validate_inputs(fwd);
+  if (input.params.camera_model != 0)
+    throw std::runtime_error("projection_ewa_3dgs_fused_backward currently supports pinhole only.");
+  if (input.radii.scalar_type() != at::kInt) throw std::runtime_error("radii must be int32.");
+  if (input.v_means2d.sizes().vec() != projection_shape(input.means, input.viewmats, 2) ||
+      input.v_conics.sizes().vec() != projection_shape(input.means, input.viewmats, 3) ||
+      input.v_depths.sizes().vec() != projection_scalar_shape(input.means, input.viewmats))
+    throw std::runtime_error("projection backward cotangent shape mismatch.");
+  require_device(input.means, "means");
+  require_device(input.viewmats, "viewmats");
+  require_device(input.Ks, "Ks");
+  const Dims d = dims_of(input.means, input.viewmats, input.Ks);
+  const auto& p = input.params;
+  check_gaussian_params(input.means, input.covars, input.quats, input.scales, p.use_covars, d.B * d.N);
+  const int64_t BCN = d.B * d.C * d.N;
+  if (input.radii.numel() != BCN * 2 || input.conics.numel() != BCN * 3)
+    throw std::runtime_error("radii / conics must have shapes [..., C, N, 2] / [..., C, N, 3].");
+  const bool use_comp = p.calc_compensations && !is_empty(input.compensations) && !is_empty(input.v_compensations);
+  if (use_comp && (input.compensations.numel() != BCN || input.v_compensations.numel() != BCN))
+    throw std::runtime_error("compensations / v_compensations must have shape [..., C, N].");
+  const c10::DeviceGuard guard(input.means.device());
+  const array means = contig(input.means);
+  const array covars = p.use_covars ? contig(input.covars) : array();
+  const array quats = p.use_covars ? array() : contig(input.quats);
+  const array scales = p.use_covars ? array() : contig(input.scales);
+  const array viewmats = contig(input.viewmats.to(at::kFloat));
+  const array Ks = contig(input.Ks.to(at::kFloat));
+  const array radii = contig(input.radii);
+  const array conics = contig(input.conics.to(at::kFloat));
+  const array comps = use_comp ? contig(input.compensations.to(at::kFloat)) : array();
+  const array v_comps = use_comp ? contig(input.v_compensations.to(at::kFloat)) : array();
+  const array v_m2 = contig(input.v_means2d.to(at::kFloat));
+  const array v_dep = contig(input.v_depths.to(at::kFloat));
+  const array v_con = contig(input.v_conics.to(at::kFloat));
+  array v_means = at::empty(means.sizes(), f32_like(means));
+  array v_covars = p.use_covars ? at::empty(covars.sizes(), f32_like(means)) : at::empty({0}, f32_like(means));
+  array v_quats = p.use_covars ? at::empty({0}, f32_like(means)) : at::empty(quats.sizes(), f32_like(means));
+  array v_scales = p.use_covars ? at::empty({0}, f32_like(means)) : at::empty(scales.sizes(), f32_like(means));
+  array v_viewmats = input.viewmats_requires_grad ? at::empty(viewmats.sizes(), f32_like(means))
+                                                  : at::empty({0}, f32_like(means));
+  const size_t ws_bytes =
+      gsplat_hip_projection_bwd_workspace_size(d.B, d.C, d.N, input.viewmats_requires_grad ? 1 : 0);
+  array ws = at::empty({static_cast<int64_t>(ws_bytes)}, u8_like(means));
+  const gsplat_projection_params cp = to_c(p);
+  check(gsplat_hip_projection_bwd(
+      means.data_ptr<float>(), p.use_covars ? covars.data_ptr<float>() : nullptr,
+      p.use_covars ? nullptr : quats.data_ptr<float>(), p.use_covars ? nullptr : scales.data_ptr<float>(),
+      viewmats.data_ptr<float>(), Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, radii.data_ptr<int32_t>(),
+      conics.data_ptr<float>(), use_comp ? comps.data_ptr<float>() : nullptr, v_m2.data_ptr<float>(),
+      v_dep.data_ptr<float>(), v_con.data_ptr<float>(), use_comp ? v_comps.data_ptr<float>() : nullptr,
+      v_means.data_ptr<float>(), p.use_covars ? v_covars.data_ptr<float>() : nullptr,
+      p.use_covars ? nullptr : v_quats.data_ptr<float>(), p.use_covars ? nullptr : v_scales.data_ptr<float>(),
+      input.viewmats_requires_grad ? v_viewmats.data_ptr<float>() : nullptr,
+      ws_bytes ? ws.data_ptr<uint8_t>() : nullptr, ws_bytes, stream_for(input.s, means)));
+  return {v_means, v_covars, v_quats, v_scales, v_viewmats};
+}
+
+}  // namespace gsplat_core

@@ -1,0 +1,70 @@
+// Tile intersection operator API; mirrors
+// gsplat_core/include/gsplat_intersect.h:12-83 of the reference.
+#pragma once
+
+#include "gsplat_common.h"
+
+namespace gsplat_core {
+
+struct IntersectTileParams {
+  int I;
+  int tile_size;
+  int tile_width;
+  int tile_height;
+  bool sort;
+  bool segmented;
+  bool packed;
+  bool use_conics;
+  bool use_opacities;
+};
+
+struct IntersectTileInput {
+  array means2d;
+  array radii;
+  array depths;
+  array conics;
+  array opacities;
+  array image_ids;
+  array gaussian_ids;
+  StreamOrDevice s;
+  IntersectTileParams params;
+};
+
+enum IntersectTileOutputIndex {
+  kTilesPerGauss = 0,
+  kIsectIds = 1,
+  kFlattenIds = 2,
+};
+
+struct IntersectOffsetParams {
+  int I;
+  int tile_width;
+  int tile_height;
+};
+
+struct IntersectTileEncodeParams {
+  int I;
+  int tile_size;
+  int tile_width;
+  int tile_height;
+  int total_isects;
+};
+
+std::vector<array> gsplat_intersect_tile(const IntersectTileInput& input);
+
+std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& input);
+
+array gsplat_intersect_tile_count(const IntersectTileInput& input);
+
+array gsplat_intersect_tile_offsets(const array& tiles_per_gauss, StreamOrDevice s = {});
+
+std::vector<array> gsplat_intersect_tile_encode(const IntersectTileInput& input, const array& tile_offsets,
+                                                int total_isects);
+
+std::vector<array> gsplat_intersect_tile_sort(const array& isect_ids, const array& flatten_ids,
+                                              StreamOrDevice s = {});
+
+array gsplat_intersect_offset(const array& isect_ids, int I, int tile_width, int tile_height,
+                              StreamOrDevice s = {});
+
+}  // namespace gsplat_core

@@ -1,0 +1,99 @@
+// Shared helpers for the gfx950 splatting kernels: error plumbing for the C
+// ABI, launch-size checks, and wave64 reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "gsplat_hip.h"
+
+namespace gsplat_hip {
+
+constexpr int kWave = 64;
+
+// Constants shared by projection and rasterization
+// (gsplat_core/gsplat_projection.cpp:63-65, gsplat_core/gsplat_rasterize.cpp:23-26).
+constexpr float kAlphaThreshold = 1.0f / 255.0f;
+constexpr float kGaussianExtend = 3.33f;
+constexpr float kMinCompensation = 0.005f;
+constexpr float kMaxAlpha = 0.99f;
+constexpr float kTransmittanceThreshold = 1.0e-4f;
+constexpr float kMinOneMinusAlpha = 1.0e-6f;
+
+void set_error(const std::string& msg);
+
+// Turns the last HIP launch/runtime error into a C-ABI status.
+int check_hip(hipError_t err, const char* what);
+int check_launch(const char* what);
+
+inline int invalid(const std::string& msg) {
+  set_error(msg);
+  return GSPLAT_ERR_INVALID_ARGUMENT;
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline unsigned grid_for(int64_t n, int block) {
+  return static_cast<unsigned>((n + block - 1) / block);
+}
+
+// Grid dimension limit for x (HIP: 2^31 - 1) -- callers check before launch.
+constexpr int64_t kMaxGridX = 2147483647LL;
+
+// Zero-fill a float/int buffer with a kernel (graph-capture safe, unlike a
+// memset node).
+int fill_zero(void* ptr, int64_t bytes, hipStream_t stream);
+
+// ---------------------------------------------------------------------------
+// wave64 reductions with DPP row operations. Result valid in lane 63; use
+// wave_sum_uniform() for a wave-uniform (scalar) value.
+__device__ __forceinline__ float wave_sum_lane63(float v) {
+  // Within each row of 16 lanes: shifted partial sums (row_shr 1, 2, 4, 8);
+  // invalid sources read as 0 (old = 0).
+  int x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false));
+  x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false));
+  x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false));
+  x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false));
+  // lane 15 of each row now holds the row sum: row_bcast:15 into rows 1 and 3,
+  // then row_bcast:31 into rows 2 and 3.
+  x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false));
+  x = __builtin_bit_cast(int, v);
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_uniform(float v) {
+  v = wave_sum_lane63(v);
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+__device__ __forceinline__ int wave_sum_int_uniform(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave (integers).
+__device__ __forceinline__ int wave_inclusive_scan(int v) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int y = __shfl_up(v, off, kWave);
+    if (lane >= off) v += y;
+  }
+  return v;
+}
+
+}  // namespace gsplat_hip

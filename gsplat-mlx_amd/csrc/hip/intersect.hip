@@ -1,0 +1,263 @@
+// Dense AABB tile intersection for gfx950: count + exclusive scan, encode,
+// and tile offsets.
+//
+// Integer semantics follow gsplat_core/gsplat_intersect.cpp:60-112 (rect and
+// key layout), :309-339 (count), :433-485 (encode order) and :605-641
+// (offsets = lower_bound). Tile ids are bit-exact with the reference: the rect
+// uses the same float divisions, floor/ceil and clamps.
+#include <cmath>
+
+#include "scan.hpp"
+
+namespace gsplat_hip {
+namespace {
+
+struct TileRect {
+  int min_x, min_y, max_x, max_y;
+};
+
+// gsplat_intersect.cpp:67-99
+__device__ __forceinline__ TileRect aabb_tile_rect(float mx, float my, int rx, int ry, int ts, int tw, int th) {
+  TileRect r = {0, 0, 0, 0};
+  if (rx <= 0 || ry <= 0) return r;
+  const float fts = static_cast<float>(ts);
+  const float trx = static_cast<float>(rx) / fts;
+  const float try_ = static_cast<float>(ry) / fts;
+  const float tx = mx / fts;
+  const float ty = my / fts;
+  r.min_x = min(max(0, static_cast<int>(floorf(tx - trx))), tw);
+  r.min_y = min(max(0, static_cast<int>(floorf(ty - try_))), th);
+  r.max_x = min(max(0, static_cast<int>(ceilf(tx + trx))), tw);
+  r.max_y = min(max(0, static_cast<int>(ceilf(ty + try_))), th);
+  return r;
+}
+
+// Count per Gaussian fused with the block-local exclusive scan.
+__global__ void __launch_bounds__(kScanBlock) count_scan_local_kernel(const float* __restrict__ means2d,
+                                                                      const int32_t* __restrict__ radii,
+                                                                      int64_t n, int ts, int tw, int th,
+                                                                      int32_t* __restrict__ counts,
+                                                                      int32_t* __restrict__ offsets,
+                                                                      int64_t* __restrict__ block_sums) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile + static_cast<int64_t>(threadIdx.x) * kScanItems;
+  int32_t v[kScanItems];
+  int64_t sum = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    const int64_t i = base + k;
+    int32_t c = 0;
+    if (i < n) {
+      const TileRect r = aabb_tile_rect(means2d[i * 2], means2d[i * 2 + 1], radii[i * 2], radii[i * 2 + 1], ts, tw, th);
+      c = (r.max_y - r.min_y) * (r.max_x - r.min_x);
+      counts[i] = c;
+    }
+    v[k] = c;
+    sum += c;
+  }
+  int64_t total;
+  int64_t run = block_exclusive_scan(sum, &total);
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    if (base + k < n) offsets[base + k] = static_cast<int32_t>(run);
+    run += v[k];
+  }
+  if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
+}
+
+__global__ void __launch_bounds__(kScanBlock) block_sums_scan_kernel(int64_t* __restrict__ sums, int64_t nb,
+                                                                    int64_t* __restrict__ total_dev) {
+  int64_t carry = 0;
+  for (int64_t start = 0; start < nb; start += kScanBlock) {
+    const int64_t i = start + threadIdx.x;
+    const int64_t v = i < nb ? sums[i] : 0;
+    int64_t tot;
+    const int64_t ex = block_exclusive_scan(v, &tot);
+    if (i < nb) sums[i] = carry + ex;
+    carry += tot;
+  }
+  if (threadIdx.x == 0) *total_dev = carry;
+}
+
+__global__ void __launch_bounds__(kScanBlock) add_block_prefix_kernel(int32_t* __restrict__ offsets, int64_t n,
+                                                                     const int64_t* __restrict__ sums) {
+  const int64_t add = sums[blockIdx.x];
+  if (add == 0) return;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  for (int k = threadIdx.x; k < kScanTile; k += kScanBlock) {
+    const int64_t i = base + k;
+    if (i < n) offsets[i] = static_cast<int32_t>(offsets[i] + add);
+  }
+}
+
+// Load-balanced encode: a block owns kEncodeG consecutive Gaussians and their
+// contiguous output range; each output slot finds its Gaussian by binary
+// search over the LDS copy of the offsets, so consecutive lanes write
+// consecutive keys (coalesced) however unequal the per-Gaussian counts are.
+constexpr int kEncodeBlock = 256;
+constexpr int kEncodeG = 256;
+
+__global__ void __launch_bounds__(kEncodeBlock) encode_kernel(const float* __restrict__ means2d,
+                                                             const int32_t* __restrict__ radii,
+                                                             const float* __restrict__ depths,
+                                                             const int32_t* __restrict__ offsets, int64_t numel,
+                                                             int64_t n_per_image, int ts, int tw, int th,
+                                                             int tile_bits, int64_t n_isects,
+                                                             int64_t* __restrict__ isect_ids,
+                                                             int32_t* __restrict__ flatten_ids) {
+  __shared__ int32_t s_off[kEncodeG];
+  __shared__ int32_t s_minx[kEncodeG];
+  __shared__ int32_t s_miny[kEncodeG];
+  __shared__ int32_t s_w[kEncodeG];
+  __shared__ int64_t s_hi[kEncodeG];  // image/tile-row independent high key part: image << (32 + tile_bits)
+  __shared__ uint32_t s_bits[kEncodeG];
+  __shared__ int64_t s_end;
+  const int64_t g0 = static_cast<int64_t>(blockIdx.x) * kEncodeG;
+  const int cnt = static_cast<int>(min<int64_t>(kEncodeG, numel - g0));
+  const int t = threadIdx.x;
+  if (t < cnt) {
+    const int64_t g = g0 + t;
+    const TileRect r = aabb_tile_rect(means2d[g * 2], means2d[g * 2 + 1], radii[g * 2], radii[g * 2 + 1], ts, tw, th);
+    const int32_t off = offsets[g];
+    s_off[t] = off;
+    s_minx[t] = r.min_x;
+    s_miny[t] = r.min_y;
+    s_w[t] = r.max_x - r.min_x;
+    s_hi[t] = static_cast<int64_t>(g / n_per_image) << (32 + tile_bits);
+    s_bits[t] = __float_as_uint(depths[g]);
+    if (t == cnt - 1) s_end = static_cast<int64_t>(off) + (r.max_y - r.min_y) * (r.max_x - r.min_x);
+  }
+  __syncthreads();
+  // Offsets from the scan are consistent; clamping only keeps writes in
+  // bounds for inconsistent caller-supplied offsets.
+  const int64_t start = max<int64_t>(s_off[0], 0);
+  const int64_t end = min<int64_t>(s_end, n_isects);
+  for (int64_t o = start + t; o < end; o += kEncodeBlock) {
+    // last j with s_off[j] <= o
+    int lo = 0, hi = cnt - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_off[mid] <= o)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int j = lo;
+    const int k = static_cast<int>(o - s_off[j]);
+    const int w = max(s_w[j], 1);
+    const int row = k / w;
+    const int col = k - row * w;
+    const int64_t tile = static_cast<int64_t>(s_miny[j] + row) * tw + (s_minx[j] + col);
+    isect_ids[o] = s_hi[j] | (tile << 32) | static_cast<int64_t>(s_bits[j]);
+    flatten_ids[o] = static_cast<int32_t>(g0 + j);
+  }
+}
+
+// Tile offsets as lower_bound over sorted keys (gsplat_intersect.cpp:605-641),
+// computed in O(n_isects): entry i owns the offset slots o whose search key
+// (o / n_tiles) << tile_bits | (o % n_tiles) lies in (v[i-1], v[i]], with
+// v = isect_ids >> 32; slots past the last key get n_isects.
+__device__ __forceinline__ int64_t first_slot_above(int64_t v, int tile_bits, int64_t n_tiles, int64_t n_offsets) {
+  if (v < 0) return 0;
+  const int64_t img = v >> tile_bits;
+  const int64_t t = v & ((static_cast<int64_t>(1) << tile_bits) - 1);
+  int64_t o = (t + 1 < n_tiles) ? img * n_tiles + t + 1 : (img + 1) * n_tiles;
+  return min(o, n_offsets);
+}
+
+__global__ void __launch_bounds__(256) offsets_kernel(const int64_t* __restrict__ ids, int64_t n, int tile_bits,
+                                                      int64_t n_tiles, int64_t n_offsets, int32_t* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int64_t lo = i == 0 ? 0 : first_slot_above(ids[i - 1] >> 32, tile_bits, n_tiles, n_offsets);
+  const int64_t hi = first_slot_above(ids[i] >> 32, tile_bits, n_tiles, n_offsets);
+  for (int64_t o = lo; o < hi; ++o) out[o] = static_cast<int32_t>(i);
+  if (i == n - 1)
+    for (int64_t o = hi; o < n_offsets; ++o) out[o] = static_cast<int32_t>(n);
+}
+
+__global__ void fill_i32_kernel(int32_t* __restrict__ out, int64_t n, int32_t value) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) out[i] = value;
+}
+
+// floor(log2(n)) + 1 with the reference's float log2 (gsplat_intersect.cpp:60-65).
+int floor_log2_plus_one(int64_t value) {
+  return static_cast<int>(std::floor(std::log2(static_cast<float>(value)))) + 1;
+}
+
+}  // namespace
+}  // namespace gsplat_hip
+
+using namespace gsplat_hip;
+
+extern "C" size_t gsplat_hip_isect_count_scan_workspace_size(int64_t numel) { return scan_workspace_bytes(numel); }
+
+extern "C" int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* radii, int64_t numel,
+                                           int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                           int32_t* tiles_per_gauss, int32_t* offsets, int64_t* total_dev,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+  hipStream_t s = as_stream(stream);
+  if (numel < 0 || tile_size <= 0 || tile_width <= 0 || tile_height <= 0)
+    return invalid("intersect_tile_count: invalid sizes.");
+  if (!total_dev) return invalid("intersect_tile_count: null total.");
+  if (numel == 0) return fill_zero(total_dev, sizeof(int64_t), s);
+  if (!means2d || !radii || !tiles_per_gauss || !offsets) return invalid("intersect_tile_count: null pointer.");
+  if (!workspace || workspace_bytes < scan_workspace_bytes(numel)) {
+    set_error("intersect_tile_count: workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  const int64_t nb = scan_num_blocks(numel);
+  int64_t* sums = static_cast<int64_t*>(workspace);
+  count_scan_local_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(means2d, radii, numel, tile_size,
+                                                                          tile_width, tile_height, tiles_per_gauss,
+                                                                          offsets, sums);
+  int rc = check_launch("intersect_tile_count");
+  if (rc) return rc;
+  block_sums_scan_kernel<<<1, kScanBlock, 0, s>>>(sums, nb, total_dev);
+  rc = check_launch("intersect_tile_offsets (block sums)");
+  if (rc || nb == 1) return rc;
+  add_block_prefix_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(offsets, numel, sums);
+  return check_launch("intersect_tile_offsets (fixup)");
+}
+
+extern "C" int gsplat_hip_isect_encode(const float* means2d, const int32_t* radii, const float* depths,
+                                       const int32_t* offsets, int64_t I, int64_t numel, int32_t tile_size,
+                                       int32_t tile_width, int32_t tile_height, int64_t n_isects, int64_t* isect_ids,
+                                       int32_t* flatten_ids, void* stream) {
+  if (I <= 0 || numel < 0 || numel % I != 0)
+    return invalid("intersect_tile_encode dense path expects depths size to equal I * N.");
+  if (tile_size <= 0 || tile_width <= 0 || tile_height <= 0) return invalid("intersect_tile_encode: invalid tiles.");
+  if (n_isects < 0) return invalid("intersect_tile_encode expects non-negative total_isects.");
+  const int64_t n_tiles = static_cast<int64_t>(tile_width) * tile_height;
+  const int tile_bits = floor_log2_plus_one(n_tiles);
+  const int image_bits = floor_log2_plus_one(I);
+  if (image_bits + tile_bits > 32)
+    return invalid("intersect_tile_encode image id and tile id require more than 32 bits.");
+  if (numel == 0 || n_isects == 0) return GSPLAT_OK;
+  if (!means2d || !radii || !depths || !offsets || !isect_ids || !flatten_ids)
+    return invalid("intersect_tile_encode: null pointer.");
+  const int64_t nb = (numel + kEncodeG - 1) / kEncodeG;
+  encode_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, as_stream(stream)>>>(
+      means2d, radii, depths, offsets, numel, numel / I, tile_size, tile_width, tile_height, tile_bits, n_isects,
+      isect_ids, flatten_ids);
+  return check_launch("intersect_tile_encode");
+}
+
+extern "C" int gsplat_hip_isect_offset(const int64_t* isect_ids, int64_t n_isects, int32_t I, int32_t tile_width,
+                                       int32_t tile_height, int32_t* offsets, void* stream) {
+  if (I <= 0 || tile_width <= 0 || tile_height <= 0)
+    return invalid("intersect_offset expects positive image and tile dimensions.");
+  if (n_isects < 0) return invalid("intersect_offset: negative size.");
+  hipStream_t s = as_stream(stream);
+  const int64_t n_tiles = static_cast<int64_t>(tile_width) * tile_height;
+  const int64_t n_offsets = n_tiles * I;
+  if (!offsets) return invalid("intersect_offset: null pointer.");
+  if (n_isects == 0) {
+    fill_i32_kernel<<<grid_for(n_offsets, 256), 256, 0, s>>>(offsets, n_offsets, 0);
+    return check_launch("intersect_offset (empty)");
+  }
+  if (!isect_ids) return invalid("intersect_offset: null pointer.");
+  const int tile_bits = floor_log2_plus_one(n_tiles);
+  offsets_kernel<<<grid_for(n_isects, 256), 256, 0, s>>>(isect_ids, n_isects, tile_bits, n_tiles, n_offsets, offsets);
+  return check_launch("intersect_offset");
+}

@@ -1,0 +1,55 @@
+// Device-wide exclusive scan of int32 counts (reduce-then-scan, no inter-block
+// waiting): block-local scans, one block scanning the block totals, and a
+// fix-up pass. Used by the tile count scan and by the radix sort's
+// digit-major histogram scan.
+#pragma once
+
+#include "common.hpp"
+
+namespace gsplat_hip {
+
+constexpr int kScanBlock = 256;
+constexpr int kScanItems = 4;
+constexpr int kScanTile = kScanBlock * kScanItems;
+
+inline int64_t scan_num_blocks(int64_t n) { return (n + kScanTile - 1) / kScanTile; }
+
+// Block-exclusive scan of an int value per thread; returns the exclusive
+// prefix and writes the block total to *block_total (all threads).
+// Requires blockDim.x == kScanBlock; every thread of the block must call it.
+__device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* block_total) {
+  __shared__ int64_t wave_tot[kScanBlock / kWave];
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  // 64-bit inclusive wave scan with shuffles
+  int64_t inc = v;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const int64_t y = __shfl_up(inc, off, kWave);
+    if (lane >= off) inc += y;
+  }
+  if (lane == kWave - 1) wave_tot[wave] = inc;
+  __syncthreads();
+  int64_t wave_base = 0, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kScanBlock / kWave; ++w) {
+    const int64_t t = wave_tot[w];
+    if (w < wave) wave_base += t;
+    tot += t;
+  }
+  __syncthreads();
+  *block_total = tot;
+  return wave_base + inc - v;
+}
+
+// Bytes of workspace for scan_exclusive_i32 over n values.
+inline size_t scan_workspace_bytes(int64_t n) {
+  return static_cast<size_t>(scan_num_blocks(n) + 1) * sizeof(int64_t);
+}
+
+// out[i] = sum_{j<i} in[j] (may alias in); *total_dev (int64) = sum of all.
+// Partial sums are int64; out values must fit int32 (caller checks total).
+int scan_exclusive_i32(const int32_t* in, int32_t* out, int64_t n, int64_t* total_dev, void* workspace,
+                       hipStream_t stream);
+
+}  // namespace gsplat_hip

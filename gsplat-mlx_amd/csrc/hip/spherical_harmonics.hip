@@ -1,0 +1,367 @@
+// Real spherical harmonics (degrees 0..4), forward / backward, for gfx950.
+//
+// Layout is the reference's AoS: coeffs [n, K, 3], 12*K bytes per Gaussian.
+// A block of kShBlock Gaussians stages the active (degree+1)^2 bases of its
+// rows through LDS with consecutive lanes reading consecutive floats, so the
+// HBM stream is read once, coalesced, instead of each lane striding 12*K
+// bytes. The backward writes v_coeffs the same way: each lane computes its
+// Gaussian's basis into LDS, then the block writes the [kShBlock, K, 3] slab
+// with consecutive lanes on consecutive floats. Index splits use exact
+// multiply-high reciprocals (valid for the block-slab index range).
+//
+// Math follows gsplat_core/gsplat_spherical_harmonics.cpp:112-425 in the same
+// operation order (FMA contraction off for this file).
+#include "common.hpp"
+
+namespace gsplat_hip {
+namespace {
+
+constexpr int kShBlock = 128;
+constexpr float kC0 = 0.2820947917738781f;
+constexpr float kC1 = 0.48860251190292f;
+
+// floor(i / d) for i * (m*d - 2^32) < 2^32, with m = ceil(2^32 / d).
+__host__ __device__ inline uint32_t magic_for(uint32_t d) {
+  return static_cast<uint32_t>((0x100000000ull + d - 1) / d);
+}
+__device__ __forceinline__ uint32_t fast_div(uint32_t i, uint32_t m) { return __umulhi(i, m); }
+
+// gsplat_spherical_harmonics.cpp:112-187
+template <int DEG>
+__device__ __forceinline__ void sh_basis(float dx, float dy, float dz, float* basis) {
+  constexpr int A = (DEG + 1) * (DEG + 1);
+#pragma unroll
+  for (int i = 0; i < A; ++i) basis[i] = 0.0f;
+  basis[0] = kC0;
+  if (DEG < 1) return;
+  const float norm = sqrtf(dx * dx + dy * dy + dz * dz);
+  if (norm == 0.0f) return;
+  const float x = dx / norm, y = dy / norm, z = dz / norm;
+  basis[1] = -kC1 * y;
+  basis[2] = kC1 * z;
+  basis[3] = -kC1 * x;
+  if (DEG < 2) return;
+  const float z2 = z * z;
+  const float f_tmp0_b = -1.092548430592079f * z;
+  const float f_c1 = x * x - y * y;
+  const float f_s1 = 2.0f * x * y;
+  basis[4] = 0.5462742152960395f * f_s1;
+  basis[5] = f_tmp0_b * y;
+  basis[6] = 0.9461746957575601f * z2 - 0.3153915652525201f;
+  basis[7] = f_tmp0_b * x;
+  basis[8] = 0.5462742152960395f * f_c1;
+  if (DEG < 3) return;
+  const float f_tmp0_c = -2.285228997322329f * z2 + 0.4570457994644658f;
+  const float f_tmp1_b = 1.445305721320277f * z;
+  const float f_c2 = x * f_c1 - y * f_s1;
+  const float f_s2 = x * f_s1 + y * f_c1;
+  basis[9] = -0.5900435899266435f * f_s2;
+  basis[10] = f_tmp1_b * f_s1;
+  basis[11] = f_tmp0_c * y;
+  basis[12] = z * (1.865881662950577f * z2 - 1.119528997770346f);
+  basis[13] = f_tmp0_c * x;
+  basis[14] = f_tmp1_b * f_c1;
+  basis[15] = -0.5900435899266435f * f_c2;
+  if (DEG < 4) return;
+  const float f_tmp0_d = z * (-4.683325804901025f * z2 + 2.007139630671868f);
+  const float f_tmp1_c = 3.31161143515146f * z2 - 0.47308734787878f;
+  const float f_tmp2_b = -1.770130769779931f * z;
+  const float f_c3 = x * f_c2 - y * f_s2;
+  const float f_s3 = x * f_s2 + y * f_c2;
+  basis[16] = 0.6258357354491763f * f_s3;
+  basis[17] = f_tmp2_b * f_s2;
+  basis[18] = f_tmp1_c * f_s1;
+  basis[19] = f_tmp0_d * y;
+  basis[20] = 1.984313483298443f * z * basis[12] - 1.006230589874905f * basis[6];
+  basis[21] = f_tmp0_d * x;
+  basis[22] = f_tmp1_c * f_c1;
+  basis[23] = f_tmp2_b * f_c2;
+  basis[24] = 0.6258357354491763f * f_c3;
+}
+
+// Copies the first A*3 floats of `cnt` rows of stride K*3 into LDS.
+template <int A>
+__device__ __forceinline__ void stage_rows(float* __restrict__ lds, const float* __restrict__ src, int cnt,
+                                           int64_t row_stride) {
+  constexpr int W = A * 3;
+  constexpr uint32_t m = (0x100000000ull + W - 1) / W;
+  const int total = cnt * W;
+  for (int i = threadIdx.x; i < total; i += kShBlock) {
+    const uint32_t r = fast_div(static_cast<uint32_t>(i), m);
+    const uint32_t c = static_cast<uint32_t>(i) - r * W;
+    lds[i] = src[r * row_stride + c];
+  }
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShBlock) sh_fwd_kernel(const float* __restrict__ dirs,
+                                                          const float* __restrict__ coeffs,
+                                                          const uint8_t* __restrict__ masks, int64_t n, int64_t K,
+                                                          float* __restrict__ colors) {
+  constexpr int A = (DEG + 1) * (DEG + 1);
+  __shared__ float sc[kShBlock * A * 3];
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShBlock;
+  const int cnt = static_cast<int>(min<int64_t>(kShBlock, n - e0));
+  stage_rows<A>(sc, coeffs + e0 * K * 3, cnt, K * 3);
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t >= cnt) return;
+  const int64_t e = e0 + t;
+  float out[3] = {0.0f, 0.0f, 0.0f};
+  if (!masks || masks[e]) {
+    const float d0 = dirs[e * 3], d1 = dirs[e * 3 + 1], d2 = dirs[e * 3 + 2];
+    const float* co = sc + t * A * 3;
+    float basis[A];
+    sh_basis<DEG>(d0, d1, d2, basis);
+    const float norm = sqrtf(d0 * d0 + d1 * d1 + d2 * d2);
+#pragma unroll
+    for (int ch = 0; ch < 3; ++ch) {
+      float result = kC0 * co[ch];
+      if (DEG >= 1 && norm != 0.0f) {
+        const float x = d0 / norm, y = d1 / norm, z = d2 / norm;
+        result += kC1 * (-y * co[3 + ch] + z * co[6 + ch] - x * co[9 + ch]);
+#pragma unroll
+        for (int l = 2; l <= DEG; ++l) {
+          float band = basis[l * l] * co[l * l * 3 + ch];
+#pragma unroll
+          for (int b = l * l + 1; b < (l + 1) * (l + 1); ++b) band += basis[b] * co[b * 3 + ch];
+          result += band;
+        }
+      }
+      out[ch] = result;
+    }
+  }
+  colors[e * 3] = out[0];
+  colors[e * 3 + 1] = out[1];
+  colors[e * 3 + 2] = out[2];
+}
+
+// gsplat_spherical_harmonics.cpp:288-425
+template <int DEG>
+__device__ __forceinline__ void sh_dir_vjp(const float dir[3], const float* co, const float vc[3], float v_dir[3]) {
+  v_dir[0] = v_dir[1] = v_dir[2] = 0.0f;
+  if (DEG < 1) return;
+  const float norm = sqrtf(dir[0] * dir[0] + dir[1] * dir[1] + dir[2] * dir[2]);
+  if (norm == 0.0f) return;
+  const float inorm = 1.0f / norm;
+  const float x = dir[0] * inorm, y = dir[1] * inorm, z = dir[2] * inorm;
+  constexpr int A = (DEG + 1) * (DEG + 1);
+  float dx[A], dy[A], dz[A];
+#pragma unroll
+  for (int i = 0; i < A; ++i) dx[i] = dy[i] = dz[i] = 0.0f;
+  dx[3] = -kC1;
+  dy[1] = -kC1;
+  dz[2] = kC1;
+  const float z2 = z * z;
+  const float f_tmp0_b = -1.092548430592079f * z;
+  const float f_c1 = x * x - y * y;
+  const float f_s1 = 2.0f * x * y;
+  const float f_tmp0_b_z = -1.092548430592079f;
+  const float f_c1_x = 2.0f * x, f_c1_y = -2.0f * y;
+  const float f_s1_x = 2.0f * y, f_s1_y = 2.0f * x;
+  const float p_sh6_z = 2.0f * 0.9461746957575601f * z;
+  if constexpr (DEG >= 2) {
+    dx[4] = 0.5462742152960395f * f_s1_x;
+    dy[4] = 0.5462742152960395f * f_s1_y;
+    dy[5] = f_tmp0_b;
+    dz[5] = f_tmp0_b_z * y;
+    dz[6] = p_sh6_z;
+    dx[7] = f_tmp0_b;
+    dz[7] = f_tmp0_b_z * x;
+    dx[8] = 0.5462742152960395f * f_c1_x;
+    dy[8] = 0.5462742152960395f * f_c1_y;
+  }
+  const float f_tmp0_c = -2.285228997322329f * z2 + 0.4570457994644658f;
+  const float f_tmp1_b = 1.445305721320277f * z;
+  const float f_c2 = x * f_c1 - y * f_s1;
+  const float f_s2 = x * f_s1 + y * f_c1;
+  const float p_sh12 = z * (1.865881662950577f * z2 - 1.119528997770346f);
+  const float f_tmp0_c_z = -2.285228997322329f * 2.0f * z;
+  const float f_tmp1_b_z = 1.445305721320277f;
+  const float f_c2_x = f_c1 + x * f_c1_x - y * f_s1_x;
+  const float f_c2_y = x * f_c1_y - f_s1 - y * f_s1_y;
+  const float f_s2_x = f_s1 + x * f_s1_x + y * f_c1_x;
+  const float f_s2_y = x * f_s1_y + f_c1 + y * f_c1_y;
+  const float p_sh12_z = 3.0f * 1.865881662950577f * z2 - 1.119528997770346f;
+  if constexpr (DEG >= 3) {
+    dx[9] = -0.5900435899266435f * f_s2_x;
+    dy[9] = -0.5900435899266435f * f_s2_y;
+    dx[10] = f_tmp1_b * f_s1_x;
+    dy[10] = f_tmp1_b * f_s1_y;
+    dz[10] = f_tmp1_b_z * f_s1;
+    dy[11] = f_tmp0_c;
+    dz[11] = f_tmp0_c_z * y;
+    dz[12] = p_sh12_z;
+    dx[13] = f_tmp0_c;
+    dz[13] = f_tmp0_c_z * x;
+    dx[14] = f_tmp1_b * f_c1_x;
+    dy[14] = f_tmp1_b * f_c1_y;
+    dz[14] = f_tmp1_b_z * f_c1;
+    dx[15] = -0.5900435899266435f * f_c2_x;
+    dy[15] = -0.5900435899266435f * f_c2_y;
+  }
+  if constexpr (DEG >= 4) {
+    const float f_tmp0_d = z * (-4.683325804901025f * z2 + 2.007139630671868f);
+    const float f_tmp1_c = 3.31161143515146f * z2 - 0.47308734787878f;
+    const float f_tmp2_b = -1.770130769779931f * z;
+    const float f_tmp0_d_z = 3.0f * -4.683325804901025f * z2 + 2.007139630671868f;
+    const float f_tmp1_c_z = 2.0f * 3.31161143515146f * z;
+    const float f_tmp2_b_z = -1.770130769779931f;
+    const float f_c3_x = f_c2 + x * f_c2_x - y * f_s2_x;
+    const float f_c3_y = x * f_c2_y - f_s2 - y * f_s2_y;
+    const float f_s3_x = f_s2 + y * f_c2_x + x * f_s2_x;
+    const float f_s3_y = x * f_s2_y + f_c2 + y * f_c2_y;
+    dx[16] = 0.6258357354491763f * f_s3_x;
+    dy[16] = 0.6258357354491763f * f_s3_y;
+    dx[17] = f_tmp2_b * f_s2_x;
+    dy[17] = f_tmp2_b * f_s2_y;
+    dz[17] = f_tmp2_b_z * f_s2;
+    dx[18] = f_tmp1_c * f_s1_x;
+    dy[18] = f_tmp1_c * f_s1_y;
+    dz[18] = f_tmp1_c_z * f_s1;
+    dy[19] = f_tmp0_d;
+    dz[19] = f_tmp0_d_z * y;
+    dz[20] = 1.984313483298443f * (p_sh12 + z * p_sh12_z) - 1.006230589874905f * p_sh6_z;
+    dx[21] = f_tmp0_d;
+    dz[21] = f_tmp0_d_z * x;
+    dx[22] = f_tmp1_c * f_c1_x;
+    dy[22] = f_tmp1_c * f_c1_y;
+    dz[22] = f_tmp1_c_z * f_c1;
+    dx[23] = f_tmp2_b * f_c2_x;
+    dy[23] = f_tmp2_b * f_c2_y;
+    dz[23] = f_tmp2_b_z * f_c2;
+    dx[24] = 0.6258357354491763f * f_c3_x;
+    dy[24] = 0.6258357354491763f * f_c3_y;
+  }
+  float vn[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int b = 1; b < A; ++b) {
+    const float vb = co[b * 3] * vc[0] + co[b * 3 + 1] * vc[1] + co[b * 3 + 2] * vc[2];
+    vn[0] += dx[b] * vb;
+    vn[1] += dy[b] * vb;
+    vn[2] += dz[b] * vb;
+  }
+  const float dot = vn[0] * x + vn[1] * y + vn[2] * z;
+  v_dir[0] = (vn[0] - dot * x) * inorm;
+  v_dir[1] = (vn[1] - dot * y) * inorm;
+  v_dir[2] = (vn[2] - dot * z) * inorm;
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShBlock) sh_bwd_kernel(const float* __restrict__ dirs,
+                                                          const float* __restrict__ coeffs,
+                                                          const uint8_t* __restrict__ masks,
+                                                          const float* __restrict__ v_colors, int64_t n, int64_t K,
+                                                          uint32_t k3_magic, float* __restrict__ v_dirs,
+                                                          float* __restrict__ v_coeffs) {
+  constexpr int A = (DEG + 1) * (DEG + 1);
+  __shared__ float sc[DEG >= 1 ? kShBlock * A * 3 : 1];
+  __shared__ float sb[kShBlock * (A + 3)];  // per-lane basis (A) then v_color (3)
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShBlock;
+  const int cnt = static_cast<int>(min<int64_t>(kShBlock, n - e0));
+  const int t = threadIdx.x;
+  if (v_dirs && DEG >= 1) stage_rows<A>(sc, coeffs + e0 * K * 3, cnt, K * 3);
+  float* my = sb + t * (A + 3);
+  bool on = false;
+  float dir[3] = {0.0f, 0.0f, 0.0f};
+  float vc[3] = {0.0f, 0.0f, 0.0f};
+  if (t < cnt) {
+    const int64_t e = e0 + t;
+    on = !masks || masks[e];
+    dir[0] = dirs[e * 3];
+    dir[1] = dirs[e * 3 + 1];
+    dir[2] = dirs[e * 3 + 2];
+    vc[0] = v_colors[e * 3];
+    vc[1] = v_colors[e * 3 + 1];
+    vc[2] = v_colors[e * 3 + 2];
+    float basis[A];
+    sh_basis<DEG>(dir[0], dir[1], dir[2], basis);
+#pragma unroll
+    for (int b = 0; b < A; ++b) my[b] = on ? basis[b] : 0.0f;
+    my[A] = vc[0];
+    my[A + 1] = vc[1];
+    my[A + 2] = vc[2];
+  }
+  __syncthreads();
+  if (t < cnt && v_dirs) {
+    const int64_t e = e0 + t;
+    float vd[3] = {0.0f, 0.0f, 0.0f};
+    if (on && DEG >= 1) sh_dir_vjp<DEG>(dir, sc + t * A * 3, vc, vd);
+    v_dirs[e * 3] = vd[0];
+    v_dirs[e * 3 + 1] = vd[1];
+    v_dirs[e * 3 + 2] = vd[2];
+  }
+  // Coalesced write of the [cnt, K, 3] slab of v_coeffs.
+  const uint32_t K3 = static_cast<uint32_t>(K * 3);
+  const uint32_t total = static_cast<uint32_t>(cnt) * K3;
+  float* out = v_coeffs + e0 * K * 3;
+  for (uint32_t i = t; i < total; i += kShBlock) {
+    const uint32_t r = fast_div(i, k3_magic);
+    const uint32_t c = i - r * K3;
+    const uint32_t b = c / 3u;
+    const uint32_t ch = c - b * 3u;
+    const float* row = sb + r * (A + 3);
+    out[i] = b < static_cast<uint32_t>(A) ? row[b] * row[A + ch] : 0.0f;
+  }
+}
+
+template <int DEG>
+int launch_fwd(const float* dirs, const float* coeffs, const uint8_t* masks, int64_t n, int64_t K, float* colors,
+               hipStream_t s) {
+  sh_fwd_kernel<DEG><<<grid_for(n, kShBlock), kShBlock, 0, s>>>(dirs, coeffs, masks, n, K, colors);
+  return check_launch("spherical_harmonics_forward");
+}
+
+template <int DEG>
+int launch_bwd(const float* dirs, const float* coeffs, const uint8_t* masks, const float* v_colors, int64_t n,
+               int64_t K, float* v_dirs, float* v_coeffs, hipStream_t s) {
+  sh_bwd_kernel<DEG><<<grid_for(n, kShBlock), kShBlock, 0, s>>>(dirs, coeffs, masks, v_colors, n, K,
+                                                               magic_for(static_cast<uint32_t>(K * 3)), v_dirs,
+                                                               v_coeffs);
+  return check_launch("spherical_harmonics_backward");
+}
+
+}  // namespace
+}  // namespace gsplat_hip
+
+using namespace gsplat_hip;
+
+extern "C" int gsplat_hip_spherical_harmonics_fwd(int32_t degree, const float* dirs, const float* coeffs,
+                                                  const uint8_t* masks, int64_t n, int64_t K, float* colors,
+                                                  void* stream) {
+  if (degree < 0 || degree > 4) return invalid("spherical_harmonics_forward supports degree 0..4.");
+  if (K < (degree + 1) * (degree + 1)) return invalid("coeffs has fewer SH bases than degrees_to_use requires.");
+  if (n < 0) return invalid("spherical_harmonics_forward: negative size.");
+  if (n == 0) return GSPLAT_OK;
+  if (!dirs || !coeffs || !colors) return invalid("spherical_harmonics_forward: null pointer.");
+  if (K > 1024) return invalid("spherical_harmonics_forward: K exceeds 1024 bases.");
+  hipStream_t s = as_stream(stream);
+  switch (degree) {
+    case 0: return launch_fwd<0>(dirs, coeffs, masks, n, K, colors, s);
+    case 1: return launch_fwd<1>(dirs, coeffs, masks, n, K, colors, s);
+    case 2: return launch_fwd<2>(dirs, coeffs, masks, n, K, colors, s);
+    case 3: return launch_fwd<3>(dirs, coeffs, masks, n, K, colors, s);
+    default: return launch_fwd<4>(dirs, coeffs, masks, n, K, colors, s);
+  }
+}
+
+extern "C" int gsplat_hip_spherical_harmonics_bwd(int32_t degree, const float* dirs, const float* coeffs,
+                                                  const uint8_t* masks, const float* v_colors, int64_t n, int64_t K,
+                                                  float* v_dirs, float* v_coeffs, void* stream) {
+  if (degree < 0 || degree > 4) return invalid("spherical_harmonics_backward supports degree 0..4.");
+  if (K < (degree + 1) * (degree + 1)) return invalid("coeffs has fewer SH bases than degrees_to_use requires.");
+  if (n < 0) return invalid("spherical_harmonics_backward: negative size.");
+  if (n == 0) return GSPLAT_OK;
+  if (!dirs || !coeffs || !v_colors || !v_coeffs) return invalid("spherical_harmonics_backward: null pointer.");
+  // The slab index i < kShBlock*K*3 keeps the multiply-high split exact
+  // while kShBlock * (3K)^2 < 2^32, i.e. K <= 1024.
+  if (K > 1024) return invalid("spherical_harmonics_backward: K exceeds 1024 bases.");
+  hipStream_t s = as_stream(stream);
+  switch (degree) {
+    case 0: return launch_bwd<0>(dirs, coeffs, masks, v_colors, n, K, v_dirs, v_coeffs, s);
+    case 1: return launch_bwd<1>(dirs, coeffs, masks, v_colors, n, K, v_dirs, v_coeffs, s);
+    case 2: return launch_bwd<2>(dirs, coeffs, masks, v_colors, n, K, v_dirs, v_coeffs, s);
+    case 3: return launch_bwd<3>(dirs, coeffs, masks, v_colors, n, K, v_dirs, v_coeffs, s);
+    default: return launch_bwd<4>(dirs, coeffs, masks, v_colors, n, K, v_dirs, v_coeffs, s);
+  }
+}

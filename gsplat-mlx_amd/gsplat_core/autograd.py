@@ -1,0 +1,204 @@
+"""Differentiable wrappers: one torch.autograd.Function per reference primitive.
+
+Each ``backward`` routes cotangents exactly as the reference ``Primitive::vjp``:
+  * quat_scale_to_covar_preci -- gsplat_quat_scale_to_covar.cpp:582-613
+  * projection_ewa_3dgs_fused -- gsplat_projection.cpp:1130-1208 (opacities and
+    Ks get zero gradients; viewspace_points receives the means2d cotangent as
+    the densification proxy; view matrices get a gradient only when they
+    require one)
+  * spherical_harmonics -- gsplat_spherical_harmonics.cpp:670-705 (v_dirs only
+    when dirs require a gradient)
+  * rasterize_to_pixels_3dgs -- gsplat_rasterize.cpp:749-795 (absgrad off)
+Intersection outputs carry no gradient (the reference callers stop_gradient
+them, scanner_points_training_utils.py:1093-1101).
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _gsplat_core as _C
+
+
+def _empty(ref: torch.Tensor) -> torch.Tensor:
+    return torch.zeros(0, dtype=torch.float32, device=ref.device)
+
+
+def _nonempty(t):
+    return t is not None and t.numel() > 0
+
+
+class _QuatScaleToCovarPreci(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, quats, scales, compute_covar, compute_preci, triu):
+        out = _C.quat_scale_to_covar_preci_forward({"quats": quats, "scales": scales}, compute_covar, compute_preci,
+                                                   triu)
+        ctx.save_for_backward(quats, scales)
+        ctx.flags = (compute_covar, compute_preci, triu)
+        return out["covars"], out["precis"]
+
+    @staticmethod
+    def backward(ctx, v_covars, v_precis):
+        quats, scales = ctx.saved_tensors
+        compute_covar, compute_preci, triu = ctx.flags
+        cot = {}
+        if compute_covar:
+            cot["v_covars"] = v_covars.contiguous() if v_covars is not None else None
+        if compute_preci:
+            cot["v_precis"] = v_precis.contiguous() if v_precis is not None else None
+        cot = {k: v for k, v in cot.items() if v is not None}
+        if not cot:
+            return torch.zeros_like(quats), torch.zeros_like(scales), None, None, None
+        out = _C.quat_scale_to_covar_preci_backward({"quats": quats, "scales": scales}, cot, triu)
+        return out["v_quats"], out["v_scales"], None, None, None
+
+
+def quat_scale_to_covar_preci(quats, scales, compute_covar=True, compute_preci=True, triu=True):
+    return _QuatScaleToCovarPreci.apply(quats, scales, compute_covar, compute_preci, triu)
+
+
+class _ProjectionEWA3DGSFused(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means, covars, quats, scales, opacities, viewmats, Ks, viewspace_points, image_width,
+                image_height, eps2d, near_plane, far_plane, radius_clip, calc_compensations, camera_model):
+        inputs = {"means": means, "viewmats": viewmats, "Ks": Ks}
+        for k, v in (("covars", covars), ("quats", quats), ("scales", scales), ("opacities", opacities),
+                     ("viewspace_points", viewspace_points)):
+            if _nonempty(v):
+                inputs[k] = v
+        out = _C.projection_ewa_3dgs_fused_forward(inputs, image_width, image_height, eps2d, near_plane, far_plane,
+                                                   radius_clip, calc_compensations, camera_model)
+        ctx.save_for_backward(means, covars, quats, scales, viewmats, Ks, out["radii"], out["conics"],
+                              out["compensations"])
+        ctx.params = (image_width, image_height, eps2d, calc_compensations, camera_model, _nonempty(covars))
+        ctx.mark_non_differentiable(out["radii"])
+        return out["means2d"], out["depths"], out["conics"], out["compensations"], out["radii"]
+
+    @staticmethod
+    def backward(ctx, v_means2d, v_depths, v_conics, v_compensations, _v_radii):
+        means, covars, quats, scales, viewmats, Ks, radii, conics, comps = ctx.saved_tensors
+        W, H, eps2d, calc_comp, camera_model, use_covars = ctx.params
+        if camera_model != 0:
+            raise RuntimeError("GSPlatProjectionEWA3DGSFused vjp currently supports pinhole only.")
+        shape2 = radii.shape
+        v_means2d = torch.zeros(shape2, dtype=torch.float32, device=means.device) if v_means2d is None else v_means2d
+        v_depths = torch.zeros(shape2[:-1], dtype=torch.float32, device=means.device) if v_depths is None else v_depths
+        v_conics = (torch.zeros(conics.shape, dtype=torch.float32, device=means.device) if v_conics is None
+                    else v_conics)
+        inputs = {"means": means, "viewmats": viewmats, "Ks": Ks}
+        if use_covars:
+            inputs["covars"] = covars
+        else:
+            inputs["quats"] = quats
+            inputs["scales"] = scales
+        fwd = {"radii": radii, "conics": conics}
+        cot = {"v_means2d": v_means2d.contiguous(), "v_depths": v_depths.contiguous(),
+               "v_conics": v_conics.contiguous()}
+        if calc_comp:
+            fwd["compensations"] = comps
+            cot["v_compensations"] = (torch.zeros_like(comps) if v_compensations is None
+                                      else v_compensations.contiguous())
+        needs_viewmats = ctx.needs_input_grad[5]
+        # The forward's own parameters govern the VJP (gsplat_projection.cpp:1151-1177);
+        # near/far/radius_clip only affect culling, already encoded in radii.
+        out = _C.projection_ewa_3dgs_fused_backward(inputs, fwd, cot, W, H, eps2d, camera_model, needs_viewmats)
+        g_covars = out["v_covars"] if use_covars else (torch.zeros_like(covars) if covars is not None else None)
+        g_quats = None if use_covars else out["v_quats"]
+        g_scales = None if use_covars else out["v_scales"]
+        g_opac = None
+        g_view = out["v_viewmats"] if needs_viewmats else None
+        g_vsp = v_means2d if ctx.needs_input_grad[7] else None
+        return (out["v_means"], g_covars, g_quats, g_scales, g_opac, g_view, None, g_vsp) + (None,) * 8
+
+
+def projection_ewa_3dgs_fused(means, viewmats, Ks, image_width, image_height, quats=None, scales=None, covars=None,
+                              opacities=None, viewspace_points=None, eps2d=0.3, near_plane=0.01, far_plane=1e10,
+                              radius_clip=0.0, calc_compensations=False, camera_model=0):
+    """Differentiable projection; returns the reference binding's output dict."""
+    e = _empty(means)
+    m2, d, c, comp, r = _ProjectionEWA3DGSFused.apply(
+        means, covars if covars is not None else e, quats if quats is not None else e,
+        scales if scales is not None else e, opacities if opacities is not None else e, viewmats, Ks,
+        viewspace_points if viewspace_points is not None else e, image_width, image_height, eps2d, near_plane,
+        far_plane, radius_clip, calc_compensations, camera_model)
+    return {"radii": r, "means2d": m2, "depths": d, "conics": c, "compensations": comp,
+            "viewspace_points": viewspace_points}
+
+
+class _SphericalHarmonics(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, degrees_to_use, dirs, coeffs, masks):
+        inputs = {"dirs": dirs, "coeffs": coeffs}
+        if _nonempty(masks):
+            inputs["masks"] = masks
+        colors = _C.spherical_harmonics_forward(degrees_to_use, inputs)
+        ctx.save_for_backward(dirs, coeffs, masks)
+        ctx.degree = degrees_to_use
+        return colors
+
+    @staticmethod
+    def backward(ctx, v_colors):
+        dirs, coeffs, masks = ctx.saved_tensors
+        inputs = {"dirs": dirs, "coeffs": coeffs}
+        if _nonempty(masks):
+            inputs["masks"] = masks
+        compute_v_dirs = ctx.needs_input_grad[1]
+        out = _C.spherical_harmonics_backward(ctx.degree, inputs, {"v_colors": v_colors.contiguous()},
+                                              compute_v_dirs)
+        return None, out["v_dirs"] if compute_v_dirs else None, out["v_coeffs"], None
+
+
+def spherical_harmonics(degrees_to_use, dirs, coeffs, masks=None):
+    return _SphericalHarmonics.apply(degrees_to_use, dirs, coeffs, masks if masks is not None else _empty(dirs))
+
+
+class _RasterizeToPixels3DGS(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, image_width,
+                image_height, tile_size):
+        inputs = {"means2d": means2d, "conics": conics, "colors": colors, "opacities": opacities,
+                  "tile_offsets": tile_offsets, "flatten_ids": flatten_ids}
+        if _nonempty(backgrounds):
+            inputs["backgrounds"] = backgrounds
+        if _nonempty(masks):
+            inputs["masks"] = masks
+        out = _C.rasterize_to_pixels_3dgs_forward(inputs, image_width, image_height, tile_size)
+        ctx.save_for_backward(means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids,
+                              out["render_alphas"], out["last_ids"])
+        ctx.dims = (image_width, image_height, tile_size)
+        ctx.mark_non_differentiable(out["last_ids"])
+        return out["render_colors"], out["render_alphas"], out["last_ids"]
+
+    @staticmethod
+    def backward(ctx, v_render_colors, v_render_alphas, _v_last_ids):
+        (means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, render_alphas,
+         last_ids) = ctx.saved_tensors
+        W, H, ts = ctx.dims
+        inputs = {"means2d": means2d, "conics": conics, "colors": colors, "opacities": opacities,
+                  "tile_offsets": tile_offsets, "flatten_ids": flatten_ids}
+        use_bg = _nonempty(backgrounds)
+        if use_bg:
+            inputs["backgrounds"] = backgrounds
+        if _nonempty(masks):
+            inputs["masks"] = masks
+        if v_render_colors is None:
+            v_render_colors = torch.zeros(render_alphas.shape[:-1] + (colors.shape[-1],), dtype=torch.float32,
+                                          device=colors.device)
+        if v_render_alphas is None:
+            v_render_alphas = torch.zeros_like(render_alphas)
+        out = _C.rasterize_to_pixels_3dgs_backward(
+            inputs, {"render_alphas": render_alphas, "last_ids": last_ids},
+            {"v_render_colors": v_render_colors.contiguous(), "v_render_alphas": v_render_alphas.contiguous()},
+            W, H, ts, False)
+        return (out["v_means2d"], out["v_conics"], out["v_colors"], out["v_opacities"],
+                out["v_backgrounds"] if use_bg else None, None, None, None, None, None, None)
+
+
+def rasterize_to_pixels_3dgs(means2d, conics, colors, opacities, tile_offsets, flatten_ids, image_width, image_height,
+                             tile_size, backgrounds=None, masks=None):
+    """Differentiable rasterization; returns the reference binding's output dict."""
+    e = _empty(means2d)
+    rc, ra, li = _RasterizeToPixels3DGS.apply(means2d, conics, colors, opacities,
+                                             backgrounds if backgrounds is not None else e,
+                                             masks if masks is not None else e, tile_offsets, flatten_ids,
+                                             image_width, image_height, tile_size)
+    return {"render_colors": rc, "render_alphas": ra, "last_ids": li}

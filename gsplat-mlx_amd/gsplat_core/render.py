@@ -1,0 +1,92 @@
+"""Caller-side composition of the operator chain (torch), mirroring the
+reference training call sites:
+
+  camera_center_from_viewmat  scanner_points_training_utils.py:1005-1008
+  sh_colors_for_camera        scanner_points_training_utils.py:1011-1034
+  render_sh_model             scanner_points_training_utils.py:1050-1121
+  render_rgb_model            train_image_fitting_3dgs_mlx.py:165-237 /
+                              render_random_3dgs_png.py:114-168
+  l1_loss                     image L1 term of image_loss_components
+
+Every operator call goes through the differentiable wrappers in
+``gsplat_core.autograd`` (HIP kernels); the glue is plain torch elementwise
+math on the device.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _gsplat_core as _C
+from .autograd import projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs, spherical_harmonics
+
+
+def normalize_quats(quats: torch.Tensor) -> torch.Tensor:
+    """scanner_points_training_utils.py:39-41"""
+    norm = torch.sqrt(torch.sum(quats * quats, dim=-1, keepdim=True))
+    return quats / torch.clamp(norm, min=1.0e-8)
+
+
+def camera_center_from_viewmat(viewmats: torch.Tensor) -> torch.Tensor:
+    rot = viewmats[:, :, :3, :3]
+    trans = viewmats[:, :, :3, 3]
+    return -torch.matmul(rot.transpose(-1, -2), trans[..., None])[..., 0]
+
+
+def sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree):
+    active = (sh_degree + 1) ** 2
+    dirs = means[:, None, :, :] - camera_center_from_viewmat(viewmats)[:, :, None, :]
+    dirs = dirs / torch.clamp(torch.sqrt(torch.sum(dirs * dirs, dim=-1, keepdim=True)), min=1.0e-8)
+    coeffs = torch.cat([features_dc[:, :, None, :], features_rest[:, :, : active - 1, :]], dim=2)
+    coeffs = coeffs[:, None].expand(*dirs.shape[:-1], active, 3)
+    colors = spherical_harmonics(sh_degree, dirs.reshape(-1, 3), coeffs.reshape(-1, active, 3))
+    return torch.clamp((colors + 0.5).reshape(*dirs.shape[:-1], 3), 0.0, 1.0)
+
+
+def tile_grid(width: int, height: int, tile_size: int):
+    return (width + tile_size - 1) // tile_size, (height + tile_size - 1) // tile_size
+
+
+def _intersect(proj, width, height, tile_size):
+    tw, th = tile_grid(width, height, tile_size)
+    isect = _C.intersect_tile_forward(
+        {"means2d": proj["means2d"].detach(), "radii": proj["radii"], "depths": proj["depths"].detach()},
+        1, tile_size, tw, th, True, False)
+    offsets = _C.intersect_offset_forward(isect["isect_ids"], 1, tw, th)
+    return isect, offsets
+
+
+def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks, width,
+                    height, tile_size, sh_degree, viewspace_points=None, background=(0.025, 0.025, 0.025),
+                    far_plane=100.0):
+    """One camera (viewmats [1,1,4,4]); returns the render dict plus radii,
+    tiles_per_gauss and flatten_ids, like the reference."""
+    proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=normalize_quats(quats),
+                                     scales=torch.exp(log_scales), viewspace_points=viewspace_points, eps2d=0.3,
+                                     near_plane=0.01, far_plane=far_plane, radius_clip=0.0,
+                                     calc_compensations=False, camera_model=0)
+    isect, offsets = _intersect(proj, width, height, tile_size)
+    colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)
+    bg = torch.tensor([list(background)], dtype=torch.float32, device=means.device)
+    render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, torch.sigmoid(opacity_logits)[:, None],
+                                      offsets, isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
+    return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],
+            "flatten_ids": isect["flatten_ids"], "isect_ids": isect["isect_ids"], "tile_offsets": offsets}
+
+
+def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, width, height, tile_size,
+                     background=(0.0, 0.0, 0.0), opacities_in_projection=False, far_plane=1e10):
+    opac = torch.sigmoid(opacity_logits)
+    proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=normalize_quats(quats),
+                                     scales=torch.exp(log_scales),
+                                     opacities=opac if opacities_in_projection else None, eps2d=0.3,
+                                     near_plane=0.01, far_plane=far_plane)
+    isect, offsets = _intersect(proj, width, height, tile_size)
+    bg = torch.tensor([list(background)], dtype=torch.float32, device=means.device)
+    render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors[:, None], opac[:, None], offsets,
+                                      isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
+    return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],
+            "flatten_ids": isect["flatten_ids"], "isect_ids": isect["isect_ids"], "tile_offsets": offsets}
+
+
+def l1_loss(image: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    return torch.mean(torch.abs(image - target))

@@ -1,0 +1,176 @@
+"""Seeded synthetic scenes for the benchmark and parity workloads.
+
+numpy ``default_rng(seed)`` float32 arrays, generated on the host; the same
+arrays feed the GPU path and the CPU oracle. Distributions:
+
+  random_forward   N=10,000, 256x256, f=256: means U[-1,1]^3 (z += 4), quats
+                   N(0,1)^4 normalised, scales exp(U[-5,-2]), opacities
+                   sigmoid(N(0,1)), RGB colors U[0,1]^3; forward only
+                   (mirrors scripts/test/render_random_3dgs_png.py:61-168).
+  image_fit        N=100,000, 512x512, f=512: as above with means x,y U[-2,2],
+                   z U[3,6]; target U[0,1]; RGB colors (no SH)
+                   (train_image_fitting_3dgs_mlx.py:165-237, 431-454).
+  sh3_1m           N=1,000,000, 1297x840, f=1150, principal point at the image
+                   centre: means N(0, 2^2 I) + (0,0,6), log-scales N(-4,
+                   0.5^2), quats N(0,1)^4, opacity logits N(0,1), SH degree 3
+                   (DC N(0,0.3^2), rest N(0,0.05^2)); far 100; background 0.025
+                   (scanner_points_training_utils.py:1050-1121).
+  multiview_3m     N=3,000,000, configs as sh3_1m with means centred at the
+                   origin, 8 cameras on a ring of radius 8 looking at it,
+                   1920x1080, f=1600.
+  heavy_6m         N=6,000,000, 3840x2160, f=3000: log-scales N(-2.5, 0.7^2);
+                   30% opacity logits N(3,1), rest N(-1,1); means
+                   x N(0,7^2), y N(0,3.94^2), z N(30,6^2).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import numpy as np
+
+
+@dataclass
+class Scene:
+    name: str
+    width: int
+    height: int
+    tile_size: int
+    means: np.ndarray  # [1, N, 3]
+    quats: np.ndarray  # [1, N, 4] (raw; normalised by the model)
+    log_scales: np.ndarray  # [1, N, 3]
+    opacity_logits: np.ndarray  # [1, N]
+    viewmats: np.ndarray  # [1, C, 4, 4]
+    Ks: np.ndarray  # [1, C, 3, 3]
+    sh_degree: int = -1  # -1: RGB colors, else SH degree
+    colors: np.ndarray | None = None  # [1, N, 3] when sh_degree < 0
+    features_dc: np.ndarray | None = None  # [1, N, 3]
+    features_rest: np.ndarray | None = None  # [1, N, K-1, 3]
+    near_plane: float = 0.01
+    far_plane: float = 1e10
+    background: tuple = (0.0, 0.0, 0.0)
+    opacities_in_projection: bool = False
+    target: np.ndarray | None = None  # [C, H, W, 3]
+    extra: dict = field(default_factory=dict)
+
+    @property
+    def n(self) -> int:
+        return self.means.shape[1]
+
+    @property
+    def n_cameras(self) -> int:
+        return self.viewmats.shape[1]
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def _K(f, cx, cy, C=1):
+    K = np.zeros((1, C, 3, 3), np.float32)
+    K[..., 0, 0] = f
+    K[..., 1, 1] = f
+    K[..., 0, 2] = cx
+    K[..., 1, 2] = cy
+    K[..., 2, 2] = 1
+    return K
+
+
+def _identity_view(C=1):
+    return np.tile(np.eye(4, dtype=np.float32), (1, C, 1, 1))
+
+
+def _ring_views(C, radius):
+    """World-to-camera matrices of C cameras on a horizontal ring looking at
+    the origin (camera +z forward, +y down)."""
+    views = np.zeros((1, C, 4, 4), np.float32)
+    for c in range(C):
+        a = 2 * np.pi * c / C
+        pos = np.array([radius * np.sin(a), 0.0, -radius * np.cos(a)])
+        fwd = -pos / np.linalg.norm(pos)
+        down = np.array([0.0, 1.0, 0.0])
+        right = np.cross(down, fwd)
+        right /= np.linalg.norm(right)
+        down = np.cross(fwd, right)
+        R = np.stack([right, down, fwd])  # rows: camera axes in world coords
+        views[0, c, :3, :3] = R
+        views[0, c, :3, 3] = -R @ pos
+        views[0, c, 3, 3] = 1
+    return views
+
+
+def _sh_features(rng, n, degree):
+    K = (degree + 1) ** 2
+    dc = rng.normal(0, 0.3, (1, n, 3)).astype(np.float32)
+    rest = rng.normal(0, 0.05, (1, n, K - 1, 3)).astype(np.float32)
+    return dc, rest
+
+
+def make_scene(name: str, seed: int = 0, n: int | None = None, width: int | None = None,
+               height: int | None = None, with_target: bool = True) -> Scene:
+    """Builds one of the named workloads; n / width / height override the
+    defaults (used for parity-size variants of the same distributions)."""
+    rng = np.random.default_rng(seed)
+    if name == "random_forward":
+        n = n or 10_000
+        W, H = width or 256, height or 256
+        means = rng.uniform(-1, 1, (1, n, 3)).astype(np.float32)
+        means[..., 2] += 4
+        quats = rng.normal(size=(1, n, 4)).astype(np.float32)
+        log_scales = rng.uniform(-5, -2, (1, n, 3)).astype(np.float32)
+        opac_logits = rng.normal(size=(1, n)).astype(np.float32)
+        colors = rng.uniform(0, 1, (1, n, 3)).astype(np.float32)
+        f = 256.0 * W / 256.0
+        return Scene(name, W, H, 16, means, quats, log_scales, opac_logits, _identity_view(), _K(f, W / 2, H / 2),
+                     colors=colors, opacities_in_projection=True)
+    if name == "image_fit":
+        n = n or 100_000
+        W, H = width or 512, height or 512
+        means = np.stack([rng.uniform(-2, 2, (1, n)), rng.uniform(-2, 2, (1, n)), rng.uniform(3, 6, (1, n))],
+                         -1).astype(np.float32)
+        quats = rng.normal(size=(1, n, 4)).astype(np.float32)
+        log_scales = rng.uniform(-5, -2, (1, n, 3)).astype(np.float32)
+        opac_logits = rng.normal(size=(1, n)).astype(np.float32)
+        colors = rng.uniform(0, 1, (1, n, 3)).astype(np.float32)
+        target = rng.uniform(0, 1, (1, H, W, 3)).astype(np.float32) if with_target else None
+        f = 512.0 * W / 512.0
+        return Scene(name, W, H, 16, means, quats, log_scales, opac_logits, _identity_view(), _K(f, W / 2, H / 2),
+                     colors=colors, target=target)
+    if name in ("sh3_1m", "multiview_3m"):
+        multi = name == "multiview_3m"
+        n = n or (3_000_000 if multi else 1_000_000)
+        W, H = (width or 1920, height or 1080) if multi else (width or 1297, height or 840)
+        means = rng.normal(0, 2, (1, n, 3)).astype(np.float32)
+        if not multi:
+            means[..., 2] += 6
+        quats = rng.normal(size=(1, n, 4)).astype(np.float32)
+        log_scales = rng.normal(-4, 0.5, (1, n, 3)).astype(np.float32)
+        opac_logits = rng.normal(size=(1, n)).astype(np.float32)
+        dc, rest = _sh_features(rng, n, 3)
+        if multi:
+            C = 8
+            views, Ks = _ring_views(C, 8.0), _K(1600.0 * W / 1920.0, W / 2, H / 2, C)
+        else:
+            C = 1
+            views, Ks = _identity_view(), _K(1150.0 * W / 1297.0, W / 2, H / 2)
+        target = rng.uniform(0, 1, (C, H, W, 3)).astype(np.float32) if with_target else None
+        return Scene(name, W, H, 16, means, quats, log_scales, opac_logits, views, Ks, sh_degree=3, features_dc=dc,
+                     features_rest=rest, far_plane=100.0, background=(0.025, 0.025, 0.025), target=target)
+    if name == "heavy_6m":
+        n = n or 6_000_000
+        W, H = width or 3840, height or 2160
+        means = np.stack([rng.normal(0, 7, (1, n)), rng.normal(0, 3.94, (1, n)), rng.normal(30, 6, (1, n))],
+                         -1).astype(np.float32)
+        quats = rng.normal(size=(1, n, 4)).astype(np.float32)
+        log_scales = rng.normal(-2.5, 0.7, (1, n, 3)).astype(np.float32)
+        hi = rng.random((1, n)) < 0.3
+        opac_logits = np.where(hi, rng.normal(3, 1, (1, n)), rng.normal(-1, 1, (1, n))).astype(np.float32)
+        dc, rest = _sh_features(rng, n, 3)
+        target = rng.uniform(0, 1, (1, H, W, 3)).astype(np.float32) if with_target else None
+        return Scene(name, W, H, 16, means, quats, log_scales, opac_logits, _identity_view(),
+                     _K(3000.0 * W / 3840.0, W / 2, H / 2), sh_degree=3, features_dc=dc, features_rest=rest,
+                     far_plane=100.0, background=(0.025, 0.025, 0.025), target=target)
+    raise ValueError(f"unknown scene {name!r}")
+
+
+def opacities(scene: Scene) -> np.ndarray:
+    return _sigmoid(scene.opacity_logits).astype(np.float32)

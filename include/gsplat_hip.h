@@ -1,0 +1,212 @@
+/*
+ * gsplat_hip.h -- C ABI of the MI355X (gfx950) splatting operator chain.
+ *
+ * Plain pointers, sizes and a HIP stream (passed as void*); no torch or MLX
+ * types. Every pointer is device memory; inputs are read-only and C-contiguous
+ * in the reference layouts (AoS float32, int32 radii/offsets/ids, int64 keys).
+ * Outputs are caller-allocated; each entry point writes every element of its
+ * outputs (including zeros for culled / masked entries), so callers need not
+ * clear them. Work is enqueued on `stream` and returns without synchronizing,
+ * except where a function says otherwise.
+ *
+ * Return value: GSPLAT_OK (0) or a GSPLAT_ERR_* code; gsplat_hip_last_error()
+ * then returns a message for the calling thread.
+ *
+ * Each entry point replaces the device half (`eval_gpu`) of one reference MLX
+ * primitive, or an MLX library op on the path; the reference file:line of
+ * the interface it replaces is given beside it.
+ */
+#ifndef GSPLAT_HIP_H_
+#define GSPLAT_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  GSPLAT_OK = 0,
+  GSPLAT_ERR_INVALID_ARGUMENT = 1,
+  GSPLAT_ERR_HIP = 2,
+  GSPLAT_ERR_WORKSPACE_TOO_SMALL = 3,
+};
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* gsplat_hip_last_error(void);
+
+/* ABI version of this library (major * 100 + minor). */
+int gsplat_hip_abi_version(void);
+
+/* ---------------------------------------------------------------------------
+ * quat_scale_to_covar_preci
+ * Replaces GSPlatQuatScaleToCovarPreci(/Backward)::eval_gpu
+ * (gsplat_core/gsplat_quat_scale_to_covar.cpp:470-552,
+ *  gsplat_core/include/gsplat_quat_scale_to_covar.h:42-46).
+ * quats [n,4] (w,x,y,z), scales [n,3]; covars/precis [n,6] (triu) or [n,3,3];
+ * a disabled output may be NULL. Backward: v_covars / v_precis may be NULL
+ * (not requested); v_quats [n,4], v_scales [n,3].
+ * ------------------------------------------------------------------------- */
+int gsplat_hip_quat_scale_to_covar_preci_fwd(const float* quats, const float* scales, int64_t n,
+                                             int32_t compute_covar, int32_t compute_preci,
+                                             int32_t triu, float* covars, float* precis,
+                                             void* stream);
+int gsplat_hip_quat_scale_to_covar_preci_bwd(const float* quats, const float* scales,
+                                             const float* v_covars, const float* v_precis,
+                                             int64_t n, int32_t triu, float* v_quats,
+                                             float* v_scales, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused EWA projection.
+ * Replaces GSPlatProjectionEWA3DGSFused(/Backward)::eval_gpu
+ * (gsplat_core/gsplat_projection.cpp:654-855,
+ *  gsplat_core/include/gsplat_projection.h:12-77). Field meanings follow
+ * ProjectionEWA3DGSFusedParams (gsplat_projection.h:12-23).
+ * ------------------------------------------------------------------------- */
+typedef struct gsplat_projection_params {
+  int32_t image_width;
+  int32_t image_height;
+  float eps2d;
+  float near_plane;
+  float far_plane;
+  float radius_clip;
+  int32_t calc_compensations;
+  int32_t camera_model; /* 0 pinhole, 1 orthographic, 2 fisheye (forward only) */
+  int32_t use_covars;
+  int32_t use_opacities;
+} gsplat_projection_params;
+
+/* means [B,N,3]; covars [B,N,6] (use_covars) or quats [B,N,4] + scales
+ * [B,N,3]; opacities [B,N] (use_opacities, else NULL); viewmats [B,C,4,4]
+ * row-major world-to-camera; Ks [B,C,3,3]. Outputs over [B,C,N]: radii
+ * (int32, x2), means2d (x2), depths, conics (x3), compensations
+ * (calc_compensations, else NULL). */
+int gsplat_hip_projection_fwd(const float* means, const float* covars, const float* quats,
+                              const float* scales, const float* opacities,
+                              const float* viewmats, const float* Ks, int64_t B, int64_t C,
+                              int64_t N, const gsplat_projection_params* params,
+                              int32_t* radii, float* means2d, float* depths, float* conics,
+                              float* compensations, void* stream);
+
+/* Pinhole only (as the reference). Gradients w.r.t. means [B,N,3] and either
+ * covars [B,N,6] or quats [B,N,4] + scales [B,N,3] (the other pair NULL);
+ * v_viewmats [B,C,4,4] when non-NULL (needs a workspace of
+ * gsplat_hip_projection_bwd_workspace_size bytes, else workspace may be NULL).
+ * compensations / v_compensations are NULL unless calc_compensations. */
+size_t gsplat_hip_projection_bwd_workspace_size(int64_t B, int64_t C, int64_t N,
+                                                int32_t viewmats_grad);
+int gsplat_hip_projection_bwd(const float* means, const float* covars, const float* quats,
+                              const float* scales, const float* viewmats, const float* Ks,
+                              int64_t B, int64_t C, int64_t N,
+                              const gsplat_projection_params* params, const int32_t* radii,
+                              const float* conics, const float* compensations,
+                              const float* v_means2d, const float* v_depths,
+                              const float* v_conics, const float* v_compensations,
+                              float* v_means, float* v_covars, float* v_quats, float* v_scales,
+                              float* v_viewmats, void* workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Real spherical harmonics, degrees 0..4.
+ * Replaces GSPlatSphericalHarmonics(/Backward)::eval_gpu
+ * (gsplat_core/gsplat_spherical_harmonics.cpp:556-658,
+ *  gsplat_core/include/gsplat_spherical_harmonics.h:35-39).
+ * dirs [n,3], coeffs [n,K,3] with K >= (degree+1)^2, masks [n] (uint8/bool,
+ * NULL = all on). Backward: v_dirs [n,3] (NULL = not requested),
+ * v_coeffs [n,K,3].
+ * ------------------------------------------------------------------------- */
+int gsplat_hip_spherical_harmonics_fwd(int32_t degree, const float* dirs, const float* coeffs,
+                                       const uint8_t* masks, int64_t n, int64_t K,
+                                       float* colors, void* stream);
+int gsplat_hip_spherical_harmonics_bwd(int32_t degree, const float* dirs, const float* coeffs,
+                                       const uint8_t* masks, const float* v_colors, int64_t n,
+                                       int64_t K, float* v_dirs, float* v_coeffs, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Tile intersection (dense AABB binning).
+ * count + exclusive scan: replaces GSPlatIntersectTileCount::eval_gpu
+ * (gsplat_core/gsplat_intersect.cpp:340-381) followed by mx::cumsum
+ * (gsplat_intersect.cpp:196-211). means2d [numel,2], radii [numel,2] int32;
+ * writes tiles_per_gauss [numel] and offsets [numel] (exclusive scan), and
+ * the total intersection count as one int64 at *total_dev (device memory).
+ * ------------------------------------------------------------------------- */
+size_t gsplat_hip_isect_count_scan_workspace_size(int64_t numel);
+int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* radii, int64_t numel,
+                                int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                int32_t* tiles_per_gauss, int32_t* offsets, int64_t* total_dev,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Exclusive scan of int32 values (out may alias in); replaces mx::cumsum
+ * (inclusive=false) in gsplat_intersect_tile_offsets
+ * (gsplat_core/gsplat_intersect.cpp:196-211). The int64 total is written to
+ * *total_dev (device memory) when non-NULL. Partial sums must fit int32. */
+size_t gsplat_hip_exclusive_scan_i32_workspace_size(int64_t n);
+int gsplat_hip_exclusive_scan_i32(const int32_t* in, int32_t* out, int64_t n, int64_t* total_dev,
+                                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Replaces GSPlatIntersectTileEncode::eval_gpu (gsplat_intersect.cpp:487-538):
+ * key = image << (32 + tile_bits) | tile << 32 | float_bits(depth), written
+ * Gaussian-major, row-major within each Gaussian's tile rectangle, with
+ * flatten_id = global (image * N + n) index. depths [numel], offsets from
+ * the scan, n_isects = total. numel = I * n_per_image. */
+int gsplat_hip_isect_encode(const float* means2d, const int32_t* radii, const float* depths,
+                            const int32_t* offsets, int64_t I, int64_t numel,
+                            int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                            int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
+                            void* stream);
+
+/* Stable ascending sort of int64 keys (non-negative) carrying int32 values;
+ * replaces mx::argsort + 2x mx::take (gsplat_intersect.cpp:266-286). Only
+ * the low `key_bits` bits are compared (keys must be < 2^key_bits). Inputs
+ * are left unchanged. */
+size_t gsplat_hip_isect_sort_workspace_size(int64_t n);
+int gsplat_hip_isect_sort(const int64_t* keys_in, const int32_t* vals_in, int64_t n,
+                          int32_t key_bits, int64_t* keys_out, int32_t* vals_out,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* Replaces GSPlatIntersectOffset::eval_gpu (gsplat_intersect.cpp:643-681):
+ * offsets [I, tile_height, tile_width] = lower_bound of (image << tile_bits |
+ * tile) over the sorted isect_ids >> 32. */
+int gsplat_hip_isect_offset(const int64_t* isect_ids, int64_t n_isects, int32_t I,
+                            int32_t tile_width, int32_t tile_height, int32_t* offsets,
+                            void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Rasterization to pixels (front-to-back alpha compositing).
+ * Replaces GSPlatRasterizeToPixels3DGS(/Backward)::eval_gpu
+ * (gsplat_core/gsplat_rasterize.cpp:571-738,
+ *  gsplat_core/include/gsplat_rasterize.h:67-71).
+ * means2d [I,N,2], conics [I,N,3], colors [I,N,channels], opacities [I,N],
+ * backgrounds [I,channels] (NULL = black), masks [I,th,tw] (NULL = all on),
+ * tile_offsets [I,th,tw], flatten_ids [n_isects].
+ * Forward outputs: render_colors [I,H,W,channels], render_alphas [I,H,W],
+ * last_ids [I,H,W]. Backward outputs (accumulated over all pixels):
+ * v_means2d_abs (NULL unless absgrad), v_means2d, v_conics, v_colors,
+ * v_opacities, v_backgrounds (NULL unless backgrounds).
+ * ------------------------------------------------------------------------- */
+int gsplat_hip_rasterize_fwd(const float* means2d, const float* conics, const float* colors,
+                             const float* opacities, const float* backgrounds,
+                             const uint8_t* masks, const int32_t* tile_offsets,
+                             const int32_t* flatten_ids, int64_t I, int64_t N, int32_t channels,
+                             int32_t image_width, int32_t image_height, int32_t tile_size,
+                             int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                             float* render_colors, float* render_alphas, int32_t* last_ids,
+                             void* stream);
+int gsplat_hip_rasterize_bwd(const float* means2d, const float* conics, const float* colors,
+                             const float* opacities, const float* backgrounds,
+                             const uint8_t* masks, const int32_t* tile_offsets,
+                             const int32_t* flatten_ids, int64_t I, int64_t N, int32_t channels,
+                             int32_t image_width, int32_t image_height, int32_t tile_size,
+                             int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                             const float* render_alphas, const int32_t* last_ids,
+                             const float* v_render_colors, const float* v_render_alphas,
+                             float* v_means2d_abs, float* v_means2d, float* v_conics,
+                             float* v_colors, float* v_opacities, float* v_backgrounds,
+                             void* stream);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* GSPLAT_HIP_H_ */
