@@ -1,0 +1,353 @@
+#!/usr/bin/env python3
+"""Benchmark: forward+backward of the splatting chain on one MI355X.
+
+Workload (default ``sh3_1m``): 1,000,000 Gaussians, SH degree 3, one
+1297x840 camera; one step = projection -> tile intersection (count, scan,
+count read-back, encode, radix sort) -> tile offsets -> SH colors ->
+rasterize -> L1 loss -> backward through rasterize, SH and projection to the
+Gaussian parameters (autograd, as the reference training step
+scanner_points_training_utils.py:2076-2123 without the optimizer). Inputs are
+seeded synthetic arrays resident on the GPU before timing.
+
+Prints ONE JSON line on stdout (diagnostics go to stderr):
+  value = Mpix/s of the whole job (pixels rendered fwd+bwd per second),
+  ms_per_step, roofline of the dominant kernel (per-kernel durations from HIP
+  events recorded around each launch, on the launch stream, over the timed
+  steps), and the CPU baseline (the oracle, single-threaded, on this host).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "gsplat-mlx_amd"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+FP32_PEAK_TFLOPS = 157.3  # MI355X FP32 (vector and matrix)
+
+# Algorithmic work per unit (minimum read-once/write-once bytes, or flops per
+# rasterizer evaluation), per kernel; units are Gaussians (G), intersections
+# (M) or evaluated (pixel, list entry) pairs (E).
+FWD_FLOPS_PER_EVAL = 27
+BWD_FLOPS_PER_EVAL = 75
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", default="sh3_1m", choices=["sh3_1m", "image_fit", "random_forward"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-band-rows", type=int, default=6, help="tile rows of the CPU rasterize sample")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="first run a device copy of this many MiB (counter calibration for rocprofv3 --pmc)")
+    return ap.parse_args()
+
+
+class Profiler:
+    """ctypes view of the C ABI's opt-in kernel timing."""
+
+    def __init__(self):
+        path = os.path.join(ROOT, "gsplat-mlx_amd", "gsplat_core", "libgsplat_hip.so")
+        self.lib = ctypes.CDLL(path)
+        self.lib.gsplat_hip_profile_report.restype = ctypes.c_size_t
+        self.lib.gsplat_hip_profile_report.argtypes = [ctypes.c_char_p, ctypes.c_size_t]
+
+    def enable(self, on):
+        self.lib.gsplat_hip_profile_enable(1 if on else 0)
+
+    def reset(self):
+        self.lib.gsplat_hip_profile_reset()
+
+    def report(self):
+        n = self.lib.gsplat_hip_profile_report(None, 0)
+        buf = ctypes.create_string_buffer(n + 1)
+        self.lib.gsplat_hip_profile_report(buf, n + 1)
+        out = {}
+        for line in buf.value.decode().splitlines():
+            name, cnt, ms = line.split("\t")
+            out[name] = (int(cnt), float(ms))
+        return out
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (every box here has one GPU); "
+              "run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import gsplat_core  # noqa: F401  (loads the HIP extension; fails loudly if missing)
+    from gsplat_core import render as R
+    from gsplat_core.scenes import make_scene
+
+    dev = torch.device("cuda:0")
+    if args.copy_probe_mib > 0:
+        n = args.copy_probe_mib * (1 << 20) // 4
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy probe: 3 x {args.copy_probe_mib} MiB device copy (reads and writes {args.copy_probe_mib} MiB each)")
+        del src, dst
+    t0 = time.time()
+    scene = make_scene(args.workload, seed=0)
+    log(f"[bench] scene {args.workload}: N={scene.n} {scene.width}x{scene.height} ({time.time() - t0:.1f}s)")
+
+    def param(a):
+        return torch.from_numpy(np.ascontiguousarray(a)).to(dev).requires_grad_(True)
+
+    means = param(scene.means)
+    quats = param(scene.quats)
+    log_scales = param(scene.log_scales)
+    opacity_logits = param(scene.opacity_logits)
+    viewmats = torch.from_numpy(scene.viewmats).to(dev)
+    Ks = torch.from_numpy(scene.Ks).to(dev)
+    sh = scene.sh_degree >= 0
+    if sh:
+        features_dc = param(scene.features_dc)
+        features_rest = param(scene.features_rest)
+        params = [means, quats, log_scales, features_dc, features_rest, opacity_logits]
+    else:
+        colors = param(scene.colors)
+        params = [means, quats, log_scales, colors, opacity_logits]
+    viewspace = torch.zeros((1, 1, scene.n, 2), device=dev, requires_grad=True)
+    target = torch.from_numpy(scene.target).to(dev) if scene.target is not None else None
+    W, H, ts = scene.width, scene.height, scene.tile_size
+    forward_only = target is None
+
+    def step():
+        for p in params + [viewspace]:
+            p.grad = None
+        if sh:
+            out = R.render_sh_model(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks,
+                                    W, H, ts, scene.sh_degree, viewspace_points=viewspace,
+                                    background=scene.background, far_plane=scene.far_plane)
+        else:
+            out = R.render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, W, H, ts,
+                                     background=scene.background,
+                                     opacities_in_projection=scene.opacities_in_projection,
+                                     far_plane=scene.far_plane)
+        if not forward_only:
+            loss = R.l1_loss(out["render_colors"], target)
+            loss.backward()
+        return out
+
+    prof = Profiler()
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Headline: K steps, no profiling events.
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    t_total = time.perf_counter() - t_start
+    ms_per_step = 1000.0 * t_total / args.steps
+    mpix = scene.n_cameras * W * H / 1e6
+    value = mpix * args.steps / t_total
+    log(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} Mpix/s")
+
+    # Same K steps again with per-kernel HIP events (launch stream) for the roofline.
+    prof.reset()
+    prof.enable(True)
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    t_prof = 1000.0 * (time.perf_counter() - tp) / args.steps
+    prof.enable(False)
+    kernels = prof.report()
+    log(f"[bench] profiled pass: {t_prof:.3f} ms/step")
+    per_step = {k: (c / args.steps, ms / args.steps) for k, (c, ms) in kernels.items()}
+    for k, (c, ms) in sorted(per_step.items(), key=lambda kv: -kv[1][1]):
+        log(f"[bench]   {k:28s} {c:5.1f} launches/step {ms * 1000:9.1f} us/step")
+
+    # Work units of this step.
+    N = scene.n
+    M = int(out["isect_ids"].numel())
+    offsets = out["tile_offsets"].reshape(-1).long()
+    ends = torch.cat([offsets[1:], torch.tensor([M], device=dev)])
+    th, tw = out["tile_offsets"].shape[-2:]
+    pix_tile = (torch.arange(H, device=dev)[:, None] // ts) * tw + (torch.arange(W, device=dev)[None, :] // ts)
+    start_p = offsets[pix_tile]
+    end_p = ends[pix_tile]
+    last = out["last_ids"].reshape(H, W).long()
+    e_fwd_max = int(torch.sum(end_p - start_p))  # entries examined without early termination
+    e_bwd = int(torch.clamp(torch.minimum(last, end_p - 1) - start_p + 1, min=0).sum())
+    K = (scene.sh_degree + 1) ** 2 if sh else 0
+    units = {
+        "raster_bwd": ("flops", BWD_FLOPS_PER_EVAL * e_bwd),
+        "raster_fwd": ("flops", FWD_FLOPS_PER_EVAL * e_fwd_max),
+        "sort_scatter": ("bytes", 24 * M),
+        "sort_histogram": ("bytes", 8 * M),
+        "sh_bwd": ("bytes", (12 + 12 * K + 12 + 12 + 12 * K) * N),
+        "sh_fwd": ("bytes", (12 + 12 * K + 12) * N),
+        "projection_fwd": ("bytes", 72 * N),
+        "projection_bwd": ("bytes", 124 * N),
+        "isect_count_scan": ("bytes", 24 * N),
+        "isect_encode": ("bytes", 24 * N + 12 * M),
+        "isect_offsets": ("bytes", 8 * M),
+    }
+    dom = max(per_step, key=lambda k: per_step[k][1])
+    calls, ms_step = per_step[dom]
+    avg_ms = ms_step / calls
+    roofline = None
+    if dom in units:
+        kind, amount = units[dom]
+        per_launch = amount  # one launch per step for every kernel in the table except the sort passes
+        if dom.startswith("sort_"):
+            per_launch = amount  # each pass moves the whole key/value array once
+        if kind == "flops":
+            achieved = per_launch / (avg_ms * 1e-3) / 1e12
+            roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
+                        "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                        "kernel": dom, "avg_ms": round(avg_ms, 4),
+                        "note": "compute roofline: FP32 VALU (no MFMA on this path), peak = MI355X FP32"}
+        else:
+            achieved = per_launch / (avg_ms * 1e-3) / 1e9
+            roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                        "avg_ms": round(avg_ms, 4)}
+    log(f"[bench] N={N} M={M} E_fwd(no termination)={e_fwd_max} E_bwd={e_bwd} dominant={dom} {avg_ms:.4f} ms")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(scene, args.cpu_band_rows, mpix)
+
+    line = {
+        "metric": "fwd+bwd ms/frame & Mpix/s, 1M Gaussians SH3 1297x840; % of HBM/VALU roofline",
+        "value": round(value, 2),
+        "unit": "Mpix/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy scene, resident in HBM)",
+        "config": {"workload": f"{args.workload}: {N} Gaussians, SH degree {scene.sh_degree}, "
+                               f"{scene.n_cameras}x{W}x{H}, tile {ts}, forward+backward (L1 loss)",
+                   "n_gaussians": N, "image": [W, H], "n_isects": M, "sh_degree": scene.sh_degree},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels_us_per_step": {k: round(v[1] * 1000, 1) for k, v in sorted(per_step.items())},
+    }
+    print(json.dumps(line), flush=True)
+
+
+def cpu_baseline(scene, band_rows, mpix):
+    """The oracle (single-threaded C++, this host) over a bounded sample of the
+    same frame: every per-Gaussian and per-intersection stage on the full
+    scene; rasterize forward+backward on a band of `band_rows` tile rows
+    through the image centre, scaled to the full frame by its share of
+    intersections. Returns ms/frame and Mpix/s."""
+    import numpy as np
+
+    sys.path.insert(0, ROOT)
+    from oracle import oracle as O
+
+    O.build()
+    t = {}
+    clock = time.perf_counter
+    W, H, ts = scene.width, scene.height, scene.tile_size
+    tw, th = (W + ts - 1) // ts, (H + ts - 1) // ts
+    quats = scene.quats / np.maximum(np.linalg.norm(scene.quats, axis=-1, keepdims=True), 1e-8)
+    scales = np.exp(scene.log_scales)
+    opac = (1 / (1 + np.exp(-scene.opacity_logits))).astype(np.float32)
+    sh = scene.sh_degree >= 0
+
+    c = clock()
+    proj = O.projection_forward(scene.means, scene.viewmats, scene.Ks, W, H, quats=quats.astype(np.float32),
+                                scales=scales.astype(np.float32), far_plane=scene.far_plane,
+                                opacities=opac if scene.opacities_in_projection else None)
+    t["projection_fwd"] = clock() - c
+    c = clock()
+    isect = O.isect_tile(proj["means2d"], proj["radii"], proj["depths"], 1, ts, tw, th)
+    offs = O.isect_offset(isect["isect_ids"], 1, tw, th)
+    t["isect+sort+offsets"] = clock() - c
+    M = isect["isect_ids"].size
+    if sh:
+        K = (scene.sh_degree + 1) ** 2
+        campos = -scene.viewmats[0, 0, :3, :3].T @ scene.viewmats[0, 0, :3, 3]
+        dirs = scene.means[0] - campos
+        dirs = (dirs / np.maximum(np.linalg.norm(dirs, axis=-1, keepdims=True), 1e-8)).astype(np.float32)
+        coeffs = np.concatenate([scene.features_dc[0][:, None], scene.features_rest[0][:, :K - 1]], 1)
+        c = clock()
+        colors = O.sh_forward(scene.sh_degree, dirs, coeffs)
+        t["sh_fwd"] = clock() - c
+        colors = np.clip(colors + 0.5, 0, 1)[None, None]
+    else:
+        colors = scene.colors[:, None]
+    # rasterize band: tile rows [r0, r0 + band_rows)
+    r0 = max(0, th // 2 - band_rows // 2)
+    r1 = min(th, r0 + band_rows)
+    o = offs[0].ravel()
+    b_start = int(o[r0 * tw])
+    b_end = int(o[r1 * tw]) if r1 < th else M
+    band_offs = (offs[:, r0:r1] - b_start).astype(np.int32)
+    band_ids = isect["flatten_ids"][b_start:b_end]
+    m2 = proj["means2d"].copy()
+    m2[..., 1] -= r0 * ts
+    bh = min(H, r1 * ts) - r0 * ts
+    bg = np.array([scene.background], np.float32)
+    c = clock()
+    fwd = O.raster_forward(m2, proj["conics"], colors, opac[:, None], band_offs, band_ids, W, bh, ts, backgrounds=bg)
+    t_rf = clock() - c
+    if scene.target is not None:
+        tgt = scene.target[:, r0 * ts:r0 * ts + bh]
+        v_rc = (np.sign(fwd["render_colors"] - tgt) / (H * W * 3)).astype(np.float32)
+        c = clock()
+        bwd = O.raster_backward(m2, proj["conics"], colors, opac[:, None], band_offs, band_ids, W, bh, ts,
+                                fwd["render_alphas"], fwd["last_ids"], v_rc, np.zeros_like(fwd["render_alphas"]),
+                                backgrounds=bg)
+        t_rb = clock() - c
+        share = M / max(1, b_end - b_start)
+        t["raster_fwd (scaled)"] = t_rf * share
+        t["raster_bwd (scaled)"] = t_rb * share
+        v_colors = bwd["v_colors"][0, 0]
+        if sh:
+            c = clock()
+            O.sh_backward(scene.sh_degree, dirs, coeffs, v_colors)
+            t["sh_bwd"] = clock() - c
+        c = clock()
+        O.projection_backward(scene.means, scene.viewmats, scene.Ks, W, H, proj["radii"], proj["conics"],
+                              bwd["v_means2d"], np.zeros_like(proj["depths"]), bwd["v_conics"],
+                              quats=quats.astype(np.float32), scales=scales.astype(np.float32))
+        t["projection_bwd"] = clock() - c
+    else:
+        t["raster_fwd (scaled)"] = t_rf * M / max(1, b_end - b_start)
+        share = M / max(1, b_end - b_start)
+    total_s = sum(t.values())
+    measured = total_s - t.get("raster_fwd (scaled)", 0) - t.get("raster_bwd (scaled)", 0) + \
+        (t.get("raster_fwd (scaled)", 0) + t.get("raster_bwd (scaled)", 0)) / share
+    log("[bench] cpu baseline stages (s): " + ", ".join(f"{k}={v:.3f}" for k, v in t.items()))
+    return {"value": round(mpix / total_s, 4), "unit": "Mpix/s", "cores": 1, "kind": "port",
+            "ms_per_frame": round(1000 * total_s, 1),
+            "sample": (f"oracle (plain C++, 1 thread) on this host: projection, SH, intersection, sort, offsets "
+                       f"and their backwards on all {scene.n} Gaussians / {M} intersections; rasterize fwd+bwd on "
+                       f"tile rows {r0}-{r1 - 1} ({b_end - b_start} intersections) scaled by the frame's "
+                       f"intersection share x{share:.2f}; {measured:.1f} s of CPU work measured")}
+
+
+if __name__ == "__main__":
+    main()

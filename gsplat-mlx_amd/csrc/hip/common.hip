@@ -1,9 +1,16 @@
-// Error plumbing and small utility kernels shared by every entry point.
+// Error plumbing, opt-in kernel timing and small utility kernels shared by
+// every entry point.
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
 #include "common.hpp"
 
 namespace gsplat_hip {
-
 namespace {
+
 thread_local std::string g_last_error;
 
 __global__ void fill_zero_u32(uint32_t* __restrict__ p, int64_t n) {
@@ -15,7 +22,56 @@ __global__ void fill_zero_u8(uint8_t* __restrict__ p, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
 }
+
+struct TimedLaunch {
+  const char* name;
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+
+bool g_profile = false;
+std::vector<TimedLaunch> g_pending;
+std::map<std::string, std::pair<int64_t, double>> g_totals;  // name -> (launches, total ms)
+
+void drain_pending() {
+  for (const TimedLaunch& t : g_pending) {
+    float ms = 0.0f;
+    if (hipEventSynchronize(t.stop) == hipSuccess && hipEventElapsedTime(&ms, t.start, t.stop) == hipSuccess) {
+      auto& tot = g_totals[t.name];
+      tot.first += 1;
+      tot.second += ms;
+    }
+    (void)hipEventDestroy(t.start);
+    (void)hipEventDestroy(t.stop);
+  }
+  g_pending.clear();
+}
+
 }  // namespace
+
+KernelTimer::KernelTimer(const char* name, hipStream_t stream) : name_(name), stream_(stream) {
+  if (!g_profile) return;
+  if (hipEventCreate(&start_) != hipSuccess) {
+    start_ = nullptr;
+    return;
+  }
+  if (hipEventRecord(start_, stream_) != hipSuccess) {
+    (void)hipEventDestroy(start_);
+    start_ = nullptr;
+  }
+}
+
+KernelTimer::~KernelTimer() {
+  if (!start_) return;
+  hipEvent_t stop = nullptr;
+  if (hipEventCreate(&stop) == hipSuccess && hipEventRecord(stop, stream_) == hipSuccess) {
+    g_pending.push_back({name_, start_, stop});
+    if (g_pending.size() > 4096) drain_pending();
+  } else {
+    (void)hipEventDestroy(start_);
+    if (stop) (void)hipEventDestroy(stop);
+  }
+}
 
 void set_error(const std::string& msg) { g_last_error = msg; }
 
@@ -29,6 +85,7 @@ int check_launch(const char* what) { return check_hip(hipGetLastError(), what); 
 
 int fill_zero(void* ptr, int64_t bytes, hipStream_t stream) {
   if (bytes <= 0) return GSPLAT_OK;
+  KernelTimer timer("fill_zero", stream);
   if (reinterpret_cast<uintptr_t>(ptr) % 4 == 0 && bytes % 4 == 0) {
     const int64_t n = bytes / 4;
     const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
@@ -44,3 +101,27 @@ int fill_zero(void* ptr, int64_t bytes, hipStream_t stream) {
 extern "C" const char* gsplat_hip_last_error(void) { return gsplat_hip::g_last_error.c_str(); }
 
 extern "C" int gsplat_hip_abi_version(void) { return 100; }
+
+extern "C" void gsplat_hip_profile_enable(int32_t enable) { gsplat_hip::g_profile = enable != 0; }
+
+extern "C" void gsplat_hip_profile_reset(void) {
+  gsplat_hip::drain_pending();
+  gsplat_hip::g_totals.clear();
+}
+
+extern "C" size_t gsplat_hip_profile_report(char* buf, size_t buf_len) {
+  gsplat_hip::drain_pending();
+  std::string out;
+  for (const auto& kv : gsplat_hip::g_totals) {
+    char line[256];
+    std::snprintf(line, sizeof(line), "%s\t%lld\t%.6f\n", kv.first.c_str(), static_cast<long long>(kv.second.first),
+                  kv.second.second);
+    out += line;
+  }
+  if (buf && buf_len > 0) {
+    const size_t n = std::min(out.size(), buf_len - 1);
+    std::memcpy(buf, out.data(), n);
+    buf[n] = '\0';
+  }
+  return out.size();
+}

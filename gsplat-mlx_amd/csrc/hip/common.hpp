@@ -43,6 +43,21 @@ inline unsigned grid_for(int64_t n, int block) {
 // Grid dimension limit for x (HIP: 2^31 - 1) -- callers check before launch.
 constexpr int64_t kMaxGridX = 2147483647LL;
 
+// Brackets the kernel launches of its scope with HIP events on `stream` while
+// profiling is enabled (gsplat_hip_profile_enable); no-op otherwise.
+class KernelTimer {
+ public:
+  KernelTimer(const char* name, hipStream_t stream);
+  ~KernelTimer();
+  KernelTimer(const KernelTimer&) = delete;
+  KernelTimer& operator=(const KernelTimer&) = delete;
+
+ private:
+  const char* name_;
+  hipStream_t stream_;
+  hipEvent_t start_ = nullptr;
+};
+
 // Zero-fill a float/int buffer with a kernel (graph-capture safe, unlike a
 // memset node).
 int fill_zero(void* ptr, int64_t bytes, hipStream_t stream);

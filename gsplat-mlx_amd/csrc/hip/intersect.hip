@@ -208,15 +208,24 @@ extern "C" int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* 
   }
   const int64_t nb = scan_num_blocks(numel);
   int64_t* sums = static_cast<int64_t*>(workspace);
-  count_scan_local_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(means2d, radii, numel, tile_size,
-                                                                          tile_width, tile_height, tiles_per_gauss,
-                                                                          offsets, sums);
+  {
+    KernelTimer timer("isect_count_scan", s);
+    count_scan_local_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(means2d, radii, numel, tile_size,
+                                                                            tile_width, tile_height, tiles_per_gauss,
+                                                                            offsets, sums);
+  }
   int rc = check_launch("intersect_tile_count");
   if (rc) return rc;
-  block_sums_scan_kernel<<<1, kScanBlock, 0, s>>>(sums, nb, total_dev);
+  {
+    KernelTimer timer("scan_block_sums", s);
+    block_sums_scan_kernel<<<1, kScanBlock, 0, s>>>(sums, nb, total_dev);
+  }
   rc = check_launch("intersect_tile_offsets (block sums)");
   if (rc || nb == 1) return rc;
-  add_block_prefix_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(offsets, numel, sums);
+  {
+    KernelTimer timer("scan_fixup", s);
+    add_block_prefix_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(offsets, numel, sums);
+  }
   return check_launch("intersect_tile_offsets (fixup)");
 }
 
@@ -237,9 +246,12 @@ extern "C" int gsplat_hip_isect_encode(const float* means2d, const int32_t* radi
   if (!means2d || !radii || !depths || !offsets || !isect_ids || !flatten_ids)
     return invalid("intersect_tile_encode: null pointer.");
   const int64_t nb = (numel + kEncodeG - 1) / kEncodeG;
-  encode_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, as_stream(stream)>>>(
-      means2d, radii, depths, offsets, numel, numel / I, tile_size, tile_width, tile_height, tile_bits, n_isects,
-      isect_ids, flatten_ids);
+  {
+    KernelTimer timer("isect_encode", as_stream(stream));
+    encode_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, as_stream(stream)>>>(
+        means2d, radii, depths, offsets, numel, numel / I, tile_size, tile_width, tile_height, tile_bits, n_isects,
+        isect_ids, flatten_ids);
+  }
   return check_launch("intersect_tile_encode");
 }
 
@@ -253,11 +265,17 @@ extern "C" int gsplat_hip_isect_offset(const int64_t* isect_ids, int64_t n_isect
   const int64_t n_offsets = n_tiles * I;
   if (!offsets) return invalid("intersect_offset: null pointer.");
   if (n_isects == 0) {
-    fill_i32_kernel<<<grid_for(n_offsets, 256), 256, 0, s>>>(offsets, n_offsets, 0);
+    {
+      KernelTimer timer("isect_offsets", s);
+      fill_i32_kernel<<<grid_for(n_offsets, 256), 256, 0, s>>>(offsets, n_offsets, 0);
+    }
     return check_launch("intersect_offset (empty)");
   }
   if (!isect_ids) return invalid("intersect_offset: null pointer.");
   const int tile_bits = floor_log2_plus_one(n_tiles);
-  offsets_kernel<<<grid_for(n_isects, 256), 256, 0, s>>>(isect_ids, n_isects, tile_bits, n_tiles, n_offsets, offsets);
+  {
+    KernelTimer timer("isect_offsets", s);
+    offsets_kernel<<<grid_for(n_isects, 256), 256, 0, s>>>(isect_ids, n_isects, tile_bits, n_tiles, n_offsets, offsets);
+  }
   return check_launch("intersect_offset");
 }

@@ -520,9 +520,12 @@ extern "C" int gsplat_hip_projection_fwd(const float* means, const float* covars
     return invalid("projection_ewa_3dgs_fused_forward: null compensations.");
   if (B * C > 65535) return invalid("projection_ewa_3dgs_fused_forward: B*C exceeds 65535 cameras.");
   const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B * C));
-  projection_fwd_kernel<<<grid, kProjBlock, 0, as_stream(stream)>>>(
-      means, covars, quats, scales, opacities, viewmats, Ks, C, N, p, radii, means2d, depths, conics,
-      p.calc_compensations ? compensations : nullptr);
+  {
+    KernelTimer timer("projection_fwd", as_stream(stream));
+    projection_fwd_kernel<<<grid, kProjBlock, 0, as_stream(stream)>>>(
+        means, covars, quats, scales, opacities, viewmats, Ks, C, N, p, radii, means2d, depths, conics,
+        p.calc_compensations ? compensations : nullptr);
+  }
   return check_launch("projection_ewa_3dgs_fused_forward");
 }
 
@@ -566,12 +569,18 @@ extern "C" int gsplat_hip_projection_bwd(const float* means, const float* covars
     partials = static_cast<float*>(workspace);
   }
   const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B));
-  projection_bwd_kernel<<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p, radii,
-                                                    conics, compensations, v_means2d, v_depths, v_conics,
-                                                    v_compensations, v_means, v_covars, v_quats, v_scales, partials);
+  {
+    KernelTimer timer("projection_bwd", s);
+    projection_bwd_kernel<<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p, radii,
+                                                      conics, compensations, v_means2d, v_depths, v_conics,
+                                                      v_compensations, v_means, v_covars, v_quats, v_scales, partials);
+  }
   int rc = check_launch("projection_ewa_3dgs_fused_backward");
   if (rc != GSPLAT_OK || !v_viewmats) return rc;
   if (C == 0) return GSPLAT_OK;
-  viewmat_reduce_kernel<<<static_cast<unsigned>(B * C), 256, 0, s>>>(partials, static_cast<int>(grid.x), v_viewmats);
+  {
+    KernelTimer timer("projection_bwd_viewmats", s);
+    viewmat_reduce_kernel<<<static_cast<unsigned>(B * C), 256, 0, s>>>(partials, static_cast<int>(grid.x), v_viewmats);
+  }
   return check_launch("projection_ewa_3dgs_fused_backward (viewmats)");
 }

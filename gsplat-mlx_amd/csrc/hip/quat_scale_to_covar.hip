@@ -161,8 +161,11 @@ extern "C" int gsplat_hip_quat_scale_to_covar_preci_fwd(const float* quats, cons
   if (!quats || !scales || (compute_covar && !covars) || (compute_preci && !precis))
     return invalid("quat_scale_to_covar_preci_forward: null pointer.");
   if (grid_for(n, 256) > kMaxGridX) return invalid("quat_scale_to_covar_preci_forward: too many elements.");
-  qs_fwd_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(quats, scales, n, compute_covar, compute_preci,
-                                                                  triu, covars, precis);
+  {
+    KernelTimer timer("quat_scale_to_covar_fwd", as_stream(stream));
+    qs_fwd_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(quats, scales, n, compute_covar, compute_preci,
+                                                                    triu, covars, precis);
+  }
   return check_launch("quat_scale_to_covar_preci_forward");
 }
 
@@ -174,7 +177,10 @@ extern "C" int gsplat_hip_quat_scale_to_covar_preci_bwd(const float* quats, cons
   if (n == 0) return GSPLAT_OK;
   if (!quats || !scales || !v_quats || !v_scales)
     return invalid("quat_scale_to_covar_preci_backward: null pointer.");
-  qs_bwd_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(quats, scales, v_covars, v_precis, n, triu,
-                                                                  v_quats, v_scales);
+  {
+    KernelTimer timer("quat_scale_to_covar_bwd", as_stream(stream));
+    qs_bwd_kernel<<<grid_for(n, 256), 256, 0, as_stream(stream)>>>(quats, scales, v_covars, v_precis, n, triu,
+                                                                    v_quats, v_scales);
+  }
   return check_launch("quat_scale_to_covar_preci_backward");
 }

@@ -202,7 +202,10 @@ extern "C" int gsplat_hip_isect_sort(const int64_t* keys_in, const int32_t* vals
   uint64_t* kout = reinterpret_cast<uint64_t*>(keys_out);
   const int passes = (key_bits + 7) / 8;
   if (passes == 0) {
-    copy_kernel<<<grid_for(n, 256), 256, 0, s>>>(kin, vals_in, n, kout, vals_out);
+    {
+      KernelTimer timer("sort_copy", s);
+      copy_kernel<<<grid_for(n, 256), 256, 0, s>>>(kin, vals_in, n, kout, vals_out);
+    }
     return check_launch("intersect_tile_sort (copy)");
   }
   SortWorkspace ws;
@@ -219,12 +222,18 @@ extern "C" int gsplat_hip_isect_sort(const int64_t* keys_in, const int32_t* vals
     uint64_t* dst_k = to_out ? kout : ws.keys_alt;
     int32_t* dst_v = to_out ? vals_out : ws.vals_alt;
     const int shift = 8 * p;
-    hist_kernel<<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, n, shift, nb, ws.hist);
+    {
+      KernelTimer timer("sort_histogram", s);
+      hist_kernel<<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, n, shift, nb, ws.hist);
+    }
     int rc = check_launch("intersect_tile_sort (histogram)");
     if (rc) return rc;
     rc = scan_exclusive_i32(ws.hist, ws.hist, nb * kRadix, nullptr, ws.scan_ws, s);
     if (rc) return rc;
-    scatter_kernel<<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, src_v, n, shift, nb, ws.hist, dst_k, dst_v);
+    {
+      KernelTimer timer("sort_scatter", s);
+      scatter_kernel<<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, src_v, n, shift, nb, ws.hist, dst_k, dst_v);
+    }
     rc = check_launch("intersect_tile_sort (scatter)");
     if (rc) return rc;
     src_k = dst_k;

@@ -170,14 +170,40 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
   last_ids[pix] = cur;
 }
 
-// Adds a wave-reduced value to *dst from one lane (dst is wave-uniform).
-__device__ __forceinline__ void wave_atomic_add(float* dst, float v, int lane) {
-  const float s = wave_sum_uniform(v);
-  if (lane == 0) unsafeAtomicAdd(dst, s);
+// Wave-wide sums of NV values, interleaved so the independent DPP chains hide
+// each other's hazards: row_shr 1/2/4/8 within each 16-lane row, then
+// row_bcast 15 / 31 across rows; lane 63 ends up with the wave total.
+template <int NV>
+__device__ __forceinline__ void wave_reduce_lane63(float (&v)[NV]) {
+#pragma unroll
+  for (int step = 0; step < 6; ++step) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int x = __builtin_bit_cast(int, v[i]);
+      int y;
+      switch (step) {
+        case 0: y = __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false); break;  // row_shr:1
+        case 1: y = __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false); break;  // row_shr:2
+        case 2: y = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false); break;  // row_shr:4
+        case 3: y = __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false); break;  // row_shr:8
+        case 4: y = __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false); break;  // row_bcast:15
+        default: y = __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false); break; // row_bcast:31
+      }
+      v[i] += __builtin_bit_cast(float, y);
+    }
+  }
 }
 
-template <int CH>
-__global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, const float* __restrict__ render_alphas,
+// Backward. The tile's list is walked back-to-front in batches of BB entries
+// from the block's largest last_id. For each entry every lane computes its
+// pixel's partial gradients; a wave with at least one contributing lane sums
+// them across the wave (DPP) and lane 63 stores the NV sums into the wave's
+// own accumulator slot for that entry (plain LDS stores: each (wave, entry)
+// slot is written at most once per batch, so no LDS atomics). After the batch
+// the block adds up the per-wave slots and flushes one global atomic per
+// (entry, nonzero component).
+template <int CH, bool ABS>
+__global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, int BB, const float* __restrict__ render_alphas,
                                                           const int32_t* __restrict__ last_ids,
                                                           const float* __restrict__ v_render_colors,
                                                           const float* __restrict__ v_render_alphas,
@@ -187,12 +213,18 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, const fl
                                                           float* __restrict__ v_backgrounds) {
   constexpr int LC = CH > 0 ? CH : 1;
   constexpr int AC = CH > 0 ? CH : kMaxChannels;
+  // accumulated components per Gaussian: colors (CH), conic (3), mean (2),
+  // opacity (1), |mean| (2, absgrad only)
+  constexpr int NG = ABS ? 8 : 6;  // geometry components
+  constexpr int NV = (CH > 0 ? CH : 0) + NG;
   extern __shared__ float smem[];
   const int BS = blockDim.x;
-  float2* s_xy = reinterpret_cast<float2*>(smem);
-  float4* s_co = reinterpret_cast<float4*>(smem + 2 * BS);
-  int32_t* s_g = reinterpret_cast<int32_t*>(smem + 6 * BS);
-  float* s_col = smem + 7 * BS;  // [BS][LC] (CH > 0)
+  const int n_waves = BS / kWave;
+  float2* s_xy = reinterpret_cast<float2*>(smem);            // [BB]
+  float4* s_co = reinterpret_cast<float4*>(smem + 2 * BB);   // [BB] conic xyz, opacity
+  int32_t* s_g = reinterpret_cast<int32_t*>(smem + 6 * BB);  // [BB]
+  float* s_col = smem + 7 * BB;                              // [BB][LC] (CH > 0)
+  float* s_acc = s_col + (CH > 0 ? LC * BB : 0);             // [n_waves][BB][NV]
   __shared__ int s_max_last;
 
   const int channels = CH > 0 ? CH : a.channels;
@@ -201,6 +233,7 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, const fl
   const int tile = ty * a.tw + tx;
   const int t = threadIdx.x;
   const int lane = t % kWave;
+  const int wave = t / kWave;
   const int x = tx * a.ts + t % a.ts;
   const int y = ty * a.ts + t / a.ts;
   // blocks are padded to whole wave64s (the DPP reductions need every lane);
@@ -229,22 +262,32 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, const fl
   if (bg) {
     for (int c = 0; c < channels; ++c) bg_dot += bg[c] * v_rc[c];
     // v_backgrounds = sum over pixels of T_final * v_rc (gsplat_rasterize.cpp:459-464)
-    for (int c = 0; c < channels; ++c) wave_atomic_add(v_backgrounds + image * channels + c, T_final * v_rc[c], lane);
+    for (int c = 0; c < channels; ++c) {
+      const float s = wave_sum_uniform(T_final * v_rc[c]);
+      if (lane == 0) unsafeAtomicAdd(v_backgrounds + image * channels + c, s);
+    }
   }
+  const float t_final_ra_coef = T_final * v_ra;  // times ra below
+  const float t_final_bg_coef = -T_final * bg_dot;
 
-  // Entries past every lane's last contributor are skipped wholesale.
+  // Entries past every lane's last contributor are skipped wholesale: the
+  // block starts at its largest last_id, each wave skips entries past its own.
   if (t == 0) s_max_last = -1;
   __syncthreads();
   const int64_t my_last = inside ? min<int64_t>(end - 1, bin_final) : start - 1;
   if (my_last >= start) atomicMax(&s_max_last, static_cast<int>(my_last - start));
+  int64_t wave_last = my_last;
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) wave_last = max(wave_last, __shfl_xor(wave_last, off, kWave));
   __syncthreads();
   const int64_t stop = start + s_max_last + 1;  // exclusive end of the needed range
+  const int acc_words = n_waves * BB * NV;
 
-  for (int64_t b1 = stop; b1 > start; b1 -= BS) {
-    const int64_t b0 = max<int64_t>(start, b1 - BS);
-    __syncthreads();  // previous batch fully consumed
+  for (int64_t b1 = stop; b1 > start; b1 -= BB) {
+    const int64_t b0 = max<int64_t>(start, b1 - BB);
+    __syncthreads();  // previous batch fully consumed and flushed
     const int64_t j = b1 - 1 - t;  // slot k holds entry b1 - 1 - k (back to front)
-    if (j >= b0) {
+    if (t < BB && j >= b0) {
       float2 xy;
       float4 co;
       const int32_t g = load_gaussian(a, j, &xy, &co);
@@ -256,13 +299,16 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, const fl
         for (int c = 0; c < CH; ++c) s_col[t * CH + c] = a.colors[static_cast<int64_t>(g) * CH + c];
       }
     }
+    // acc_words is a multiple of 4 (BB is a multiple of 64)
+    for (int w = t * 4; w < acc_words; w += BS * 4)
+      *reinterpret_cast<float4*>(s_acc + w) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     __syncthreads();
     const int cnt = static_cast<int>(b1 - b0);
     for (int k = 0; k < cnt; ++k) {
       const int64_t idx = b1 - 1 - k;
+      if (idx > wave_last) continue;  // wave-uniform
       const float2 m = s_xy[k];
       const float4 co = s_co[k];
-      const int32_t g = s_g[k];
       const float dx = m.x - px;
       const float dy = m.y - py;
       const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
@@ -270,64 +316,109 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, const fl
       const float alpha = fminf(kMaxAlpha, co.w * vis);
       const bool valid = idx <= bin_final && !(sigma < 0.0f || alpha < kAlphaThreshold);
       if (__ballot(valid) == 0) continue;
-      float v_col[AC];
-      float v_c0 = 0.0f, v_c1 = 0.0f, v_c2 = 0.0f, v_x = 0.0f, v_y = 0.0f, v_op = 0.0f;
-      for (int c = 0; c < channels; ++c) v_col[c] = 0.0f;
+      float v[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) v[i] = 0.0f;
+      float v_col_generic[CH > 0 ? 1 : kMaxChannels];
       if (valid) {
-        const float ra = 1.0f / fmaxf(kMinOneMinusAlpha, 1.0f - alpha);
+        const float ra = __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - alpha));
         T *= ra;
         const float fac = alpha * T;
         float v_alpha = 0.0f;
         if constexpr (CH > 0) {
 #pragma unroll
           for (int c = 0; c < CH; ++c) {
-            v_col[c] = fac * v_rc[c];
-            v_alpha += (s_col[k * CH + c] * T - buffer[c] * ra) * v_rc[c];
+            const float col = s_col[k * CH + c];
+            v[c] = fac * v_rc[c];
+            v_alpha += (col * T - buffer[c] * ra) * v_rc[c];
+            buffer[c] += col * fac;
           }
         } else {
-          const float* col = a.colors + static_cast<int64_t>(g) * channels;
+          const float* col = a.colors + static_cast<int64_t>(s_g[k]) * channels;
           for (int c = 0; c < channels; ++c) {
-            v_col[c] = fac * v_rc[c];
+            v_col_generic[c] = fac * v_rc[c];
             v_alpha += (col[c] * T - buffer[c] * ra) * v_rc[c];
+            buffer[c] += col[c] * fac;
           }
         }
-        v_alpha += T_final * ra * v_ra;
-        if (bg) v_alpha += -T_final * ra * bg_dot;
+        v_alpha += ra * (t_final_ra_coef + t_final_bg_coef);
         if (co.w * vis <= kMaxAlpha) {
           const float v_sigma = -co.w * vis * v_alpha;
-          v_x = v_sigma * (co.x * dx + co.y * dy);
-          v_y = v_sigma * (co.y * dx + co.z * dy);
-          v_c0 = 0.5f * v_sigma * dx * dx;
-          v_c1 = v_sigma * dx * dy;
-          v_c2 = 0.5f * v_sigma * dy * dy;
-          v_op = vis * v_alpha;
+          const float vx = v_sigma * (co.x * dx + co.y * dy);
+          const float vy = v_sigma * (co.y * dx + co.z * dy);
+          constexpr int o = CH > 0 ? CH : 0;
+          v[o + 0] = 0.5f * v_sigma * dx * dx;
+          v[o + 1] = v_sigma * dx * dy;
+          v[o + 2] = 0.5f * v_sigma * dy * dy;
+          v[o + 3] = vx;
+          v[o + 4] = vy;
+          v[o + 5] = vis * v_alpha;
+          if constexpr (ABS) {
+            v[o + 6] = fabsf(vx);
+            v[o + 7] = fabsf(vy);
+          }
         }
-        if constexpr (CH > 0) {
-#pragma unroll
-          for (int c = 0; c < CH; ++c) buffer[c] += s_col[k * CH + c] * fac;
-        } else {
-          const float* col = a.colors + static_cast<int64_t>(g) * channels;
-          for (int c = 0; c < channels; ++c) buffer[c] += col[c] * fac;
+      } else if constexpr (CH == 0) {
+        for (int c = 0; c < channels; ++c) v_col_generic[c] = 0.0f;
+      }
+      if constexpr (CH == 0) {
+        // generic channel count: colour gradients go straight to global memory
+        const int64_t gg = s_g[k];
+        for (int c = 0; c < channels; ++c) {
+          const float s = wave_sum_uniform(v_col_generic[c]);
+          if (lane == 0 && s != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, s);
         }
       }
-      const int64_t gg = g;
-      for (int c = 0; c < channels; ++c) wave_atomic_add(v_colors + gg * channels + c, v_col[c], lane);
-      wave_atomic_add(v_conics + gg * 3, v_c0, lane);
-      wave_atomic_add(v_conics + gg * 3 + 1, v_c1, lane);
-      wave_atomic_add(v_conics + gg * 3 + 2, v_c2, lane);
-      wave_atomic_add(v_means2d + gg * 2, v_x, lane);
-      wave_atomic_add(v_means2d + gg * 2 + 1, v_y, lane);
-      wave_atomic_add(v_opacities + gg, v_op, lane);
-      if (v_means2d_abs) {
-        wave_atomic_add(v_means2d_abs + gg * 2, fabsf(v_x), lane);
-        wave_atomic_add(v_means2d_abs + gg * 2 + 1, fabsf(v_y), lane);
+      wave_reduce_lane63<NV>(v);
+      if (lane == kWave - 1) {
+        float* acc = s_acc + (wave * BB + k) * NV;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) acc[i] = v[i];
+      }
+    }
+    __syncthreads();
+    // flush: thread t owns slot t (entry b1 - 1 - t); sums the waves' slots
+    if (t < cnt) {
+      float acc[NV];
+#pragma unroll
+      for (int i = 0; i < NV; ++i) acc[i] = s_acc[t * NV + i];
+      for (int w = 1; w < n_waves; ++w) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) acc[i] += s_acc[(w * BB + t) * NV + i];
+      }
+      const int64_t gg = s_g[t];
+      constexpr int o = CH > 0 ? CH : 0;
+      if constexpr (CH > 0) {
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+          if (acc[c] != 0.0f) unsafeAtomicAdd(v_colors + gg * CH + c, acc[c]);
+      }
+      if (acc[o + 0] != 0.0f) unsafeAtomicAdd(v_conics + gg * 3, acc[o + 0]);
+      if (acc[o + 1] != 0.0f) unsafeAtomicAdd(v_conics + gg * 3 + 1, acc[o + 1]);
+      if (acc[o + 2] != 0.0f) unsafeAtomicAdd(v_conics + gg * 3 + 2, acc[o + 2]);
+      if (acc[o + 3] != 0.0f) unsafeAtomicAdd(v_means2d + gg * 2, acc[o + 3]);
+      if (acc[o + 4] != 0.0f) unsafeAtomicAdd(v_means2d + gg * 2 + 1, acc[o + 4]);
+      if (acc[o + 5] != 0.0f) unsafeAtomicAdd(v_opacities + gg, acc[o + 5]);
+      if constexpr (ABS) {
+        if (acc[o + 6] != 0.0f) unsafeAtomicAdd(v_means2d_abs + gg * 2, acc[o + 6]);
+        if (acc[o + 7] != 0.0f) unsafeAtomicAdd(v_means2d_abs + gg * 2 + 1, acc[o + 7]);
       }
     }
   }
 }
 
 size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (6 + (ch > 0 ? ch : 0) + (ch > 0 ? 0 : 1)) * 4; }
-size_t bwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (7 + (ch > 0 ? ch : 0)) * 4; }
+// Backward batch length: 128 entries for blocks of up to 256 lanes, 64 above
+// (bounds the per-wave accumulators to 48 KiB at 1024 lanes, 4 channels,
+// absgrad); never more than the block so one lane loads one record.
+int bwd_batch(int bs) { return bs <= 128 ? bs : (bs <= 256 ? 128 : 64); }
+// records (7 + colors) per batch slot plus NV accumulators per (wave, slot)
+size_t bwd_smem(int ch, int bs, bool absgrad) {
+  const int bb = bwd_batch(bs);
+  const int cc = ch > 0 ? ch : 0;
+  const int nv = cc + (absgrad ? 8 : 6);
+  return static_cast<size_t>(bb) * (7 + cc + (bs / kWave) * nv) * 4;
+}
 
 int check_args(const RasterArgs& a, const char* what) {
   if (a.I < 0 || a.N < 0 || a.channels <= 0 || a.W < 0 || a.H < 0 || a.ts <= 0 || a.tw < 0 || a.th < 0 ||
@@ -367,6 +458,7 @@ extern "C" int gsplat_hip_rasterize_fwd(const float* means2d, const float* conic
   hipStream_t s = as_stream(stream);
   const int ch = channels <= 4 ? channels : 0;
   const size_t sm = fwd_smem(ch, bs);
+  KernelTimer timer("raster_fwd", s);
   switch (ch) {
     case 1: raster_fwd_kernel<1><<<grid, bs, sm, s>>>(a, render_colors, render_alphas, last_ids); break;
     case 2: raster_fwd_kernel<2><<<grid, bs, sm, s>>>(a, render_colors, render_alphas, last_ids); break;
@@ -409,11 +501,18 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   const dim3 grid(tile_width, tile_height, static_cast<unsigned>(I));
   const int bs = (tile_size * tile_size + kWave - 1) / kWave * kWave;
   const int ch = channels <= 4 ? channels : 0;
-  const size_t sm = bwd_smem(ch, bs);
+  const size_t sm = bwd_smem(ch, bs, v_means2d_abs != nullptr);
+  const int bb = bwd_batch(bs);
+  KernelTimer timer("raster_bwd", s);
 #define GSPLAT_BWD_LAUNCH(C)                                                                                     \
-  raster_bwd_kernel<C><<<grid, bs, sm, s>>>(a, render_alphas, last_ids, v_render_colors, v_render_alphas,        \
-                                            v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities,           \
-                                            v_backgrounds)
+  if (v_means2d_abs)                                                                                             \
+    raster_bwd_kernel<C, true><<<grid, bs, sm, s>>>(a, bb, render_alphas, last_ids, v_render_colors, v_render_alphas, \
+                                                    v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities,   \
+                                                    v_backgrounds);                                              \
+  else                                                                                                           \
+    raster_bwd_kernel<C, false><<<grid, bs, sm, s>>>(a, bb, render_alphas, last_ids, v_render_colors,                 \
+                                                     v_render_alphas, nullptr, v_means2d, v_conics, v_colors,     \
+                                                     v_opacities, v_backgrounds)
   switch (ch) {
     case 1: GSPLAT_BWD_LAUNCH(1); break;
     case 2: GSPLAT_BWD_LAUNCH(2); break;

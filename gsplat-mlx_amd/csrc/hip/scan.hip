@@ -62,14 +62,23 @@ int scan_exclusive_i32(const int32_t* in, int32_t* out, int64_t n, int64_t* tota
   const int64_t nb = scan_num_blocks(n);
   if (nb > kMaxGridX) return invalid("scan: too many elements.");
   int64_t* sums = static_cast<int64_t*>(workspace);
-  scan_local_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, stream>>>(in, out, n, sums);
+  {
+    KernelTimer timer("scan_local", stream);
+    scan_local_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, stream>>>(in, out, n, sums);
+  }
   int rc = check_launch("scan (local)");
   if (rc) return rc;
-  scan_block_sums_kernel<<<1, kScanBlock, 0, stream>>>(sums, nb, total_dev);
+  {
+    KernelTimer timer("scan_block_sums", stream);
+    scan_block_sums_kernel<<<1, kScanBlock, 0, stream>>>(sums, nb, total_dev);
+  }
   rc = check_launch("scan (block sums)");
   if (rc) return rc;
   if (nb > 1) {
-    scan_fixup_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, stream>>>(out, n, sums);
+    {
+      KernelTimer timer("scan_fixup", stream);
+      scan_fixup_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, stream>>>(out, n, sums);
+    }
     rc = check_launch("scan (fixup)");
   }
   return rc;

@@ -79,17 +79,39 @@ __device__ __forceinline__ void sh_basis(float dx, float dy, float dz, float* ba
   basis[24] = 0.6258357354491763f * f_c3;
 }
 
-// Copies the first A*3 floats of `cnt` rows of stride K*3 into LDS.
+// LDS row stride for W floats per row: odd, so lanes reading the same column
+// of consecutive rows hit distinct banks.
+__host__ __device__ constexpr int padded(int w) { return w | 1; }
+
+// Copies the first W = A*3 floats of `cnt` rows (row stride k3 floats in
+// global memory) into LDS rows of stride padded(W). The block's rows are one
+// contiguous span of cnt*k3 floats; it is read front to back with 16-byte
+// loads when aligned (unrolled for more loads in flight), else 4-byte loads.
 template <int A>
 __device__ __forceinline__ void stage_rows(float* __restrict__ lds, const float* __restrict__ src, int cnt,
-                                           int64_t row_stride) {
+                                           uint32_t k3, uint32_t k3_magic) {
   constexpr int W = A * 3;
-  constexpr uint32_t m = (0x100000000ull + W - 1) / W;
-  const int total = cnt * W;
-  for (int i = threadIdx.x; i < total; i += kShBlock) {
-    const uint32_t r = fast_div(static_cast<uint32_t>(i), m);
-    const uint32_t c = static_cast<uint32_t>(i) - r * W;
-    lds[i] = src[r * row_stride + c];
+  constexpr int PW = padded(W);
+  const uint32_t total = static_cast<uint32_t>(cnt) * k3;
+  auto put = [&](uint32_t f, float v) {
+    const uint32_t r = fast_div(f, k3_magic);
+    const uint32_t c = f - r * k3;
+    if (c < static_cast<uint32_t>(W)) lds[r * PW + c] = v;
+  };
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0 && (total & 3) == 0) {
+    const float4* src4 = reinterpret_cast<const float4*>(src);
+    const uint32_t total4 = total >> 2;
+#pragma unroll 4
+    for (uint32_t i = threadIdx.x; i < total4; i += kShBlock) {
+      const float4 v = src4[i];
+      put(4 * i, v.x);
+      put(4 * i + 1, v.y);
+      put(4 * i + 2, v.z);
+      put(4 * i + 3, v.w);
+    }
+  } else {
+#pragma unroll 4
+    for (uint32_t i = threadIdx.x; i < total; i += kShBlock) put(i, src[i]);
   }
 }
 
@@ -97,12 +119,13 @@ template <int DEG>
 __global__ void __launch_bounds__(kShBlock) sh_fwd_kernel(const float* __restrict__ dirs,
                                                           const float* __restrict__ coeffs,
                                                           const uint8_t* __restrict__ masks, int64_t n, int64_t K,
-                                                          float* __restrict__ colors) {
+                                                          uint32_t k3_magic, float* __restrict__ colors) {
   constexpr int A = (DEG + 1) * (DEG + 1);
-  __shared__ float sc[kShBlock * A * 3];
+  constexpr int PW = padded(A * 3);
+  __shared__ float sc[kShBlock * PW];
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShBlock;
   const int cnt = static_cast<int>(min<int64_t>(kShBlock, n - e0));
-  stage_rows<A>(sc, coeffs + e0 * K * 3, cnt, K * 3);
+  stage_rows<A>(sc, coeffs + e0 * K * 3, cnt, static_cast<uint32_t>(K * 3), k3_magic);
   __syncthreads();
   const int t = threadIdx.x;
   if (t >= cnt) return;
@@ -110,7 +133,7 @@ __global__ void __launch_bounds__(kShBlock) sh_fwd_kernel(const float* __restric
   float out[3] = {0.0f, 0.0f, 0.0f};
   if (!masks || masks[e]) {
     const float d0 = dirs[e * 3], d1 = dirs[e * 3 + 1], d2 = dirs[e * 3 + 2];
-    const float* co = sc + t * A * 3;
+    const float* co = sc + t * PW;
     float basis[A];
     sh_basis<DEG>(d0, d1, d2, basis);
     const float norm = sqrtf(d0 * d0 + d1 * d1 + d2 * d2);
@@ -255,13 +278,15 @@ __global__ void __launch_bounds__(kShBlock) sh_bwd_kernel(const float* __restric
                                                           uint32_t k3_magic, float* __restrict__ v_dirs,
                                                           float* __restrict__ v_coeffs) {
   constexpr int A = (DEG + 1) * (DEG + 1);
-  __shared__ float sc[DEG >= 1 ? kShBlock * A * 3 : 1];
-  __shared__ float sb[kShBlock * (A + 3)];  // per-lane basis (A) then v_color (3)
+  constexpr int PW = padded(A * 3);
+  constexpr int SB = padded(A + 3);
+  __shared__ float sc[DEG >= 1 ? kShBlock * PW : 1];
+  __shared__ float sb[kShBlock * SB];  // per-lane basis (A) then v_color (3)
   const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShBlock;
   const int cnt = static_cast<int>(min<int64_t>(kShBlock, n - e0));
   const int t = threadIdx.x;
-  if (v_dirs && DEG >= 1) stage_rows<A>(sc, coeffs + e0 * K * 3, cnt, K * 3);
-  float* my = sb + t * (A + 3);
+  if (v_dirs && DEG >= 1) stage_rows<A>(sc, coeffs + e0 * K * 3, cnt, static_cast<uint32_t>(K * 3), k3_magic);
+  float* my = sb + t * SB;
   bool on = false;
   float dir[3] = {0.0f, 0.0f, 0.0f};
   float vc[3] = {0.0f, 0.0f, 0.0f};
@@ -286,38 +311,54 @@ __global__ void __launch_bounds__(kShBlock) sh_bwd_kernel(const float* __restric
   if (t < cnt && v_dirs) {
     const int64_t e = e0 + t;
     float vd[3] = {0.0f, 0.0f, 0.0f};
-    if (on && DEG >= 1) sh_dir_vjp<DEG>(dir, sc + t * A * 3, vc, vd);
+    if (on && DEG >= 1) sh_dir_vjp<DEG>(dir, sc + t * PW, vc, vd);
     v_dirs[e * 3] = vd[0];
     v_dirs[e * 3 + 1] = vd[1];
     v_dirs[e * 3 + 2] = vd[2];
   }
-  // Coalesced write of the [cnt, K, 3] slab of v_coeffs.
+  // Coalesced write of the [cnt, K, 3] slab of v_coeffs (16-byte stores when
+  // aligned).
   const uint32_t K3 = static_cast<uint32_t>(K * 3);
   const uint32_t total = static_cast<uint32_t>(cnt) * K3;
   float* out = v_coeffs + e0 * K * 3;
-  for (uint32_t i = t; i < total; i += kShBlock) {
+  auto value = [&](uint32_t i) {
     const uint32_t r = fast_div(i, k3_magic);
     const uint32_t c = i - r * K3;
     const uint32_t b = c / 3u;
     const uint32_t ch = c - b * 3u;
-    const float* row = sb + r * (A + 3);
-    out[i] = b < static_cast<uint32_t>(A) ? row[b] * row[A + ch] : 0.0f;
+    const float* row = sb + r * SB;
+    return b < static_cast<uint32_t>(A) ? row[b] * row[A + ch] : 0.0f;
+  };
+  if ((reinterpret_cast<uintptr_t>(out) & 15) == 0 && (total & 3) == 0) {
+    float4* out4 = reinterpret_cast<float4*>(out);
+#pragma unroll 2
+    for (uint32_t i = t; i < (total >> 2); i += kShBlock)
+      out4[i] = make_float4(value(4 * i), value(4 * i + 1), value(4 * i + 2), value(4 * i + 3));
+  } else {
+    for (uint32_t i = t; i < total; i += kShBlock) out[i] = value(i);
   }
 }
 
 template <int DEG>
 int launch_fwd(const float* dirs, const float* coeffs, const uint8_t* masks, int64_t n, int64_t K, float* colors,
                hipStream_t s) {
-  sh_fwd_kernel<DEG><<<grid_for(n, kShBlock), kShBlock, 0, s>>>(dirs, coeffs, masks, n, K, colors);
+  {
+    KernelTimer timer("sh_fwd", s);
+    sh_fwd_kernel<DEG><<<grid_for(n, kShBlock), kShBlock, 0, s>>>(dirs, coeffs, masks, n, K,
+                                                                  magic_for(static_cast<uint32_t>(K * 3)), colors);
+  }
   return check_launch("spherical_harmonics_forward");
 }
 
 template <int DEG>
 int launch_bwd(const float* dirs, const float* coeffs, const uint8_t* masks, const float* v_colors, int64_t n,
                int64_t K, float* v_dirs, float* v_coeffs, hipStream_t s) {
-  sh_bwd_kernel<DEG><<<grid_for(n, kShBlock), kShBlock, 0, s>>>(dirs, coeffs, masks, v_colors, n, K,
-                                                               magic_for(static_cast<uint32_t>(K * 3)), v_dirs,
-                                                               v_coeffs);
+  {
+    KernelTimer timer("sh_bwd", s);
+    sh_bwd_kernel<DEG><<<grid_for(n, kShBlock), kShBlock, 0, s>>>(dirs, coeffs, masks, v_colors, n, K,
+                                                                 magic_for(static_cast<uint32_t>(K * 3)), v_dirs,
+                                                                 v_coeffs);
+  }
   return check_launch("spherical_harmonics_backward");
 }
 

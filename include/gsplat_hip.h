@@ -39,6 +39,18 @@ const char* gsplat_hip_last_error(void);
 /* ABI version of this library (major * 100 + minor). */
 int gsplat_hip_abi_version(void);
 
+/* Opt-in kernel timing (no counterpart in the reference; used by the
+ * benchmark). While enabled, every entry point brackets each kernel it
+ * launches with a pair of HIP events recorded on the launch stream.
+ * gsplat_hip_profile_report() waits for the recorded events, writes one line
+ * "name<TAB>launches<TAB>total_ms" per kernel into buf (NUL-terminated,
+ * truncated to buf_len) and returns the length of the full report; it keeps
+ * the totals until gsplat_hip_profile_reset(). Not for concurrent use from
+ * several host threads. */
+void gsplat_hip_profile_enable(int32_t enable);
+void gsplat_hip_profile_reset(void);
+size_t gsplat_hip_profile_report(char* buf, size_t buf_len);
+
 /* ---------------------------------------------------------------------------
  * quat_scale_to_covar_preci
  * Replaces GSPlatQuatScaleToCovarPreci(/Backward)::eval_gpu
