@@ -3,6 +3,8 @@
 // HIP C-ABI.
 #include "gsplat_rasterize.h"
 
+#include <algorithm>
+
 #include "core_util.h"
 
 namespace gsplat_core {
@@ -143,6 +145,8 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
   array v_col = at::empty(colors.sizes(), f32_like(means2d));
   array v_op = at::empty(opac.sizes(), f32_like(means2d));
   array v_bg = p.use_backgrounds ? at::empty(bg.sizes(), f32_like(means2d)) : at::empty({0}, f32_like(means2d));
+  const size_t ws_bytes = gsplat_hip_rasterize_bwd_workspace_size(l.I, l.tw, l.th);
+  array ws = at::empty({static_cast<int64_t>(std::max<size_t>(ws_bytes, 1))}, u8_like(means2d));
   check(gsplat_hip_rasterize_bwd(
       means2d.data_ptr<float>(), conics.data_ptr<float>(), colors.data_ptr<float>(), opac.data_ptr<float>(),
       p.use_backgrounds ? bg.data_ptr<float>() : nullptr, p.use_masks ? masks.data_ptr<uint8_t>() : nullptr,
@@ -150,7 +154,8 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
       p.tile_size, l.tw, l.th, flat.numel(), ra.data_ptr<float>(), li.data_ptr<int32_t>(), v_rc.data_ptr<float>(),
       v_ra.data_ptr<float>(), input.absgrad ? v_abs.data_ptr<float>() : nullptr, v_m2.data_ptr<float>(),
       v_con.data_ptr<float>(), v_col.data_ptr<float>(), v_op.data_ptr<float>(),
-      p.use_backgrounds ? v_bg.data_ptr<float>() : nullptr, stream_for(input.s, means2d)));
+      p.use_backgrounds ? v_bg.data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(), ws_bytes,
+      stream_for(input.s, means2d)));
   return {v_abs, v_m2, v_con, v_col, v_op, v_bg};
 }
 

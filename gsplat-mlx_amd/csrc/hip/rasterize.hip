@@ -16,7 +16,11 @@
 // and :432-554 (backward) operation for operation; the Gaussian falloff and
 // alpha tests are evaluated exactly as the reference (no FMA contraction in
 // this file) so compositing decisions match it.
+#include <algorithm>
+#include <climits>
+
 #include "common.hpp"
+#include "scan.hpp"
 
 namespace gsplat_hip {
 namespace {
@@ -170,53 +174,115 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
   last_ids[pix] = cur;
 }
 
-// Wave-wide sums of NV values, interleaved so the independent DPP chains hide
-// each other's hazards: row_shr 1/2/4/8 within each 16-lane row, then
-// row_bcast 15 / 31 across rows; lane 63 ends up with the wave total.
-template <int NV>
-__device__ __forceinline__ void wave_reduce_lane63(float (&v)[NV]) {
-#pragma unroll
-  for (int step = 0; step < 6; ++step) {
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int x = __builtin_bit_cast(int, v[i]);
-      int y;
-      switch (step) {
-        case 0: y = __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false); break;  // row_shr:1
-        case 1: y = __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false); break;  // row_shr:2
-        case 2: y = __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false); break;  // row_shr:4
-        case 3: y = __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false); break;  // row_shr:8
-        case 4: y = __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false); break;  // row_bcast:15
-        default: y = __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false); break; // row_bcast:31
-      }
-      v[i] += __builtin_bit_cast(float, y);
-    }
-  }
+// Wave-wide sums of N values per lane by transposition (gfx950): three
+// exchange levels halve the number of live values while doubling the lanes
+// each one covers -- permlane32_swap (lane ^ 32), permlane16_swap (lane ^ 16),
+// DPP row_ror:8 (lane ^ 8) -- then quad_perm / row_half_mirror DPP adds finish
+// the sums inside each group of 8 lanes. A pair (a, b) at a level leaves the
+// sum of a on lanes whose level bit is 0 and of b where it is 1; an unpaired
+// last value is summed on both sides. After the call, value y[m] on a lane
+// with bits h = lane[5], r = lane[4], e = lane[3] is the wave total of input
+// red_index<N>(m, h, r, e); all 8 lanes of a group hold the same totals.
+// Costs about 2.3 VALU per value instead of 6 DPP steps per value.
+template <int N>
+struct Red {
+  static constexpr int NA = (N + 1) / 2;   // after lane ^ 32
+  static constexpr int NB = (NA + 1) / 2;  // after lane ^ 16
+  static constexpr int NC = (NB + 1) / 2;  // after lane ^ 8
+};
+
+template <int N>
+__device__ __forceinline__ int red_index(int m, int h, int r, int e) {
+  int c = 2 * m + e;
+  if (c >= Red<N>::NB) c = 2 * m;
+  int b = 2 * c + r;
+  if (b >= Red<N>::NA) b = 2 * c;
+  int v = 2 * b + h;
+  if (v >= N) v = 2 * b;
+  return v;
 }
 
-// Backward. The tile's list is walked back-to-front in batches of BB entries
-// from the block's largest last_id. For each entry every lane computes its
-// pixel's partial gradients; a wave with at least one contributing lane sums
-// them across the wave (DPP) and lane 63 stores the NV sums into the wave's
-// own accumulator slot for that entry (plain LDS stores: each (wave, entry)
-// slot is written at most once per batch, so no LDS atomics). After the batch
-// the block adds up the per-wave slots and flushes one global atomic per
-// (entry, nonzero component).
-template <int CH, bool ABS>
-__global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, int BB, const float* __restrict__ render_alphas,
-                                                          const int32_t* __restrict__ last_ids,
-                                                          const float* __restrict__ v_render_colors,
-                                                          const float* __restrict__ v_render_alphas,
-                                                          float* __restrict__ v_means2d_abs,
-                                                          float* __restrict__ v_means2d, float* __restrict__ v_conics,
-                                                          float* __restrict__ v_colors, float* __restrict__ v_opacities,
-                                                          float* __restrict__ v_backgrounds) {
+__device__ __forceinline__ float fbits(unsigned u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ unsigned ubits(float f) { return __builtin_bit_cast(unsigned, f); }
+
+template <int N>
+__device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float (&y)[Red<N>::NC], bool e_bit) {
+  constexpr int NA = Red<N>::NA, NB = Red<N>::NB, NC = Red<N>::NC;
+  float w[NA];
+#pragma unroll
+  for (int i = 0; i < NA; ++i) {
+    const float a = v[2 * i];
+    const float b = (2 * i + 1 < N) ? v[2 * i + 1] : a;
+    const auto sw = __builtin_amdgcn_permlane32_swap(ubits(a), ubits(b), false, false);
+    w[i] = fbits(sw[0]) + fbits(sw[1]);
+  }
+  float x[NB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    const float a = w[2 * i];
+    const float b = (2 * i + 1 < NA) ? w[2 * i + 1] : a;
+    const auto sw = __builtin_amdgcn_permlane16_swap(ubits(a), ubits(b), false, false);
+    x[i] = fbits(sw[0]) + fbits(sw[1]);
+  }
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const float a = x[2 * i];
+    if (2 * i + 1 < NB) {
+      const float b = x[2 * i + 1];
+      const float send = e_bit ? a : b;
+      const float keep = e_bit ? b : a;
+      y[i] = keep + fbits(__builtin_amdgcn_update_dpp(0u, ubits(send), 0x128, 0xf, 0xf, false));  // row_ror:8
+    } else {
+      y[i] = a + fbits(__builtin_amdgcn_update_dpp(0u, ubits(a), 0x128, 0xf, 0xf, false));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NC; ++i) y[i] += fbits(__builtin_amdgcn_update_dpp(0u, ubits(y[i]), 0xB1, 0xf, 0xf, false));   // lane ^ 1
+#pragma unroll
+  for (int i = 0; i < NC; ++i) y[i] += fbits(__builtin_amdgcn_update_dpp(0u, ubits(y[i]), 0x4E, 0xf, 0xf, false));   // lane ^ 2
+#pragma unroll
+  for (int i = 0; i < NC; ++i) y[i] += fbits(__builtin_amdgcn_update_dpp(0u, ubits(y[i]), 0x141, 0xf, 0xf, false));  // 7 - lane
+}
+
+// Backward. Persistent blocks take (tile, band) units from a counter in the
+// heavy-first order of `order`; a tile is split into n_bands bands, each a
+// block of lanes owning P pixels per lane (pixel q = ((band * waves + wave) *
+// P + p) * 64 + lane, so a wave covers a compact run of 64 * P pixels).
+// The tile's list is walked back-to-front in batches of BB entries from the
+// band's largest last_id; the next batch's records are loaded into registers
+// while the current one is processed. For each entry every lane sums the
+// partial gradients of its pixels in a reduced basis (see below); a wave with
+// a contributing pixel sums them over the wave (wave_transpose_reduce) and one
+// lane per 8-lane group stores its totals into the wave's accumulator slot
+// for that entry (plain LDS stores; each (wave, entry) slot is written at most
+// once per batch). After the batch the block adds up the per-wave slots,
+// maps them back to gradients and flushes one global atomic per (entry,
+// nonzero component).
+//
+// Per pixel, with the reference's per-channel `buffer` (gsplat_rasterize.cpp:
+// 500-546) folded into B = sum_c buffer_c * v_rc_c and D = sum_c col_c * v_rc_c:
+//   v_alpha = T D + ra (coef - B),  B += fac D,
+// and the geometry gradients accumulated as h = v_sigma * (dx, dy):
+//   v_conic = (hx dx / 2, hx dy, hy dy / 2),  v_mean2d = conic * (sum hx, sum hy)
+// (the conic is the same for every pixel of an entry, so it is applied once
+// after the reduction). Accumulated components: colors (CH), hx dx, hx dy,
+// hy dy, hx, hy, vis * v_alpha, and |v_mean2d| per pixel (x, y) with absgrad.
+// CH == 0 (runtime channel count) uses P == 1 and sends colour gradients
+// straight to global memory.
+template <int CH, bool ABS, int P>
+__global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
+    RasterArgs a, int BB, int n_bands, int64_t n_units, const int32_t* __restrict__ order,
+    int32_t* __restrict__ unit_counter, const float* __restrict__ render_alphas, const int32_t* __restrict__ last_ids,
+    const float* __restrict__ v_render_colors, const float* __restrict__ v_render_alphas,
+    float* __restrict__ v_means2d_abs, float* __restrict__ v_means2d, float* __restrict__ v_conics,
+    float* __restrict__ v_colors, float* __restrict__ v_opacities, float* __restrict__ v_backgrounds) {
+  static_assert(CH > 0 || P == 1, "runtime channel counts use one pixel per lane");
   constexpr int LC = CH > 0 ? CH : 1;
   constexpr int AC = CH > 0 ? CH : kMaxChannels;
-  // accumulated components per Gaussian: colors (CH), conic (3), mean (2),
-  // opacity (1), |mean| (2, absgrad only)
   constexpr int NG = ABS ? 8 : 6;  // geometry components
   constexpr int NV = (CH > 0 ? CH : 0) + NG;
+  constexpr int o = CH > 0 ? CH : 0;  // first geometry component
+  constexpr int NC = Red<NV>::NC;
   extern __shared__ float smem[];
   const int BS = blockDim.x;
   const int n_waves = BS / kWave;
@@ -226,195 +292,342 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(RasterArgs a, int BB, 
   float* s_col = smem + 7 * BB;                              // [BB][LC] (CH > 0)
   float* s_acc = s_col + (CH > 0 ? LC * BB : 0);             // [n_waves][BB][NV]
   __shared__ int s_max_last;
+  __shared__ int64_t s_unit;
 
   const int channels = CH > 0 ? CH : a.channels;
-  const int tx = blockIdx.x, ty = blockIdx.y;
-  const int64_t image = blockIdx.z;
-  const int tile = ty * a.tw + tx;
   const int t = threadIdx.x;
   const int lane = t % kWave;
   const int wave = t / kWave;
-  const int x = tx * a.ts + t % a.ts;
-  const int y = ty * a.ts + t / a.ts;
-  // blocks are padded to whole wave64s (the DPP reductions need every lane);
-  // padding lanes own no pixel
-  const bool inside = t < a.ts * a.ts && x < a.W && y < a.H;
-  const int64_t pix = (image * a.H + y) * static_cast<int64_t>(a.W) + x;
-  const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
-  if (a.masks && !a.masks[image * n_tiles + tile]) return;  // masked tiles contribute nothing
-  const float* bg = a.backgrounds ? a.backgrounds + image * channels : nullptr;
-
-  int64_t start, end;
-  tile_range(a, image, tile, &start, &end);
-  const float px = static_cast<float>(x) + 0.5f;
-  const float py = static_cast<float>(y) + 0.5f;
-  const float T_final = inside ? 1.0f - render_alphas[pix] : 1.0f;
-  float T = T_final;
-  const int64_t bin_final = inside ? last_ids[pix] : -1;
-  float v_rc[AC];
-  float buffer[AC];
-  float bg_dot = 0.0f;
-  for (int c = 0; c < channels; ++c) {
-    v_rc[c] = inside ? v_render_colors[pix * channels + c] : 0.0f;
-    buffer[c] = 0.0f;
-  }
-  const float v_ra = inside ? v_render_alphas[pix] : 0.0f;
-  if (bg) {
-    for (int c = 0; c < channels; ++c) bg_dot += bg[c] * v_rc[c];
-    // v_backgrounds = sum over pixels of T_final * v_rc (gsplat_rasterize.cpp:459-464)
-    for (int c = 0; c < channels; ++c) {
-      const float s = wave_sum_uniform(T_final * v_rc[c]);
-      if (lane == 0) unsafeAtomicAdd(v_backgrounds + image * channels + c, s);
-    }
-  }
-  const float t_final_ra_coef = T_final * v_ra;  // times ra below
-  const float t_final_bg_coef = -T_final * bg_dot;
-
-  // Entries past every lane's last contributor are skipped wholesale: the
-  // block starts at its largest last_id, each wave skips entries past its own.
-  if (t == 0) s_max_last = -1;
-  __syncthreads();
-  const int64_t my_last = inside ? min<int64_t>(end - 1, bin_final) : start - 1;
-  if (my_last >= start) atomicMax(&s_max_last, static_cast<int>(my_last - start));
-  int64_t wave_last = my_last;
+  const bool e_bit = (lane >> 3) & 1;
+  const int red_slot = lane & 7;  // lane 7 of each 8-lane group stores
+  int red_idx[NC];
 #pragma unroll
-  for (int off = 1; off < kWave; off <<= 1) wave_last = max(wave_last, __shfl_xor(wave_last, off, kWave));
-  __syncthreads();
-  const int64_t stop = start + s_max_last + 1;  // exclusive end of the needed range
+  for (int m = 0; m < NC; ++m) red_idx[m] = red_index<NV>(m, (lane >> 5) & 1, (lane >> 4) & 1, (lane >> 3) & 1);
+  const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
   const int acc_words = n_waves * BB * NV;
 
-  for (int64_t b1 = stop; b1 > start; b1 -= BB) {
-    const int64_t b0 = max<int64_t>(start, b1 - BB);
-    __syncthreads();  // previous batch fully consumed and flushed
-    const int64_t j = b1 - 1 - t;  // slot k holds entry b1 - 1 - k (back to front)
-    if (t < BB && j >= b0) {
-      float2 xy;
-      float4 co;
-      const int32_t g = load_gaussian(a, j, &xy, &co);
-      s_xy[t] = xy;
-      s_co[t] = co;
-      s_g[t] = g;
-      if constexpr (CH > 0) {
-#pragma unroll
-        for (int c = 0; c < CH; ++c) s_col[t * CH + c] = a.colors[static_cast<int64_t>(g) * CH + c];
-      }
-    }
-    // acc_words is a multiple of 4 (BB is a multiple of 64)
-    for (int w = t * 4; w < acc_words; w += BS * 4)
-      *reinterpret_cast<float4*>(s_acc + w) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  for (;;) {
+    __syncthreads();  // the previous unit is done with LDS
+    if (t == 0) s_unit = atomicAdd(unit_counter, 1);
     __syncthreads();
-    const int cnt = static_cast<int>(b1 - b0);
-    for (int k = 0; k < cnt; ++k) {
-      const int64_t idx = b1 - 1 - k;
-      if (idx > wave_last) continue;  // wave-uniform
-      const float2 m = s_xy[k];
-      const float4 co = s_co[k];
-      const float dx = m.x - px;
-      const float dy = m.y - py;
-      const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
-      const float vis = expf(-sigma);
-      const float alpha = fminf(kMaxAlpha, co.w * vis);
-      const bool valid = idx <= bin_final && !(sigma < 0.0f || alpha < kAlphaThreshold);
-      if (__ballot(valid) == 0) continue;
-      float v[NV];
+    const int64_t unit = s_unit;
+    if (unit >= n_units) break;  // uniform across the block
+    const int64_t it = order[unit / n_bands];
+    const int band = static_cast<int>(unit % n_bands);
+    const int64_t image = it / n_tiles;
+    const int tile = static_cast<int>(it % n_tiles);
+    const int tx = tile % a.tw, ty = tile / a.tw;
+    if (a.masks && !a.masks[image * n_tiles + tile]) continue;  // masked tiles contribute nothing
+    const float* bg = a.backgrounds ? a.backgrounds + image * channels : nullptr;
+    int64_t start, end;
+    tile_range(a, image, tile, &start, &end);
+
+    // per-pixel state; blocks are padded to whole wave64s (the reductions
+    // need every lane) and padding pixels own nothing
+    float px[P], py[P], T[P], B[P], coef[P];
+    int last_rel[P];  // last contributor relative to start, -1 for none
+    float v_rc[P][AC];
+    int my_last = -1;
 #pragma unroll
-      for (int i = 0; i < NV; ++i) v[i] = 0.0f;
-      float v_col_generic[CH > 0 ? 1 : kMaxChannels];
-      if (valid) {
-        const float ra = __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - alpha));
-        T *= ra;
-        const float fac = alpha * T;
-        float v_alpha = 0.0f;
+    for (int p = 0; p < P; ++p) {
+      const int q = ((band * n_waves + wave) * P + p) * kWave + lane;
+      const int x = tx * a.ts + q % a.ts;
+      const int y = ty * a.ts + q / a.ts;
+      const bool inside = q < a.ts * a.ts && x < a.W && y < a.H;
+      const int64_t pix = (image * a.H + y) * static_cast<int64_t>(a.W) + x;
+      px[p] = static_cast<float>(x) + 0.5f;
+      py[p] = static_cast<float>(y) + 0.5f;
+      const float T_final = inside ? 1.0f - render_alphas[pix] : 1.0f;
+      T[p] = T_final;
+      B[p] = 0.0f;
+      last_rel[p] = -1;
+      if (inside) {
+        const int64_t l = min<int64_t>(end - 1, last_ids[pix]) - start;
+        last_rel[p] = static_cast<int>(max<int64_t>(-1, min<int64_t>(l, INT32_MAX)));
+      }
+      my_last = max(my_last, last_rel[p]);
+      float bg_dot = 0.0f;
+      for (int c = 0; c < channels; ++c) v_rc[p][c] = inside ? v_render_colors[pix * channels + c] : 0.0f;
+      const float v_ra = inside ? v_render_alphas[pix] : 0.0f;
+      if (bg) {
+        for (int c = 0; c < channels; ++c) bg_dot += bg[c] * v_rc[p][c];
+        // v_backgrounds = sum over pixels of T_final * v_rc (gsplat_rasterize.cpp:459-464)
+        for (int c = 0; c < channels; ++c) {
+          const float sum = wave_sum_uniform(T_final * v_rc[p][c]);
+          if (lane == 0) unsafeAtomicAdd(v_backgrounds + image * channels + c, sum);
+        }
+      }
+      // d(final-transmittance terms)/d(alpha) = ra * coef
+      coef[p] = T_final * v_ra + -T_final * bg_dot;
+    }
+
+    // Entries past every pixel's last contributor are skipped wholesale: the
+    // block starts at its largest last_id, each wave skips entries past its own.
+    if (t == 0) s_max_last = -1;
+    __syncthreads();
+    if (my_last >= 0) atomicMax(&s_max_last, my_last);
+    int wave_last = my_last;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) wave_last = max(wave_last, __shfl_xor(wave_last, off, kWave));
+    __syncthreads();
+    const int64_t stop = start + s_max_last + 1;  // exclusive end of the needed range
+
+    // register prefetch of one batch record (lanes t < BB)
+    float2 r_xy = make_float2(0.0f, 0.0f);
+    float4 r_co = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int32_t r_g = 0;
+    float r_col[LC];
+    auto fetch = [&](int64_t hi, int64_t lo) {
+      const int64_t j = hi - 1 - t;  // slot t holds entry hi - 1 - t (back to front)
+      if (t < BB && j >= lo) {
+        r_g = load_gaussian(a, j, &r_xy, &r_co);
         if constexpr (CH > 0) {
 #pragma unroll
-          for (int c = 0; c < CH; ++c) {
-            const float col = s_col[k * CH + c];
-            v[c] = fac * v_rc[c];
-            v_alpha += (col * T - buffer[c] * ra) * v_rc[c];
-            buffer[c] += col * fac;
+          for (int c = 0; c < CH; ++c) r_col[c] = a.colors[static_cast<int64_t>(r_g) * CH + c];
+        }
+      }
+    };
+    if (stop > start) fetch(stop, max<int64_t>(start, stop - BB));
+
+    for (int64_t b1 = stop; b1 > start; b1 -= BB) {
+      const int64_t b0 = max<int64_t>(start, b1 - BB);
+      __syncthreads();  // previous batch fully consumed and flushed
+      if (t < BB && b1 - 1 - t >= b0) {
+        s_xy[t] = r_xy;
+        s_co[t] = r_co;
+        s_g[t] = r_g;
+        if constexpr (CH > 0) {
+#pragma unroll
+          for (int c = 0; c < CH; ++c) s_col[t * CH + c] = r_col[c];
+        }
+      }
+      // acc_words is a multiple of 4 (BB is a multiple of 64)
+      for (int w = t * 4; w < acc_words; w += BS * 4)
+        *reinterpret_cast<float4*>(s_acc + w) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      __syncthreads();
+      if (b0 > start) fetch(b0, max<int64_t>(start, b0 - BB));  // next batch, in flight during this one
+      const int cnt = static_cast<int>(b1 - b0);
+      const int k_rel0 = static_cast<int>(b1 - 1 - start);  // entry of slot 0, relative to start
+      for (int k = 0; k < cnt; ++k) {
+        const int k_rel = k_rel0 - k;
+        if (k_rel > wave_last) continue;  // wave-uniform
+        const float2 m = s_xy[k];
+        const float4 co = s_co[k];
+        float col[LC];
+        if constexpr (CH > 0) {
+#pragma unroll
+          for (int c = 0; c < CH; ++c) col[c] = s_col[k * CH + c];
+        }
+        const float* gcol = nullptr;
+        if constexpr (CH == 0) gcol = a.colors + static_cast<int64_t>(s_g[k]) * channels;
+        float v[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) v[i] = 0.0f;
+        float v_col_generic[CH > 0 ? 1 : kMaxChannels];
+        if constexpr (CH == 0) {
+          for (int c = 0; c < channels; ++c) v_col_generic[c] = 0.0f;
+        }
+        bool any = false;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          const float dx = m.x - px[p];
+          const float dy = m.y - py[p];
+          const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
+          const float vis = expf(-sigma);
+          const float a_raw = co.w * vis;
+          const float alpha = fminf(kMaxAlpha, a_raw);
+          const bool valid = k_rel <= last_rel[p] && !(sigma < 0.0f || alpha < kAlphaThreshold);
+          if (!valid) continue;
+          any = true;
+          const float ra = __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - alpha));
+          T[p] *= ra;
+          const float fac = alpha * T[p];
+          float D = 0.0f;
+          if constexpr (CH > 0) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c) {
+              D += col[c] * v_rc[p][c];
+              v[c] += fac * v_rc[p][c];
+            }
+          } else {
+            for (int c = 0; c < channels; ++c) {
+              D += gcol[c] * v_rc[p][c];
+              v_col_generic[c] = fac * v_rc[p][c];
+            }
           }
-        } else {
-          const float* col = a.colors + static_cast<int64_t>(s_g[k]) * channels;
+          const float v_alpha = T[p] * D + ra * (coef[p] - B[p]);
+          B[p] += fac * D;
+          if (a_raw <= kMaxAlpha) {
+            const float v_sigma = -a_raw * v_alpha;
+            const float hx = v_sigma * dx;
+            const float hy = v_sigma * dy;
+            v[o + 0] += hx * dx;
+            v[o + 1] += hx * dy;
+            v[o + 2] += hy * dy;
+            v[o + 3] += hx;
+            v[o + 4] += hy;
+            v[o + 5] += vis * v_alpha;
+            if constexpr (ABS) {
+              v[o + 6] += fabsf(co.x * hx + co.y * hy);
+              v[o + 7] += fabsf(co.y * hx + co.z * hy);
+            }
+          }
+        }
+        if (__ballot(any) == 0) continue;
+        if constexpr (CH == 0) {
+          const int64_t gg = s_g[k];
           for (int c = 0; c < channels; ++c) {
-            v_col_generic[c] = fac * v_rc[c];
-            v_alpha += (col[c] * T - buffer[c] * ra) * v_rc[c];
-            buffer[c] += col[c] * fac;
+            const float sum = wave_sum_uniform(v_col_generic[c]);
+            if (lane == 0 && sum != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, sum);
           }
         }
-        v_alpha += ra * (t_final_ra_coef + t_final_bg_coef);
-        if (co.w * vis <= kMaxAlpha) {
-          const float v_sigma = -co.w * vis * v_alpha;
-          const float vx = v_sigma * (co.x * dx + co.y * dy);
-          const float vy = v_sigma * (co.y * dx + co.z * dy);
-          constexpr int o = CH > 0 ? CH : 0;
-          v[o + 0] = 0.5f * v_sigma * dx * dx;
-          v[o + 1] = v_sigma * dx * dy;
-          v[o + 2] = 0.5f * v_sigma * dy * dy;
-          v[o + 3] = vx;
-          v[o + 4] = vy;
-          v[o + 5] = vis * v_alpha;
-          if constexpr (ABS) {
-            v[o + 6] = fabsf(vx);
-            v[o + 7] = fabsf(vy);
-          }
-        }
-      } else if constexpr (CH == 0) {
-        for (int c = 0; c < channels; ++c) v_col_generic[c] = 0.0f;
-      }
-      if constexpr (CH == 0) {
-        // generic channel count: colour gradients go straight to global memory
-        const int64_t gg = s_g[k];
-        for (int c = 0; c < channels; ++c) {
-          const float s = wave_sum_uniform(v_col_generic[c]);
-          if (lane == 0 && s != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, s);
+        float y[NC];
+        wave_transpose_reduce<NV>(v, y, e_bit);
+        if (red_slot == 7) {
+          float* acc = s_acc + (wave * BB + k) * NV;
+#pragma unroll
+          for (int mm = 0; mm < NC; ++mm) acc[red_idx[mm]] = y[mm];
         }
       }
-      wave_reduce_lane63<NV>(v);
-      if (lane == kWave - 1) {
-        float* acc = s_acc + (wave * BB + k) * NV;
+      __syncthreads();
+      // flush: thread t owns slot t (entry b1 - 1 - t); sums the waves' slots
+      if (t < cnt) {
+        float acc[NV];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) acc[i] = v[i];
-      }
-    }
-    __syncthreads();
-    // flush: thread t owns slot t (entry b1 - 1 - t); sums the waves' slots
-    if (t < cnt) {
-      float acc[NV];
+        for (int i = 0; i < NV; ++i) acc[i] = s_acc[t * NV + i];
+        for (int w = 1; w < n_waves; ++w) {
 #pragma unroll
-      for (int i = 0; i < NV; ++i) acc[i] = s_acc[t * NV + i];
-      for (int w = 1; w < n_waves; ++w) {
+          for (int i = 0; i < NV; ++i) acc[i] += s_acc[(w * BB + t) * NV + i];
+        }
+        const int64_t gg = s_g[t];
+        const float4 co = s_co[t];
+        if constexpr (CH > 0) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) acc[i] += s_acc[(w * BB + t) * NV + i];
-      }
-      const int64_t gg = s_g[t];
-      constexpr int o = CH > 0 ? CH : 0;
-      if constexpr (CH > 0) {
-#pragma unroll
-        for (int c = 0; c < CH; ++c)
-          if (acc[c] != 0.0f) unsafeAtomicAdd(v_colors + gg * CH + c, acc[c]);
-      }
-      if (acc[o + 0] != 0.0f) unsafeAtomicAdd(v_conics + gg * 3, acc[o + 0]);
-      if (acc[o + 1] != 0.0f) unsafeAtomicAdd(v_conics + gg * 3 + 1, acc[o + 1]);
-      if (acc[o + 2] != 0.0f) unsafeAtomicAdd(v_conics + gg * 3 + 2, acc[o + 2]);
-      if (acc[o + 3] != 0.0f) unsafeAtomicAdd(v_means2d + gg * 2, acc[o + 3]);
-      if (acc[o + 4] != 0.0f) unsafeAtomicAdd(v_means2d + gg * 2 + 1, acc[o + 4]);
-      if (acc[o + 5] != 0.0f) unsafeAtomicAdd(v_opacities + gg, acc[o + 5]);
-      if constexpr (ABS) {
-        if (acc[o + 6] != 0.0f) unsafeAtomicAdd(v_means2d_abs + gg * 2, acc[o + 6]);
-        if (acc[o + 7] != 0.0f) unsafeAtomicAdd(v_means2d_abs + gg * 2 + 1, acc[o + 7]);
+          for (int c = 0; c < CH; ++c)
+            if (acc[c] != 0.0f) unsafeAtomicAdd(v_colors + gg * CH + c, acc[c]);
+        }
+        const float vc0 = 0.5f * acc[o + 0], vc1 = acc[o + 1], vc2 = 0.5f * acc[o + 2];
+        const float vmx = co.x * acc[o + 3] + co.y * acc[o + 4];
+        const float vmy = co.y * acc[o + 3] + co.z * acc[o + 4];
+        if (vc0 != 0.0f) unsafeAtomicAdd(v_conics + gg * 3, vc0);
+        if (vc1 != 0.0f) unsafeAtomicAdd(v_conics + gg * 3 + 1, vc1);
+        if (vc2 != 0.0f) unsafeAtomicAdd(v_conics + gg * 3 + 2, vc2);
+        if (vmx != 0.0f) unsafeAtomicAdd(v_means2d + gg * 2, vmx);
+        if (vmy != 0.0f) unsafeAtomicAdd(v_means2d + gg * 2 + 1, vmy);
+        if (acc[o + 5] != 0.0f) unsafeAtomicAdd(v_opacities + gg, acc[o + 5]);
+        if constexpr (ABS) {
+          if (acc[o + 6] != 0.0f) unsafeAtomicAdd(v_means2d_abs + gg * 2, acc[o + 6]);
+          if (acc[o + 7] != 0.0f) unsafeAtomicAdd(v_means2d_abs + gg * 2 + 1, acc[o + 7]);
+        }
       }
     }
   }
 }
 
+// Heavy-first tile schedule for the backward. A tile's cost is the number of
+// list entries its pixels replay (largest last_id - start + 1, 0 when masked
+// or empty). Blocks are dispatched in descending cost order, so the longest
+// tiles start first and the end of the launch is made of short ones (greedy
+// longest-processing-time scheduling over the hardware's dynamic dispatch).
+constexpr int kCostBuckets = 4096;  // costs >= 4095 share the heaviest bucket
+
+__global__ void __launch_bounds__(256) tile_cost_kernel(RasterArgs a, const int32_t* __restrict__ last_ids,
+                                                        int32_t* __restrict__ cost) {
+  __shared__ int s_best[256 / kWave];
+  const int tx = blockIdx.x, ty = blockIdx.y;
+  const int64_t image = blockIdx.z;
+  const int tile = ty * a.tw + tx;
+  const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
+  const int t = threadIdx.x;
+  int64_t start, end;
+  tile_range(a, image, tile, &start, &end);
+  int best = 0;
+  if (!(a.masks && !a.masks[image * n_tiles + tile])) {
+    for (int q = t; q < a.ts * a.ts; q += 256) {
+      const int x = tx * a.ts + q % a.ts;
+      const int y = ty * a.ts + q / a.ts;
+      if (x >= a.W || y >= a.H) continue;
+      const int64_t last = min<int64_t>(end - 1, last_ids[(image * a.H + y) * static_cast<int64_t>(a.W) + x]);
+      best = max(best, static_cast<int>(min<int64_t>(max<int64_t>(last - start + 1, 0), INT32_MAX)));
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) best = max(best, __shfl_xor(best, off, kWave));
+  if (t % kWave == 0) s_best[t / kWave] = best;
+  __syncthreads();
+  if (t == 0) {
+    for (int w = 1; w < 256 / kWave; ++w) best = max(best, s_best[w]);
+    cost[image * n_tiles + tile] = best;
+  }
+}
+
+// One block: counting sort of the n tile costs into descending order.
+__global__ void __launch_bounds__(kScanBlock) tile_order_kernel(const int32_t* __restrict__ cost, int64_t n,
+                                                                int32_t* __restrict__ order,
+                                                                int32_t* __restrict__ unit_counter) {
+  static_assert(kCostBuckets % kScanBlock == 0, "buckets per thread");
+  constexpr int PER = kCostBuckets / kScanBlock;
+  __shared__ int hist[kCostBuckets];
+  const int t = threadIdx.x;
+  if (t == 0) *unit_counter = 0;  // the backward's work counter starts from the first unit
+  for (int i = t; i < kCostBuckets; i += kScanBlock) hist[i] = 0;
+  __syncthreads();
+  for (int64_t i = t; i < n; i += kScanBlock) atomicAdd(&hist[kCostBuckets - 1 - min(cost[i], kCostBuckets - 1)], 1);
+  __syncthreads();
+  int sum = 0;
+#pragma unroll
+  for (int j = 0; j < PER; ++j) sum += hist[t * PER + j];
+  int64_t total;
+  int running = static_cast<int>(block_exclusive_scan(sum, &total));
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int v = hist[t * PER + j];
+    hist[t * PER + j] = running;
+    running += v;
+  }
+  __syncthreads();
+  for (int64_t i = t; i < n; i += kScanBlock) {
+    const int pos = atomicAdd(&hist[kCostBuckets - 1 - min(cost[i], kCostBuckets - 1)], 1);
+    order[pos] = static_cast<int32_t>(i);
+  }
+}
+
+size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+// cost [n] int32, order [n] int32, unit counter int32
+size_t bwd_workspace_bytes(int64_t n_tiles_total) {
+  return 2 * align256(static_cast<size_t>(n_tiles_total) * 4) + 256;
+}
+
+// Resident blocks of `kernel` on the current device (persistent launches).
+int64_t resident_blocks(const void* kernel, int block, size_t smem) {
+  int dev = 0, cus = 0, per_cu = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, smem) != hipSuccess || per_cu <= 0 ||
+      cus <= 0)
+    return 0;
+  return static_cast<int64_t>(per_cu) * cus;
+}
+
 size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (6 + (ch > 0 ? ch : 0) + (ch > 0 ? 0 : 1)) * 4; }
-// Backward batch length: 128 entries for blocks of up to 256 lanes, 64 above
-// (bounds the per-wave accumulators to 48 KiB at 1024 lanes, 4 channels,
-// absgrad); never more than the block so one lane loads one record.
-int bwd_batch(int bs) { return bs <= 128 ? bs : (bs <= 256 ? 128 : 64); }
+// Backward work split: pixels per lane and waves per block; a tile's pixels
+// are split over n_bands blocks of bwd_block lanes.
+// Backward work split: one pixel per lane and the whole tile in one block
+// (measured fastest on gfx950 for 16x16 tiles against 2 or 4 pixels per lane
+// and against splitting a tile over several blocks: the lower register count
+// keeps six waves per SIMD resident). Batch length: 128 entries for blocks of
+// up to 256 lanes, 64 above (bounds the per-wave accumulators to 48 KiB at
+// 1024 lanes, 4 channels, absgrad); never more than the block, so one lane
+// loads one record.
+struct BwdShape {
+  int ppl, bs, n_bands, bb;
+};
+BwdShape bwd_shape(int ts) {
+  const int bs = (ts * ts + kWave - 1) / kWave * kWave;
+  return {1, bs, 1, bs <= 128 ? bs : (bs <= 256 ? 128 : 64)};
+}
 // records (7 + colors) per batch slot plus NV accumulators per (wave, slot)
-size_t bwd_smem(int ch, int bs, bool absgrad) {
-  const int bb = bwd_batch(bs);
+size_t bwd_smem(int ch, int bs, int bb, bool absgrad) {
   const int cc = ch > 0 ? ch : 0;
   const int nv = cc + (absgrad ? 8 : 6);
   return static_cast<size_t>(bb) * (7 + cc + (bs / kWave) * nv) * 4;
@@ -477,7 +690,8 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
                                         const float* render_alphas, const int32_t* last_ids,
                                         const float* v_render_colors, const float* v_render_alphas,
                                         float* v_means2d_abs, float* v_means2d, float* v_conics, float* v_colors,
-                                        float* v_opacities, float* v_backgrounds, void* stream) {
+                                        float* v_opacities, float* v_backgrounds, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
   RasterArgs a{means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, N, channels,
                image_width, image_height, tile_size, tile_width, tile_height, I, n_isects};
   int rc = check_args(a, "rasterize_to_pixels_3dgs_backward");
@@ -495,31 +709,65 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   if (v_means2d_abs && (rc = fill_zero(v_means2d_abs, G * 2 * sizeof(float), s))) return rc;
   if (backgrounds && (rc = fill_zero(v_backgrounds, I * channels * sizeof(float), s))) return rc;
   if (I == 0 || tile_width == 0 || tile_height == 0) return GSPLAT_OK;
+  const dim3 grid(tile_width, tile_height, static_cast<unsigned>(I));
   if (!tile_offsets || !render_alphas || !last_ids || !v_render_colors || !v_render_alphas ||
       (n_isects > 0 && (!flatten_ids || !means2d || !conics || !colors || !opacities)))
     return invalid("rasterize_to_pixels_3dgs_backward: null pointer.");
-  const dim3 grid(tile_width, tile_height, static_cast<unsigned>(I));
-  const int bs = (tile_size * tile_size + kWave - 1) / kWave * kWave;
   const int ch = channels <= 4 ? channels : 0;
-  const size_t sm = bwd_smem(ch, bs, v_means2d_abs != nullptr);
-  const int bb = bwd_batch(bs);
-  KernelTimer timer("raster_bwd", s);
-#define GSPLAT_BWD_LAUNCH(C)                                                                                     \
-  if (v_means2d_abs)                                                                                             \
-    raster_bwd_kernel<C, true><<<grid, bs, sm, s>>>(a, bb, render_alphas, last_ids, v_render_colors, v_render_alphas, \
-                                                    v_means2d_abs, v_means2d, v_conics, v_colors, v_opacities,   \
-                                                    v_backgrounds);                                              \
-  else                                                                                                           \
-    raster_bwd_kernel<C, false><<<grid, bs, sm, s>>>(a, bb, render_alphas, last_ids, v_render_colors,                 \
-                                                     v_render_alphas, nullptr, v_means2d, v_conics, v_colors,     \
-                                                     v_opacities, v_backgrounds)
-  switch (ch) {
-    case 1: GSPLAT_BWD_LAUNCH(1); break;
-    case 2: GSPLAT_BWD_LAUNCH(2); break;
-    case 3: GSPLAT_BWD_LAUNCH(3); break;
-    case 4: GSPLAT_BWD_LAUNCH(4); break;
-    default: GSPLAT_BWD_LAUNCH(0); break;
+  const BwdShape shape = bwd_shape(tile_size);
+  const int bs = shape.bs;
+  const int64_t n_total = I * tile_width * static_cast<int64_t>(tile_height);
+  // the int32 unit counter may run past n_units by one per resident block
+  if (n_total * shape.n_bands > INT32_MAX / 2) return invalid("rasterize_to_pixels_3dgs_backward: too many tiles.");
+  if (!workspace || workspace_bytes < bwd_workspace_bytes(n_total)) {
+    set_error("rasterize_to_pixels_3dgs_backward: workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
   }
+  int32_t* cost = static_cast<int32_t*>(workspace);
+  int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(n_total * 4));
+  int32_t* counter = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + 2 * align256(n_total * 4));
+  {
+    KernelTimer timer("raster_bwd_schedule", s);
+    tile_cost_kernel<<<grid, 256, 0, s>>>(a, last_ids, cost);
+    tile_order_kernel<<<1, kScanBlock, 0, s>>>(cost, n_total, order, counter);
+  }
+  if ((rc = check_launch("rasterize_to_pixels_3dgs_backward"))) return rc;
+  const int64_t n_units = n_total * shape.n_bands;
+  const int bb = shape.bb;
+  const size_t sm = bwd_smem(ch, bs, bb, v_means2d_abs != nullptr);
+  KernelTimer timer("raster_bwd", s);
+  // persistent launch: as many blocks as fit on the device at once, each
+  // taking units from the counter until all are done
+#define GSPLAT_BWD_LAUNCH(C, ABS_, PPL, VABS)                                                                   \
+  {                                                                                                            \
+    const void* fn = reinterpret_cast<const void*>(&raster_bwd_kernel<C, ABS_, PPL>);                          \
+    const int64_t res = resident_blocks(fn, bs, sm);                                                           \
+    if (res <= 0) return check_hip(hipGetLastError(), "rasterize_to_pixels_3dgs_backward: occupancy query");   \
+    const unsigned nb = static_cast<unsigned>(std::min<int64_t>(n_units, res));                                \
+    raster_bwd_kernel<C, ABS_, PPL><<<nb, bs, sm, s>>>(a, bb, shape.n_bands, n_units, order, counter,          \
+                                                       render_alphas, last_ids, v_render_colors, v_render_alphas, \
+                                                       VABS, v_means2d, v_conics, v_colors, v_opacities,        \
+                                                       v_backgrounds);                                          \
+  }
+#define GSPLAT_BWD_ABS(C, PPL)                          \
+  if (v_means2d_abs) {                                  \
+    GSPLAT_BWD_LAUNCH(C, true, PPL, v_means2d_abs)      \
+  } else {                                              \
+    GSPLAT_BWD_LAUNCH(C, false, PPL, nullptr)           \
+  }
+  switch (ch) {
+    case 1: GSPLAT_BWD_ABS(1, 1); break;
+    case 2: GSPLAT_BWD_ABS(2, 1); break;
+    case 3: GSPLAT_BWD_ABS(3, 1); break;
+    case 4: GSPLAT_BWD_ABS(4, 1); break;
+    default: GSPLAT_BWD_ABS(0, 1); break;
+  }
+#undef GSPLAT_BWD_ABS
 #undef GSPLAT_BWD_LAUNCH
   return check_launch("rasterize_to_pixels_3dgs_backward");
+}
+
+extern "C" size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t tile_width, int32_t tile_height) {
+  if (I <= 0 || tile_width <= 0 || tile_height <= 0) return 0;
+  return bwd_workspace_bytes(I * tile_width * static_cast<int64_t>(tile_height));
 }
