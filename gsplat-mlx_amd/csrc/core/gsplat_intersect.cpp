@@ -214,13 +214,24 @@ std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& in
   const array depths = contig(input.depths);
   array ids = at::empty({total}, i64_like(means2d));
   array flat = at::empty({total}, i32_like(means2d));
+  if (input.params.sort) {
+    // depth-presorted encode + 32-bit key sort; same result as encode
+    // followed by the stable 64-bit key sort
+    const size_t ws_bytes = gsplat_hip_isect_tile_sorted_workspace_size(depths.numel(), total);
+    array ws = workspace(ws_bytes, means2d);
+    check(gsplat_hip_isect_tile_sorted(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(),
+                                       depths.data_ptr<float>(), c.tiles_per_gauss.data_ptr<int32_t>(),
+                                       input.params.I, depths.numel(), input.params.tile_size,
+                                       input.params.tile_width, input.params.tile_height, total,
+                                       ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), ws.data_ptr<uint8_t>(),
+                                       ws_bytes, stream));
+    return {c.tiles_per_gauss, ids, flat};
+  }
   check(gsplat_hip_isect_encode(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), depths.data_ptr<float>(),
                                 c.offsets.data_ptr<int32_t>(), input.params.I, depths.numel(),
                                 input.params.tile_size, input.params.tile_width, input.params.tile_height, total,
                                 ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), stream));
-  if (!input.params.sort) return {c.tiles_per_gauss, ids, flat};
-  auto sorted = sort_pairs(ids, flat, encoded_key_bits(input.params.I, n_tiles), stream);
-  return {c.tiles_per_gauss, sorted[0], sorted[1]};
+  return {c.tiles_per_gauss, ids, flat};
 }
 
 std::vector<array> gsplat_intersect_tile(const IntersectTileInput& input) {

@@ -5,8 +5,10 @@
 // key layout), :309-339 (count), :433-485 (encode order) and :605-641
 // (offsets = lower_bound). Tile ids are bit-exact with the reference: the rect
 // uses the same float divisions, floor/ceil and clamps.
+#include <algorithm>
 #include <cmath>
 
+#include "radix_sort.hpp"
 #include "scan.hpp"
 
 namespace gsplat_hip {
@@ -152,6 +154,136 @@ __global__ void __launch_bounds__(kEncodeBlock) encode_kernel(const float* __res
   }
 }
 
+// ---------------------------------------------------------------------------
+// Depth-presorted pipeline: the sorted output of encode + stable sort by the
+// 64-bit key, without sorting 64-bit keys over all intersections.
+//  1. (image, gaussian) pairs are stably sorted by their depth bits (32-bit
+//     keys over the I*N pairs);
+//  2. the per-pair tile counts are gathered in that order and scanned;
+//  3. the encoder writes each pair's tiles in depth order with 32-bit keys
+//     image << tile_bits | tile;
+//  4. a stable sort of those keys (image_bits + tile_bits bits, usually two
+//     8-bit passes) groups entries by (image, tile) and keeps depth order
+//     inside each group;
+//  5. the 64-bit keys are rebuilt as key32 << 32 | depth bits.
+// Equal 64-bit keys come out in ascending pair index, exactly as a stable sort
+// of the encode order (pair-major) leaves them.
+
+__global__ void __launch_bounds__(256) depth_keys_kernel(const float* __restrict__ depths, int64_t n,
+                                                         uint32_t* __restrict__ keys, int32_t* __restrict__ idx) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  keys[i] = __float_as_uint(depths[i]);
+  idx[i] = static_cast<int32_t>(i);
+}
+
+__global__ void __launch_bounds__(256) gather_counts_kernel(const int32_t* __restrict__ counts,
+                                                            const int32_t* __restrict__ perm, int64_t n,
+                                                            int32_t* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) out[i] = counts[perm[i]];
+}
+
+// Encode in depth order: a block owns kEncodeG consecutive ranks (pairs
+// perm[rank]) and their contiguous output range (offsets over ranks), found
+// per output slot by binary search as in encode_kernel.
+__global__ void __launch_bounds__(kEncodeBlock) encode_presorted_kernel(
+    const float* __restrict__ means2d, const int32_t* __restrict__ radii, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ offsets, int64_t numel, int64_t n_per_image, int ts, int tw, int th, int tile_bits,
+    int64_t n_isects, uint32_t* __restrict__ keys, int32_t* __restrict__ vals) {
+  __shared__ int32_t s_off[kEncodeG];
+  __shared__ int32_t s_minx[kEncodeG];
+  __shared__ int32_t s_miny[kEncodeG];
+  __shared__ int32_t s_w[kEncodeG];
+  __shared__ uint32_t s_hi[kEncodeG];  // image << tile_bits
+  __shared__ int32_t s_g[kEncodeG];
+  __shared__ int64_t s_end;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kEncodeG;
+  const int cnt = static_cast<int>(min<int64_t>(kEncodeG, numel - r0));
+  const int t = threadIdx.x;
+  if (t < cnt) {
+    const int64_t g = perm[r0 + t];
+    const TileRect r = aabb_tile_rect(means2d[g * 2], means2d[g * 2 + 1], radii[g * 2], radii[g * 2 + 1], ts, tw, th);
+    const int32_t off = offsets[r0 + t];
+    s_off[t] = off;
+    s_minx[t] = r.min_x;
+    s_miny[t] = r.min_y;
+    s_w[t] = r.max_x - r.min_x;
+    s_hi[t] = static_cast<uint32_t>(g / n_per_image) << tile_bits;
+    s_g[t] = static_cast<int32_t>(g);
+    if (t == cnt - 1) s_end = static_cast<int64_t>(off) + (r.max_y - r.min_y) * (r.max_x - r.min_x);
+  }
+  __syncthreads();
+  const int64_t start = max<int64_t>(s_off[0], 0);
+  const int64_t end = min<int64_t>(s_end, n_isects);
+  for (int64_t o = start + t; o < end; o += kEncodeBlock) {
+    int lo = 0, hi = cnt - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_off[mid] <= o)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    const int j = lo;
+    const int k = static_cast<int>(o - s_off[j]);
+    const int w = max(s_w[j], 1);
+    const int row = k / w;
+    const int col = k - row * w;
+    const uint32_t tile = static_cast<uint32_t>((s_miny[j] + row) * tw + (s_minx[j] + col));
+    keys[o] = s_hi[j] | tile;
+    vals[o] = s_g[j];
+  }
+}
+
+__global__ void __launch_bounds__(256) assemble_ids_kernel(const uint32_t* __restrict__ keys,
+                                                           const int32_t* __restrict__ flat,
+                                                           const float* __restrict__ depths, int64_t n,
+                                                           int64_t* __restrict__ isect_ids) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  isect_ids[i] = static_cast<int64_t>((static_cast<uint64_t>(keys[i]) << 32) | __float_as_uint(depths[flat[i]]));
+}
+
+struct PresortLayout {
+  uint32_t* dkeys;
+  int32_t* didx;
+  uint32_t* dkeys_sorted;
+  int32_t* perm;
+  int32_t* offs;
+  uint32_t* tkeys;
+  int32_t* tvals;
+  uint32_t* tkeys_sorted;
+  void* sort_ws;
+  size_t sort_ws_bytes;
+  void* scan_ws;
+};
+
+inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+size_t presort_layout(int64_t numel, int64_t n_isects, PresortLayout* l, void* base) {
+  const size_t pn = align256(static_cast<size_t>(numel) * 4);
+  const size_t pm = align256(static_cast<size_t>(n_isects) * 4);
+  const size_t sort_b =
+      align256(std::max(radix_sort_workspace_bytes<uint32_t>(numel), radix_sort_workspace_bytes<uint32_t>(n_isects)));
+  const size_t scan_b = align256(scan_workspace_bytes(numel));
+  if (l && base) {
+    char* p = static_cast<char*>(base);
+    l->dkeys = reinterpret_cast<uint32_t*>(p);
+    l->didx = reinterpret_cast<int32_t*>(p + pn);
+    l->dkeys_sorted = reinterpret_cast<uint32_t*>(p + 2 * pn);
+    l->perm = reinterpret_cast<int32_t*>(p + 3 * pn);
+    l->offs = reinterpret_cast<int32_t*>(p + 4 * pn);
+    l->tkeys = reinterpret_cast<uint32_t*>(p + 5 * pn);
+    l->tvals = reinterpret_cast<int32_t*>(p + 5 * pn + pm);
+    l->tkeys_sorted = reinterpret_cast<uint32_t*>(p + 5 * pn + 2 * pm);
+    l->sort_ws = p + 5 * pn + 3 * pm;
+    l->sort_ws_bytes = sort_b;
+    l->scan_ws = p + 5 * pn + 3 * pm + sort_b;
+  }
+  return 5 * pn + 3 * pm + sort_b + scan_b;
+}
+
 // Tile offsets as lower_bound over sorted keys (gsplat_intersect.cpp:605-641),
 // computed in O(n_isects): entry i owns the offset slots o whose search key
 // (o / n_tiles) << tile_bits | (o % n_tiles) lies in (v[i-1], v[i]], with
@@ -278,4 +410,68 @@ extern "C" int gsplat_hip_isect_offset(const int64_t* isect_ids, int64_t n_isect
     offsets_kernel<<<grid_for(n_isects, 256), 256, 0, s>>>(isect_ids, n_isects, tile_bits, n_tiles, n_offsets, offsets);
   }
   return check_launch("intersect_offset");
+}
+
+extern "C" size_t gsplat_hip_isect_tile_sorted_workspace_size(int64_t numel, int64_t n_isects) {
+  if (numel <= 0 || n_isects <= 0) return 0;
+  return presort_layout(numel, n_isects, nullptr, nullptr);
+}
+
+extern "C" int gsplat_hip_isect_tile_sorted(const float* means2d, const int32_t* radii, const float* depths,
+                                            const int32_t* tiles_per_gauss, int64_t I, int64_t numel,
+                                            int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                            int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "intersect_tile";
+  if (I <= 0 || numel < 0 || numel % I != 0)
+    return invalid("intersect_tile dense path expects depths size to equal I * N.");
+  if (tile_size <= 0 || tile_width <= 0 || tile_height <= 0) return invalid("intersect_tile: invalid tiles.");
+  if (n_isects < 0) return invalid("intersect_tile: negative intersection count.");
+  if (numel > INT32_MAX || n_isects > INT32_MAX) return invalid("intersect_tile: more than 2^31-1 entries.");
+  const int64_t n_tiles = static_cast<int64_t>(tile_width) * tile_height;
+  const int tile_bits = floor_log2_plus_one(n_tiles);
+  const int image_bits = floor_log2_plus_one(I);
+  if (image_bits + tile_bits > 32)
+    return invalid("intersect_tile_encode image id and tile id require more than 32 bits.");
+  if (numel == 0 || n_isects == 0) return GSPLAT_OK;
+  if (!means2d || !radii || !depths || !tiles_per_gauss || !isect_ids || !flatten_ids)
+    return invalid("intersect_tile: null pointer.");
+  PresortLayout l;
+  if (!workspace || workspace_bytes < presort_layout(numel, n_isects, &l, workspace)) {
+    set_error("intersect_tile: workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  hipStream_t s = as_stream(stream);
+  int rc;
+  {
+    KernelTimer timer("isect_depth_keys", s);
+    depth_keys_kernel<<<grid_for(numel, 256), 256, 0, s>>>(depths, numel, l.dkeys, l.didx);
+  }
+  if ((rc = check_launch(what))) return rc;
+  if ((rc = radix_sort_pairs<uint32_t>(l.dkeys, l.didx, numel, 0, 32, l.dkeys_sorted, l.perm, l.sort_ws,
+                                       l.sort_ws_bytes, s, what)))
+    return rc;
+  {
+    KernelTimer timer("isect_gather_counts", s);
+    gather_counts_kernel<<<grid_for(numel, 256), 256, 0, s>>>(tiles_per_gauss, l.perm, numel, l.offs);
+  }
+  if ((rc = check_launch(what))) return rc;
+  if ((rc = scan_exclusive_i32(l.offs, l.offs, numel, nullptr, l.scan_ws, s))) return rc;
+  {
+    KernelTimer timer("isect_encode", s);
+    const int64_t nb = (numel + kEncodeG - 1) / kEncodeG;
+    encode_presorted_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
+        means2d, radii, l.perm, l.offs, numel, numel / I, tile_size, tile_width, tile_height, tile_bits, n_isects,
+        l.tkeys, l.tvals);
+  }
+  if ((rc = check_launch(what))) return rc;
+  if ((rc = radix_sort_pairs<uint32_t>(l.tkeys, l.tvals, n_isects, 0, image_bits + tile_bits, l.tkeys_sorted,
+                                       flatten_ids, l.sort_ws, l.sort_ws_bytes, s, what)))
+    return rc;
+  {
+    KernelTimer timer("isect_assemble_ids", s);
+    assemble_ids_kernel<<<grid_for(n_isects, 256), 256, 0, s>>>(l.tkeys_sorted, flatten_ids, depths, n_isects,
+                                                                isect_ids);
+  }
+  return check_launch(what);
 }

@@ -1,10 +1,12 @@
-// Stable LSD radix sort of 64-bit keys carrying 32-bit values, for gfx950.
+// Stable LSD radix sort of 32- or 64-bit keys carrying 32-bit values, for
+// gfx950.
 //
-// Replaces mx::argsort + mx::take (gsplat_core/gsplat_intersect.cpp:266-286)
-// with a stable sort: equal keys keep their input (encode) order, which for
-// the intersection keys is ascending flatten_id.
+// The standalone entry point replaces mx::argsort + mx::take
+// (gsplat_core/gsplat_intersect.cpp:266-286) with a stable sort: equal keys
+// keep their input (encode) order, which for the intersection keys is
+// ascending flatten_id.
 //
-// Only the low key_bits bits are sorted, 8 bits per pass. Each pass is
+// Only the requested key bits are sorted, 8 bits per pass. Each pass is
 // reduce-then-scan with no inter-block waiting:
 //   1. histogram: each block counts the digits of its kTile keys -> block_hist
 //      stored digit-major ([digit][block]);
@@ -14,6 +16,7 @@
 //      reorders the tile by digit in LDS, then writes each digit run to its
 //      global start, so stores of one run are contiguous.
 // The final pass always lands in keys_out/vals_out; inputs are not modified.
+#include "radix_sort.hpp"
 #include "scan.hpp"
 
 namespace gsplat_hip {
@@ -25,11 +28,13 @@ constexpr int kTile = kSortBlock * kSortItems;  // keys per block
 constexpr int kRadix = 256;
 constexpr int kWaves = kSortBlock / kWave;
 
-__device__ __forceinline__ uint32_t digit_of(uint64_t key, int shift) {
+template <typename K>
+__device__ __forceinline__ uint32_t digit_of(K key, int shift) {
   return static_cast<uint32_t>(key >> shift) & (kRadix - 1);
 }
 
-__global__ void __launch_bounds__(kSortBlock) hist_kernel(const uint64_t* __restrict__ keys, int64_t n, int shift,
+template <typename K>
+__global__ void __launch_bounds__(kSortBlock) hist_kernel(const K* __restrict__ keys, int64_t n, int shift,
                                                           int64_t num_blocks, int32_t* __restrict__ block_hist) {
   __shared__ int32_t h[kRadix];
   h[threadIdx.x] = 0;
@@ -44,13 +49,14 @@ __global__ void __launch_bounds__(kSortBlock) hist_kernel(const uint64_t* __rest
   block_hist[static_cast<int64_t>(threadIdx.x) * num_blocks + blockIdx.x] = h[threadIdx.x];
 }
 
-__global__ void __launch_bounds__(kSortBlock) scatter_kernel(const uint64_t* __restrict__ keys_in,
+template <typename K>
+__global__ void __launch_bounds__(kSortBlock) scatter_kernel(const K* __restrict__ keys_in,
                                                              const int32_t* __restrict__ vals_in, int64_t n, int shift,
                                                              int64_t num_blocks,
                                                              const int32_t* __restrict__ digit_block_start,
-                                                             uint64_t* __restrict__ keys_out,
+                                                             K* __restrict__ keys_out,
                                                              int32_t* __restrict__ vals_out) {
-  __shared__ uint64_t s_keys[kTile];
+  __shared__ K s_keys[kTile];
   __shared__ int32_t s_vals[kTile];
   // per-wave digit counts -> per-wave digit bases; double-buffered by round
   // parity so clearing round r+1's buffer cannot race round r's readers
@@ -64,7 +70,7 @@ __global__ void __launch_bounds__(kSortBlock) scatter_kernel(const uint64_t* __r
   const int64_t base = static_cast<int64_t>(blockIdx.x) * kTile;
   const int cnt = static_cast<int>(min<int64_t>(kTile, n - base));
 
-  uint64_t k[kSortItems];
+  K k[kSortItems];
   int32_t v[kSortItems];
   int32_t rank[kSortItems];
 #pragma unroll
@@ -141,7 +147,7 @@ __global__ void __launch_bounds__(kSortBlock) scatter_kernel(const uint64_t* __r
   }
   __syncthreads();
   for (int j = t; j < cnt; j += kSortBlock) {
-    const uint64_t key = s_keys[j];
+    const K key = s_keys[j];
     const uint32_t d = digit_of(key, shift);
     const int64_t dst = static_cast<int64_t>(s_global[d]) + (j - s_tile_start[d]);
     keys_out[dst] = key;
@@ -149,8 +155,9 @@ __global__ void __launch_bounds__(kSortBlock) scatter_kernel(const uint64_t* __r
   }
 }
 
-__global__ void copy_kernel(const uint64_t* __restrict__ k_in, const int32_t* __restrict__ v_in, int64_t n,
-                            uint64_t* __restrict__ k_out, int32_t* __restrict__ v_out) {
+template <typename K>
+__global__ void copy_kernel(const K* __restrict__ k_in, const int32_t* __restrict__ v_in, int64_t n,
+                            K* __restrict__ k_out, int32_t* __restrict__ v_out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < n) {
     k_out[i] = k_in[i];
@@ -158,8 +165,9 @@ __global__ void copy_kernel(const uint64_t* __restrict__ k_in, const int32_t* __
   }
 }
 
+template <typename K>
 struct SortWorkspace {
-  uint64_t* keys_alt;
+  K* keys_alt;
   int32_t* vals_alt;
   int32_t* hist;
   void* scan_ws;
@@ -167,15 +175,16 @@ struct SortWorkspace {
 
 inline size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
-size_t layout(int64_t n, SortWorkspace* ws, void* base) {
+template <typename K>
+size_t layout(int64_t n, SortWorkspace<K>* ws, void* base) {
   const int64_t nb = (n + kTile - 1) / kTile;
-  const size_t keys_b = align_up(static_cast<size_t>(n) * sizeof(uint64_t));
+  const size_t keys_b = align_up(static_cast<size_t>(n) * sizeof(K));
   const size_t vals_b = align_up(static_cast<size_t>(n) * sizeof(int32_t));
   const size_t hist_b = align_up(static_cast<size_t>(nb) * kRadix * sizeof(int32_t));
   const size_t scan_b = align_up(scan_workspace_bytes(nb * kRadix));
   if (ws && base) {
     char* p = static_cast<char*>(base);
-    ws->keys_alt = reinterpret_cast<uint64_t*>(p);
+    ws->keys_alt = reinterpret_cast<K*>(p);
     ws->vals_alt = reinterpret_cast<int32_t*>(p + keys_b);
     ws->hist = reinterpret_cast<int32_t*>(p + keys_b + vals_b);
     ws->scan_ws = p + keys_b + vals_b + hist_b;
@@ -184,60 +193,84 @@ size_t layout(int64_t n, SortWorkspace* ws, void* base) {
 }
 
 }  // namespace
+
+template <typename K>
+size_t radix_sort_workspace_bytes(int64_t n) {
+  return n <= 0 ? 0 : layout<K>(n, nullptr, nullptr);
+}
+
+template <typename K>
+int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bit_lo, int bit_hi, K* keys_out,
+                     int32_t* vals_out, void* workspace, size_t workspace_bytes, hipStream_t s, const char* what) {
+  const std::string w(what);
+  if (n < 0 || bit_lo < 0 || bit_hi > static_cast<int>(8 * sizeof(K)) || bit_lo > bit_hi)
+    return invalid(w + ": invalid sort arguments.");
+  if (n == 0) return GSPLAT_OK;
+  if (!keys_in || !vals_in || !keys_out || !vals_out) return invalid(w + ": null pointer.");
+  if (n > (static_cast<int64_t>(1) << 31) - 1) return invalid(w + ": more than 2^31-1 keys.");
+  const int passes = (bit_hi - bit_lo + 7) / 8;
+  if (passes == 0) {
+    {
+      KernelTimer timer("sort_copy", s);
+      copy_kernel<K><<<grid_for(n, 256), 256, 0, s>>>(keys_in, vals_in, n, keys_out, vals_out);
+    }
+    return check_launch(what);
+  }
+  SortWorkspace<K> ws;
+  if (!workspace || workspace_bytes < layout<K>(n, &ws, workspace)) {
+    set_error(w + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  const int64_t nb = (n + kTile - 1) / kTile;
+  const K* src_k = keys_in;
+  const int32_t* src_v = vals_in;
+  for (int p = 0; p < passes; ++p) {
+    // the last pass writes keys_out: alternate so that parity works out
+    const bool to_out = ((passes - 1 - p) % 2) == 0;
+    K* dst_k = to_out ? keys_out : ws.keys_alt;
+    int32_t* dst_v = to_out ? vals_out : ws.vals_alt;
+    const int shift = bit_lo + 8 * p;
+    {
+      KernelTimer timer("sort_histogram", s);
+      hist_kernel<K><<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, n, shift, nb, ws.hist);
+    }
+    int rc = check_launch(what);
+    if (rc) return rc;
+    rc = scan_exclusive_i32(ws.hist, ws.hist, nb * kRadix, nullptr, ws.scan_ws, s);
+    if (rc) return rc;
+    {
+      KernelTimer timer("sort_scatter", s);
+      scatter_kernel<K><<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, src_v, n, shift, nb, ws.hist, dst_k,
+                                                                         dst_v);
+    }
+    rc = check_launch(what);
+    if (rc) return rc;
+    src_k = dst_k;
+    src_v = dst_v;
+  }
+  return GSPLAT_OK;
+}
+
+template size_t radix_sort_workspace_bytes<uint32_t>(int64_t);
+template size_t radix_sort_workspace_bytes<uint64_t>(int64_t);
+template int radix_sort_pairs<uint32_t>(const uint32_t*, const int32_t*, int64_t, int, int, uint32_t*, int32_t*,
+                                        void*, size_t, hipStream_t, const char*);
+template int radix_sort_pairs<uint64_t>(const uint64_t*, const int32_t*, int64_t, int, int, uint64_t*, int32_t*,
+                                        void*, size_t, hipStream_t, const char*);
+
 }  // namespace gsplat_hip
 
 using namespace gsplat_hip;
 
-extern "C" size_t gsplat_hip_isect_sort_workspace_size(int64_t n) { return n <= 0 ? 0 : layout(n, nullptr, nullptr); }
+extern "C" size_t gsplat_hip_isect_sort_workspace_size(int64_t n) { return radix_sort_workspace_bytes<uint64_t>(n); }
 
 extern "C" int gsplat_hip_isect_sort(const int64_t* keys_in, const int32_t* vals_in, int64_t n, int32_t key_bits,
                                      int64_t* keys_out, int32_t* vals_out, void* workspace, size_t workspace_bytes,
                                      void* stream) {
   if (n < 0 || key_bits < 0 || key_bits > 64) return invalid("intersect_tile_sort: invalid arguments.");
   if (n == 0) return GSPLAT_OK;
-  if (!keys_in || !vals_in || !keys_out || !vals_out) return invalid("intersect_tile_sort: null pointer.");
-  if (n > (static_cast<int64_t>(1) << 31) - 1) return invalid("intersect_tile_sort: more than 2^31-1 keys.");
-  hipStream_t s = as_stream(stream);
-  const uint64_t* kin = reinterpret_cast<const uint64_t*>(keys_in);
-  uint64_t* kout = reinterpret_cast<uint64_t*>(keys_out);
-  const int passes = (key_bits + 7) / 8;
-  if (passes == 0) {
-    {
-      KernelTimer timer("sort_copy", s);
-      copy_kernel<<<grid_for(n, 256), 256, 0, s>>>(kin, vals_in, n, kout, vals_out);
-    }
-    return check_launch("intersect_tile_sort (copy)");
-  }
-  SortWorkspace ws;
-  if (!workspace || workspace_bytes < layout(n, &ws, workspace)) {
-    set_error("intersect_tile_sort: workspace too small.");
-    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
-  }
-  const int64_t nb = (n + kTile - 1) / kTile;
-  const uint64_t* src_k = kin;
-  const int32_t* src_v = vals_in;
-  for (int p = 0; p < passes; ++p) {
-    // the last pass writes keys_out: alternate so that parity works out
-    const bool to_out = ((passes - 1 - p) % 2) == 0;
-    uint64_t* dst_k = to_out ? kout : ws.keys_alt;
-    int32_t* dst_v = to_out ? vals_out : ws.vals_alt;
-    const int shift = 8 * p;
-    {
-      KernelTimer timer("sort_histogram", s);
-      hist_kernel<<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, n, shift, nb, ws.hist);
-    }
-    int rc = check_launch("intersect_tile_sort (histogram)");
-    if (rc) return rc;
-    rc = scan_exclusive_i32(ws.hist, ws.hist, nb * kRadix, nullptr, ws.scan_ws, s);
-    if (rc) return rc;
-    {
-      KernelTimer timer("sort_scatter", s);
-      scatter_kernel<<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, src_v, n, shift, nb, ws.hist, dst_k, dst_v);
-    }
-    rc = check_launch("intersect_tile_sort (scatter)");
-    if (rc) return rc;
-    src_k = dst_k;
-    src_v = dst_v;
-  }
-  return GSPLAT_OK;
+  if (!keys_out) return invalid("intersect_tile_sort: null pointer.");
+  return radix_sort_pairs<uint64_t>(reinterpret_cast<const uint64_t*>(keys_in), vals_in, n, 0, key_bits,
+                                    reinterpret_cast<uint64_t*>(keys_out), vals_out, workspace, workspace_bytes,
+                                    as_stream(stream), "intersect_tile_sort");
 }

@@ -1,0 +1,23 @@
+// Stable LSD radix sort of 32- or 64-bit unsigned keys carrying int32 values
+// (device-wide, for gfx950). Shared by the standalone intersection sort and
+// the depth-presorted intersection pipeline.
+#pragma once
+
+#include "common.hpp"
+
+namespace gsplat_hip {
+
+// Workspace bytes for sorting n pairs with K-sized keys.
+template <typename K>
+size_t radix_sort_workspace_bytes(int64_t n);
+
+// Sorts bits [bit_lo, bit_hi) of the keys, 8 bits per pass (stable: equal
+// digits keep their input order). Key bits at and above bit_hi must be zero
+// or equal for all keys, bits below bit_lo are ignored. The result always
+// lands in keys_out / vals_out; the inputs are not modified.
+template <typename K>
+int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bit_lo, int bit_hi, K* keys_out,
+                     int32_t* vals_out, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                     const char* what);
+
+}  // namespace gsplat_hip

@@ -177,6 +177,21 @@ int gsplat_hip_isect_sort(const int64_t* keys_in, const int32_t* vals_in, int64_
                           int32_t key_bits, int64_t* keys_out, int32_t* vals_out,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Sorted intersections in one call: replaces the encode + sort of
+ * GSPlatIntersectTile (gsplat_intersect.cpp:487-538 then :266-286) and
+ * returns exactly what gsplat_hip_isect_encode followed by a stable
+ * gsplat_hip_isect_sort returns -- isect_ids sorted by the 64-bit key, ties
+ * in ascending flatten_id -- without sorting 64-bit keys: pairs are first
+ * sorted by depth bits, encoded in that order with 32-bit (image, tile) keys,
+ * and stably sorted by those. tiles_per_gauss [numel] from
+ * gsplat_hip_isect_count_scan, n_isects = its total. */
+size_t gsplat_hip_isect_tile_sorted_workspace_size(int64_t numel, int64_t n_isects);
+int gsplat_hip_isect_tile_sorted(const float* means2d, const int32_t* radii, const float* depths,
+                                 const int32_t* tiles_per_gauss, int64_t I, int64_t numel,
+                                 int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                 int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
+                                 void* workspace, size_t workspace_bytes, void* stream);
+
 /* Replaces GSPlatIntersectOffset::eval_gpu (gsplat_intersect.cpp:643-681):
  * offsets [I, tile_height, tile_width] = lower_bound of (image << tile_bits |
  * tile) over the sorted isect_ids >> 32. */

@@ -46,22 +46,32 @@ def test_known_answers():
     assert host(srt["flatten_ids"]).tolist() == [1, 1, 1, 1, 0, 0, 0, 0]
 
 
-def random_projected(rng, I, N, W, H, ties):
+def random_projected(rng, I, N, W, H, ties, signed=False):
     means2d = np.stack([rng.uniform(-30, W + 30, (I, N)), rng.uniform(-30, H + 30, (I, N))], -1).astype(np.float32)
     radii = rng.integers(0, 60, size=(I, N, 2)).astype(np.int32)
     radii[rng.random((I, N)) < 0.2] = 0
     depths = rng.uniform(0.1, 50, (I, N)).astype(np.float32)
     if ties:
         depths = np.round(depths * 2).astype(np.float32) / 2
+    if signed:
+        # negative, -0.0 and +0.0 depths: the key holds the raw float bits, so
+        # negative depths sort after every positive one
+        pick = rng.random((I, N))
+        depths[pick < 0.1] *= -1
+        depths[(pick >= 0.1) & (pick < 0.15)] = -0.0
+        depths[(pick >= 0.15) & (pick < 0.2)] = 0.0
     return means2d, radii, depths
 
 
-@pytest.mark.parametrize("I,N,W,H,ts,ties", [(1, 20000, 640, 480, 16, False), (3, 7000, 300, 200, 16, True),
-                                             (2, 5000, 130, 70, 8, True), (1, 3000, 1297, 840, 16, True)])
-def test_random_bit_exact(oracle, I, N, W, H, ts, ties):
+@pytest.mark.parametrize("I,N,W,H,ts,ties,signed", [(1, 20000, 640, 480, 16, False, False),
+                                                    (3, 7000, 300, 200, 16, True, False),
+                                                    (2, 5000, 130, 70, 8, True, False),
+                                                    (1, 3000, 1297, 840, 16, True, False),
+                                                    (2, 4000, 200, 150, 16, True, True)])
+def test_random_bit_exact(oracle, I, N, W, H, ts, ties, signed):
     g = gsplat()
     rng = np.random.default_rng(I * 100 + N)
-    m, r, d = random_projected(rng, I, N, W, H, ties)
+    m, r, d = random_projected(rng, I, N, W, H, ties, signed)
     tw, th = (W + ts - 1) // ts, (H + ts - 1) // ts
     got = g.intersect_tile_forward({"means2d": dev(m), "radii": dev(r), "depths": dev(d)}, I, ts, tw, th)
     exp = oracle.isect_tile(m, r, d, I, ts, tw, th, sort=True)
