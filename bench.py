@@ -48,7 +48,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", default="sh3_1m", choices=["sh3_1m", "image_fit", "random_forward"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-band-rows", type=int, default=6, help="tile rows of the CPU rasterize sample")
+    ap.add_argument("--cpu-band-rows", type=int, default=0,
+                    help="tile rows of the CPU rasterize sample (0: the whole image)")
+    ap.add_argument("--cpu-repeats", type=int, default=3, help="CPU baseline runs (median per stage)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="first run a device copy of this many MiB (counter calibration for rocprofv3 --pmc)")
     return ap.parse_args()
@@ -218,19 +220,21 @@ def main():
         if kind == "flops":
             achieved = per_launch / (avg_ms * 1e-3) / 1e12
             roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
-                        "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "traffic": None,
+                        "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
+                        "traffic": measured_traffic(args.workload, dom),
                         "kernel": dom, "avg_ms": round(avg_ms, 4),
                         "note": "compute roofline: FP32 VALU (no MFMA on this path), peak = MI355X FP32"}
         else:
             achieved = per_launch / (avg_ms * 1e-3) / 1e9
             roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                        "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom,
+                        "frac": round(achieved / HBM_PEAK_GBS, 4),
+                        "traffic": measured_traffic(args.workload, dom), "kernel": dom,
                         "avg_ms": round(avg_ms, 4)}
     log(f"[bench] N={N} M={M} E_fwd(no termination)={e_fwd_max} E_bwd={e_bwd} dominant={dom} {avg_ms:.4f} ms")
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(scene, args.cpu_band_rows, mpix)
+        cpu = cpu_baseline(scene, args.cpu_band_rows, args.cpu_repeats, mpix)
 
     line = {
         "metric": "fwd+bwd ms/frame & Mpix/s, 1M Gaussians SH3 1297x840; % of HBM/VALU roofline",
@@ -255,98 +259,119 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(scene, band_rows, mpix):
-    """The oracle (single-threaded C++, this host) over a bounded sample of the
-    same frame: every per-Gaussian and per-intersection stage on the full
-    scene; rasterize forward+backward on a band of `band_rows` tile rows
-    through the image centre, scaled to the full frame by its share of
-    intersections. Returns ms/frame and Mpix/s."""
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE runs, each scaled by the copy-kernel
+    calibration factor), or None when none was recorded for this workload."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = rec.get("kernels", {}).get(kernel)
+    if rec.get("workload") != workload or not k:
+        return None
+    cal = rec["calibration"]
+    return int((k["fetch_kib"] * cal["FETCH_SIZE"] + k["write_kib"] * cal["WRITE_SIZE"]) * 1024)
+
+
+def cpu_baseline(scene, band_rows, repeats, mpix):
+    """The oracle (single-threaded C++, this host) on the same frame: every
+    per-Gaussian and per-intersection stage on the full scene, and rasterize
+    forward+backward on the whole image (band_rows <= 0) or on a band of tile
+    rows through the image centre scaled to the full frame by its share of
+    intersections. Each stage is the median of `repeats` runs. Returns
+    ms/frame and Mpix/s."""
     import numpy as np
 
     sys.path.insert(0, ROOT)
     from oracle import oracle as O
 
     O.build()
-    t = {}
     clock = time.perf_counter
     W, H, ts = scene.width, scene.height, scene.tile_size
     tw, th = (W + ts - 1) // ts, (H + ts - 1) // ts
-    quats = scene.quats / np.maximum(np.linalg.norm(scene.quats, axis=-1, keepdims=True), 1e-8)
-    scales = np.exp(scene.log_scales)
+    quats = (scene.quats / np.maximum(np.linalg.norm(scene.quats, axis=-1, keepdims=True), 1e-8)).astype(np.float32)
+    scales = np.exp(scene.log_scales).astype(np.float32)
     opac = (1 / (1 + np.exp(-scene.opacity_logits))).astype(np.float32)
     sh = scene.sh_degree >= 0
-
-    c = clock()
-    proj = O.projection_forward(scene.means, scene.viewmats, scene.Ks, W, H, quats=quats.astype(np.float32),
-                                scales=scales.astype(np.float32), far_plane=scene.far_plane,
-                                opacities=opac if scene.opacities_in_projection else None)
-    t["projection_fwd"] = clock() - c
-    c = clock()
-    isect = O.isect_tile(proj["means2d"], proj["radii"], proj["depths"], 1, ts, tw, th)
-    offs = O.isect_offset(isect["isect_ids"], 1, tw, th)
-    t["isect+sort+offsets"] = clock() - c
-    M = isect["isect_ids"].size
-    if sh:
-        K = (scene.sh_degree + 1) ** 2
-        campos = -scene.viewmats[0, 0, :3, :3].T @ scene.viewmats[0, 0, :3, 3]
-        dirs = scene.means[0] - campos
-        dirs = (dirs / np.maximum(np.linalg.norm(dirs, axis=-1, keepdims=True), 1e-8)).astype(np.float32)
-        coeffs = np.concatenate([scene.features_dc[0][:, None], scene.features_rest[0][:, :K - 1]], 1)
-        c = clock()
-        colors = O.sh_forward(scene.sh_degree, dirs, coeffs)
-        t["sh_fwd"] = clock() - c
-        colors = np.clip(colors + 0.5, 0, 1)[None, None]
-    else:
-        colors = scene.colors[:, None]
-    # rasterize band: tile rows [r0, r0 + band_rows)
-    r0 = max(0, th // 2 - band_rows // 2)
-    r1 = min(th, r0 + band_rows)
-    o = offs[0].ravel()
-    b_start = int(o[r0 * tw])
-    b_end = int(o[r1 * tw]) if r1 < th else M
-    band_offs = (offs[:, r0:r1] - b_start).astype(np.int32)
-    band_ids = isect["flatten_ids"][b_start:b_end]
-    m2 = proj["means2d"].copy()
-    m2[..., 1] -= r0 * ts
-    bh = min(H, r1 * ts) - r0 * ts
     bg = np.array([scene.background], np.float32)
-    c = clock()
-    fwd = O.raster_forward(m2, proj["conics"], colors, opac[:, None], band_offs, band_ids, W, bh, ts, backgrounds=bg)
-    t_rf = clock() - c
-    if scene.target is not None:
-        tgt = scene.target[:, r0 * ts:r0 * ts + bh]
-        v_rc = (np.sign(fwd["render_colors"] - tgt) / (H * W * 3)).astype(np.float32)
-        c = clock()
-        bwd = O.raster_backward(m2, proj["conics"], colors, opac[:, None], band_offs, band_ids, W, bh, ts,
-                                fwd["render_alphas"], fwd["last_ids"], v_rc, np.zeros_like(fwd["render_alphas"]),
-                                backgrounds=bg)
-        t_rb = clock() - c
-        share = M / max(1, b_end - b_start)
-        t["raster_fwd (scaled)"] = t_rf * share
-        t["raster_bwd (scaled)"] = t_rb * share
-        v_colors = bwd["v_colors"][0, 0]
-        if sh:
-            c = clock()
-            O.sh_backward(scene.sh_degree, dirs, coeffs, v_colors)
-            t["sh_bwd"] = clock() - c
-        c = clock()
-        O.projection_backward(scene.means, scene.viewmats, scene.Ks, W, H, proj["radii"], proj["conics"],
-                              bwd["v_means2d"], np.zeros_like(proj["depths"]), bwd["v_conics"],
-                              quats=quats.astype(np.float32), scales=scales.astype(np.float32))
-        t["projection_bwd"] = clock() - c
+    if band_rows <= 0 or band_rows >= th:
+        r0, r1 = 0, th
     else:
-        t["raster_fwd (scaled)"] = t_rf * M / max(1, b_end - b_start)
+        r0 = max(0, th // 2 - band_rows // 2)
+        r1 = min(th, r0 + band_rows)
+    runs = []
+    for _ in range(max(1, repeats)):
+        t = {}
+        c = clock()
+        proj = O.projection_forward(scene.means, scene.viewmats, scene.Ks, W, H, quats=quats, scales=scales,
+                                    far_plane=scene.far_plane,
+                                    opacities=opac if scene.opacities_in_projection else None)
+        t["projection_fwd"] = clock() - c
+        c = clock()
+        isect = O.isect_tile(proj["means2d"], proj["radii"], proj["depths"], 1, ts, tw, th)
+        offs = O.isect_offset(isect["isect_ids"], 1, tw, th)
+        t["isect+sort+offsets"] = clock() - c
+        M = isect["isect_ids"].size
+        if sh:
+            K = (scene.sh_degree + 1) ** 2
+            campos = -scene.viewmats[0, 0, :3, :3].T @ scene.viewmats[0, 0, :3, 3]
+            dirs = scene.means[0] - campos
+            dirs = (dirs / np.maximum(np.linalg.norm(dirs, axis=-1, keepdims=True), 1e-8)).astype(np.float32)
+            coeffs = np.concatenate([scene.features_dc[0][:, None], scene.features_rest[0][:, :K - 1]], 1)
+            c = clock()
+            colors = O.sh_forward(scene.sh_degree, dirs, coeffs)
+            t["sh_fwd"] = clock() - c
+            colors = np.clip(colors + 0.5, 0, 1)[None, None]
+        else:
+            colors = scene.colors[:, None]
+        o = offs[0].ravel()
+        b_start = int(o[r0 * tw])
+        b_end = int(o[r1 * tw]) if r1 < th else M
+        band_offs = (offs[:, r0:r1] - b_start).astype(np.int32)
+        band_ids = isect["flatten_ids"][b_start:b_end]
+        m2 = proj["means2d"].copy()
+        m2[..., 1] -= r0 * ts
+        bh = min(H, r1 * ts) - r0 * ts
         share = M / max(1, b_end - b_start)
-    total_s = sum(t.values())
-    measured = total_s - t.get("raster_fwd (scaled)", 0) - t.get("raster_bwd (scaled)", 0) + \
-        (t.get("raster_fwd (scaled)", 0) + t.get("raster_bwd (scaled)", 0)) / share
-    log("[bench] cpu baseline stages (s): " + ", ".join(f"{k}={v:.3f}" for k, v in t.items()))
+        c = clock()
+        fwd = O.raster_forward(m2, proj["conics"], colors, opac[:, None], band_offs, band_ids, W, bh, ts,
+                               backgrounds=bg)
+        t["raster_fwd"] = (clock() - c) * share
+        if scene.target is not None:
+            tgt = scene.target[:, r0 * ts:r0 * ts + bh]
+            v_rc = (np.sign(fwd["render_colors"] - tgt) / (H * W * 3)).astype(np.float32)
+            c = clock()
+            bwd = O.raster_backward(m2, proj["conics"], colors, opac[:, None], band_offs, band_ids, W, bh, ts,
+                                    fwd["render_alphas"], fwd["last_ids"], v_rc,
+                                    np.zeros_like(fwd["render_alphas"]), backgrounds=bg)
+            t["raster_bwd"] = (clock() - c) * share
+            if sh:
+                c = clock()
+                O.sh_backward(scene.sh_degree, dirs, coeffs, bwd["v_colors"][0, 0])
+                t["sh_bwd"] = clock() - c
+            c = clock()
+            O.projection_backward(scene.means, scene.viewmats, scene.Ks, W, H, proj["radii"], proj["conics"],
+                                  bwd["v_means2d"], np.zeros_like(proj["depths"]), bwd["v_conics"],
+                                  quats=quats, scales=scales)
+            t["projection_bwd"] = clock() - c
+        runs.append(t)
+    med = {k: float(np.median([r[k] for r in runs])) for k in runs[0]}
+    total_s = sum(med.values())
+    log("[bench] cpu baseline stages (s, median of %d): " % len(runs) +
+        ", ".join(f"{k}={v:.3f}" for k, v in med.items()))
+    if r0 == 0 and r1 == th:
+        raster = "rasterize fwd+bwd on the whole image"
+    else:
+        raster = (f"rasterize fwd+bwd on tile rows {r0}-{r1 - 1} ({b_end - b_start} intersections) scaled by the "
+                  f"frame's intersection share x{share:.2f}")
     return {"value": round(mpix / total_s, 4), "unit": "Mpix/s", "cores": 1, "kind": "port",
             "ms_per_frame": round(1000 * total_s, 1),
-            "sample": (f"oracle (plain C++, 1 thread) on this host: projection, SH, intersection, sort, offsets "
-                       f"and their backwards on all {scene.n} Gaussians / {M} intersections; rasterize fwd+bwd on "
-                       f"tile rows {r0}-{r1 - 1} ({b_end - b_start} intersections) scaled by the frame's "
-                       f"intersection share x{share:.2f}; {measured:.1f} s of CPU work measured")}
+            "sample": (f"oracle (plain C++ -O2, 1 thread) on this host: projection, SH, intersection, sort, offsets "
+                       f"and their backwards on all {scene.n} Gaussians / {M} intersections; {raster}; median of "
+                       f"{len(runs)} runs per stage")}
 
 
 if __name__ == "__main__":

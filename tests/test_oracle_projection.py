@@ -156,6 +156,53 @@ def test_textbook_ewa(oracle):
     assert checked > 100
 
 
+def _fisheye_project(p, fx, fy, cx, cy):
+    """Equidistant fisheye: image radius = f * theta, theta = angle to the
+    optical axis (the model of gsplat_projection.metal:170-200)."""
+    x, y, z = p
+    r = np.hypot(x, y)
+    theta = np.arctan2(r, z)
+    return np.array([fx * theta * x / r + cx, fy * theta * y / r + cy])
+
+
+@pytest.mark.parametrize("camera_model", [1, 2])
+def test_textbook_ortho_and_fisheye(oracle, camera_model):
+    """Orthographic (mean2d = f * (x, y) + c, J = diag(f) on x, y) and
+    equidistant fisheye (J by central differences of the projection written
+    above) against the oracle's camera models; conic = (J Sigma_c J^T + eps)^-1."""
+    rng = np.random.default_rng(5 + camera_model)
+    means, quats, scales, viewmats, Ks = _random_scene(rng, 1, 1, 150)
+    out = oracle.projection_forward(means, viewmats, Ks, 320, 240, quats=quats, scales=scales,
+                                    camera_model=camera_model)
+    Rq = Rotation.from_quat(quats[0][:, [1, 2, 3, 0]]).as_matrix()
+    Sig = Rq @ (scales[0][:, :, None] ** 2 * np.swapaxes(Rq, -1, -2))
+    R, t = viewmats[0, 0, :3, :3], viewmats[0, 0, :3, 3]
+    fx, fy, cx, cy = Ks[0, 0, 0, 0], Ks[0, 0, 1, 1], Ks[0, 0, 0, 2], Ks[0, 0, 1, 2]
+    checked = 0
+    for n in range(150):
+        if out["radii"][0, 0, n, 0] == 0:
+            continue
+        p = R @ means[0, n] + t
+        if camera_model == 1:
+            m2 = np.array([fx * p[0] + cx, fy * p[1] + cy])
+            J = np.array([[fx, 0, 0], [0, fy, 0]])
+            tol = 1e-9
+        else:
+            m2 = _fisheye_project(p, fx, fy, cx, cy)
+            h = 1e-6
+            J = np.stack([(_fisheye_project(p + h * e, fx, fy, cx, cy) - _fisheye_project(p - h * e, fx, fy, cx, cy))
+                          / (2 * h) for e in np.eye(3)], axis=1)
+            tol = 1e-5  # the model's 1e-7 regularisers and the difference step
+        S2 = J @ R @ Sig[n] @ R.T @ J.T + 0.3 * np.eye(2)
+        inv = np.linalg.inv(S2)
+        np.testing.assert_allclose(out["means2d"][0, 0, n], m2, rtol=tol)
+        np.testing.assert_allclose(out["conics"][0, 0, n], [inv[0, 0], inv[0, 1], inv[1, 1]], rtol=tol,
+                                   atol=tol * np.abs(inv).max())
+        np.testing.assert_allclose(out["depths"][0, 0, n], p[2], rtol=1e-12)
+        checked += 1
+    assert checked > 50
+
+
 def _proj_loss(oracle, means, quats, scales, covars, viewmats, Ks, cot, fixed_radii, calc_comp):
     kw = dict(covars=covars) if covars is not None else dict(quats=quats, scales=scales)
     out = oracle.projection_forward(means, viewmats, Ks, 320, 240, calc_compensations=calc_comp, **kw)
