@@ -230,6 +230,25 @@ py::dict quat_scale_to_covar_preci_backward(const TensorMap& inputs, const Tenso
   return r;
 }
 
+// Caller-side SH glue fused into the kernels (addition to the reference
+// surface; see gsplat_sh_camera_colors_forward).
+at::Tensor sh_camera_colors_forward(int degrees_to_use, const TensorMap& inputs) {
+  return gsplat_core::gsplat_sh_camera_colors_forward(
+      degrees_to_use, require_key(inputs, "means"), require_key(inputs, "campos"), require_key(inputs, "features_dc"),
+      require_key(inputs, "features_rest"));
+}
+
+py::dict sh_camera_colors_backward(int degrees_to_use, const TensorMap& inputs, const TensorMap& cotangents) {
+  auto out = gsplat_core::gsplat_sh_camera_colors_backward(
+      degrees_to_use, require_key(inputs, "means"), require_key(inputs, "campos"), require_key(inputs, "features_dc"),
+      require_key(inputs, "features_rest"), require_key(cotangents, "v_colors"));
+  py::dict r;
+  r["v_means"] = out[0];
+  r["v_features_dc"] = out[1];
+  r["v_features_rest"] = out[2];
+  return r;
+}
+
 // Template smoke entries of the reference (gsplat_core/dummy.cpp:7-13).
 int dummy_add(int a, int b) { return a + b; }
 
@@ -264,6 +283,9 @@ PYBIND11_MODULE(_gsplat_core, m) {
   m.def("spherical_harmonics_forward", &spherical_harmonics_forward, py::arg("degrees_to_use"), py::arg("inputs"));
   m.def("spherical_harmonics_backward", &spherical_harmonics_backward, py::arg("degrees_to_use"), py::arg("inputs"),
         py::arg("cotangents"), py::arg("compute_v_dirs") = true);
+  m.def("sh_camera_colors_forward", &sh_camera_colors_forward, py::arg("degrees_to_use"), py::arg("inputs"));
+  m.def("sh_camera_colors_backward", &sh_camera_colors_backward, py::arg("degrees_to_use"), py::arg("inputs"),
+        py::arg("cotangents"));
   m.def("quat_scale_to_covar_preci_forward", &quat_scale_to_covar_preci_forward, py::arg("inputs"),
         py::arg("compute_covar") = true, py::arg("compute_preci") = true, py::arg("triu") = true);
   m.def("quat_scale_to_covar_preci_backward", &quat_scale_to_covar_preci_backward, py::arg("inputs"),

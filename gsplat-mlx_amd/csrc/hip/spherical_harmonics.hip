@@ -339,6 +339,252 @@ __global__ void __launch_bounds__(kShBlock) sh_bwd_kernel(const float* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// Camera colours from SH fused with the caller's glue
+// (scanner_points_training_utils.py:1005-1034): for every camera c,
+//   d = means - campos[c],  n = d / max(|d|, 1e-8),
+//   colors[c] = clamp(SH(n; [dc, rest[:A-1]]) + 0.5, 0, 1),
+// without materialising the concatenated and camera-broadcast [C, N, K, 3]
+// coefficients. The SH evaluation is the same code and operation order as
+// sh_fwd_kernel. The backward recomputes the pre-clamp colour, passes the
+// gradient where 0 <= colour + 0.5 <= 1 (torch.clamp's rule), and sums the
+// coefficient and mean gradients over cameras in registers (no atomics).
+
+// Copies `cnt` rows of W floats (global row stride k3 floats, one contiguous
+// span) into LDS rows of stride PW at column offset `col0`.
+template <int W, int PW>
+__device__ __forceinline__ void stage_cols(float* __restrict__ lds, int col0, const float* __restrict__ src, int cnt,
+                                           uint32_t k3, uint32_t k3_magic) {
+  const uint32_t total = static_cast<uint32_t>(cnt) * k3;
+  auto put = [&](uint32_t f, float v) {
+    const uint32_t r = fast_div(f, k3_magic);
+    const uint32_t c = f - r * k3;
+    if (c < static_cast<uint32_t>(W)) lds[r * PW + col0 + c] = v;
+  };
+  if ((reinterpret_cast<uintptr_t>(src) & 15) == 0 && (total & 3) == 0) {
+    const float4* src4 = reinterpret_cast<const float4*>(src);
+    const uint32_t total4 = total >> 2;
+#pragma unroll 4
+    for (uint32_t i = threadIdx.x; i < total4; i += kShBlock) {
+      const float4 v = src4[i];
+      put(4 * i, v.x);
+      put(4 * i + 1, v.y);
+      put(4 * i + 2, v.z);
+      put(4 * i + 3, v.w);
+    }
+  } else {
+#pragma unroll 4
+    for (uint32_t i = threadIdx.x; i < total; i += kShBlock) put(i, src[i]);
+  }
+}
+
+// Colour of coefficient row `co` ([A][3]) at direction d; sh_fwd_kernel's
+// per-channel arithmetic.
+template <int DEG>
+__device__ __forceinline__ void sh_eval(const float d[3], const float* co, float out[3]) {
+  constexpr int A = (DEG + 1) * (DEG + 1);
+  float basis[A];
+  sh_basis<DEG>(d[0], d[1], d[2], basis);
+  const float norm = sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
+#pragma unroll
+  for (int ch = 0; ch < 3; ++ch) {
+    float result = kC0 * co[ch];
+    if (DEG >= 1 && norm != 0.0f) {
+      const float x = d[0] / norm, y = d[1] / norm, z = d[2] / norm;
+      result += kC1 * (-y * co[3 + ch] + z * co[6 + ch] - x * co[9 + ch]);
+#pragma unroll
+      for (int l = 2; l <= DEG; ++l) {
+        float band = basis[l * l] * co[l * l * 3 + ch];
+#pragma unroll
+        for (int b = l * l + 1; b < (l + 1) * (l + 1); ++b) band += basis[b] * co[b * 3 + ch];
+        result += band;
+      }
+    }
+    out[ch] = result;
+  }
+}
+
+// The caller's view direction: n = d / max(|d|, 1e-8) (NaN propagates as in
+// torch.clamp). Returns |d|.
+__device__ __forceinline__ float view_dir(const float* __restrict__ m, const float cp[3], float d[3], float n[3]) {
+  d[0] = m[0] - cp[0];
+  d[1] = m[1] - cp[1];
+  d[2] = m[2] - cp[2];
+  const float norm = sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
+  const float sc = norm < 1.0e-8f ? 1.0e-8f : norm;
+  n[0] = d[0] / sc;
+  n[1] = d[1] / sc;
+  n[2] = d[2] / sc;
+  return norm;
+}
+
+__device__ __forceinline__ float clamp01(float x) { return x < 0.0f ? 0.0f : (x > 1.0f ? 1.0f : x); }
+
+template <int DEG>
+__global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __restrict__ means,
+                                                              const float* __restrict__ campos,
+                                                              const float* __restrict__ dc,
+                                                              const float* __restrict__ rest, int64_t C, int64_t N,
+                                                              int64_t R, uint32_t r3_magic,
+                                                              float* __restrict__ colors) {
+  constexpr int A = (DEG + 1) * (DEG + 1);
+  constexpr int PW = padded(A * 3);
+  __shared__ float sc[kShBlock * PW];
+  const int64_t b = blockIdx.y;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShBlock;
+  const int cnt = static_cast<int>(min<int64_t>(kShBlock, N - e0));
+  const int t = threadIdx.x;
+  if constexpr (A > 1)
+    stage_cols<(A - 1) * 3, PW>(sc, 3, rest + (b * N + e0) * R * 3, cnt, static_cast<uint32_t>(R * 3), r3_magic);
+  if (t < cnt) {
+    const int64_t g = b * N + e0 + t;
+    sc[t * PW] = dc[g * 3];
+    sc[t * PW + 1] = dc[g * 3 + 1];
+    sc[t * PW + 2] = dc[g * 3 + 2];
+  }
+  __syncthreads();
+  if (t >= cnt) return;
+  const int64_t g = b * N + e0 + t;
+  const float* co = sc + t * PW;
+  for (int64_t c = 0; c < C; ++c) {
+    const float cp[3] = {campos[(b * C + c) * 3], campos[(b * C + c) * 3 + 1], campos[(b * C + c) * 3 + 2]};
+    float d[3], n[3], raw[3];
+    view_dir(means + g * 3, cp, d, n);
+    sh_eval<DEG>(n, co, raw);
+    float* out = colors + ((b * C + c) * N + e0 + t) * 3;
+    out[0] = clamp01(raw[0] + 0.5f);
+    out[1] = clamp01(raw[1] + 0.5f);
+    out[2] = clamp01(raw[2] + 0.5f);
+  }
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShBlock) sh_cam_bwd_kernel(const float* __restrict__ means,
+                                                              const float* __restrict__ campos,
+                                                              const float* __restrict__ dc,
+                                                              const float* __restrict__ rest,
+                                                              const float* __restrict__ v_colors, int64_t C, int64_t N,
+                                                              int64_t R, uint32_t r3_magic,
+                                                              float* __restrict__ v_means, float* __restrict__ v_dc,
+                                                              float* __restrict__ v_rest) {
+  constexpr int A = (DEG + 1) * (DEG + 1);
+  constexpr int PW = padded(A * 3);
+  __shared__ float sc[kShBlock * PW];
+  const int64_t b = blockIdx.y;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShBlock;
+  const int cnt = static_cast<int>(min<int64_t>(kShBlock, N - e0));
+  const int t = threadIdx.x;
+  if constexpr (A > 1)
+    stage_cols<(A - 1) * 3, PW>(sc, 3, rest + (b * N + e0) * R * 3, cnt, static_cast<uint32_t>(R * 3), r3_magic);
+  if (t < cnt) {
+    const int64_t g = b * N + e0 + t;
+    sc[t * PW] = dc[g * 3];
+    sc[t * PW + 1] = dc[g * 3 + 1];
+    sc[t * PW + 2] = dc[g * 3 + 2];
+  }
+  __syncthreads();
+  float vco[A * 3];
+#pragma unroll
+  for (int i = 0; i < A * 3; ++i) vco[i] = 0.0f;
+  float vm[3] = {0.0f, 0.0f, 0.0f};
+  if (t < cnt) {
+    const int64_t g = b * N + e0 + t;
+    float* co = sc + t * PW;
+    for (int64_t c = 0; c < C; ++c) {
+      const float cp[3] = {campos[(b * C + c) * 3], campos[(b * C + c) * 3 + 1], campos[(b * C + c) * 3 + 2]};
+      float d[3], n[3], raw[3];
+      const float norm = view_dir(means + g * 3, cp, d, n);
+      sh_eval<DEG>(n, co, raw);
+      const float* vc = v_colors + ((b * C + c) * N + e0 + t) * 3;
+      float gcol[3];
+#pragma unroll
+      for (int ch = 0; ch < 3; ++ch) {
+        const float x = raw[ch] + 0.5f;
+        gcol[ch] = (x >= 0.0f && x <= 1.0f) ? vc[ch] : 0.0f;
+      }
+      float basis[A];
+      sh_basis<DEG>(n[0], n[1], n[2], basis);
+#pragma unroll
+      for (int k = 0; k < A; ++k) {
+        vco[k * 3] += basis[k] * gcol[0];
+        vco[k * 3 + 1] += basis[k] * gcol[1];
+        vco[k * 3 + 2] += basis[k] * gcol[2];
+      }
+      if constexpr (DEG >= 1) {
+        float vn[3];
+        sh_dir_vjp<DEG>(n, co, gcol, vn);
+        // through n = d / max(|d|, 1e-8)
+        if (norm >= 1.0e-8f) {
+          const float dot = vn[0] * n[0] + vn[1] * n[1] + vn[2] * n[2];
+          vm[0] += (vn[0] - n[0] * dot) / norm;
+          vm[1] += (vn[1] - n[1] * dot) / norm;
+          vm[2] += (vn[2] - n[2] * dot) / norm;
+        } else {
+          vm[0] += vn[0] / 1.0e-8f;
+          vm[1] += vn[1] / 1.0e-8f;
+          vm[2] += vn[2] / 1.0e-8f;
+        }
+      }
+    }
+    v_means[g * 3] = vm[0];
+    v_means[g * 3 + 1] = vm[1];
+    v_means[g * 3 + 2] = vm[2];
+    v_dc[g * 3] = vco[0];
+    v_dc[g * 3 + 1] = vco[1];
+    v_dc[g * 3 + 2] = vco[2];
+    // this lane's coefficient row is no longer read: reuse it for the
+    // gradient row
+#pragma unroll
+    for (int i = 3; i < A * 3; ++i) co[i] = vco[i];
+  }
+  if (R == 0) return;  // uniform
+  __syncthreads();
+  // coalesced write of the [cnt, R, 3] slab of v_rest; bases past the active
+  // degree get zero
+  const uint32_t R3 = static_cast<uint32_t>(R * 3);
+  const uint32_t total = static_cast<uint32_t>(cnt) * R3;
+  float* out = v_rest + (b * N + e0) * R * 3;
+  auto value = [&](uint32_t i) {
+    const uint32_t r = fast_div(i, r3_magic);
+    const uint32_t c = i - r * R3;
+    return c < static_cast<uint32_t>((A - 1) * 3) ? sc[r * PW + 3 + c] : 0.0f;
+  };
+  if ((reinterpret_cast<uintptr_t>(out) & 15) == 0 && (total & 3) == 0) {
+    float4* out4 = reinterpret_cast<float4*>(out);
+#pragma unroll 2
+    for (uint32_t i = t; i < (total >> 2); i += kShBlock)
+      out4[i] = make_float4(value(4 * i), value(4 * i + 1), value(4 * i + 2), value(4 * i + 3));
+  } else {
+    for (uint32_t i = t; i < total; i += kShBlock) out[i] = value(i);
+  }
+}
+
+template <int DEG>
+int launch_cam_fwd(const float* means, const float* campos, const float* dc, const float* rest, int64_t B, int64_t C,
+                   int64_t N, int64_t R, float* colors, hipStream_t s) {
+  {
+    KernelTimer timer("sh_camera_fwd", s);
+    const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
+    sh_cam_fwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, campos, dc, rest, C, N, R,
+                                                      magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), colors);
+  }
+  return check_launch("sh_camera_colors_forward");
+}
+
+template <int DEG>
+int launch_cam_bwd(const float* means, const float* campos, const float* dc, const float* rest, const float* v_colors,
+                   int64_t B, int64_t C, int64_t N, int64_t R, float* v_means, float* v_dc, float* v_rest,
+                   hipStream_t s) {
+  {
+    KernelTimer timer("sh_camera_bwd", s);
+    const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
+    sh_cam_bwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, campos, dc, rest, v_colors, C, N, R,
+                                                      magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), v_means,
+                                                      v_dc, v_rest);
+  }
+  return check_launch("sh_camera_colors_backward");
+}
+
 template <int DEG>
 int launch_fwd(const float* dirs, const float* coeffs, const uint8_t* masks, int64_t n, int64_t K, float* colors,
                hipStream_t s) {
@@ -404,5 +650,61 @@ extern "C" int gsplat_hip_spherical_harmonics_bwd(int32_t degree, const float* d
     case 2: return launch_bwd<2>(dirs, coeffs, masks, v_colors, n, K, v_dirs, v_coeffs, s);
     case 3: return launch_bwd<3>(dirs, coeffs, masks, v_colors, n, K, v_dirs, v_coeffs, s);
     default: return launch_bwd<4>(dirs, coeffs, masks, v_colors, n, K, v_dirs, v_coeffs, s);
+  }
+}
+
+static int check_cam_args(int32_t degree, int64_t B, int64_t C, int64_t N, int64_t R, const char* what) {
+  const std::string w(what);
+  if (degree < 0 || degree > 4) return invalid(w + " supports degree 0..4.");
+  if (B < 0 || C < 0 || N < 0 || R < 0) return invalid(w + ": negative size.");
+  if (R < (degree + 1) * (degree + 1) - 1) return invalid(w + ": features_rest has fewer bases than the degree needs.");
+  if (R > 1023) return invalid(w + ": features_rest exceeds 1023 bases.");
+  if (B > 65535) return invalid(w + ": batch exceeds 65535.");
+  return GSPLAT_OK;
+}
+
+extern "C" int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* campos,
+                                               const float* features_dc, const float* features_rest, int64_t B,
+                                               int64_t C, int64_t N, int64_t R, float* colors, void* stream) {
+  const char* what = "sh_camera_colors_forward";
+  int rc = check_cam_args(degree, B, C, N, R, what);
+  if (rc) return rc;
+  if (B == 0 || C == 0 || N == 0) return GSPLAT_OK;
+  if (!means || !campos || !features_dc || (R > 0 && !features_rest) || !colors)
+    return invalid(std::string(what) + ": null pointer.");
+  hipStream_t s = as_stream(stream);
+  switch (degree) {
+    case 0: return launch_cam_fwd<0>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
+    case 1: return launch_cam_fwd<1>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
+    case 2: return launch_cam_fwd<2>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
+    case 3: return launch_cam_fwd<3>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
+    default: return launch_cam_fwd<4>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
+  }
+}
+
+extern "C" int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const float* campos,
+                                               const float* features_dc, const float* features_rest,
+                                               const float* v_colors, int64_t B, int64_t C, int64_t N, int64_t R,
+                                               float* v_means, float* v_features_dc, float* v_features_rest,
+                                               void* stream) {
+  const char* what = "sh_camera_colors_backward";
+  int rc = check_cam_args(degree, B, C, N, R, what);
+  if (rc) return rc;
+  if (B == 0 || N == 0) return GSPLAT_OK;
+  if (!means || !features_dc || (R > 0 && (!features_rest || !v_features_rest)) || !v_means || !v_features_dc ||
+      (C > 0 && (!campos || !v_colors)))
+    return invalid(std::string(what) + ": null pointer.");
+  hipStream_t s = as_stream(stream);
+  switch (degree) {
+    case 0: return launch_cam_bwd<0>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+                                     v_features_dc, v_features_rest, s);
+    case 1: return launch_cam_bwd<1>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+                                     v_features_dc, v_features_rest, s);
+    case 2: return launch_cam_bwd<2>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+                                     v_features_dc, v_features_rest, s);
+    case 3: return launch_cam_bwd<3>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+                                     v_features_dc, v_features_rest, s);
+    default: return launch_cam_bwd<4>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+                                      v_features_dc, v_features_rest, s);
   }
 }

@@ -151,6 +151,35 @@ def spherical_harmonics(degrees_to_use, dirs, coeffs, masks=None):
     return _SphericalHarmonics.apply(degrees_to_use, dirs, coeffs, masks if masks is not None else _empty(dirs))
 
 
+class _ShCameraColors(torch.autograd.Function):
+    """colors [B, C, N, 3] = clamp(SH(normalize(means - campos[c])) + 0.5, 0, 1)
+    with the coefficient concat / broadcast of the reference caller
+    (scanner_points_training_utils.py:1011-1034) fused into the kernels.
+    campos carries no gradient."""
+
+    @staticmethod
+    def forward(ctx, degrees_to_use, means, campos, features_dc, features_rest):
+        inputs = {"means": means, "campos": campos, "features_dc": features_dc, "features_rest": features_rest}
+        colors = _C.sh_camera_colors_forward(degrees_to_use, inputs)
+        ctx.save_for_backward(means, campos, features_dc, features_rest)
+        ctx.degree = degrees_to_use
+        return colors
+
+    @staticmethod
+    def backward(ctx, v_colors):
+        means, campos, features_dc, features_rest = ctx.saved_tensors
+        inputs = {"means": means, "campos": campos, "features_dc": features_dc, "features_rest": features_rest}
+        out = _C.sh_camera_colors_backward(ctx.degree, inputs, {"v_colors": v_colors.contiguous()})
+        return None, out["v_means"], None, out["v_features_dc"], out["v_features_rest"]
+
+
+def sh_camera_colors(degrees_to_use, means, campos, features_dc, features_rest):
+    """Fused camera colours; campos must not require grad."""
+    if campos.requires_grad:
+        raise ValueError("sh_camera_colors: campos gradients are not supported; detach the camera centres.")
+    return _ShCameraColors.apply(degrees_to_use, means, campos, features_dc, features_rest)
+
+
 class _RasterizeToPixels3DGS(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, image_width,

@@ -17,7 +17,7 @@ from __future__ import annotations
 import torch
 
 from . import _gsplat_core as _C
-from .autograd import projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs, spherical_harmonics
+from .autograd import projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs, sh_camera_colors, spherical_harmonics
 
 
 def normalize_quats(quats: torch.Tensor) -> torch.Tensor:
@@ -33,6 +33,17 @@ def camera_center_from_viewmat(viewmats: torch.Tensor) -> torch.Tensor:
 
 
 def sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree):
+    """scanner_points_training_utils.py:1011-1034. The normalisation, the
+    coefficient concat / broadcast and the clip run inside the fused SH
+    kernels when the camera centres need no gradient; otherwise the
+    reference's composition of elementwise ops and the SH operator runs."""
+    if not viewmats.requires_grad:
+        campos = camera_center_from_viewmat(viewmats).contiguous()
+        return sh_camera_colors(sh_degree, means, campos, features_dc, features_rest)
+    return sh_colors_for_camera_unfused(means, features_dc, features_rest, viewmats, sh_degree)
+
+
+def sh_colors_for_camera_unfused(means, features_dc, features_rest, viewmats, sh_degree):
     active = (sh_degree + 1) ** 2
     dirs = means[:, None, :, :] - camera_center_from_viewmat(viewmats)[:, :, None, :]
     dirs = dirs / torch.clamp(torch.sqrt(torch.sum(dirs * dirs, dim=-1, keepdim=True)), min=1.0e-8)
