@@ -23,6 +23,23 @@ __global__ void fill_zero_u8(uint8_t* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0;
 }
 
+struct ZeroSpans {
+  float* ptr[kMaxZeroSpans];
+  int64_t end[kMaxZeroSpans];  // inclusive prefix of counts
+  int n;
+};
+
+__global__ void fill_zero_spans_kernel(ZeroSpans z) {
+  const int64_t total = z.end[z.n - 1];
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
+    int k = 0;
+    while (i >= z.end[k]) ++k;
+    const int64_t start = k == 0 ? 0 : z.end[k - 1];
+    z.ptr[k][i - start] = 0.0f;
+  }
+}
+
 struct TimedLaunch {
   const char* name;
   hipEvent_t start;
@@ -93,6 +110,23 @@ int fill_zero(void* ptr, int64_t bytes, hipStream_t stream) {
   } else {
     fill_zero_u8<<<grid_for(bytes, 256), 256, 0, stream>>>(static_cast<uint8_t*>(ptr), bytes);
   }
+  return check_launch("fill_zero");
+}
+
+int fill_zero_spans(const ZeroSpan* spans, int n_spans, hipStream_t stream) {
+  ZeroSpans z{};
+  int64_t run = 0;
+  for (int i = 0; i < n_spans && i < kMaxZeroSpans; ++i) {
+    if (!spans[i].ptr || spans[i].count <= 0) continue;
+    z.ptr[z.n] = spans[i].ptr;
+    run += spans[i].count;
+    z.end[z.n] = run;
+    ++z.n;
+  }
+  if (z.n == 0) return GSPLAT_OK;
+  KernelTimer timer("fill_zero", stream);
+  const int64_t blocks = std::min<int64_t>((run + 255) / 256, 65536);
+  fill_zero_spans_kernel<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(z);
   return check_launch("fill_zero");
 }
 

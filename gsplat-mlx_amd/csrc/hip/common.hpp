@@ -62,6 +62,15 @@ class KernelTimer {
 // memset node).
 int fill_zero(void* ptr, int64_t bytes, hipStream_t stream);
 
+// Zero-fills up to kMaxZeroSpans float buffers in one launch (null or empty
+// spans are skipped).
+constexpr int kMaxZeroSpans = 8;
+struct ZeroSpan {
+  float* ptr;
+  int64_t count;  // floats
+};
+int fill_zero_spans(const ZeroSpan* spans, int n_spans, hipStream_t stream);
+
 // ---------------------------------------------------------------------------
 // wave64 reductions with DPP row operations. Result valid in lane 63; use
 // wave_sum_uniform() for a wave-uniform (scalar) value.

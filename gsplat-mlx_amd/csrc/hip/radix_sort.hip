@@ -6,8 +6,26 @@
 // keep their input (encode) order, which for the intersection keys is
 // ascending flatten_id.
 //
-// Only the requested key bits are sorted, 8 bits per pass. Each pass is
-// reduce-then-scan with no inter-block waiting:
+// Only the requested key bits are sorted, 8 bits per pass.
+//
+// Main path (fewer than 2^30 keys), one kernel per pass after one histogram
+// kernel ("onesweep"):
+//   0. one read of the keys builds the global digit histogram of every pass;
+//   1. per pass, block b sorts partition b of 4096 keys (workgroups are
+//      dispatched in index order on each XCD, so a waiting block's
+//      predecessors on its own XCD are resident or done, and no block of a
+//      higher index can hold the slot a lower one needs), ranks its keys stably (each wave ranks a contiguous quarter with
+//      ballots and wave-private running digit counts), publishes its digit
+//      counts, and obtains the exclusive prefix over earlier partitions by
+//      decoupled look-back: per digit, walk back over predecessors' published
+//      words (flag | count in one 32-bit word) until one carries an inclusive
+//      prefix. Every partition publishes its counts before it looks back, so
+//      the walk always ends; it is additionally bounded, setting an error
+//      word instead of spinning forever. The tile is then reordered by digit
+//      in LDS and written out in coalesced runs.
+//
+// Fallback (2^30 keys or more, where a count no longer fits beside the
+// flags) is reduce-then-scan with no inter-block waiting:
 //   1. histogram: each block counts the digits of its kTile keys -> block_hist
 //      stored digit-major ([digit][block]);
 //   2. exclusive scan of block_hist -> global start of (digit, block);
@@ -16,6 +34,8 @@
 //      reorders the tile by digit in LDS, then writes each digit run to its
 //      global start, so stores of one run are contiguous.
 // The final pass always lands in keys_out/vals_out; inputs are not modified.
+#include <algorithm>
+
 #include "radix_sort.hpp"
 #include "scan.hpp"
 
@@ -165,31 +185,250 @@ __global__ void copy_kernel(const K* __restrict__ k_in, const int32_t* __restric
   }
 }
 
+// ---------------------------------------------------------------------------
+// Onesweep pass kernels.
+constexpr int kOsItems = 16;
+constexpr int kOsWaveKeys = kWave * kOsItems;     // keys ranked by one wave
+constexpr int kOsTile = kSortBlock * kOsItems;    // keys per partition (4096)
+constexpr uint32_t kFlagAggregate = 1u << 30;     // count of this partition only
+constexpr uint32_t kFlagPrefix = 2u << 30;        // inclusive prefix through this partition
+constexpr uint32_t kCountMask = (1u << 30) - 1u;
+constexpr int kMaxPasses = 8;
+constexpr int kSpinLimit = 1 << 18;
+constexpr int kLookbackWindow = 16;
+
+template <typename K>
+__global__ void __launch_bounds__(kSortBlock) global_hist_kernel(const K* __restrict__ keys, int64_t n, int bit_lo,
+                                                                 int passes, uint32_t* __restrict__ hist) {
+  __shared__ uint32_t h[kMaxPasses][kRadix];
+  const int t = threadIdx.x;
+  for (int p = 0; p < passes; ++p) h[p][t] = 0;
+  __syncthreads();
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSortBlock;
+  for (int64_t i0 = static_cast<int64_t>(blockIdx.x) * kSortBlock; i0 < n; i0 += stride) {
+    const int64_t i = i0 + t;
+    const bool valid = i < n;
+    const K k = valid ? keys[i] : K(0);
+    const uint64_t lanes_below = (t % kWave == 0) ? 0ull : (~0ull >> (kWave - t % kWave));
+    for (int p = 0; p < passes; ++p) {
+      // one LDS add per distinct digit of the wave (lanes with equal digits
+      // found by 8 ballots), so repeated high digits do not serialize
+      const uint32_t d = digit_of(k, bit_lo + 8 * p);
+      uint64_t peers = __ballot(valid);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t m = __ballot(bit);
+        peers &= bit ? m : ~m;
+      }
+      if (valid && (peers & lanes_below) == 0) atomicAdd(&h[p][d], static_cast<uint32_t>(__popcll(peers)));
+    }
+  }
+  __syncthreads();
+  for (int p = 0; p < passes; ++p) {
+    const uint32_t c = h[p][t];
+    if (c) atomicAdd(&hist[p * kRadix + t], c);
+  }
+}
+
+template <typename K>
+__global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restrict__ keys_in,
+                                                              const int32_t* __restrict__ vals_in, int64_t n,
+                                                              int shift, const uint32_t* __restrict__ hist,
+                                                              uint32_t* __restrict__ lookback,
+                                                              int32_t* __restrict__ error_word,
+                                                              K* __restrict__ keys_out, int32_t* __restrict__ vals_out) {
+  __shared__ K s_keys[kOsTile];
+  __shared__ int32_t s_vals[kOsTile];
+  __shared__ uint32_t s_wcnt[kWaves][kRadix];  // per-wave running counts, then per-wave bases
+  __shared__ uint32_t s_tile_start[kRadix];
+  __shared__ uint32_t s_gbase[kRadix];
+  __shared__ uint32_t s_wsum[kWaves];
+  const int t = threadIdx.x;
+  const int lane = t % kWave;
+  const int wave = t / kWave;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
+  __syncthreads();
+  const int64_t part = blockIdx.x;
+  const int64_t base = part * kOsTile;
+  const int cnt = static_cast<int>(min<int64_t>(kOsTile, n - base));
+
+  // load: wave w owns tile keys [w * 1024, (w + 1) * 1024), round r covers
+  // w * 1024 + r * 64 + lane, so (wave, round, lane) is input order
+  K k[kOsItems];
+  int32_t v[kOsItems];
+  uint32_t rank[kOsItems];
+#pragma unroll
+  for (int r = 0; r < kOsItems; ++r) {
+    const int idx = wave * kOsWaveKeys + r * kWave + lane;
+    if (idx < cnt) {
+      k[r] = keys_in[base + idx];
+      v[r] = vals_in[base + idx];
+    } else {
+      k[r] = 0;
+      v[r] = 0;
+    }
+  }
+  const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
+  uint32_t* wc = s_wcnt[wave];
+#pragma unroll
+  for (int r = 0; r < kOsItems; ++r) {
+    const bool valid = wave * kOsWaveKeys + r * kWave + lane < cnt;
+    const uint32_t d = digit_of(k[r], shift);
+    uint64_t peers = __ballot(valid);
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const bool bit = (d >> b) & 1u;
+      const uint64_t m = __ballot(bit);
+      peers &= bit ? m : ~m;
+    }
+    // all lanes read the wave's running count of their digit, then one lane
+    // per digit advances it; a wave's LDS accesses complete in issue order
+    const uint32_t my = static_cast<uint32_t>(__popcll(peers & lanes_below));
+    const uint32_t cur = valid ? wc[d] : 0u;
+    rank[r] = cur + my;
+    if (valid && my == 0) wc[d] = cur + static_cast<uint32_t>(__popcll(peers));
+  }
+  __syncthreads();
+  // thread t owns digit t: per-wave exclusive bases and the tile total
+  uint32_t total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    const uint32_t c = s_wcnt[w][t];
+    s_wcnt[w][t] = total;
+    total += c;
+  }
+  // publish this partition's count, then look back for the exclusive prefix
+  uint32_t* my_word = lookback + part * kRadix + t;
+  if (part == 0) {
+    __hip_atomic_store(my_word, kFlagPrefix | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    __hip_atomic_store(my_word, kFlagAggregate | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  uint32_t prefix = 0;
+  if (part > 0) {
+    // read kLookbackWindow predecessors per step (loads in flight together);
+    // positions before partition 0 read as an empty prefix
+    int64_t p = part - 1;
+    int spins = 0;
+    for (;;) {
+      uint32_t x[kLookbackWindow];
+#pragma unroll
+      for (int i = 0; i < kLookbackWindow; ++i)
+        x[i] = p - i >= 0 ? __hip_atomic_load(lookback + (p - i) * kRadix + t, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT)
+                          : kFlagPrefix;
+      int used = 0;
+      bool done = false;
+#pragma unroll
+      for (int i = 0; i < kLookbackWindow; ++i) {
+        if (done || used < i) continue;  // stop at the first prefix or the first word not yet published
+        const uint32_t flag = x[i] & ~kCountMask;
+        if (flag == 0) continue;
+        prefix += x[i] & kCountMask;
+        used = i + 1;
+        if (flag == kFlagPrefix) done = true;
+      }
+      if (done) break;
+      p -= used;
+      if (used == 0) {
+        if (++spins > kSpinLimit) {
+          atomicExch(error_word, 1);
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+    }
+    __hip_atomic_store(my_word, kFlagPrefix | (prefix + total), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  // global start of digit t = sum of all smaller digits' totals (from the
+  // histogram) + this digit's count in earlier partitions
+  {
+    const uint32_t c = hist[t];
+    const int inc = wave_inclusive_scan(static_cast<int>(c));
+    if (lane == kWave - 1) s_wsum[wave] = static_cast<uint32_t>(inc);
+    // tile-local exclusive start of digit t (scan of totals) shares the sync
+    __syncthreads();
+    uint32_t wb = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      if (w < wave) wb += s_wsum[w];
+    s_gbase[t] = wb + static_cast<uint32_t>(inc) - c + prefix;
+  }
+  __syncthreads();
+  {
+    const int inc = wave_inclusive_scan(static_cast<int>(total));
+    if (lane == kWave - 1) s_wsum[wave] = static_cast<uint32_t>(inc);
+    __syncthreads();
+    uint32_t wb = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      if (w < wave) wb += s_wsum[w];
+    s_tile_start[t] = wb + static_cast<uint32_t>(inc) - total;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < kOsItems; ++r) {
+    if (wave * kOsWaveKeys + r * kWave + lane < cnt) {
+      const uint32_t d = digit_of(k[r], shift);
+      const uint32_t pos = s_tile_start[d] + wc[d] + rank[r];
+      s_keys[pos] = k[r];
+      s_vals[pos] = v[r];
+    }
+  }
+  __syncthreads();
+  for (int j = t; j < cnt; j += kSortBlock) {
+    const K key = s_keys[j];
+    const uint32_t d = digit_of(key, shift);
+    const int64_t dst = static_cast<int64_t>(s_gbase[d]) + (j - static_cast<int64_t>(s_tile_start[d]));
+    keys_out[dst] = key;
+    vals_out[dst] = s_vals[j];
+  }
+}
+
 template <typename K>
 struct SortWorkspace {
   K* keys_alt;
   int32_t* vals_alt;
   int32_t* hist;
   void* scan_ws;
+  // onesweep
+  uint32_t* os_hist;      // [kMaxPasses][256]
+  int32_t* os_error;      // set when a look-back gives up (never expected)
+  uint32_t* os_lookback;  // [passes][n_parts][256]
 };
 
 inline size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+// Keys below this count take the onesweep path (counts fit beside the flags).
+constexpr int64_t kOnesweepMaxKeys = static_cast<int64_t>(1) << 30;
+
 template <typename K>
 size_t layout(int64_t n, SortWorkspace<K>* ws, void* base) {
   const int64_t nb = (n + kTile - 1) / kTile;
+  const int64_t n_parts = (n + kOsTile - 1) / kOsTile;
+  const int max_passes = static_cast<int>(sizeof(K));
   const size_t keys_b = align_up(static_cast<size_t>(n) * sizeof(K));
   const size_t vals_b = align_up(static_cast<size_t>(n) * sizeof(int32_t));
-  const size_t hist_b = align_up(static_cast<size_t>(nb) * kRadix * sizeof(int32_t));
-  const size_t scan_b = align_up(scan_workspace_bytes(nb * kRadix));
+  const bool onesweep = n < kOnesweepMaxKeys;
+  const size_t hist_b = onesweep ? 0 : align_up(static_cast<size_t>(nb) * kRadix * sizeof(int32_t));
+  const size_t scan_b = onesweep ? 0 : align_up(scan_workspace_bytes(nb * kRadix));
+  const size_t oh_b = onesweep ? align_up(kMaxPasses * kRadix * sizeof(uint32_t)) : 0;
+  const size_t ot_b = onesweep ? align_up(sizeof(int32_t)) : 0;
+  const size_t ol_b = onesweep ? align_up(static_cast<size_t>(max_passes) * n_parts * kRadix * sizeof(uint32_t)) : 0;
   if (ws && base) {
     char* p = static_cast<char*>(base);
     ws->keys_alt = reinterpret_cast<K*>(p);
     ws->vals_alt = reinterpret_cast<int32_t*>(p + keys_b);
     ws->hist = reinterpret_cast<int32_t*>(p + keys_b + vals_b);
     ws->scan_ws = p + keys_b + vals_b + hist_b;
+    char* q = p + keys_b + vals_b + hist_b + scan_b;
+    ws->os_hist = reinterpret_cast<uint32_t*>(q);
+    ws->os_error = reinterpret_cast<int32_t*>(q + oh_b);
+    ws->os_lookback = reinterpret_cast<uint32_t*>(q + oh_b + ot_b);
   }
-  return keys_b + vals_b + hist_b + scan_b;
+  return keys_b + vals_b + hist_b + scan_b + oh_b + ot_b + ol_b;
 }
 
 }  // namespace
@@ -220,6 +459,39 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
   if (!workspace || workspace_bytes < layout<K>(n, &ws, workspace)) {
     set_error(w + ": workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  if (n < kOnesweepMaxKeys) {
+    const int64_t n_parts = (n + kOsTile - 1) / kOsTile;
+    // histograms, error word and this sort's look-back words start at zero
+    const int64_t clear = reinterpret_cast<char*>(ws.os_lookback + passes * n_parts * kRadix) -
+                          reinterpret_cast<char*>(ws.os_hist);
+    int rc = fill_zero(ws.os_hist, clear, s);
+    if (rc) return rc;
+    {
+      KernelTimer timer("sort_histogram", s);
+      // few blocks: each adds its histogram into the same 256 * passes
+      // global words, and same-address device atomics serialize
+      const int64_t hb = std::min<int64_t>(n_parts, 128);
+      global_hist_kernel<K><<<static_cast<unsigned>(hb), kSortBlock, 0, s>>>(keys_in, n, bit_lo, passes, ws.os_hist);
+    }
+    if ((rc = check_launch(what))) return rc;
+    const K* src_k = keys_in;
+    const int32_t* src_v = vals_in;
+    for (int p = 0; p < passes; ++p) {
+      const bool to_out = ((passes - 1 - p) % 2) == 0;
+      K* dst_k = to_out ? keys_out : ws.keys_alt;
+      int32_t* dst_v = to_out ? vals_out : ws.vals_alt;
+      {
+        KernelTimer timer("sort_onesweep", s);
+        onesweep_kernel<K><<<static_cast<unsigned>(n_parts), kSortBlock, 0, s>>>(
+            src_k, src_v, n, bit_lo + 8 * p, ws.os_hist + p * kRadix, ws.os_lookback + p * n_parts * kRadix,
+            ws.os_error, dst_k, dst_v);
+      }
+      if ((rc = check_launch(what))) return rc;
+      src_k = dst_k;
+      src_v = dst_v;
+    }
+    return GSPLAT_OK;
   }
   const int64_t nb = (n + kTile - 1) / kTile;
   const K* src_k = keys_in;

@@ -72,6 +72,79 @@ __device__ __forceinline__ int32_t load_gaussian(const RasterArgs& a, int64_t j,
   return g;
 }
 
+// ---------------------------------------------------------------------------
+// Per-wave culling. When a batch record is staged, its loader tests it once
+// against every wave's pixel rectangle and stores a bit mask; each wave
+// collects the set bits of 64 records at a time with one ballot and visits
+// only those records. A bit is cleared only when no pixel of the wave can
+// pass the alpha test: alpha = min(0.99, o exp(-sigma)) >= 1/255 needs
+// sigma <= ln(255 o), and the minimum of sigma over the rectangle of the
+// wave's pixel centres (a positive-definite quadratic: zero if the mean is
+// inside, else the smallest of the four clamped edge minima) exceeds
+// 1.05 ln(255 o) + 1e-4. For conics with det > 1e-4 c0 c2 the float32
+// rounding of that minimum and of the per-pixel sigma, exp and threshold is
+// below 1%, well inside the slack; other conics, non-finite values and NaN
+// opacities are never culled, and opacities <= 0 always are (alpha <= 0).
+// Culled records cannot change a pixel of that wave, so results are
+// unchanged.
+struct PixRect {
+  float x0, x1, y0, y1;
+};
+
+// Bounding rectangle of the pixel centres owned by wave w of a tile whose
+// lanes map to pixels q = lane index within the tile (row-major, ts wide).
+__device__ __forceinline__ PixRect wave_rect(int w, int ts, int tx, int ty) {
+  const int q0 = w * kWave;
+  const int q1 = min(q0 + kWave, ts * ts) - 1;
+  const int r0 = q0 / ts, r1 = q1 / ts;
+  int c0 = 0, c1 = ts - 1;
+  if (r0 == r1) {
+    c0 = q0 % ts;
+    c1 = q1 % ts;
+  }
+  PixRect r;
+  r.x0 = static_cast<float>(tx * ts + c0) + 0.5f;
+  r.x1 = static_cast<float>(tx * ts + c1) + 0.5f;
+  r.y0 = static_cast<float>(ty * ts + r0) + 0.5f;
+  r.y1 = static_cast<float>(ty * ts + r1) + 0.5f;
+  return r;
+}
+
+__device__ __forceinline__ float quad_form(float c0, float c1, float c2, float dx, float dy) {
+  return 0.5f * (c0 * dx * dx + c2 * dy * dy) + c1 * dx * dy;
+}
+
+__device__ __forceinline__ bool may_touch(float2 m, float4 co, const PixRect& r) {
+  const float o = co.w;
+  if (o <= 0.0f) return false;
+  const float t = logf(255.0f * o);
+  const float c0 = co.x, c1 = co.y, c2 = co.z;
+  if (!(t < 1.0e30f) || !(c0 > 0.0f && c2 > 0.0f && c0 < 1.0e30f && c2 < 1.0e30f) ||
+      !(c0 * c2 - c1 * c1 > 1.0e-4f * c0 * c2) || !(fabsf(m.x) < 1.0e30f) || !(fabsf(m.y) < 1.0e30f))
+    return true;
+  if (m.x >= r.x0 && m.x <= r.x1 && m.y >= r.y0 && m.y <= r.y1) return true;
+  float best = __builtin_huge_valf();
+  // vertical edges (dx fixed), then horizontal edges (dy fixed)
+  for (int e = 0; e < 2; ++e) {
+    const float dx = m.x - (e ? r.x1 : r.x0);
+    const float dy = fminf(fmaxf(-c1 * dx / c2, m.y - r.y1), m.y - r.y0);
+    best = fminf(best, quad_form(c0, c1, c2, dx, dy));
+  }
+  for (int e = 0; e < 2; ++e) {
+    const float dy = m.y - (e ? r.y1 : r.y0);
+    const float dx = fminf(fmaxf(-c1 * dy / c0, m.x - r.x1), m.x - r.x0);
+    best = fminf(best, quad_form(c0, c1, c2, dx, dy));
+  }
+  return !(best > 1.05f * t + 1.0e-4f);
+}
+
+__device__ __forceinline__ uint32_t touch_mask(float2 m, float4 co, int n_waves, int ts, int tx, int ty) {
+  uint32_t mask = 0;
+  for (int w = 0; w < n_waves; ++w)
+    if (may_touch(m, co, wave_rect(w, ts, tx, ty))) mask |= 1u << w;
+  return mask;
+}
+
 // CH in 1..4: colors staged in LDS; CH == 0: runtime channel count (<= 64),
 // colors read from global memory.
 template <int CH>
@@ -85,12 +158,16 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
   float4* s_co = reinterpret_cast<float4*>(smem + 2 * BS);  // conic xyz, opacity
   float* s_col = smem + 6 * BS;                            // [BS][LC] (CH > 0)
   int32_t* s_g = reinterpret_cast<int32_t*>(smem + 6 * BS + (CH > 0 ? LC * BS : 0));
+  uint32_t* s_mask = reinterpret_cast<uint32_t*>(s_g + BS);  // per-wave touch bits
 
   const int channels = CH > 0 ? CH : a.channels;
   const int tx = blockIdx.x, ty = blockIdx.y;
   const int64_t image = blockIdx.z;
   const int tile = ty * a.tw + tx;
   const int t = threadIdx.x;
+  const int lane = t % kWave;
+  const int wave = t / kWave;
+  const int n_waves = BS / kWave;
   const int x = tx * a.ts + t % a.ts;
   const int y = ty * a.ts + t / a.ts;
   // blocks are padded to whole wave64s; padding lanes own no pixel
@@ -127,6 +204,7 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
       const int32_t g = load_gaussian(a, j, &xy, &co);
       s_xy[t] = xy;
       s_co[t] = co;
+      s_mask[t] = touch_mask(xy, co, n_waves, a.ts, tx, ty);
       if constexpr (CH > 0) {
 #pragma unroll
         for (int c = 0; c < CH; ++c) s_col[t * CH + c] = a.colors[static_cast<int64_t>(g) * CH + c];
@@ -136,8 +214,14 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
     }
     __syncthreads();
     const int cnt = static_cast<int>(min<int64_t>(BS, end - b0));
-    if (!done) {
-      for (int k = 0; k < cnt; ++k) {
+    for (int c0 = 0; c0 < cnt; c0 += kWave) {
+      // records of this 64-slot chunk that may touch this wave (all lanes vote)
+      const int kl = c0 + lane;
+      uint64_t bits = __ballot(kl < cnt && ((s_mask[kl] >> wave) & 1u));
+      if (done) continue;
+      while (bits) {
+        const int k = c0 + __builtin_ctzll(bits);
+        bits &= bits - 1;
         const float2 m = s_xy[k];
         const float4 co = s_co[k];
         const float dx = m.x - px;
@@ -289,7 +373,8 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
   float2* s_xy = reinterpret_cast<float2*>(smem);            // [BB]
   float4* s_co = reinterpret_cast<float4*>(smem + 2 * BB);   // [BB] conic xyz, opacity
   int32_t* s_g = reinterpret_cast<int32_t*>(smem + 6 * BB);  // [BB]
-  float* s_col = smem + 7 * BB;                              // [BB][LC] (CH > 0)
+  uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + 7 * BB);  // [BB] per-wave touch bits
+  float* s_col = smem + 8 * BB;                              // [BB][LC] (CH > 0)
   float* s_acc = s_col + (CH > 0 ? LC * BB : 0);             // [n_waves][BB][NV]
   __shared__ int s_max_last;
   __shared__ int64_t s_unit;
@@ -376,11 +461,15 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
     float2 r_xy = make_float2(0.0f, 0.0f);
     float4 r_co = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     int32_t r_g = 0;
+    uint32_t r_mask = 0;
     float r_col[LC];
     auto fetch = [&](int64_t hi, int64_t lo) {
       const int64_t j = hi - 1 - t;  // slot t holds entry hi - 1 - t (back to front)
       if (t < BB && j >= lo) {
         r_g = load_gaussian(a, j, &r_xy, &r_co);
+        // the rectangles follow the one-pixel-per-lane mapping; other
+        // mappings keep every record
+        r_mask = P == 1 ? touch_mask(r_xy, r_co, n_waves * n_bands, a.ts, tx, ty) >> (band * n_waves) : ~0u;
         if constexpr (CH > 0) {
 #pragma unroll
           for (int c = 0; c < CH; ++c) r_col[c] = a.colors[static_cast<int64_t>(r_g) * CH + c];
@@ -396,6 +485,7 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
         s_xy[t] = r_xy;
         s_co[t] = r_co;
         s_g[t] = r_g;
+        s_mask[t] = r_mask;
         if constexpr (CH > 0) {
 #pragma unroll
           for (int c = 0; c < CH; ++c) s_col[t * CH + c] = r_col[c];
@@ -408,9 +498,15 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
       if (b0 > start) fetch(b0, max<int64_t>(start, b0 - BB));  // next batch, in flight during this one
       const int cnt = static_cast<int>(b1 - b0);
       const int k_rel0 = static_cast<int>(b1 - 1 - start);  // entry of slot 0, relative to start
-      for (int k = 0; k < cnt; ++k) {
+      for (int c0 = 0; c0 < cnt; c0 += kWave) {
+        // records of this 64-slot chunk that may touch this wave and are not
+        // past its last contributor (all lanes vote)
+        const int kl = c0 + lane;
+        uint64_t bits = __ballot(kl < cnt && k_rel0 - kl <= wave_last && ((s_mask[kl] >> wave) & 1u));
+        while (bits) {
+        const int k = c0 + __builtin_ctzll(bits);
+        bits &= bits - 1;
         const int k_rel = k_rel0 - k;
-        if (k_rel > wave_last) continue;  // wave-uniform
         const float2 m = s_xy[k];
         const float4 co = s_co[k];
         float col[LC];
@@ -487,6 +583,7 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
           float* acc = s_acc + (wave * BB + k) * NV;
 #pragma unroll
           for (int mm = 0; mm < NC; ++mm) acc[red_idx[mm]] = y[mm];
+        }
         }
       }
       __syncthreads();
@@ -609,7 +706,8 @@ int64_t resident_blocks(const void* kernel, int block, size_t smem) {
   return static_cast<int64_t>(per_cu) * cus;
 }
 
-size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (6 + (ch > 0 ? ch : 0) + (ch > 0 ? 0 : 1)) * 4; }
+// records: mean 2, conic+opacity 4, colours (CH > 0), Gaussian id, touch mask
+size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (8 + (ch > 0 ? ch : 0)) * 4; }
 // Backward work split: pixels per lane and waves per block; a tile's pixels
 // are split over n_bands blocks of bwd_block lanes.
 // Backward work split: one pixel per lane and the whole tile in one block
@@ -626,11 +724,12 @@ BwdShape bwd_shape(int ts) {
   const int bs = (ts * ts + kWave - 1) / kWave * kWave;
   return {1, bs, 1, bs <= 128 ? bs : (bs <= 256 ? 128 : 64)};
 }
-// records (7 + colors) per batch slot plus NV accumulators per (wave, slot)
+// records (8 words + colours: mean, conic+opacity, id, touch mask) per batch
+// slot plus NV accumulators per (wave, slot)
 size_t bwd_smem(int ch, int bs, int bb, bool absgrad) {
   const int cc = ch > 0 ? ch : 0;
   const int nv = cc + (absgrad ? 8 : 6);
-  return static_cast<size_t>(bb) * (7 + cc + (bs / kWave) * nv) * 4;
+  return static_cast<size_t>(bb) * (8 + cc + (bs / kWave) * nv) * 4;
 }
 
 int check_args(const RasterArgs& a, const char* what) {
@@ -702,12 +801,15 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   hipStream_t s = as_stream(stream);
   const int64_t G = I * N;
   // outputs are accumulated: clear them first
-  if ((rc = fill_zero(v_means2d, G * 2 * sizeof(float), s))) return rc;
-  if ((rc = fill_zero(v_conics, G * 3 * sizeof(float), s))) return rc;
-  if ((rc = fill_zero(v_colors, G * channels * sizeof(float), s))) return rc;
-  if ((rc = fill_zero(v_opacities, G * sizeof(float), s))) return rc;
-  if (v_means2d_abs && (rc = fill_zero(v_means2d_abs, G * 2 * sizeof(float), s))) return rc;
-  if (backgrounds && (rc = fill_zero(v_backgrounds, I * channels * sizeof(float), s))) return rc;
+  {
+    const ZeroSpan spans[] = {{v_means2d, G * 2},
+                              {v_conics, G * 3},
+                              {v_colors, G * channels},
+                              {v_opacities, G},
+                              {v_means2d_abs, v_means2d_abs ? G * 2 : 0},
+                              {v_backgrounds, backgrounds ? I * channels : 0}};
+    if ((rc = fill_zero_spans(spans, 6, s))) return rc;
+  }
   if (I == 0 || tile_width == 0 || tile_height == 0) return GSPLAT_OK;
   const dim3 grid(tile_width, tile_height, static_cast<unsigned>(I));
   if (!tile_offsets || !render_alphas || !last_ids || !v_render_colors || !v_render_alphas ||
