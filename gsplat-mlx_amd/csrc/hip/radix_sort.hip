@@ -10,7 +10,8 @@
 //
 // Main path (fewer than 2^30 keys), one kernel per pass after one histogram
 // kernel ("onesweep"):
-//   0. one read of the keys builds the global digit histogram of every pass;
+//   0. one read of the keys builds the global digit histogram of every pass
+//      (per-block rows, then a small add kernel);
 //   1. per pass, block b sorts partition b of 4096 keys (workgroups are
 //      dispatched in index order on each XCD, so a waiting block's
 //      predecessors on its own XCD are resident or done, and no block of a
@@ -197,38 +198,50 @@ constexpr int kMaxPasses = 8;
 constexpr int kSpinLimit = 1 << 18;
 constexpr int kLookbackWindow = 16;
 
+// Global digit histograms of every pass in two steps without same-address
+// atomic pile-ups: each of up to kHistBlocks blocks histograms its share of
+// partitions in LDS (16 keys per lane in flight) and stores its own row of
+// partial counts; then small blocks each add up kHistRowsPerAdd rows and add
+// the sums into the [passes][256] totals.
+constexpr int kHistBlocks = 512;
+constexpr int kHistRowsPerAdd = 32;
+
 template <typename K>
-__global__ void __launch_bounds__(kSortBlock) global_hist_kernel(const K* __restrict__ keys, int64_t n, int bit_lo,
-                                                                 int passes, uint32_t* __restrict__ hist) {
+__global__ void __launch_bounds__(kSortBlock) hist_partial_kernel(const K* __restrict__ keys, int64_t n,
+                                                                  int bit_lo, int passes,
+                                                                  uint32_t* __restrict__ partial) {
   __shared__ uint32_t h[kMaxPasses][kRadix];
   const int t = threadIdx.x;
   for (int p = 0; p < passes; ++p) h[p][t] = 0;
   __syncthreads();
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kSortBlock;
-  for (int64_t i0 = static_cast<int64_t>(blockIdx.x) * kSortBlock; i0 < n; i0 += stride) {
-    const int64_t i = i0 + t;
-    const bool valid = i < n;
-    const K k = valid ? keys[i] : K(0);
-    const uint64_t lanes_below = (t % kWave == 0) ? 0ull : (~0ull >> (kWave - t % kWave));
-    for (int p = 0; p < passes; ++p) {
-      // one LDS add per distinct digit of the wave (lanes with equal digits
-      // found by 8 ballots), so repeated high digits do not serialize
-      const uint32_t d = digit_of(k, bit_lo + 8 * p);
-      uint64_t peers = __ballot(valid);
+  const int64_t n_parts = (n + kOsTile - 1) / kOsTile;
+  for (int64_t part = blockIdx.x; part < n_parts; part += gridDim.x) {
+    const int64_t base = part * kOsTile;
+    K k[kOsItems];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const bool bit = (d >> b) & 1u;
-        const uint64_t m = __ballot(bit);
-        peers &= bit ? m : ~m;
-      }
-      if (valid && (peers & lanes_below) == 0) atomicAdd(&h[p][d], static_cast<uint32_t>(__popcll(peers)));
+    for (int r = 0; r < kOsItems; ++r) {
+      const int64_t i = base + r * kSortBlock + t;
+      k[r] = i < n ? keys[i] : K(0);
+    }
+#pragma unroll
+    for (int r = 0; r < kOsItems; ++r) {
+      if (base + r * kSortBlock + t >= n) continue;
+      for (int p = 0; p < passes; ++p) atomicAdd(&h[p][digit_of(k[r], bit_lo + 8 * p)], 1u);
     }
   }
   __syncthreads();
-  for (int p = 0; p < passes; ++p) {
-    const uint32_t c = h[p][t];
-    if (c) atomicAdd(&hist[p * kRadix + t], c);
-  }
+  for (int p = 0; p < passes; ++p) partial[(static_cast<int64_t>(blockIdx.x) * kMaxPasses + p) * kRadix + t] = h[p][t];
+}
+
+__global__ void __launch_bounds__(kSortBlock) hist_add_kernel(const uint32_t* __restrict__ partial, int rows,
+                                                              uint32_t* __restrict__ hist) {
+  const int p = blockIdx.y;
+  const int t = threadIdx.x;
+  const int r0 = blockIdx.x * kHistRowsPerAdd;
+  const int r1 = min(rows, r0 + kHistRowsPerAdd);
+  uint32_t sum = 0;
+  for (int r = r0; r < r1; ++r) sum += partial[(static_cast<int64_t>(r) * kMaxPasses + p) * kRadix + t];
+  if (sum) atomicAdd(&hist[p * kRadix + t], sum);
 }
 
 template <typename K>
@@ -397,6 +410,7 @@ struct SortWorkspace {
   uint32_t* os_hist;      // [kMaxPasses][256]
   int32_t* os_error;      // set when a look-back gives up (never expected)
   uint32_t* os_lookback;  // [passes][n_parts][256]
+  uint32_t* os_partial;   // [kHistBlocks][kMaxPasses][256] per-block histogram rows
 };
 
 inline size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -417,6 +431,7 @@ size_t layout(int64_t n, SortWorkspace<K>* ws, void* base) {
   const size_t oh_b = onesweep ? align_up(kMaxPasses * kRadix * sizeof(uint32_t)) : 0;
   const size_t ot_b = onesweep ? align_up(sizeof(int32_t)) : 0;
   const size_t ol_b = onesweep ? align_up(static_cast<size_t>(max_passes) * n_parts * kRadix * sizeof(uint32_t)) : 0;
+  const size_t op_b = onesweep ? align_up(static_cast<size_t>(kHistBlocks) * kMaxPasses * kRadix * sizeof(uint32_t)) : 0;
   if (ws && base) {
     char* p = static_cast<char*>(base);
     ws->keys_alt = reinterpret_cast<K*>(p);
@@ -427,8 +442,9 @@ size_t layout(int64_t n, SortWorkspace<K>* ws, void* base) {
     ws->os_hist = reinterpret_cast<uint32_t*>(q);
     ws->os_error = reinterpret_cast<int32_t*>(q + oh_b);
     ws->os_lookback = reinterpret_cast<uint32_t*>(q + oh_b + ot_b);
+    ws->os_partial = reinterpret_cast<uint32_t*>(q + oh_b + ot_b + ol_b);
   }
-  return keys_b + vals_b + hist_b + scan_b + oh_b + ot_b + ol_b;
+  return keys_b + vals_b + hist_b + scan_b + oh_b + ot_b + ol_b + op_b;
 }
 
 }  // namespace
@@ -469,10 +485,11 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
     if (rc) return rc;
     {
       KernelTimer timer("sort_histogram", s);
-      // few blocks: each adds its histogram into the same 256 * passes
-      // global words, and same-address device atomics serialize
-      const int64_t hb = std::min<int64_t>(n_parts, 128);
-      global_hist_kernel<K><<<static_cast<unsigned>(hb), kSortBlock, 0, s>>>(keys_in, n, bit_lo, passes, ws.os_hist);
+      const int hb = static_cast<int>(std::min<int64_t>(n_parts, kHistBlocks));
+      hist_partial_kernel<K><<<static_cast<unsigned>(hb), kSortBlock, 0, s>>>(keys_in, n, bit_lo, passes,
+                                                                              ws.os_partial);
+      const dim3 add_grid((hb + kHistRowsPerAdd - 1) / kHistRowsPerAdd, passes);
+      hist_add_kernel<<<add_grid, kSortBlock, 0, s>>>(ws.os_partial, hb, ws.os_hist);
     }
     if ((rc = check_launch(what))) return rc;
     const K* src_k = keys_in;

@@ -328,20 +328,20 @@ __device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float
   for (int i = 0; i < NC; ++i) y[i] += fbits(__builtin_amdgcn_update_dpp(0u, ubits(y[i]), 0x141, 0xf, 0xf, false));  // 7 - lane
 }
 
-// Backward. Persistent blocks take (tile, band) units from a counter in the
-// heavy-first order of `order`; a tile is split into n_bands bands, each a
-// block of lanes owning P pixels per lane (pixel q = ((band * waves + wave) *
-// P + p) * 64 + lane, so a wave covers a compact run of 64 * P pixels).
-// The tile's list is walked back-to-front in batches of BB entries from the
-// band's largest last_id; the next batch's records are loaded into registers
-// while the current one is processed. For each entry every lane sums the
-// partial gradients of its pixels in a reduced basis (see below); a wave with
-// a contributing pixel sums them over the wave (wave_transpose_reduce) and one
-// lane per 8-lane group stores its totals into the wave's accumulator slot
-// for that entry (plain LDS stores; each (wave, entry) slot is written at most
-// once per batch). After the batch the block adds up the per-wave slots,
-// maps them back to gradients and flushes one global atomic per (entry,
-// nonzero component).
+// Backward. Persistent blocks take tiles from a counter in the heavy-first
+// order of `order`; one lane owns one pixel of the tile (blocks are padded to
+// whole wave64s; padding lanes own nothing). The tile's list is walked
+// back-to-front in batches of BB entries from the tile's largest last_id; the
+// next batch's records are loaded into registers while the current one is
+// processed, and each staged record carries its per-wave touch mask. For each
+// entry a wave visits (ballot over 64 slots, past-last and culled entries
+// skipped), every lane computes its pixel's partial gradients in a reduced
+// basis (below); a wave with a contributing lane sums them over the wave
+// (wave_transpose_reduce) and one lane per 8-lane group stores its totals
+// into the wave's accumulator slot for that entry (plain LDS stores; each
+// (wave, entry) slot is written at most once per batch). After the batch the
+// block adds up the per-wave slots, maps them back to gradients and flushes
+// one global atomic per (entry, nonzero component).
 //
 // Per pixel, with the reference's per-channel `buffer` (gsplat_rasterize.cpp:
 // 500-546) folded into B = sum_c buffer_c * v_rc_c and D = sum_c col_c * v_rc_c:
@@ -351,16 +351,17 @@ __device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float
 // (the conic is the same for every pixel of an entry, so it is applied once
 // after the reduction). Accumulated components: colors (CH), hx dx, hx dy,
 // hy dy, hx, hy, vis * v_alpha, and |v_mean2d| per pixel (x, y) with absgrad.
-// CH == 0 (runtime channel count) uses P == 1 and sends colour gradients
-// straight to global memory.
-template <int CH, bool ABS, int P>
-__global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
-    RasterArgs a, int BB, int n_bands, int64_t n_units, const int32_t* __restrict__ order,
-    int32_t* __restrict__ unit_counter, const float* __restrict__ render_alphas, const int32_t* __restrict__ last_ids,
+// The contribution is computed on every lane of a visiting wave and selected
+// to zero where the pixel does not contribute (no branches, no accumulators
+// to clear). CH == 0 (runtime channel count) sends colour gradients straight
+// to global memory.
+template <int CH, bool ABS>
+__global__ void __launch_bounds__(1024) raster_bwd_kernel(
+    RasterArgs a, int BB, int64_t n_units, const int32_t* __restrict__ order, int32_t* __restrict__ unit_counter,
+    const float* __restrict__ render_alphas, const int32_t* __restrict__ last_ids,
     const float* __restrict__ v_render_colors, const float* __restrict__ v_render_alphas,
     float* __restrict__ v_means2d_abs, float* __restrict__ v_means2d, float* __restrict__ v_conics,
     float* __restrict__ v_colors, float* __restrict__ v_opacities, float* __restrict__ v_backgrounds) {
-  static_assert(CH > 0 || P == 1, "runtime channel counts use one pixel per lane");
   constexpr int LC = CH > 0 ? CH : 1;
   constexpr int AC = CH > 0 ? CH : kMaxChannels;
   constexpr int NG = ABS ? 8 : 6;  // geometry components
@@ -370,12 +371,12 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
   extern __shared__ float smem[];
   const int BS = blockDim.x;
   const int n_waves = BS / kWave;
-  float2* s_xy = reinterpret_cast<float2*>(smem);            // [BB]
-  float4* s_co = reinterpret_cast<float4*>(smem + 2 * BB);   // [BB] conic xyz, opacity
-  int32_t* s_g = reinterpret_cast<int32_t*>(smem + 6 * BB);  // [BB]
-  uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + 7 * BB);  // [BB] per-wave touch bits
-  float* s_col = smem + 8 * BB;                              // [BB][LC] (CH > 0)
-  float* s_acc = s_col + (CH > 0 ? LC * BB : 0);             // [n_waves][BB][NV]
+  float2* s_xy = reinterpret_cast<float2*>(smem);                  // [BB]
+  float4* s_co = reinterpret_cast<float4*>(smem + 2 * BB);         // [BB] conic xyz, opacity
+  int32_t* s_g = reinterpret_cast<int32_t*>(smem + 6 * BB);        // [BB]
+  uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + 7 * BB);   // [BB] per-wave touch bits
+  float* s_col = smem + 8 * BB;                                    // [BB][LC] (CH > 0)
+  float* s_acc = s_col + (CH > 0 ? LC * BB : 0);                   // [n_waves][BB][NV]
   __shared__ int s_max_last;
   __shared__ int64_t s_unit;
 
@@ -384,21 +385,21 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
   const int lane = t % kWave;
   const int wave = t / kWave;
   const bool e_bit = (lane >> 3) & 1;
-  const int red_slot = lane & 7;  // lane 7 of each 8-lane group stores
+  const bool red_slot = (lane & 7) == 7;  // lane 7 of each 8-lane group stores
   int red_idx[NC];
 #pragma unroll
   for (int m = 0; m < NC; ++m) red_idx[m] = red_index<NV>(m, (lane >> 5) & 1, (lane >> 4) & 1, (lane >> 3) & 1);
+  float* const s_acc_wave = s_acc + wave * BB * NV;
   const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
   const int acc_words = n_waves * BB * NV;
 
   for (;;) {
-    __syncthreads();  // the previous unit is done with LDS
+    __syncthreads();  // the previous tile is done with LDS
     if (t == 0) s_unit = atomicAdd(unit_counter, 1);
     __syncthreads();
     const int64_t unit = s_unit;
     if (unit >= n_units) break;  // uniform across the block
-    const int64_t it = order[unit / n_bands];
-    const int band = static_cast<int>(unit % n_bands);
+    const int64_t it = order[unit];
     const int64_t image = it / n_tiles;
     const int tile = static_cast<int>(it % n_tiles);
     const int tx = tile % a.tw, ty = tile / a.tw;
@@ -407,51 +408,41 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
     int64_t start, end;
     tile_range(a, image, tile, &start, &end);
 
-    // per-pixel state; blocks are padded to whole wave64s (the reductions
-    // need every lane) and padding pixels own nothing
-    float px[P], py[P], T[P], B[P], coef[P];
-    int last_rel[P];  // last contributor relative to start, -1 for none
-    float v_rc[P][AC];
-    int my_last = -1;
-#pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int q = ((band * n_waves + wave) * P + p) * kWave + lane;
-      const int x = tx * a.ts + q % a.ts;
-      const int y = ty * a.ts + q / a.ts;
-      const bool inside = q < a.ts * a.ts && x < a.W && y < a.H;
-      const int64_t pix = (image * a.H + y) * static_cast<int64_t>(a.W) + x;
-      px[p] = static_cast<float>(x) + 0.5f;
-      py[p] = static_cast<float>(y) + 0.5f;
-      const float T_final = inside ? 1.0f - render_alphas[pix] : 1.0f;
-      T[p] = T_final;
-      B[p] = 0.0f;
-      last_rel[p] = -1;
-      if (inside) {
-        const int64_t l = min<int64_t>(end - 1, last_ids[pix]) - start;
-        last_rel[p] = static_cast<int>(max<int64_t>(-1, min<int64_t>(l, INT32_MAX)));
-      }
-      my_last = max(my_last, last_rel[p]);
-      float bg_dot = 0.0f;
-      for (int c = 0; c < channels; ++c) v_rc[p][c] = inside ? v_render_colors[pix * channels + c] : 0.0f;
-      const float v_ra = inside ? v_render_alphas[pix] : 0.0f;
-      if (bg) {
-        for (int c = 0; c < channels; ++c) bg_dot += bg[c] * v_rc[p][c];
-        // v_backgrounds = sum over pixels of T_final * v_rc (gsplat_rasterize.cpp:459-464)
-        for (int c = 0; c < channels; ++c) {
-          const float sum = wave_sum_uniform(T_final * v_rc[p][c]);
-          if (lane == 0) unsafeAtomicAdd(v_backgrounds + image * channels + c, sum);
-        }
-      }
-      // d(final-transmittance terms)/d(alpha) = ra * coef
-      coef[p] = T_final * v_ra + -T_final * bg_dot;
+    const int x = tx * a.ts + t % a.ts;
+    const int y = ty * a.ts + t / a.ts;
+    const bool inside = t < a.ts * a.ts && x < a.W && y < a.H;
+    const int64_t pix = (image * a.H + y) * static_cast<int64_t>(a.W) + x;
+    const float px = static_cast<float>(x) + 0.5f;
+    const float py = static_cast<float>(y) + 0.5f;
+    const float T_final = inside ? 1.0f - render_alphas[pix] : 1.0f;
+    float T = T_final;
+    float B = 0.0f;
+    int last_rel = -1;  // last contributor relative to start, -1 for none
+    if (inside) {
+      const int64_t l = min<int64_t>(end - 1, last_ids[pix]) - start;
+      last_rel = static_cast<int>(max<int64_t>(-1, min<int64_t>(l, INT32_MAX)));
     }
+    float v_rc[AC];
+    float bg_dot = 0.0f;
+    for (int c = 0; c < channels; ++c) v_rc[c] = inside ? v_render_colors[pix * channels + c] : 0.0f;
+    const float v_ra = inside ? v_render_alphas[pix] : 0.0f;
+    if (bg) {
+      for (int c = 0; c < channels; ++c) bg_dot += bg[c] * v_rc[c];
+      // v_backgrounds = sum over pixels of T_final * v_rc (gsplat_rasterize.cpp:459-464)
+      for (int c = 0; c < channels; ++c) {
+        const float sum = wave_sum_uniform(T_final * v_rc[c]);
+        if (lane == 0) unsafeAtomicAdd(v_backgrounds + image * channels + c, sum);
+      }
+    }
+    // d(final-transmittance terms)/d(alpha) = ra * coef
+    const float coef = T_final * v_ra + -T_final * bg_dot;
 
     // Entries past every pixel's last contributor are skipped wholesale: the
     // block starts at its largest last_id, each wave skips entries past its own.
     if (t == 0) s_max_last = -1;
     __syncthreads();
-    if (my_last >= 0) atomicMax(&s_max_last, my_last);
-    int wave_last = my_last;
+    if (last_rel >= 0) atomicMax(&s_max_last, last_rel);
+    int wave_last = last_rel;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) wave_last = max(wave_last, __shfl_xor(wave_last, off, kWave));
     __syncthreads();
@@ -467,9 +458,7 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
       const int64_t j = hi - 1 - t;  // slot t holds entry hi - 1 - t (back to front)
       if (t < BB && j >= lo) {
         r_g = load_gaussian(a, j, &r_xy, &r_co);
-        // the rectangles follow the one-pixel-per-lane mapping; other
-        // mappings keep every record
-        r_mask = P == 1 ? touch_mask(r_xy, r_co, n_waves * n_bands, a.ts, tx, ty) >> (band * n_waves) : ~0u;
+        r_mask = touch_mask(r_xy, r_co, n_waves, a.ts, tx, ty);
         if constexpr (CH > 0) {
 #pragma unroll
           for (int c = 0; c < CH; ++c) r_col[c] = a.colors[static_cast<int64_t>(r_g) * CH + c];
@@ -499,91 +488,97 @@ __global__ void __launch_bounds__(P > 1 ? 256 : 1024) raster_bwd_kernel(
       const int cnt = static_cast<int>(b1 - b0);
       const int k_rel0 = static_cast<int>(b1 - 1 - start);  // entry of slot 0, relative to start
       for (int c0 = 0; c0 < cnt; c0 += kWave) {
-        // records of this 64-slot chunk that may touch this wave and are not
-        // past its last contributor (all lanes vote)
+        // slots of this chunk that may touch this wave and are not past its
+        // last contributor (all lanes vote)
         const int kl = c0 + lane;
         uint64_t bits = __ballot(kl < cnt && k_rel0 - kl <= wave_last && ((s_mask[kl] >> wave) & 1u));
-        while (bits) {
-        const int k = c0 + __builtin_ctzll(bits);
+        if (!bits) continue;
+        // software-pipelined: the next visited slot's record is read from LDS
+        // while the current one is processed
+        int k = c0 + __builtin_ctzll(bits);
         bits &= bits - 1;
-        const int k_rel = k_rel0 - k;
-        const float2 m = s_xy[k];
-        const float4 co = s_co[k];
+        float2 m = s_xy[k];
+        float4 co = s_co[k];
         float col[LC];
         if constexpr (CH > 0) {
 #pragma unroll
           for (int c = 0; c < CH; ++c) col[c] = s_col[k * CH + c];
         }
-        const float* gcol = nullptr;
-        if constexpr (CH == 0) gcol = a.colors + static_cast<int64_t>(s_g[k]) * channels;
-        float v[NV];
+        for (;;) {
+          const bool more = bits != 0;
+          const int kn = more ? c0 + __builtin_ctzll(bits) : k;
+          bits &= bits - 1;
+          const float2 mn = s_xy[kn];
+          const float4 con = s_co[kn];
+          float coln[LC];
+          if constexpr (CH > 0) {
 #pragma unroll
-        for (int i = 0; i < NV; ++i) v[i] = 0.0f;
-        float v_col_generic[CH > 0 ? 1 : kMaxChannels];
-        if constexpr (CH == 0) {
-          for (int c = 0; c < channels; ++c) v_col_generic[c] = 0.0f;
-        }
-        bool any = false;
-#pragma unroll
-        for (int p = 0; p < P; ++p) {
-          const float dx = m.x - px[p];
-          const float dy = m.y - py[p];
+            for (int c = 0; c < CH; ++c) coln[c] = s_col[kn * CH + c];
+          }
+          const int k_rel = k_rel0 - k;
+          const float dx = m.x - px;
+          const float dy = m.y - py;
           const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
           const float vis = expf(-sigma);
           const float a_raw = co.w * vis;
           const float alpha = fminf(kMaxAlpha, a_raw);
-          const bool valid = k_rel <= last_rel[p] && !(sigma < 0.0f || alpha < kAlphaThreshold);
-          if (!valid) continue;
-          any = true;
+          const bool valid = k_rel <= last_rel && !(sigma < 0.0f || alpha < kAlphaThreshold);
+          if (__ballot(valid) != 0) {
+          // contribution of this pixel, selected to zero unless valid
           const float ra = __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - alpha));
-          T[p] *= ra;
-          const float fac = alpha * T[p];
+          const float T_new = T * ra;
+          const float fac = alpha * T_new;
+          float v[NV];
           float D = 0.0f;
           if constexpr (CH > 0) {
 #pragma unroll
             for (int c = 0; c < CH; ++c) {
-              D += col[c] * v_rc[p][c];
-              v[c] += fac * v_rc[p][c];
+              D += col[c] * v_rc[c];
+              v[c] = valid ? fac * v_rc[c] : 0.0f;
             }
           } else {
+            const float* gcol = a.colors + static_cast<int64_t>(s_g[k]) * channels;
+            const int64_t gg = s_g[k];
+            for (int c = 0; c < channels; ++c) D += gcol[c] * v_rc[c];
             for (int c = 0; c < channels; ++c) {
-              D += gcol[c] * v_rc[p][c];
-              v_col_generic[c] = fac * v_rc[p][c];
+              const float sum = wave_sum_uniform(valid ? fac * v_rc[c] : 0.0f);
+              if (lane == 0 && sum != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, sum);
             }
           }
-          const float v_alpha = T[p] * D + ra * (coef[p] - B[p]);
-          B[p] += fac * D;
-          if (a_raw <= kMaxAlpha) {
-            const float v_sigma = -a_raw * v_alpha;
-            const float hx = v_sigma * dx;
-            const float hy = v_sigma * dy;
-            v[o + 0] += hx * dx;
-            v[o + 1] += hx * dy;
-            v[o + 2] += hy * dy;
-            v[o + 3] += hx;
-            v[o + 4] += hy;
-            v[o + 5] += vis * v_alpha;
-            if constexpr (ABS) {
-              v[o + 6] += fabsf(co.x * hx + co.y * hy);
-              v[o + 7] += fabsf(co.y * hx + co.z * hy);
-            }
+          const float v_alpha = T_new * D + ra * (coef - B);
+          const float B_new = B + fac * D;
+          const bool geo = valid && a_raw <= kMaxAlpha;
+          const float v_sigma = -a_raw * v_alpha;
+          const float hx = v_sigma * dx;
+          const float hy = v_sigma * dy;
+          v[o + 0] = geo ? hx * dx : 0.0f;
+          v[o + 1] = geo ? hx * dy : 0.0f;
+          v[o + 2] = geo ? hy * dy : 0.0f;
+          v[o + 3] = geo ? hx : 0.0f;
+          v[o + 4] = geo ? hy : 0.0f;
+          v[o + 5] = geo ? vis * v_alpha : 0.0f;
+          if constexpr (ABS) {
+            v[o + 6] = geo ? fabsf(co.x * hx + co.y * hy) : 0.0f;
+            v[o + 7] = geo ? fabsf(co.y * hx + co.z * hy) : 0.0f;
           }
-        }
-        if (__ballot(any) == 0) continue;
-        if constexpr (CH == 0) {
-          const int64_t gg = s_g[k];
-          for (int c = 0; c < channels; ++c) {
-            const float sum = wave_sum_uniform(v_col_generic[c]);
-            if (lane == 0 && sum != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, sum);
-          }
-        }
-        float y[NC];
-        wave_transpose_reduce<NV>(v, y, e_bit);
-        if (red_slot == 7) {
-          float* acc = s_acc + (wave * BB + k) * NV;
+          T = valid ? T_new : T;
+          B = valid ? B_new : B;
+          float yv[NC];
+          wave_transpose_reduce<NV>(v, yv, e_bit);
+          if (red_slot) {
+            float* acc = s_acc_wave + k * NV;
 #pragma unroll
-          for (int mm = 0; mm < NC; ++mm) acc[red_idx[mm]] = y[mm];
-        }
+            for (int mm = 0; mm < NC; ++mm) acc[red_idx[mm]] = yv[mm];
+          }
+          }
+          if (!more) break;
+          k = kn;
+          m = mn;
+          co = con;
+          if constexpr (CH > 0) {
+#pragma unroll
+            for (int c = 0; c < CH; ++c) col[c] = coln[c];
+          }
         }
       }
       __syncthreads();
@@ -708,22 +703,15 @@ int64_t resident_blocks(const void* kernel, int block, size_t smem) {
 
 // records: mean 2, conic+opacity 4, colours (CH > 0), Gaussian id, touch mask
 size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (8 + (ch > 0 ? ch : 0)) * 4; }
-// Backward work split: pixels per lane and waves per block; a tile's pixels
-// are split over n_bands blocks of bwd_block lanes.
-// Backward work split: one pixel per lane and the whole tile in one block
-// (measured fastest on gfx950 for 16x16 tiles against 2 or 4 pixels per lane
-// and against splitting a tile over several blocks: the lower register count
+// Backward block: one pixel per lane, the whole tile in one block (measured
+// fastest on gfx950 for 16x16 tiles against 2 or 4 pixels per lane and
+// against splitting a tile over several blocks: the lower register count
 // keeps six waves per SIMD resident). Batch length: 128 entries for blocks of
 // up to 256 lanes, 64 above (bounds the per-wave accumulators to 48 KiB at
 // 1024 lanes, 4 channels, absgrad); never more than the block, so one lane
 // loads one record.
-struct BwdShape {
-  int ppl, bs, n_bands, bb;
-};
-BwdShape bwd_shape(int ts) {
-  const int bs = (ts * ts + kWave - 1) / kWave * kWave;
-  return {1, bs, 1, bs <= 128 ? bs : (bs <= 256 ? 128 : 64)};
-}
+int bwd_block(int ts) { return (ts * ts + kWave - 1) / kWave * kWave; }
+int bwd_batch(int bs) { return bs <= 128 ? bs : (bs <= 256 ? 128 : 64); }
 // records (8 words + colours: mean, conic+opacity, id, touch mask) per batch
 // slot plus NV accumulators per (wave, slot)
 size_t bwd_smem(int ch, int bs, int bb, bool absgrad) {
@@ -816,11 +804,10 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
       (n_isects > 0 && (!flatten_ids || !means2d || !conics || !colors || !opacities)))
     return invalid("rasterize_to_pixels_3dgs_backward: null pointer.");
   const int ch = channels <= 4 ? channels : 0;
-  const BwdShape shape = bwd_shape(tile_size);
-  const int bs = shape.bs;
+  const int bs = bwd_block(tile_size);
   const int64_t n_total = I * tile_width * static_cast<int64_t>(tile_height);
-  // the int32 unit counter may run past n_units by one per resident block
-  if (n_total * shape.n_bands > INT32_MAX / 2) return invalid("rasterize_to_pixels_3dgs_backward: too many tiles.");
+  // the int32 tile counter may run past n_total by one per resident block
+  if (n_total > INT32_MAX / 2) return invalid("rasterize_to_pixels_3dgs_backward: too many tiles.");
   if (!workspace || workspace_bytes < bwd_workspace_bytes(n_total)) {
     set_error("rasterize_to_pixels_3dgs_backward: workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
@@ -834,35 +821,33 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
     tile_order_kernel<<<1, kScanBlock, 0, s>>>(cost, n_total, order, counter);
   }
   if ((rc = check_launch("rasterize_to_pixels_3dgs_backward"))) return rc;
-  const int64_t n_units = n_total * shape.n_bands;
-  const int bb = shape.bb;
+  const int bb = bwd_batch(bs);
   const size_t sm = bwd_smem(ch, bs, bb, v_means2d_abs != nullptr);
   KernelTimer timer("raster_bwd", s);
   // persistent launch: as many blocks as fit on the device at once, each
-  // taking units from the counter until all are done
-#define GSPLAT_BWD_LAUNCH(C, ABS_, PPL, VABS)                                                                   \
+  // taking tiles from the counter until all are done
+#define GSPLAT_BWD_LAUNCH(C, ABS_, VABS)                                                                       \
   {                                                                                                            \
-    const void* fn = reinterpret_cast<const void*>(&raster_bwd_kernel<C, ABS_, PPL>);                          \
+    const void* fn = reinterpret_cast<const void*>(&raster_bwd_kernel<C, ABS_>);                               \
     const int64_t res = resident_blocks(fn, bs, sm);                                                           \
     if (res <= 0) return check_hip(hipGetLastError(), "rasterize_to_pixels_3dgs_backward: occupancy query");   \
-    const unsigned nb = static_cast<unsigned>(std::min<int64_t>(n_units, res));                                \
-    raster_bwd_kernel<C, ABS_, PPL><<<nb, bs, sm, s>>>(a, bb, shape.n_bands, n_units, order, counter,          \
-                                                       render_alphas, last_ids, v_render_colors, v_render_alphas, \
-                                                       VABS, v_means2d, v_conics, v_colors, v_opacities,        \
-                                                       v_backgrounds);                                          \
+    const unsigned nb = static_cast<unsigned>(std::min<int64_t>(n_total, res));                                \
+    raster_bwd_kernel<C, ABS_><<<nb, bs, sm, s>>>(a, bb, n_total, order, counter, render_alphas, last_ids,     \
+                                                  v_render_colors, v_render_alphas, VABS, v_means2d, v_conics, \
+                                                  v_colors, v_opacities, v_backgrounds);                        \
   }
-#define GSPLAT_BWD_ABS(C, PPL)                          \
-  if (v_means2d_abs) {                                  \
-    GSPLAT_BWD_LAUNCH(C, true, PPL, v_means2d_abs)      \
-  } else {                                              \
-    GSPLAT_BWD_LAUNCH(C, false, PPL, nullptr)           \
+#define GSPLAT_BWD_ABS(C)                            \
+  if (v_means2d_abs) {                               \
+    GSPLAT_BWD_LAUNCH(C, true, v_means2d_abs)        \
+  } else {                                           \
+    GSPLAT_BWD_LAUNCH(C, false, nullptr)             \
   }
   switch (ch) {
-    case 1: GSPLAT_BWD_ABS(1, 1); break;
-    case 2: GSPLAT_BWD_ABS(2, 1); break;
-    case 3: GSPLAT_BWD_ABS(3, 1); break;
-    case 4: GSPLAT_BWD_ABS(4, 1); break;
-    default: GSPLAT_BWD_ABS(0, 1); break;
+    case 1: GSPLAT_BWD_ABS(1); break;
+    case 2: GSPLAT_BWD_ABS(2); break;
+    case 3: GSPLAT_BWD_ABS(3); break;
+    case 4: GSPLAT_BWD_ABS(4); break;
+    default: GSPLAT_BWD_ABS(0); break;
   }
 #undef GSPLAT_BWD_ABS
 #undef GSPLAT_BWD_LAUNCH
