@@ -357,7 +357,8 @@ __device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float
 // to global memory.
 template <int CH, bool ABS>
 __global__ void __launch_bounds__(1024) raster_bwd_kernel(
-    RasterArgs a, int BB, int64_t n_units, const int32_t* __restrict__ order, int32_t* __restrict__ unit_counter,
+    RasterArgs a, int BB, int64_t n_units, const int32_t* __restrict__ order, const int32_t* __restrict__ cost,
+    int32_t* __restrict__ unit_counter,
     const float* __restrict__ render_alphas, const int32_t* __restrict__ last_ids,
     const float* __restrict__ v_render_colors, const float* __restrict__ v_render_alphas,
     float* __restrict__ v_means2d_abs, float* __restrict__ v_means2d, float* __restrict__ v_conics,
@@ -377,7 +378,6 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
   uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + 7 * BB);   // [BB] per-wave touch bits
   float* s_col = smem + 8 * BB;                                    // [BB][LC] (CH > 0)
   float* s_acc = s_col + (CH > 0 ? LC * BB : 0);                   // [n_waves][BB][NV]
-  __shared__ int s_max_last;
   __shared__ int64_t s_unit;
 
   const int channels = CH > 0 ? CH : a.channels;
@@ -393,20 +393,43 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
   const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
   const int acc_words = n_waves * BB * NV;
 
+  // the next tile is claimed one tile ahead (kept in a register of thread 0
+  // until the tile ends), so the counter's latency overlaps the tile's work
+  if (t == 0) s_unit = atomicAdd(unit_counter, 1);
   for (;;) {
-    __syncthreads();  // the previous tile is done with LDS
-    if (t == 0) s_unit = atomicAdd(unit_counter, 1);
-    __syncthreads();
+    __syncthreads();  // the previous tile is done with LDS; s_unit is visible
     const int64_t unit = s_unit;
     if (unit >= n_units) break;  // uniform across the block
+    int32_t next_unit = 0;
+    if (t == 0) next_unit = atomicAdd(unit_counter, 1);
     const int64_t it = order[unit];
     const int64_t image = it / n_tiles;
     const int tile = static_cast<int>(it % n_tiles);
     const int tx = tile % a.tw, ty = tile / a.tw;
-    if (a.masks && !a.masks[image * n_tiles + tile]) continue;  // masked tiles contribute nothing
-    const float* bg = a.backgrounds ? a.backgrounds + image * channels : nullptr;
+    // masked tiles contribute nothing; their cost is 0, so the walk is empty
     int64_t start, end;
     tile_range(a, image, tile, &start, &end);
+    // the tile's replay length (largest last_id - start + 1) from the schedule
+    // pass; the first batch is fetched before the pixel state is read
+    const int64_t stop = start + cost[it];
+    // register prefetch of one batch record (lanes t < BB)
+    float2 r_xy = make_float2(0.0f, 0.0f);
+    float4 r_co = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int32_t r_g = 0;
+    uint32_t r_mask = 0;
+    float r_col[LC];
+    auto fetch = [&](int64_t hi, int64_t lo) {
+      const int64_t j = hi - 1 - t;  // slot t holds entry hi - 1 - t (back to front)
+      if (t < BB && j >= lo) {
+        r_g = load_gaussian(a, j, &r_xy, &r_co);
+        r_mask = touch_mask(r_xy, r_co, n_waves, a.ts, tx, ty);
+        if constexpr (CH > 0) {
+#pragma unroll
+          for (int c = 0; c < CH; ++c) r_col[c] = a.colors[static_cast<int64_t>(r_g) * CH + c];
+        }
+      }
+    };
+    if (stop > start) fetch(stop, max<int64_t>(start, stop - BB));
 
     const int x = tx * a.ts + t % a.ts;
     const int y = ty * a.ts + t / a.ts;
@@ -426,46 +449,17 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
     float bg_dot = 0.0f;
     for (int c = 0; c < channels; ++c) v_rc[c] = inside ? v_render_colors[pix * channels + c] : 0.0f;
     const float v_ra = inside ? v_render_alphas[pix] : 0.0f;
-    if (bg) {
+    if (a.backgrounds) {
+      const float* bg = a.backgrounds + image * channels;
       for (int c = 0; c < channels; ++c) bg_dot += bg[c] * v_rc[c];
-      // v_backgrounds = sum over pixels of T_final * v_rc (gsplat_rasterize.cpp:459-464)
-      for (int c = 0; c < channels; ++c) {
-        const float sum = wave_sum_uniform(T_final * v_rc[c]);
-        if (lane == 0) unsafeAtomicAdd(v_backgrounds + image * channels + c, sum);
-      }
     }
     // d(final-transmittance terms)/d(alpha) = ra * coef
     const float coef = T_final * v_ra + -T_final * bg_dot;
-
-    // Entries past every pixel's last contributor are skipped wholesale: the
-    // block starts at its largest last_id, each wave skips entries past its own.
-    if (t == 0) s_max_last = -1;
-    __syncthreads();
-    if (last_rel >= 0) atomicMax(&s_max_last, last_rel);
+    // entries past every pixel of the wave's last contributor are skipped
     int wave_last = last_rel;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) wave_last = max(wave_last, __shfl_xor(wave_last, off, kWave));
-    __syncthreads();
-    const int64_t stop = start + s_max_last + 1;  // exclusive end of the needed range
 
-    // register prefetch of one batch record (lanes t < BB)
-    float2 r_xy = make_float2(0.0f, 0.0f);
-    float4 r_co = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    int32_t r_g = 0;
-    uint32_t r_mask = 0;
-    float r_col[LC];
-    auto fetch = [&](int64_t hi, int64_t lo) {
-      const int64_t j = hi - 1 - t;  // slot t holds entry hi - 1 - t (back to front)
-      if (t < BB && j >= lo) {
-        r_g = load_gaussian(a, j, &r_xy, &r_co);
-        r_mask = touch_mask(r_xy, r_co, n_waves, a.ts, tx, ty);
-        if constexpr (CH > 0) {
-#pragma unroll
-          for (int c = 0; c < CH; ++c) r_col[c] = a.colors[static_cast<int64_t>(r_g) * CH + c];
-        }
-      }
-    };
-    if (stop > start) fetch(stop, max<int64_t>(start, stop - BB));
 
     for (int64_t b1 = stop; b1 > start; b1 -= BB) {
       const int64_t b0 = max<int64_t>(start, b1 - BB);
@@ -613,6 +607,44 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
         }
       }
     }
+    __syncthreads();  // every thread has read this tile's s_unit
+    if (t == 0) s_unit = next_unit;
+  }
+}
+
+// v_backgrounds[i, c] = sum over the unmasked pixels of image i of
+// (1 - render_alpha) * v_render_colors[c] (gsplat_rasterize.cpp:459-464): a
+// few blocks per image reduce their pixel range, then one atomic per
+// (block, channel).
+constexpr int kBgBlocks = 64;
+
+__global__ void __launch_bounds__(256) background_grad_kernel(RasterArgs a, const float* __restrict__ render_alphas,
+                                                              const float* __restrict__ v_render_colors,
+                                                              float* __restrict__ v_backgrounds) {
+  __shared__ float s_sum[256 / kWave][kMaxChannels];
+  const int64_t image = blockIdx.y;
+  const int64_t n_pix = static_cast<int64_t>(a.W) * a.H;
+  const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
+  const int t = threadIdx.x;
+  const int channels = a.channels;
+  float acc[kMaxChannels];
+  for (int c = 0; c < channels; ++c) acc[c] = 0.0f;
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + t; p < n_pix; p += static_cast<int64_t>(gridDim.x) * 256) {
+    const int x = static_cast<int>(p % a.W), y = static_cast<int>(p / a.W);
+    if (a.masks && !a.masks[image * n_tiles + (y / a.ts) * a.tw + x / a.ts]) continue;
+    const int64_t pix = image * n_pix + p;
+    const float T_final = 1.0f - render_alphas[pix];
+    for (int c = 0; c < channels; ++c) acc[c] += T_final * v_render_colors[pix * channels + c];
+  }
+  for (int c = 0; c < channels; ++c) {
+    const float w = wave_sum_uniform(acc[c]);
+    if (t % kWave == 0) s_sum[t / kWave][c] = w;
+  }
+  __syncthreads();
+  if (t < channels) {
+    float sum = 0.0f;
+    for (int w = 0; w < 256 / kWave; ++w) sum += s_sum[w][t];
+    unsafeAtomicAdd(v_backgrounds + image * channels + t, sum);
   }
 }
 
@@ -821,6 +853,12 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
     tile_order_kernel<<<1, kScanBlock, 0, s>>>(cost, n_total, order, counter);
   }
   if ((rc = check_launch("rasterize_to_pixels_3dgs_backward"))) return rc;
+  if (backgrounds) {
+    KernelTimer timer("raster_bwd_background", s);
+    background_grad_kernel<<<dim3(kBgBlocks, static_cast<unsigned>(I)), 256, 0, s>>>(a, render_alphas,
+                                                                                       v_render_colors, v_backgrounds);
+    if ((rc = check_launch("rasterize_to_pixels_3dgs_backward"))) return rc;
+  }
   const int bb = bwd_batch(bs);
   const size_t sm = bwd_smem(ch, bs, bb, v_means2d_abs != nullptr);
   KernelTimer timer("raster_bwd", s);
@@ -832,7 +870,7 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
     const int64_t res = resident_blocks(fn, bs, sm);                                                           \
     if (res <= 0) return check_hip(hipGetLastError(), "rasterize_to_pixels_3dgs_backward: occupancy query");   \
     const unsigned nb = static_cast<unsigned>(std::min<int64_t>(n_total, res));                                \
-    raster_bwd_kernel<C, ABS_><<<nb, bs, sm, s>>>(a, bb, n_total, order, counter, render_alphas, last_ids,     \
+    raster_bwd_kernel<C, ABS_><<<nb, bs, sm, s>>>(a, bb, n_total, order, cost, counter, render_alphas, last_ids,\
                                                   v_render_colors, v_render_alphas, VABS, v_means2d, v_conics, \
                                                   v_colors, v_opacities, v_backgrounds);                        \
   }
