@@ -328,9 +328,9 @@ __device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float
   for (int i = 0; i < NC; ++i) y[i] += fbits(__builtin_amdgcn_update_dpp(0u, ubits(y[i]), 0x141, 0xf, 0xf, false));  // 7 - lane
 }
 
-// Backward. Persistent blocks take tiles from a counter in the heavy-first
-// order of `order`; one lane owns one pixel of the tile (blocks are padded to
-// whole wave64s; padding lanes own nothing). The tile's list is walked
+// Backward. Persistent blocks walk the heavy-first tile order of `order`
+// (dealt statically, see below); one lane owns one pixel of the tile (blocks
+// are padded to whole wave64s; padding lanes own nothing). The tile's list is walked
 // back-to-front in batches of BB entries from the tile's largest last_id; the
 // next batch's records are loaded into registers while the current one is
 // processed, and each staged record carries its per-wave touch mask. For each
@@ -358,7 +358,6 @@ __device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float
 template <int CH, bool ABS>
 __global__ void __launch_bounds__(1024) raster_bwd_kernel(
     RasterArgs a, int BB, int64_t n_units, const int32_t* __restrict__ order, const int32_t* __restrict__ cost,
-    int32_t* __restrict__ unit_counter,
     const float* __restrict__ render_alphas, const int32_t* __restrict__ last_ids,
     const float* __restrict__ v_render_colors, const float* __restrict__ v_render_alphas,
     float* __restrict__ v_means2d_abs, float* __restrict__ v_means2d, float* __restrict__ v_conics,
@@ -378,7 +377,6 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
   uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + 7 * BB);   // [BB] per-wave touch bits
   float* s_col = smem + 8 * BB;                                    // [BB][LC] (CH > 0)
   float* s_acc = s_col + (CH > 0 ? LC * BB : 0);                   // [n_waves][BB][NV]
-  __shared__ int64_t s_unit;
 
   const int channels = CH > 0 ? CH : a.channels;
   const int t = threadIdx.x;
@@ -393,15 +391,16 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
   const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
   const int acc_words = n_waves * BB * NV;
 
-  // the next tile is claimed one tile ahead (kept in a register of thread 0
-  // until the tile ends), so the counter's latency overlaps the tile's work
-  if (t == 0) s_unit = atomicAdd(unit_counter, 1);
-  for (;;) {
-    __syncthreads();  // the previous tile is done with LDS; s_unit is visible
-    const int64_t unit = s_unit;
+  // Static heavy-first schedule: round r gives block b the tile at rank
+  // r * nb + b (r even) or r * nb + nb - 1 - b (r odd) of the cost-sorted
+  // order ("snake" dealing, so every block gets a similar mix of heavy and
+  // light tiles). No shared counter: device-scope atomics on one address
+  // serialize across the whole GPU.
+  const int64_t nb = gridDim.x;
+  for (int64_t r = 0;; ++r) {
+    const int64_t unit = r * nb + ((r & 1) ? nb - 1 - blockIdx.x : blockIdx.x);
     if (unit >= n_units) break;  // uniform across the block
-    int32_t next_unit = 0;
-    if (t == 0) next_unit = atomicAdd(unit_counter, 1);
+    __syncthreads();  // the previous tile is done with LDS
     const int64_t it = order[unit];
     const int64_t image = it / n_tiles;
     const int tile = static_cast<int>(it % n_tiles);
@@ -607,8 +606,6 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
         }
       }
     }
-    __syncthreads();  // every thread has read this tile's s_unit
-    if (t == 0) s_unit = next_unit;
   }
 }
 
@@ -687,13 +684,11 @@ __global__ void __launch_bounds__(256) tile_cost_kernel(RasterArgs a, const int3
 
 // One block: counting sort of the n tile costs into descending order.
 __global__ void __launch_bounds__(kScanBlock) tile_order_kernel(const int32_t* __restrict__ cost, int64_t n,
-                                                                int32_t* __restrict__ order,
-                                                                int32_t* __restrict__ unit_counter) {
+                                                                int32_t* __restrict__ order) {
   static_assert(kCostBuckets % kScanBlock == 0, "buckets per thread");
   constexpr int PER = kCostBuckets / kScanBlock;
   __shared__ int hist[kCostBuckets];
   const int t = threadIdx.x;
-  if (t == 0) *unit_counter = 0;  // the backward's work counter starts from the first unit
   for (int i = t; i < kCostBuckets; i += kScanBlock) hist[i] = 0;
   __syncthreads();
   for (int64_t i = t; i < n; i += kScanBlock) atomicAdd(&hist[kCostBuckets - 1 - min(cost[i], kCostBuckets - 1)], 1);
@@ -717,10 +712,8 @@ __global__ void __launch_bounds__(kScanBlock) tile_order_kernel(const int32_t* _
 }
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
-// cost [n] int32, order [n] int32, unit counter int32
-size_t bwd_workspace_bytes(int64_t n_tiles_total) {
-  return 2 * align256(static_cast<size_t>(n_tiles_total) * 4) + 256;
-}
+// cost [n] int32, order [n] int32
+size_t bwd_workspace_bytes(int64_t n_tiles_total) { return 2 * align256(static_cast<size_t>(n_tiles_total) * 4); }
 
 // Resident blocks of `kernel` on the current device (persistent launches).
 int64_t resident_blocks(const void* kernel, int block, size_t smem) {
@@ -838,19 +831,17 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   const int ch = channels <= 4 ? channels : 0;
   const int bs = bwd_block(tile_size);
   const int64_t n_total = I * tile_width * static_cast<int64_t>(tile_height);
-  // the int32 tile counter may run past n_total by one per resident block
-  if (n_total > INT32_MAX / 2) return invalid("rasterize_to_pixels_3dgs_backward: too many tiles.");
+  if (n_total > INT32_MAX) return invalid("rasterize_to_pixels_3dgs_backward: too many tiles.");
   if (!workspace || workspace_bytes < bwd_workspace_bytes(n_total)) {
     set_error("rasterize_to_pixels_3dgs_backward: workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
   }
   int32_t* cost = static_cast<int32_t*>(workspace);
   int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(n_total * 4));
-  int32_t* counter = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + 2 * align256(n_total * 4));
   {
     KernelTimer timer("raster_bwd_schedule", s);
     tile_cost_kernel<<<grid, 256, 0, s>>>(a, last_ids, cost);
-    tile_order_kernel<<<1, kScanBlock, 0, s>>>(cost, n_total, order, counter);
+    tile_order_kernel<<<1, kScanBlock, 0, s>>>(cost, n_total, order);
   }
   if ((rc = check_launch("rasterize_to_pixels_3dgs_backward"))) return rc;
   if (backgrounds) {
@@ -863,14 +854,14 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   const size_t sm = bwd_smem(ch, bs, bb, v_means2d_abs != nullptr);
   KernelTimer timer("raster_bwd", s);
   // persistent launch: as many blocks as fit on the device at once, each
-  // taking tiles from the counter until all are done
+  // walking its share of the heavy-first order
 #define GSPLAT_BWD_LAUNCH(C, ABS_, VABS)                                                                       \
   {                                                                                                            \
     const void* fn = reinterpret_cast<const void*>(&raster_bwd_kernel<C, ABS_>);                               \
     const int64_t res = resident_blocks(fn, bs, sm);                                                           \
     if (res <= 0) return check_hip(hipGetLastError(), "rasterize_to_pixels_3dgs_backward: occupancy query");   \
     const unsigned nb = static_cast<unsigned>(std::min<int64_t>(n_total, res));                                \
-    raster_bwd_kernel<C, ABS_><<<nb, bs, sm, s>>>(a, bb, n_total, order, cost, counter, render_alphas, last_ids,\
+    raster_bwd_kernel<C, ABS_><<<nb, bs, sm, s>>>(a, bb, n_total, order, cost, render_alphas, last_ids,       \
                                                   v_render_colors, v_render_alphas, VABS, v_means2d, v_conics, \
                                                   v_colors, v_opacities, v_backgrounds);                        \
   }

@@ -22,6 +22,7 @@ from .autograd import (  # noqa: E402,F401
     projection_ewa_3dgs_fused,
     quat_scale_to_covar_preci,
     rasterize_to_pixels_3dgs,
+    sh_camera_colors,
     spherical_harmonics,
 )
 
@@ -38,8 +39,11 @@ __all__ = [
     "spherical_harmonics_backward",
     "quat_scale_to_covar_preci_forward",
     "quat_scale_to_covar_preci_backward",
+    "sh_camera_colors_forward",
+    "sh_camera_colors_backward",
     "projection_ewa_3dgs_fused",
     "quat_scale_to_covar_preci",
     "rasterize_to_pixels_3dgs",
+    "sh_camera_colors",
     "spherical_harmonics",
 ]
