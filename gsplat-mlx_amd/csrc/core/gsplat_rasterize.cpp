@@ -145,7 +145,7 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
   array v_col = at::empty(colors.sizes(), f32_like(means2d));
   array v_op = at::empty(opac.sizes(), f32_like(means2d));
   array v_bg = p.use_backgrounds ? at::empty(bg.sizes(), f32_like(means2d)) : at::empty({0}, f32_like(means2d));
-  const size_t ws_bytes = gsplat_hip_rasterize_bwd_workspace_size(l.I, l.tw, l.th);
+  const size_t ws_bytes = gsplat_hip_rasterize_bwd_workspace_size(l.I, static_cast<int32_t>(l.channels), l.tw, l.th);
   array ws = at::empty({static_cast<int64_t>(std::max<size_t>(ws_bytes, 1))}, u8_like(means2d));
   check(gsplat_hip_rasterize_bwd(
       means2d.data_ptr<float>(), conics.data_ptr<float>(), colors.data_ptr<float>(), opac.data_ptr<float>(),

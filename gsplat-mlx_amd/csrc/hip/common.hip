@@ -13,11 +13,6 @@ namespace {
 
 thread_local std::string g_last_error;
 
-__global__ void fill_zero_u32(uint32_t* __restrict__ p, int64_t n) {
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = 0u;
-}
-
 __global__ void fill_zero_u8(uint8_t* __restrict__ p, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 0;
@@ -25,19 +20,24 @@ __global__ void fill_zero_u8(uint8_t* __restrict__ p, int64_t n) {
 
 struct ZeroSpans {
   float* ptr[kMaxZeroSpans];
-  int64_t end[kMaxZeroSpans];  // inclusive prefix of counts
-  int n;
+  int64_t count[kMaxZeroSpans];  // floats
 };
 
-__global__ void fill_zero_spans_kernel(ZeroSpans z) {
-  const int64_t total = z.end[z.n - 1];
+// blockIdx.y selects the span; 16-byte stores over its aligned body, plain
+// stores for the unaligned head and the tail.
+__global__ void __launch_bounds__(256) fill_zero_spans_kernel(ZeroSpans z) {
+  float* p = z.ptr[blockIdx.y];
+  const int64_t n = z.count[blockIdx.y];
+  const int64_t head = std::min<int64_t>(n, ((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / 4);
+  const int64_t n4 = (n - head) / 4;
+  const int64_t tail = n - head - 4 * n4;
+  const int t = threadIdx.x;
+  if (blockIdx.x == 0 && t < head) p[t] = 0.0f;
+  if (blockIdx.x == 0 && t < tail) p[head + 4 * n4 + t] = 0.0f;
+  float4* q = reinterpret_cast<float4*>(p + head);
   const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += stride) {
-    int k = 0;
-    while (i >= z.end[k]) ++k;
-    const int64_t start = k == 0 ? 0 : z.end[k - 1];
-    z.ptr[k][i - start] = 0.0f;
-  }
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + t; i < n4; i += stride)
+    q[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 }
 
 struct TimedLaunch {
@@ -102,31 +102,31 @@ int check_launch(const char* what) { return check_hip(hipGetLastError(), what); 
 
 int fill_zero(void* ptr, int64_t bytes, hipStream_t stream) {
   if (bytes <= 0) return GSPLAT_OK;
-  KernelTimer timer("fill_zero", stream);
   if (reinterpret_cast<uintptr_t>(ptr) % 4 == 0 && bytes % 4 == 0) {
-    const int64_t n = bytes / 4;
-    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 65536);
-    fill_zero_u32<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(static_cast<uint32_t*>(ptr), n);
-  } else {
-    fill_zero_u8<<<grid_for(bytes, 256), 256, 0, stream>>>(static_cast<uint8_t*>(ptr), bytes);
+    const ZeroSpan span{static_cast<float*>(ptr), bytes / 4};
+    return fill_zero_spans(&span, 1, stream);
   }
+  KernelTimer timer("fill_zero", stream);
+  fill_zero_u8<<<grid_for(bytes, 256), 256, 0, stream>>>(static_cast<uint8_t*>(ptr), bytes);
   return check_launch("fill_zero");
 }
 
 int fill_zero_spans(const ZeroSpan* spans, int n_spans, hipStream_t stream) {
   ZeroSpans z{};
-  int64_t run = 0;
+  int n = 0;
+  int64_t largest = 0;
   for (int i = 0; i < n_spans && i < kMaxZeroSpans; ++i) {
     if (!spans[i].ptr || spans[i].count <= 0) continue;
-    z.ptr[z.n] = spans[i].ptr;
-    run += spans[i].count;
-    z.end[z.n] = run;
-    ++z.n;
+    z.ptr[n] = spans[i].ptr;
+    z.count[n] = spans[i].count;
+    largest = std::max(largest, spans[i].count);
+    ++n;
   }
-  if (z.n == 0) return GSPLAT_OK;
+  if (n == 0) return GSPLAT_OK;
   KernelTimer timer("fill_zero", stream);
-  const int64_t blocks = std::min<int64_t>((run + 255) / 256, 65536);
-  fill_zero_spans_kernel<<<static_cast<unsigned>(blocks), 256, 0, stream>>>(z);
+  // about four float4 stores per thread on the largest span
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((largest / 4 + 1023) / 1024, 4096));
+  fill_zero_spans_kernel<<<dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(n)), 256, 0, stream>>>(z);
   return check_launch("fill_zero");
 }
 

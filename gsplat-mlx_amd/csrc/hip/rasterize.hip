@@ -1,16 +1,19 @@
 // Tile rasterization (front-to-back alpha compositing) forward / backward for
 // gfx950.
 //
-// One block per (image, tile) with tile_size^2 lanes, one pixel per lane
-// (16x16 tiles -> 4 wave64s, each covering 16x4 pixels). The tile's sorted
-// Gaussian list is walked in batches of blockDim entries: each lane gathers
-// one Gaussian record (mean, conic, opacity, colors) into LDS, then every
-// lane evaluates the whole batch from LDS. Forward stops when every lane of
-// the block has saturated (block vote). Backward walks the same lists
-// back-to-front from the block's largest last_id, rebuilding transmittance
-// per pixel, and reduces each Gaussian's partial gradients across the wave
-// with DPP before one atomic per (wave, Gaussian, component); waves where no
-// lane contributes skip the reduction.
+// Forward: one block per (image, tile) with tile_size^2 lanes, one pixel per
+// lane (16x16 tiles -> 4 wave64s, each covering 16x4 pixels). The tile's
+// sorted Gaussian list is walked in batches of blockDim entries: each lane
+// gathers one Gaussian record (mean, conic, opacity, colors) into LDS and
+// tests it against every wave's pixel rectangle, then each wave evaluates
+// only the records that may touch it. The forward stops when every lane of
+// the block has saturated (block vote).
+//
+// Backward: persistent blocks walk the tiles heaviest first and replay each
+// tile's list back-to-front from its largest last_id, rebuilding
+// transmittance per pixel; per record, a wave sums its lanes' partial
+// gradients by a transposed DPP/permlane reduction into per-wave LDS slots,
+// and each batch ends with one atomic per (record, nonzero component).
 //
 // Per-pixel math follows gsplat_core/gsplat_rasterize.cpp:291-368 (forward)
 // and :432-554 (backward) operation for operation; the Gaussian falloff and
@@ -613,82 +616,135 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
 // (1 - render_alpha) * v_render_colors[c] (gsplat_rasterize.cpp:459-464): a
 // few blocks per image reduce their pixel range, then one atomic per
 // (block, channel).
-constexpr int kBgBlocks = 64;
-
-__global__ void __launch_bounds__(256) background_grad_kernel(RasterArgs a, const float* __restrict__ render_alphas,
-                                                              const float* __restrict__ v_render_colors,
-                                                              float* __restrict__ v_backgrounds) {
-  __shared__ float s_sum[256 / kWave][kMaxChannels];
-  const int64_t image = blockIdx.y;
-  const int64_t n_pix = static_cast<int64_t>(a.W) * a.H;
-  const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
-  const int t = threadIdx.x;
-  const int channels = a.channels;
-  float acc[kMaxChannels];
-  for (int c = 0; c < channels; ++c) acc[c] = 0.0f;
-  for (int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + t; p < n_pix; p += static_cast<int64_t>(gridDim.x) * 256) {
-    const int x = static_cast<int>(p % a.W), y = static_cast<int>(p / a.W);
-    if (a.masks && !a.masks[image * n_tiles + (y / a.ts) * a.tw + x / a.ts]) continue;
-    const int64_t pix = image * n_pix + p;
-    const float T_final = 1.0f - render_alphas[pix];
-    for (int c = 0; c < channels; ++c) acc[c] += T_final * v_render_colors[pix * channels + c];
-  }
-  for (int c = 0; c < channels; ++c) {
-    const float w = wave_sum_uniform(acc[c]);
-    if (t % kWave == 0) s_sum[t / kWave][c] = w;
-  }
-  __syncthreads();
-  if (t < channels) {
-    float sum = 0.0f;
-    for (int w = 0; w < 256 / kWave; ++w) sum += s_sum[w][t];
-    unsafeAtomicAdd(v_backgrounds + image * channels + t, sum);
-  }
-}
-
 // Heavy-first tile schedule for the backward. A tile's cost is the number of
 // list entries its pixels replay (largest last_id - start + 1, 0 when masked
-// or empty). Blocks are dispatched in descending cost order, so the longest
-// tiles start first and the end of the launch is made of short ones (greedy
-// longest-processing-time scheduling over the hardware's dynamic dispatch).
+// or empty). The persistent backward walks the tiles in descending cost
+// order, so the longest tiles start first and the end of the launch is made
+// of short ones (greedy longest-processing-time scheduling).
+//
+// The same pass over the tile's pixels also forms the tile's share of the
+// background gradient, v_backgrounds[c] = sum over unmasked pixels of
+// (1 - render_alpha) * v_render_colors[c] (the background enters each pixel
+// as T_final * bg): one partial per (tile, channel), summed per image by the
+// order kernel's extra blocks. No atomics: every partial has one writer.
 constexpr int kCostBuckets = 4096;  // costs >= 4095 share the heaviest bucket
 
+template <int CH>
 __global__ void __launch_bounds__(256) tile_cost_kernel(RasterArgs a, const int32_t* __restrict__ last_ids,
-                                                        int32_t* __restrict__ cost) {
+                                                        const float* __restrict__ render_alphas,
+                                                        const float* __restrict__ v_render_colors,
+                                                        int32_t* __restrict__ cost, float* __restrict__ bg_part) {
+  constexpr int LC = CH > 0 ? CH : 1;
   __shared__ int s_best[256 / kWave];
+  __shared__ float s_sum[256 / kWave][LC];
   const int tx = blockIdx.x, ty = blockIdx.y;
   const int64_t image = blockIdx.z;
   const int tile = ty * a.tw + tx;
   const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
+  const int64_t unit = image * n_tiles + tile;
   const int t = threadIdx.x;
+  const int channels = CH > 0 ? CH : a.channels;
   int64_t start, end;
   tile_range(a, image, tile, &start, &end);
+  const bool live = !(a.masks && !a.masks[unit]);
   int best = 0;
-  if (!(a.masks && !a.masks[image * n_tiles + tile])) {
+  float acc[LC];
+#pragma unroll
+  for (int c = 0; c < LC; ++c) acc[c] = 0.0f;
+  if (live) {
     for (int q = t; q < a.ts * a.ts; q += 256) {
       const int x = tx * a.ts + q % a.ts;
       const int y = ty * a.ts + q / a.ts;
       if (x >= a.W || y >= a.H) continue;
-      const int64_t last = min<int64_t>(end - 1, last_ids[(image * a.H + y) * static_cast<int64_t>(a.W) + x]);
+      const int64_t pix = (image * a.H + y) * static_cast<int64_t>(a.W) + x;
+      const int64_t last = min<int64_t>(end - 1, last_ids[pix]);
       best = max(best, static_cast<int>(min<int64_t>(max<int64_t>(last - start + 1, 0), INT32_MAX)));
+      if constexpr (CH > 0) {
+        if (bg_part) {
+          const float T_final = 1.0f - render_alphas[pix];
+#pragma unroll
+          for (int c = 0; c < CH; ++c) acc[c] += T_final * v_render_colors[pix * CH + c];
+        }
+      }
     }
   }
 #pragma unroll
   for (int off = 1; off < kWave; off <<= 1) best = max(best, __shfl_xor(best, off, kWave));
   if (t % kWave == 0) s_best[t / kWave] = best;
+  if (bg_part && CH > 0) {
+#pragma unroll
+    for (int c = 0; c < LC; ++c) {
+      const float w = wave_sum_uniform(acc[c]);
+      if (t % kWave == 0) s_sum[t / kWave][c] = w;
+    }
+  }
   __syncthreads();
   if (t == 0) {
     for (int w = 1; w < 256 / kWave; ++w) best = max(best, s_best[w]);
-    cost[image * n_tiles + tile] = best;
+    cost[unit] = best;
+  }
+  if (!bg_part) return;
+  if constexpr (CH > 0) {
+    if (t < CH) {
+      float sum = 0.0f;
+      for (int w = 0; w < 256 / kWave; ++w) sum += s_sum[w][t];
+      bg_part[unit * CH + t] = sum;
+    }
+  } else {
+    // any channel count: one channel at a time
+    for (int c = 0; c < channels; ++c) {
+      float v = 0.0f;
+      if (live) {
+        for (int q = t; q < a.ts * a.ts; q += 256) {
+          const int x = tx * a.ts + q % a.ts;
+          const int y = ty * a.ts + q / a.ts;
+          if (x >= a.W || y >= a.H) continue;
+          const int64_t pix = (image * a.H + y) * static_cast<int64_t>(a.W) + x;
+          v += (1.0f - render_alphas[pix]) * v_render_colors[pix * channels + c];
+        }
+      }
+      const float w = wave_sum_uniform(v);
+      __syncthreads();  // the previous channel's partials have been read
+      if (t % kWave == 0) s_sum[t / kWave][0] = w;
+      __syncthreads();
+      if (t == 0) {
+        float sum = 0.0f;
+        for (int k = 0; k < 256 / kWave; ++k) sum += s_sum[k][0];
+        bg_part[unit * channels + c] = sum;
+      }
+    }
   }
 }
 
-// One block: counting sort of the n tile costs into descending order.
+// Block 0: counting sort of the n tile costs into descending order. Blocks
+// 1 .. I * channels (when bg_part is set): v_backgrounds[i][c] as the sum of
+// image i's per-tile partials of channel c, in tile order (deterministic).
 __global__ void __launch_bounds__(kScanBlock) tile_order_kernel(const int32_t* __restrict__ cost, int64_t n,
-                                                                int32_t* __restrict__ order) {
+                                                                int32_t* __restrict__ order,
+                                                                const float* __restrict__ bg_part, int64_t n_tiles,
+                                                                int channels, float* __restrict__ v_backgrounds) {
   static_assert(kCostBuckets % kScanBlock == 0, "buckets per thread");
   constexpr int PER = kCostBuckets / kScanBlock;
   __shared__ int hist[kCostBuckets];
   const int t = threadIdx.x;
+  if (blockIdx.x > 0) {
+    const int64_t ic = blockIdx.x - 1;  // image * channels + c
+    const int64_t image = ic / channels;
+    const int c = static_cast<int>(ic % channels);
+    const float* part = bg_part + image * n_tiles * channels + c;
+    float v = 0.0f;
+    for (int64_t j = t; j < n_tiles; j += kScanBlock) v += part[j * channels];
+    float* s_sum = reinterpret_cast<float*>(hist);
+    const float w = wave_sum_uniform(v);
+    if (t % kWave == 0) s_sum[t / kWave] = w;
+    __syncthreads();
+    if (t == 0) {
+      float sum = 0.0f;
+      for (int k = 0; k < kScanBlock / kWave; ++k) sum += s_sum[k];
+      v_backgrounds[ic] = sum;
+    }
+    return;
+  }
   for (int i = t; i < kCostBuckets; i += kScanBlock) hist[i] = 0;
   __syncthreads();
   for (int64_t i = t; i < n; i += kScanBlock) atomicAdd(&hist[kCostBuckets - 1 - min(cost[i], kCostBuckets - 1)], 1);
@@ -712,8 +768,11 @@ __global__ void __launch_bounds__(kScanBlock) tile_order_kernel(const int32_t* _
 }
 
 size_t align256(size_t b) { return (b + 255) / 256 * 256; }
-// cost [n] int32, order [n] int32
-size_t bwd_workspace_bytes(int64_t n_tiles_total) { return 2 * align256(static_cast<size_t>(n_tiles_total) * 4); }
+// cost [n] int32, order [n] int32, background partials [n][channels] float
+size_t bwd_workspace_bytes(int64_t n_tiles_total, int channels) {
+  return 2 * align256(static_cast<size_t>(n_tiles_total) * 4) +
+         align256(static_cast<size_t>(n_tiles_total) * channels * 4);
+}
 
 // Resident blocks of `kernel` on the current device (persistent launches).
 int64_t resident_blocks(const void* kernel, int block, size_t smem) {
@@ -832,24 +891,30 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   const int bs = bwd_block(tile_size);
   const int64_t n_total = I * tile_width * static_cast<int64_t>(tile_height);
   if (n_total > INT32_MAX) return invalid("rasterize_to_pixels_3dgs_backward: too many tiles.");
-  if (!workspace || workspace_bytes < bwd_workspace_bytes(n_total)) {
+  if (!workspace || workspace_bytes < bwd_workspace_bytes(n_total, channels)) {
     set_error("rasterize_to_pixels_3dgs_backward: workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
   }
   int32_t* cost = static_cast<int32_t*>(workspace);
   int32_t* order = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align256(n_total * 4));
+  float* bg_part =
+      backgrounds ? reinterpret_cast<float*>(static_cast<char*>(workspace) + 2 * align256(n_total * 4)) : nullptr;
   {
     KernelTimer timer("raster_bwd_schedule", s);
-    tile_cost_kernel<<<grid, 256, 0, s>>>(a, last_ids, cost);
-    tile_order_kernel<<<1, kScanBlock, 0, s>>>(cost, n_total, order);
+    switch (ch) {
+      case 1: tile_cost_kernel<1><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
+      case 2: tile_cost_kernel<2><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
+      case 3: tile_cost_kernel<3><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
+      case 4: tile_cost_kernel<4><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
+      default: tile_cost_kernel<0><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
+    }
+    // block 0 orders the tiles; one more block per (image, channel) sums the background partials
+    const unsigned order_blocks = 1 + (backgrounds ? static_cast<unsigned>(I * channels) : 0u);
+    tile_order_kernel<<<order_blocks, kScanBlock, 0, s>>>(cost, n_total, order, bg_part,
+                                                          tile_width * static_cast<int64_t>(tile_height), channels,
+                                                          v_backgrounds);
   }
   if ((rc = check_launch("rasterize_to_pixels_3dgs_backward"))) return rc;
-  if (backgrounds) {
-    KernelTimer timer("raster_bwd_background", s);
-    background_grad_kernel<<<dim3(kBgBlocks, static_cast<unsigned>(I)), 256, 0, s>>>(a, render_alphas,
-                                                                                       v_render_colors, v_backgrounds);
-    if ((rc = check_launch("rasterize_to_pixels_3dgs_backward"))) return rc;
-  }
   const int bb = bwd_batch(bs);
   const size_t sm = bwd_smem(ch, bs, bb, v_means2d_abs != nullptr);
   KernelTimer timer("raster_bwd", s);
@@ -883,7 +948,8 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   return check_launch("rasterize_to_pixels_3dgs_backward");
 }
 
-extern "C" size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t tile_width, int32_t tile_height) {
-  if (I <= 0 || tile_width <= 0 || tile_height <= 0) return 0;
-  return bwd_workspace_bytes(I * tile_width * static_cast<int64_t>(tile_height));
+extern "C" size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t channels, int32_t tile_width,
+                                                          int32_t tile_height) {
+  if (I <= 0 || tile_width <= 0 || tile_height <= 0 || channels <= 0) return 0;
+  return bwd_workspace_bytes(I * tile_width * static_cast<int64_t>(tile_height), channels);
 }

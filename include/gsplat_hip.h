@@ -256,10 +256,12 @@ int gsplat_hip_rasterize_bwd(const float* means2d, const float* conics, const fl
                              void* workspace, size_t workspace_bytes, void* stream);
 
 /* Bytes of device workspace rasterize_bwd needs for I images of
- * tile_width x tile_height tiles (its heavy-first tile schedule: one cost and
- * one order entry per tile). No counterpart in the reference, whose CPU
- * backward allocates nothing of the kind. */
-size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t tile_width, int32_t tile_height);
+ * tile_width x tile_height tiles and `channels` colour channels (its
+ * heavy-first tile schedule: one cost and one order entry per tile; and one
+ * background-gradient partial per tile and channel). No counterpart in the
+ * reference, whose CPU backward allocates nothing of the kind. */
+size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t channels, int32_t tile_width,
+                                               int32_t tile_height);
 
 #ifdef __cplusplus
 }  /* extern "C" */

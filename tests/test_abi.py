@@ -60,7 +60,8 @@ def test_workspace_sizes(lib):
                        ("gsplat_hip_isect_count_scan_workspace_size", (ctypes.c_int64,)),
                        ("gsplat_hip_exclusive_scan_i32_workspace_size", (ctypes.c_int64,)),
                        ("gsplat_hip_isect_tile_sorted_workspace_size", (ctypes.c_int64, ctypes.c_int64)),
-                       ("gsplat_hip_rasterize_bwd_workspace_size", (ctypes.c_int64, ctypes.c_int32, ctypes.c_int32))):
+                       ("gsplat_hip_rasterize_bwd_workspace_size",
+                        (ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32))):
         f = getattr(lib, name)
         f.restype = ctypes.c_size_t
         f.argtypes = list(args)
@@ -72,8 +73,10 @@ def test_workspace_sizes(lib):
     assert big >= 12 * 5_000_000
     assert lib.gsplat_hip_isect_tile_sorted_workspace_size(1_000_000, 5_400_000) > 12 * 5_400_000
     assert lib.gsplat_hip_isect_tile_sorted_workspace_size(0, 10) == 0
-    assert lib.gsplat_hip_rasterize_bwd_workspace_size(1, 82, 53) >= 2 * 4 * 82 * 53
-    assert lib.gsplat_hip_rasterize_bwd_workspace_size(0, 82, 53) == 0
+    # cost + order per tile, one background partial per tile and channel
+    assert lib.gsplat_hip_rasterize_bwd_workspace_size(1, 3, 82, 53) >= (2 + 3) * 4 * 82 * 53
+    assert lib.gsplat_hip_rasterize_bwd_workspace_size(2, 64, 82, 53) >= 2 * (2 + 64) * 4 * 82 * 53
+    assert lib.gsplat_hip_rasterize_bwd_workspace_size(0, 3, 82, 53) == 0
     assert lib.gsplat_hip_exclusive_scan_i32_workspace_size(1 << 20) > 0
 
 
