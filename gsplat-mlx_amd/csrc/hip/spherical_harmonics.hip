@@ -160,8 +160,8 @@ __global__ void __launch_bounds__(kShBlock) sh_fwd_kernel(const float* __restric
 }
 
 // gsplat_spherical_harmonics.cpp:288-425
-template <int DEG>
-__device__ __forceinline__ void sh_dir_vjp(const float dir[3], const float* co, const float vc[3], float v_dir[3]) {
+template <int DEG, class Co>
+__device__ __forceinline__ void sh_dir_vjp(const float dir[3], const Co& co, const float vc[3], float v_dir[3]) {
   v_dir[0] = v_dir[1] = v_dir[2] = 0.0f;
   if (DEG < 1) return;
   const float norm = sqrtf(dir[0] * dir[0] + dir[1] * dir[1] + dir[2] * dir[2]);
@@ -257,7 +257,7 @@ __device__ __forceinline__ void sh_dir_vjp(const float dir[3], const float* co, 
     dy[24] = 0.6258357354491763f * f_c3_y;
   }
   float vn[3] = {0.0f, 0.0f, 0.0f};
-#pragma unroll
+#pragma clang loop unroll(full)
   for (int b = 1; b < A; ++b) {
     const float vb = co[b * 3] * vc[0] + co[b * 3 + 1] * vc[1] + co[b * 3 + 2] * vc[2];
     vn[0] += dx[b] * vb;
@@ -378,24 +378,25 @@ __device__ __forceinline__ void stage_cols(float* __restrict__ lds, int col0, co
   }
 }
 
-// Colour of coefficient row `co` ([A][3]) at direction d; sh_fwd_kernel's
-// per-channel arithmetic.
-template <int DEG>
-__device__ __forceinline__ void sh_eval(const float d[3], const float* co, float out[3]) {
+// Colour of coefficient row `co` ([A][3]: an LDS pointer or a register
+// array) at direction d; sh_fwd_kernel's per-channel arithmetic. Loops are
+// fully unrolled so a register array is never indexed dynamically.
+template <int DEG, class Co>
+__device__ __forceinline__ void sh_eval(const float d[3], const Co& co, float out[3]) {
   constexpr int A = (DEG + 1) * (DEG + 1);
   float basis[A];
   sh_basis<DEG>(d[0], d[1], d[2], basis);
   const float norm = sqrtf(d[0] * d[0] + d[1] * d[1] + d[2] * d[2]);
-#pragma unroll
+#pragma clang loop unroll(full)
   for (int ch = 0; ch < 3; ++ch) {
     float result = kC0 * co[ch];
     if (DEG >= 1 && norm != 0.0f) {
       const float x = d[0] / norm, y = d[1] / norm, z = d[2] / norm;
       result += kC1 * (-y * co[3 + ch] + z * co[6 + ch] - x * co[9 + ch]);
-#pragma unroll
+#pragma clang loop unroll(full)
       for (int l = 2; l <= DEG; ++l) {
         float band = basis[l * l] * co[l * l * 3 + ch];
-#pragma unroll
+#pragma clang loop unroll(full)
         for (int b = l * l + 1; b < (l + 1) * (l + 1); ++b) band += basis[b] * co[b * 3 + ch];
         result += band;
       }
@@ -416,6 +417,21 @@ __device__ __forceinline__ float view_dir(const float* __restrict__ m, const flo
   n[1] = d[1] / sc;
   n[2] = d[2] / sc;
   return norm;
+}
+
+// Adds the gradient through n = d / max(|d|, 1e-8) of v_n to v_d (the
+// gradient of the means).
+__device__ __forceinline__ void view_dir_vjp(const float vn[3], const float n[3], float norm, float vd[3]) {
+  if (norm >= 1.0e-8f) {
+    const float dot = vn[0] * n[0] + vn[1] * n[1] + vn[2] * n[2];
+    vd[0] += (vn[0] - n[0] * dot) / norm;
+    vd[1] += (vn[1] - n[1] * dot) / norm;
+    vd[2] += (vn[2] - n[2] * dot) / norm;
+  } else {
+    vd[0] += vn[0] / 1.0e-8f;
+    vd[1] += vn[1] / 1.0e-8f;
+    vd[2] += vn[2] / 1.0e-8f;
+  }
 }
 
 __device__ __forceinline__ float clamp01(float x) { return x < 0.0f ? 0.0f : (x > 1.0f ? 1.0f : x); }
@@ -513,17 +529,7 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_bwd_kernel(const float* __res
       if constexpr (DEG >= 1) {
         float vn[3];
         sh_dir_vjp<DEG>(n, co, gcol, vn);
-        // through n = d / max(|d|, 1e-8)
-        if (norm >= 1.0e-8f) {
-          const float dot = vn[0] * n[0] + vn[1] * n[1] + vn[2] * n[2];
-          vm[0] += (vn[0] - n[0] * dot) / norm;
-          vm[1] += (vn[1] - n[1] * dot) / norm;
-          vm[2] += (vn[2] - n[2] * dot) / norm;
-        } else {
-          vm[0] += vn[0] / 1.0e-8f;
-          vm[1] += vn[1] / 1.0e-8f;
-          vm[2] += vn[2] / 1.0e-8f;
-        }
+        view_dir_vjp(vn, n, norm, vm);
       }
     }
     v_means[g * 3] = vm[0];
@@ -559,14 +565,182 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_bwd_kernel(const float* __res
   }
 }
 
+// Slab variant of the camera kernels for the common layout where
+// features_rest holds exactly the active bases (R == (degree+1)^2 - 1) and
+// the row length R*3 is odd (degrees 0, 1 and 3). The block's rows of rest,
+// dc and means are each one contiguous span, copied into LDS unchanged with
+// 16-byte loads (no index split); the
+// odd row stride keeps a lane-per-row LDS read conflict-free. Each lane then
+// holds its Gaussian's coefficients in registers for every camera. Same
+// arithmetic as sh_cam_fwd_kernel / sh_cam_bwd_kernel, so results are
+// identical.
+constexpr int kShSlab = 256;
+
+template <int W>
+__device__ __forceinline__ void stage_slab(float* __restrict__ dst, const float* __restrict__ src, int cnt) {
+  if (cnt == kShSlab && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    static_assert((kShSlab * W) % 4 == 0, "whole float4s per slab");
+    constexpr int T4 = kShSlab * W / 4;
+    constexpr int PER = (T4 + kShSlab - 1) / kShSlab;
+    const float4* s4 = reinterpret_cast<const float4*>(src);
+    float4* d4 = reinterpret_cast<float4*>(dst);
+    // global and LDS do not alias: the compiler hoists every load above the stores
+#pragma clang loop unroll(full)
+    for (int i = 0; i < PER; ++i) {
+      const int idx = threadIdx.x + i * kShSlab;
+      if (idx < T4) d4[idx] = s4[idx];
+    }
+  } else {
+    for (int idx = threadIdx.x; idx < cnt * W; idx += kShSlab) dst[idx] = src[idx];
+  }
+}
+
+// Stages the block's slabs and loads lane t's row [dc, rest] into co.
+template <int DEG>
+__device__ __forceinline__ void slab_rows(const float* __restrict__ means, const float* __restrict__ dc,
+                                          const float* __restrict__ rest, int64_t row0, int cnt, float* s_rest,
+                                          float* s_dc, float* s_m, float (&co)[(DEG + 1) * (DEG + 1) * 3],
+                                          float (&m)[3]) {
+  constexpr int R3 = ((DEG + 1) * (DEG + 1) - 1) * 3;
+  if constexpr (R3 > 0) stage_slab<R3>(s_rest, rest + row0 * R3, cnt);
+  stage_slab<3>(s_dc, dc + row0 * 3, cnt);
+  stage_slab<3>(s_m, means + row0 * 3, cnt);
+  __syncthreads();
+  const int t = threadIdx.x;
+  if (t >= cnt) return;
+  co[0] = s_dc[t * 3];
+  co[1] = s_dc[t * 3 + 1];
+  co[2] = s_dc[t * 3 + 2];
+#pragma clang loop unroll(full)
+  for (int i = 0; i < R3; ++i) co[3 + i] = s_rest[t * R3 + i];
+  m[0] = s_m[t * 3];
+  m[1] = s_m[t * 3 + 1];
+  m[2] = s_m[t * 3 + 2];
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* __restrict__ means,
+                                                                  const float* __restrict__ campos,
+                                                                  const float* __restrict__ dc,
+                                                                  const float* __restrict__ rest, int64_t C,
+                                                                  int64_t N, float* __restrict__ colors) {
+  constexpr int A = (DEG + 1) * (DEG + 1);
+  constexpr int R3 = (A - 1) * 3;
+  __shared__ __align__(16) float s_rest[R3 > 0 ? kShSlab * R3 : 4];
+  __shared__ __align__(16) float s_dc[kShSlab * 3];
+  __shared__ __align__(16) float s_m[kShSlab * 3];
+  const int64_t b = blockIdx.y;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShSlab;
+  const int cnt = static_cast<int>(min<int64_t>(kShSlab, N - e0));
+  const int t = threadIdx.x;
+  float co[A * 3], m[3];
+  slab_rows<DEG>(means, dc, rest, b * N + e0, cnt, s_rest, s_dc, s_m, co, m);
+  if (t >= cnt) return;
+  for (int64_t c = 0; c < C; ++c) {
+    const float cp[3] = {campos[(b * C + c) * 3], campos[(b * C + c) * 3 + 1], campos[(b * C + c) * 3 + 2]};
+    float d[3], n[3], raw[3];
+    view_dir(m, cp, d, n);
+    sh_eval<DEG>(n, co, raw);
+    float* out = colors + ((b * C + c) * N + e0 + t) * 3;
+    out[0] = clamp01(raw[0] + 0.5f);
+    out[1] = clamp01(raw[1] + 0.5f);
+    out[2] = clamp01(raw[2] + 0.5f);
+  }
+}
+
+template <int DEG>
+__global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
+    const float* __restrict__ means, const float* __restrict__ campos, const float* __restrict__ dc,
+    const float* __restrict__ rest, const float* __restrict__ v_colors, int64_t C, int64_t N,
+    float* __restrict__ v_means, float* __restrict__ v_dc, float* __restrict__ v_rest) {
+  constexpr int A = (DEG + 1) * (DEG + 1);
+  constexpr int R3 = (A - 1) * 3;
+  __shared__ __align__(16) float s_rest[R3 > 0 ? kShSlab * R3 : 4];
+  __shared__ __align__(16) float s_dc[kShSlab * 3];
+  __shared__ __align__(16) float s_m[kShSlab * 3];
+  const int64_t b = blockIdx.y;
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShSlab;
+  const int cnt = static_cast<int>(min<int64_t>(kShSlab, N - e0));
+  const int t = threadIdx.x;
+  float co[A * 3], m[3];
+  slab_rows<DEG>(means, dc, rest, b * N + e0, cnt, s_rest, s_dc, s_m, co, m);
+  if (t < cnt) {
+    const int64_t g = b * N + e0 + t;
+    float vco[A * 3];
+#pragma clang loop unroll(full)
+    for (int i = 0; i < A * 3; ++i) vco[i] = 0.0f;
+    float vm[3] = {0.0f, 0.0f, 0.0f};
+    for (int64_t c = 0; c < C; ++c) {
+      const float cp[3] = {campos[(b * C + c) * 3], campos[(b * C + c) * 3 + 1], campos[(b * C + c) * 3 + 2]};
+      float d[3], n[3], raw[3];
+      const float norm = view_dir(m, cp, d, n);
+      sh_eval<DEG>(n, co, raw);
+      const float* vc = v_colors + ((b * C + c) * N + e0 + t) * 3;
+      float gcol[3];
+#pragma clang loop unroll(full)
+      for (int ch = 0; ch < 3; ++ch) {
+        const float x = raw[ch] + 0.5f;
+        gcol[ch] = (x >= 0.0f && x <= 1.0f) ? vc[ch] : 0.0f;
+      }
+      float basis[A];
+      sh_basis<DEG>(n[0], n[1], n[2], basis);
+#pragma clang loop unroll(full)
+      for (int k = 0; k < A; ++k) {
+        vco[k * 3] += basis[k] * gcol[0];
+        vco[k * 3 + 1] += basis[k] * gcol[1];
+        vco[k * 3 + 2] += basis[k] * gcol[2];
+      }
+      if constexpr (DEG >= 1) {
+        float vn[3];
+        sh_dir_vjp<DEG>(n, co, gcol, vn);
+        view_dir_vjp(vn, n, norm, vm);
+      }
+    }
+    v_means[g * 3] = vm[0];
+    v_means[g * 3 + 1] = vm[1];
+    v_means[g * 3 + 2] = vm[2];
+    v_dc[g * 3] = vco[0];
+    v_dc[g * 3 + 1] = vco[1];
+    v_dc[g * 3 + 2] = vco[2];
+    // this lane's staged row is no longer read: reuse it for the gradient row
+#pragma clang loop unroll(full)
+    for (int i = 0; i < R3; ++i) s_rest[t * R3 + i] = vco[3 + i];
+  }
+  if constexpr (R3 > 0) {
+    __syncthreads();
+    float* out = v_rest + (b * N + e0) * R3;
+    if (cnt == kShSlab && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+      float4* o4 = reinterpret_cast<float4*>(out);
+      const float4* s4 = reinterpret_cast<const float4*>(s_rest);
+      for (int idx = t; idx < kShSlab * R3 / 4; idx += kShSlab) o4[idx] = s4[idx];
+    } else {
+      for (int idx = t; idx < cnt * R3; idx += kShSlab) out[idx] = s_rest[idx];
+    }
+  }
+}
+
+// The slab kernels need rest rows of exactly the active bases with an odd
+// float count (degrees 0, 1, 3); other layouts take the general kernels.
+constexpr bool slab_degree(int deg) { return deg == 0 || deg == 1 || deg == 3; }
+
 template <int DEG>
 int launch_cam_fwd(const float* means, const float* campos, const float* dc, const float* rest, int64_t B, int64_t C,
                    int64_t N, int64_t R, float* colors, hipStream_t s) {
   {
     KernelTimer timer("sh_camera_fwd", s);
-    const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
-    sh_cam_fwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, campos, dc, rest, C, N, R,
-                                                      magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), colors);
+    bool slab = false;
+    if constexpr (slab_degree(DEG)) {
+      if (R == (DEG + 1) * (DEG + 1) - 1) {
+        const dim3 grid(grid_for(N, kShSlab), static_cast<unsigned>(B));
+        sh_cam_fwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, campos, dc, rest, C, N, colors);
+        slab = true;
+      }
+    }
+    if (!slab) {
+      const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
+      sh_cam_fwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, campos, dc, rest, C, N, R,
+                                                        magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), colors);
+    }
   }
   return check_launch("sh_camera_colors_forward");
 }
@@ -577,10 +751,21 @@ int launch_cam_bwd(const float* means, const float* campos, const float* dc, con
                    hipStream_t s) {
   {
     KernelTimer timer("sh_camera_bwd", s);
-    const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
-    sh_cam_bwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, campos, dc, rest, v_colors, C, N, R,
-                                                      magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), v_means,
-                                                      v_dc, v_rest);
+    bool slab = false;
+    if constexpr (slab_degree(DEG)) {
+      if (R == (DEG + 1) * (DEG + 1) - 1) {
+        const dim3 grid(grid_for(N, kShSlab), static_cast<unsigned>(B));
+        sh_cam_bwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, campos, dc, rest, v_colors, C, N, v_means, v_dc,
+                                                              v_rest);
+        slab = true;
+      }
+    }
+    if (!slab) {
+      const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
+      sh_cam_bwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, campos, dc, rest, v_colors, C, N, R,
+                                                        magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), v_means,
+                                                        v_dc, v_rest);
+    }
   }
   return check_launch("sh_camera_colors_backward");
 }

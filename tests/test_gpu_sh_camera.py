@@ -71,8 +71,11 @@ def _oracle_backward(oracle, degree, means, campos, coeffs, raw, dirs, norms, v_
     return v_means, v_dc, v_rest
 
 
+# R == (degree+1)^2 - 1 with degree 0, 1, 3 takes the slab kernels (B = 2
+# with N = 3001 also exercises their unaligned path); the rest the general ones
 @pytest.mark.parametrize("degree,B,C,R", [(0, 1, 1, 0), (1, 1, 2, 3), (2, 2, 1, 15), (3, 1, 1, 15),
-                                          (3, 2, 3, 15), (4, 1, 2, 24)])
+                                          (3, 2, 3, 15), (4, 1, 2, 24), (0, 1, 2, 15), (1, 2, 1, 15),
+                                          (2, 1, 1, 8)])
 def test_fused_vs_oracle(oracle, degree, B, C, R):
     g = gsplat()
     rng = np.random.default_rng(degree * 100 + C * 10 + R)
