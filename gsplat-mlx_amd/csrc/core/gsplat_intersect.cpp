@@ -8,6 +8,7 @@
 
 #include <cmath>
 #include <limits>
+#include <map>
 
 #include "core_util.h"
 
@@ -87,18 +88,58 @@ Counted count_and_scan(const IntersectTileInput& input, void* stream) {
 }
 
 // The one device->host read of the chain (gsplat_intersect.cpp:155-170),
-// ordered after the count/scan kernels on their stream.
-int read_total(const array& total_dev, void* stream) {
-  int64_t total = 0;
+// ordered after the count/scan kernels on their stream. It is split in two so
+// that work which does not need the count can be queued between the copy and
+// the wait: the copy lands in a pinned host word and an event marks it, so
+// the wait ends when the copy is done rather than when the stream drains.
+struct CountReadback {
+  int64_t* host = nullptr;
+  hipEvent_t done = nullptr;
+};
+
+CountReadback& readback_slot() {
+  // one slot per host thread and device; the call that starts a read-back
+  // also finishes it before returning
+  thread_local std::map<int, CountReadback> slots;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) throw std::runtime_error("intersect_tile: no current HIP device.");
+  CountReadback& r = slots[dev];
+  if (!r.host) {
+    void* p = nullptr;
+    if (hipHostMalloc(&p, sizeof(int64_t), hipHostMallocDefault) != hipSuccess)
+      throw std::runtime_error("intersect_tile: pinned host allocation for the count failed.");
+    r.host = static_cast<int64_t*>(p);
+  }
+  if (!r.done && hipEventCreateWithFlags(&r.done, hipEventDisableTiming) != hipSuccess)
+    throw std::runtime_error("intersect_tile: event creation failed.");
+  return r;
+}
+
+void start_read_total(const array& total_dev, void* stream, CountReadback& r) {
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t err = hipMemcpyAsync(&total, total_dev.data_ptr<int64_t>(), sizeof(int64_t), hipMemcpyDeviceToHost, s);
-  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  hipError_t err =
+      hipMemcpyAsync(r.host, total_dev.data_ptr<int64_t>(), sizeof(int64_t), hipMemcpyDeviceToHost, s);
+  if (err == hipSuccess) err = hipEventRecord(r.done, s);
   if (err != hipSuccess)
     throw std::runtime_error(std::string("intersect_tile: reading the intersection count failed: ") +
                              hipGetErrorString(err));
+}
+
+int finish_read_total(CountReadback& r) {
+  const hipError_t err = hipEventSynchronize(r.done);
+  if (err != hipSuccess)
+    throw std::runtime_error(std::string("intersect_tile: reading the intersection count failed: ") +
+                             hipGetErrorString(err));
+  const int64_t total = *r.host;
   if (total > static_cast<int64_t>(INT32_MAX))
     throw std::runtime_error("intersect_tile: more than 2^31-1 intersections (int32 offsets overflow).");
   return static_cast<int>(total);
+}
+
+int read_total(const array& total_dev, void* stream) {
+  CountReadback& r = readback_slot();
+  start_read_total(total_dev, stream, r);
+  return finish_read_total(r);
 }
 
 std::vector<array> sort_pairs(const array& keys, const array& vals, int key_bits, void* stream) {
@@ -208,25 +249,39 @@ std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& in
   const c10::DeviceGuard guard(input.means2d.device());
   void* stream = stream_for(input.s, input.means2d);
   Counted c = count_and_scan(input, stream);
-  const int total = read_total(c.total, stream);
   const array means2d = contig(input.means2d);
   const array radii = contig(input.radii);
   const array depths = contig(input.depths);
-  array ids = at::empty({total}, i64_like(means2d));
-  array flat = at::empty({total}, i32_like(means2d));
   if (input.params.sort) {
     // depth-presorted encode + 32-bit key sort; same result as encode
-    // followed by the stable 64-bit key sort
-    const size_t ws_bytes = gsplat_hip_isect_tile_sorted_workspace_size(depths.numel(), total);
-    array ws = workspace(ws_bytes, means2d);
-    check(gsplat_hip_isect_tile_sorted(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(),
-                                       depths.data_ptr<float>(), c.tiles_per_gauss.data_ptr<int32_t>(),
-                                       input.params.I, depths.numel(), input.params.tile_size,
-                                       input.params.tile_width, input.params.tile_height, total,
-                                       ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), ws.data_ptr<uint8_t>(),
-                                       ws_bytes, stream));
+    // followed by the stable 64-bit key sort. The depth order needs only the
+    // counts, so it is queued before waiting for their total.
+    CountReadback& r = readback_slot();
+    start_read_total(c.total, stream, r);
+    const int64_t numel = depths.numel();
+    array perm = at::empty({numel}, i32_like(means2d));
+    array offs = at::empty({numel}, i32_like(means2d));
+    const size_t ws1_bytes = gsplat_hip_isect_depth_order_workspace_size(numel);
+    array ws1 = workspace(ws1_bytes, means2d);
+    check(gsplat_hip_isect_depth_order(depths.data_ptr<float>(), c.tiles_per_gauss.data_ptr<int32_t>(), numel,
+                                       perm.data_ptr<int32_t>(), offs.data_ptr<int32_t>(), ws1.data_ptr<uint8_t>(),
+                                       ws1_bytes, stream));
+    const int total = finish_read_total(r);
+    array ids = at::empty({total}, i64_like(means2d));
+    array flat = at::empty({total}, i32_like(means2d));
+    const size_t ws2_bytes = gsplat_hip_isect_encode_sorted_workspace_size(total);
+    array ws2 = workspace(ws2_bytes, means2d);
+    check(gsplat_hip_isect_encode_sorted(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(),
+                                         depths.data_ptr<float>(), perm.data_ptr<int32_t>(),
+                                         offs.data_ptr<int32_t>(), input.params.I, numel, input.params.tile_size,
+                                         input.params.tile_width, input.params.tile_height, total,
+                                         ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), ws2.data_ptr<uint8_t>(),
+                                         ws2_bytes, stream));
     return {c.tiles_per_gauss, ids, flat};
   }
+  const int total = read_total(c.total, stream);
+  array ids = at::empty({total}, i64_like(means2d));
+  array flat = at::empty({total}, i32_like(means2d));
   check(gsplat_hip_isect_encode(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), depths.data_ptr<float>(),
                                 c.offsets.data_ptr<int32_t>(), input.params.I, depths.numel(),
                                 input.params.tile_size, input.params.tile_width, input.params.tile_height, total,

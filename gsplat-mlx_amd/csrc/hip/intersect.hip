@@ -245,43 +245,71 @@ __global__ void __launch_bounds__(256) assemble_ids_kernel(const uint32_t* __res
   isect_ids[i] = static_cast<int64_t>((static_cast<uint64_t>(keys[i]) << 32) | __float_as_uint(depths[flat[i]]));
 }
 
-struct PresortLayout {
+// floor(log2(n)) + 1 with the reference's float log2 (gsplat_intersect.cpp:60-65).
+int floor_log2_plus_one(int64_t value) {
+  return static_cast<int>(std::floor(std::log2(static_cast<float>(value)))) + 1;
+}
+
+inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+// Steps 1-2 (depth order of the pairs and the scanned counts in that order):
+// workspace [dkeys | didx | dkeys_sorted | sort | scan] over numel pairs.
+struct DepthOrderLayout {
   uint32_t* dkeys;
   int32_t* didx;
   uint32_t* dkeys_sorted;
-  int32_t* perm;
-  int32_t* offs;
-  uint32_t* tkeys;
-  int32_t* tvals;
-  uint32_t* tkeys_sorted;
   void* sort_ws;
   size_t sort_ws_bytes;
   void* scan_ws;
 };
 
-inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
-
-size_t presort_layout(int64_t numel, int64_t n_isects, PresortLayout* l, void* base) {
+size_t depth_order_layout(int64_t numel, DepthOrderLayout* l, void* base) {
   const size_t pn = align256(static_cast<size_t>(numel) * 4);
-  const size_t pm = align256(static_cast<size_t>(n_isects) * 4);
-  const size_t sort_b =
-      align256(std::max(radix_sort_workspace_bytes<uint32_t>(numel), radix_sort_workspace_bytes<uint32_t>(n_isects)));
+  const size_t sort_b = align256(radix_sort_workspace_bytes<uint32_t>(numel));
   const size_t scan_b = align256(scan_workspace_bytes(numel));
   if (l && base) {
     char* p = static_cast<char*>(base);
     l->dkeys = reinterpret_cast<uint32_t*>(p);
     l->didx = reinterpret_cast<int32_t*>(p + pn);
     l->dkeys_sorted = reinterpret_cast<uint32_t*>(p + 2 * pn);
-    l->perm = reinterpret_cast<int32_t*>(p + 3 * pn);
-    l->offs = reinterpret_cast<int32_t*>(p + 4 * pn);
-    l->tkeys = reinterpret_cast<uint32_t*>(p + 5 * pn);
-    l->tvals = reinterpret_cast<int32_t*>(p + 5 * pn + pm);
-    l->tkeys_sorted = reinterpret_cast<uint32_t*>(p + 5 * pn + 2 * pm);
-    l->sort_ws = p + 5 * pn + 3 * pm;
+    l->sort_ws = p + 3 * pn;
     l->sort_ws_bytes = sort_b;
-    l->scan_ws = p + 5 * pn + 3 * pm + sort_b;
+    l->scan_ws = p + 3 * pn + sort_b;
   }
-  return 5 * pn + 3 * pm + sort_b + scan_b;
+  return 3 * pn + sort_b + scan_b;
+}
+
+// Steps 3-5 (encode in depth order, sort by (image, tile), rebuild keys):
+// workspace [tkeys | tvals | tkeys_sorted | sort] over n_isects entries.
+struct EncodeSortedLayout {
+  uint32_t* tkeys;
+  int32_t* tvals;
+  uint32_t* tkeys_sorted;
+  void* sort_ws;
+  size_t sort_ws_bytes;
+};
+
+size_t encode_sorted_layout(int64_t n_isects, EncodeSortedLayout* l, void* base) {
+  const size_t pm = align256(static_cast<size_t>(n_isects) * 4);
+  const size_t sort_b = align256(radix_sort_workspace_bytes<uint32_t>(n_isects));
+  if (l && base) {
+    char* p = static_cast<char*>(base);
+    l->tkeys = reinterpret_cast<uint32_t*>(p);
+    l->tvals = reinterpret_cast<int32_t*>(p + pm);
+    l->tkeys_sorted = reinterpret_cast<uint32_t*>(p + 2 * pm);
+    l->sort_ws = p + 3 * pm;
+    l->sort_ws_bytes = sort_b;
+  }
+  return 3 * pm + sort_b;
+}
+
+int check_tile_bits(int64_t I, int32_t tile_width, int32_t tile_height, int* tile_bits, int* image_bits) {
+  const int64_t n_tiles = static_cast<int64_t>(tile_width) * tile_height;
+  *tile_bits = floor_log2_plus_one(n_tiles);
+  *image_bits = floor_log2_plus_one(I);
+  if (*image_bits + *tile_bits > 32)
+    return invalid("intersect_tile_encode image id and tile id require more than 32 bits.");
+  return GSPLAT_OK;
 }
 
 // Tile offsets as lower_bound over sorted keys (gsplat_intersect.cpp:605-641),
@@ -310,11 +338,6 @@ __global__ void __launch_bounds__(256) offsets_kernel(const int64_t* __restrict_
 __global__ void fill_i32_kernel(int32_t* __restrict__ out, int64_t n, int32_t value) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < n) out[i] = value;
-}
-
-// floor(log2(n)) + 1 with the reference's float log2 (gsplat_intersect.cpp:60-65).
-int floor_log2_plus_one(int64_t value) {
-  return static_cast<int>(std::floor(std::log2(static_cast<float>(value)))) + 1;
 }
 
 }  // namespace
@@ -412,32 +435,21 @@ extern "C" int gsplat_hip_isect_offset(const int64_t* isect_ids, int64_t n_isect
   return check_launch("intersect_offset");
 }
 
-extern "C" size_t gsplat_hip_isect_tile_sorted_workspace_size(int64_t numel, int64_t n_isects) {
-  if (numel <= 0 || n_isects <= 0) return 0;
-  return presort_layout(numel, n_isects, nullptr, nullptr);
+extern "C" size_t gsplat_hip_isect_depth_order_workspace_size(int64_t numel) {
+  if (numel <= 0) return 0;
+  return depth_order_layout(numel, nullptr, nullptr);
 }
 
-extern "C" int gsplat_hip_isect_tile_sorted(const float* means2d, const int32_t* radii, const float* depths,
-                                            const int32_t* tiles_per_gauss, int64_t I, int64_t numel,
-                                            int32_t tile_size, int32_t tile_width, int32_t tile_height,
-                                            int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
-                                            void* workspace, size_t workspace_bytes, void* stream) {
+extern "C" int gsplat_hip_isect_depth_order(const float* depths, const int32_t* tiles_per_gauss, int64_t numel,
+                                            int32_t* perm, int32_t* offsets, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
   const char* what = "intersect_tile";
-  if (I <= 0 || numel < 0 || numel % I != 0)
-    return invalid("intersect_tile dense path expects depths size to equal I * N.");
-  if (tile_size <= 0 || tile_width <= 0 || tile_height <= 0) return invalid("intersect_tile: invalid tiles.");
-  if (n_isects < 0) return invalid("intersect_tile: negative intersection count.");
-  if (numel > INT32_MAX || n_isects > INT32_MAX) return invalid("intersect_tile: more than 2^31-1 entries.");
-  const int64_t n_tiles = static_cast<int64_t>(tile_width) * tile_height;
-  const int tile_bits = floor_log2_plus_one(n_tiles);
-  const int image_bits = floor_log2_plus_one(I);
-  if (image_bits + tile_bits > 32)
-    return invalid("intersect_tile_encode image id and tile id require more than 32 bits.");
-  if (numel == 0 || n_isects == 0) return GSPLAT_OK;
-  if (!means2d || !radii || !depths || !tiles_per_gauss || !isect_ids || !flatten_ids)
-    return invalid("intersect_tile: null pointer.");
-  PresortLayout l;
-  if (!workspace || workspace_bytes < presort_layout(numel, n_isects, &l, workspace)) {
+  if (numel < 0) return invalid("intersect_tile: negative size.");
+  if (numel > INT32_MAX) return invalid("intersect_tile: more than 2^31-1 entries.");
+  if (numel == 0) return GSPLAT_OK;
+  if (!depths || !tiles_per_gauss || !perm || !offsets) return invalid("intersect_tile: null pointer.");
+  DepthOrderLayout l;
+  if (!workspace || workspace_bytes < depth_order_layout(numel, &l, workspace)) {
     set_error("intersect_tile: workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
   }
@@ -448,20 +460,49 @@ extern "C" int gsplat_hip_isect_tile_sorted(const float* means2d, const int32_t*
     depth_keys_kernel<<<grid_for(numel, 256), 256, 0, s>>>(depths, numel, l.dkeys, l.didx);
   }
   if ((rc = check_launch(what))) return rc;
-  if ((rc = radix_sort_pairs<uint32_t>(l.dkeys, l.didx, numel, 0, 32, l.dkeys_sorted, l.perm, l.sort_ws,
+  if ((rc = radix_sort_pairs<uint32_t>(l.dkeys, l.didx, numel, 0, 32, l.dkeys_sorted, perm, l.sort_ws,
                                        l.sort_ws_bytes, s, what)))
     return rc;
   {
     KernelTimer timer("isect_gather_counts", s);
-    gather_counts_kernel<<<grid_for(numel, 256), 256, 0, s>>>(tiles_per_gauss, l.perm, numel, l.offs);
+    gather_counts_kernel<<<grid_for(numel, 256), 256, 0, s>>>(tiles_per_gauss, perm, numel, offsets);
   }
   if ((rc = check_launch(what))) return rc;
-  if ((rc = scan_exclusive_i32(l.offs, l.offs, numel, nullptr, l.scan_ws, s))) return rc;
+  return scan_exclusive_i32(offsets, offsets, numel, nullptr, l.scan_ws, s);
+}
+
+extern "C" size_t gsplat_hip_isect_encode_sorted_workspace_size(int64_t n_isects) {
+  if (n_isects <= 0) return 0;
+  return encode_sorted_layout(n_isects, nullptr, nullptr);
+}
+
+extern "C" int gsplat_hip_isect_encode_sorted(const float* means2d, const int32_t* radii, const float* depths,
+                                              const int32_t* perm, const int32_t* offsets, int64_t I, int64_t numel,
+                                              int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                              int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
+                                              void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "intersect_tile";
+  if (I <= 0 || numel < 0 || numel % I != 0)
+    return invalid("intersect_tile dense path expects depths size to equal I * N.");
+  if (tile_size <= 0 || tile_width <= 0 || tile_height <= 0) return invalid("intersect_tile: invalid tiles.");
+  if (n_isects < 0) return invalid("intersect_tile: negative intersection count.");
+  if (numel > INT32_MAX || n_isects > INT32_MAX) return invalid("intersect_tile: more than 2^31-1 entries.");
+  int tile_bits, image_bits, rc;
+  if ((rc = check_tile_bits(I, tile_width, tile_height, &tile_bits, &image_bits))) return rc;
+  if (numel == 0 || n_isects == 0) return GSPLAT_OK;
+  if (!means2d || !radii || !depths || !perm || !offsets || !isect_ids || !flatten_ids)
+    return invalid("intersect_tile: null pointer.");
+  EncodeSortedLayout l;
+  if (!workspace || workspace_bytes < encode_sorted_layout(n_isects, &l, workspace)) {
+    set_error("intersect_tile: workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  hipStream_t s = as_stream(stream);
   {
     KernelTimer timer("isect_encode", s);
     const int64_t nb = (numel + kEncodeG - 1) / kEncodeG;
     encode_presorted_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
-        means2d, radii, l.perm, l.offs, numel, numel / I, tile_size, tile_width, tile_height, tile_bits, n_isects,
+        means2d, radii, perm, offsets, numel, numel / I, tile_size, tile_width, tile_height, tile_bits, n_isects,
         l.tkeys, l.tvals);
   }
   if ((rc = check_launch(what))) return rc;
@@ -474,4 +515,52 @@ extern "C" int gsplat_hip_isect_tile_sorted(const float* means2d, const int32_t*
                                                                 isect_ids);
   }
   return check_launch(what);
+}
+
+// One call: [perm | offsets | shared phase workspace] (the two phases run in
+// stream order, so their scratch overlaps).
+static size_t tile_sorted_layout(int64_t numel, int64_t n_isects, int32_t** perm, int32_t** offs, void** phase,
+                                 void* base) {
+  const size_t pn = align256(static_cast<size_t>(numel) * 4);
+  if (base) {
+    char* p = static_cast<char*>(base);
+    *perm = reinterpret_cast<int32_t*>(p);
+    *offs = reinterpret_cast<int32_t*>(p + pn);
+    *phase = p + 2 * pn;
+  }
+  return 2 * pn + std::max(depth_order_layout(numel, nullptr, nullptr), encode_sorted_layout(n_isects, nullptr, nullptr));
+}
+
+extern "C" size_t gsplat_hip_isect_tile_sorted_workspace_size(int64_t numel, int64_t n_isects) {
+  if (numel <= 0 || n_isects <= 0) return 0;
+  return tile_sorted_layout(numel, n_isects, nullptr, nullptr, nullptr, nullptr);
+}
+
+extern "C" int gsplat_hip_isect_tile_sorted(const float* means2d, const int32_t* radii, const float* depths,
+                                            const int32_t* tiles_per_gauss, int64_t I, int64_t numel,
+                                            int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                            int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
+                                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (I <= 0 || numel < 0 || numel % I != 0)
+    return invalid("intersect_tile dense path expects depths size to equal I * N.");
+  if (tile_size <= 0 || tile_width <= 0 || tile_height <= 0) return invalid("intersect_tile: invalid tiles.");
+  if (n_isects < 0) return invalid("intersect_tile: negative intersection count.");
+  if (numel > INT32_MAX || n_isects > INT32_MAX) return invalid("intersect_tile: more than 2^31-1 entries.");
+  int tile_bits, image_bits, rc;
+  if ((rc = check_tile_bits(I, tile_width, tile_height, &tile_bits, &image_bits))) return rc;
+  if (numel == 0 || n_isects == 0) return GSPLAT_OK;
+  if (!means2d || !radii || !depths || !tiles_per_gauss || !isect_ids || !flatten_ids)
+    return invalid("intersect_tile: null pointer.");
+  int32_t *perm = nullptr, *offs = nullptr;
+  void* phase = nullptr;
+  const size_t need = tile_sorted_layout(numel, n_isects, &perm, &offs, &phase, workspace);
+  if (!workspace || workspace_bytes < need) {
+    set_error("intersect_tile: workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  const size_t phase_bytes = workspace_bytes - (static_cast<char*>(phase) - static_cast<char*>(workspace));
+  if ((rc = gsplat_hip_isect_depth_order(depths, tiles_per_gauss, numel, perm, offs, phase, phase_bytes, stream)))
+    return rc;
+  return gsplat_hip_isect_encode_sorted(means2d, radii, depths, perm, offs, I, numel, tile_size, tile_width,
+                                        tile_height, n_isects, isect_ids, flatten_ids, phase, phase_bytes, stream);
 }

@@ -53,6 +53,21 @@ def sh_colors_for_camera_unfused(means, features_dc, features_rest, viewmats, sh
     return torch.clamp((colors + 0.5).reshape(*dirs.shape[:-1], 3), 0.0, 1.0)
 
 
+_BACKGROUNDS: dict = {}
+
+
+def background_tensor(background, device) -> torch.Tensor:
+    """[1, 3] background colour on `device`, made once per (colour, device):
+    building it from a Python list each call is a host-to-device copy that
+    waits for the stream to drain."""
+    key = (tuple(float(c) for c in background), str(device))
+    bg = _BACKGROUNDS.get(key)
+    if bg is None:
+        bg = torch.tensor([list(key[0])], dtype=torch.float32, device=device)
+        _BACKGROUNDS[key] = bg
+    return bg
+
+
 def tile_grid(width: int, height: int, tile_size: int):
     return (width + tile_size - 1) // tile_size, (height + tile_size - 1) // tile_size
 
@@ -77,7 +92,7 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
                                      calc_compensations=False, camera_model=0)
     isect, offsets = _intersect(proj, width, height, tile_size)
     colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)
-    bg = torch.tensor([list(background)], dtype=torch.float32, device=means.device)
+    bg = background_tensor(background, means.device)
     render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, torch.sigmoid(opacity_logits)[:, None],
                                       offsets, isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
     return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],
@@ -92,7 +107,7 @@ def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats,
                                      opacities=opac if opacities_in_projection else None, eps2d=0.3,
                                      near_plane=0.01, far_plane=far_plane)
     isect, offsets = _intersect(proj, width, height, tile_size)
-    bg = torch.tensor([list(background)], dtype=torch.float32, device=means.device)
+    bg = background_tensor(background, means.device)
     render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors[:, None], opac[:, None], offsets,
                                       isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
     return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],

@@ -215,6 +215,26 @@ int gsplat_hip_isect_tile_sorted(const float* means2d, const int32_t* radii, con
                                  int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
                                  void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same result in two steps, so that a caller who must read the
+ * intersection count back to the host can queue the first step before
+ * waiting (no counterpart in the reference, whose count read-back is at
+ * gsplat_intersect.cpp:155-170):
+ *  depth_order: perm [numel] = pair indices stably sorted by depth bits,
+ *    offsets [numel] = exclusive scan of tiles_per_gauss[perm]; needs only
+ *    the counts, not their total.
+ *  encode_sorted: from perm and offsets, the sorted isect_ids and
+ *    flatten_ids of n_isects entries (n_isects = the counts' total). */
+size_t gsplat_hip_isect_depth_order_workspace_size(int64_t numel);
+int gsplat_hip_isect_depth_order(const float* depths, const int32_t* tiles_per_gauss, int64_t numel,
+                                 int32_t* perm, int32_t* offsets, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+size_t gsplat_hip_isect_encode_sorted_workspace_size(int64_t n_isects);
+int gsplat_hip_isect_encode_sorted(const float* means2d, const int32_t* radii, const float* depths,
+                                   const int32_t* perm, const int32_t* offsets, int64_t I, int64_t numel,
+                                   int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                   int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
+                                   void* workspace, size_t workspace_bytes, void* stream);
+
 /* Replaces GSPlatIntersectOffset::eval_gpu (gsplat_intersect.cpp:643-681):
  * offsets [I, tile_height, tile_width] = lower_bound of (image << tile_bits |
  * tile) over the sorted isect_ids >> 32. */

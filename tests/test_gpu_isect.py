@@ -158,3 +158,35 @@ def test_large_properties():
     want = torch.arange(tw * th, device=keys.device, dtype=torch.int64)
     lb = torch.searchsorted(keys >> 32, want, right=False)
     assert torch.equal(offs, lb)
+
+
+def test_c_abi_tile_sorted_one_call(oracle):
+    """gsplat_hip_isect_tile_sorted (both steps in one call, shared
+    workspace) gives the oracle's sorted keys and ids."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    I, N, W, H, ts = 2, 6000, 300, 200, 16
+    m, r, d = random_projected(rng, I, N, W, H, True, True)
+    tw, th = (W + ts - 1) // ts, (H + ts - 1) // ts
+    exp = oracle.isect_tile(m, r, d, I, ts, tw, th, sort=True)
+    counts = oracle.isect_count(m, r, ts, tw, th).astype(np.int32)
+    n_isects = int(counts.sum())
+    lib = ctypes.CDLL(LIB)
+    p, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    lib.gsplat_hip_isect_tile_sorted_workspace_size.restype = ctypes.c_size_t
+    lib.gsplat_hip_isect_tile_sorted_workspace_size.argtypes = [i64, i64]
+    lib.gsplat_hip_isect_tile_sorted.restype = ctypes.c_int
+    lib.gsplat_hip_isect_tile_sorted.argtypes = [p, p, p, p, i64, i64, i32, i32, i32, i64, p, p, p, ctypes.c_size_t, p]
+    ws_bytes = lib.gsplat_hip_isect_tile_sorted_workspace_size(I * N, n_isects)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    md, rd, dd, cd = dev(m), dev(r), dev(d), dev(counts)
+    ids = torch.empty(n_isects, dtype=torch.int64, device="cuda")
+    flat = torch.empty(n_isects, dtype=torch.int32, device="cuda")
+    rc = lib.gsplat_hip_isect_tile_sorted(md.data_ptr(), rd.data_ptr(), dd.data_ptr(), cd.data_ptr(), I, I * N, ts,
+                                          tw, th, n_isects, ids.data_ptr(), flat.data_ptr(), ws.data_ptr(), ws_bytes,
+                                          torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(ids), exp["isect_ids"])
+    np.testing.assert_array_equal(host(flat), exp["flatten_ids"])
