@@ -236,15 +236,6 @@ __global__ void __launch_bounds__(kEncodeBlock) encode_presorted_kernel(
   }
 }
 
-__global__ void __launch_bounds__(256) assemble_ids_kernel(const uint32_t* __restrict__ keys,
-                                                           const int32_t* __restrict__ flat,
-                                                           const float* __restrict__ depths, int64_t n,
-                                                           int64_t* __restrict__ isect_ids) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n) return;
-  isect_ids[i] = static_cast<int64_t>((static_cast<uint64_t>(keys[i]) << 32) | __float_as_uint(depths[flat[i]]));
-}
-
 // floor(log2(n)) + 1 with the reference's float log2 (gsplat_intersect.cpp:60-65).
 int floor_log2_plus_one(int64_t value) {
   return static_cast<int>(std::floor(std::log2(static_cast<float>(value)))) + 1;
@@ -506,15 +497,9 @@ extern "C" int gsplat_hip_isect_encode_sorted(const float* means2d, const int32_
         l.tkeys, l.tvals);
   }
   if ((rc = check_launch(what))) return rc;
-  if ((rc = radix_sort_pairs<uint32_t>(l.tkeys, l.tvals, n_isects, 0, image_bits + tile_bits, l.tkeys_sorted,
-                                       flatten_ids, l.sort_ws, l.sort_ws_bytes, s, what)))
-    return rc;
-  {
-    KernelTimer timer("isect_assemble_ids", s);
-    assemble_ids_kernel<<<grid_for(n_isects, 256), 256, 0, s>>>(l.tkeys_sorted, flatten_ids, depths, n_isects,
-                                                                isect_ids);
-  }
-  return check_launch(what);
+  // the last pass writes the 64-bit ids (key << 32 | depth bits) directly
+  return radix_sort_pairs<uint32_t>(l.tkeys, l.tvals, n_isects, 0, image_bits + tile_bits, l.tkeys_sorted,
+                                    flatten_ids, l.sort_ws, l.sort_ws_bytes, s, what, depths, isect_ids);
 }
 
 // One call: [perm | offsets | shared phase workspace] (the two phases run in

@@ -196,7 +196,7 @@ constexpr uint32_t kFlagPrefix = 2u << 30;        // inclusive prefix through th
 constexpr uint32_t kCountMask = (1u << 30) - 1u;
 constexpr int kMaxPasses = 8;
 constexpr int kSpinLimit = 1 << 18;
-constexpr int kLookbackWindow = 16;
+constexpr int kLookbackWindow = 8;
 
 // Global digit histograms of every pass in two steps without same-address
 // atomic pile-ups: each of up to kHistBlocks blocks histograms its share of
@@ -244,25 +244,33 @@ __global__ void __launch_bounds__(kSortBlock) hist_add_kernel(const uint32_t* __
   if (sum) atomicAdd(&hist[p * kRadix + t], sum);
 }
 
+// Where a pass writes: keys and values, or (ids set, 32-bit keys, last pass
+// of the intersection sort) 64-bit ids key << 32 | depth bits of the value's
+// pair plus the values.
 template <typename K>
+struct OsOut {
+  K* keys;
+  int32_t* vals;
+  const float* depths;
+  int64_t* ids;
+};
+
+template <typename K, bool ASM>
 __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restrict__ keys_in,
                                                               const int32_t* __restrict__ vals_in, int64_t n,
                                                               int shift, const uint32_t* __restrict__ hist,
                                                               uint32_t* __restrict__ lookback,
-                                                              int32_t* __restrict__ error_word,
-                                                              K* __restrict__ keys_out, int32_t* __restrict__ vals_out) {
+                                                              int32_t* __restrict__ error_word, OsOut<K> out) {
   __shared__ K s_keys[kOsTile];
   __shared__ int32_t s_vals[kOsTile];
   __shared__ uint32_t s_wcnt[kWaves][kRadix];  // per-wave running counts, then per-wave bases
   __shared__ uint32_t s_tile_start[kRadix];
   __shared__ uint32_t s_gbase[kRadix];
   __shared__ uint32_t s_wsum[kWaves];
+  __shared__ uint32_t s_hsum[kWaves];
   const int t = threadIdx.x;
   const int lane = t % kWave;
   const int wave = t / kWave;
-#pragma unroll
-  for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
-  __syncthreads();
   const int64_t part = blockIdx.x;
   const int64_t base = part * kOsTile;
   const int cnt = static_cast<int>(min<int64_t>(kOsTile, n - base));
@@ -283,6 +291,19 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
       v[r] = 0;
     }
   }
+  // thread t owns digit t: start of digit t over the whole pass (scan of the
+  // pass histogram), kept in a register until the look-back adds the prefix
+  const uint32_t hc = hist[t];
+  const int hinc = wave_inclusive_scan(static_cast<int>(hc));
+  if (lane == kWave - 1) s_hsum[wave] = static_cast<uint32_t>(hinc);
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
+  __syncthreads();
+  uint32_t gstart = static_cast<uint32_t>(hinc) - hc;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w)
+    if (w < wave) gstart += s_hsum[w];
+
   const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
   uint32_t* wc = s_wcnt[wave];
 #pragma unroll
@@ -304,7 +325,7 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
     if (valid && my == 0) wc[d] = cur + static_cast<uint32_t>(__popcll(peers));
   }
   __syncthreads();
-  // thread t owns digit t: per-wave exclusive bases and the tile total
+  // per-wave exclusive bases of digit t and the partition's count of it
   uint32_t total = 0;
 #pragma unroll
   for (int w = 0; w < kWaves; ++w) {
@@ -312,12 +333,32 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
     s_wcnt[w][t] = total;
     total += c;
   }
-  // publish this partition's count, then look back for the exclusive prefix
+  // publish this partition's count as early as possible
   uint32_t* my_word = lookback + part * kRadix + t;
-  if (part == 0) {
-    __hip_atomic_store(my_word, kFlagPrefix | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
-    __hip_atomic_store(my_word, kFlagAggregate | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(my_word, (part == 0 ? kFlagPrefix : kFlagAggregate) | total, __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+  {
+    // partition-local exclusive start of digit t (scan of the counts)
+    const int inc = wave_inclusive_scan(static_cast<int>(total));
+    if (lane == kWave - 1) s_wsum[wave] = static_cast<uint32_t>(inc);
+    __syncthreads();
+    uint32_t wb = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w)
+      if (w < wave) wb += s_wsum[w];
+    s_tile_start[t] = wb + static_cast<uint32_t>(inc) - total;
+  }
+  __syncthreads();
+  // reorder the partition by digit in LDS before looking back, so the keys
+  // leave registers while earlier partitions publish
+#pragma unroll
+  for (int r = 0; r < kOsItems; ++r) {
+    if (wave * kOsWaveKeys + r * kWave + lane < cnt) {
+      const uint32_t d = digit_of(k[r], shift);
+      const uint32_t pos = s_tile_start[d] + wc[d] + rank[r];
+      s_keys[pos] = k[r];
+      s_vals[pos] = v[r];
+    }
   }
   uint32_t prefix = 0;
   if (part > 0) {
@@ -355,48 +396,19 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
     }
     __hip_atomic_store(my_word, kFlagPrefix | (prefix + total), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  // global start of digit t = sum of all smaller digits' totals (from the
-  // histogram) + this digit's count in earlier partitions
-  {
-    const uint32_t c = hist[t];
-    const int inc = wave_inclusive_scan(static_cast<int>(c));
-    if (lane == kWave - 1) s_wsum[wave] = static_cast<uint32_t>(inc);
-    // tile-local exclusive start of digit t (scan of totals) shares the sync
-    __syncthreads();
-    uint32_t wb = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      if (w < wave) wb += s_wsum[w];
-    s_gbase[t] = wb + static_cast<uint32_t>(inc) - c + prefix;
-  }
-  __syncthreads();
-  {
-    const int inc = wave_inclusive_scan(static_cast<int>(total));
-    if (lane == kWave - 1) s_wsum[wave] = static_cast<uint32_t>(inc);
-    __syncthreads();
-    uint32_t wb = 0;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w)
-      if (w < wave) wb += s_wsum[w];
-    s_tile_start[t] = wb + static_cast<uint32_t>(inc) - total;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < kOsItems; ++r) {
-    if (wave * kOsWaveKeys + r * kWave + lane < cnt) {
-      const uint32_t d = digit_of(k[r], shift);
-      const uint32_t pos = s_tile_start[d] + wc[d] + rank[r];
-      s_keys[pos] = k[r];
-      s_vals[pos] = v[r];
-    }
-  }
+  s_gbase[t] = gstart + prefix;
   __syncthreads();
   for (int j = t; j < cnt; j += kSortBlock) {
     const K key = s_keys[j];
     const uint32_t d = digit_of(key, shift);
     const int64_t dst = static_cast<int64_t>(s_gbase[d]) + (j - static_cast<int64_t>(s_tile_start[d]));
-    keys_out[dst] = key;
-    vals_out[dst] = s_vals[j];
+    const int32_t val = s_vals[j];
+    if constexpr (ASM) {
+      out.ids[dst] = static_cast<int64_t>((static_cast<uint64_t>(key) << 32) | __float_as_uint(out.depths[val]));
+    } else {
+      out.keys[dst] = key;
+    }
+    out.vals[dst] = val;
   }
 }
 
@@ -447,6 +459,27 @@ size_t layout(int64_t n, SortWorkspace<K>* ws, void* base) {
   return keys_b + vals_b + hist_b + scan_b + oh_b + ot_b + ol_b + op_b;
 }
 
+// ids[i] = keys[i] << 32 | bits of depths[vals[i]] (32-bit keys).
+template <typename K>
+__global__ void __launch_bounds__(256) assemble_ids_kernel(const K* __restrict__ keys,
+                                                           const int32_t* __restrict__ vals,
+                                                           const float* __restrict__ depths, int64_t n,
+                                                           int64_t* __restrict__ ids) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  ids[i] = static_cast<int64_t>((static_cast<uint64_t>(keys[i]) << 32) | __float_as_uint(depths[vals[i]]));
+}
+
+template <typename K>
+int assemble(const K* keys, const int32_t* vals, const float* depths, int64_t n, int64_t* ids, hipStream_t s,
+             const char* what) {
+  {
+    KernelTimer timer("sort_assemble_ids", s);
+    assemble_ids_kernel<K><<<grid_for(n, 256), 256, 0, s>>>(keys, vals, depths, n, ids);
+  }
+  return check_launch(what);
+}
+
 }  // namespace
 
 template <typename K>
@@ -456,8 +489,10 @@ size_t radix_sort_workspace_bytes(int64_t n) {
 
 template <typename K>
 int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bit_lo, int bit_hi, K* keys_out,
-                     int32_t* vals_out, void* workspace, size_t workspace_bytes, hipStream_t s, const char* what) {
+                     int32_t* vals_out, void* workspace, size_t workspace_bytes, hipStream_t s, const char* what,
+                     const float* asm_depths, int64_t* asm_ids) {
   const std::string w(what);
+  if (asm_ids && (sizeof(K) != 4 || !asm_depths)) return invalid(w + ": invalid sort arguments.");
   if (n < 0 || bit_lo < 0 || bit_hi > static_cast<int>(8 * sizeof(K)) || bit_lo > bit_hi)
     return invalid(w + ": invalid sort arguments.");
   if (n == 0) return GSPLAT_OK;
@@ -469,6 +504,7 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
       KernelTimer timer("sort_copy", s);
       copy_kernel<K><<<grid_for(n, 256), 256, 0, s>>>(keys_in, vals_in, n, keys_out, vals_out);
     }
+    if (asm_ids) return assemble(keys_out, vals_out, asm_depths, n, asm_ids, s, what);
     return check_launch(what);
   }
   SortWorkspace<K> ws;
@@ -500,9 +536,23 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
       int32_t* dst_v = to_out ? vals_out : ws.vals_alt;
       {
         KernelTimer timer("sort_onesweep", s);
-        onesweep_kernel<K><<<static_cast<unsigned>(n_parts), kSortBlock, 0, s>>>(
-            src_k, src_v, n, bit_lo + 8 * p, ws.os_hist + p * kRadix, ws.os_lookback + p * n_parts * kRadix,
-            ws.os_error, dst_k, dst_v);
+        const OsOut<K> o{dst_k, dst_v, asm_depths, asm_ids};
+        const unsigned grid = static_cast<unsigned>(n_parts);
+        bool launched = false;
+        if constexpr (sizeof(K) == 4) {
+          if (asm_ids && p == passes - 1) {
+            onesweep_kernel<K, true><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, bit_lo + 8 * p,
+                                                                 ws.os_hist + p * kRadix,
+                                                                 ws.os_lookback + p * n_parts * kRadix, ws.os_error,
+                                                                 o);
+            launched = true;
+          }
+        }
+        if (!launched) {
+          onesweep_kernel<K, false><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, bit_lo + 8 * p,
+                                                                ws.os_hist + p * kRadix,
+                                                                ws.os_lookback + p * n_parts * kRadix, ws.os_error, o);
+        }
       }
       if ((rc = check_launch(what))) return rc;
       src_k = dst_k;
@@ -537,15 +587,16 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
     src_k = dst_k;
     src_v = dst_v;
   }
+  if (asm_ids) return assemble(keys_out, vals_out, asm_depths, n, asm_ids, s, what);
   return GSPLAT_OK;
 }
 
 template size_t radix_sort_workspace_bytes<uint32_t>(int64_t);
 template size_t radix_sort_workspace_bytes<uint64_t>(int64_t);
 template int radix_sort_pairs<uint32_t>(const uint32_t*, const int32_t*, int64_t, int, int, uint32_t*, int32_t*,
-                                        void*, size_t, hipStream_t, const char*);
+                                        void*, size_t, hipStream_t, const char*, const float*, int64_t*);
 template int radix_sort_pairs<uint64_t>(const uint64_t*, const int32_t*, int64_t, int, int, uint64_t*, int32_t*,
-                                        void*, size_t, hipStream_t, const char*);
+                                        void*, size_t, hipStream_t, const char*, const float*, int64_t*);
 
 }  // namespace gsplat_hip
 

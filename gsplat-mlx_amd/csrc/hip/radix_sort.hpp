@@ -15,9 +15,13 @@ size_t radix_sort_workspace_bytes(int64_t n);
 // digits keep their input order). Key bits at and above bit_hi must be zero
 // or equal for all keys, bits below bit_lo are ignored. The result always
 // lands in keys_out / vals_out; the inputs are not modified.
+//
+// With asm_ids set (32-bit keys only), the sorted keys are not stored;
+// instead asm_ids[i] = sorted key << 32 | bits of asm_depths[sorted value]
+// (keys_out is then only scratch between passes).
 template <typename K>
 int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bit_lo, int bit_hi, K* keys_out,
                      int32_t* vals_out, void* workspace, size_t workspace_bytes, hipStream_t stream,
-                     const char* what);
+                     const char* what, const float* asm_depths = nullptr, int64_t* asm_ids = nullptr);
 
 }  // namespace gsplat_hip

@@ -75,6 +75,26 @@ __device__ __forceinline__ int32_t load_gaussian(const RasterArgs& a, int64_t j,
   return g;
 }
 
+// exp(y) by Cody-Waite reduction: y log2(e) = n + f with the product kept
+// exact to about 2^-48 (log2(e) split into a float head and tail, the head's
+// rounding error recovered by an FMA), 2^f from v_exp_f32, scaled by 2^n.
+// The tail is log2(e) - head truncated to float (0x32a5705f), the value the
+// device library's expf uses, which makes this bit-identical to expf for
+// every float y > -103 (compared exhaustively on gfx950); it only drops
+// expf's range selects. Below -103 both results are under 2^-148, so o * exp
+// fails the 1/255 alpha test for any finite opacity and the value is never
+// used.
+__device__ __forceinline__ float exp_alpha(float y) {
+  const float head = 1.44269502162933349609375f;  // float(log2 e)
+  const float tail = __uint_as_float(0x32a5705fu);
+  const float ph = y * head;
+  float pl = __builtin_fmaf(y, head, -ph);
+  pl = __builtin_fmaf(y, tail, pl);
+  const float n = __builtin_rintf(ph);
+  const float f = (ph - n) + pl;
+  return __builtin_ldexpf(__builtin_amdgcn_exp2f(f), static_cast<int>(n));
+}
+
 // ---------------------------------------------------------------------------
 // Per-wave culling. When a batch record is staged, its loader tests it once
 // against every wave's pixel rectangle and stores a bit mask; each wave
@@ -221,7 +241,7 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
       // records of this 64-slot chunk that may touch this wave (all lanes vote)
       const int kl = c0 + lane;
       uint64_t bits = __ballot(kl < cnt && ((s_mask[kl] >> wave) & 1u));
-      if (done) continue;
+      if (__ballot(!done) == 0) bits = 0;  // every pixel of the wave has saturated
       while (bits) {
         const int k = c0 + __builtin_ctzll(bits);
         bits &= bits - 1;
@@ -230,23 +250,29 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
         const float dx = m.x - px;
         const float dy = m.y - py;
         const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
-        const float alpha = fminf(kMaxAlpha, co.w * expf(-sigma));
-        if (sigma < 0.0f || alpha < kAlphaThreshold) continue;
+        const float alpha = fminf(kMaxAlpha, co.w * exp_alpha(-sigma));
+        // branch-free form of: skip when sigma < 0 or alpha < 1/255; stop
+        // (without this record) when T would fall to the threshold
+        const bool pass = !done && !(sigma < 0.0f || alpha < kAlphaThreshold);
         const float next_T = T * (1.0f - alpha);
-        if (next_T <= kTransmittanceThreshold) {
-          done = true;
-          break;
-        }
-        const float vis = alpha * T;
+        const bool sat = pass && next_T <= kTransmittanceThreshold;
+        const bool take = pass && !sat;
+        done = done || sat;
+        const float vis = take ? alpha * T : 0.0f;
         if constexpr (CH > 0) {
 #pragma unroll
-          for (int c = 0; c < CH; ++c) acc[c] += s_col[k * CH + c] * vis;
+          for (int c = 0; c < CH; ++c) {
+            const float add = s_col[k * CH + c] * vis;
+            acc[c] += take ? add : 0.0f;  // a skipped record adds nothing, even a non-finite colour
+          }
         } else {
-          const float* col = a.colors + static_cast<int64_t>(s_g[k]) * channels;
-          for (int c = 0; c < channels; ++c) acc[c] += col[c] * vis;
+          if (take) {
+            const float* col = a.colors + static_cast<int64_t>(s_g[k]) * channels;
+            for (int c = 0; c < channels; ++c) acc[c] += col[c] * vis;
+          }
         }
-        cur = static_cast<int32_t>(b0 + k);
-        T = next_T;
+        cur = take ? static_cast<int32_t>(b0 + k) : cur;
+        T = take ? next_T : T;
       }
     }
   }
@@ -515,7 +541,7 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
           const float dx = m.x - px;
           const float dy = m.y - py;
           const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
-          const float vis = expf(-sigma);
+          const float vis = exp_alpha(-sigma);
           const float a_raw = co.w * vis;
           const float alpha = fminf(kMaxAlpha, a_raw);
           const bool valid = k_rel <= last_rel && !(sigma < 0.0f || alpha < kAlphaThreshold);
