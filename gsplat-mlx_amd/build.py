@@ -28,9 +28,9 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = os.environ.get("GSPLAT_OFFLOAD_ARCH", "gfx950")
 
 HIP_SOURCES = ["common", "quat_scale_to_covar", "projection", "spherical_harmonics", "scan", "intersect",
-               "radix_sort", "rasterize"]
+               "radix_sort", "rasterize", "training_glue"]
 CORE_SOURCES = ["gsplat_quat_scale_to_covar", "gsplat_projection", "gsplat_spherical_harmonics",
-                "gsplat_intersect", "gsplat_rasterize"]
+                "gsplat_intersect", "gsplat_rasterize", "gsplat_training_glue"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",

@@ -249,6 +249,40 @@ py::dict sh_camera_colors_backward(int degrees_to_use, const TensorMap& inputs, 
   return r;
 }
 
+// Training-step glue fused into kernels (additions to the reference surface;
+// see gsplat_training_glue.h).
+py::dict gaussian_activations_forward(const TensorMap& inputs) {
+  auto out = gsplat_core::gsplat_gaussian_activations_forward(
+      get_or_empty(inputs, "quats"), get_or_empty(inputs, "log_scales"), get_or_empty(inputs, "opacity_logits"));
+  py::dict r;
+  r["quats"] = out[0];
+  r["scales"] = out[1];
+  r["opacities"] = out[2];
+  return r;
+}
+
+py::dict gaussian_activations_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
+                                       const TensorMap& cotangents) {
+  auto out = gsplat_core::gsplat_gaussian_activations_backward(
+      get_or_empty(inputs, "quats"), get_or_empty(forward_outputs, "scales"),
+      get_or_empty(forward_outputs, "opacities"), get_or_empty(cotangents, "v_quats"),
+      get_or_empty(cotangents, "v_scales"), get_or_empty(cotangents, "v_opacities"));
+  py::dict r;
+  r["v_quats"] = out[0];
+  r["v_log_scales"] = out[1];
+  r["v_opacity_logits"] = out[2];
+  return r;
+}
+
+at::Tensor l1_loss_forward(const at::Tensor& image, const at::Tensor& target) {
+  return gsplat_core::gsplat_l1_loss_forward(image, target);
+}
+
+py::tuple l1_loss_backward(const at::Tensor& image, const at::Tensor& target, const at::Tensor& grad) {
+  auto out = gsplat_core::gsplat_l1_loss_backward(image, target, grad);
+  return py::make_tuple(out[0], out[1]);
+}
+
 // Template smoke entries of the reference (gsplat_core/dummy.cpp:7-13).
 int dummy_add(int a, int b) { return a + b; }
 
@@ -286,6 +320,11 @@ PYBIND11_MODULE(_gsplat_core, m) {
   m.def("sh_camera_colors_forward", &sh_camera_colors_forward, py::arg("degrees_to_use"), py::arg("inputs"));
   m.def("sh_camera_colors_backward", &sh_camera_colors_backward, py::arg("degrees_to_use"), py::arg("inputs"),
         py::arg("cotangents"));
+  m.def("gaussian_activations_forward", &gaussian_activations_forward, py::arg("inputs"));
+  m.def("gaussian_activations_backward", &gaussian_activations_backward, py::arg("inputs"),
+        py::arg("forward_outputs"), py::arg("cotangents"));
+  m.def("l1_loss_forward", &l1_loss_forward, py::arg("image"), py::arg("target"));
+  m.def("l1_loss_backward", &l1_loss_backward, py::arg("image"), py::arg("target"), py::arg("grad"));
   m.def("quat_scale_to_covar_preci_forward", &quat_scale_to_covar_preci_forward, py::arg("inputs"),
         py::arg("compute_covar") = true, py::arg("compute_preci") = true, py::arg("triu") = true);
   m.def("quat_scale_to_covar_preci_backward", &quat_scale_to_covar_preci_backward, py::arg("inputs"),

@@ -1,0 +1,117 @@
+// Training-step glue operator layer: validation, allocation, streams; compute
+// is the HIP C-ABI (training_glue.hip).
+#include "gsplat_training_glue.h"
+
+#include "core_util.h"
+
+namespace gsplat_core {
+namespace {
+using namespace detail;
+
+void require_f32(const array& a, const char* name) {
+  if (a.scalar_type() != at::kFloat) throw std::runtime_error(std::string(name) + " must be float32.");
+  require_device(a, name);
+}
+
+// Gaussian count shared by the defined activation inputs.
+int64_t activation_count(const array& quats, const array& log_scales, const array& logits) {
+  int64_t n = -1;
+  auto take = [&](const array& a, int64_t per, const char* name) {
+    if (is_empty(a)) return;
+    require_f32(a, name);
+    if (a.numel() % per != 0 || (per > 1 && a.size(-1) != per))
+      throw std::runtime_error(std::string(name) + " has the wrong trailing dimension.");
+    const int64_t m = a.numel() / per;
+    if (n >= 0 && m != n) throw std::runtime_error("gaussian_activations: inputs disagree on the Gaussian count.");
+    n = m;
+  };
+  take(quats, 4, "quats");
+  take(log_scales, 3, "log_scales");
+  take(logits, 1, "opacity_logits");
+  return n < 0 ? 0 : n;
+}
+
+}  // namespace
+
+std::vector<array> gsplat_gaussian_activations_forward(const array& quats_in, const array& log_scales_in,
+                                                       const array& logits_in, StreamOrDevice s) {
+  const int64_t n = activation_count(quats_in, log_scales_in, logits_in);
+  const array* ref = !is_empty(quats_in) ? &quats_in : (!is_empty(log_scales_in) ? &log_scales_in : &logits_in);
+  if (is_empty(*ref)) return {empty_f32(), empty_f32(), empty_f32()};
+  const c10::DeviceGuard guard(ref->device());
+  const array quats = is_empty(quats_in) ? array() : contig(quats_in);
+  const array log_scales = is_empty(log_scales_in) ? array() : contig(log_scales_in);
+  const array logits = is_empty(logits_in) ? array() : contig(logits_in);
+  array qo = is_empty(quats) ? at::empty({0}, f32_like(*ref)) : at::empty(quats.sizes(), f32_like(*ref));
+  array so = is_empty(log_scales) ? at::empty({0}, f32_like(*ref)) : at::empty(log_scales.sizes(), f32_like(*ref));
+  array oo = is_empty(logits) ? at::empty({0}, f32_like(*ref)) : at::empty(logits.sizes(), f32_like(*ref));
+  check(gsplat_hip_gaussian_activations_fwd(ptr_or_null<float>(quats), ptr_or_null<float>(log_scales),
+                                            ptr_or_null<float>(logits), n,
+                                            is_empty(quats) ? nullptr : qo.data_ptr<float>(),
+                                            is_empty(log_scales) ? nullptr : so.data_ptr<float>(),
+                                            is_empty(logits) ? nullptr : oo.data_ptr<float>(), stream_for(s, *ref)));
+  return {qo, so, oo};
+}
+
+std::vector<array> gsplat_gaussian_activations_backward(const array& quats_in, const array& scales_in,
+                                                        const array& opac_in, const array& v_q_in,
+                                                        const array& v_s_in, const array& v_o_in, StreamOrDevice s) {
+  const int64_t n = activation_count(quats_in, scales_in, opac_in);
+  const array* ref = !is_empty(quats_in) ? &quats_in : (!is_empty(scales_in) ? &scales_in : &opac_in);
+  if (is_empty(*ref)) return {empty_f32(), empty_f32(), empty_f32()};
+  const c10::DeviceGuard guard(ref->device());
+  auto cot = [&](const array& v, const array& like, const char* name) -> array {
+    if (is_empty(v) || is_empty(like)) return array();
+    require_f32(v, name);
+    if (v.numel() != like.numel()) throw std::runtime_error(std::string(name) + " must match its output's shape.");
+    return contig(v);
+  };
+  const array quats = is_empty(quats_in) ? array() : contig(quats_in);
+  const array scales = is_empty(scales_in) ? array() : contig(scales_in);
+  const array opac = is_empty(opac_in) ? array() : contig(opac_in);
+  const array v_q = cot(v_q_in, quats, "v_quats"), v_s = cot(v_s_in, scales, "v_scales"),
+              v_o = cot(v_o_in, opac, "v_opacities");
+  array gq = is_empty(quats) ? at::empty({0}, f32_like(*ref)) : at::empty(quats.sizes(), f32_like(*ref));
+  array gs = is_empty(scales) ? at::empty({0}, f32_like(*ref)) : at::empty(scales.sizes(), f32_like(*ref));
+  array go = is_empty(opac) ? at::empty({0}, f32_like(*ref)) : at::empty(opac.sizes(), f32_like(*ref));
+  check(gsplat_hip_gaussian_activations_bwd(
+      ptr_or_null<float>(quats), ptr_or_null<float>(scales), ptr_or_null<float>(opac), ptr_or_null<float>(v_q),
+      ptr_or_null<float>(v_s), ptr_or_null<float>(v_o), n, is_empty(quats) ? nullptr : gq.data_ptr<float>(),
+      is_empty(scales) ? nullptr : gs.data_ptr<float>(), is_empty(opac) ? nullptr : go.data_ptr<float>(),
+      stream_for(s, *ref)));
+  return {gq, gs, go};
+}
+
+array gsplat_l1_loss_forward(const array& a_in, const array& b_in, StreamOrDevice s) {
+  require_f32(a_in, "image");
+  require_f32(b_in, "target");
+  if (a_in.sizes() != b_in.sizes()) throw std::runtime_error("l1_loss: image and target shapes differ.");
+  const c10::DeviceGuard guard(a_in.device());
+  const array a = contig(a_in), b = contig(b_in);
+  array loss = at::empty({}, f32_like(a));
+  const size_t ws_bytes = gsplat_hip_l1_loss_workspace_size(a.numel());
+  array ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, u8_like(a));
+  check(gsplat_hip_l1_loss_fwd(a.numel() ? a.data_ptr<float>() : nullptr, b.numel() ? b.data_ptr<float>() : nullptr,
+                               a.numel(), loss.data_ptr<float>(), ws.data_ptr<uint8_t>(), ws_bytes,
+                               stream_for(s, a)));
+  return loss;
+}
+
+std::vector<array> gsplat_l1_loss_backward(const array& a_in, const array& b_in, const array& grad_in,
+                                           StreamOrDevice s) {
+  require_f32(a_in, "image");
+  require_f32(b_in, "target");
+  require_f32(grad_in, "grad");
+  if (a_in.sizes() != b_in.sizes()) throw std::runtime_error("l1_loss: image and target shapes differ.");
+  if (grad_in.numel() != 1) throw std::runtime_error("l1_loss: the cotangent must be a scalar.");
+  const c10::DeviceGuard guard(a_in.device());
+  const array a = contig(a_in), b = contig(b_in), g = contig(grad_in);
+  array va = at::empty(a.sizes(), f32_like(a));
+  array vb = at::empty(b.sizes(), f32_like(a));
+  if (a.numel() == 0) return {va, vb};
+  check(gsplat_hip_l1_loss_bwd(a.data_ptr<float>(), b.data_ptr<float>(), a.numel(), g.data_ptr<float>(),
+                               va.data_ptr<float>(), vb.data_ptr<float>(), stream_for(s, a)));
+  return {va, vb};
+}
+
+}  // namespace gsplat_core

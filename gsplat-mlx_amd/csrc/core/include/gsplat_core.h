@@ -6,3 +6,4 @@
 #include "gsplat_quat_scale_to_covar.h"
 #include "gsplat_rasterize.h"
 #include "gsplat_spherical_harmonics.h"
+#include "gsplat_training_glue.h"

@@ -19,6 +19,8 @@ except ImportError as exc:  # pragma: no cover - exercised only on broken instal
     ) from exc
 
 from .autograd import (  # noqa: E402,F401
+    gaussian_activations,
+    l1_loss,
     projection_ewa_3dgs_fused,
     quat_scale_to_covar_preci,
     rasterize_to_pixels_3dgs,
@@ -41,6 +43,12 @@ __all__ = [
     "quat_scale_to_covar_preci_backward",
     "sh_camera_colors_forward",
     "sh_camera_colors_backward",
+    "gaussian_activations_forward",
+    "gaussian_activations_backward",
+    "l1_loss_forward",
+    "l1_loss_backward",
+    "gaussian_activations",
+    "l1_loss",
     "projection_ewa_3dgs_fused",
     "quat_scale_to_covar_preci",
     "rasterize_to_pixels_3dgs",

@@ -11,6 +11,13 @@ Each ``backward`` routes cotangents exactly as the reference ``Primitive::vjp``:
   * rasterize_to_pixels_3dgs -- gsplat_rasterize.cpp:749-795 (absgrad off)
 Intersection outputs carry no gradient (the reference callers stop_gradient
 them, scanner_points_training_utils.py:1093-1101).
+
+Two more Functions fuse the training step's elementwise glue into HIP kernels
+(no counterpart primitive in the reference; they replace the framework
+composition at its call sites):
+  * gaussian_activations -- normalize_quats / exp / sigmoid of the model
+    parameters (scanner_points_training_utils.py:39-41, 306-316)
+  * l1_loss -- the image L1 term of image_loss_components (:1147-1160)
 """
 from __future__ import annotations
 
@@ -231,3 +238,55 @@ def rasterize_to_pixels_3dgs(means2d, conics, colors, opacities, tile_offsets, f
                                              masks if masks is not None else e, tile_offsets, flatten_ids,
                                              image_width, image_height, tile_size)
     return {"render_colors": rc, "render_alphas": ra, "last_ids": li}
+
+
+class _GaussianActivations(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, quats, log_scales, opacity_logits):
+        out = _C.gaussian_activations_forward({"quats": quats, "log_scales": log_scales,
+                                               "opacity_logits": opacity_logits})
+        ctx.save_for_backward(quats, out["scales"], out["opacities"])
+        return out["quats"], out["scales"], out["opacities"]
+
+    @staticmethod
+    def backward(ctx, v_quats, v_scales, v_opacities):
+        quats, scales, opacities = ctx.saved_tensors
+        need_q, need_s, need_o = ctx.needs_input_grad
+        inputs = {"quats": quats} if need_q else {}
+        fwd = {}
+        if need_s:
+            fwd["scales"] = scales
+        if need_o:
+            fwd["opacities"] = opacities
+        cot = {}
+        for key, v, need in (("v_quats", v_quats, need_q), ("v_scales", v_scales, need_s),
+                             ("v_opacities", v_opacities, need_o)):
+            if need and v is not None:
+                cot[key] = v.contiguous()
+        out = _C.gaussian_activations_backward(inputs, fwd, cot)
+        return (out["v_quats"] if need_q else None, out["v_log_scales"] if need_s else None,
+                out["v_opacity_logits"] if need_o else None)
+
+
+def gaussian_activations(quats, log_scales, opacity_logits):
+    """(quats / max(|quats|, 1e-8), exp(log_scales), sigmoid(opacity_logits))
+    in one kernel per direction."""
+    return _GaussianActivations.apply(quats, log_scales, opacity_logits)
+
+
+class _L1Loss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, image, target):
+        ctx.save_for_backward(image, target)
+        return _C.l1_loss_forward(image, target)
+
+    @staticmethod
+    def backward(ctx, grad):
+        image, target = ctx.saved_tensors
+        v_image, v_target = _C.l1_loss_backward(image, target, grad.contiguous())
+        return (v_image if ctx.needs_input_grad[0] else None, v_target if ctx.needs_input_grad[1] else None)
+
+
+def l1_loss(image, target):
+    """mean(|image - target|) as a 0-d tensor, forward and backward in HIP."""
+    return _L1Loss.apply(image, target)

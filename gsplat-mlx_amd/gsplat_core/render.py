@@ -6,18 +6,23 @@ reference training call sites:
   render_sh_model             scanner_points_training_utils.py:1050-1121
   render_rgb_model            train_image_fitting_3dgs_mlx.py:165-237 /
                               render_random_3dgs_png.py:114-168
-  l1_loss                     image L1 term of image_loss_components
+  l1_loss                     image L1 term of image_loss_components,
+                              scanner_points_training_utils.py:1147-1160
 
 Every operator call goes through the differentiable wrappers in
-``gsplat_core.autograd`` (HIP kernels); the glue is plain torch elementwise
-math on the device.
+``gsplat_core.autograd`` (HIP kernels). The parameter activations (quaternion
+normalisation, exp of the log-scales, sigmoid of the opacity logits), the SH
+colour glue and the L1 loss also run as fused HIP kernels; the torch
+compositions they replace are kept beside them (``*_unfused``) as the
+reference for tests.
 """
 from __future__ import annotations
 
 import torch
 
 from . import _gsplat_core as _C
-from .autograd import projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs, sh_camera_colors, spherical_harmonics
+from .autograd import (gaussian_activations, l1_loss as _l1_loss, projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs,
+                       sh_camera_colors, spherical_harmonics)
 
 
 def normalize_quats(quats: torch.Tensor) -> torch.Tensor:
@@ -86,14 +91,15 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
                     far_plane=100.0):
     """One camera (viewmats [1,1,4,4]); returns the render dict plus radii,
     tiles_per_gauss and flatten_ids, like the reference."""
-    proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=normalize_quats(quats),
-                                     scales=torch.exp(log_scales), viewspace_points=viewspace_points, eps2d=0.3,
+    quats_n, scales, opac = gaussian_activations(quats, log_scales, opacity_logits)
+    proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=quats_n,
+                                     scales=scales, viewspace_points=viewspace_points, eps2d=0.3,
                                      near_plane=0.01, far_plane=far_plane, radius_clip=0.0,
                                      calc_compensations=False, camera_model=0)
     isect, offsets = _intersect(proj, width, height, tile_size)
     colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)
     bg = background_tensor(background, means.device)
-    render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, torch.sigmoid(opacity_logits)[:, None],
+    render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, opac[:, None],
                                       offsets, isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
     return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],
             "flatten_ids": isect["flatten_ids"], "isect_ids": isect["isect_ids"], "tile_offsets": offsets}
@@ -101,9 +107,9 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
 
 def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, width, height, tile_size,
                      background=(0.0, 0.0, 0.0), opacities_in_projection=False, far_plane=1e10):
-    opac = torch.sigmoid(opacity_logits)
-    proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=normalize_quats(quats),
-                                     scales=torch.exp(log_scales),
+    quats_n, scales, opac = gaussian_activations(quats, log_scales, opacity_logits)
+    proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=quats_n,
+                                     scales=scales,
                                      opacities=opac if opacities_in_projection else None, eps2d=0.3,
                                      near_plane=0.01, far_plane=far_plane)
     isect, offsets = _intersect(proj, width, height, tile_size)
@@ -115,4 +121,13 @@ def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats,
 
 
 def l1_loss(image: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
+    """mean(|image - target|) (fused HIP kernels)."""
+    return _l1_loss(image, target)
+
+
+def l1_loss_unfused(image: torch.Tensor, target: torch.Tensor) -> torch.Tensor:
     return torch.mean(torch.abs(image - target))
+
+
+def gaussian_activations_unfused(quats, log_scales, opacity_logits):
+    return normalize_quats(quats), torch.exp(log_scales), torch.sigmoid(opacity_logits)

@@ -283,6 +283,36 @@ int gsplat_hip_rasterize_bwd(const float* means2d, const float* conics, const fl
 size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t channels, int32_t tile_width,
                                                int32_t tile_height);
 
+/* ---------------------------------------------------------------------------
+ * Training-step glue around the chain, one kernel per direction. No
+ * counterpart operator in the reference: these replace the framework
+ * elementwise composition at its call sites.
+ * Parameter activations (scanner_points_training_utils.py:39-41 and the
+ * model properties at :306-316), n Gaussians:
+ *   quats_out [n,4] = quats / max(|quats|, 1e-8), scales_out [n,3] =
+ *   exp(log_scales), opacities_out [n] = sigmoid(opacity_logits).
+ * Any input group may be NULL (skipped). The backward writes v_quats,
+ * v_log_scales, v_logits (each may be NULL); a NULL cotangent counts as zero.
+ * It reads the raw quats and the forward's scales and opacities. */
+int gsplat_hip_gaussian_activations_fwd(const float* quats, const float* log_scales,
+                                        const float* opacity_logits, int64_t n, float* quats_out,
+                                        float* scales_out, float* opacities_out, void* stream);
+int gsplat_hip_gaussian_activations_bwd(const float* quats, const float* scales, const float* opacities,
+                                        const float* v_quats_out, const float* v_scales,
+                                        const float* v_opacities, int64_t n, float* v_quats,
+                                        float* v_log_scales, float* v_logits, void* stream);
+
+/* Image L1 term mean(|a - b|) over n values into the device scalar *loss
+ * (nn.losses.l1_loss in image_loss_components,
+ * scanner_points_training_utils.py:1147-1160). The backward reads the device scalar cotangent
+ * *grad and writes v_a = grad / n * sign(a - b) and v_b = -v_a (either may be
+ * NULL). */
+size_t gsplat_hip_l1_loss_workspace_size(int64_t n);
+int gsplat_hip_l1_loss_fwd(const float* a, const float* b, int64_t n, float* loss, void* workspace,
+                           size_t workspace_bytes, void* stream);
+int gsplat_hip_l1_loss_bwd(const float* a, const float* b, int64_t n, const float* grad, float* v_a,
+                           float* v_b, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif
