@@ -18,11 +18,6 @@ __global__ void fill_zero_u8(uint8_t* __restrict__ p, int64_t n) {
   if (i < n) p[i] = 0;
 }
 
-struct ZeroSpans {
-  float* ptr[kMaxZeroSpans];
-  int64_t count[kMaxZeroSpans];  // floats
-};
-
 // blockIdx.y selects the span; 16-byte stores over its aligned body, plain
 // stores for the unaligned head and the tail.
 __global__ void __launch_bounds__(256) fill_zero_spans_kernel(ZeroSpans z) {
@@ -112,21 +107,14 @@ int fill_zero(void* ptr, int64_t bytes, hipStream_t stream) {
 }
 
 int fill_zero_spans(const ZeroSpan* spans, int n_spans, hipStream_t stream) {
-  ZeroSpans z{};
-  int n = 0;
+  const ZeroSpans z = pack_zero_spans(spans, n_spans);
+  if (z.n == 0) return GSPLAT_OK;
   int64_t largest = 0;
-  for (int i = 0; i < n_spans && i < kMaxZeroSpans; ++i) {
-    if (!spans[i].ptr || spans[i].count <= 0) continue;
-    z.ptr[n] = spans[i].ptr;
-    z.count[n] = spans[i].count;
-    largest = std::max(largest, spans[i].count);
-    ++n;
-  }
-  if (n == 0) return GSPLAT_OK;
+  for (int k = 0; k < z.n; ++k) largest = std::max(largest, z.count[k]);
   KernelTimer timer("fill_zero", stream);
   // about four float4 stores per thread on the largest span
   const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((largest / 4 + 1023) / 1024, 4096));
-  fill_zero_spans_kernel<<<dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(n)), 256, 0, stream>>>(z);
+  fill_zero_spans_kernel<<<dim3(static_cast<unsigned>(blocks), static_cast<unsigned>(z.n)), 256, 0, stream>>>(z);
   return check_launch("fill_zero");
 }
 

@@ -71,6 +71,42 @@ struct ZeroSpan {
 };
 int fill_zero_spans(const ZeroSpan* spans, int n_spans, hipStream_t stream);
 
+// The same spans packed for a kernel argument, so that a kernel which runs
+// anyway before the buffers are used can clear them (zero_spans_share)
+// instead of a launch of its own.
+struct ZeroSpans {
+  float* ptr[kMaxZeroSpans];
+  int64_t count[kMaxZeroSpans];  // floats
+  int n;
+};
+
+inline ZeroSpans pack_zero_spans(const ZeroSpan* spans, int n_spans) {
+  ZeroSpans z{};
+  for (int i = 0; i < n_spans && i < kMaxZeroSpans; ++i) {
+    if (!spans[i].ptr || spans[i].count <= 0) continue;
+    z.ptr[z.n] = spans[i].ptr;
+    z.count[z.n] = spans[i].count;
+    ++z.n;
+  }
+  return z;
+}
+
+// Thread `worker` of `n_workers` clears its share of every span: 16-byte
+// stores over each span's aligned body, plain stores for the head and tail.
+__device__ __forceinline__ void zero_spans_share(const ZeroSpans& z, int64_t worker, int64_t n_workers) {
+  for (int k = 0; k < z.n; ++k) {
+    float* p = z.ptr[k];
+    const int64_t n = z.count[k];
+    const int64_t head = n < 4 ? n : ((16 - (reinterpret_cast<uintptr_t>(p) & 15)) & 15) / 4;
+    const int64_t n4 = (n - head) / 4;
+    const int64_t tail = n - head - 4 * n4;
+    if (worker < head) p[worker] = 0.0f;
+    if (worker < tail) p[head + 4 * n4 + worker] = 0.0f;
+    float4* q = reinterpret_cast<float4*>(p + head);
+    for (int64_t i = worker; i < n4; i += n_workers) q[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // wave64 reductions with DPP row operations. Result valid in lane 63; use
 // wave_sum_uniform() for a wave-uniform (scalar) value.

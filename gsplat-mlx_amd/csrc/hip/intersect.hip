@@ -177,13 +177,6 @@ __global__ void __launch_bounds__(256) depth_keys_kernel(const float* __restrict
   idx[i] = static_cast<int32_t>(i);
 }
 
-__global__ void __launch_bounds__(256) gather_counts_kernel(const int32_t* __restrict__ counts,
-                                                            const int32_t* __restrict__ perm, int64_t n,
-                                                            int32_t* __restrict__ out) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) out[i] = counts[perm[i]];
-}
-
 // Encode in depth order: a block owns kEncodeG consecutive ranks (pairs
 // perm[rank]) and their contiguous output range (offsets over ranks), found
 // per output slot by binary search as in encode_kernel.
@@ -451,14 +444,10 @@ extern "C" int gsplat_hip_isect_depth_order(const float* depths, const int32_t* 
     depth_keys_kernel<<<grid_for(numel, 256), 256, 0, s>>>(depths, numel, l.dkeys, l.didx);
   }
   if ((rc = check_launch(what))) return rc;
+  // the last pass also gathers the counts into depth order
   if ((rc = radix_sort_pairs<uint32_t>(l.dkeys, l.didx, numel, 0, 32, l.dkeys_sorted, perm, l.sort_ws,
-                                       l.sort_ws_bytes, s, what)))
+                                       l.sort_ws_bytes, s, what, nullptr, nullptr, tiles_per_gauss, offsets)))
     return rc;
-  {
-    KernelTimer timer("isect_gather_counts", s);
-    gather_counts_kernel<<<grid_for(numel, 256), 256, 0, s>>>(tiles_per_gauss, perm, numel, offsets);
-  }
-  if ((rc = check_launch(what))) return rc;
   return scan_exclusive_i32(offsets, offsets, numel, nullptr, l.scan_ws, s);
 }
 

@@ -209,9 +209,16 @@ constexpr int kHistRowsPerAdd = 32;
 template <typename K>
 __global__ void __launch_bounds__(kSortBlock) hist_partial_kernel(const K* __restrict__ keys, int64_t n,
                                                                   int bit_lo, int passes,
-                                                                  uint32_t* __restrict__ partial) {
+                                                                  uint32_t* __restrict__ partial,
+                                                                  uint32_t* __restrict__ clear, int64_t clear_words) {
   __shared__ uint32_t h[kMaxPasses][kRadix];
   const int t = threadIdx.x;
+  // the totals the add kernel accumulates into, the error word and the
+  // passes' look-back words start at zero (cleared here instead of a launch
+  // of its own; the kernels that use them run after this one)
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kSortBlock + t; i < clear_words;
+       i += static_cast<int64_t>(gridDim.x) * kSortBlock)
+    clear[i] = 0u;
   for (int p = 0; p < passes; ++p) h[p][t] = 0;
   __syncthreads();
   const int64_t n_parts = (n + kOsTile - 1) / kOsTile;
@@ -244,18 +251,20 @@ __global__ void __launch_bounds__(kSortBlock) hist_add_kernel(const uint32_t* __
   if (sum) atomicAdd(&hist[p * kRadix + t], sum);
 }
 
-// Where a pass writes: keys and values, or (ids set, 32-bit keys, last pass
-// of the intersection sort) 64-bit ids key << 32 | depth bits of the value's
-// pair plus the values.
+// Where a pass writes: keys and values; or (ASM, 32-bit keys, last pass of
+// the intersection sort) 64-bit ids key << 32 | depth bits of the value's
+// pair plus the values; GATHER adds gather[value] at the same position.
 template <typename K>
 struct OsOut {
   K* keys;
   int32_t* vals;
-  const float* depths;
+  const float* depths;    // ASM: ids = key << 32 | bits of depths[value]
   int64_t* ids;
+  const int32_t* gather;  // GATHER: gathered = gather[value] beside the keys
+  int32_t* gathered;
 };
 
-template <typename K, bool ASM>
+template <typename K, bool ASM, bool GATHER>
 __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restrict__ keys_in,
                                                               const int32_t* __restrict__ vals_in, int64_t n,
                                                               int shift, const uint32_t* __restrict__ hist,
@@ -408,6 +417,7 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
     } else {
       out.keys[dst] = key;
     }
+    if constexpr (GATHER) out.gathered[dst] = out.gather[val];
     out.vals[dst] = val;
   }
 }
@@ -480,6 +490,21 @@ int assemble(const K* keys, const int32_t* vals, const float* depths, int64_t n,
   return check_launch(what);
 }
 
+// out[i] = src[idx[i]].
+__global__ void __launch_bounds__(256) gather_kernel(const int32_t* __restrict__ idx, const int32_t* __restrict__ src,
+                                                     int64_t n, int32_t* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i < n) out[i] = src[idx[i]];
+}
+
+int gather(const int32_t* idx, const int32_t* src, int64_t n, int32_t* out, hipStream_t s, const char* what) {
+  {
+    KernelTimer timer("sort_gather", s);
+    gather_kernel<<<grid_for(n, 256), 256, 0, s>>>(idx, src, n, out);
+  }
+  return check_launch(what);
+}
+
 }  // namespace
 
 template <typename K>
@@ -490,9 +515,10 @@ size_t radix_sort_workspace_bytes(int64_t n) {
 template <typename K>
 int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bit_lo, int bit_hi, K* keys_out,
                      int32_t* vals_out, void* workspace, size_t workspace_bytes, hipStream_t s, const char* what,
-                     const float* asm_depths, int64_t* asm_ids) {
+                     const float* asm_depths, int64_t* asm_ids, const int32_t* gather_src, int32_t* gather_dst) {
   const std::string w(what);
   if (asm_ids && (sizeof(K) != 4 || !asm_depths)) return invalid(w + ": invalid sort arguments.");
+  if (gather_dst && (asm_ids || !gather_src)) return invalid(w + ": invalid sort arguments.");
   if (n < 0 || bit_lo < 0 || bit_hi > static_cast<int>(8 * sizeof(K)) || bit_lo > bit_hi)
     return invalid(w + ": invalid sort arguments.");
   if (n == 0) return GSPLAT_OK;
@@ -505,6 +531,7 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
       copy_kernel<K><<<grid_for(n, 256), 256, 0, s>>>(keys_in, vals_in, n, keys_out, vals_out);
     }
     if (asm_ids) return assemble(keys_out, vals_out, asm_depths, n, asm_ids, s, what);
+    if (gather_dst) return gather(vals_out, gather_src, n, gather_dst, s, what);
     return check_launch(what);
   }
   SortWorkspace<K> ws;
@@ -515,15 +542,14 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
   if (n < kOnesweepMaxKeys) {
     const int64_t n_parts = (n + kOsTile - 1) / kOsTile;
     // histograms, error word and this sort's look-back words start at zero
-    const int64_t clear = reinterpret_cast<char*>(ws.os_lookback + passes * n_parts * kRadix) -
-                          reinterpret_cast<char*>(ws.os_hist);
-    int rc = fill_zero(ws.os_hist, clear, s);
-    if (rc) return rc;
+    const int64_t clear_words = (reinterpret_cast<char*>(ws.os_lookback + passes * n_parts * kRadix) -
+                                 reinterpret_cast<char*>(ws.os_hist)) / 4;
+    int rc;
     {
       KernelTimer timer("sort_histogram", s);
       const int hb = static_cast<int>(std::min<int64_t>(n_parts, kHistBlocks));
-      hist_partial_kernel<K><<<static_cast<unsigned>(hb), kSortBlock, 0, s>>>(keys_in, n, bit_lo, passes,
-                                                                              ws.os_partial);
+      hist_partial_kernel<K><<<static_cast<unsigned>(hb), kSortBlock, 0, s>>>(
+          keys_in, n, bit_lo, passes, ws.os_partial, ws.os_hist, clear_words);
       const dim3 add_grid((hb + kHistRowsPerAdd - 1) / kHistRowsPerAdd, passes);
       hist_add_kernel<<<add_grid, kSortBlock, 0, s>>>(ws.os_partial, hb, ws.os_hist);
     }
@@ -536,23 +562,28 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
       int32_t* dst_v = to_out ? vals_out : ws.vals_alt;
       {
         KernelTimer timer("sort_onesweep", s);
-        const OsOut<K> o{dst_k, dst_v, asm_depths, asm_ids};
+        const bool last = p == passes - 1;
+        const OsOut<K> o{dst_k, dst_v, asm_depths, asm_ids, gather_src, gather_dst};
         const unsigned grid = static_cast<unsigned>(n_parts);
+        const uint32_t* hist_p = ws.os_hist + p * kRadix;
+        uint32_t* look_p = ws.os_lookback + p * n_parts * kRadix;
+        const int shift = bit_lo + 8 * p;
         bool launched = false;
         if constexpr (sizeof(K) == 4) {
-          if (asm_ids && p == passes - 1) {
-            onesweep_kernel<K, true><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, bit_lo + 8 * p,
-                                                                 ws.os_hist + p * kRadix,
-                                                                 ws.os_lookback + p * n_parts * kRadix, ws.os_error,
-                                                                 o);
+          if (last && asm_ids) {
+            onesweep_kernel<K, true, false><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, shift, hist_p, look_p,
+                                                                        ws.os_error, o);
             launched = true;
           }
         }
-        if (!launched) {
-          onesweep_kernel<K, false><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, bit_lo + 8 * p,
-                                                                ws.os_hist + p * kRadix,
-                                                                ws.os_lookback + p * n_parts * kRadix, ws.os_error, o);
+        if (!launched && last && gather_dst) {
+          onesweep_kernel<K, false, true><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, shift, hist_p, look_p,
+                                                                      ws.os_error, o);
+          launched = true;
         }
+        if (!launched)
+          onesweep_kernel<K, false, false><<<grid, kSortBlock, 0, s>>>(src_k, src_v, n, shift, hist_p, look_p,
+                                                                       ws.os_error, o);
       }
       if ((rc = check_launch(what))) return rc;
       src_k = dst_k;
@@ -588,15 +619,18 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
     src_v = dst_v;
   }
   if (asm_ids) return assemble(keys_out, vals_out, asm_depths, n, asm_ids, s, what);
+  if (gather_dst) return gather(vals_out, gather_src, n, gather_dst, s, what);
   return GSPLAT_OK;
 }
 
 template size_t radix_sort_workspace_bytes<uint32_t>(int64_t);
 template size_t radix_sort_workspace_bytes<uint64_t>(int64_t);
 template int radix_sort_pairs<uint32_t>(const uint32_t*, const int32_t*, int64_t, int, int, uint32_t*, int32_t*,
-                                        void*, size_t, hipStream_t, const char*, const float*, int64_t*);
+                                        void*, size_t, hipStream_t, const char*, const float*, int64_t*,
+                                        const int32_t*, int32_t*);
 template int radix_sort_pairs<uint64_t>(const uint64_t*, const int32_t*, int64_t, int, int, uint64_t*, int32_t*,
-                                        void*, size_t, hipStream_t, const char*, const float*, int64_t*);
+                                        void*, size_t, hipStream_t, const char*, const float*, int64_t*,
+                                        const int32_t*, int32_t*);
 
 }  // namespace gsplat_hip
 

@@ -659,7 +659,8 @@ template <int CH>
 __global__ void __launch_bounds__(256) tile_cost_kernel(RasterArgs a, const int32_t* __restrict__ last_ids,
                                                         const float* __restrict__ render_alphas,
                                                         const float* __restrict__ v_render_colors,
-                                                        int32_t* __restrict__ cost, float* __restrict__ bg_part) {
+                                                        int32_t* __restrict__ cost, float* __restrict__ bg_part,
+                                                        ZeroSpans zero) {
   constexpr int LC = CH > 0 ? CH : 1;
   __shared__ int s_best[256 / kWave];
   __shared__ float s_sum[256 / kWave][LC];
@@ -670,6 +671,9 @@ __global__ void __launch_bounds__(256) tile_cost_kernel(RasterArgs a, const int3
   const int64_t unit = image * n_tiles + tile;
   const int t = threadIdx.x;
   const int channels = CH > 0 ? CH : a.channels;
+  // the backward's accumulated outputs start at zero: cleared here, one
+  // launch ahead of the kernel that accumulates into them
+  zero_spans_share(zero, unit * 256 + t, static_cast<int64_t>(a.I) * n_tiles * 256);
   int64_t start, end;
   tile_range(a, image, tile, &start, &end);
   const bool live = !(a.masks && !a.masks[unit]);
@@ -898,17 +902,16 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   if (backgrounds && !v_backgrounds) return invalid("rasterize_to_pixels_3dgs_backward: null v_backgrounds.");
   hipStream_t s = as_stream(stream);
   const int64_t G = I * N;
-  // outputs are accumulated: clear them first
-  {
-    const ZeroSpan spans[] = {{v_means2d, G * 2},
-                              {v_conics, G * 3},
-                              {v_colors, G * channels},
-                              {v_opacities, G},
-                              {v_means2d_abs, v_means2d_abs ? G * 2 : 0},
-                              {v_backgrounds, backgrounds ? I * channels : 0}};
-    if ((rc = fill_zero_spans(spans, 6, s))) return rc;
-  }
-  if (I == 0 || tile_width == 0 || tile_height == 0) return GSPLAT_OK;
+  // outputs are accumulated from zero; the schedule kernel clears them
+  // (v_backgrounds is written whole by the order kernel)
+  const ZeroSpan spans[] = {{v_means2d, G * 2},
+                            {v_conics, G * 3},
+                            {v_colors, G * channels},
+                            {v_opacities, G},
+                            {v_means2d_abs, v_means2d_abs ? G * 2 : 0},
+                            {v_backgrounds, backgrounds ? I * channels : 0}};
+  if (I == 0 || tile_width == 0 || tile_height == 0) return fill_zero_spans(spans, 6, s);
+  const ZeroSpans zero = pack_zero_spans(spans, 5);
   const dim3 grid(tile_width, tile_height, static_cast<unsigned>(I));
   if (!tile_offsets || !render_alphas || !last_ids || !v_render_colors || !v_render_alphas ||
       (n_isects > 0 && (!flatten_ids || !means2d || !conics || !colors || !opacities)))
@@ -928,11 +931,11 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   {
     KernelTimer timer("raster_bwd_schedule", s);
     switch (ch) {
-      case 1: tile_cost_kernel<1><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
-      case 2: tile_cost_kernel<2><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
-      case 3: tile_cost_kernel<3><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
-      case 4: tile_cost_kernel<4><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
-      default: tile_cost_kernel<0><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part); break;
+      case 1: tile_cost_kernel<1><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part, zero); break;
+      case 2: tile_cost_kernel<2><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part, zero); break;
+      case 3: tile_cost_kernel<3><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part, zero); break;
+      case 4: tile_cost_kernel<4><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part, zero); break;
+      default: tile_cost_kernel<0><<<grid, 256, 0, s>>>(a, last_ids, render_alphas, v_render_colors, cost, bg_part, zero); break;
     }
     // block 0 orders the tiles; one more block per (image, channel) sums the background partials
     const unsigned order_blocks = 1 + (backgrounds ? static_cast<unsigned>(I * channels) : 0u);
