@@ -177,55 +177,104 @@ __global__ void __launch_bounds__(256) depth_keys_kernel(const float* __restrict
   idx[i] = static_cast<int32_t>(i);
 }
 
-// Encode in depth order: a block owns kEncodeG consecutive ranks (pairs
-// perm[rank]) and their contiguous output range (offsets over ranks), found
-// per output slot by binary search as in encode_kernel.
+// Encode in depth order, balanced over ranks and outputs alike ("merge
+// path"): the ranks' output starts (offsets, non-decreasing) and the output
+// slots 0..n_isects-1 form one merged sequence of numel + n_isects items, rank
+// r placed before slot j when offsets[r] <= j. Block b takes items
+// [b K, (b+1) K): at most K slots and K ranks (plus the rank already open at
+// its first slot), whatever the per-Gaussian counts, so one Gaussian with
+// thousands of tiles no longer holds one block for the whole launch.
+
+constexpr int kMergeItems = 1024;  // merged items per block
+constexpr int kMergeOuts = kMergeItems / kEncodeBlock;  // slots per thread (at most)
+
+// First r in [0, R] with offs[r] + r >= d (offs[R] + R taken as M + R), found
+// by one wave in 64-way steps; every lane returns it.
+__device__ int64_t merge_split(const int32_t* __restrict__ offs, int64_t R, int64_t M, int64_t d, int lane) {
+  int64_t lo = max<int64_t>(0, d - M), hi = min<int64_t>(d, R);
+  while (hi > lo) {
+    const int64_t step = (hi - lo + kWave - 1) / kWave;
+    const int64_t p = min<int64_t>(lo + lane * step, hi);
+    const int64_t f = p == R ? M + R : static_cast<int64_t>(offs[p]) + p;
+    const uint64_t b = __ballot(f >= d);
+    if (b == 0) {
+      lo = lo + (kWave - 1) * step + 1;  // after the last probe
+    } else {
+      const int first = __builtin_ctzll(b);
+      const int64_t p_first = min<int64_t>(lo + first * step, hi);
+      if (first > 0) lo = lo + (first - 1) * step + 1;
+      hi = p_first;
+    }
+  }
+  return min<int64_t>(lo, R);  // bounded even for offsets that are not a scan
+}
+
 __global__ void __launch_bounds__(kEncodeBlock) encode_presorted_kernel(
     const float* __restrict__ means2d, const int32_t* __restrict__ radii, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, int64_t numel, int64_t n_per_image, int ts, int tw, int th, int tile_bits,
     int64_t n_isects, uint32_t* __restrict__ keys, int32_t* __restrict__ vals) {
-  __shared__ int32_t s_off[kEncodeG];
-  __shared__ int32_t s_minx[kEncodeG];
-  __shared__ int32_t s_miny[kEncodeG];
-  __shared__ int32_t s_w[kEncodeG];
-  __shared__ uint32_t s_hi[kEncodeG];  // image << tile_bits
-  __shared__ int32_t s_g[kEncodeG];
-  __shared__ int64_t s_end;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kEncodeG;
-  const int cnt = static_cast<int>(min<int64_t>(kEncodeG, numel - r0));
+  constexpr int kRanks = kMergeItems + 1;
+  __shared__ int32_t s_off[kRanks];
+  __shared__ int32_t s_minx[kRanks];
+  __shared__ int32_t s_miny[kRanks];
+  __shared__ int32_t s_w[kRanks];
+  __shared__ uint32_t s_hi[kRanks];  // image << tile_bits
+  __shared__ int32_t s_g[kRanks];
+  __shared__ int64_t s_split[2];
   const int t = threadIdx.x;
-  if (t < cnt) {
-    const int64_t g = perm[r0 + t];
-    const TileRect r = aabb_tile_rect(means2d[g * 2], means2d[g * 2 + 1], radii[g * 2], radii[g * 2 + 1], ts, tw, th);
-    const int32_t off = offsets[r0 + t];
-    s_off[t] = off;
-    s_minx[t] = r.min_x;
-    s_miny[t] = r.min_y;
-    s_w[t] = r.max_x - r.min_x;
-    s_hi[t] = static_cast<uint32_t>(g / n_per_image) << tile_bits;
-    s_g[t] = static_cast<int32_t>(g);
-    if (t == cnt - 1) s_end = static_cast<int64_t>(off) + (r.max_y - r.min_y) * (r.max_x - r.min_x);
+  const int lane = t % kWave;
+  const int wave = t / kWave;
+  const int64_t total = numel + n_isects;
+  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kMergeItems;
+  const int64_t d1 = min<int64_t>(d0 + kMergeItems, total);
+  if (wave < 2) {
+    const int64_t r = merge_split(offsets, numel, n_isects, wave == 0 ? d0 : d1, lane);
+    if (lane == 0) s_split[wave] = r;
   }
   __syncthreads();
-  const int64_t start = max<int64_t>(s_off[0], 0);
-  const int64_t end = min<int64_t>(s_end, n_isects);
-  for (int64_t o = start + t; o < end; o += kEncodeBlock) {
-    int lo = 0, hi = cnt - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_off[mid] <= o)
-        lo = mid;
-      else
-        hi = mid - 1;
-    }
-    const int j = lo;
-    const int k = static_cast<int>(o - s_off[j]);
-    const int w = max(s_w[j], 1);
+  const int64_t r0 = s_split[0], r1 = s_split[1];
+  const int64_t j0 = d0 - r0, j1 = d1 - r1;
+  // ranks [rs, r1): the rank open at slot j0 (r0 - 1) and the ones starting in the block
+  const int64_t rs = r0 > 0 ? r0 - 1 : 0;
+  const int nr = static_cast<int>(min<int64_t>(max<int64_t>(r1 - rs, 0), kRanks));
+  for (int i = t; i < nr; i += kEncodeBlock) {
+    const int64_t g = perm[rs + i];
+    TileRect rect = {0, 0, 0, 0};
+    if (g >= 0 && g < numel)
+      rect = aabb_tile_rect(means2d[g * 2], means2d[g * 2 + 1], radii[g * 2], radii[g * 2 + 1], ts, tw, th);
+    s_off[i] = offsets[rs + i];
+    s_minx[i] = rect.min_x;
+    s_miny[i] = rect.min_y;
+    s_w[i] = max(rect.max_x - rect.min_x, 1);
+    s_hi[i] = static_cast<uint32_t>(max<int64_t>(g, 0) / n_per_image) << tile_bits;
+    s_g[i] = static_cast<int32_t>(g);
+  }
+  __syncthreads();
+  if (nr == 0) return;
+  // thread t owns slots j0 + t * kMergeOuts .. + kMergeOuts - 1: one binary
+  // search for the first, then walk forward
+  const int64_t jb = j0 + static_cast<int64_t>(t) * kMergeOuts;
+  if (jb >= min<int64_t>(j1, n_isects)) return;
+  int lo = 0, hi = nr - 1;  // last i with s_off[i] <= jb
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_off[mid] <= jb)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  int i = lo;
+#pragma unroll
+  for (int q = 0; q < kMergeOuts; ++q) {
+    const int64_t j = jb + q;
+    if (j >= j1 || j >= n_isects) break;
+    while (i + 1 < nr && s_off[i + 1] <= j) ++i;
+    const int k = static_cast<int>(j - s_off[i]);
+    const int w = s_w[i];
     const int row = k / w;
     const int col = k - row * w;
-    const uint32_t tile = static_cast<uint32_t>((s_miny[j] + row) * tw + (s_minx[j] + col));
-    keys[o] = s_hi[j] | tile;
-    vals[o] = s_g[j];
+    keys[j] = s_hi[i] | static_cast<uint32_t>((s_miny[i] + row) * tw + (s_minx[i] + col));
+    vals[j] = s_g[i];
   }
 }
 
@@ -480,7 +529,7 @@ extern "C" int gsplat_hip_isect_encode_sorted(const float* means2d, const int32_
   hipStream_t s = as_stream(stream);
   {
     KernelTimer timer("isect_encode", s);
-    const int64_t nb = (numel + kEncodeG - 1) / kEncodeG;
+    const int64_t nb = (numel + n_isects + kMergeItems - 1) / kMergeItems;
     encode_presorted_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
         means2d, radii, perm, offsets, numel, numel / I, tile_size, tile_width, tile_height, tile_bits, n_isects,
         l.tkeys, l.tvals);
