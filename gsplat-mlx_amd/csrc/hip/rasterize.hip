@@ -2,7 +2,7 @@
 // gfx950.
 //
 // Forward: one block per (image, tile) with tile_size^2 lanes, one pixel per
-// lane (16x16 tiles -> 4 wave64s, each covering 16x4 pixels). The tile's
+// lane (16x16 tiles -> 4 wave64s, each covering an 8x8 block). The tile's
 // sorted Gaussian list is walked in batches of blockDim entries: each lane
 // gathers one Gaussian record (mean, conic, opacity, colors) into LDS and
 // tests it against every wave's pixel rectangle, then each wave evaluates
@@ -114,16 +114,43 @@ struct PixRect {
   float x0, x1, y0, y1;
 };
 
-// Bounding rectangle of the pixel centres owned by wave w of a tile whose
-// lanes map to pixels q = lane index within the tile (row-major, ts wide).
+// Lane -> pixel of a tile. When the tile side is a multiple of 8, each
+// wave64 owns an 8x8 block (waves row-major over the blocks); the square
+// footprint is touched by fewer Gaussians than a 16x4 strip of the same
+// area, so fewer records pass the per-wave cull. Other tile sides map lanes
+// row-major. Lanes past ts*ts (padding) map outside the tile.
+__device__ __forceinline__ void lane_pixel(int t, int ts, int* qx, int* qy) {
+  if ((ts & 7) == 0) {
+    const int w = t / kWave, l = t % kWave;
+    const int bpr = ts >> 3;  // 8x8 blocks per tile row
+    *qx = (w % bpr) * 8 + (l & 7);
+    *qy = (w / bpr) * 8 + (l >> 3);
+  } else {
+    *qx = t % ts;
+    *qy = t / ts;
+  }
+}
+
+// Bounding rectangle of the pixel centres owned by wave w (lane_pixel's map).
 __device__ __forceinline__ PixRect wave_rect(int w, int ts, int tx, int ty) {
-  const int q0 = w * kWave;
-  const int q1 = min(q0 + kWave, ts * ts) - 1;
-  const int r0 = q0 / ts, r1 = q1 / ts;
-  int c0 = 0, c1 = ts - 1;
-  if (r0 == r1) {
-    c0 = q0 % ts;
-    c1 = q1 % ts;
+  int c0, c1, r0, r1;
+  if ((ts & 7) == 0) {
+    const int bpr = ts >> 3;
+    c0 = (w % bpr) * 8;
+    c1 = c0 + 7;
+    r0 = (w / bpr) * 8;
+    r1 = r0 + 7;
+  } else {
+    const int q0 = w * kWave;
+    const int q1 = min(q0 + kWave, ts * ts) - 1;
+    r0 = q0 / ts;
+    r1 = q1 / ts;
+    c0 = 0;
+    c1 = ts - 1;
+    if (r0 == r1) {
+      c0 = q0 % ts;
+      c1 = q1 % ts;
+    }
   }
   PixRect r;
   r.x0 = static_cast<float>(tx * ts + c0) + 0.5f;
@@ -191,8 +218,10 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
   const int lane = t % kWave;
   const int wave = t / kWave;
   const int n_waves = BS / kWave;
-  const int x = tx * a.ts + t % a.ts;
-  const int y = ty * a.ts + t / a.ts;
+  int qx, qy;
+  lane_pixel(t, a.ts, &qx, &qy);
+  const int x = tx * a.ts + qx;
+  const int y = ty * a.ts + qy;
   // blocks are padded to whole wave64s; padding lanes own no pixel
   const bool inside = t < a.ts * a.ts && x < a.W && y < a.H;
   const int64_t pix = (image * a.H + y) * static_cast<int64_t>(a.W) + x;
@@ -459,8 +488,10 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
     };
     if (stop > start) fetch(stop, max<int64_t>(start, stop - BB));
 
-    const int x = tx * a.ts + t % a.ts;
-    const int y = ty * a.ts + t / a.ts;
+    int qx, qy;
+    lane_pixel(t, a.ts, &qx, &qy);
+    const int x = tx * a.ts + qx;
+    const int y = ty * a.ts + qy;
     const bool inside = t < a.ts * a.ts && x < a.W && y < a.H;
     const int64_t pix = (image * a.H + y) * static_cast<int64_t>(a.W) + x;
     const float px = static_cast<float>(x) + 0.5f;
