@@ -71,7 +71,7 @@ py::dict projection_ewa_3dgs_fused_backward(const TensorMap& inputs, const Tenso
   in.conics = require_key(forward_outputs, "conics");
   in.compensations = get_or_empty(forward_outputs, "compensations");
   in.v_means2d = require_key(cotangents, "v_means2d");
-  in.v_depths = require_key(cotangents, "v_depths");
+  in.v_depths = get_or_empty(cotangents, "v_depths");  // absent = zeros
   in.v_conics = require_key(cotangents, "v_conics");
   in.v_compensations = get_or_empty(cotangents, "v_compensations");
   const bool use_covars = in.covars.numel() != 0;
@@ -155,7 +155,7 @@ py::dict rasterize_to_pixels_3dgs_backward(const TensorMap& inputs, const Tensor
   in.render_alphas = require_key(forward_outputs, "render_alphas");
   in.last_ids = require_key(forward_outputs, "last_ids");
   in.v_render_colors = require_key(cotangents, "v_render_colors");
-  in.v_render_alphas = require_key(cotangents, "v_render_alphas");
+  in.v_render_alphas = get_or_empty(cotangents, "v_render_alphas");  // absent = zeros
   in.backgrounds = get_or_empty(inputs, "backgrounds");
   in.masks = get_or_empty(inputs, "masks");
   in.params = {image_width, image_height, tile_size, in.backgrounds.numel() != 0, in.masks.numel() != 0,

@@ -144,9 +144,11 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA
   if (input.params.camera_model != 0)
     throw std::runtime_error("projection_ewa_3dgs_fused_backward currently supports pinhole only.");
   if (input.radii.scalar_type() != at::kInt) throw std::runtime_error("radii must be int32.");
+  // an empty v_depths stands for zeros (callers whose loss ignores depths)
+  const bool use_v_depths = !is_empty(input.v_depths);
   if (input.v_means2d.sizes().vec() != projection_shape(input.means, input.viewmats, 2) ||
       input.v_conics.sizes().vec() != projection_shape(input.means, input.viewmats, 3) ||
-      input.v_depths.sizes().vec() != projection_scalar_shape(input.means, input.viewmats))
+      (use_v_depths && input.v_depths.sizes().vec() != projection_scalar_shape(input.means, input.viewmats)))
     throw std::runtime_error("projection backward cotangent shape mismatch.");
   require_device(input.means, "means");
   require_device(input.viewmats, "viewmats");
@@ -172,7 +174,7 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA
   const array comps = use_comp ? contig(input.compensations.to(at::kFloat)) : array();
   const array v_comps = use_comp ? contig(input.v_compensations.to(at::kFloat)) : array();
   const array v_m2 = contig(input.v_means2d.to(at::kFloat));
-  const array v_dep = contig(input.v_depths.to(at::kFloat));
+  const array v_dep = use_v_depths ? contig(input.v_depths.to(at::kFloat)) : array();
   const array v_con = contig(input.v_conics.to(at::kFloat));
   array v_means = at::empty(means.sizes(), f32_like(means));
   array v_covars = p.use_covars ? at::empty(covars.sizes(), f32_like(means)) : at::empty({0}, f32_like(means));
@@ -189,7 +191,8 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA
       p.use_covars ? nullptr : quats.data_ptr<float>(), p.use_covars ? nullptr : scales.data_ptr<float>(),
       viewmats.data_ptr<float>(), Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, radii.data_ptr<int32_t>(),
       conics.data_ptr<float>(), use_comp ? comps.data_ptr<float>() : nullptr, v_m2.data_ptr<float>(),
-      v_dep.data_ptr<float>(), v_con.data_ptr<float>(), use_comp ? v_comps.data_ptr<float>() : nullptr,
+      use_v_depths ? v_dep.data_ptr<float>() : nullptr, v_con.data_ptr<float>(),
+      use_comp ? v_comps.data_ptr<float>() : nullptr,
       v_means.data_ptr<float>(), p.use_covars ? v_covars.data_ptr<float>() : nullptr,
       p.use_covars ? nullptr : v_quats.data_ptr<float>(), p.use_covars ? nullptr : v_scales.data_ptr<float>(),
       input.viewmats_requires_grad ? v_viewmats.data_ptr<float>() : nullptr,

@@ -120,7 +120,9 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
   auto rc_shape = image_prefix(input.tile_offsets);
   rc_shape.insert(rc_shape.end(), {p.image_height, p.image_width, input.colors.size(-1)});
   if (input.v_render_colors.sizes().vec() != rc_shape) throw std::runtime_error("v_render_colors shape mismatch.");
-  if (input.v_render_alphas.sizes() != input.render_alphas.sizes())
+  // an empty v_render_alphas stands for zeros (losses on the colours only)
+  const bool use_v_ra = !is_empty(input.v_render_alphas);
+  if (use_v_ra && input.v_render_alphas.sizes() != input.render_alphas.sizes())
     throw std::runtime_error("v_render_alphas shape mismatch.");
   require_inputs(fwd);
   const Layout l = layout_of(fwd);
@@ -130,7 +132,7 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
   require_device(input.render_alphas, "render_alphas");
   require_device(input.last_ids, "last_ids");
   require_device(input.v_render_colors, "v_render_colors");
-  require_device(input.v_render_alphas, "v_render_alphas");
+  if (use_v_ra) require_device(input.v_render_alphas, "v_render_alphas");
   require_dtype(input.last_ids, at::kInt, "last_ids must be int32.");
   const c10::DeviceGuard guard(input.means2d.device());
   const array means2d = contig(input.means2d), conics = contig(input.conics), colors = contig(input.colors);
@@ -138,7 +140,8 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
   const array bg = p.use_backgrounds ? contig(input.backgrounds.to(at::kFloat)) : array();
   const array masks = p.use_masks ? mask_u8(input.masks) : array();
   const array ra = contig(input.render_alphas.to(at::kFloat)), li = contig(input.last_ids);
-  const array v_rc = contig(input.v_render_colors.to(at::kFloat)), v_ra = contig(input.v_render_alphas.to(at::kFloat));
+  const array v_rc = contig(input.v_render_colors.to(at::kFloat));
+  const array v_ra = use_v_ra ? contig(input.v_render_alphas.to(at::kFloat)) : array();
   array v_abs = input.absgrad ? at::empty(means2d.sizes(), f32_like(means2d)) : at::empty({0}, f32_like(means2d));
   array v_m2 = at::empty(means2d.sizes(), f32_like(means2d));
   array v_con = at::empty(conics.sizes(), f32_like(means2d));
@@ -152,7 +155,8 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
       p.use_backgrounds ? bg.data_ptr<float>() : nullptr, p.use_masks ? masks.data_ptr<uint8_t>() : nullptr,
       offsets.data_ptr<int32_t>(), flat.data_ptr<int32_t>(), l.I, l.N, l.channels, p.image_width, p.image_height,
       p.tile_size, l.tw, l.th, flat.numel(), ra.data_ptr<float>(), li.data_ptr<int32_t>(), v_rc.data_ptr<float>(),
-      v_ra.data_ptr<float>(), input.absgrad ? v_abs.data_ptr<float>() : nullptr, v_m2.data_ptr<float>(),
+      use_v_ra ? v_ra.data_ptr<float>() : nullptr, input.absgrad ? v_abs.data_ptr<float>() : nullptr,
+      v_m2.data_ptr<float>(),
       v_con.data_ptr<float>(), v_col.data_ptr<float>(), v_op.data_ptr<float>(),
       p.use_backgrounds ? v_bg.data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(), ws_bytes,
       stream_for(input.s, means2d)));

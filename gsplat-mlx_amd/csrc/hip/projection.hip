@@ -415,7 +415,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
       float mc[3];
       world_to_cam(f, mw, mc);
       const Mat3 cc = mat3_mul(mat3_mul(f.R, cw), mat3_tr(f.R));
-      float v_mc[3] = {0.0f, 0.0f, v_depths[idx]};
+      float v_mc[3] = {0.0f, 0.0f, v_depths ? v_depths[idx] : 0.0f};
       const float vm2[2] = {v_means2d[idx * 2], v_means2d[idx * 2 + 1]};
       Mat3 v_cc;
       persp_proj_vjp(mc, cc, f, p.image_width, p.image_height, v_cov2d, vm2, v_mc, v_cc);
@@ -552,7 +552,7 @@ extern "C" int gsplat_hip_projection_bwd(const float* means, const float* covars
     if (v_viewmats && B * C > 0) return fill_zero(v_viewmats, B * C * 16 * sizeof(float), s);
     return GSPLAT_OK;
   }
-  if (!means || !viewmats || !Ks || !radii || !conics || !v_means2d || !v_depths || !v_conics || !v_means)
+  if (!means || !viewmats || !Ks || !radii || !conics || !v_means2d || !v_conics || !v_means)
     return invalid("projection_ewa_3dgs_fused_backward: null pointer.");
   if (p.use_covars ? (!covars || !v_covars) : (!quats || !scales || !v_quats || !v_scales))
     return invalid("projection_ewa_3dgs_fused_backward expects covars or quats+scales.");

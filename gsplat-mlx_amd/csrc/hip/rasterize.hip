@@ -507,7 +507,7 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
     float v_rc[AC];
     float bg_dot = 0.0f;
     for (int c = 0; c < channels; ++c) v_rc[c] = inside ? v_render_colors[pix * channels + c] : 0.0f;
-    const float v_ra = inside ? v_render_alphas[pix] : 0.0f;
+    const float v_ra = inside && v_render_alphas ? v_render_alphas[pix] : 0.0f;
     if (a.backgrounds) {
       const float* bg = a.backgrounds + image * channels;
       for (int c = 0; c < channels; ++c) bg_dot += bg[c] * v_rc[c];
@@ -944,7 +944,7 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
   if (I == 0 || tile_width == 0 || tile_height == 0) return fill_zero_spans(spans, 6, s);
   const ZeroSpans zero = pack_zero_spans(spans, 5);
   const dim3 grid(tile_width, tile_height, static_cast<unsigned>(I));
-  if (!tile_offsets || !render_alphas || !last_ids || !v_render_colors || !v_render_alphas ||
+  if (!tile_offsets || !render_alphas || !last_ids || !v_render_colors ||
       (n_isects > 0 && (!flatten_ids || !means2d || !conics || !colors || !opacities)))
     return invalid("rasterize_to_pixels_3dgs_backward: null pointer.");
   const int ch = channels <= 4 ? channels : 0;

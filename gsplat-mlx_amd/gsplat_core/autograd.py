@@ -37,6 +37,7 @@ def _nonempty(t):
 class _QuatScaleToCovarPreci(torch.autograd.Function):
     @staticmethod
     def forward(ctx, quats, scales, compute_covar, compute_preci, triu):
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
         out = _C.quat_scale_to_covar_preci_forward({"quats": quats, "scales": scales}, compute_covar, compute_preci,
                                                    triu)
         ctx.save_for_backward(quats, scales)
@@ -67,6 +68,7 @@ class _ProjectionEWA3DGSFused(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means, covars, quats, scales, opacities, viewmats, Ks, viewspace_points, image_width,
                 image_height, eps2d, near_plane, far_plane, radius_clip, calc_compensations, camera_model):
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
         inputs = {"means": means, "viewmats": viewmats, "Ks": Ks}
         for k, v in (("covars", covars), ("quats", quats), ("scales", scales), ("opacities", opacities),
                      ("viewspace_points", viewspace_points)):
@@ -88,7 +90,7 @@ class _ProjectionEWA3DGSFused(torch.autograd.Function):
             raise RuntimeError("GSPlatProjectionEWA3DGSFused vjp currently supports pinhole only.")
         shape2 = radii.shape
         v_means2d = torch.zeros(shape2, dtype=torch.float32, device=means.device) if v_means2d is None else v_means2d
-        v_depths = torch.zeros(shape2[:-1], dtype=torch.float32, device=means.device) if v_depths is None else v_depths
+        v_depths = _empty(means) if v_depths is None else v_depths  # empty = zeros
         v_conics = (torch.zeros(conics.shape, dtype=torch.float32, device=means.device) if v_conics is None
                     else v_conics)
         inputs = {"means": means, "viewmats": viewmats, "Ks": Ks}
@@ -98,8 +100,9 @@ class _ProjectionEWA3DGSFused(torch.autograd.Function):
             inputs["quats"] = quats
             inputs["scales"] = scales
         fwd = {"radii": radii, "conics": conics}
-        cot = {"v_means2d": v_means2d.contiguous(), "v_depths": v_depths.contiguous(),
-               "v_conics": v_conics.contiguous()}
+        cot = {"v_means2d": v_means2d.contiguous(), "v_conics": v_conics.contiguous()}
+        if v_depths.numel():
+            cot["v_depths"] = v_depths.contiguous()
         if calc_comp:
             fwd["compensations"] = comps
             cot["v_compensations"] = (torch.zeros_like(comps) if v_compensations is None
@@ -134,6 +137,7 @@ def projection_ewa_3dgs_fused(means, viewmats, Ks, image_width, image_height, qu
 class _SphericalHarmonics(torch.autograd.Function):
     @staticmethod
     def forward(ctx, degrees_to_use, dirs, coeffs, masks):
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
         inputs = {"dirs": dirs, "coeffs": coeffs}
         if _nonempty(masks):
             inputs["masks"] = masks
@@ -166,6 +170,7 @@ class _ShCameraColors(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, degrees_to_use, means, campos, features_dc, features_rest):
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
         inputs = {"means": means, "campos": campos, "features_dc": features_dc, "features_rest": features_rest}
         colors = _C.sh_camera_colors_forward(degrees_to_use, inputs)
         ctx.save_for_backward(means, campos, features_dc, features_rest)
@@ -191,6 +196,7 @@ class _RasterizeToPixels3DGS(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, image_width,
                 image_height, tile_size):
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
         inputs = {"means2d": means2d, "conics": conics, "colors": colors, "opacities": opacities,
                   "tile_offsets": tile_offsets, "flatten_ids": flatten_ids}
         if _nonempty(backgrounds):
@@ -219,12 +225,11 @@ class _RasterizeToPixels3DGS(torch.autograd.Function):
         if v_render_colors is None:
             v_render_colors = torch.zeros(render_alphas.shape[:-1] + (colors.shape[-1],), dtype=torch.float32,
                                           device=colors.device)
-        if v_render_alphas is None:
-            v_render_alphas = torch.zeros_like(render_alphas)
+        cot = {"v_render_colors": v_render_colors.contiguous()}
+        if v_render_alphas is not None:  # absent = zeros
+            cot["v_render_alphas"] = v_render_alphas.contiguous()
         out = _C.rasterize_to_pixels_3dgs_backward(
-            inputs, {"render_alphas": render_alphas, "last_ids": last_ids},
-            {"v_render_colors": v_render_colors.contiguous(), "v_render_alphas": v_render_alphas.contiguous()},
-            W, H, ts, False)
+            inputs, {"render_alphas": render_alphas, "last_ids": last_ids}, cot, W, H, ts, False)
         return (out["v_means2d"], out["v_conics"], out["v_colors"], out["v_opacities"],
                 out["v_backgrounds"] if use_bg else None, None, None, None, None, None, None)
 
@@ -243,6 +248,7 @@ def rasterize_to_pixels_3dgs(means2d, conics, colors, opacities, tile_offsets, f
 class _GaussianActivations(torch.autograd.Function):
     @staticmethod
     def forward(ctx, quats, log_scales, opacity_logits):
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
         out = _C.gaussian_activations_forward({"quats": quats, "log_scales": log_scales,
                                                "opacity_logits": opacity_logits})
         ctx.save_for_backward(quats, out["scales"], out["opacities"])
@@ -277,6 +283,7 @@ def gaussian_activations(quats, log_scales, opacity_logits):
 class _L1Loss(torch.autograd.Function):
     @staticmethod
     def forward(ctx, image, target):
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
         ctx.save_for_backward(image, target)
         return _C.l1_loss_forward(image, target)
 

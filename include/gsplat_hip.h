@@ -105,7 +105,9 @@ int gsplat_hip_projection_fwd(const float* means, const float* covars, const flo
  * covars [B,N,6] or quats [B,N,4] + scales [B,N,3] (the other pair NULL);
  * v_viewmats [B,C,4,4] when non-NULL (needs a workspace of
  * gsplat_hip_projection_bwd_workspace_size bytes, else workspace may be NULL).
- * compensations / v_compensations are NULL unless calc_compensations. */
+ * compensations / v_compensations are NULL unless calc_compensations.
+ * v_depths may be NULL, meaning zeros (the reference always passes an
+ * array; NULL saves the caller a zero fill when its loss ignores depth). */
 size_t gsplat_hip_projection_bwd_workspace_size(int64_t B, int64_t C, int64_t N,
                                                 int32_t viewmats_grad);
 int gsplat_hip_projection_bwd(const float* means, const float* covars, const float* quats,
@@ -253,7 +255,8 @@ int gsplat_hip_isect_offset(const int64_t* isect_ids, int64_t n_isects, int32_t 
  * Forward outputs: render_colors [I,H,W,channels], render_alphas [I,H,W],
  * last_ids [I,H,W]. Backward outputs (accumulated over all pixels):
  * v_means2d_abs (NULL unless absgrad), v_means2d, v_conics, v_colors,
- * v_opacities, v_backgrounds (NULL unless backgrounds).
+ * v_opacities, v_backgrounds (NULL unless backgrounds). The backward's
+ * v_render_alphas may be NULL, meaning zeros (losses on the colours only).
  * ------------------------------------------------------------------------- */
 int gsplat_hip_rasterize_fwd(const float* means2d, const float* conics, const float* colors,
                              const float* opacities, const float* backgrounds,

@@ -182,6 +182,13 @@ def test_projection_backward_vs_oracle(oracle, use_covars, calc_comp, C):
                                    v_compensations=vcomp if calc_comp else None, viewmats_requires_grad=True)
     for k in e:
         assert_close_rel(host(out[k]), e[k], GRAD_RTOL, k)
+    # an absent v_depths means zeros
+    cot0 = dict(cot, v_depths=dev(np.zeros_like(vd)))
+    cot_absent = {k: v for k, v in cot.items() if k != "v_depths"}
+    a = g.projection_ewa_3dgs_fused_backward(inputs, fwd, cot0, 320, 240, viewmats_requires_grad=True)
+    b = g.projection_ewa_3dgs_fused_backward(inputs, fwd, cot_absent, 320, 240, viewmats_requires_grad=True)
+    for k in a:
+        np.testing.assert_allclose(host(b[k]), host(a[k]), rtol=1e-6, atol=1e-30, err_msg=k)
 
 
 # ------------------------------------------------------------------------- SH

@@ -125,6 +125,14 @@ def test_forward_backward_vs_oracle(oracle, I, N, W, H, ts, C, masks, opac):
                                 backgrounds=s["backgrounds"], masks=s.get("masks"), absgrad=True)
     for k in ("v_means2d", "v_conics", "v_colors", "v_opacities", "v_backgrounds", "v_means2d_abs"):
         assert_close_rel(host(bwd[k]), eb[k], GRAD_RTOL, k)
+    if I == 1 and C == 3 and not masks:
+        # an absent v_render_alphas means zeros
+        fo = {"render_alphas": got["render_alphas"], "last_ids": got["last_ids"]}
+        z = g.rasterize_to_pixels_3dgs_backward(_raster_inputs(s), fo, {"v_render_colors": dev(v_rc),
+                                                                        "v_render_alphas": dev(0 * v_ra)}, W, H, ts)
+        n = g.rasterize_to_pixels_3dgs_backward(_raster_inputs(s), fo, {"v_render_colors": dev(v_rc)}, W, H, ts)
+        for k in ("v_means2d", "v_conics", "v_colors", "v_opacities", "v_backgrounds"):
+            assert_close_rel(host(n[k]), host(z[k]), 1e-5, k)
 
 
 def test_empty_lists_and_no_background(oracle):
