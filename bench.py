@@ -131,6 +131,7 @@ def main():
     target = torch.from_numpy(scene.target).to(dev) if scene.target is not None else None
     W, H, ts = scene.width, scene.height, scene.tile_size
     forward_only = target is None
+    seed = torch.ones((), device=dev)
 
     def step():
         for p in params + [viewspace]:
@@ -146,7 +147,7 @@ def main():
                                      far_plane=scene.far_plane)
         if not forward_only:
             loss = R.l1_loss(out["render_colors"], target)
-            loss.backward()
+            loss.backward(seed)  # d loss / d loss = 1, allocated once
         return out
 
     prof = Profiler()

@@ -234,13 +234,13 @@ py::dict quat_scale_to_covar_preci_backward(const TensorMap& inputs, const Tenso
 // surface; see gsplat_sh_camera_colors_forward).
 at::Tensor sh_camera_colors_forward(int degrees_to_use, const TensorMap& inputs) {
   return gsplat_core::gsplat_sh_camera_colors_forward(
-      degrees_to_use, require_key(inputs, "means"), require_key(inputs, "campos"), require_key(inputs, "features_dc"),
+      degrees_to_use, require_key(inputs, "means"), require_key(inputs, "viewmats"), require_key(inputs, "features_dc"),
       require_key(inputs, "features_rest"));
 }
 
 py::dict sh_camera_colors_backward(int degrees_to_use, const TensorMap& inputs, const TensorMap& cotangents) {
   auto out = gsplat_core::gsplat_sh_camera_colors_backward(
-      degrees_to_use, require_key(inputs, "means"), require_key(inputs, "campos"), require_key(inputs, "features_dc"),
+      degrees_to_use, require_key(inputs, "means"), require_key(inputs, "viewmats"), require_key(inputs, "features_dc"),
       require_key(inputs, "features_rest"), require_key(cotangents, "v_colors"));
   py::dict r;
   r["v_means"] = out[0];

@@ -27,28 +27,29 @@ struct CamDims {
   int64_t B, C, N, R;
 };
 
-CamDims validate_camera(const char* op, int degree, const array& means, const array& campos, const array& dc,
+CamDims validate_camera(const char* op, int degree, const array& means, const array& viewmats, const array& dc,
                         const array& rest) {
   const std::string o(op);
   if (degree < 0 || degree > 4) throw std::runtime_error(o + " supports degree 0..4.");
   if (means.dim() < 2 || means.size(-1) != 3) throw std::runtime_error("means must have shape [..., N, 3].");
-  if (campos.dim() < 2 || campos.size(-1) != 3) throw std::runtime_error("campos must have shape [..., C, 3].");
+  if (viewmats.dim() < 3 || viewmats.size(-1) != 4 || viewmats.size(-2) != 4)
+    throw std::runtime_error("viewmats must have shape [..., C, 4, 4].");
   if (dc.sizes() != means.sizes()) throw std::runtime_error("features_dc must have the shape of means.");
   if (rest.dim() != means.dim() + 1 || rest.size(-1) != 3)
     throw std::runtime_error("features_rest must have shape [..., N, R, 3].");
-  for (const array* a : {&means, &campos, &dc, &rest})
+  for (const array* a : {&means, &viewmats, &dc, &rest})
     if (a->scalar_type() != at::kFloat) throw std::runtime_error(o + " supports float32 arrays only.");
   CamDims d;
   d.N = means.size(-2);
   d.B = d.N > 0 ? means.numel() / (d.N * 3) : 0;
-  d.C = campos.size(-2);
+  d.C = viewmats.size(-3);
   d.R = rest.size(-2);
-  if (campos.numel() != d.B * d.C * 3) throw std::runtime_error("campos batch dimensions must match means.");
+  if (viewmats.numel() != d.B * d.C * 16) throw std::runtime_error("viewmats batch dimensions must match means.");
   if (rest.numel() != d.B * d.N * d.R * 3) throw std::runtime_error("features_rest batch dimensions must match means.");
   if (d.R < (degree + 1) * (degree + 1) - 1)
     throw std::runtime_error("features_rest has fewer SH bases than degrees_to_use requires.");
   require_device(means, "means");
-  require_device(campos, "campos");
+  require_device(viewmats, "viewmats");
   require_device(dc, "features_dc");
   require_device(rest, "features_rest");
   return d;
@@ -56,34 +57,34 @@ CamDims validate_camera(const char* op, int degree, const array& means, const ar
 
 }  // namespace
 
-array gsplat_sh_camera_colors_forward(int degree, const array& means_in, const array& campos_in, const array& dc_in,
+array gsplat_sh_camera_colors_forward(int degree, const array& means_in, const array& viewmats_in, const array& dc_in,
                                       const array& rest_in, StreamOrDevice s) {
-  const CamDims d = validate_camera("sh_camera_colors_forward", degree, means_in, campos_in, dc_in, rest_in);
+  const CamDims d = validate_camera("sh_camera_colors_forward", degree, means_in, viewmats_in, dc_in, rest_in);
   const c10::DeviceGuard guard(means_in.device());
-  const array means = contig(means_in), campos = contig(campos_in), dc = contig(dc_in), rest = contig(rest_in);
+  const array means = contig(means_in), viewmats = contig(viewmats_in), dc = contig(dc_in), rest = contig(rest_in);
   std::vector<int64_t> shape(means.sizes().begin(), means.sizes().end() - 2);
   shape.insert(shape.end(), {d.C, d.N, 3});
   array colors = at::empty(shape, f32_like(means));
-  check(gsplat_hip_sh_camera_colors_fwd(degree, means.data_ptr<float>(), campos.data_ptr<float>(),
+  check(gsplat_hip_sh_camera_colors_fwd(degree, means.data_ptr<float>(), viewmats.data_ptr<float>(),
                                         dc.data_ptr<float>(), d.R > 0 ? rest.data_ptr<float>() : nullptr, d.B, d.C,
                                         d.N, d.R, colors.data_ptr<float>(), stream_for(s, means)));
   return colors;
 }
 
-std::vector<array> gsplat_sh_camera_colors_backward(int degree, const array& means_in, const array& campos_in,
+std::vector<array> gsplat_sh_camera_colors_backward(int degree, const array& means_in, const array& viewmats_in,
                                                     const array& dc_in, const array& rest_in,
                                                     const array& v_colors_in, StreamOrDevice s) {
-  const CamDims d = validate_camera("sh_camera_colors_backward", degree, means_in, campos_in, dc_in, rest_in);
+  const CamDims d = validate_camera("sh_camera_colors_backward", degree, means_in, viewmats_in, dc_in, rest_in);
   if (v_colors_in.numel() != d.B * d.C * d.N * 3 || v_colors_in.scalar_type() != at::kFloat)
     throw std::runtime_error("v_colors must have shape [..., C, N, 3] (float32).");
   require_device(v_colors_in, "v_colors");
   const c10::DeviceGuard guard(means_in.device());
-  const array means = contig(means_in), campos = contig(campos_in), dc = contig(dc_in), rest = contig(rest_in);
+  const array means = contig(means_in), viewmats = contig(viewmats_in), dc = contig(dc_in), rest = contig(rest_in);
   const array v_colors = contig(v_colors_in);
   array v_means = at::empty(means.sizes(), f32_like(means));
   array v_dc = at::empty(dc.sizes(), f32_like(means));
   array v_rest = at::empty(rest.sizes(), f32_like(means));
-  check(gsplat_hip_sh_camera_colors_bwd(degree, means.data_ptr<float>(), campos.data_ptr<float>(),
+  check(gsplat_hip_sh_camera_colors_bwd(degree, means.data_ptr<float>(), viewmats.data_ptr<float>(),
                                         dc.data_ptr<float>(), d.R > 0 ? rest.data_ptr<float>() : nullptr,
                                         v_colors.data_ptr<float>(), d.B, d.C, d.N, d.R, v_means.data_ptr<float>(),
                                         v_dc.data_ptr<float>(), d.R > 0 ? v_rest.data_ptr<float>() : nullptr,

@@ -38,15 +38,16 @@ std::vector<array> gsplat_spherical_harmonics_backward(const SphericalHarmonicsB
 // Caller-side composition fused into one kernel per direction (no reference
 // counterpart as an operator; it is the glue of
 // scanner_points_training_utils.py:1005-1034): colors [B, C, N, 3] =
-// clamp(SH(normalize(means - campos[c]); [dc, rest]) + 0.5, 0, 1) for means
-// [B, N, 3], campos [B, C, 3], features_dc [B, N, 3], features_rest
-// [B, N, R, 3] (R >= (degree + 1)^2 - 1).
-array gsplat_sh_camera_colors_forward(int degree, const array& means, const array& campos, const array& features_dc,
+// clamp(SH(normalize(means - campos[c]); [dc, rest]) + 0.5, 0, 1) with
+// campos[c] = -R^T t of viewmats[c] = [R | t], for means [B, N, 3], viewmats
+// [B, C, 4, 4], features_dc [B, N, 3], features_rest [B, N, R, 3]
+// (R >= (degree + 1)^2 - 1).
+array gsplat_sh_camera_colors_forward(int degree, const array& means, const array& viewmats, const array& features_dc,
                                       const array& features_rest, StreamOrDevice s = {});
 
 // Gradients {v_means, v_features_dc, v_features_rest} of the above, summed
-// over cameras (campos gets none).
-std::vector<array> gsplat_sh_camera_colors_backward(int degree, const array& means, const array& campos,
+// over cameras (viewmats get none).
+std::vector<array> gsplat_sh_camera_colors_backward(int degree, const array& means, const array& viewmats,
                                                     const array& features_dc, const array& features_rest,
                                                     const array& v_colors, StreamOrDevice s = {});
 

@@ -341,7 +341,8 @@ __global__ void __launch_bounds__(kShBlock) sh_bwd_kernel(const float* __restric
 
 // ---------------------------------------------------------------------------
 // Camera colours from SH fused with the caller's glue
-// (scanner_points_training_utils.py:1005-1034): for every camera c,
+// (scanner_points_training_utils.py:1005-1034): for every camera c with
+// world-to-camera matrix [R | t] and centre campos[c] = -R^T t,
 //   d = means - campos[c],  n = d / max(|d|, 1e-8),
 //   colors[c] = clamp(SH(n; [dc, rest[:A-1]]) + 0.5, 0, 1),
 // without materialising the concatenated and camera-broadcast [C, N, K, 3]
@@ -405,6 +406,13 @@ __device__ __forceinline__ void sh_eval(const float d[3], const Co& co, float ou
   }
 }
 
+// Camera centre of world-to-camera matrix vm (row-major 4x4, [R | t]):
+// -R^T t, as camera_center_from_viewmat (scanner_points_training_utils.py:1005-1008).
+__device__ __forceinline__ void camera_centre(const float* __restrict__ vm, float cp[3]) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) cp[i] = -((vm[i] * vm[3] + vm[4 + i] * vm[7]) + vm[8 + i] * vm[11]);
+}
+
 // The caller's view direction: n = d / max(|d|, 1e-8) (NaN propagates as in
 // torch.clamp). Returns |d|.
 __device__ __forceinline__ float view_dir(const float* __restrict__ m, const float cp[3], float d[3], float n[3]) {
@@ -438,7 +446,7 @@ __device__ __forceinline__ float clamp01(float x) { return x < 0.0f ? 0.0f : (x 
 
 template <int DEG>
 __global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __restrict__ means,
-                                                              const float* __restrict__ campos,
+                                                              const float* __restrict__ viewmats,
                                                               const float* __restrict__ dc,
                                                               const float* __restrict__ rest, int64_t C, int64_t N,
                                                               int64_t R, uint32_t r3_magic,
@@ -463,7 +471,8 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __res
   const int64_t g = b * N + e0 + t;
   const float* co = sc + t * PW;
   for (int64_t c = 0; c < C; ++c) {
-    const float cp[3] = {campos[(b * C + c) * 3], campos[(b * C + c) * 3 + 1], campos[(b * C + c) * 3 + 2]};
+    float cp[3];
+    camera_centre(viewmats + (b * C + c) * 16, cp);
     float d[3], n[3], raw[3];
     view_dir(means + g * 3, cp, d, n);
     sh_eval<DEG>(n, co, raw);
@@ -476,7 +485,7 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __res
 
 template <int DEG>
 __global__ void __launch_bounds__(kShBlock) sh_cam_bwd_kernel(const float* __restrict__ means,
-                                                              const float* __restrict__ campos,
+                                                              const float* __restrict__ viewmats,
                                                               const float* __restrict__ dc,
                                                               const float* __restrict__ rest,
                                                               const float* __restrict__ v_colors, int64_t C, int64_t N,
@@ -507,7 +516,8 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_bwd_kernel(const float* __res
     const int64_t g = b * N + e0 + t;
     float* co = sc + t * PW;
     for (int64_t c = 0; c < C; ++c) {
-      const float cp[3] = {campos[(b * C + c) * 3], campos[(b * C + c) * 3 + 1], campos[(b * C + c) * 3 + 2]};
+      float cp[3];
+    camera_centre(viewmats + (b * C + c) * 16, cp);
       float d[3], n[3], raw[3];
       const float norm = view_dir(means + g * 3, cp, d, n);
       sh_eval<DEG>(n, co, raw);
@@ -620,7 +630,7 @@ __device__ __forceinline__ void slab_rows(const float* __restrict__ means, const
 
 template <int DEG>
 __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* __restrict__ means,
-                                                                  const float* __restrict__ campos,
+                                                                  const float* __restrict__ viewmats,
                                                                   const float* __restrict__ dc,
                                                                   const float* __restrict__ rest, int64_t C,
                                                                   int64_t N, float* __restrict__ colors) {
@@ -637,7 +647,8 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
   slab_rows<DEG>(means, dc, rest, b * N + e0, cnt, s_rest, s_dc, s_m, co, m);
   if (t >= cnt) return;
   for (int64_t c = 0; c < C; ++c) {
-    const float cp[3] = {campos[(b * C + c) * 3], campos[(b * C + c) * 3 + 1], campos[(b * C + c) * 3 + 2]};
+    float cp[3];
+    camera_centre(viewmats + (b * C + c) * 16, cp);
     float d[3], n[3], raw[3];
     view_dir(m, cp, d, n);
     sh_eval<DEG>(n, co, raw);
@@ -650,7 +661,7 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
 
 template <int DEG>
 __global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
-    const float* __restrict__ means, const float* __restrict__ campos, const float* __restrict__ dc,
+    const float* __restrict__ means, const float* __restrict__ viewmats, const float* __restrict__ dc,
     const float* __restrict__ rest, const float* __restrict__ v_colors, int64_t C, int64_t N,
     float* __restrict__ v_means, float* __restrict__ v_dc, float* __restrict__ v_rest) {
   constexpr int A = (DEG + 1) * (DEG + 1);
@@ -671,7 +682,8 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
     for (int i = 0; i < A * 3; ++i) vco[i] = 0.0f;
     float vm[3] = {0.0f, 0.0f, 0.0f};
     for (int64_t c = 0; c < C; ++c) {
-      const float cp[3] = {campos[(b * C + c) * 3], campos[(b * C + c) * 3 + 1], campos[(b * C + c) * 3 + 2]};
+      float cp[3];
+    camera_centre(viewmats + (b * C + c) * 16, cp);
       float d[3], n[3], raw[3];
       const float norm = view_dir(m, cp, d, n);
       sh_eval<DEG>(n, co, raw);
@@ -724,7 +736,7 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
 constexpr bool slab_degree(int deg) { return deg == 0 || deg == 1 || deg == 3; }
 
 template <int DEG>
-int launch_cam_fwd(const float* means, const float* campos, const float* dc, const float* rest, int64_t B, int64_t C,
+int launch_cam_fwd(const float* means, const float* viewmats, const float* dc, const float* rest, int64_t B, int64_t C,
                    int64_t N, int64_t R, float* colors, hipStream_t s) {
   {
     KernelTimer timer("sh_camera_fwd", s);
@@ -732,13 +744,13 @@ int launch_cam_fwd(const float* means, const float* campos, const float* dc, con
     if constexpr (slab_degree(DEG)) {
       if (R == (DEG + 1) * (DEG + 1) - 1) {
         const dim3 grid(grid_for(N, kShSlab), static_cast<unsigned>(B));
-        sh_cam_fwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, campos, dc, rest, C, N, colors);
+        sh_cam_fwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, C, N, colors);
         slab = true;
       }
     }
     if (!slab) {
       const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
-      sh_cam_fwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, campos, dc, rest, C, N, R,
+      sh_cam_fwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, viewmats, dc, rest, C, N, R,
                                                         magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), colors);
     }
   }
@@ -746,7 +758,7 @@ int launch_cam_fwd(const float* means, const float* campos, const float* dc, con
 }
 
 template <int DEG>
-int launch_cam_bwd(const float* means, const float* campos, const float* dc, const float* rest, const float* v_colors,
+int launch_cam_bwd(const float* means, const float* viewmats, const float* dc, const float* rest, const float* v_colors,
                    int64_t B, int64_t C, int64_t N, int64_t R, float* v_means, float* v_dc, float* v_rest,
                    hipStream_t s) {
   {
@@ -755,14 +767,14 @@ int launch_cam_bwd(const float* means, const float* campos, const float* dc, con
     if constexpr (slab_degree(DEG)) {
       if (R == (DEG + 1) * (DEG + 1) - 1) {
         const dim3 grid(grid_for(N, kShSlab), static_cast<unsigned>(B));
-        sh_cam_bwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, campos, dc, rest, v_colors, C, N, v_means, v_dc,
+        sh_cam_bwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, v_colors, C, N, v_means, v_dc,
                                                               v_rest);
         slab = true;
       }
     }
     if (!slab) {
       const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
-      sh_cam_bwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, campos, dc, rest, v_colors, C, N, R,
+      sh_cam_bwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, viewmats, dc, rest, v_colors, C, N, R,
                                                         magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), v_means,
                                                         v_dc, v_rest);
     }
@@ -848,26 +860,26 @@ static int check_cam_args(int32_t degree, int64_t B, int64_t C, int64_t N, int64
   return GSPLAT_OK;
 }
 
-extern "C" int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* campos,
+extern "C" int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* viewmats,
                                                const float* features_dc, const float* features_rest, int64_t B,
                                                int64_t C, int64_t N, int64_t R, float* colors, void* stream) {
   const char* what = "sh_camera_colors_forward";
   int rc = check_cam_args(degree, B, C, N, R, what);
   if (rc) return rc;
   if (B == 0 || C == 0 || N == 0) return GSPLAT_OK;
-  if (!means || !campos || !features_dc || (R > 0 && !features_rest) || !colors)
+  if (!means || !viewmats || !features_dc || (R > 0 && !features_rest) || !colors)
     return invalid(std::string(what) + ": null pointer.");
   hipStream_t s = as_stream(stream);
   switch (degree) {
-    case 0: return launch_cam_fwd<0>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
-    case 1: return launch_cam_fwd<1>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
-    case 2: return launch_cam_fwd<2>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
-    case 3: return launch_cam_fwd<3>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
-    default: return launch_cam_fwd<4>(means, campos, features_dc, features_rest, B, C, N, R, colors, s);
+    case 0: return launch_cam_fwd<0>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
+    case 1: return launch_cam_fwd<1>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
+    case 2: return launch_cam_fwd<2>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
+    case 3: return launch_cam_fwd<3>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
+    default: return launch_cam_fwd<4>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
   }
 }
 
-extern "C" int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const float* campos,
+extern "C" int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const float* viewmats,
                                                const float* features_dc, const float* features_rest,
                                                const float* v_colors, int64_t B, int64_t C, int64_t N, int64_t R,
                                                float* v_means, float* v_features_dc, float* v_features_rest,
@@ -877,19 +889,19 @@ extern "C" int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* mean
   if (rc) return rc;
   if (B == 0 || N == 0) return GSPLAT_OK;
   if (!means || !features_dc || (R > 0 && (!features_rest || !v_features_rest)) || !v_means || !v_features_dc ||
-      (C > 0 && (!campos || !v_colors)))
+      (C > 0 && (!viewmats || !v_colors)))
     return invalid(std::string(what) + ": null pointer.");
   hipStream_t s = as_stream(stream);
   switch (degree) {
-    case 0: return launch_cam_bwd<0>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+    case 0: return launch_cam_bwd<0>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
                                      v_features_dc, v_features_rest, s);
-    case 1: return launch_cam_bwd<1>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+    case 1: return launch_cam_bwd<1>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
                                      v_features_dc, v_features_rest, s);
-    case 2: return launch_cam_bwd<2>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+    case 2: return launch_cam_bwd<2>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
                                      v_features_dc, v_features_rest, s);
-    case 3: return launch_cam_bwd<3>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+    case 3: return launch_cam_bwd<3>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
                                      v_features_dc, v_features_rest, s);
-    default: return launch_cam_bwd<4>(means, campos, features_dc, features_rest, v_colors, B, C, N, R, v_means,
+    default: return launch_cam_bwd<4>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
                                       v_features_dc, v_features_rest, s);
   }
 }

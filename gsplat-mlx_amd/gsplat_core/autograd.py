@@ -164,32 +164,32 @@ def spherical_harmonics(degrees_to_use, dirs, coeffs, masks=None):
 
 class _ShCameraColors(torch.autograd.Function):
     """colors [B, C, N, 3] = clamp(SH(normalize(means - campos[c])) + 0.5, 0, 1)
-    with the coefficient concat / broadcast of the reference caller
-    (scanner_points_training_utils.py:1011-1034) fused into the kernels.
-    campos carries no gradient."""
+    with campos[c] = -R^T t of viewmats[c] and the coefficient concat /
+    broadcast of the reference caller (scanner_points_training_utils.py:
+    1005-1034) fused into the kernels. The view matrices carry no gradient."""
 
     @staticmethod
-    def forward(ctx, degrees_to_use, means, campos, features_dc, features_rest):
+    def forward(ctx, degrees_to_use, means, viewmats, features_dc, features_rest):
         ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
-        inputs = {"means": means, "campos": campos, "features_dc": features_dc, "features_rest": features_rest}
+        inputs = {"means": means, "viewmats": viewmats, "features_dc": features_dc, "features_rest": features_rest}
         colors = _C.sh_camera_colors_forward(degrees_to_use, inputs)
-        ctx.save_for_backward(means, campos, features_dc, features_rest)
+        ctx.save_for_backward(means, viewmats, features_dc, features_rest)
         ctx.degree = degrees_to_use
         return colors
 
     @staticmethod
     def backward(ctx, v_colors):
-        means, campos, features_dc, features_rest = ctx.saved_tensors
-        inputs = {"means": means, "campos": campos, "features_dc": features_dc, "features_rest": features_rest}
+        means, viewmats, features_dc, features_rest = ctx.saved_tensors
+        inputs = {"means": means, "viewmats": viewmats, "features_dc": features_dc, "features_rest": features_rest}
         out = _C.sh_camera_colors_backward(ctx.degree, inputs, {"v_colors": v_colors.contiguous()})
         return None, out["v_means"], None, out["v_features_dc"], out["v_features_rest"]
 
 
-def sh_camera_colors(degrees_to_use, means, campos, features_dc, features_rest):
-    """Fused camera colours; campos must not require grad."""
-    if campos.requires_grad:
-        raise ValueError("sh_camera_colors: campos gradients are not supported; detach the camera centres.")
-    return _ShCameraColors.apply(degrees_to_use, means, campos, features_dc, features_rest)
+def sh_camera_colors(degrees_to_use, means, viewmats, features_dc, features_rest):
+    """Fused camera colours; viewmats must not require grad."""
+    if viewmats.requires_grad:
+        raise ValueError("sh_camera_colors: view-matrix gradients are not supported; detach viewmats.")
+    return _ShCameraColors.apply(degrees_to_use, means, viewmats, features_dc, features_rest)
 
 
 class _RasterizeToPixels3DGS(torch.autograd.Function):

@@ -43,8 +43,7 @@ def sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)
     kernels when the camera centres need no gradient; otherwise the
     reference's composition of elementwise ops and the SH operator runs."""
     if not viewmats.requires_grad:
-        campos = camera_center_from_viewmat(viewmats).contiguous()
-        return sh_camera_colors(sh_degree, means, campos, features_dc, features_rest)
+        return sh_camera_colors(sh_degree, means, viewmats.contiguous(), features_dc, features_rest)
     return sh_colors_for_camera_unfused(means, features_dc, features_rest, viewmats, sh_degree)
 
 

@@ -140,21 +140,23 @@ int gsplat_hip_spherical_harmonics_bwd(int32_t degree, const float* dirs, const 
 /* Camera colours from SH with the caller's glue fused in. No counterpart
  * operator in the reference: it replaces the composition in
  * sh_colors_for_camera / camera_center_from_viewmat
- * (scanner_points_training_utils.py:1005-1034), i.e. per camera c
- *   n = (means - campos[c]) / max(|means - campos[c]|, 1e-8),
+ * (scanner_points_training_utils.py:1005-1034), i.e. per camera c with
+ * world-to-camera matrix viewmats[c] = [R | t] (row-major 4x4) and centre
+ * campos = -R^T t,
+ *   n = (means - campos) / max(|means - campos|, 1e-8),
  *   colors[c] = clamp(SH_degree(n; [features_dc, features_rest]) + 0.5, 0, 1)
  * with the SH evaluated as gsplat_hip_spherical_harmonics_fwd does, and
  * without materialising the concatenated, camera-broadcast coefficients.
- * means [B,N,3], campos [B,C,3], features_dc [B,N,3], features_rest
+ * means [B,N,3], viewmats [B,C,4,4], features_dc [B,N,3], features_rest
  * [B,N,R,3] (R >= (degree+1)^2 - 1, may be NULL when R == 0),
  * colors [B,C,N,3]. The backward passes v_colors where
  * 0 <= colour + 0.5 <= 1 (torch.clamp's rule) and writes v_means, v_features_dc,
- * v_features_rest summed over the C cameras (inactive bases get 0); campos
- * gets no gradient. */
-int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* campos,
+ * v_features_rest summed over the C cameras (inactive bases get 0); the view
+ * matrices get no gradient. */
+int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* viewmats,
                                     const float* features_dc, const float* features_rest, int64_t B,
                                     int64_t C, int64_t N, int64_t R, float* colors, void* stream);
-int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const float* campos,
+int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const float* viewmats,
                                     const float* features_dc, const float* features_rest,
                                     const float* v_colors, int64_t B, int64_t C, int64_t N, int64_t R,
                                     float* v_means, float* v_features_dc, float* v_features_rest,

@@ -1,8 +1,9 @@
 """GPU parity of the fused camera-colour SH path against (1) the oracle's SH
 wrapped in a numpy restatement of the caller glue of
-scanner_points_training_utils.py:1005-1034 (normalise means - campos with
-max(|d|, 1e-8), concat [dc, rest], clip(SH + 0.5, 0, 1)), and (2) the
-unfused torch composition (elementwise ops + the SH operator) with autograd.
+scanner_points_training_utils.py:1005-1034 (camera centre -R^T t of each view
+matrix, normalise means - campos with max(|d|, 1e-8), concat [dc, rest],
+clip(SH + 0.5, 0, 1)), and (2) the unfused torch composition (elementwise ops
++ the SH operator) with autograd.
 
 Tolerances: colours within 1e-5 relative, gradients within 1e-3 relative
 (_helpers.assert_close_rel). Inputs are nudged away from the clip bounds so
@@ -16,6 +17,23 @@ pytestmark = pytest.mark.gpu
 
 FWD_RTOL = 1e-5
 GRAD_RTOL = 1e-3
+
+
+def _views(rng, B, C):
+    """Random view matrices [B, C, 4, 4] and their centres -R^T t, computed
+    with the kernel's float32 operation order (so a mean placed at a centre
+    gives d = 0 exactly)."""
+    from scipy.spatial.transform import Rotation
+
+    vm = np.zeros((B, C, 4, 4), np.float32)
+    vm[..., 3, 3] = 1
+    vm[..., :3, :3] = Rotation.random(B * C, random_state=int(rng.integers(1 << 30))).as_matrix().reshape(B, C, 3, 3)
+    vm[..., :3, 3] = rng.normal(size=(B, C, 3))
+    R, t = vm[..., :3, :3], vm[..., :3, 3]
+    campos = np.empty((B, C, 3), np.float32)
+    for i in range(3):
+        campos[..., i] = -((R[..., 0, i] * t[..., 0] + R[..., 1, i] * t[..., 1]) + R[..., 2, i] * t[..., 2])
+    return vm, campos
 
 
 def _oracle_forward(oracle, degree, means, campos, dc, rest):
@@ -81,13 +99,13 @@ def test_fused_vs_oracle(oracle, degree, B, C, R):
     rng = np.random.default_rng(degree * 100 + C * 10 + R)
     N = 3001  # not a multiple of the block size
     means = (rng.normal(size=(B, N, 3)) * 2 + [0, 0, 6]).astype(np.float32)
-    campos = rng.normal(size=(B, C, 3)).astype(np.float32)
+    vm, campos = _views(rng, B, C)
     means[0, 5] = campos[0, 0]  # a Gaussian at a camera centre: DC only
     dc = rng.normal(scale=0.3, size=(B, N, 3)).astype(np.float32)
     rest = rng.normal(scale=0.1, size=(B, N, R, 3)).astype(np.float32)
     dc = _nudge_off_bounds(oracle, degree, means, campos, dc, rest)
     raw, dirs, norms, coeffs = _oracle_forward(oracle, degree, means, campos, dc, rest)
-    inputs = {"means": dev(means), "campos": dev(campos), "features_dc": dev(dc), "features_rest": dev(rest)}
+    inputs = {"means": dev(means), "viewmats": dev(vm), "features_dc": dev(dc), "features_rest": dev(rest)}
     colors = host(g._gsplat_core.sh_camera_colors_forward(degree, inputs))
     assert colors.shape == (B, C, N, 3)
     assert_close_rel(colors, np.clip(raw + 0.5, 0, 1), FWD_RTOL, "colors")
@@ -132,8 +150,8 @@ def test_errors():
     g = gsplat()
     z = lambda *s: dev(np.zeros(s, np.float32))  # noqa: E731
     with pytest.raises(RuntimeError, match="fewer SH bases"):
-        g._gsplat_core.sh_camera_colors_forward(3, {"means": z(1, 4, 3), "campos": z(1, 1, 3),
+        g._gsplat_core.sh_camera_colors_forward(3, {"means": z(1, 4, 3), "viewmats": z(1, 1, 4, 4),
                                                     "features_dc": z(1, 4, 3), "features_rest": z(1, 4, 8, 3)})
     with pytest.raises(RuntimeError, match="features_dc"):
-        g._gsplat_core.sh_camera_colors_forward(1, {"means": z(1, 4, 3), "campos": z(1, 1, 3),
+        g._gsplat_core.sh_camera_colors_forward(1, {"means": z(1, 4, 3), "viewmats": z(1, 1, 4, 4),
                                                     "features_dc": z(1, 5, 3), "features_rest": z(1, 4, 3, 3)})
