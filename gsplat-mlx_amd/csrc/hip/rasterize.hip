@@ -18,7 +18,8 @@
 // Per-pixel math follows gsplat_core/gsplat_rasterize.cpp:291-368 (forward)
 // and :432-554 (backward) operation for operation; the Gaussian falloff and
 // alpha tests are evaluated exactly as the reference (no FMA contraction in
-// this file) so compositing decisions match it.
+// this file; the backward's gradient arithmetic uses explicit FMAs) so
+// compositing decisions match it.
 #include <algorithm>
 #include <climits>
 
@@ -29,6 +30,10 @@ namespace gsplat_hip {
 namespace {
 
 constexpr int kMaxChannels = 64;
+
+// Words of one backward batch record in LDS: conic xyz + opacity, then mean
+// xy and the CH staged colours (none for CH == 0), padded to 16 bytes.
+__host__ __device__ constexpr int bwd_record_words(int ch) { return 4 + (2 + ch + 3) / 4 * 4; }
 
 struct RasterArgs {
   const float* means2d;
@@ -322,9 +327,11 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
 // DPP row_ror:8 (lane ^ 8) -- then quad_perm / row_half_mirror DPP adds finish
 // the sums inside each group of 8 lanes. A pair (a, b) at a level leaves the
 // sum of a on lanes whose level bit is 0 and of b where it is 1; an unpaired
-// last value is summed on both sides. After the call, value y[m] on a lane
-// with bits h = lane[5], r = lane[4], e = lane[3] is the wave total of input
-// red_index<N>(m, h, r, e); all 8 lanes of a group hold the same totals.
+// last value is summed on its bit-0 side only at the permlane levels (its
+// partner register holds a dead value) and on both sides at the DPP level. After the call, value y[m] on a lane with bits
+// h = lane[5], r = lane[4], e = lane[3] is the wave total of input
+// red_index<N>(m, h, r, e) (N: not a total, to be discarded); all 8 lanes of
+// a group hold the same values.
 // Costs about 2.3 VALU per value instead of 6 DPP steps per value.
 template <int N>
 struct Red {
@@ -333,15 +340,17 @@ struct Red {
   static constexpr int NC = (NB + 1) / 2;  // after lane ^ 8
 };
 
+// Input index of y[m] on a lane with bits (h, r, e), or N where that lane's
+// y[m] is not a total: an unpaired value at the permlane levels is exchanged
+// with a dead register (no copy), so only its bit-0 side holds its sum.
 template <int N>
 __device__ __forceinline__ int red_index(int m, int h, int r, int e) {
   int c = 2 * m + e;
   if (c >= Red<N>::NB) c = 2 * m;
-  int b = 2 * c + r;
-  if (b >= Red<N>::NA) b = 2 * c;
-  int v = 2 * b + h;
-  if (v >= N) v = 2 * b;
-  return v;
+  const int b = 2 * c + r;
+  if (b >= Red<N>::NA) return N;
+  const int v = 2 * b + h;
+  return v < N ? v : N;
 }
 
 __device__ __forceinline__ float fbits(unsigned u) { return __builtin_bit_cast(float, u); }
@@ -350,21 +359,25 @@ __device__ __forceinline__ unsigned ubits(float f) { return __builtin_bit_cast(u
 template <int N>
 __device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float (&y)[Red<N>::NC], bool e_bit) {
   constexpr int NA = Red<N>::NA, NB = Red<N>::NB, NC = Red<N>::NC;
+  static_assert(N >= 3, "the unpaired exchange reuses the previous pair's register");
+  // the unpaired value's partner is the previous pair's second swap output,
+  // dead once added, so no register is copied for it
   float w[NA];
+  unsigned spare = 0u;
 #pragma unroll
   for (int i = 0; i < NA; ++i) {
-    const float a = v[2 * i];
-    const float b = (2 * i + 1 < N) ? v[2 * i + 1] : a;
-    const auto sw = __builtin_amdgcn_permlane32_swap(ubits(a), ubits(b), false, false);
+    const unsigned b = (2 * i + 1 < N) ? ubits(v[2 * i + 1]) : spare;
+    const auto sw = __builtin_amdgcn_permlane32_swap(ubits(v[2 * i]), b, false, false);
     w[i] = fbits(sw[0]) + fbits(sw[1]);
+    spare = sw[1];
   }
   float x[NB];
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
-    const float a = w[2 * i];
-    const float b = (2 * i + 1 < NA) ? w[2 * i + 1] : a;
-    const auto sw = __builtin_amdgcn_permlane16_swap(ubits(a), ubits(b), false, false);
+    const unsigned b = (2 * i + 1 < NA) ? ubits(w[2 * i + 1]) : spare;
+    const auto sw = __builtin_amdgcn_permlane16_swap(ubits(w[2 * i]), b, false, false);
     x[i] = fbits(sw[0]) + fbits(sw[1]);
+    spare = sw[1];
   }
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
@@ -383,7 +396,7 @@ __device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float
 #pragma unroll
   for (int i = 0; i < NC; ++i) y[i] += fbits(__builtin_amdgcn_update_dpp(0u, ubits(y[i]), 0x4E, 0xf, 0xf, false));   // lane ^ 2
 #pragma unroll
-  for (int i = 0; i < NC; ++i) y[i] += fbits(__builtin_amdgcn_update_dpp(0u, ubits(y[i]), 0x141, 0xf, 0xf, false));  // 7 - lane
+  for (int i = 0; i < NC; ++i) y[i] += fbits(__builtin_amdgcn_mov_dpp(ubits(y[i]), 0x141, 0xf, 0xf, true));  // 7 - lane
 }
 
 // Backward. Persistent blocks walk the heavy-first tile order of `order`
@@ -426,15 +439,17 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
   constexpr int NV = (CH > 0 ? CH : 0) + NG;
   constexpr int o = CH > 0 ? CH : 0;  // first geometry component
   constexpr int NC = Red<NV>::NC;
+  constexpr int NS = NV + 1;  // accumulator words per (wave, slot); the last takes discarded values
+  constexpr int RW = bwd_record_words(CH);
   extern __shared__ float smem[];
   const int BS = blockDim.x;
   const int n_waves = BS / kWave;
-  float2* s_xy = reinterpret_cast<float2*>(smem);                  // [BB]
-  float4* s_co = reinterpret_cast<float4*>(smem + 2 * BB);         // [BB] conic xyz, opacity
-  int32_t* s_g = reinterpret_cast<int32_t*>(smem + 6 * BB);        // [BB]
-  uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + 7 * BB);   // [BB] per-wave touch bits
-  float* s_col = smem + 8 * BB;                                    // [BB][LC] (CH > 0)
-  float* s_acc = s_col + (CH > 0 ? LC * BB : 0);                   // [n_waves][BB][NV]
+  // one record per batch slot, read through a single address: conic xyz +
+  // opacity, then mean xy and the colours (CH > 0), padded to 16 bytes
+  float* s_rec = smem;                                                  // [BB][RW]
+  int32_t* s_g = reinterpret_cast<int32_t*>(smem + RW * BB);           // [BB]
+  uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + (RW + 1) * BB);  // [BB] per-wave touch bits
+  float* s_acc = smem + (RW + 2) * BB;                                  // [n_waves][BB][NS]
 
   const int channels = CH > 0 ? CH : a.channels;
   const int t = threadIdx.x;
@@ -442,12 +457,13 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
   const int wave = t / kWave;
   const bool e_bit = (lane >> 3) & 1;
   const bool red_slot = (lane & 7) == 7;  // lane 7 of each 8-lane group stores
-  int red_idx[NC];
+  // this lane's accumulator words for entry slot 0 (slot k adds k * NS)
+  float* red_at[NC];
 #pragma unroll
-  for (int m = 0; m < NC; ++m) red_idx[m] = red_index<NV>(m, (lane >> 5) & 1, (lane >> 4) & 1, (lane >> 3) & 1);
-  float* const s_acc_wave = s_acc + wave * BB * NV;
+  for (int m = 0; m < NC; ++m)
+    red_at[m] = s_acc + wave * BB * NS + red_index<NV>(m, (lane >> 5) & 1, (lane >> 4) & 1, (lane >> 3) & 1);
   const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
-  const int acc_words = n_waves * BB * NV;
+  const int acc_words = n_waves * BB * NS;
 
   // Static heavy-first schedule: round r gives block b the tile at rank
   // r * nb + b (r even) or r * nb + nb - 1 - b (r odd) of the cost-sorted
@@ -524,14 +540,22 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
       const int64_t b0 = max<int64_t>(start, b1 - BB);
       __syncthreads();  // previous batch fully consumed and flushed
       if (t < BB && b1 - 1 - t >= b0) {
-        s_xy[t] = r_xy;
-        s_co[t] = r_co;
-        s_g[t] = r_g;
-        s_mask[t] = r_mask;
+        float* rec = s_rec + t * RW;
+        *reinterpret_cast<float4*>(rec) = r_co;
+        float tail[RW - 4];
+#pragma unroll
+        for (int i = 0; i < RW - 4; ++i) tail[i] = 0.0f;
+        tail[0] = r_xy.x;
+        tail[1] = r_xy.y;
         if constexpr (CH > 0) {
 #pragma unroll
-          for (int c = 0; c < CH; ++c) s_col[t * CH + c] = r_col[c];
+          for (int c = 0; c < CH; ++c) tail[2 + c] = r_col[c];
         }
+#pragma unroll
+        for (int i = 0; i < RW - 4; i += 4)
+          *reinterpret_cast<float4*>(rec + 4 + i) = make_float4(tail[i], tail[i + 1], tail[i + 2], tail[i + 3]);
+        s_g[t] = r_g;
+        s_mask[t] = r_mask;
       }
       // acc_words is a multiple of 4 (BB is a multiple of 64)
       for (int w = t * 4; w < acc_words; w += BS * 4)
@@ -540,98 +564,107 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
       if (b0 > start) fetch(b0, max<int64_t>(start, b0 - BB));  // next batch, in flight during this one
       const int cnt = static_cast<int>(b1 - b0);
       const int k_rel0 = static_cast<int>(b1 - 1 - start);  // entry of slot 0, relative to start
+      // One visit: this lane's pixel against the record of slot k (co: conic
+      // + opacity, xc: mean xy + colours 0-1, ex: colours 2-3 when CH > 2).
+      auto visit = [&](int k, const float4& co, const float4& xc, const float4& ex) {
+        const int k_rel = k_rel0 - k;
+        const float dx = xc.x - px;
+        const float dy = xc.y - py;
+        const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
+        const float vis = exp_alpha(-sigma);
+        const float a_raw = co.w * vis;
+        const float alpha = fminf(kMaxAlpha, a_raw);
+        const bool valid = k_rel <= last_rel && !(sigma < 0.0f || alpha < kAlphaThreshold);
+        if (__builtin_amdgcn_ballot_w64(valid) == 0) return;
+        // A lane that does not contribute takes ra = 1 and alpha = 0, so T
+        // stays exactly T and fac is 0; B, the colour terms and the geometry
+        // terms are still selected, so non-finite values of the record or of
+        // the pixel's cotangent never reach another pixel's sums.
+        const float ra = valid ? __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - alpha)) : 1.0f;
+        const float T_new = T * ra;
+        const float fac = (valid ? alpha : 0.0f) * T_new;
+        float v[NV];
+        float D;
+        if constexpr (CH > 0) {
+          const float col0 = xc.z;
+          D = col0 * v_rc[0];
+          v[0] = valid ? fac * v_rc[0] : 0.0f;
+#pragma unroll
+          for (int c = 1; c < CH; ++c) {
+            const float colc = c == 1 ? xc.w : (c == 2 ? ex.x : ex.y);
+            D = __builtin_fmaf(colc, v_rc[c], D);
+            v[c] = valid ? fac * v_rc[c] : 0.0f;
+          }
+        } else {
+          const float* gcol = a.colors + static_cast<int64_t>(s_g[k]) * channels;
+          const int64_t gg = s_g[k];
+          D = 0.0f;
+          for (int c = 0; c < channels; ++c) D = __builtin_fmaf(gcol[c], v_rc[c], D);
+          for (int c = 0; c < channels; ++c) {
+            const float sum = wave_sum_uniform(valid ? fac * v_rc[c] : 0.0f);
+            if (lane == 0 && sum != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, sum);
+          }
+        }
+        const float v_alpha = __builtin_fmaf(T_new, D, ra * (coef - B));
+        B = valid ? __builtin_fmaf(fac, D, B) : B;
+        T = T_new;
+        const bool geo = valid && a_raw <= kMaxAlpha;
+        const float v_sigma = geo ? -a_raw * v_alpha : 0.0f;
+        const float gx = geo ? dx : 0.0f;
+        const float gy = geo ? dy : 0.0f;
+        const float hx = v_sigma * gx;
+        const float hy = v_sigma * gy;
+        v[o + 0] = hx * gx;
+        v[o + 1] = hx * gy;
+        v[o + 2] = hy * gy;
+        v[o + 3] = hx;
+        v[o + 4] = hy;
+        v[o + 5] = geo ? vis * v_alpha : 0.0f;
+        if constexpr (ABS) {
+          v[o + 6] = geo ? fabsf(__builtin_fmaf(co.x, hx, co.y * hy)) : 0.0f;
+          v[o + 7] = geo ? fabsf(__builtin_fmaf(co.y, hx, co.z * hy)) : 0.0f;
+        }
+        float yv[NC];
+        wave_transpose_reduce<NV>(v, yv, e_bit);
+        if (red_slot) {
+#pragma unroll
+          for (int mm = 0; mm < NC; ++mm) red_at[mm][k * NS] = yv[mm];
+        }
+      };
       for (int c0 = 0; c0 < cnt; c0 += kWave) {
         // slots of this chunk that may touch this wave and are not past its
         // last contributor (all lanes vote)
         const int kl = c0 + lane;
         uint64_t bits = __ballot(kl < cnt && k_rel0 - kl <= wave_last && ((s_mask[kl] >> wave) & 1u));
         if (!bits) continue;
-        // software-pipelined: the next visited slot's record is read from LDS
-        // while the current one is processed
+        // Software-pipelined over two register sets: the next visited slot's
+        // record is read from LDS while the current one is processed.
+        auto load = [&](int k, float4& co, float4& xc, float4& ex) {
+          const float4* rec = reinterpret_cast<const float4*>(s_rec + k * RW);
+          co = rec[0];
+          xc = rec[1];
+          if constexpr (RW > 8) ex = rec[2];
+        };
         int k = c0 + __builtin_ctzll(bits);
         bits &= bits - 1;
-        float2 m = s_xy[k];
-        float4 co = s_co[k];
-        float col[LC];
-        if constexpr (CH > 0) {
-#pragma unroll
-          for (int c = 0; c < CH; ++c) col[c] = s_col[k * CH + c];
-        }
+        float4 co_a, xc_a, ex_a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 co_b, xc_b, ex_b = ex_a;
+        load(k, co_a, xc_a, ex_a);
         for (;;) {
-          const bool more = bits != 0;
-          const int kn = more ? c0 + __builtin_ctzll(bits) : k;
+          bool more = bits != 0;
+          int kn = more ? c0 + __builtin_ctzll(bits) : k;
           bits &= bits - 1;
-          const float2 mn = s_xy[kn];
-          const float4 con = s_co[kn];
-          float coln[LC];
-          if constexpr (CH > 0) {
-#pragma unroll
-            for (int c = 0; c < CH; ++c) coln[c] = s_col[kn * CH + c];
-          }
-          const int k_rel = k_rel0 - k;
-          const float dx = m.x - px;
-          const float dy = m.y - py;
-          const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
-          const float vis = exp_alpha(-sigma);
-          const float a_raw = co.w * vis;
-          const float alpha = fminf(kMaxAlpha, a_raw);
-          const bool valid = k_rel <= last_rel && !(sigma < 0.0f || alpha < kAlphaThreshold);
-          if (__ballot(valid) != 0) {
-          // contribution of this pixel, selected to zero unless valid
-          const float ra = __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - alpha));
-          const float T_new = T * ra;
-          const float fac = alpha * T_new;
-          float v[NV];
-          float D = 0.0f;
-          if constexpr (CH > 0) {
-#pragma unroll
-            for (int c = 0; c < CH; ++c) {
-              D += col[c] * v_rc[c];
-              v[c] = valid ? fac * v_rc[c] : 0.0f;
-            }
-          } else {
-            const float* gcol = a.colors + static_cast<int64_t>(s_g[k]) * channels;
-            const int64_t gg = s_g[k];
-            for (int c = 0; c < channels; ++c) D += gcol[c] * v_rc[c];
-            for (int c = 0; c < channels; ++c) {
-              const float sum = wave_sum_uniform(valid ? fac * v_rc[c] : 0.0f);
-              if (lane == 0 && sum != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, sum);
-            }
-          }
-          const float v_alpha = T_new * D + ra * (coef - B);
-          const float B_new = B + fac * D;
-          const bool geo = valid && a_raw <= kMaxAlpha;
-          const float v_sigma = -a_raw * v_alpha;
-          const float hx = v_sigma * dx;
-          const float hy = v_sigma * dy;
-          v[o + 0] = geo ? hx * dx : 0.0f;
-          v[o + 1] = geo ? hx * dy : 0.0f;
-          v[o + 2] = geo ? hy * dy : 0.0f;
-          v[o + 3] = geo ? hx : 0.0f;
-          v[o + 4] = geo ? hy : 0.0f;
-          v[o + 5] = geo ? vis * v_alpha : 0.0f;
-          if constexpr (ABS) {
-            v[o + 6] = geo ? fabsf(co.x * hx + co.y * hy) : 0.0f;
-            v[o + 7] = geo ? fabsf(co.y * hx + co.z * hy) : 0.0f;
-          }
-          T = valid ? T_new : T;
-          B = valid ? B_new : B;
-          float yv[NC];
-          wave_transpose_reduce<NV>(v, yv, e_bit);
-          if (red_slot) {
-            float* acc = s_acc_wave + k * NV;
-#pragma unroll
-            for (int mm = 0; mm < NC; ++mm) acc[red_idx[mm]] = yv[mm];
-          }
-          }
+          load(kn, co_b, xc_b, ex_b);
+          visit(k, co_a, xc_a, ex_a);
           if (!more) break;
           k = kn;
-          m = mn;
-          co = con;
-          if constexpr (CH > 0) {
-#pragma unroll
-            for (int c = 0; c < CH; ++c) col[c] = coln[c];
-          }
+          more = bits != 0;
+          kn = more ? c0 + __builtin_ctzll(bits) : k;
+          bits &= bits - 1;
+          load(kn, co_a, xc_a, ex_a);
+          visit(k, co_b, xc_b, ex_b);
+          if (!more) break;
+          k = kn;
         }
       }
       __syncthreads();
@@ -639,13 +672,13 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
       if (t < cnt) {
         float acc[NV];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) acc[i] = s_acc[t * NV + i];
+        for (int i = 0; i < NV; ++i) acc[i] = s_acc[t * NS + i];
         for (int w = 1; w < n_waves; ++w) {
 #pragma unroll
-          for (int i = 0; i < NV; ++i) acc[i] += s_acc[(w * BB + t) * NV + i];
+          for (int i = 0; i < NV; ++i) acc[i] += s_acc[(w * BB + t) * NS + i];
         }
         const int64_t gg = s_g[t];
-        const float4 co = s_co[t];
+        const float4 co = *reinterpret_cast<const float4*>(s_rec + t * RW);
         if constexpr (CH > 0) {
 #pragma unroll
           for (int c = 0; c < CH; ++c)
@@ -852,17 +885,17 @@ size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (8 + (ch > 0 
 // fastest on gfx950 for 16x16 tiles against 2 or 4 pixels per lane and
 // against splitting a tile over several blocks: the lower register count
 // keeps six waves per SIMD resident). Batch length: 128 entries for blocks of
-// up to 256 lanes, 64 above (bounds the per-wave accumulators to 48 KiB at
+// up to 256 lanes, 64 above (bounds the per-wave accumulators to 52 KiB at
 // 1024 lanes, 4 channels, absgrad); never more than the block, so one lane
 // loads one record.
 int bwd_block(int ts) { return (ts * ts + kWave - 1) / kWave * kWave; }
 int bwd_batch(int bs) { return bs <= 128 ? bs : (bs <= 256 ? 128 : 64); }
-// records (8 words + colours: mean, conic+opacity, id, touch mask) per batch
-// slot plus NV accumulators per (wave, slot)
+// records (bwd_record_words, then id and touch mask) per batch slot plus NV + 1
+// accumulator words per (wave, slot)
 size_t bwd_smem(int ch, int bs, int bb, bool absgrad) {
   const int cc = ch > 0 ? ch : 0;
-  const int nv = cc + (absgrad ? 8 : 6);
-  return static_cast<size_t>(bb) * (8 + cc + (bs / kWave) * nv) * 4;
+  const int ns = cc + (absgrad ? 8 : 6) + 1;
+  return static_cast<size_t>(bb) * (bwd_record_words(ch) + 2 + (bs / kWave) * ns) * 4;
 }
 
 int check_args(const RasterArgs& a, const char* what) {
