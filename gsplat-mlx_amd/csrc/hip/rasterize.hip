@@ -32,8 +32,9 @@ namespace {
 constexpr int kMaxChannels = 64;
 
 // Words of one backward batch record in LDS: conic xyz + opacity, then mean
-// xy and the CH staged colours (none for CH == 0), padded to 16 bytes.
-__host__ __device__ constexpr int bwd_record_words(int ch) { return 4 + (2 + ch + 3) / 4 * 4; }
+// xy, the CH staged colours (none for CH == 0), the Gaussian id and the
+// per-wave touch mask, padded to 16 bytes.
+__host__ __device__ constexpr int bwd_record_words(int ch) { return 4 + (2 + ch + 2 + 3) / 4 * 4; }
 
 struct RasterArgs {
   const float* means2d;
@@ -445,11 +446,12 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
   const int BS = blockDim.x;
   const int n_waves = BS / kWave;
   // one record per batch slot, read through a single address: conic xyz +
-  // opacity, then mean xy and the colours (CH > 0), padded to 16 bytes
-  float* s_rec = smem;                                                  // [BB][RW]
-  int32_t* s_g = reinterpret_cast<int32_t*>(smem + RW * BB);           // [BB]
-  uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + (RW + 1) * BB);  // [BB] per-wave touch bits
-  float* s_acc = smem + (RW + 2) * BB;                                  // [n_waves][BB][NS]
+  // opacity, mean xy, colours (CH > 0), Gaussian id, per-wave touch bits
+  constexpr int GW = 6 + o;  // word of the Gaussian id; the touch mask follows
+  float* s_rec = smem;                  // [BB][RW]
+  float* s_acc = smem + RW * BB;        // [n_waves][BB][NS]
+  auto s_g = [&](int k) { return __float_as_int(s_rec[k * RW + GW]); };
+  auto s_mask = [&](int k) { return __float_as_uint(s_rec[k * RW + GW + 1]); };
 
   const int channels = CH > 0 ? CH : a.channels;
   const int t = threadIdx.x;
@@ -551,11 +553,11 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
 #pragma unroll
           for (int c = 0; c < CH; ++c) tail[2 + c] = r_col[c];
         }
+        tail[GW - 4] = __int_as_float(r_g);
+        tail[GW - 3] = __uint_as_float(r_mask);
 #pragma unroll
         for (int i = 0; i < RW - 4; i += 4)
           *reinterpret_cast<float4*>(rec + 4 + i) = make_float4(tail[i], tail[i + 1], tail[i + 2], tail[i + 3]);
-        s_g[t] = r_g;
-        s_mask[t] = r_mask;
       }
       // acc_words is a multiple of 4 (BB is a multiple of 64)
       for (int w = t * 4; w < acc_words; w += BS * 4)
@@ -564,30 +566,45 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
       if (b0 > start) fetch(b0, max<int64_t>(start, b0 - BB));  // next batch, in flight during this one
       const int cnt = static_cast<int>(b1 - b0);
       const int k_rel0 = static_cast<int>(b1 - 1 - start);  // entry of slot 0, relative to start
-      // One visit: this lane's pixel against the record of slot k (co: conic
-      // + opacity, xc: mean xy + colours 0-1, ex: colours 2-3 when CH > 2).
-      auto visit = [&](int k, const float4& co, const float4& xc, const float4& ex) {
+      // Visits come in pairs of straight-line code so that the two records'
+      // falloff, alpha and wave reductions overlap; only transmittance T and
+      // the buffer B pass from the first visit to the second (list order,
+      // back to front). A chunk with an odd number of visits ends with an
+      // inert second visit: no lane valid, nothing stored.
+      struct Fall {
+        float dx, dy, vis, a_raw, alpha;
+        bool valid;
+      };
+      // falloff of this lane's pixel under the record of slot k (co: conic +
+      // opacity, xc: mean xy + colours 0-1, ex: colours 2-3 when CH > 2)
+      auto falloff = [&](int k, const float4& co, const float4& xc) {
+        Fall f;
         const int k_rel = k_rel0 - k;
-        const float dx = xc.x - px;
-        const float dy = xc.y - py;
-        const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
-        const float vis = exp_alpha(-sigma);
-        const float a_raw = co.w * vis;
-        const float alpha = fminf(kMaxAlpha, a_raw);
-        const bool valid = k_rel <= last_rel && !(sigma < 0.0f || alpha < kAlphaThreshold);
-        if (__builtin_amdgcn_ballot_w64(valid) == 0) return;
+        f.dx = xc.x - px;
+        f.dy = xc.y - py;
+        const float sigma = 0.5f * (co.x * f.dx * f.dx + co.z * f.dy * f.dy) + co.y * f.dx * f.dy;
+        f.vis = exp_alpha(-sigma);
+        f.a_raw = co.w * f.vis;
+        f.alpha = fminf(kMaxAlpha, f.a_raw);
+        f.valid = k_rel <= last_rel && !(sigma < 0.0f || f.alpha < kAlphaThreshold);
+        return f;
+      };
+      // this lane's partial gradients for slot k, summed over the wave into
+      // yv (red_index layout); the caller stores them
+      auto contribute = [&](int k, const float4& co, const float4& xc, const float4& ex, const Fall& f,
+                            bool store, float (&yv)[NC]) {
+        const bool valid = f.valid;
         // A lane that does not contribute takes ra = 1 and alpha = 0, so T
         // stays exactly T and fac is 0; B, the colour terms and the geometry
         // terms are still selected, so non-finite values of the record or of
         // the pixel's cotangent never reach another pixel's sums.
-        const float ra = valid ? __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - alpha)) : 1.0f;
+        const float ra = valid ? __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - f.alpha)) : 1.0f;
         const float T_new = T * ra;
-        const float fac = (valid ? alpha : 0.0f) * T_new;
+        const float fac = (valid ? f.alpha : 0.0f) * T_new;
         float v[NV];
         float D;
         if constexpr (CH > 0) {
-          const float col0 = xc.z;
-          D = col0 * v_rc[0];
+          D = xc.z * v_rc[0];
           v[0] = valid ? fac * v_rc[0] : 0.0f;
 #pragma unroll
           for (int c = 1; c < CH; ++c) {
@@ -596,22 +613,22 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
             v[c] = valid ? fac * v_rc[c] : 0.0f;
           }
         } else {
-          const float* gcol = a.colors + static_cast<int64_t>(s_g[k]) * channels;
-          const int64_t gg = s_g[k];
+          const int64_t gg = s_g(k);
+          const float* gcol = a.colors + gg * channels;
           D = 0.0f;
           for (int c = 0; c < channels; ++c) D = __builtin_fmaf(gcol[c], v_rc[c], D);
           for (int c = 0; c < channels; ++c) {
             const float sum = wave_sum_uniform(valid ? fac * v_rc[c] : 0.0f);
-            if (lane == 0 && sum != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, sum);
+            if (store && lane == 0 && sum != 0.0f) unsafeAtomicAdd(v_colors + gg * channels + c, sum);
           }
         }
         const float v_alpha = __builtin_fmaf(T_new, D, ra * (coef - B));
         B = valid ? __builtin_fmaf(fac, D, B) : B;
         T = T_new;
-        const bool geo = valid && a_raw <= kMaxAlpha;
-        const float v_sigma = geo ? -a_raw * v_alpha : 0.0f;
-        const float gx = geo ? dx : 0.0f;
-        const float gy = geo ? dy : 0.0f;
+        const bool geo = valid && f.a_raw <= kMaxAlpha;
+        const float v_sigma = geo ? -f.a_raw * v_alpha : 0.0f;
+        const float gx = geo ? f.dx : 0.0f;
+        const float gy = geo ? f.dy : 0.0f;
         const float hx = v_sigma * gx;
         const float hy = v_sigma * gy;
         v[o + 0] = hx * gx;
@@ -619,52 +636,48 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
         v[o + 2] = hy * gy;
         v[o + 3] = hx;
         v[o + 4] = hy;
-        v[o + 5] = geo ? vis * v_alpha : 0.0f;
+        v[o + 5] = geo ? f.vis * v_alpha : 0.0f;
         if constexpr (ABS) {
           v[o + 6] = geo ? fabsf(__builtin_fmaf(co.x, hx, co.y * hy)) : 0.0f;
           v[o + 7] = geo ? fabsf(__builtin_fmaf(co.y, hx, co.z * hy)) : 0.0f;
         }
-        float yv[NC];
         wave_transpose_reduce<NV>(v, yv, e_bit);
-        if (red_slot) {
-#pragma unroll
-          for (int mm = 0; mm < NC; ++mm) red_at[mm][k * NS] = yv[mm];
-        }
+      };
+      auto load = [&](int k, float4& co, float4& xc, float4& ex) {
+        const float4* rec = reinterpret_cast<const float4*>(s_rec + k * RW);
+        co = rec[0];
+        xc = rec[1];
+        if constexpr (RW > 8) ex = rec[2];
       };
       for (int c0 = 0; c0 < cnt; c0 += kWave) {
         // slots of this chunk that may touch this wave and are not past its
         // last contributor (all lanes vote)
         const int kl = c0 + lane;
-        uint64_t bits = __ballot(kl < cnt && k_rel0 - kl <= wave_last && ((s_mask[kl] >> wave) & 1u));
-        if (!bits) continue;
-        // Software-pipelined over two register sets: the next visited slot's
-        // record is read from LDS while the current one is processed.
-        auto load = [&](int k, float4& co, float4& xc, float4& ex) {
-          const float4* rec = reinterpret_cast<const float4*>(s_rec + k * RW);
-          co = rec[0];
-          xc = rec[1];
-          if constexpr (RW > 8) ex = rec[2];
-        };
-        int k = c0 + __builtin_ctzll(bits);
-        bits &= bits - 1;
-        float4 co_a, xc_a, ex_a = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        float4 co_b, xc_b, ex_b = ex_a;
-        load(k, co_a, xc_a, ex_a);
-        for (;;) {
-          bool more = bits != 0;
-          int kn = more ? c0 + __builtin_ctzll(bits) : k;
+        uint64_t bits = __ballot(kl < cnt && k_rel0 - kl <= wave_last && ((s_mask(kl) >> wave) & 1u));
+        while (bits) {
+          const int k1 = c0 + __builtin_ctzll(bits);
           bits &= bits - 1;
-          load(kn, co_b, xc_b, ex_b);
-          visit(k, co_a, xc_a, ex_a);
-          if (!more) break;
-          k = kn;
-          more = bits != 0;
-          kn = more ? c0 + __builtin_ctzll(bits) : k;
+          const bool two = bits != 0;
+          const int k2 = two ? c0 + __builtin_ctzll(bits) : k1;
           bits &= bits - 1;
-          load(kn, co_a, xc_a, ex_a);
-          visit(k, co_b, xc_b, ex_b);
-          if (!more) break;
-          k = kn;
+          float4 co1, xc1, ex1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+          float4 co2, xc2, ex2 = ex1;
+          load(k1, co1, xc1, ex1);
+          load(k2, co2, xc2, ex2);
+          const Fall f1 = falloff(k1, co1, xc1);
+          Fall f2 = falloff(k2, co2, xc2);
+          f2.valid = f2.valid && two;
+          float y1[NC], y2[NC];
+          contribute(k1, co1, xc1, ex1, f1, true, y1);
+          contribute(k2, co2, xc2, ex2, f2, two, y2);
+          if (red_slot) {
+#pragma unroll
+            for (int mm = 0; mm < NC; ++mm) red_at[mm][k1 * NS] = y1[mm];
+            if (two) {
+#pragma unroll
+              for (int mm = 0; mm < NC; ++mm) red_at[mm][k2 * NS] = y2[mm];
+            }
+          }
         }
       }
       __syncthreads();
@@ -677,7 +690,7 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
 #pragma unroll
           for (int i = 0; i < NV; ++i) acc[i] += s_acc[(w * BB + t) * NS + i];
         }
-        const int64_t gg = s_g[t];
+        const int64_t gg = s_g(t);
         const float4 co = *reinterpret_cast<const float4*>(s_rec + t * RW);
         if constexpr (CH > 0) {
 #pragma unroll
@@ -890,12 +903,12 @@ size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (8 + (ch > 0 
 // loads one record.
 int bwd_block(int ts) { return (ts * ts + kWave - 1) / kWave * kWave; }
 int bwd_batch(int bs) { return bs <= 128 ? bs : (bs <= 256 ? 128 : 64); }
-// records (bwd_record_words, then id and touch mask) per batch slot plus NV + 1
-// accumulator words per (wave, slot)
+// one record (bwd_record_words) per batch slot plus NV + 1 accumulator words
+// per (wave, slot)
 size_t bwd_smem(int ch, int bs, int bb, bool absgrad) {
   const int cc = ch > 0 ? ch : 0;
   const int ns = cc + (absgrad ? 8 : 6) + 1;
-  return static_cast<size_t>(bb) * (bwd_record_words(ch) + 2 + (bs / kWave) * ns) * 4;
+  return static_cast<size_t>(bb) * (bwd_record_words(ch) + (bs / kWave) * ns) * 4;
 }
 
 int check_args(const RasterArgs& a, const char* what) {
