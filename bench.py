@@ -46,7 +46,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", default="sh3_1m", choices=["sh3_1m", "image_fit", "random_forward"])
+    ap.add_argument("--workload", default="sh3_1m",
+                    choices=["sh3_1m", "image_fit", "random_forward", "multiview_3m", "heavy_6m"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-band-rows", type=int, default=0,
                     help="tile rows of the CPU rasterize sample (0: the whole image)")
@@ -127,7 +128,7 @@ def main():
     else:
         colors = param(scene.colors)
         params = [means, quats, log_scales, colors, opacity_logits]
-    viewspace = torch.zeros((1, 1, scene.n, 2), device=dev, requires_grad=True)
+    viewspace = torch.zeros((1, scene.n_cameras, scene.n, 2), device=dev, requires_grad=True)
     target = torch.from_numpy(scene.target).to(dev) if scene.target is not None else None
     W, H, ts = scene.width, scene.height, scene.tile_size
     forward_only = target is None
@@ -185,39 +186,64 @@ def main():
 
     # Work units of this step.
     N = scene.n
+    n_img = scene.n_cameras
     M = int(out["isect_ids"].numel())
     offsets = out["tile_offsets"].reshape(-1).long()
     ends = torch.cat([offsets[1:], torch.tensor([M], device=dev)])
     th, tw = out["tile_offsets"].shape[-2:]
     pix_tile = (torch.arange(H, device=dev)[:, None] // ts) * tw + (torch.arange(W, device=dev)[None, :] // ts)
+    pix_tile = pix_tile[None] + (torch.arange(n_img, device=dev) * (tw * th))[:, None, None]
     start_p = offsets[pix_tile]
     end_p = ends[pix_tile]
-    last = out["last_ids"].reshape(H, W).long()
+    last = out["last_ids"].reshape(n_img, H, W).long()
     e_fwd_max = int(torch.sum(end_p - start_p))  # entries examined without early termination
     e_bwd = int(torch.clamp(torch.minimum(last, end_p - 1) - start_p + 1, min=0).sum())
     K = (scene.sh_degree + 1) ** 2 if sh else 0
+    NC = N * n_img  # projected (Gaussian, camera) pairs
+    P = n_img * W * H
+    # Algorithmic work per step of each timed kernel (all its launches):
+    # bytes read once + written once, or FP32 flops for the rasterizer (the
+    # reference's per-evaluation operation counts x the evaluations up to
+    # each pixel's last contributor).
     units = {
         "raster_bwd": ("flops", BWD_FLOPS_PER_EVAL * e_bwd),
-        "raster_fwd": ("flops", FWD_FLOPS_PER_EVAL * e_fwd_max),
-        "sort_scatter": ("bytes", 24 * M),
-        "sort_histogram": ("bytes", 8 * M),
-        "sh_bwd": ("bytes", (12 + 12 * K + 12 + 12 + 12 * K) * N),
-        "sh_fwd": ("bytes", (12 + 12 * K + 12) * N),
-        "projection_fwd": ("bytes", 72 * N),
-        "projection_bwd": ("bytes", 124 * N),
-        "isect_count_scan": ("bytes", 24 * N),
-        "isect_encode": ("bytes", 24 * N + 12 * M),
+        "raster_fwd": ("flops", FWD_FLOPS_PER_EVAL * e_bwd),
+        "activations_fwd": ("bytes", 64 * N),
+        "activations_bwd": ("bytes", 96 * N),
+        "projection_fwd": ("bytes", (72 + (4 if scene.opacities_in_projection else 0)) * NC),
+        "projection_bwd": ("bytes", (80 + 40 * n_img) * N),
+        "sh_camera_fwd": ("bytes", (12 + 12 * K + 12 * n_img) * N),
+        "sh_camera_bwd": ("bytes", (24 + 24 * K + 12 * n_img) * N),
+        "isect_count_scan": ("bytes", 20 * NC),
+        "isect_depth_keys": ("bytes", 12 * NC),
+        "sort_histogram": ("bytes", 4 * (NC + M)),
+        "sort_onesweep": ("bytes", 64 * NC + 40 * M),
+        "isect_encode": ("bytes", 24 * NC + 8 * M),
         "isect_offsets": ("bytes", 8 * M),
+        "raster_bwd_schedule": ("bytes", 20 * P + 36 * NC),
+        "l1_loss_fwd": ("bytes", 24 * P),
+        "l1_loss_bwd": ("bytes", 36 * P),
     }
+    stages = {}
+    for k, (calls, ms) in sorted(per_step.items()):
+        if k not in units or ms <= 0:
+            continue
+        kind, amount = units[k]
+        if kind == "flops":
+            rate = amount / (ms * 1e-3) / 1e12
+            stages[k] = {"us": round(ms * 1000, 1), "achieved": round(rate, 2), "unit": "TFLOP/s",
+                         "frac": round(rate / FP32_PEAK_TFLOPS, 4)}
+        else:
+            rate = amount / (ms * 1e-3) / 1e9
+            stages[k] = {"us": round(ms * 1000, 1), "achieved": round(rate, 1), "unit": "GB/s",
+                         "frac": round(rate / HBM_PEAK_GBS, 4)}
     dom = max(per_step, key=lambda k: per_step[k][1])
     calls, ms_step = per_step[dom]
     avg_ms = ms_step / calls
     roofline = None
     if dom in units:
         kind, amount = units[dom]
-        per_launch = amount  # one launch per step for every kernel in the table except the sort passes
-        if dom.startswith("sort_"):
-            per_launch = amount  # each pass moves the whole key/value array once
+        per_launch = amount / calls
         if kind == "flops":
             achieved = per_launch / (avg_ms * 1e-3) / 1e12
             roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
@@ -234,8 +260,10 @@ def main():
     log(f"[bench] N={N} M={M} E_fwd(no termination)={e_fwd_max} E_bwd={e_bwd} dominant={dom} {avg_ms:.4f} ms")
 
     cpu = None
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and n_img == 1:
         cpu = cpu_baseline(scene, args.cpu_band_rows, args.cpu_repeats, mpix)
+    elif not args.no_cpu_baseline:
+        log("[bench] cpu baseline: single-camera workloads only")
 
     line = {
         "metric": "fwd+bwd ms/frame & Mpix/s, 1M Gaussians SH3 1297x840; % of HBM/VALU roofline",
@@ -255,6 +283,7 @@ def main():
                    "n_gaussians": N, "image": [W, H], "n_isects": M, "sh_degree": scene.sh_degree},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "stages": stages,
         "kernels_us_per_step": {k: round(v[1] * 1000, 1) for k, v in sorted(per_step.items())},
     }
     print(json.dumps(line), flush=True)

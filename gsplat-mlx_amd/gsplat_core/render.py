@@ -76,29 +76,40 @@ def tile_grid(width: int, height: int, tile_size: int):
     return (width + tile_size - 1) // tile_size, (height + tile_size - 1) // tile_size
 
 
-def _intersect(proj, width, height, tile_size):
+def _intersect(proj, width, height, tile_size, images=1):
     tw, th = tile_grid(width, height, tile_size)
     isect = _C.intersect_tile_forward(
         {"means2d": proj["means2d"].detach(), "radii": proj["radii"], "depths": proj["depths"].detach()},
-        1, tile_size, tw, th, True, False)
-    offsets = _C.intersect_offset_forward(isect["isect_ids"], 1, tw, th)
+        images, tile_size, tw, th, True, False)
+    offsets = _C.intersect_offset_forward(isect["isect_ids"], images, tw, th)
     return isect, offsets
+
+
+def _per_image(opacities, background, n_images, device):
+    """Opacities [1, C, N] and backgrounds [C, 3] for C images of the same
+    Gaussians (the expand's backward sums the opacity gradient over cameras)."""
+    bg = background_tensor(background, device)
+    if n_images == 1:
+        return opacities[:, None], bg
+    return opacities[:, None].expand(-1, n_images, -1).contiguous(), bg.expand(n_images, -1)
 
 
 def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks, width,
                     height, tile_size, sh_degree, viewspace_points=None, background=(0.025, 0.025, 0.025),
                     far_plane=100.0):
-    """One camera (viewmats [1,1,4,4]); returns the render dict plus radii,
+    """C cameras (viewmats [1, C, 4, 4]) rendered as C images of the same
+    Gaussians; returns the render dict ([C, H, W, ...] images) plus radii,
     tiles_per_gauss and flatten_ids, like the reference."""
+    C = viewmats.shape[1]
     quats_n, scales, opac = gaussian_activations(quats, log_scales, opacity_logits)
     proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=quats_n,
                                      scales=scales, viewspace_points=viewspace_points, eps2d=0.3,
                                      near_plane=0.01, far_plane=far_plane, radius_clip=0.0,
                                      calc_compensations=False, camera_model=0)
-    isect, offsets = _intersect(proj, width, height, tile_size)
+    isect, offsets = _intersect(proj, width, height, tile_size, C)
     colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)
-    bg = background_tensor(background, means.device)
-    render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, opac[:, None],
+    opac_img, bg = _per_image(opac, background, C, means.device)
+    render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, opac_img,
                                       offsets, isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
     return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],
             "flatten_ids": isect["flatten_ids"], "isect_ids": isect["isect_ids"], "tile_offsets": offsets}
@@ -106,14 +117,17 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
 
 def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, width, height, tile_size,
                      background=(0.0, 0.0, 0.0), opacities_in_projection=False, far_plane=1e10):
+    """RGB colours per Gaussian; C cameras (viewmats [1, C, 4, 4]) as C images."""
+    C = viewmats.shape[1]
     quats_n, scales, opac = gaussian_activations(quats, log_scales, opacity_logits)
     proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=quats_n,
                                      scales=scales,
                                      opacities=opac if opacities_in_projection else None, eps2d=0.3,
                                      near_plane=0.01, far_plane=far_plane)
-    isect, offsets = _intersect(proj, width, height, tile_size)
-    bg = background_tensor(background, means.device)
-    render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors[:, None], opac[:, None], offsets,
+    isect, offsets = _intersect(proj, width, height, tile_size, C)
+    opac_img, bg = _per_image(opac, background, C, means.device)
+    colors_img = colors[:, None] if C == 1 else colors[:, None].expand(-1, C, -1, -1).contiguous()
+    render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors_img, opac_img, offsets,
                                       isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
     return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],
             "flatten_ids": isect["flatten_ids"], "isect_ids": isect["isect_ids"], "tile_offsets": offsets}
