@@ -208,10 +208,11 @@ def main():
     units = {
         "raster_bwd": ("flops", BWD_FLOPS_PER_EVAL * e_bwd),
         "raster_fwd": ("flops", FWD_FLOPS_PER_EVAL * e_bwd),
-        "activations_fwd": ("bytes", 64 * N),
-        "activations_bwd": ("bytes", 96 * N),
-        "projection_fwd": ("bytes", (72 + (4 if scene.opacities_in_projection else 0)) * NC),
-        "projection_bwd": ("bytes", (80 + 40 * n_img) * N),
+        # the activated projection also reads the opacity logits and writes
+        # the opacities (forward), reads them and the opacity cotangent and
+        # writes the logits' gradient (backward)
+        "projection_fwd": ("bytes", (72 + (4 if scene.opacities_in_projection else 0)) * NC + 8 * N),
+        "projection_bwd": ("bytes", (80 + 40 * n_img) * N + 12 * N),
         "sh_camera_fwd": ("bytes", (12 + 12 * K + 12 * n_img) * N),
         "sh_camera_bwd": ("bytes", (24 + 24 * K + 12 * n_img) * N),
         "isect_count_scan": ("bytes", 20 * NC),

@@ -261,6 +261,61 @@ py::dict gaussian_activations_forward(const TensorMap& inputs) {
   return r;
 }
 
+// Activated projection: the activations fused into the projection. inputs:
+// means, quats (raw), log_scales, opacity_logits (optional), viewmats, Ks.
+py::dict activated_projection_forward(const TensorMap& inputs, int image_width, int image_height, float eps2d,
+                                      float near_plane, float far_plane, float radius_clip, bool calc_compensations,
+                                      int camera_model, bool opacities_in_projection) {
+  gsplat_core::ProjectionEWA3DGSFusedInput in;
+  in.means = require_key(inputs, "means");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.quats = require_key(inputs, "quats");
+  in.scales = require_key(inputs, "log_scales");
+  in.opacities = get_or_empty(inputs, "opacity_logits");
+  in.params = {image_width, image_height, eps2d, near_plane, far_plane, radius_clip, calc_compensations,
+               camera_model, false, opacities_in_projection && in.opacities.numel() != 0};
+  auto out = gsplat_core::gsplat_activated_projection_forward(in);
+  py::dict r;
+  r["radii"] = out[gsplat_core::kRadii];
+  r["means2d"] = out[gsplat_core::kMeans2D];
+  r["depths"] = out[gsplat_core::kDepths];
+  r["conics"] = out[gsplat_core::kConics];
+  r["compensations"] = out[gsplat_core::kCompensations];
+  r["opacities"] = out[5];
+  return r;
+}
+
+py::dict activated_projection_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
+                                       const TensorMap& cotangents, int image_width, int image_height, float eps2d,
+                                       int camera_model, bool viewmats_requires_grad) {
+  gsplat_core::ProjectionEWA3DGSFusedBackwardInput in;
+  in.means = require_key(inputs, "means");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.quats = require_key(inputs, "quats");
+  in.scales = require_key(inputs, "log_scales");
+  in.radii = require_key(forward_outputs, "radii");
+  in.conics = require_key(forward_outputs, "conics");
+  in.compensations = get_or_empty(forward_outputs, "compensations");
+  in.v_means2d = require_key(cotangents, "v_means2d");
+  in.v_depths = get_or_empty(cotangents, "v_depths");  // absent = zeros
+  in.v_conics = require_key(cotangents, "v_conics");
+  in.v_compensations = get_or_empty(cotangents, "v_compensations");
+  in.params = {image_width, image_height, eps2d, -1.0e20f, 1.0e20f, 0.0f, in.compensations.numel() != 0,
+               camera_model, false, false};
+  in.viewmats_requires_grad = viewmats_requires_grad;
+  auto out = gsplat_core::gsplat_activated_projection_backward(in, get_or_empty(inputs, "opacity_logits"),
+                                                               get_or_empty(cotangents, "v_opacities"));
+  py::dict r;
+  r["v_means"] = out[0];
+  r["v_quats"] = out[1];
+  r["v_log_scales"] = out[2];
+  r["v_opacity_logits"] = out[3];
+  if (viewmats_requires_grad) r["v_viewmats"] = out[4];
+  return r;
+}
+
 py::dict gaussian_activations_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
                                        const TensorMap& cotangents) {
   auto out = gsplat_core::gsplat_gaussian_activations_backward(
@@ -323,6 +378,13 @@ PYBIND11_MODULE(_gsplat_core, m) {
   m.def("gaussian_activations_forward", &gaussian_activations_forward, py::arg("inputs"));
   m.def("gaussian_activations_backward", &gaussian_activations_backward, py::arg("inputs"),
         py::arg("forward_outputs"), py::arg("cotangents"));
+  m.def("activated_projection_forward", &activated_projection_forward, py::arg("inputs"), py::arg("image_width"),
+        py::arg("image_height"), py::arg("eps2d") = 0.3f, py::arg("near_plane") = 0.01f,
+        py::arg("far_plane") = 1.0e10f, py::arg("radius_clip") = 0.0f, py::arg("calc_compensations") = false,
+        py::arg("camera_model") = 0, py::arg("opacities_in_projection") = false);
+  m.def("activated_projection_backward", &activated_projection_backward, py::arg("inputs"),
+        py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
+        py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
   m.def("l1_loss_forward", &l1_loss_forward, py::arg("image"), py::arg("target"));
   m.def("l1_loss_backward", &l1_loss_backward, py::arg("image"), py::arg("target"), py::arg("grad"));
   m.def("quat_scale_to_covar_preci_forward", &quat_scale_to_covar_preci_forward, py::arg("inputs"),

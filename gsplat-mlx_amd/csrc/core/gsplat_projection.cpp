@@ -4,6 +4,7 @@
 #include "gsplat_projection.h"
 
 #include "core_util.h"
+#include "gsplat_training_glue.h"
 
 namespace gsplat_core {
 namespace {
@@ -89,9 +90,12 @@ gsplat_projection_params to_c(const ProjectionEWA3DGSFusedParams& p) {
   return c;
 }
 
-}  // namespace
-
-std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFusedInput& input) {
+// The operator (act false) and the activated projection (act true: quats,
+// scales and opacities hold raw quaternions, log-scales and opacity logits;
+// a sixth output holds the sigmoid opacities).
+std::vector<array> projection_forward_impl(const ProjectionEWA3DGSFusedInput& input, bool act) {
+  if (act && input.params.use_covars)
+    throw std::runtime_error("activated_projection takes quats and log_scales, not covars.");
   validate_inputs(input);
   require_device(input.means, "means");
   require_device(input.viewmats, "viewmats");
@@ -99,7 +103,8 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFused
   const Dims d = dims_of(input.means, input.viewmats, input.Ks);
   const auto& p = input.params;
   check_gaussian_params(input.means, input.covars, input.quats, input.scales, p.use_covars, d.B * d.N);
-  if (p.use_opacities) {
+  const bool have_opac = p.use_opacities || (act && !is_empty(input.opacities));
+  if (have_opac) {
     require_device(input.opacities, "opacities");
     require_dtype(input.opacities, at::kFloat, "projection_ewa_3dgs_fused expects float32 opacities.");
     if (input.opacities.numel() != d.B * d.N) throw std::runtime_error("opacities must have shape [..., N].");
@@ -109,7 +114,7 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFused
   const array covars = p.use_covars ? contig(input.covars) : array();
   const array quats = p.use_covars ? array() : contig(input.quats);
   const array scales = p.use_covars ? array() : contig(input.scales);
-  const array opac = p.use_opacities ? contig(input.opacities) : array();
+  const array opac = have_opac ? contig(input.opacities) : array();
   const array viewmats = contig(input.viewmats.to(at::kFloat));
   const array Ks = contig(input.Ks.to(at::kFloat));
   const auto scalar_shape = projection_scalar_shape(means, viewmats);
@@ -119,18 +124,33 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFused
   array comps = p.calc_compensations ? at::empty(scalar_shape, f32_like(means)) : at::empty({0}, f32_like(means));
   array radii = at::empty(projection_shape(means, viewmats, 2), i32_like(means));
   const gsplat_projection_params cp = to_c(p);
-  check(gsplat_hip_projection_fwd(means.data_ptr<float>(), p.use_covars ? covars.data_ptr<float>() : nullptr,
-                                  p.use_covars ? nullptr : quats.data_ptr<float>(),
-                                  p.use_covars ? nullptr : scales.data_ptr<float>(),
-                                  p.use_opacities ? opac.data_ptr<float>() : nullptr, viewmats.data_ptr<float>(),
-                                  Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, radii.data_ptr<int32_t>(),
-                                  means2d.data_ptr<float>(), depths.data_ptr<float>(), conics.data_ptr<float>(),
-                                  p.calc_compensations ? comps.data_ptr<float>() : nullptr,
-                                  stream_for(input.s, means)));
-  return {means2d, depths, conics, comps, radii};
+  if (!act) {
+    check(gsplat_hip_projection_fwd(means.data_ptr<float>(), p.use_covars ? covars.data_ptr<float>() : nullptr,
+                                    p.use_covars ? nullptr : quats.data_ptr<float>(),
+                                    p.use_covars ? nullptr : scales.data_ptr<float>(),
+                                    p.use_opacities ? opac.data_ptr<float>() : nullptr, viewmats.data_ptr<float>(),
+                                    Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, radii.data_ptr<int32_t>(),
+                                    means2d.data_ptr<float>(), depths.data_ptr<float>(), conics.data_ptr<float>(),
+                                    p.calc_compensations ? comps.data_ptr<float>() : nullptr,
+                                    stream_for(input.s, means)));
+    return {means2d, depths, conics, comps, radii};
+  }
+  array opac_out = have_opac ? at::empty(opac.sizes(), f32_like(means)) : at::empty({0}, f32_like(means));
+  check(gsplat_hip_activated_projection_fwd(
+      means.data_ptr<float>(), quats.data_ptr<float>(), scales.data_ptr<float>(),
+      have_opac ? opac.data_ptr<float>() : nullptr, viewmats.data_ptr<float>(), Ks.data_ptr<float>(), d.B, d.C,
+      d.N, &cp, radii.data_ptr<int32_t>(), means2d.data_ptr<float>(), depths.data_ptr<float>(),
+      conics.data_ptr<float>(), p.calc_compensations ? comps.data_ptr<float>() : nullptr,
+      have_opac ? opac_out.data_ptr<float>() : nullptr, stream_for(input.s, means)));
+  return {means2d, depths, conics, comps, radii, opac_out};
 }
 
-std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA3DGSFusedBackwardInput& input) {
+// The operator (act false) and the activated projection (act true; logits and
+// v_opac feed the fifth output, the opacity logits' gradient).
+std::vector<array> projection_backward_impl(const ProjectionEWA3DGSFusedBackwardInput& input, bool act,
+                                            const array& logits_in, const array& v_opac_in) {
+  if (act && input.params.use_covars)
+    throw std::runtime_error("activated_projection takes quats and log_scales, not covars.");
   // gsplat_projection.cpp:144-172
   ProjectionEWA3DGSFusedInput fwd;
   fwd.means = input.means;
@@ -186,6 +206,34 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA
       gsplat_hip_projection_bwd_workspace_size(d.B, d.C, d.N, input.viewmats_requires_grad ? 1 : 0);
   array ws = at::empty({static_cast<int64_t>(ws_bytes)}, u8_like(means));
   const gsplat_projection_params cp = to_c(p);
+  if (act) {
+    const bool have_logits = !is_empty(logits_in);
+    const bool have_v_opac = have_logits && !is_empty(v_opac_in);
+    if (have_logits) {
+      require_device(logits_in, "opacity_logits");
+      require_dtype(logits_in, at::kFloat, "activated_projection expects float32 opacity_logits.");
+      if (logits_in.numel() != d.B * d.N) throw std::runtime_error("opacity_logits must have shape [..., N].");
+    }
+    if (have_v_opac) {
+      require_device(v_opac_in, "v_opacities");
+      if (v_opac_in.numel() != d.B * d.N) throw std::runtime_error("v_opacities must have shape [..., N].");
+    }
+    const array logits = have_logits ? contig(logits_in) : array();
+    const array v_opac = have_v_opac ? contig(v_opac_in.to(at::kFloat)) : array();
+    array v_logits = have_logits ? at::empty(logits.sizes(), f32_like(means)) : at::empty({0}, f32_like(means));
+    check(gsplat_hip_activated_projection_bwd(
+        means.data_ptr<float>(), quats.data_ptr<float>(), scales.data_ptr<float>(),
+        have_logits ? logits.data_ptr<float>() : nullptr, viewmats.data_ptr<float>(), Ks.data_ptr<float>(), d.B,
+        d.C, d.N, &cp, radii.data_ptr<int32_t>(), conics.data_ptr<float>(),
+        use_comp ? comps.data_ptr<float>() : nullptr, v_m2.data_ptr<float>(),
+        use_v_depths ? v_dep.data_ptr<float>() : nullptr, v_con.data_ptr<float>(),
+        use_comp ? v_comps.data_ptr<float>() : nullptr, have_v_opac ? v_opac.data_ptr<float>() : nullptr,
+        v_means.data_ptr<float>(), v_quats.data_ptr<float>(), v_scales.data_ptr<float>(),
+        have_logits ? v_logits.data_ptr<float>() : nullptr,
+        input.viewmats_requires_grad ? v_viewmats.data_ptr<float>() : nullptr,
+        ws_bytes ? ws.data_ptr<uint8_t>() : nullptr, ws_bytes, stream_for(input.s, means)));
+    return {v_means, v_quats, v_scales, v_logits, v_viewmats};
+  }
   check(gsplat_hip_projection_bwd(
       means.data_ptr<float>(), p.use_covars ? covars.data_ptr<float>() : nullptr,
       p.use_covars ? nullptr : quats.data_ptr<float>(), p.use_covars ? nullptr : scales.data_ptr<float>(),
@@ -198,6 +246,25 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA
       input.viewmats_requires_grad ? v_viewmats.data_ptr<float>() : nullptr,
       ws_bytes ? ws.data_ptr<uint8_t>() : nullptr, ws_bytes, stream_for(input.s, means)));
   return {v_means, v_covars, v_quats, v_scales, v_viewmats};
+}
+
+}  // namespace
+
+std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFusedInput& input) {
+  return projection_forward_impl(input, false);
+}
+
+std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA3DGSFusedBackwardInput& input) {
+  return projection_backward_impl(input, false, array(), array());
+}
+
+std::vector<array> gsplat_activated_projection_forward(const ProjectionEWA3DGSFusedInput& input) {
+  return projection_forward_impl(input, true);
+}
+
+std::vector<array> gsplat_activated_projection_backward(const ProjectionEWA3DGSFusedBackwardInput& input,
+                                                        const array& opacity_logits, const array& v_opacities) {
+  return projection_backward_impl(input, true, opacity_logits, v_opacities);
 }
 
 }  // namespace gsplat_core

@@ -5,8 +5,25 @@
 #pragma once
 
 #include "gsplat_common.h"
+#include "gsplat_projection.h"
 
 namespace gsplat_core {
+
+// Activated projection: the activations below fused into the fused EWA
+// projection. The fields of `input` carry the raw model parameters: quats
+// (quaternions), scales (log-scales) and opacities (opacity logits, may be
+// empty); params.use_covars must be false. Returns the projection's
+// {means2d, depths, conics, compensations, radii} plus opacities =
+// sigmoid(opacity_logits) (empty without logits), equal to
+// gsplat_gaussian_activations_forward followed by the projection.
+std::vector<array> gsplat_activated_projection_forward(const ProjectionEWA3DGSFusedInput& input);
+
+// {v_means, v_quats, v_log_scales, v_opacity_logits, v_viewmats}: the
+// projection's VJP through the activations; `input` as the projection
+// backward's with raw quats and log-scales, plus the opacity logits and the
+// cotangent of the opacities output (empty: zeros).
+std::vector<array> gsplat_activated_projection_backward(const ProjectionEWA3DGSFusedBackwardInput& input,
+                                                        const array& opacity_logits, const array& v_opacities);
 
 // {quats / max(|quats|, 1e-8), exp(log_scales), sigmoid(opacity_logits)};
 // each input may be undefined / empty (its output is then empty).

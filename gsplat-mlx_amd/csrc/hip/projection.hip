@@ -12,6 +12,16 @@
 // with wave DPP sums + LDS and writes one row of a partials buffer, which a
 // second kernel sums per camera (deterministic; replaces the reference's
 // one-thread-per-camera O(N) loop, gsplat_projection.metal:571-676).
+//
+// Activated projection (ACT = true): the same kernels read the model's raw
+// parameters -- quaternions, log-scales and opacity logits -- and apply the
+// training step's activations (quats / max(|quats|, 1e-8), exp, sigmoid;
+// scanner_points_training_utils.py:39-41, 306-316) on load, with the
+// operations of training_glue.hip's activation kernels, so the result equals
+// the activation kernel followed by the projection bit for bit. The forward
+// also writes the sigmoid opacities the rasterizer takes; the backward maps
+// the quaternion and scale gradients through the activations and turns the
+// rasterizer's opacity gradient into the logits' gradient.
 #include "common.hpp"
 #include "mat3.hpp"
 
@@ -19,6 +29,49 @@ namespace gsplat_hip {
 namespace {
 
 constexpr int kProjBlock = 256;
+
+// Parameter activations, the operations of training_glue.hip's kernels.
+__device__ __forceinline__ void activate_quat(const float qr[4], float q[4]) {
+  const float r = sqrtf(((qr[0] * qr[0] + qr[1] * qr[1]) + qr[2] * qr[2]) + qr[3] * qr[3]);
+  const float norm = r < 1.0e-8f ? 1.0e-8f : r;  // clamp(min=1e-8); NaN stays NaN
+#pragma unroll
+  for (int k = 0; k < 4; ++k) q[k] = qr[k] / norm;
+}
+
+// d(quats / max(|quats|, 1e-8)) / d quats applied to v
+__device__ __forceinline__ void activate_quat_vjp(const float qr[4], const float v[4], float g[4]) {
+  const float norm = sqrtf(((qr[0] * qr[0] + qr[1] * qr[1]) + qr[2] * qr[2]) + qr[3] * qr[3]);
+  if (norm >= 1.0e-8f) {
+    float nq[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) nq[k] = qr[k] / norm;
+    const float dot = ((v[0] * nq[0] + v[1] * nq[1]) + v[2] * nq[2]) + v[3] * nq[3];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) g[k] = (v[k] - nq[k] * dot) / norm;
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) g[k] = v[k] / 1.0e-8f;
+  }
+}
+
+__device__ __forceinline__ float sigmoid_of(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// quaternion and scales of Gaussian g (ACT: activated from the raw parameters)
+template <bool ACT>
+__device__ __forceinline__ void load_quat_scale(const float* __restrict__ quats, const float* __restrict__ scales,
+                                                int64_t g, float q[4], float s[3]) {
+  const float qr[4] = {quats[g * 4], quats[g * 4 + 1], quats[g * 4 + 2], quats[g * 4 + 3]};
+  if constexpr (ACT) {
+    activate_quat(qr, q);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) s[k] = expf(scales[g * 3 + k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q[k] = qr[k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) s[k] = scales[g * 3 + k];
+  }
+}
 
 struct CamFrame {
   Mat3 R;
@@ -132,12 +185,16 @@ __device__ __forceinline__ void camera_jacobian(int model, const float mc[3], co
   m2[1] = f.fy * y * rz + f.cy;
 }
 
+// ACT: quats, scales and opacities hold the raw parameters (quaternions,
+// log-scales, opacity logits) and opac_out (if non-null) receives the sigmoid
+// opacities, written by the first camera of each batch.
+template <bool ACT>
 __global__ void __launch_bounds__(kProjBlock) projection_fwd_kernel(
     const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities, const float* __restrict__ viewmats,
     const float* __restrict__ Ks, int64_t C, int64_t N, gsplat_projection_params p, int32_t* __restrict__ radii,
     float* __restrict__ means2d, float* __restrict__ depths, float* __restrict__ conics,
-    float* __restrict__ compensations) {
+    float* __restrict__ compensations, float* __restrict__ opac_out) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
   if (n >= N) return;
   const int64_t cam = blockIdx.y;  // b * C + c
@@ -145,6 +202,9 @@ __global__ void __launch_bounds__(kProjBlock) projection_fwd_kernel(
   const int64_t g = b * N + n;
   const int64_t idx = cam * N + n;
   const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
+  if constexpr (ACT) {
+    if (opac_out && cam == b * C) opac_out[g] = sigmoid_of(opacities[g]);
+  }
 
   int32_t rx_out = 0, ry_out = 0;
   float m2x = 0.0f, m2y = 0.0f, depth = 0.0f, c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, comp_out = 0.0f;
@@ -158,8 +218,8 @@ __global__ void __launch_bounds__(kProjBlock) projection_fwd_kernel(
     if (p.use_covars) {
       cw = read_covar(covars + g * 6);
     } else {
-      const float q[4] = {quats[g * 4], quats[g * 4 + 1], quats[g * 4 + 2], quats[g * 4 + 3]};
-      const float s[3] = {scales[g * 3], scales[g * 3 + 1], scales[g * 3 + 2]};
+      float q[4], s[3];
+      load_quat_scale<ACT>(quats, scales, g, q, s);
       cw = covar_from_quat_scale(q, s);
     }
     const Mat3 cc = mat3_mul(mat3_mul(f.R, cw), mat3_tr(f.R));
@@ -185,7 +245,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_fwd_kernel(
     valid = det > 0.0f;
     float extend = kGaussianExtend;
     if (valid && p.use_opacities) {
-      float op = opacities[g];
+      float op = ACT ? sigmoid_of(opacities[g]) : opacities[g];
       if (p.calc_compensations) op *= comp;
       valid = !(op < kAlphaThreshold);
       if (valid) extend = fminf(kGaussianExtend, sqrtf(2.0f * logf(op / kAlphaThreshold)));
@@ -356,6 +416,10 @@ __device__ __forceinline__ void block_sum12_store(float vals[12], float* __restr
   __syncthreads();
 }
 
+// ACT: quats / scales hold quaternions / log-scales (raw), v_quats / v_scales
+// receive their gradients, and v_logits (if non-null) = v_opac * o (1 - o)
+// with o = sigmoid(logits) (v_opac null: zeros).
+template <bool ACT>
 __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ viewmats, const float* __restrict__ Ks, int64_t C,
@@ -363,7 +427,8 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     const float* __restrict__ compensations, const float* __restrict__ v_means2d,
     const float* __restrict__ v_depths, const float* __restrict__ v_conics,
     const float* __restrict__ v_compensations, float* __restrict__ v_means, float* __restrict__ v_covars,
-    float* __restrict__ v_quats, float* __restrict__ v_scales, float* __restrict__ vm_partials) {
+    float* __restrict__ v_quats, float* __restrict__ v_scales, float* __restrict__ vm_partials,
+    const float* __restrict__ logits, const float* __restrict__ v_opac, float* __restrict__ v_logits) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
   const int64_t b = blockIdx.y;
   const bool in_range = n < N;
@@ -380,8 +445,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     if (p.use_covars) {
       cw = read_covar(covars + g * 6);
     } else {
-      q[0] = quats[g * 4]; q[1] = quats[g * 4 + 1]; q[2] = quats[g * 4 + 2]; q[3] = quats[g * 4 + 3];
-      s[0] = scales[g * 3]; s[1] = scales[g * 3 + 1]; s[2] = scales[g * 3 + 2];
+      load_quat_scale<ACT>(quats, scales, g, q, s);
       cw = covar_from_quat_scale(q, s);
     }
   } else {
@@ -458,11 +522,31 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     float vq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     float vs[3] = {0.0f, 0.0f, 0.0f};
     quat_scale_to_covar_vjp(q, s, v_cw_total, vq, vs);
+    if constexpr (ACT) {
+      const float qr[4] = {quats[g * 4], quats[g * 4 + 1], quats[g * 4 + 2], quats[g * 4 + 3]};
+      float vr[4];
+      activate_quat_vjp(qr, vq, vr);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vq[i] = vr[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) vs[i] = vs[i] * s[i];  // d exp(x) / dx = exp(x)
+      if (v_logits) {
+        const float o = sigmoid_of(logits[g]);
+        v_logits[g] = v_opac ? (v_opac[g] * (1.0f - o)) * o : 0.0f;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) v_quats[g * 4 + i] = vq[i];
 #pragma unroll
     for (int i = 0; i < 3; ++i) v_scales[g * 3 + i] = vs[i];
   }
+}
+
+// Opacities of an activated projection without cameras.
+__global__ void __launch_bounds__(kProjBlock) sigmoid_kernel(const float* __restrict__ x, int64_t n,
+                                                             float* __restrict__ y) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
+  if (i < n) y[i] = sigmoid_of(x[i]);
 }
 
 // One block per camera: sums the per-block partials and writes the 4x4
@@ -502,31 +586,114 @@ __global__ void __launch_bounds__(256) viewmat_reduce_kernel(const float* __rest
 
 using namespace gsplat_hip;
 
+namespace {
+
+// Shared by the operator entry points and the activated ones. `what` names
+// the operator in error messages; for ACT the quats / scales / opacities
+// arguments carry the raw parameters.
+template <bool ACT>
+int projection_fwd_impl(const char* what, const float* means, const float* covars, const float* quats,
+                        const float* scales, const float* opacities, const float* viewmats, const float* Ks,
+                        int64_t B, int64_t C, int64_t N, const gsplat_projection_params* params, int32_t* radii,
+                        float* means2d, float* depths, float* conics, float* compensations, float* opac_out,
+                        void* stream) {
+  const std::string op(what);
+  if (!params) return invalid(op + ": null params.");
+  if (B < 0 || C < 0 || N < 0) return invalid(op + ": negative size.");
+  const gsplat_projection_params& p = *params;
+  if (ACT && p.use_covars) return invalid(op + ": the activated projection takes quats and log-scales, not covars.");
+  hipStream_t s = as_stream(stream);
+  if (B * C * N == 0) {
+    // the opacities depend on the Gaussians only (C == 0 still has them)
+    if (ACT && opac_out && B * N > 0) {
+      if (!opacities) return invalid(op + ": opacities requested without opacity logits.");
+      KernelTimer timer("projection_fwd", s);
+      sigmoid_kernel<<<grid_for(B * N, kProjBlock), kProjBlock, 0, s>>>(opacities, B * N, opac_out);
+      return check_launch(what);
+    }
+    return GSPLAT_OK;
+  }
+  if (!means || !viewmats || !Ks || !radii || !means2d || !depths || !conics) return invalid(op + ": null pointer.");
+  if (p.use_covars ? !covars : (!quats || !scales)) return invalid(op + " expects covars or quats+scales.");
+  if (p.use_opacities && !opacities) return invalid(op + ": null opacities.");
+  if (ACT && opac_out && !opacities) return invalid(op + ": opacities requested without opacity logits.");
+  if (p.calc_compensations && !compensations) return invalid(op + ": null compensations.");
+  if (B * C > 65535) return invalid(op + ": B*C exceeds 65535 cameras.");
+  const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B * C));
+  {
+    KernelTimer timer("projection_fwd", s);
+    projection_fwd_kernel<ACT><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, opacities, viewmats, Ks, C,
+                                                           N, p, radii, means2d, depths, conics,
+                                                           p.calc_compensations ? compensations : nullptr,
+                                                           ACT ? opac_out : nullptr);
+  }
+  return check_launch(what);
+}
+
+template <bool ACT>
+int projection_bwd_impl(const char* what, const float* means, const float* covars, const float* quats,
+                        const float* scales, const float* viewmats, const float* Ks, int64_t B, int64_t C, int64_t N,
+                        const gsplat_projection_params* params, const int32_t* radii, const float* conics,
+                        const float* compensations, const float* v_means2d, const float* v_depths,
+                        const float* v_conics, const float* v_compensations, float* v_means, float* v_covars,
+                        float* v_quats, float* v_scales, float* v_viewmats, const float* logits,
+                        const float* v_opac, float* v_logits, void* workspace, size_t workspace_bytes,
+                        void* stream) {
+  const std::string op(what);
+  if (!params) return invalid(op + ": null params.");
+  const gsplat_projection_params& p = *params;
+  if (p.camera_model != 0) return invalid(op + " currently supports pinhole only.");
+  if (B < 0 || C < 0 || N < 0) return invalid(op + ": negative size.");
+  if (ACT && p.use_covars) return invalid(op + ": the activated projection takes quats and log-scales, not covars.");
+  if (ACT && v_logits && !logits) return invalid(op + ": v_opacity_logits requested without opacity logits.");
+  hipStream_t s = as_stream(stream);
+  if (B * N == 0) {
+    if (v_viewmats && B * C > 0) return fill_zero(v_viewmats, B * C * 16 * sizeof(float), s);
+    return GSPLAT_OK;
+  }
+  if (!means || !viewmats || !Ks || !radii || !conics || !v_means2d || !v_conics || !v_means)
+    return invalid(op + ": null pointer.");
+  if (p.use_covars ? (!covars || !v_covars) : (!quats || !scales || !v_quats || !v_scales))
+    return invalid(op + " expects covars or quats+scales.");
+  if (v_compensations && !compensations) return invalid(op + ": v_compensations without compensations.");
+  if (B > 65535) return invalid(op + ": batch exceeds 65535.");
+  float* partials = nullptr;
+  if (v_viewmats && C > 0) {
+    const size_t need = gsplat_hip_projection_bwd_workspace_size(B, C, N, 1);
+    if (!workspace || workspace_bytes < need) {
+      set_error(op + ": workspace too small for v_viewmats.");
+      return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+    }
+    partials = static_cast<float*>(workspace);
+  }
+  const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B));
+  {
+    KernelTimer timer("projection_bwd", s);
+    projection_bwd_kernel<ACT><<<grid, kProjBlock, 0, s>>>(
+        means, covars, quats, scales, viewmats, Ks, C, N, p, radii, conics, compensations, v_means2d, v_depths,
+        v_conics, v_compensations, v_means, v_covars, v_quats, v_scales, partials, ACT ? logits : nullptr,
+        ACT ? v_opac : nullptr, ACT ? v_logits : nullptr);
+  }
+  int rc = check_launch(what);
+  if (rc != GSPLAT_OK || !v_viewmats) return rc;
+  if (C == 0) return GSPLAT_OK;
+  {
+    KernelTimer timer("projection_bwd_viewmats", s);
+    viewmat_reduce_kernel<<<static_cast<unsigned>(B * C), 256, 0, s>>>(partials, static_cast<int>(grid.x), v_viewmats);
+  }
+  return check_launch(what);
+}
+
+}  // namespace
+
 extern "C" int gsplat_hip_projection_fwd(const float* means, const float* covars, const float* quats,
                                          const float* scales, const float* opacities, const float* viewmats,
                                          const float* Ks, int64_t B, int64_t C, int64_t N,
                                          const gsplat_projection_params* params, int32_t* radii, float* means2d,
                                          float* depths, float* conics, float* compensations, void* stream) {
-  if (!params) return invalid("projection_ewa_3dgs_fused_forward: null params.");
-  if (B < 0 || C < 0 || N < 0) return invalid("projection_ewa_3dgs_fused_forward: negative size.");
-  if (B * C * N == 0) return GSPLAT_OK;
-  const gsplat_projection_params& p = *params;
-  if (!means || !viewmats || !Ks || !radii || !means2d || !depths || !conics)
-    return invalid("projection_ewa_3dgs_fused_forward: null pointer.");
-  if (p.use_covars ? !covars : (!quats || !scales))
-    return invalid("projection_ewa_3dgs_fused_forward expects covars or quats+scales.");
-  if (p.use_opacities && !opacities) return invalid("projection_ewa_3dgs_fused_forward: null opacities.");
-  if (p.calc_compensations && !compensations)
-    return invalid("projection_ewa_3dgs_fused_forward: null compensations.");
-  if (B * C > 65535) return invalid("projection_ewa_3dgs_fused_forward: B*C exceeds 65535 cameras.");
-  const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B * C));
-  {
-    KernelTimer timer("projection_fwd", as_stream(stream));
-    projection_fwd_kernel<<<grid, kProjBlock, 0, as_stream(stream)>>>(
-        means, covars, quats, scales, opacities, viewmats, Ks, C, N, p, radii, means2d, depths, conics,
-        p.calc_compensations ? compensations : nullptr);
-  }
-  return check_launch("projection_ewa_3dgs_fused_forward");
+  return projection_fwd_impl<false>("projection_ewa_3dgs_fused_forward", means, covars, quats, scales, opacities,
+                                    viewmats, Ks, B, C, N, params, radii, means2d, depths, conics, compensations,
+                                    nullptr, stream);
 }
 
 extern "C" size_t gsplat_hip_projection_bwd_workspace_size(int64_t B, int64_t C, int64_t N, int32_t viewmats_grad) {
@@ -542,45 +709,33 @@ extern "C" int gsplat_hip_projection_bwd(const float* means, const float* covars
                                          const float* v_compensations, float* v_means, float* v_covars,
                                          float* v_quats, float* v_scales, float* v_viewmats, void* workspace,
                                          size_t workspace_bytes, void* stream) {
-  if (!params) return invalid("projection_ewa_3dgs_fused_backward: null params.");
-  const gsplat_projection_params& p = *params;
-  if (p.camera_model != 0)
-    return invalid("projection_ewa_3dgs_fused_backward currently supports pinhole only.");
-  if (B < 0 || C < 0 || N < 0) return invalid("projection_ewa_3dgs_fused_backward: negative size.");
-  hipStream_t s = as_stream(stream);
-  if (B * N == 0) {
-    if (v_viewmats && B * C > 0) return fill_zero(v_viewmats, B * C * 16 * sizeof(float), s);
-    return GSPLAT_OK;
-  }
-  if (!means || !viewmats || !Ks || !radii || !conics || !v_means2d || !v_conics || !v_means)
-    return invalid("projection_ewa_3dgs_fused_backward: null pointer.");
-  if (p.use_covars ? (!covars || !v_covars) : (!quats || !scales || !v_quats || !v_scales))
-    return invalid("projection_ewa_3dgs_fused_backward expects covars or quats+scales.");
-  if (v_compensations && !compensations)
-    return invalid("projection_ewa_3dgs_fused_backward: v_compensations without compensations.");
-  if (B > 65535) return invalid("projection_ewa_3dgs_fused_backward: batch exceeds 65535.");
-  float* partials = nullptr;
-  if (v_viewmats && C > 0) {
-    const size_t need = gsplat_hip_projection_bwd_workspace_size(B, C, N, 1);
-    if (!workspace || workspace_bytes < need) {
-      set_error("projection_ewa_3dgs_fused_backward: workspace too small for v_viewmats.");
-      return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
-    }
-    partials = static_cast<float*>(workspace);
-  }
-  const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B));
-  {
-    KernelTimer timer("projection_bwd", s);
-    projection_bwd_kernel<<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p, radii,
-                                                      conics, compensations, v_means2d, v_depths, v_conics,
-                                                      v_compensations, v_means, v_covars, v_quats, v_scales, partials);
-  }
-  int rc = check_launch("projection_ewa_3dgs_fused_backward");
-  if (rc != GSPLAT_OK || !v_viewmats) return rc;
-  if (C == 0) return GSPLAT_OK;
-  {
-    KernelTimer timer("projection_bwd_viewmats", s);
-    viewmat_reduce_kernel<<<static_cast<unsigned>(B * C), 256, 0, s>>>(partials, static_cast<int>(grid.x), v_viewmats);
-  }
-  return check_launch("projection_ewa_3dgs_fused_backward (viewmats)");
+  return projection_bwd_impl<false>("projection_ewa_3dgs_fused_backward", means, covars, quats, scales, viewmats, Ks,
+                                    B, C, N, params, radii, conics, compensations, v_means2d, v_depths, v_conics,
+                                    v_compensations, v_means, v_covars, v_quats, v_scales, v_viewmats, nullptr,
+                                    nullptr, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gsplat_hip_activated_projection_fwd(const float* means, const float* quats, const float* log_scales,
+                                                   const float* opacity_logits, const float* viewmats,
+                                                   const float* Ks, int64_t B, int64_t C, int64_t N,
+                                                   const gsplat_projection_params* params, int32_t* radii,
+                                                   float* means2d, float* depths, float* conics,
+                                                   float* compensations, float* opacities, void* stream) {
+  return projection_fwd_impl<true>("activated_projection_forward", means, nullptr, quats, log_scales,
+                                   opacity_logits, viewmats, Ks, B, C, N, params, radii, means2d, depths, conics,
+                                   compensations, opacities, stream);
+}
+
+extern "C" int gsplat_hip_activated_projection_bwd(
+    const float* means, const float* quats, const float* log_scales, const float* opacity_logits,
+    const float* viewmats, const float* Ks, int64_t B, int64_t C, int64_t N, const gsplat_projection_params* params,
+    const int32_t* radii, const float* conics, const float* compensations, const float* v_means2d,
+    const float* v_depths, const float* v_conics, const float* v_compensations, const float* v_opacities,
+    float* v_means, float* v_quats, float* v_log_scales, float* v_opacity_logits, float* v_viewmats,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  return projection_bwd_impl<true>("activated_projection_backward", means, nullptr, quats, log_scales, viewmats, Ks,
+                                   B, C, N, params, radii, conics, compensations, v_means2d, v_depths, v_conics,
+                                   v_compensations, v_means, nullptr, v_quats, v_log_scales, v_viewmats,
+                                   opacity_logits, v_opacities, v_opacity_logits, workspace, workspace_bytes,
+                                   stream);
 }

@@ -19,6 +19,7 @@ except ImportError as exc:  # pragma: no cover - exercised only on broken instal
     ) from exc
 
 from .autograd import (  # noqa: E402,F401
+    activated_projection,
     gaussian_activations,
     l1_loss,
     projection_ewa_3dgs_fused,
@@ -45,8 +46,11 @@ __all__ = [
     "sh_camera_colors_backward",
     "gaussian_activations_forward",
     "gaussian_activations_backward",
+    "activated_projection_forward",
+    "activated_projection_backward",
     "l1_loss_forward",
     "l1_loss_backward",
+    "activated_projection",
     "gaussian_activations",
     "l1_loss",
     "projection_ewa_3dgs_fused",

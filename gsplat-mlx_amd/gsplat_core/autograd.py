@@ -12,11 +12,13 @@ Each ``backward`` routes cotangents exactly as the reference ``Primitive::vjp``:
 Intersection outputs carry no gradient (the reference callers stop_gradient
 them, scanner_points_training_utils.py:1093-1101).
 
-Two more Functions fuse the training step's elementwise glue into HIP kernels
+More Functions fuse the training step's elementwise glue into HIP kernels
 (no counterpart primitive in the reference; they replace the framework
 composition at its call sites):
   * gaussian_activations -- normalize_quats / exp / sigmoid of the model
     parameters (scanner_points_training_utils.py:39-41, 306-316)
+  * activated_projection -- those activations inside the projection kernels
+  * sh_camera_colors -- the camera-colour SH glue (:1005-1034)
   * l1_loss -- the image L1 term of image_loss_components (:1147-1160)
 """
 from __future__ import annotations
@@ -278,6 +280,73 @@ def gaussian_activations(quats, log_scales, opacity_logits):
     """(quats / max(|quats|, 1e-8), exp(log_scales), sigmoid(opacity_logits))
     in one kernel per direction."""
     return _GaussianActivations.apply(quats, log_scales, opacity_logits)
+
+
+class _ActivatedProjection(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, means, quats, log_scales, opacity_logits, viewmats, Ks, viewspace_points, image_width,
+                image_height, eps2d, near_plane, far_plane, radius_clip, calc_compensations, camera_model,
+                opacities_in_projection):
+        ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
+        inputs = {"means": means, "quats": quats, "log_scales": log_scales, "viewmats": viewmats, "Ks": Ks}
+        if _nonempty(opacity_logits):
+            inputs["opacity_logits"] = opacity_logits
+        out = _C.activated_projection_forward(inputs, image_width, image_height, eps2d, near_plane, far_plane,
+                                              radius_clip, calc_compensations, camera_model,
+                                              opacities_in_projection)
+        ctx.save_for_backward(means, quats, log_scales, opacity_logits, viewmats, Ks, out["radii"], out["conics"],
+                              out["compensations"])
+        ctx.params = (image_width, image_height, eps2d, calc_compensations, camera_model)
+        ctx.mark_non_differentiable(out["radii"])
+        return (out["means2d"], out["depths"], out["conics"], out["compensations"], out["radii"],
+                out["opacities"])
+
+    @staticmethod
+    def backward(ctx, v_means2d, v_depths, v_conics, v_compensations, _v_radii, v_opacities):
+        means, quats, log_scales, logits, viewmats, Ks, radii, conics, comps = ctx.saved_tensors
+        W, H, eps2d, calc_comp, camera_model = ctx.params
+        if camera_model != 0:
+            raise RuntimeError("GSPlatProjectionEWA3DGSFused vjp currently supports pinhole only.")
+        dev = means.device
+        v_means2d = torch.zeros(radii.shape, dtype=torch.float32, device=dev) if v_means2d is None else v_means2d
+        v_conics = torch.zeros(conics.shape, dtype=torch.float32, device=dev) if v_conics is None else v_conics
+        inputs = {"means": means, "quats": quats, "log_scales": log_scales, "viewmats": viewmats, "Ks": Ks}
+        if _nonempty(logits):
+            inputs["opacity_logits"] = logits
+        fwd = {"radii": radii, "conics": conics}
+        cot = {"v_means2d": v_means2d.contiguous(), "v_conics": v_conics.contiguous()}
+        if v_depths is not None:  # absent = zeros
+            cot["v_depths"] = v_depths.contiguous()
+        if calc_comp:
+            fwd["compensations"] = comps
+            cot["v_compensations"] = (torch.zeros_like(comps) if v_compensations is None
+                                      else v_compensations.contiguous())
+        if v_opacities is not None:  # absent = zeros
+            cot["v_opacities"] = v_opacities.contiguous()
+        needs_viewmats = ctx.needs_input_grad[4]
+        out = _C.activated_projection_backward(inputs, fwd, cot, W, H, eps2d, camera_model, needs_viewmats)
+        g_logits = out["v_opacity_logits"] if ctx.needs_input_grad[3] else None
+        g_view = out["v_viewmats"] if needs_viewmats else None
+        g_vsp = v_means2d if ctx.needs_input_grad[6] else None
+        return (out["v_means"], out["v_quats"], out["v_log_scales"], g_logits, g_view, None, g_vsp) + (None,) * 9
+
+
+def activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks, image_width, image_height,
+                         viewspace_points=None, eps2d=0.3, near_plane=0.01, far_plane=1e10, radius_clip=0.0,
+                         calc_compensations=False, camera_model=0, opacities_in_projection=False):
+    """gaussian_activations followed by projection_ewa_3dgs_fused, in the
+    projection's kernels: takes the raw parameters (quaternions, log-scales,
+    opacity logits) and returns the projection's dict plus the sigmoid
+    opacities the rasterizer takes. With opacities_in_projection the
+    projection also culls by opacity, as projection_ewa_3dgs_fused(...,
+    opacities=...) does."""
+    e = _empty(means)
+    m2, d, c, comp, r, opac = _ActivatedProjection.apply(
+        means, quats, log_scales, opacity_logits if opacity_logits is not None else e, viewmats, Ks,
+        viewspace_points if viewspace_points is not None else e, image_width, image_height, eps2d, near_plane,
+        far_plane, radius_clip, calc_compensations, camera_model, opacities_in_projection)
+    return {"radii": r, "means2d": m2, "depths": d, "conics": c, "compensations": comp,
+            "viewspace_points": viewspace_points, "opacities": opac}
 
 
 class _L1Loss(torch.autograd.Function):

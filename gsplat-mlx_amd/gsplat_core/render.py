@@ -11,9 +11,10 @@ reference training call sites:
 
 Every operator call goes through the differentiable wrappers in
 ``gsplat_core.autograd`` (HIP kernels). The parameter activations (quaternion
-normalisation, exp of the log-scales, sigmoid of the opacity logits), the SH
-colour glue and the L1 loss also run as fused HIP kernels; the torch
-compositions they replace are kept beside them (``*_unfused``) as the
+normalisation, exp of the log-scales, sigmoid of the opacity logits) run
+inside the projection kernels (activated_projection); the SH colour glue and
+the L1 loss also run as fused HIP kernels. The compositions they replace are
+kept beside them (``*_unfused``, gaussian_activations + the projection) as the
 reference for tests.
 """
 from __future__ import annotations
@@ -21,8 +22,8 @@ from __future__ import annotations
 import torch
 
 from . import _gsplat_core as _C
-from .autograd import (gaussian_activations, l1_loss as _l1_loss, projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs,
-                       sh_camera_colors, spherical_harmonics)
+from .autograd import (activated_projection, gaussian_activations, l1_loss as _l1_loss, projection_ewa_3dgs_fused,
+                       rasterize_to_pixels_3dgs, sh_camera_colors, spherical_harmonics)
 
 
 def normalize_quats(quats: torch.Tensor) -> torch.Tensor:
@@ -101,11 +102,11 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
     Gaussians; returns the render dict ([C, H, W, ...] images) plus radii,
     tiles_per_gauss and flatten_ids, like the reference."""
     C = viewmats.shape[1]
-    quats_n, scales, opac = gaussian_activations(quats, log_scales, opacity_logits)
-    proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=quats_n,
-                                     scales=scales, viewspace_points=viewspace_points, eps2d=0.3,
-                                     near_plane=0.01, far_plane=far_plane, radius_clip=0.0,
-                                     calc_compensations=False, camera_model=0)
+    # the parameter activations run inside the projection kernels
+    proj = activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks, width, height,
+                                viewspace_points=viewspace_points, eps2d=0.3, near_plane=0.01,
+                                far_plane=far_plane, radius_clip=0.0, calc_compensations=False, camera_model=0)
+    opac = proj["opacities"]
     isect, offsets = _intersect(proj, width, height, tile_size, C)
     colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)
     opac_img, bg = _per_image(opac, background, C, means.device)
@@ -119,11 +120,10 @@ def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats,
                      background=(0.0, 0.0, 0.0), opacities_in_projection=False, far_plane=1e10):
     """RGB colours per Gaussian; C cameras (viewmats [1, C, 4, 4]) as C images."""
     C = viewmats.shape[1]
-    quats_n, scales, opac = gaussian_activations(quats, log_scales, opacity_logits)
-    proj = projection_ewa_3dgs_fused(means, viewmats, Ks, width, height, quats=quats_n,
-                                     scales=scales,
-                                     opacities=opac if opacities_in_projection else None, eps2d=0.3,
-                                     near_plane=0.01, far_plane=far_plane)
+    proj = activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks, width, height, eps2d=0.3,
+                                near_plane=0.01, far_plane=far_plane,
+                                opacities_in_projection=opacities_in_projection)
+    opac = proj["opacities"]
     isect, offsets = _intersect(proj, width, height, tile_size, C)
     opac_img, bg = _per_image(opac, background, C, means.device)
     colors_img = colors[:, None] if C == 1 else colors[:, None].expand(-1, C, -1, -1).contiguous()

@@ -307,6 +307,36 @@ int gsplat_hip_gaussian_activations_bwd(const float* quats, const float* scales,
                                         const float* v_opacities, int64_t n, float* v_quats,
                                         float* v_log_scales, float* v_logits, void* stream);
 
+/* Activated projection: the activations above fused into the fused EWA
+ * projection (gsplat_hip_projection_fwd / _bwd, pinhole backward only), for
+ * callers whose model stores raw parameters. quats [B,N,4] are raw
+ * quaternions, log_scales [B,N,3] and opacity_logits [B,N] the logarithms and
+ * logits; use_covars must be 0. Outputs as gsplat_hip_projection_fwd plus
+ * opacities [B,N] = sigmoid(opacity_logits) when non-NULL (opacity_logits
+ * NULL: no opacities; use_opacities then must be 0). The results equal
+ * gsplat_hip_gaussian_activations_fwd followed by gsplat_hip_projection_fwd
+ * bit for bit. The backward takes the projection cotangents plus
+ * v_opacities [B,N] (NULL: zeros) and writes v_means, v_quats and
+ * v_log_scales (raw-parameter gradients), v_opacity_logits [B,N] (may be
+ * NULL) and v_viewmats as gsplat_hip_projection_bwd (same workspace). */
+int gsplat_hip_activated_projection_fwd(const float* means, const float* quats,
+                                        const float* log_scales, const float* opacity_logits,
+                                        const float* viewmats, const float* Ks, int64_t B,
+                                        int64_t C, int64_t N, const gsplat_projection_params* params,
+                                        int32_t* radii, float* means2d, float* depths, float* conics,
+                                        float* compensations, float* opacities, void* stream);
+int gsplat_hip_activated_projection_bwd(const float* means, const float* quats,
+                                        const float* log_scales, const float* opacity_logits,
+                                        const float* viewmats, const float* Ks, int64_t B,
+                                        int64_t C, int64_t N, const gsplat_projection_params* params,
+                                        const int32_t* radii, const float* conics,
+                                        const float* compensations, const float* v_means2d,
+                                        const float* v_depths, const float* v_conics,
+                                        const float* v_compensations, const float* v_opacities,
+                                        float* v_means, float* v_quats, float* v_log_scales,
+                                        float* v_opacity_logits, float* v_viewmats, void* workspace,
+                                        size_t workspace_bytes, void* stream);
+
 /* Image L1 term mean(|a - b|) over n values into the device scalar *loss
  * (nn.losses.l1_loss in image_loss_components,
  * scanner_points_training_utils.py:1147-1160). The backward reads the device scalar cotangent

@@ -97,3 +97,107 @@ def test_l1_vs_torch(shape):
     np.testing.assert_allclose(gb, hb, rtol=1e-6, atol=0)
     np.testing.assert_array_equal(np.sign(ga), np.sign(a - b))
     del torch
+
+
+def _proj_scene(rng, B, C, N):
+    from scipy.spatial.transform import Rotation
+
+    means = (rng.normal(size=(B, N, 3)) * [0.6, 0.5, 0.5] + [0, 0, 4]).astype(np.float32)
+    q = rng.normal(size=(B, N, 4)).astype(np.float32)
+    ls = rng.uniform(-4, -1.5, (B, N, 3)).astype(np.float32)
+    lo = rng.normal(0, 2, size=(B, N)).astype(np.float32)
+    view = np.zeros((B, C, 4, 4), np.float32)
+    view[..., 3, 3] = 1
+    view[..., :3, :3] = Rotation.from_euler("xyz", rng.normal(scale=0.1, size=(B * C, 3))).as_matrix().reshape(
+        B, C, 3, 3)
+    view[..., :3, 3] = rng.normal(scale=0.2, size=(B, C, 3))
+    Ks = np.zeros((B, C, 3, 3), np.float32)
+    Ks[..., 0, 0], Ks[..., 1, 1], Ks[..., 0, 2], Ks[..., 1, 2], Ks[..., 2, 2] = 400, 380, 160, 120, 1
+    return means, q, ls, lo, view, Ks
+
+
+@pytest.mark.parametrize("B,C,in_proj,comp", [(1, 1, False, False), (1, 3, True, True), (2, 2, False, True)])
+def test_activated_projection_vs_composition(B, C, in_proj, comp):
+    """activated_projection equals gaussian_activations followed by
+    projection_ewa_3dgs_fused: forward bit for bit; every gradient (raw
+    parameters, view matrices, the viewspace proxy) within 1e-6 relative."""
+    import torch
+
+    g = gsplat()
+    rng = np.random.default_rng(B * 100 + C * 10 + in_proj)
+    N = 3001
+    means, q, ls, lo, view, Ks = _proj_scene(rng, B, C, N)
+    kw = dict(eps2d=0.3, near_plane=0.01, far_plane=100.0, calc_compensations=comp)
+
+    def run(fused):
+        ts = [dev(a).requires_grad_(True) for a in (means, q, ls, lo, view)]
+        vsp = torch.zeros((B, C, N, 2), device="cuda", requires_grad=True)
+        K = dev(Ks)
+        if fused:
+            out = g.activated_projection(ts[0], ts[1], ts[2], ts[3], ts[4], K, 320, 240, viewspace_points=vsp,
+                                         opacities_in_projection=in_proj, **kw)
+            opac = out["opacities"]
+        else:
+            qn, sc, opac = g.gaussian_activations(ts[1], ts[2], ts[3])
+            out = g.projection_ewa_3dgs_fused(ts[0], ts[4], K, 320, 240, quats=qn, scales=sc,
+                                              opacities=opac if in_proj else None, viewspace_points=vsp, **kw)
+        keys = ["means2d", "depths", "conics"] + (["compensations"] if comp else [])
+        gen = torch.Generator(device="cpu").manual_seed(5)
+        loss = sum((out[k] * torch.randn(out[k].shape, generator=gen).cuda()).sum() for k in keys)
+        loss = loss + (opac * torch.randn(opac.shape, generator=gen).cuda()).sum()
+        loss.backward()
+        vals = {k: host(out[k]) for k in keys + ["radii"]}
+        vals["opacities"] = host(opac)
+        return vals, [host(t.grad) for t in ts] + [host(vsp.grad)]
+
+    fv, fg = run(True)
+    ev, eg = run(False)
+    for k in ev:
+        np.testing.assert_array_equal(fv[k], ev[k], err_msg=k)
+    assert (fv["radii"] > 0).any(axis=-1).sum() > 100
+    for name, a, e in zip(["means", "quats", "log_scales", "opacity_logits", "viewmats", "viewspace"], fg, eg):
+        assert_close_rel(a, e, 1e-6, name)
+
+
+def test_activated_projection_c_abi_and_errors():
+    """The activated entry points through the C ABI: NULL logits skip the
+    opacities; covars and opacities without logits are rejected."""
+    import ctypes
+
+    import torch
+
+    import gsplat_core
+
+    lib = ctypes.CDLL(gsplat_core._gsplat_core.__file__.rsplit("/", 1)[0] + "/libgsplat_hip.so")
+    rng = np.random.default_rng(3)
+    B, C, N = 1, 1, 500
+    means, q, ls, lo, view, Ks = _proj_scene(rng, B, C, N)
+
+    class Params(ctypes.Structure):
+        _fields_ = [("image_width", ctypes.c_int32), ("image_height", ctypes.c_int32), ("eps2d", ctypes.c_float),
+                    ("near_plane", ctypes.c_float), ("far_plane", ctypes.c_float), ("radius_clip", ctypes.c_float),
+                    ("calc_compensations", ctypes.c_int32), ("camera_model", ctypes.c_int32),
+                    ("use_covars", ctypes.c_int32), ("use_opacities", ctypes.c_int32)]
+
+    p = Params(320, 240, 0.3, 0.01, 100.0, 0.0, 0, 0, 0, 0)
+    tm, tq, tl, to, tv, tk = (dev(a) for a in (means, q, ls, lo, view, Ks))
+    radii = torch.empty((B, C, N, 2), dtype=torch.int32, device="cuda")
+    m2 = torch.empty((B, C, N, 2), device="cuda")
+    dep = torch.empty((B, C, N), device="cuda")
+    con = torch.empty((B, C, N, 3), device="cuda")
+    opac = torch.full((B, N), -1.0, device="cuda")
+    f = lib.gsplat_hip_activated_projection_fwd
+    f.restype = ctypes.c_int
+    vp, i64 = ctypes.c_void_p, ctypes.c_int64
+    f.argtypes = [vp] * 6 + [i64] * 3 + [ctypes.POINTER(Params)] + [vp] * 7
+    st = torch.cuda.current_stream().cuda_stream
+    args = [tm.data_ptr(), tq.data_ptr(), tl.data_ptr(), None, tv.data_ptr(), tk.data_ptr(), B, C, N,
+            ctypes.byref(p), radii.data_ptr(), m2.data_ptr(), dep.data_ptr(), con.data_ptr(), None,
+            opac.data_ptr(), st]
+    assert f(*args) != 0  # opacities requested without logits
+    args[3] = to.data_ptr()
+    assert f(*args) == 0
+    torch.cuda.synchronize()
+    assert_close_rel(host(opac), 1.0 / (1.0 + np.exp(-lo.astype(np.float64))), 1e-6, "opacities")
+    p.use_covars = 1
+    assert f(*args) != 0  # covars are not an activated input
