@@ -201,20 +201,30 @@ __device__ __forceinline__ uint32_t touch_mask(float2 m, float4 co, int n_waves,
   return mask;
 }
 
+// Words of one forward batch record in LDS: conic xyz + opacity, then mean xy
+// and the CH staged colours (CH == 0: the Gaussian id), padded to 16 bytes.
+__host__ __device__ constexpr int fwd_record_words(int ch) { return 4 + (2 + (ch > 0 ? ch : 1) + 3) / 4 * 4; }
+// Touch-mask bit of a record whose staged colours are not all finite.
+constexpr uint32_t kNonFiniteColour = 1u << 31;
+
 // CH in 1..4: colors staged in LDS; CH == 0: runtime channel count (<= 64),
 // colors read from global memory.
+//
+// Records are visited in pairs of straight-line code (the two falloffs and
+// alpha tests overlap; compositing stays in list order, an odd count ends
+// with an inert second visit). A chunk of 64 records whose staged colours
+// are all finite accumulates colour * vis with FMAs and no select, since vis
+// is 0 for a record the pixel does not take; a chunk holding a non-finite
+// colour selects instead, so a record the pixel skips never adds a NaN.
 template <int CH>
 __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* __restrict__ render_colors,
                                                           float* __restrict__ render_alphas,
                                                           int32_t* __restrict__ last_ids) {
-  constexpr int LC = CH > 0 ? CH : 1;
+  constexpr int FW = fwd_record_words(CH);
   extern __shared__ float smem[];
   const int BS = blockDim.x;
-  float2* s_xy = reinterpret_cast<float2*>(smem);
-  float4* s_co = reinterpret_cast<float4*>(smem + 2 * BS);  // conic xyz, opacity
-  float* s_col = smem + 6 * BS;                            // [BS][LC] (CH > 0)
-  int32_t* s_g = reinterpret_cast<int32_t*>(smem + 6 * BS + (CH > 0 ? LC * BS : 0));
-  uint32_t* s_mask = reinterpret_cast<uint32_t*>(s_g + BS);  // per-wave touch bits
+  float* s_rec = smem;                                               // [BS][FW]
+  uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + FW * BS);   // [BS] per-wave touch bits
 
   const int channels = CH > 0 ? CH : a.channels;
   const int tx = blockIdx.x, ty = blockIdx.y;
@@ -260,54 +270,107 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
       float2 xy;
       float4 co;
       const int32_t g = load_gaussian(a, j, &xy, &co);
-      s_xy[t] = xy;
-      s_co[t] = co;
-      s_mask[t] = touch_mask(xy, co, n_waves, a.ts, tx, ty);
-      if constexpr (CH > 0) {
+      float* rec = s_rec + t * FW;
+      *reinterpret_cast<float4*>(rec) = co;
+      float tail[FW - 4];
 #pragma unroll
-        for (int c = 0; c < CH; ++c) s_col[t * CH + c] = a.colors[static_cast<int64_t>(g) * CH + c];
+      for (int i = 0; i < FW - 4; ++i) tail[i] = 0.0f;
+      tail[0] = xy.x;
+      tail[1] = xy.y;
+      uint32_t mask = touch_mask(xy, co, n_waves, a.ts, tx, ty);
+      if constexpr (CH > 0) {
+        bool finite = true;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+          tail[2 + c] = a.colors[static_cast<int64_t>(g) * CH + c];
+          finite = finite && fabsf(tail[2 + c]) <= 3.402823466e38f;
+        }
+        if (!finite) mask |= kNonFiniteColour;
       } else {
-        s_g[t] = g;
+        tail[2] = __int_as_float(g);
       }
+#pragma unroll
+      for (int i = 0; i < FW - 4; i += 4)
+        *reinterpret_cast<float4*>(rec + 4 + i) = make_float4(tail[i], tail[i + 1], tail[i + 2], tail[i + 3]);
+      s_mask[t] = mask;
     }
     __syncthreads();
     const int cnt = static_cast<int>(min<int64_t>(BS, end - b0));
-    for (int c0 = 0; c0 < cnt; c0 += kWave) {
-      // records of this 64-slot chunk that may touch this wave (all lanes vote)
-      const int kl = c0 + lane;
-      uint64_t bits = __ballot(kl < cnt && ((s_mask[kl] >> wave) & 1u));
-      if (__ballot(!done) == 0) bits = 0;  // every pixel of the wave has saturated
-      while (bits) {
-        const int k = c0 + __builtin_ctzll(bits);
-        bits &= bits - 1;
-        const float2 m = s_xy[k];
-        const float4 co = s_co[k];
-        const float dx = m.x - px;
-        const float dy = m.y - py;
-        const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
-        const float alpha = fminf(kMaxAlpha, co.w * exp_alpha(-sigma));
-        // branch-free form of: skip when sigma < 0 or alpha < 1/255; stop
-        // (without this record) when T would fall to the threshold
-        const bool pass = !done && !(sigma < 0.0f || alpha < kAlphaThreshold);
-        const float next_T = T * (1.0f - alpha);
-        const bool sat = pass && next_T <= kTransmittanceThreshold;
-        const bool take = pass && !sat;
-        done = done || sat;
-        const float vis = take ? alpha * T : 0.0f;
-        if constexpr (CH > 0) {
+
+    // Compositing of one visit after its falloff (list order). `careful`:
+    // the chunk holds a non-finite colour (select the colour terms).
+    auto composite = [&](int k, const float4& xc, const float4& ex, bool pass_in, float alpha, bool careful) {
+      // branch-free form of: skip when sigma < 0 or alpha < 1/255; stop
+      // (without this record) when T would fall to the threshold
+      const bool pass = !done && pass_in;
+      const float next_T = T * (1.0f - alpha);
+      const bool sat = pass && next_T <= kTransmittanceThreshold;
+      const bool take = pass && !sat;
+      done = done || sat;
+      const float vis = take ? alpha * T : 0.0f;
+      if constexpr (CH > 0) {
+        float col[4] = {xc.z, xc.w, ex.x, ex.y};
+        if (careful) {
 #pragma unroll
           for (int c = 0; c < CH; ++c) {
-            const float add = s_col[k * CH + c] * vis;
+            const float add = col[c] * vis;
             acc[c] += take ? add : 0.0f;  // a skipped record adds nothing, even a non-finite colour
           }
         } else {
-          if (take) {
-            const float* col = a.colors + static_cast<int64_t>(s_g[k]) * channels;
-            for (int c = 0; c < channels; ++c) acc[c] += col[c] * vis;
-          }
+#pragma unroll
+          for (int c = 0; c < CH; ++c) acc[c] = __builtin_fmaf(col[c], vis, acc[c]);
         }
-        cur = take ? static_cast<int32_t>(b0 + k) : cur;
-        T = take ? next_T : T;
+      } else {
+        if (take) {
+          const float* colp = a.colors + static_cast<int64_t>(__float_as_int(xc.z)) * channels;
+          for (int c = 0; c < channels; ++c) acc[c] += colp[c] * vis;
+        }
+      }
+      cur = take ? static_cast<int32_t>(b0 + k) : cur;
+      T = take ? next_T : T;
+    };
+    auto falloff = [&](const float4& co, const float4& xc, bool* pass, float* alpha) {
+      const float dx = xc.x - px;
+      const float dy = xc.y - py;
+      const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
+      *alpha = fminf(kMaxAlpha, co.w * exp_alpha(-sigma));
+      *pass = !(sigma < 0.0f || *alpha < kAlphaThreshold);
+    };
+    auto load = [&](int k, float4& co, float4& xc, float4& ex) {
+      const float4* rec = reinterpret_cast<const float4*>(s_rec + k * FW);
+      co = rec[0];
+      xc = rec[1];
+      if constexpr (FW > 8) ex = rec[2];
+    };
+    for (int c0 = 0; c0 < cnt; c0 += kWave) {
+      // records of this 64-slot chunk that may touch this wave (all lanes vote)
+      const int kl = c0 + lane;
+      const uint32_t mk = kl < cnt ? s_mask[kl] : 0u;
+      const bool mine = (mk >> wave) & 1u;
+      uint64_t bits = __ballot(mine);
+      if (__ballot(!done) == 0) bits = 0;  // every pixel of the wave has saturated
+      const bool careful = CH > 0 && __ballot(mine && (mk & kNonFiniteColour)) != 0;
+      while (bits) {
+        const int k1 = c0 + __builtin_ctzll(bits);
+        bits &= bits - 1;
+        const bool two = bits != 0;
+        const int k2 = two ? c0 + __builtin_ctzll(bits) : k1;
+        bits &= bits - 1;
+        float4 co1, xc1, ex1 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float4 co2, xc2, ex2 = ex1;
+        load(k1, co1, xc1, ex1);
+        load(k2, co2, xc2, ex2);
+        bool p1, p2;
+        float al1, al2;
+        falloff(co1, xc1, &p1, &al1);
+        falloff(co2, xc2, &p2, &al2);
+        if (careful) {
+          composite(k1, xc1, ex1, p1, al1, true);
+          composite(k2, xc2, ex2, p2 && two, al2, true);
+        } else {
+          composite(k1, xc1, ex1, p1, al1, false);
+          composite(k2, xc2, ex2, p2 && two, al2, false);
+        }
       }
     }
   }
@@ -893,7 +956,7 @@ int64_t resident_blocks(const void* kernel, int block, size_t smem) {
 }
 
 // records: mean 2, conic+opacity 4, colours (CH > 0), Gaussian id, touch mask
-size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (8 + (ch > 0 ? ch : 0)) * 4; }
+size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (fwd_record_words(ch) + 1) * 4; }
 // Backward block: one pixel per lane, the whole tile in one block (measured
 // fastest on gfx950 for 16x16 tiles against 2 or 4 pixels per lane and
 // against splitting a tile over several blocks: the lower register count
