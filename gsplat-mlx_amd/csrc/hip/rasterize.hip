@@ -204,8 +204,10 @@ __device__ __forceinline__ uint32_t touch_mask(float2 m, float4 co, int n_waves,
 // Words of one forward batch record in LDS: conic xyz + opacity, then mean xy
 // and the CH staged colours (CH == 0: the Gaussian id), padded to 16 bytes.
 __host__ __device__ constexpr int fwd_record_words(int ch) { return 4 + (2 + (ch > 0 ? ch : 1) + 3) / 4 * 4; }
-// Touch-mask bit of a record whose staged colours are not all finite.
+// Touch-mask bit of a record whose staged colours (forward) / mean
+// (backward) are not all finite.
 constexpr uint32_t kNonFiniteColour = 1u << 31;
+constexpr uint32_t kNonFiniteMean = 1u << 31;
 
 // CH in 1..4: colors staged in LDS; CH == 0: runtime channel count (<= 64),
 // colors read from global memory.
@@ -490,8 +492,14 @@ __device__ __forceinline__ void wave_transpose_reduce(const float (&v)[N], float
 // to zero where the pixel does not contribute (no branches, no accumulators
 // to clear). CH == 0 (runtime channel count) sends colour gradients straight
 // to global memory.
+// Six waves per SIMD (at most 80 VGPRs) where that needs no spills: one to
+// three channels without absgrad (the training path); the register need
+// leaves the others as they are.
+constexpr int bwd_min_waves(int ch, bool abs) { return (!abs && ch >= 1 && ch <= 3) ? 6 : 1; }
+
 template <int CH, bool ABS>
-__global__ void __launch_bounds__(1024) raster_bwd_kernel(
+__global__ void __launch_bounds__(1024) __attribute__((amdgpu_waves_per_eu(bwd_min_waves(CH, ABS))))
+raster_bwd_kernel(
     RasterArgs a, int BB, int64_t n_units, const int32_t* __restrict__ order, const int32_t* __restrict__ cost,
     const float* __restrict__ render_alphas, const int32_t* __restrict__ last_ids,
     const float* __restrict__ v_render_colors, const float* __restrict__ v_render_alphas,
@@ -595,6 +603,12 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
     }
     // d(final-transmittance terms)/d(alpha) = ra * coef
     const float coef = T_final * v_ra + -T_final * bg_dot;
+    // the wave's colour cotangents and final transmittances are all finite
+    // (then a lane that does not contribute can add fac * v_rc = 0 without a
+    // select)
+    bool rc_finite = fabsf(T_final) <= 3.402823466e38f;
+    for (int c = 0; c < channels; ++c) rc_finite = rc_finite && fabsf(v_rc[c]) <= 3.402823466e38f;
+    const bool wave_rc_finite = __ballot(!rc_finite) == 0;
     // entries past every pixel of the wave's last contributor are skipped
     int wave_last = last_rel;
 #pragma unroll
@@ -617,7 +631,8 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
           for (int c = 0; c < CH; ++c) tail[2 + c] = r_col[c];
         }
         tail[GW - 4] = __int_as_float(r_g);
-        tail[GW - 3] = __uint_as_float(r_mask);
+        const bool mean_finite = fabsf(r_xy.x) <= 3.402823466e38f && fabsf(r_xy.y) <= 3.402823466e38f;
+        tail[GW - 3] = __uint_as_float(r_mask | (mean_finite ? 0u : kNonFiniteMean));
 #pragma unroll
         for (int i = 0; i < RW - 4; i += 4)
           *reinterpret_cast<float4*>(rec + 4 + i) = make_float4(tail[i], tail[i + 1], tail[i + 2], tail[i + 3]);
@@ -655,12 +670,14 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
       // this lane's partial gradients for slot k, summed over the wave into
       // yv (red_index layout); the caller stores them
       auto contribute = [&](int k, const float4& co, const float4& xc, const float4& ex, const Fall& f,
-                            bool store, float (&yv)[NC]) {
+                            bool store, bool careful, float (&yv)[NC]) {
         const bool valid = f.valid;
         // A lane that does not contribute takes ra = 1 and alpha = 0, so T
-        // stays exactly T and fac is 0; B, the colour terms and the geometry
-        // terms are still selected, so non-finite values of the record or of
-        // the pixel's cotangent never reach another pixel's sums.
+        // stays exactly T and fac is 0; B and the geometry terms are still
+        // selected, and (careful: the chunk holds a record with a non-finite
+        // mean or the wave a non-finite colour cotangent) so are the colour
+        // terms and the offsets, so non-finite values of the record or of a
+        // pixel's cotangent never reach another pixel's sums.
         const float ra = valid ? __builtin_amdgcn_rcpf(fmaxf(kMinOneMinusAlpha, 1.0f - f.alpha)) : 1.0f;
         const float T_new = T * ra;
         const float fac = (valid ? f.alpha : 0.0f) * T_new;
@@ -668,12 +685,12 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
         float D;
         if constexpr (CH > 0) {
           D = xc.z * v_rc[0];
-          v[0] = valid ? fac * v_rc[0] : 0.0f;
+          v[0] = (careful && !valid) ? 0.0f : fac * v_rc[0];
 #pragma unroll
           for (int c = 1; c < CH; ++c) {
             const float colc = c == 1 ? xc.w : (c == 2 ? ex.x : ex.y);
             D = __builtin_fmaf(colc, v_rc[c], D);
-            v[c] = valid ? fac * v_rc[c] : 0.0f;
+            v[c] = (careful && !valid) ? 0.0f : fac * v_rc[c];
           }
         } else {
           const int64_t gg = s_g(k);
@@ -690,8 +707,8 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
         T = T_new;
         const bool geo = valid && f.a_raw <= kMaxAlpha;
         const float v_sigma = geo ? -f.a_raw * v_alpha : 0.0f;
-        const float gx = geo ? f.dx : 0.0f;
-        const float gy = geo ? f.dy : 0.0f;
+        const float gx = (careful && !geo) ? 0.0f : f.dx;
+        const float gy = (careful && !geo) ? 0.0f : f.dy;
         const float hx = v_sigma * gx;
         const float hy = v_sigma * gy;
         v[o + 0] = hx * gx;
@@ -716,7 +733,10 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
         // slots of this chunk that may touch this wave and are not past its
         // last contributor (all lanes vote)
         const int kl = c0 + lane;
-        uint64_t bits = __ballot(kl < cnt && k_rel0 - kl <= wave_last && ((s_mask(kl) >> wave) & 1u));
+        const uint32_t mk = kl < cnt ? s_mask(kl) : 0u;
+        const bool mine = k_rel0 - kl <= wave_last && ((mk >> wave) & 1u);
+        uint64_t bits = __ballot(mine);
+        const bool careful = !wave_rc_finite || __ballot(mine && (mk & kNonFiniteMean)) != 0;
         while (bits) {
           const int k1 = c0 + __builtin_ctzll(bits);
           bits &= bits - 1;
@@ -731,8 +751,13 @@ __global__ void __launch_bounds__(1024) raster_bwd_kernel(
           Fall f2 = falloff(k2, co2, xc2);
           f2.valid = f2.valid && two;
           float y1[NC], y2[NC];
-          contribute(k1, co1, xc1, ex1, f1, true, y1);
-          contribute(k2, co2, xc2, ex2, f2, two, y2);
+          if (careful) {
+            contribute(k1, co1, xc1, ex1, f1, true, true, y1);
+            contribute(k2, co2, xc2, ex2, f2, two, true, y2);
+          } else {
+            contribute(k1, co1, xc1, ex1, f1, true, false, y1);
+            contribute(k2, co2, xc2, ex2, f2, two, false, y2);
+          }
           if (red_slot) {
 #pragma unroll
             for (int mm = 0; mm < NC; ++mm) red_at[mm][k1 * NS] = y1[mm];
