@@ -147,3 +147,46 @@ def test_empty_lists_and_no_background(oracle):
     empty = dict(s, flatten_ids=np.zeros(0, np.int32), tile_offsets=np.zeros((1, 4, 4), np.int32))
     got = g.rasterize_to_pixels_3dgs_forward(_raster_inputs(empty), 64, 64, 16)
     assert np.all(host(got["render_colors"]) == 0) and np.all(host(got["render_alphas"]) == 0)
+
+
+def test_non_finite_values_stay_local(oracle):
+    """A non-finite colour reaches only the pixels that take its Gaussian, and
+    a non-finite cotangent only the Gaussians that its pixel takes (the
+    reference skips a record a pixel does not take): NaN / inf patterns equal
+    the oracle's, and the finite values agree to the usual tolerances."""
+    g = gsplat()
+    rng = np.random.default_rng(77)
+    W = H = 96
+    s = make_scene(oracle, rng, 1, 1200, W, H, 16, 3)
+    s["colors"][0, 5] = [np.inf, 0.5, 0.5]
+    s["colors"][0, 17] = [0.2, np.nan, 0.1]
+    got = g.rasterize_to_pixels_3dgs_forward(_raster_inputs(s), W, H, 16)
+    exp = _oracle_fwd(oracle, s, W, H, 16)
+    rc, erc = host(got["render_colors"]), exp["render_colors"]
+    np.testing.assert_array_equal(np.isnan(rc), np.isnan(erc))
+    np.testing.assert_array_equal(np.isinf(rc), np.isinf(erc))
+    fin = np.isfinite(erc)
+    assert fin.mean() > 0.5 and (~fin).any()
+    assert np.abs(rc[fin] - erc[fin]).max() <= IMG_ATOL
+    np.testing.assert_array_equal(host(got["last_ids"]), exp["last_ids"])
+
+    s["colors"][0, 5] = [0.9, 0.5, 0.5]
+    s["colors"][0, 17] = [0.2, 0.3, 0.1]
+    got = g.rasterize_to_pixels_3dgs_forward(_raster_inputs(s), W, H, 16)
+    exp = _oracle_fwd(oracle, s, W, H, 16)
+    v_rc = rng.normal(size=exp["render_colors"].shape).astype(np.float32)
+    v_rc[0, 40, 41, 0] = np.nan
+    v_rc[0, 70, 12, 2] = np.inf
+    v_ra = rng.normal(size=exp["render_alphas"].shape).astype(np.float32)
+    bwd = g.rasterize_to_pixels_3dgs_backward(
+        _raster_inputs(s), {"render_alphas": got["render_alphas"], "last_ids": got["last_ids"]},
+        {"v_render_colors": dev(v_rc), "v_render_alphas": dev(v_ra)}, W, H, 16)
+    eb = oracle.raster_backward(s["means2d"], s["conics"], s["colors"], s["opacities"], s["tile_offsets"],
+                                s["flatten_ids"], W, H, 16, exp["render_alphas"], exp["last_ids"], v_rc, v_ra,
+                                backgrounds=s["backgrounds"])
+    for k in ("v_means2d", "v_conics", "v_colors", "v_opacities"):
+        a, e = host(bwd[k]), eb[k]
+        np.testing.assert_array_equal(np.isfinite(a), np.isfinite(e), err_msg=k)
+        bad = ~np.isfinite(e)
+        assert bad.any() and (~bad).mean() > 0.9, k
+        assert_close_rel(np.where(bad, 0, a), np.where(bad, 0, e), GRAD_RTOL, k)
