@@ -5,9 +5,11 @@ Outputs (into gsplat-mlx_amd/gsplat_core/):
   libgsplat_core.so  C++ operator API (namespace gsplat_core, at::Tensor), calls the C ABI
   _gsplat_core*.so   Python module with the reference binding's surface
 
-Every HIP file is compiled with FMA contraction off (kernels round like the
-reference's float32 CPU loops) and with packed-FP32 instruction selection
-disabled. Run `python gsplat-mlx_amd/build.py` or `__graft_entry__.build()`.
+Every HIP file is compiled with packed-FP32 instruction selection disabled
+and, except the files in GRADIENT_ONLY, with FMA contraction off (kernels round
+like the reference's float32 CPU loops). GRADIENT_ONLY files compute only
+gradients (held to a relative tolerance) and are compiled with FMA
+contraction and fast float32 division / square root. Run `python gsplat-mlx_amd/build.py` or `__graft_entry__.build()`.
 """
 from __future__ import annotations
 
@@ -27,8 +29,9 @@ BIND_SRC = os.path.join(HERE, "csrc", "binding")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 ARCH = os.environ.get("GSPLAT_OFFLOAD_ARCH", "gfx950")
 
-HIP_SOURCES = ["common", "quat_scale_to_covar", "projection", "spherical_harmonics", "scan", "intersect",
-               "radix_sort", "rasterize", "training_glue"]
+HIP_SOURCES = ["common", "quat_scale_to_covar", "projection", "projection_bwd", "spherical_harmonics", "scan",
+               "intersect", "radix_sort", "rasterize", "training_glue"]
+GRADIENT_ONLY = {"projection_bwd"}
 CORE_SOURCES = ["gsplat_quat_scale_to_covar", "gsplat_projection", "gsplat_spherical_harmonics",
                 "gsplat_intersect", "gsplat_rasterize", "gsplat_training_glue"]
 
@@ -76,7 +79,11 @@ def build(verbose: bool = False, jobs: int | None = None) -> None:
 
     jobs_list = []
     for s, o in zip(HIP_SOURCES, hip_objs):
-        jobs_list.append(["hipcc", *HIPCC_FLAGS, *inc, "-c", os.path.join(HIP_SRC, f"{s}.hip"), "-o", o])
+        flags = list(HIPCC_FLAGS)
+        if s in GRADIENT_ONLY:
+            flags = [f for f in flags if f != "-ffp-contract=off"] + [
+                "-ffp-contract=fast", "-fno-hip-fp32-correctly-rounded-divide-sqrt"]
+        jobs_list.append(["hipcc", *flags, *inc, "-c", os.path.join(HIP_SRC, f"{s}.hip"), "-o", o])
     for s, o in zip(CORE_SOURCES, core_objs):
         jobs_list.append(["g++", *cflags, *core_inc, "-c", os.path.join(CORE_SRC, f"{s}.cpp"), "-o", o])
     jobs_list.append(["g++", *cflags, *bind_flags, *core_inc, "-c", os.path.join(BIND_SRC, "binding.cpp"),

@@ -1,0 +1,293 @@
+// Fused EWA projection backward for gfx950 (the kernel that
+// gsplat_hip_projection_bwd and gsplat_hip_activated_projection_bwd launch;
+// see projection.hip). Gradient arithmetic only, so this file is compiled
+// with FMA contraction and fast float32 division and square root; the
+// results stay within the chain's gradient tolerance of the exact ones.
+#include "projection_common.hpp"
+
+namespace gsplat_hip {
+namespace {
+
+// gsplat_projection.cpp:262-284
+__device__ __forceinline__ void add_blur_vjp(float eps2d, const float cb[4], float compensation, float v_comp,
+                                             float v_cov[4]) {
+  const float det_conic_blur = cb[0] * cb[3] - cb[1] * cb[2];
+  const float v_sqr_comp = v_comp * 0.5f / (compensation + 1.0e-6f);
+  const float one_minus_sqr_comp = 1.0f - compensation * compensation;
+  v_cov[0] += v_sqr_comp * (one_minus_sqr_comp * cb[0] - eps2d * det_conic_blur);
+  v_cov[1] += v_sqr_comp * (one_minus_sqr_comp * cb[1]);
+  v_cov[2] += v_sqr_comp * (one_minus_sqr_comp * cb[2]);
+  v_cov[3] += v_sqr_comp * (one_minus_sqr_comp * cb[3] - eps2d * det_conic_blur);
+}
+
+// gsplat_projection.cpp:286-377
+__device__ __forceinline__ void persp_proj_vjp(const float mc[3], const Mat3& cov3d, const CamFrame& f, int width,
+                                               int height, const float v_cov2d[4], const float v_mean2d[2],
+                                               float v_mc[3], Mat3& v_cov3d) {
+  const float x = mc[0], y = mc[1], z = mc[2];
+  const PerspLimits l = persp_limits(f.fx, f.fy, f.cx, f.cy, width, height);
+  const float rz = 1.0f / z;
+  const float rz2 = rz * rz;
+  const float rz3 = rz2 * rz;
+  const float x_rz = x * rz;
+  const float y_rz = y * rz;
+  const float tx = z * fminf(l.lim_x_pos, fmaxf(-l.lim_x_neg, x_rz));
+  const float ty = z * fminf(l.lim_y_pos, fmaxf(-l.lim_y_neg, y_rz));
+  const float J[6] = {f.fx * rz, 0.0f, -f.fx * tx * rz2, 0.0f, f.fy * rz, -f.fy * ty * rz2};
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc += J[r * 3 + a] * v_cov2d[r * 2 + c] * J[c * 3 + b];
+      v_cov3d.v[a * 3 + b] = acc;
+    }
+  v_mc[0] += f.fx * rz * v_mean2d[0];
+  v_mc[1] += f.fy * rz * v_mean2d[1];
+  v_mc[2] += -(f.fx * x * v_mean2d[0] + f.fy * y * v_mean2d[1]) * rz2;
+  float v_J[6];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      float left = 0.0f, right = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+          left += v_cov2d[r * 2 + c] * J[c * 3 + b] * cov3d.v[a * 3 + b];
+          right += v_cov2d[c * 2 + r] * J[c * 3 + b] * cov3d.v[b * 3 + a];
+        }
+      v_J[r * 3 + a] = left + right;
+    }
+  if (x_rz <= l.lim_x_pos && x_rz >= -l.lim_x_neg)
+    v_mc[0] += -f.fx * rz2 * v_J[2];
+  else
+    v_mc[2] += -f.fx * rz3 * tx * v_J[2];
+  if (y_rz <= l.lim_y_pos && y_rz >= -l.lim_y_neg)
+    v_mc[1] += -f.fy * rz2 * v_J[5];
+  else
+    v_mc[2] += -f.fy * rz3 * ty * v_J[5];
+  v_mc[2] += -f.fx * rz2 * v_J[0] - f.fy * rz2 * v_J[4] + 2.0f * f.fx * tx * rz3 * v_J[2] +
+             2.0f * f.fy * ty * rz3 * v_J[5];
+}
+
+// gsplat_projection.cpp:404-437
+__device__ __forceinline__ void quat_to_rotmat_vjp(const float q[4], const Mat3& v_R, float vq[4]) {
+  float w = q[0], x = q[1], y = q[2], z = q[3];
+  const float inv_norm = 1.0f / sqrtf(w * w + x * x + y * y + z * z);
+  w *= inv_norm;
+  x *= inv_norm;
+  y *= inv_norm;
+  z *= inv_norm;
+  const float* g = v_R.v;
+  const float n[4] = {
+      2.0f * (x * (g[7] - g[5]) + y * (g[2] - g[6]) + z * (g[3] - g[1])),
+      2.0f * (-2.0f * x * (g[4] + g[8]) + y * (g[1] + g[3]) + z * (g[2] + g[6]) + w * (g[7] - g[5])),
+      2.0f * (x * (g[1] + g[3]) - 2.0f * y * (g[0] + g[8]) + z * (g[5] + g[7]) + w * (g[2] - g[6])),
+      2.0f * (x * (g[2] + g[6]) + y * (g[5] + g[7]) - 2.0f * z * (g[0] + g[4]) + w * (g[3] - g[1])),
+  };
+  const float qn[4] = {w, x, y, z};
+  float dot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) dot += n[i] * qn[i];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) vq[i] += (n[i] - dot * qn[i]) * inv_norm;
+}
+
+// gsplat_projection.cpp:439-474
+__device__ __forceinline__ void quat_scale_to_covar_vjp(const float q[4], const float s[3], const Mat3& v_covar,
+                                                        float vq[4], float vs[3]) {
+  const Mat3 R = quat_to_rotmat(q);
+  Mat3 M, sym;
+#pragma unroll
+  for (int row = 0; row < 3; ++row)
+#pragma unroll
+    for (int col = 0; col < 3; ++col) {
+      M.v[row * 3 + col] = R.v[row * 3 + col] * s[col];
+      sym.v[row * 3 + col] = v_covar.v[row * 3 + col] + v_covar.v[col * 3 + row];
+    }
+  const Mat3 v_M = mat3_mul(sym, M);
+  Mat3 v_R;
+#pragma unroll
+  for (int row = 0; row < 3; ++row)
+#pragma unroll
+    for (int col = 0; col < 3; ++col) {
+      v_R.v[row * 3 + col] = v_M.v[row * 3 + col] * s[col];
+      vs[col] += v_M.v[row * 3 + col] * R.v[row * 3 + col];
+    }
+  quat_to_rotmat_vjp(q, v_R, vq);
+}
+
+// Sum of 12 per-lane values over the block; lane 0 of the block writes them.
+template <int BLOCK>
+__device__ __forceinline__ void block_sum12_store(float vals[12], float* __restrict__ out) {
+  __shared__ float red[BLOCK / kWave][12];
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+#pragma unroll
+  for (int i = 0; i < 12; ++i) {
+    const float s = wave_sum_uniform(vals[i]);
+    if (lane == 0) red[wave][i] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x < 12) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int w = 0; w < BLOCK / kWave; ++w) acc += red[w][threadIdx.x];
+    out[threadIdx.x] = acc;
+  }
+  __syncthreads();
+}
+
+// ACT: quats / scales hold quaternions / log-scales (raw), v_quats / v_scales
+// receive their gradients, and v_logits (if non-null) = v_opac * o (1 - o)
+// with o = sigmoid(logits) (v_opac null: zeros).
+template <bool ACT>
+__global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
+    const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
+    const float* __restrict__ scales, const float* __restrict__ viewmats, const float* __restrict__ Ks, int64_t C,
+    int64_t N, gsplat_projection_params p, const int32_t* __restrict__ radii, const float* __restrict__ conics,
+    const float* __restrict__ compensations, const float* __restrict__ v_means2d,
+    const float* __restrict__ v_depths, const float* __restrict__ v_conics,
+    const float* __restrict__ v_compensations, float* __restrict__ v_means, float* __restrict__ v_covars,
+    float* __restrict__ v_quats, float* __restrict__ v_scales, float* __restrict__ vm_partials,
+    const float* __restrict__ logits, const float* __restrict__ v_opac, float* __restrict__ v_logits) {
+  const int64_t n = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
+  const int64_t b = blockIdx.y;
+  const bool in_range = n < N;
+  const int64_t g = b * N + (in_range ? n : 0);
+
+  float mw[3] = {0.0f, 0.0f, 0.0f};
+  float q[4] = {1.0f, 0.0f, 0.0f, 0.0f};
+  float s[3] = {1.0f, 1.0f, 1.0f};
+  Mat3 cw;
+  if (in_range) {
+    mw[0] = means[g * 3];
+    mw[1] = means[g * 3 + 1];
+    mw[2] = means[g * 3 + 2];
+    if (p.use_covars) {
+      cw = read_covar(covars + g * 6);
+    } else {
+      load_quat_scale<ACT>(quats, scales, g, q, s);
+      cw = covar_from_quat_scale(q, s);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 9; ++i) cw.v[i] = 0.0f;
+  }
+
+  float v_mw_total[3] = {0.0f, 0.0f, 0.0f};
+  Mat3 v_cw_total;
+#pragma unroll
+  for (int i = 0; i < 9; ++i) v_cw_total.v[i] = 0.0f;
+
+  for (int64_t c = 0; c < C; ++c) {
+    const int64_t cam = b * C + c;
+    const int64_t idx = cam * N + n;
+    const bool valid = in_range && radii[idx * 2] > 0 && radii[idx * 2 + 1] > 0;
+    float vm_part[12];
+#pragma unroll
+    for (int i = 0; i < 12; ++i) vm_part[i] = 0.0f;
+    if (valid) {
+      const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
+      const float cn[3] = {conics[idx * 3], conics[idx * 3 + 1], conics[idx * 3 + 2]};
+      const float vc[3] = {v_conics[idx * 3], v_conics[idx * 3 + 1], v_conics[idx * 3 + 2]};
+      const float inv[4] = {cn[0], cn[1], cn[1], cn[2]};
+      const float vinv[4] = {vc[0], 0.5f * vc[1], 0.5f * vc[1], vc[2]};
+      const float tmp[4] = {inv[0] * vinv[0] + inv[1] * vinv[2], inv[0] * vinv[1] + inv[1] * vinv[3],
+                            inv[2] * vinv[0] + inv[3] * vinv[2], inv[2] * vinv[1] + inv[3] * vinv[3]};
+      float v_cov2d[4] = {-(tmp[0] * inv[0] + tmp[1] * inv[2]), -(tmp[0] * inv[1] + tmp[1] * inv[3]),
+                          -(tmp[2] * inv[0] + tmp[3] * inv[2]), -(tmp[2] * inv[1] + tmp[3] * inv[3])};
+      if (v_compensations) add_blur_vjp(p.eps2d, inv, compensations[idx], v_compensations[idx], v_cov2d);
+      float mc[3];
+      world_to_cam(f, mw, mc);
+      const Mat3 cc = mat3_mul(mat3_mul(f.R, cw), mat3_tr(f.R));
+      float v_mc[3] = {0.0f, 0.0f, v_depths ? v_depths[idx] : 0.0f};
+      const float vm2[2] = {v_means2d[idx * 2], v_means2d[idx * 2 + 1]};
+      Mat3 v_cc;
+      persp_proj_vjp(mc, cc, f, p.image_width, p.image_height, v_cov2d, vm2, v_mc, v_cc);
+      const float* R = f.R.v;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) v_mw_total[i] += R[i] * v_mc[0] + R[3 + i] * v_mc[1] + R[6 + i] * v_mc[2];
+      const Mat3 v_cw = mat3_mul(mat3_mul(mat3_tr(f.R), v_cc), f.R);
+#pragma unroll
+      for (int i = 0; i < 9; ++i) v_cw_total.v[i] += v_cw.v[i];
+      if (vm_partials) {
+        const Mat3 term1 = mat3_mul(mat3_mul(v_cc, f.R), mat3_tr(cw));
+        const Mat3 term2 = mat3_mul(mat3_mul(mat3_tr(v_cc), f.R), cw);
+#pragma unroll
+        for (int row = 0; row < 3; ++row) {
+#pragma unroll
+          for (int col = 0; col < 3; ++col)
+            vm_part[row * 3 + col] = v_mc[row] * mw[col] + term1.v[row * 3 + col] + term2.v[row * 3 + col];
+          vm_part[9 + row] = v_mc[row];
+        }
+      }
+    }
+    if (vm_partials) {
+      // partials layout: [B*C][gridDim.x][12]
+      block_sum12_store<kProjBlock>(vm_part, vm_partials + (cam * gridDim.x + blockIdx.x) * 12);
+    }
+  }
+  if (!in_range) return;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) v_means[g * 3 + i] = v_mw_total[i];
+  if (p.use_covars) {
+    const float* v = v_cw_total.v;
+    float* o = v_covars + g * 6;
+    o[0] = v[0];
+    o[1] = v[1] + v[3];
+    o[2] = v[2] + v[6];
+    o[3] = v[4];
+    o[4] = v[5] + v[7];
+    o[5] = v[8];
+  } else {
+    float vq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float vs[3] = {0.0f, 0.0f, 0.0f};
+    quat_scale_to_covar_vjp(q, s, v_cw_total, vq, vs);
+    if constexpr (ACT) {
+      const float qr[4] = {quats[g * 4], quats[g * 4 + 1], quats[g * 4 + 2], quats[g * 4 + 3]};
+      float vr[4];
+      activate_quat_vjp(qr, vq, vr);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) vq[i] = vr[i];
+#pragma unroll
+      for (int i = 0; i < 3; ++i) vs[i] = vs[i] * s[i];  // d exp(x) / dx = exp(x)
+      if (v_logits) {
+        const float o = sigmoid_of(logits[g]);
+        v_logits[g] = v_opac ? (v_opac[g] * (1.0f - o)) * o : 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v_quats[g * 4 + i] = vq[i];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) v_scales[g * 3 + i] = vs[i];
+  }
+}
+
+}  // namespace
+
+void launch_projection_bwd(bool act, dim3 grid, hipStream_t s, const float* means, const float* covars,
+                           const float* quats, const float* scales, const float* viewmats, const float* Ks, int64_t C,
+                           int64_t N, const gsplat_projection_params& p, const int32_t* radii, const float* conics,
+                           const float* compensations, const float* v_means2d, const float* v_depths,
+                           const float* v_conics, const float* v_compensations, float* v_means, float* v_covars,
+                           float* v_quats, float* v_scales, float* vm_partials, const float* logits,
+                           const float* v_opac, float* v_logits) {
+  if (act)
+    projection_bwd_kernel<true><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p, radii,
+                                                            conics, compensations, v_means2d, v_depths, v_conics,
+                                                            v_compensations, v_means, v_covars, v_quats, v_scales,
+                                                            vm_partials, logits, v_opac, v_logits);
+  else
+    projection_bwd_kernel<false><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p,
+                                                             radii, conics, compensations, v_means2d, v_depths,
+                                                             v_conics, v_compensations, v_means, v_covars, v_quats,
+                                                             v_scales, vm_partials, nullptr, nullptr, nullptr);
+}
+
+}  // namespace gsplat_hip
