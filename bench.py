@@ -247,11 +247,21 @@ def main():
         per_launch = amount / calls
         if kind == "flops":
             achieved = per_launch / (avg_ms * 1e-3) / 1e12
+            att = valu_attainable_tflops(prof.lib, torch)
             roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": FP32_PEAK_TFLOPS,
                         "unit": "TFLOP/s", "frac": round(achieved / FP32_PEAK_TFLOPS, 4),
                         "traffic": measured_traffic(args.workload, dom),
                         "kernel": dom, "avg_ms": round(avg_ms, 4),
-                        "note": "compute roofline: FP32 VALU (no MFMA on this path), peak = MI355X FP32"}
+                        "note": "compute roofline: FP32 VALU (no MFMA on this path), peak = MI355X FP32 "
+                                "(counts packed FP32, which this build does not use)",
+                        "attainable": {"peak": round(att, 2), "frac": round(achieved / att, 4),
+                                       "note": "measured FP32 FMA-chain probe (single, not packed, VALU "
+                                               "instructions) on this GPU in this run"}}
+            if "raster_fwd" in per_step and "raster_bwd" in per_step:
+                t_fb = (per_step["raster_fwd"][1] + per_step["raster_bwd"][1]) * 1e-3
+                fb = (FWD_FLOPS_PER_EVAL + BWD_FLOPS_PER_EVAL) * e_bwd / t_fb / 1e12
+                roofline["raster_fwd_bwd"] = {"achieved": round(fb, 3), "frac_of_attainable": round(fb / att, 4),
+                                              "ms": round(t_fb * 1e3, 4)}
         else:
             achieved = per_launch / (avg_ms * 1e-3) / 1e9
             roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
@@ -288,6 +298,33 @@ def main():
         "kernels_us_per_step": {k: round(v[1] * 1000, 1) for k, v in sorted(per_step.items())},
     }
     print(json.dumps(line), flush=True)
+
+
+def valu_attainable_tflops(lib, torch):
+    """Attainable FP32 rate of single (not packed) VALU instructions on this
+    GPU: the library's FMA-chain probe (8 independent chains per lane, 8
+    workgroups per CU) timed with HIP events on the launch stream."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    blocks, iters = 8 * cus, 4096
+    out = torch.empty(blocks * 256, device="cuda")
+    lib.gsplat_hip_valu_probe.restype = ctypes.c_int
+    lib.gsplat_hip_valu_probe.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_void_p]
+    stream = torch.cuda.current_stream()
+
+    def run():
+        if lib.gsplat_hip_valu_probe(out.data_ptr(), blocks, iters, stream.cuda_stream) != 0:
+            raise RuntimeError("valu probe failed")
+
+    run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(3):
+        run()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 3
+    return blocks * 256 * 8 * 2 * iters / (ms * 1e-3) / 1e12
 
 
 def measured_traffic(workload, kernel):

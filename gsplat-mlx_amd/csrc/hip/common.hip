@@ -118,7 +118,31 @@ int fill_zero_spans(const ZeroSpan* spans, int n_spans, hipStream_t stream) {
   return check_launch("fill_zero");
 }
 
+// Attainable FP32 VALU rate: 8 independent FMA chains per lane keep every
+// SIMD issuing single (not packed) FP32 instructions; the flops per launch
+// are blocks * 256 lanes * 8 chains * 2 * iters.
+__global__ void __launch_bounds__(256) valu_probe_kernel(float* __restrict__ out, int iters, float b, float c) {
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = static_cast<float>(threadIdx.x) * 1.0e-3f + static_cast<float>(i);
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) a[i] = __builtin_fmaf(a[i], b, c);
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) sum += a[i];
+  out[static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x] = sum;
+}
+
 }  // namespace gsplat_hip
+
+extern "C" int gsplat_hip_valu_probe(float* out, int64_t blocks, int32_t iters, void* stream) {
+  if (!out || blocks <= 0 || blocks > 65535 || iters <= 0) return gsplat_hip::invalid("valu_probe: invalid arguments.");
+  gsplat_hip::valu_probe_kernel<<<static_cast<unsigned>(blocks), 256, 0, gsplat_hip::as_stream(stream)>>>(
+      out, iters, 0.999f, 0.001f);
+  return gsplat_hip::check_launch("valu_probe");
+}
 
 extern "C" const char* gsplat_hip_last_error(void) { return gsplat_hip::g_last_error.c_str(); }
 

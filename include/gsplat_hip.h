@@ -51,6 +51,13 @@ void gsplat_hip_profile_enable(int32_t enable);
 void gsplat_hip_profile_reset(void);
 size_t gsplat_hip_profile_report(char* buf, size_t buf_len);
 
+/* Measurement probe (no counterpart in the reference; used by the
+ * benchmark): `blocks` workgroups of 256 lanes each run 8 independent FP32
+ * FMA chains of `iters` steps and write one float per lane to out
+ * [blocks * 256]. Timed by the caller, it gives the attainable FP32 rate of
+ * single (not packed) VALU instructions: blocks * 256 * 8 * 2 * iters flops. */
+int gsplat_hip_valu_probe(float* out, int64_t blocks, int32_t iters, void* stream);
+
 /* ---------------------------------------------------------------------------
  * quat_scale_to_covar_preci
  * Replaces GSPlatQuatScaleToCovarPreci(/Backward)::eval_gpu
