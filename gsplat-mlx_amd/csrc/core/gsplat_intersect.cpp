@@ -70,19 +70,22 @@ struct Counted {
   array total;  // int64 [1] on device
 };
 
-Counted count_and_scan(const IntersectTileInput& input, void* stream) {
+// with_offsets false: counts and total only (the depth-presorted path scans
+// the counts in depth order itself).
+Counted count_and_scan(const IntersectTileInput& input, void* stream, bool with_offsets = true) {
   const array means2d = contig(input.means2d);
   const array radii = contig(input.radii);
   const int64_t numel = input.depths.numel();
   Counted c;
   c.tiles_per_gauss = at::empty(input.depths.sizes(), i32_like(means2d));
-  c.offsets = at::empty(input.depths.sizes(), i32_like(means2d));
+  if (with_offsets) c.offsets = at::empty(input.depths.sizes(), i32_like(means2d));
   c.total = at::empty({1}, i64_like(means2d));
   const size_t ws_bytes = gsplat_hip_isect_count_scan_workspace_size(numel);
   array ws = workspace(ws_bytes, means2d);
   check(gsplat_hip_isect_count_scan(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), numel,
                                     input.params.tile_size, input.params.tile_width, input.params.tile_height,
-                                    c.tiles_per_gauss.data_ptr<int32_t>(), c.offsets.data_ptr<int32_t>(),
+                                    c.tiles_per_gauss.data_ptr<int32_t>(),
+                                    with_offsets ? c.offsets.data_ptr<int32_t>() : nullptr,
                                     c.total.data_ptr<int64_t>(), ws.data_ptr<uint8_t>(), ws_bytes, stream));
   return c;
 }
@@ -248,7 +251,7 @@ std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& in
     throw std::runtime_error("intersect_tile_encode image id and tile id require more than 32 bits.");
   const c10::DeviceGuard guard(input.means2d.device());
   void* stream = stream_for(input.s, input.means2d);
-  Counted c = count_and_scan(input, stream);
+  Counted c = count_and_scan(input, stream, !input.params.sort);
   const array means2d = contig(input.means2d);
   const array radii = contig(input.radii);
   const array depths = contig(input.depths);

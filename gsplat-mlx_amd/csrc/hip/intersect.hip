@@ -58,10 +58,12 @@ __global__ void __launch_bounds__(kScanBlock) count_scan_local_kernel(const floa
   }
   int64_t total;
   int64_t run = block_exclusive_scan(sum, &total);
+  if (offsets) {  // null: the caller needs only the counts and their total
 #pragma unroll
-  for (int k = 0; k < kScanItems; ++k) {
-    if (base + k < n) offsets[base + k] = static_cast<int32_t>(run);
-    run += v[k];
+    for (int k = 0; k < kScanItems; ++k) {
+      if (base + k < n) offsets[base + k] = static_cast<int32_t>(run);
+      run += v[k];
+    }
   }
   if (threadIdx.x == 0) block_sums[blockIdx.x] = total;
 }
@@ -389,7 +391,7 @@ extern "C" int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* 
     return invalid("intersect_tile_count: invalid sizes.");
   if (!total_dev) return invalid("intersect_tile_count: null total.");
   if (numel == 0) return fill_zero(total_dev, sizeof(int64_t), s);
-  if (!means2d || !radii || !tiles_per_gauss || !offsets) return invalid("intersect_tile_count: null pointer.");
+  if (!means2d || !radii || !tiles_per_gauss) return invalid("intersect_tile_count: null pointer.");
   if (!workspace || workspace_bytes < scan_workspace_bytes(numel)) {
     set_error("intersect_tile_count: workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
@@ -409,7 +411,7 @@ extern "C" int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* 
     block_sums_scan_kernel<<<1, kScanBlock, 0, s>>>(sums, nb, total_dev);
   }
   rc = check_launch("intersect_tile_offsets (block sums)");
-  if (rc || nb == 1) return rc;
+  if (rc || nb == 1 || !offsets) return rc;
   {
     KernelTimer timer("scan_fixup", s);
     add_block_prefix_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(offsets, numel, sums);

@@ -176,6 +176,9 @@ int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const fl
  * (gsplat_intersect.cpp:196-211). means2d [numel,2], radii [numel,2] int32;
  * writes tiles_per_gauss [numel] and offsets [numel] (exclusive scan), and
  * the total intersection count as one int64 at *total_dev (device memory).
+ * offsets may be NULL when only the counts and the total are needed (the
+ * depth-presorted path below scans the counts in depth order instead); that
+ * skips the scan's fix-up pass.
  * ------------------------------------------------------------------------- */
 size_t gsplat_hip_isect_count_scan_workspace_size(int64_t numel);
 int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* radii, int64_t numel,
