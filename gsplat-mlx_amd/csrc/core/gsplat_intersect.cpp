@@ -34,8 +34,8 @@ int bit_length(uint64_t v) {
 void validate_intersect_tile_input(const IntersectTileInput& input) {
   if (input.params.packed) throw std::runtime_error("intersect_tile packed path is not implemented yet.");
   if (input.params.segmented) throw std::runtime_error("intersect_tile segmented sort is not implemented yet.");
-  if (input.params.use_conics || input.params.use_opacities)
-    throw std::runtime_error("intersect_tile AccuTile conics/opacities path is not implemented yet.");
+  if (input.params.use_conics != input.params.use_opacities)
+    throw std::runtime_error("intersect_tile AccuTile path needs both conics and opacities.");
   if (input.means2d.dim() < 3 || input.means2d.size(-1) != 2)
     throw std::runtime_error("means2d must have shape [..., N, 2].");
   if (input.radii.dim() != input.means2d.dim() || input.radii.size(-1) != 2)
@@ -47,7 +47,18 @@ void validate_intersect_tile_input(const IntersectTileInput& input) {
   require_device(input.means2d, "means2d");
   require_device(input.radii, "radii");
   require_device(input.depths, "depths");
+  if (input.params.use_conics) {
+    if (input.conics.scalar_type() != at::kFloat || input.opacities.scalar_type() != at::kFloat)
+      throw std::runtime_error("intersect_tile AccuTile path expects float32 conics and opacities.");
+    if (input.conics.numel() != input.depths.numel() * 3 || input.opacities.numel() != input.depths.numel())
+      throw std::runtime_error("intersect_tile AccuTile path expects conics [..., N, 3] and opacities [..., N].");
+    require_device(input.conics, "conics");
+    require_device(input.opacities, "opacities");
+  }
 }
+
+// Ellipse tiles (conics and opacities given), else the AABB rect.
+bool accutile(const IntersectTileInput& input) { return input.params.use_conics && input.params.use_opacities; }
 
 void check_dense_size(const IntersectTileInput& input, const char* op) {
   const int64_t n = input.means2d.size(-2);
@@ -82,11 +93,21 @@ Counted count_and_scan(const IntersectTileInput& input, void* stream, bool with_
   c.total = at::empty({1}, i64_like(means2d));
   const size_t ws_bytes = gsplat_hip_isect_count_scan_workspace_size(numel);
   array ws = workspace(ws_bytes, means2d);
+  int32_t* offs = with_offsets ? c.offsets.data_ptr<int32_t>() : nullptr;
+  if (accutile(input)) {
+    const array conics = contig(input.conics);
+    const array opac = contig(input.opacities);
+    check(gsplat_hip_isect_count_scan_accutile(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(),
+                                               conics.data_ptr<float>(), opac.data_ptr<float>(), numel,
+                                               input.params.tile_size, input.params.tile_width,
+                                               input.params.tile_height, c.tiles_per_gauss.data_ptr<int32_t>(), offs,
+                                               c.total.data_ptr<int64_t>(), ws.data_ptr<uint8_t>(), ws_bytes, stream));
+    return c;
+  }
   check(gsplat_hip_isect_count_scan(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), numel,
                                     input.params.tile_size, input.params.tile_width, input.params.tile_height,
-                                    c.tiles_per_gauss.data_ptr<int32_t>(),
-                                    with_offsets ? c.offsets.data_ptr<int32_t>() : nullptr,
-                                    c.total.data_ptr<int64_t>(), ws.data_ptr<uint8_t>(), ws_bytes, stream));
+                                    c.tiles_per_gauss.data_ptr<int32_t>(), offs, c.total.data_ptr<int64_t>(),
+                                    ws.data_ptr<uint8_t>(), ws_bytes, stream));
   return c;
 }
 
@@ -167,6 +188,28 @@ int encoded_key_bits(int64_t I, int64_t n_tiles) {
   return bit_length(max_key);
 }
 
+// Encode in pair-major order (no sort): {isect_ids, flatten_ids}.
+std::vector<array> encode_unsorted(const IntersectTileInput& input, const array& means2d, const array& radii,
+                                   const array& depths, const array& offsets, int total, void* stream) {
+  array ids = at::empty({total}, i64_like(means2d));
+  array flat = at::empty({total}, i32_like(means2d));
+  if (accutile(input)) {
+    const array conics = contig(input.conics);
+    const array opac = contig(input.opacities);
+    check(gsplat_hip_isect_encode_accutile(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(),
+                                           conics.data_ptr<float>(), opac.data_ptr<float>(), depths.data_ptr<float>(),
+                                           offsets.data_ptr<int32_t>(), input.params.I, depths.numel(),
+                                           input.params.tile_size, input.params.tile_width, input.params.tile_height,
+                                           total, ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), stream));
+  } else {
+    check(gsplat_hip_isect_encode(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), depths.data_ptr<float>(),
+                                  offsets.data_ptr<int32_t>(), input.params.I, depths.numel(), input.params.tile_size,
+                                  input.params.tile_width, input.params.tile_height, total, ids.data_ptr<int64_t>(),
+                                  flat.data_ptr<int32_t>(), stream));
+  }
+  return {ids, flat};
+}
+
 }  // namespace
 
 array gsplat_intersect_tile_count(const IntersectTileInput& input) {
@@ -207,14 +250,7 @@ std::vector<array> gsplat_intersect_tile_encode(const IntersectTileInput& input,
   const array radii = contig(input.radii);
   const array depths = contig(input.depths);
   const array offsets = contig(tile_offsets);
-  array ids = at::empty({total_isects}, i64_like(means2d));
-  array flat = at::empty({total_isects}, i32_like(means2d));
-  check(gsplat_hip_isect_encode(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), depths.data_ptr<float>(),
-                                offsets.data_ptr<int32_t>(), input.params.I, depths.numel(), input.params.tile_size,
-                                input.params.tile_width, input.params.tile_height, total_isects,
-                                ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(),
-                                stream_for(input.s, means2d)));
-  return {ids, flat};
+  return encode_unsorted(input, means2d, radii, depths, offsets, total_isects, stream_for(input.s, means2d));
 }
 
 std::vector<array> gsplat_intersect_tile_sort(const array& isect_ids, const array& flatten_ids, StreamOrDevice s) {
@@ -274,22 +310,27 @@ std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& in
     array flat = at::empty({total}, i32_like(means2d));
     const size_t ws2_bytes = gsplat_hip_isect_encode_sorted_workspace_size(total);
     array ws2 = workspace(ws2_bytes, means2d);
-    check(gsplat_hip_isect_encode_sorted(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(),
-                                         depths.data_ptr<float>(), perm.data_ptr<int32_t>(),
-                                         offs.data_ptr<int32_t>(), input.params.I, numel, input.params.tile_size,
-                                         input.params.tile_width, input.params.tile_height, total,
-                                         ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), ws2.data_ptr<uint8_t>(),
-                                         ws2_bytes, stream));
+    if (accutile(input)) {
+      const array conics = contig(input.conics);
+      const array opac = contig(input.opacities);
+      check(gsplat_hip_isect_encode_sorted_accutile(
+          means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), conics.data_ptr<float>(), opac.data_ptr<float>(),
+          depths.data_ptr<float>(), perm.data_ptr<int32_t>(), offs.data_ptr<int32_t>(), input.params.I, numel,
+          input.params.tile_size, input.params.tile_width, input.params.tile_height, total, ids.data_ptr<int64_t>(),
+          flat.data_ptr<int32_t>(), ws2.data_ptr<uint8_t>(), ws2_bytes, stream));
+    } else {
+      check(gsplat_hip_isect_encode_sorted(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(),
+                                           depths.data_ptr<float>(), perm.data_ptr<int32_t>(),
+                                           offs.data_ptr<int32_t>(), input.params.I, numel, input.params.tile_size,
+                                           input.params.tile_width, input.params.tile_height, total,
+                                           ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(),
+                                           ws2.data_ptr<uint8_t>(), ws2_bytes, stream));
+    }
     return {c.tiles_per_gauss, ids, flat};
   }
   const int total = read_total(c.total, stream);
-  array ids = at::empty({total}, i64_like(means2d));
-  array flat = at::empty({total}, i32_like(means2d));
-  check(gsplat_hip_isect_encode(means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), depths.data_ptr<float>(),
-                                c.offsets.data_ptr<int32_t>(), input.params.I, depths.numel(),
-                                input.params.tile_size, input.params.tile_width, input.params.tile_height, total,
-                                ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), stream));
-  return {c.tiles_per_gauss, ids, flat};
+  auto enc = encode_unsorted(input, means2d, radii, depths, c.offsets, total, stream);
+  return {c.tiles_per_gauss, enc[0], enc[1]};
 }
 
 std::vector<array> gsplat_intersect_tile(const IntersectTileInput& input) {

@@ -34,9 +34,171 @@ __device__ __forceinline__ TileRect aabb_tile_rect(float mx, float my, int rx, i
   return r;
 }
 
-// Count per Gaussian fused with the block-local exclusive scan.
+// ---------------------------------------------------------------------------
+// Ellipse tile intersection (the use_conics / use_opacities path that
+// gsplat_intersect.cpp:123-126 rejects and leaves to upstream gsplat's
+// IntersectTile.cu, Task_Metal.md:95-115). The method is Speedy-Splat's
+// SnugBox + AccuTile (Hanson et al., CVPR 2025): a Gaussian only needs the
+// tiles where some pixel centre can pass the rasterizer's alpha test,
+// alpha = min(0.999, o exp(-sigma)) >= 1/255, sigma = d^T Q d / 2 with Q the
+// conic. That holds inside the ellipse d^T Q d <= 2 ln(255 o); the test below
+// uses the same slack as the rasterizer's per-wave cull, 1.05 ln(255 o) +
+// 1e-4, and the same conditions under which a conic is never culled, so
+// every entry it drops has alpha < 1/255 at every pixel of the dropped tile.
+//
+// Tiles are the Gaussian's AABB rect (aabb_tile_rect, the reference set)
+// intersected with the ellipse, row by row: within tile row ty the pixel
+// centres span y in [ty ts + 1/2, ty ts + ts - 1/2]; the ellipse's x-extent
+// over that slab is [xl, xr], where the extreme points of the ellipse
+// (dy = -/+ b x_ext / c) are clamped into the slab (the boundary is concave
+// on the right and convex on the left, so the clamped point is the extreme);
+// the row's tiles are the columns whose pixel centres meet [xl, xr]. Every
+// row's tiles are contiguous, and entries keep the reference's order:
+// row-major within each Gaussian.
+//
+// Only + - * /, sqrt, floor and frexp are used, with contraction off, so the
+// CPU restatement gives the same tiles bit for bit.
+//
+// mode 0: no tiles (opacity <= 0, or ln(255 o) too small for any pixel);
+// mode 1: the whole rect (non-finite values, opacity NaN or too large for
+//         the log, conic not positive-definite or det <= 1e-4 a c);
+// mode 2: per-row intervals.
+struct EllipseTiles {
+  TileRect r;
+  int mode;
+  float mx, my, a, b, det, aR, ye, dyl;
+};
+
+// ln z for finite z > 0: z = m 2^e with m in [sqrt(1/2), sqrt(2)), and
+// ln m = 2 atanh(s), s = (m - 1) / (m + 1), |s| < 0.172, by the odd series
+// to s^9 (truncation below 1e-9 relative).
+__device__ __forceinline__ float ellipse_ln(float z) {
+  int e = 0;
+  float m = frexpf(z, &e);
+  if (m < 0.70710678f) {
+    m = m * 2.0f;
+    e = e - 1;
+  }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float p = 0.11111111f;
+  p = p * s2 + 0.14285715f;
+  p = p * s2 + 0.2f;
+  p = p * s2 + 0.33333334f;
+  p = p * s2 + 1.0f;
+  return static_cast<float>(e) * 0.69314718f + 2.0f * s * p;
+}
+
+__device__ __forceinline__ EllipseTiles ellipse_tiles(const float* __restrict__ means2d,
+                                                      const int32_t* __restrict__ radii,
+                                                      const float* __restrict__ conics,
+                                                      const float* __restrict__ opacities, int64_t g, int ts,
+                                                      int tw, int th) {
+  EllipseTiles e;
+  e.mx = means2d[g * 2];
+  e.my = means2d[g * 2 + 1];
+  e.r = aabb_tile_rect(e.mx, e.my, radii[g * 2], radii[g * 2 + 1], ts, tw, th);
+  e.mode = 1;
+  e.a = e.b = e.det = e.aR = e.ye = e.dyl = 0.0f;
+  if (e.r.max_x <= e.r.min_x || e.r.max_y <= e.r.min_y) {
+    e.mode = 0;
+    return e;
+  }
+  const float o = opacities[g];
+  if (o <= 0.0f) {
+    e.mode = 0;
+    return e;
+  }
+  const float z = 255.0f * o;
+  const float a = conics[g * 3], b = conics[g * 3 + 1], c = conics[g * 3 + 2];
+  if (!(z < 3.0e38f) || !(a > 0.0f && c > 0.0f && a < 1.0e30f && c < 1.0e30f) ||
+      !(fabsf(e.mx) < 1.0e30f) || !(fabsf(e.my) < 1.0e30f))
+    return e;
+  const float det = a * c - b * b;
+  if (!(det > 1.0e-4f * a * c)) return e;
+  const float lim = 1.05f * ellipse_ln(z) + 1.0e-4f;  // bound on sigma
+  if (!(lim >= 0.0f)) {
+    e.mode = 0;
+    return e;
+  }
+  const float R = 2.0f * lim;  // bound on d^T Q d
+  const float xe = sqrtf(R * c / det);
+  e.mode = 2;
+  e.a = a;
+  e.b = b;
+  e.det = det;
+  e.aR = a * R;
+  e.ye = sqrtf(R * a / det);
+  e.dyl = b * xe / c;  // dy of the leftmost point; the rightmost is at -dyl
+  return e;
+}
+
+// Columns [*c0, *c1) of tile row ty (empty: *c1 <= *c0).
+__device__ __forceinline__ void ellipse_row(const EllipseTiles& e, int ty, int ts, int* c0, int* c1) {
+  if (e.mode != 2) {
+    *c0 = e.r.min_x;
+    *c1 = e.mode == 1 ? e.r.max_x : e.r.min_x;
+    return;
+  }
+  const float y0 = static_cast<float>(ty * ts) + 0.5f;
+  const float y1 = y0 + static_cast<float>(ts - 1);
+  const float d0 = fmaxf(y0 - e.my, -e.ye);
+  const float d1 = fminf(y1 - e.my, e.ye);
+  if (!(d0 <= d1)) {
+    *c0 = *c1 = e.r.min_x;
+    return;
+  }
+  const float dl = fminf(fmaxf(e.dyl, d0), d1);
+  const float dr = fminf(fmaxf(-e.dyl, d0), d1);
+  const float ql = sqrtf(fmaxf(e.aR - e.det * dl * dl, 0.0f));
+  const float qr = sqrtf(fmaxf(e.aR - e.det * dr * dr, 0.0f));
+  const float xl = e.mx - (e.b * dl + ql) / e.a;
+  const float xr = e.mx + (qr - e.b * dr) / e.a;
+  const float fts = static_cast<float>(ts);
+  const float lo = floorf((xl + 0.5f) / fts);
+  const float hi = floorf((xr - 0.5f) / fts) + 1.0f;
+  const float fmin = static_cast<float>(e.r.min_x), fmax = static_cast<float>(e.r.max_x);
+  *c0 = static_cast<int>(fminf(fmaxf(lo, fmin), fmax));
+  *c1 = static_cast<int>(fminf(fmaxf(hi, fmin), fmax));
+}
+
+__device__ __forceinline__ int32_t ellipse_count(const EllipseTiles& e, int ts) {
+  if (e.mode == 0) return 0;
+  if (e.mode == 1) return (e.r.max_y - e.r.min_y) * (e.r.max_x - e.r.min_x);
+  int32_t n = 0;
+  for (int ty = e.r.min_y; ty < e.r.max_y; ++ty) {
+    int c0, c1;
+    ellipse_row(e, ty, ts, &c0, &c1);
+    n += max(c1 - c0, 0);
+  }
+  return n;
+}
+
+// Tile of the Gaussian's k-th entry (row-major); false when k is past its
+// last entry (offsets inconsistent with the counts).
+__device__ __forceinline__ bool ellipse_locate(const EllipseTiles& e, int ts, int k, int* ty, int* tx, int* row_end) {
+  for (int y = e.r.min_y; y < e.r.max_y; ++y) {
+    int c0, c1;
+    ellipse_row(e, y, ts, &c0, &c1);
+    const int w = max(c1 - c0, 0);
+    if (k < w) {
+      *ty = y;
+      *tx = c0 + k;
+      *row_end = c1;
+      return true;
+    }
+    k -= w;
+  }
+  return false;
+}
+
+// Count per Gaussian fused with the block-local exclusive scan; with conics
+// and opacities (ELL) the ellipse count, else the AABB rect's.
+template <bool ELL>
 __global__ void __launch_bounds__(kScanBlock) count_scan_local_kernel(const float* __restrict__ means2d,
                                                                       const int32_t* __restrict__ radii,
+                                                                      const float* __restrict__ conics,
+                                                                      const float* __restrict__ opacities,
                                                                       int64_t n, int ts, int tw, int th,
                                                                       int32_t* __restrict__ counts,
                                                                       int32_t* __restrict__ offsets,
@@ -49,8 +211,13 @@ __global__ void __launch_bounds__(kScanBlock) count_scan_local_kernel(const floa
     const int64_t i = base + k;
     int32_t c = 0;
     if (i < n) {
-      const TileRect r = aabb_tile_rect(means2d[i * 2], means2d[i * 2 + 1], radii[i * 2], radii[i * 2 + 1], ts, tw, th);
-      c = (r.max_y - r.min_y) * (r.max_x - r.min_x);
+      if constexpr (ELL) {
+        c = ellipse_count(ellipse_tiles(means2d, radii, conics, opacities, i, ts, tw, th), ts);
+      } else {
+        const TileRect r =
+            aabb_tile_rect(means2d[i * 2], means2d[i * 2 + 1], radii[i * 2], radii[i * 2 + 1], ts, tw, th);
+        c = (r.max_y - r.min_y) * (r.max_x - r.min_x);
+      }
       counts[i] = c;
     }
     v[k] = c;
@@ -347,6 +514,97 @@ int check_tile_bits(int64_t I, int32_t tile_width, int32_t tile_height, int* til
   return GSPLAT_OK;
 }
 
+// Encode of the ellipse tiles, balanced like encode_presorted_kernel (merge
+// path over ranks and output slots). Rank r is pair perm[r], or pair r when
+// perm is NULL (the unsorted encode order). With keys32 the output is the
+// 32-bit key image << tile_bits | tile for the (image, tile) sort; else ids64
+// gets the full 64-bit id with the depth bits. Each thread locates its first
+// slot's tile by walking the Gaussian's rows and steps along the row for the
+// next ones.
+__global__ void __launch_bounds__(kEncodeBlock) encode_ellipse_kernel(
+    const float* __restrict__ means2d, const int32_t* __restrict__ radii, const float* __restrict__ conics,
+    const float* __restrict__ opacities, const float* __restrict__ depths, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ offsets, int64_t numel, int64_t n_per_image, int ts, int tw, int th, int tile_bits,
+    int64_t n_isects, uint32_t* __restrict__ keys32, int64_t* __restrict__ ids64, int32_t* __restrict__ vals) {
+  constexpr int kRanks = kMergeItems + 1;
+  __shared__ int32_t s_off[kRanks];
+  __shared__ int32_t s_g[kRanks];
+  __shared__ int64_t s_split[2];
+  const int t = threadIdx.x;
+  const int lane = t % kWave;
+  const int wave = t / kWave;
+  const int64_t total = numel + n_isects;
+  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kMergeItems;
+  const int64_t d1 = min<int64_t>(d0 + kMergeItems, total);
+  if (wave < 2) {
+    const int64_t r = merge_split(offsets, numel, n_isects, wave == 0 ? d0 : d1, lane);
+    if (lane == 0) s_split[wave] = r;
+  }
+  __syncthreads();
+  const int64_t r0 = s_split[0], r1 = s_split[1];
+  const int64_t j0 = d0 - r0, j1 = d1 - r1;
+  const int64_t rs = r0 > 0 ? r0 - 1 : 0;
+  const int nr = static_cast<int>(min<int64_t>(max<int64_t>(r1 - rs, 0), kRanks));
+  for (int i = t; i < nr; i += kEncodeBlock) {
+    s_off[i] = offsets[rs + i];
+    s_g[i] = perm ? perm[rs + i] : static_cast<int32_t>(rs + i);
+  }
+  __syncthreads();
+  if (nr == 0) return;
+  const int64_t jb = j0 + static_cast<int64_t>(t) * kMergeOuts;
+  if (jb >= min<int64_t>(j1, n_isects)) return;
+  int lo = 0, hi = nr - 1;  // last i with s_off[i] <= jb
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_off[mid] <= jb)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  int i = lo, cur = -1;
+  EllipseTiles e = {};
+  bool valid = false, ok = false;
+  int ty = 0, tx = 0, row_end = 0;
+  for (int q = 0; q < kMergeOuts; ++q) {
+    const int64_t j = jb + q;
+    if (j >= j1 || j >= n_isects) break;
+    while (i + 1 < nr && s_off[i + 1] <= j) ++i;
+    const int64_t g = s_g[i];
+    if (i != cur) {
+      cur = i;
+      valid = g >= 0 && g < numel;
+      ok = false;
+      if (valid) {
+        e = ellipse_tiles(means2d, radii, conics, opacities, g, ts, tw, th);
+        ok = ellipse_locate(e, ts, static_cast<int>(j - s_off[i]), &ty, &tx, &row_end);
+      }
+    } else if (ok && ++tx >= row_end) {
+      ok = false;
+      for (int y = ty + 1; y < e.r.max_y && !ok; ++y) {
+        int c0, c1;
+        ellipse_row(e, y, ts, &c0, &c1);
+        if (c1 > c0) {
+          ty = y;
+          tx = c0;
+          row_end = c1;
+          ok = true;
+        }
+      }
+    }
+    // offsets that disagree with the counts still get an in-range tile
+    const int tile = !valid ? 0 : ok ? ty * tw + tx : e.r.min_y * tw + e.r.min_x;
+    const uint32_t image = valid ? static_cast<uint32_t>(g / n_per_image) : 0u;
+    const uint32_t key = (image << tile_bits) | static_cast<uint32_t>(tile);
+    if (keys32) {
+      keys32[j] = key;
+    } else {
+      const uint32_t bits = valid ? __float_as_uint(depths[g]) : 0u;
+      ids64[j] = static_cast<int64_t>((static_cast<uint64_t>(key) << 32) | bits);
+    }
+    vals[j] = static_cast<int32_t>(g);
+  }
+}
+
 // Tile offsets as lower_bound over sorted keys (gsplat_intersect.cpp:605-641),
 // computed in O(n_isects): entry i owns the offset slots o whose search key
 // (o / n_tiles) << tile_bits | (o % n_tiles) lies in (v[i-1], v[i]], with
@@ -382,16 +640,18 @@ using namespace gsplat_hip;
 
 extern "C" size_t gsplat_hip_isect_count_scan_workspace_size(int64_t numel) { return scan_workspace_bytes(numel); }
 
-extern "C" int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* radii, int64_t numel,
-                                           int32_t tile_size, int32_t tile_width, int32_t tile_height,
-                                           int32_t* tiles_per_gauss, int32_t* offsets, int64_t* total_dev,
-                                           void* workspace, size_t workspace_bytes, void* stream) {
+template <bool ELL>
+static int count_scan_impl(const float* means2d, const int32_t* radii, const float* conics, const float* opacities,
+                           int64_t numel, int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                           int32_t* tiles_per_gauss, int32_t* offsets, int64_t* total_dev, void* workspace,
+                           size_t workspace_bytes, void* stream) {
   hipStream_t s = as_stream(stream);
   if (numel < 0 || tile_size <= 0 || tile_width <= 0 || tile_height <= 0)
     return invalid("intersect_tile_count: invalid sizes.");
   if (!total_dev) return invalid("intersect_tile_count: null total.");
   if (numel == 0) return fill_zero(total_dev, sizeof(int64_t), s);
   if (!means2d || !radii || !tiles_per_gauss) return invalid("intersect_tile_count: null pointer.");
+  if (ELL && (!conics || !opacities)) return invalid("intersect_tile_count: null conics or opacities.");
   if (!workspace || workspace_bytes < scan_workspace_bytes(numel)) {
     set_error("intersect_tile_count: workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
@@ -400,9 +660,8 @@ extern "C" int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* 
   int64_t* sums = static_cast<int64_t*>(workspace);
   {
     KernelTimer timer("isect_count_scan", s);
-    count_scan_local_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(means2d, radii, numel, tile_size,
-                                                                            tile_width, tile_height, tiles_per_gauss,
-                                                                            offsets, sums);
+    count_scan_local_kernel<ELL><<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(
+        means2d, radii, conics, opacities, numel, tile_size, tile_width, tile_height, tiles_per_gauss, offsets, sums);
   }
   int rc = check_launch("intersect_tile_count");
   if (rc) return rc;
@@ -417,6 +676,23 @@ extern "C" int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* 
     add_block_prefix_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(offsets, numel, sums);
   }
   return check_launch("intersect_tile_offsets (fixup)");
+}
+
+extern "C" int gsplat_hip_isect_count_scan(const float* means2d, const int32_t* radii, int64_t numel,
+                                           int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                           int32_t* tiles_per_gauss, int32_t* offsets, int64_t* total_dev,
+                                           void* workspace, size_t workspace_bytes, void* stream) {
+  return count_scan_impl<false>(means2d, radii, nullptr, nullptr, numel, tile_size, tile_width, tile_height,
+                                tiles_per_gauss, offsets, total_dev, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gsplat_hip_isect_count_scan_accutile(const float* means2d, const int32_t* radii, const float* conics,
+                                                    const float* opacities, int64_t numel, int32_t tile_size,
+                                                    int32_t tile_width, int32_t tile_height, int32_t* tiles_per_gauss,
+                                                    int32_t* offsets, int64_t* total_dev, void* workspace,
+                                                    size_t workspace_bytes, void* stream) {
+  return count_scan_impl<true>(means2d, radii, conics, opacities, numel, tile_size, tile_width, tile_height,
+                               tiles_per_gauss, offsets, total_dev, workspace, workspace_bytes, stream);
 }
 
 extern "C" int gsplat_hip_isect_encode(const float* means2d, const int32_t* radii, const float* depths,
@@ -538,6 +814,73 @@ extern "C" int gsplat_hip_isect_encode_sorted(const float* means2d, const int32_
   }
   if ((rc = check_launch(what))) return rc;
   // the last pass writes the 64-bit ids (key << 32 | depth bits) directly
+  return radix_sort_pairs<uint32_t>(l.tkeys, l.tvals, n_isects, 0, image_bits + tile_bits, l.tkeys_sorted,
+                                    flatten_ids, l.sort_ws, l.sort_ws_bytes, s, what, depths, isect_ids);
+}
+
+// Ellipse tiles, unsorted: entries in pair-major, row-major order like
+// gsplat_hip_isect_encode; offsets from gsplat_hip_isect_count_scan_accutile.
+extern "C" int gsplat_hip_isect_encode_accutile(const float* means2d, const int32_t* radii, const float* conics,
+                                                const float* opacities, const float* depths, const int32_t* offsets,
+                                                int64_t I, int64_t numel, int32_t tile_size, int32_t tile_width,
+                                                int32_t tile_height, int64_t n_isects, int64_t* isect_ids,
+                                                int32_t* flatten_ids, void* stream) {
+  if (I <= 0 || numel < 0 || numel % I != 0)
+    return invalid("intersect_tile_encode dense path expects depths size to equal I * N.");
+  if (tile_size <= 0 || tile_width <= 0 || tile_height <= 0) return invalid("intersect_tile_encode: invalid tiles.");
+  if (n_isects < 0) return invalid("intersect_tile_encode expects non-negative total_isects.");
+  if (numel > INT32_MAX || n_isects > INT32_MAX) return invalid("intersect_tile: more than 2^31-1 entries.");
+  int tile_bits, image_bits, rc;
+  if ((rc = check_tile_bits(I, tile_width, tile_height, &tile_bits, &image_bits))) return rc;
+  if (numel == 0 || n_isects == 0) return GSPLAT_OK;
+  if (!means2d || !radii || !conics || !opacities || !depths || !offsets || !isect_ids || !flatten_ids)
+    return invalid("intersect_tile_encode: null pointer.");
+  hipStream_t s = as_stream(stream);
+  {
+    KernelTimer timer("isect_encode", s);
+    const int64_t nb = (numel + n_isects + kMergeItems - 1) / kMergeItems;
+    encode_ellipse_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
+        means2d, radii, conics, opacities, depths, nullptr, offsets, numel, numel / I, tile_size, tile_width,
+        tile_height, tile_bits, n_isects, nullptr, isect_ids, flatten_ids);
+  }
+  return check_launch("intersect_tile_encode");
+}
+
+// Ellipse tiles, sorted: gsplat_hip_isect_encode_sorted with the ellipse
+// tiles (perm and offsets from gsplat_hip_isect_depth_order over the counts
+// of gsplat_hip_isect_count_scan_accutile).
+extern "C" int gsplat_hip_isect_encode_sorted_accutile(const float* means2d, const int32_t* radii,
+                                                       const float* conics, const float* opacities,
+                                                       const float* depths, const int32_t* perm,
+                                                       const int32_t* offsets, int64_t I, int64_t numel,
+                                                       int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                                       int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
+                                                       void* workspace, size_t workspace_bytes, void* stream) {
+  const char* what = "intersect_tile";
+  if (I <= 0 || numel < 0 || numel % I != 0)
+    return invalid("intersect_tile dense path expects depths size to equal I * N.");
+  if (tile_size <= 0 || tile_width <= 0 || tile_height <= 0) return invalid("intersect_tile: invalid tiles.");
+  if (n_isects < 0) return invalid("intersect_tile: negative intersection count.");
+  if (numel > INT32_MAX || n_isects > INT32_MAX) return invalid("intersect_tile: more than 2^31-1 entries.");
+  int tile_bits, image_bits, rc;
+  if ((rc = check_tile_bits(I, tile_width, tile_height, &tile_bits, &image_bits))) return rc;
+  if (numel == 0 || n_isects == 0) return GSPLAT_OK;
+  if (!means2d || !radii || !conics || !opacities || !depths || !perm || !offsets || !isect_ids || !flatten_ids)
+    return invalid("intersect_tile: null pointer.");
+  EncodeSortedLayout l;
+  if (!workspace || workspace_bytes < encode_sorted_layout(n_isects, &l, workspace)) {
+    set_error("intersect_tile: workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  hipStream_t s = as_stream(stream);
+  {
+    KernelTimer timer("isect_encode", s);
+    const int64_t nb = (numel + n_isects + kMergeItems - 1) / kMergeItems;
+    encode_ellipse_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
+        means2d, radii, conics, opacities, depths, perm, offsets, numel, numel / I, tile_size, tile_width,
+        tile_height, tile_bits, n_isects, l.tkeys, nullptr, l.tvals);
+  }
+  if ((rc = check_launch(what))) return rc;
   return radix_sort_pairs<uint32_t>(l.tkeys, l.tvals, n_isects, 0, image_bits + tile_bits, l.tkeys_sorted,
                                     flatten_ids, l.sort_ws, l.sort_ws_bytes, s, what, depths, isect_ids);
 }

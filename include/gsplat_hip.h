@@ -249,6 +249,35 @@ int gsplat_hip_isect_encode_sorted(const float* means2d, const int32_t* radii, c
                                    int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
                                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Ellipse ("AccuTile") tile intersection: the use_conics / use_opacities
+ * path of IntersectTileParams (gsplat_core/include/gsplat_intersect.h),
+ * which the reference rejects at gsplat_intersect.cpp:123-126 and leaves to
+ * upstream gsplat's IntersectTile.cu (Task_Metal.md:95-115). conics
+ * [numel,3] and opacities [numel] are the rasterizer's. A Gaussian keeps the
+ * tiles of its AABB rect whose pixel centres come within the ellipse
+ * d^T Q d <= 2 (1.05 ln(255 o) + 1e-4); every dropped entry has
+ * alpha < 1/255 at every pixel of its tile, so rendering is unchanged.
+ * Opacity <= 0 gives no tiles; non-finite values, 255 o >= 3e38 and
+ * conics with det <= 1e-4 a c keep the whole rect. Tiles stay row-major per
+ * Gaussian. The three calls replace count_scan, encode and encode_sorted
+ * (same workspaces); depth_order is shared. */
+int gsplat_hip_isect_count_scan_accutile(const float* means2d, const int32_t* radii, const float* conics,
+                                         const float* opacities, int64_t numel, int32_t tile_size,
+                                         int32_t tile_width, int32_t tile_height, int32_t* tiles_per_gauss,
+                                         int32_t* offsets, int64_t* total_dev, void* workspace,
+                                         size_t workspace_bytes, void* stream);
+int gsplat_hip_isect_encode_accutile(const float* means2d, const int32_t* radii, const float* conics,
+                                     const float* opacities, const float* depths, const int32_t* offsets,
+                                     int64_t I, int64_t numel, int32_t tile_size, int32_t tile_width,
+                                     int32_t tile_height, int64_t n_isects, int64_t* isect_ids,
+                                     int32_t* flatten_ids, void* stream);
+int gsplat_hip_isect_encode_sorted_accutile(const float* means2d, const int32_t* radii, const float* conics,
+                                            const float* opacities, const float* depths, const int32_t* perm,
+                                            const int32_t* offsets, int64_t I, int64_t numel, int32_t tile_size,
+                                            int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                            int64_t* isect_ids, int32_t* flatten_ids, void* workspace,
+                                            size_t workspace_bytes, void* stream);
+
 /* Replaces GSPlatIntersectOffset::eval_gpu (gsplat_intersect.cpp:643-681):
  * offsets [I, tile_height, tile_width] = lower_bound of (image << tile_bits |
  * tile) over the sorted isect_ids >> 32. */

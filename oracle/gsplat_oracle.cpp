@@ -1098,6 +1098,110 @@ int oracle_isect_encode(const float* means2d, const int32_t* radii, const float*
   return 0;
 }
 
+// Ellipse ("AccuTile") tiles: the use_conics / use_opacities path that the
+// reference rejects (gsplat_intersect.cpp:123-126) and that lives in upstream
+// gsplat's IntersectTile.cu, a dependency absent from the reference tree
+// (Task_Metal.md:95-115, note/gsplat_cuda_source_map.md:359-360). Restated
+// from the published method (Speedy-Splat, Hanson et al., CVPR 2025: SnugBox
+// bounds from the opacity-aware threshold, AccuTile exact tile rows) with the
+// rasterizer's threshold alpha >= 1/255 and its cull slack: the ellipse
+// d^T Q d <= 2 (1.05 ln(255 o) + 1e-4), intersected with the AABB rect, tile
+// row by tile row over the row's pixel-centre slab. Rows are listed
+// row-major, so encode keeps the reference's per-Gaussian order.
+// Parity: pinned against brute force in tests/test_oracle_isect.py (every
+// pixel that passes the rasterizer's float32 alpha test lies in a listed
+// tile; every listed tile meets the slack ellipse, every tile that meets it
+// with margin is listed, by a rectangle-minimum formulation in float64) and
+// by rendering identity (AccuTile lists render the same image as AABB lists).
+// Upstream's own tile ids are unpinned here (no fixture of them exists).
+
+// ln z, z finite > 0, by frexp and the atanh series (same float operations
+// as the device code, so both give the same bits).
+float ellipse_log(float z) {
+  int e = 0;
+  float m = std::frexp(z, &e);
+  if (m < 0.70710678f) {
+    m = m * 2.0f;
+    e = e - 1;
+  }
+  const float s = (m - 1.0f) / (m + 1.0f);
+  const float s2 = s * s;
+  float p = 0.11111111f;
+  p = p * s2 + 0.14285715f;
+  p = p * s2 + 0.2f;
+  p = p * s2 + 0.33333334f;
+  p = p * s2 + 1.0f;
+  return static_cast<float>(e) * 0.69314718f + 2.0f * s * p;
+}
+
+// Column ranges [c0, c1) of the Gaussian's tiles, one per row of its rect.
+struct EllipseRows {
+  Rect r;
+  std::vector<int> c0, c1;  // indexed by ty - r.min_y
+};
+
+EllipseRows ellipse_rows(const float* means2d, const int32_t* radii, const float* conics,
+                         const float* opacities, int64_t g, int ts, int tw, int th) {
+  const float mx = means2d[g * 2], my = means2d[g * 2 + 1];
+  EllipseRows out;
+  out.r = aabb_tile_rect(mx, my, radii[g * 2], radii[g * 2 + 1], ts, tw, th);
+  const Rect& r = out.r;
+  if (r.max_x <= r.min_x || r.max_y <= r.min_y) return out;
+  const int rows = r.max_y - r.min_y;
+  const float o = opacities[g];
+  if (o <= 0.0f) {  // alpha <= 0 everywhere
+    out.c0.assign(rows, r.min_x);
+    out.c1.assign(rows, r.min_x);
+    return out;
+  }
+  // whole rect where the threshold or the conic is unusable
+  out.c0.assign(rows, r.min_x);
+  out.c1.assign(rows, r.max_x);
+  const float a = conics[g * 3], b = conics[g * 3 + 1], c = conics[g * 3 + 2];
+  const float z = 255.0f * o;
+  if (!(z < 3.0e38f) || !(a > 0.0f && c > 0.0f && a < 1.0e30f && c < 1.0e30f) || !(std::fabs(mx) < 1.0e30f) ||
+      !(std::fabs(my) < 1.0e30f))
+    return out;
+  const float det = a * c - b * b;
+  if (!(det > 1.0e-4f * a * c)) return out;
+  const float lim = 1.05f * ellipse_log(z) + 1.0e-4f;
+  if (!(lim >= 0.0f)) {
+    out.c1 = out.c0;
+    return out;
+  }
+  const float R = 2.0f * lim;
+  const float x_ext = std::sqrt(R * c / det);
+  const float y_ext = std::sqrt(R * a / det);
+  const float aR = a * R;
+  const float dy_left = b * x_ext / c;  // leftmost point's dy; rightmost at -dy_left
+  const float fts = static_cast<float>(ts);
+  for (int ty = r.min_y; ty < r.max_y; ++ty) {
+    int& lo_col = out.c0[ty - r.min_y];
+    int& hi_col = out.c1[ty - r.min_y];
+    const float top = static_cast<float>(ty * ts) + 0.5f;  // first pixel centre of the row
+    const float bottom = top + static_cast<float>(ts - 1);
+    const float d0 = std::fmax(top - my, -y_ext);
+    const float d1 = std::fmin(bottom - my, y_ext);
+    if (!(d0 <= d1)) {
+      hi_col = lo_col = r.min_x;
+      continue;
+    }
+    const float dl = std::fmin(std::fmax(dy_left, d0), d1);
+    const float dr = std::fmin(std::fmax(-dy_left, d0), d1);
+    const float half_l = std::sqrt(std::fmax(aR - det * dl * dl, 0.0f));
+    const float half_r = std::sqrt(std::fmax(aR - det * dr * dr, 0.0f));
+    const float xl = mx - (b * dl + half_l) / a;
+    const float xr = mx + (half_r - b * dr) / a;
+    // columns whose pixel centres tx ts + 1/2 .. tx ts + ts - 1/2 meet [xl, xr]
+    const float first = std::floor((xl + 0.5f) / fts);
+    const float end = std::floor((xr - 0.5f) / fts) + 1.0f;
+    const float fmin = static_cast<float>(r.min_x), fmax = static_cast<float>(r.max_x);
+    lo_col = static_cast<int>(std::fmin(std::fmax(first, fmin), fmax));
+    hi_col = static_cast<int>(std::fmin(std::fmax(end, fmin), fmax));
+  }
+  return out;
+}
+
 // argsort + take, gsplat_intersect.cpp:266-286, as a stable sort.
 void oracle_isect_sort(const int64_t* keys, const int32_t* vals, int64_t m, int64_t* keys_out,
                        int32_t* vals_out) {
@@ -1108,6 +1212,43 @@ void oracle_isect_sort(const int64_t* keys, const int32_t* vals, int64_t m, int6
     keys_out[i] = keys[order[i]];
     vals_out[i] = vals[order[i]];
   }
+}
+
+// Ellipse tile counts (the AccuTile count: sum of the row widths).
+void oracle_isect_count_accutile(const float* means2d, const int32_t* radii, const float* conics,
+                                 const float* opacities, int64_t numel, int tile_size, int tile_width,
+                                 int tile_height, int32_t* tiles_per_gauss) {
+  for (int64_t i = 0; i < numel; ++i) {
+    const EllipseRows e = ellipse_rows(means2d, radii, conics, opacities, i, tile_size, tile_width, tile_height);
+    int32_t n = 0;
+    for (size_t k = 0; k < e.c0.size(); ++k) n += std::max(e.c1[k] - e.c0[k], 0);
+    tiles_per_gauss[i] = n;
+  }
+}
+
+// Ellipse tile encode: pair-major, row-major within each pair, ids as the
+// AABB encode's.
+int oracle_isect_encode_accutile(const float* means2d, const int32_t* radii, const float* conics,
+                                 const float* opacities, const float* depths, const int32_t* offsets, int64_t I,
+                                 int64_t numel, int tile_size, int tile_width, int tile_height, int64_t total,
+                                 int64_t* isect_ids, int32_t* flatten_ids) {
+  const int64_t n_per_image = numel / I;
+  const int tile_n_bits = floor_log2_plus_one(tile_width * tile_height);
+  for (int64_t idx = 0; idx < numel; ++idx) {
+    const int image_id = static_cast<int>(idx / n_per_image);
+    const EllipseRows e = ellipse_rows(means2d, radii, conics, opacities, idx, tile_size, tile_width, tile_height);
+    int64_t o = offsets[idx];
+    for (size_t k = 0; k < e.c0.size(); ++k) {
+      const int ty = e.r.min_y + static_cast<int>(k);
+      for (int tx = e.c0[k]; tx < e.c1[k]; ++tx) {
+        if (o < 0 || o >= total) return -1;
+        isect_ids[o] = encode_isect_id(image_id, ty * tile_width + tx, depths[idx], tile_n_bits);
+        flatten_ids[o] = static_cast<int32_t>(idx);
+        ++o;
+      }
+    }
+  }
+  return 0;
 }
 
 // GSPlatIntersectOffset::eval_cpu, gsplat_intersect.cpp:605-641.

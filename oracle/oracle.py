@@ -260,6 +260,37 @@ def isect_encode(means2d, radii, depths, offsets, I, tile_size, tile_width, tile
     return ids, fl
 
 
+def isect_count_accutile(means2d, radii, conics, opacities, tile_size, tile_width, tile_height):
+    """Ellipse (AccuTile) tile counts; the restated method is described in gsplat_oracle.cpp."""
+    m = _c(means2d, np.float32)
+    r = _c(radii, np.int32)
+    co = _c(conics, np.float32)
+    op = _c(opacities, np.float32)
+    out = np.zeros(m.shape[:-1], np.int32)
+    _fn("oracle_isect_count_accutile")(_ptr(m), _ptr(r), _ptr(co), _ptr(op), I64(out.size), tile_size, tile_width,
+                                       tile_height, _ptr(out))
+    return out
+
+
+def isect_encode_accutile(means2d, radii, conics, opacities, depths, offsets, I, tile_size, tile_width,
+                          tile_height, total):
+    m = _c(means2d, np.float32)
+    r = _c(radii, np.int32)
+    co = _c(conics, np.float32)
+    op = _c(opacities, np.float32)
+    d = _c(depths, np.float32)
+    o = _c(offsets, np.int32)
+    ids = np.zeros(total, np.int64)
+    fl = np.zeros(total, np.int32)
+    f = lib().oracle_isect_encode_accutile
+    f.restype = ctypes.c_int
+    rc = f(_ptr(m), _ptr(r), _ptr(co), _ptr(op), _ptr(d), _ptr(o), I64(I), I64(d.size), tile_size, tile_width,
+           tile_height, I64(total), _ptr(ids), _ptr(fl))
+    if rc != 0:
+        raise RuntimeError("intersect_tile_encode tile_offsets write out of bounds.")
+    return ids, fl
+
+
 def isect_sort(isect_ids, flatten_ids):
     k = _c(isect_ids, np.int64)
     v = _c(flatten_ids, np.int32)
@@ -269,11 +300,19 @@ def isect_sort(isect_ids, flatten_ids):
     return ko, vo
 
 
-def isect_tile(means2d, radii, depths, I, tile_size, tile_width, tile_height, sort=True):
-    """gsplat_intersect.cpp:288-307: count -> scan -> total -> encode -> sort."""
-    counts = isect_count(means2d, radii, tile_size, tile_width, tile_height)
-    offsets, total = exclusive_scan(counts)
-    ids, fl = isect_encode(means2d, radii, depths, offsets, I, tile_size, tile_width, tile_height, total)
+def isect_tile(means2d, radii, depths, I, tile_size, tile_width, tile_height, sort=True, conics=None,
+               opacities=None):
+    """gsplat_intersect.cpp:288-307: count -> scan -> total -> encode -> sort; with conics and
+    opacities the ellipse (AccuTile) tiles."""
+    if conics is not None:
+        counts = isect_count_accutile(means2d, radii, conics, opacities, tile_size, tile_width, tile_height)
+        offsets, total = exclusive_scan(counts)
+        ids, fl = isect_encode_accutile(means2d, radii, conics, opacities, depths, offsets, I, tile_size,
+                                        tile_width, tile_height, total)
+    else:
+        counts = isect_count(means2d, radii, tile_size, tile_width, tile_height)
+        offsets, total = exclusive_scan(counts)
+        ids, fl = isect_encode(means2d, radii, depths, offsets, I, tile_size, tile_width, tile_height, total)
     if sort:
         ids, fl = isect_sort(ids, fl)
     return {"tiles_per_gauss": counts, "isect_ids": ids, "flatten_ids": fl}

@@ -53,3 +53,25 @@ def gsplat():
     import gsplat_core
 
     return gsplat_core
+
+
+def projected_scene(rng, I, N, W, H, anisotropy=30.0):
+    """Random screen-space Gaussians as the projection would give them:
+    2D covariances with eps2d = 0.3 added, conics = inverses, radii from the
+    opacity-aware extent (gsplat_projection.metal:299-313)."""
+    s1 = rng.uniform(0.4, 12.0, (I, N))
+    s2 = s1 * rng.uniform(1.0, anisotropy, (I, N)) ** rng.choice([0.0, 1.0], (I, N), p=[0.3, 0.7])
+    th = rng.uniform(0, np.pi, (I, N))
+    c, s = np.cos(th), np.sin(th)
+    cxx = c * c * s1 * s1 + s * s * s2 * s2 + 0.3
+    cyy = s * s * s1 * s1 + c * c * s2 * s2 + 0.3
+    cxy = c * s * (s1 * s1 - s2 * s2)
+    det = cxx * cyy - cxy * cxy
+    conics = np.stack([cyy / det, -cxy / det, cxx / det], -1).astype(np.float32)
+    opac = rng.uniform(0.001, 1.0, (I, N)).astype(np.float32)
+    extend = np.minimum(3.33, np.sqrt(2.0 * np.log(np.maximum(opac * 255.0, 1.0))))
+    extend = np.where(rng.random((I, N)) < 0.3, 3.33, extend)  # some callers pass no opacities to the projection
+    radii = np.stack([np.ceil(extend * np.sqrt(cxx)), np.ceil(extend * np.sqrt(cyy))], -1).astype(np.int32)
+    means = np.stack([rng.uniform(-20, W + 20, (I, N)), rng.uniform(-20, H + 20, (I, N))], -1).astype(np.float32)
+    depths = rng.uniform(0.5, 10.0, (I, N)).astype(np.float32)
+    return means, radii, conics, opac, depths

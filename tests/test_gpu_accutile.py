@@ -1,0 +1,176 @@
+"""GPU parity for the ellipse ("AccuTile") tile intersection: counts, keys,
+sorted order and tile offsets bit-exact with the oracle, in both encode
+orders and through the C ABI; rendering through the AccuTile lists equals
+rendering through the AABB lists (images bit-exact, gradients to 1e-4: the
+per-Gaussian sums run over fewer tiles, in another order)."""
+import ctypes
+import os
+
+import numpy as np
+import pytest
+
+from _helpers import assert_close_rel, dev, gsplat, host, projected_scene
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "gsplat-mlx_amd", "gsplat_core", "libgsplat_hip.so")
+TS = 16
+
+
+def _inputs(means, radii, depths, conics=None, opac=None):
+    d = {"means2d": dev(means), "radii": dev(radii), "depths": dev(depths)}
+    if conics is not None:
+        d["conics"] = dev(conics)
+        d["opacities"] = dev(opac)
+    return d
+
+
+def _with_edge_cases(rng, means, radii, conics, opac):
+    """NaN / zero / negative / tiny / huge opacities, a non-positive-definite
+    and an ill-conditioned conic, zero radii."""
+    conics = conics.copy()
+    opac = opac.copy()
+    radii = radii.copy()
+    n = opac.shape[-1]
+    pick = rng.choice(n, 8, replace=False)
+    opac[..., pick[0]] = np.nan
+    opac[..., pick[1]] = 0.0
+    opac[..., pick[2]] = -0.5
+    opac[..., pick[3]] = 0.003
+    opac[..., pick[4]] = 40.0
+    conics[..., pick[5], :] = [1.0, 2.0, 1.0]
+    conics[..., pick[6], :] = [1.0, 0.99999, 1.0]
+    radii[..., pick[7], :] = 0
+    return means, radii, conics, opac
+
+
+@pytest.mark.parametrize("I,N,W,H,sort", [(1, 3000, 331, 217, True), (1, 3000, 331, 217, False),
+                                          (3, 2000, 200, 150, True), (2, 40000, 1297, 840, True)])
+def test_bit_exact_vs_oracle(oracle, I, N, W, H, sort):
+    rng = np.random.default_rng(I * 1000 + N)
+    means, radii, conics, opac, depths = projected_scene(rng, I, N, W, H)
+    means, radii, conics, opac = _with_edge_cases(rng, means, radii, conics, opac)
+    tw, th = (W + TS - 1) // TS, (H + TS - 1) // TS
+    print(f"accutile I={I} N={N} {W}x{H} sort={sort}", flush=True)
+    g = gsplat()
+    out = g._gsplat_core.intersect_tile_forward(_inputs(means, radii, depths, conics, opac), I, TS, tw, th, sort=sort)
+    ref = oracle.isect_tile(means, radii, depths, I, TS, tw, th, sort=sort, conics=conics, opacities=opac)
+    np.testing.assert_array_equal(host(out["tiles_per_gauss"]), ref["tiles_per_gauss"])
+    np.testing.assert_array_equal(host(out["isect_ids"]), ref["isect_ids"])
+    np.testing.assert_array_equal(host(out["flatten_ids"]), ref["flatten_ids"])
+    if sort:
+        offs = host(g._gsplat_core.intersect_offset_forward(out["isect_ids"], I, tw, th))
+        np.testing.assert_array_equal(offs, oracle.isect_offset(ref["isect_ids"], I, tw, th))
+    aabb = g._gsplat_core.intersect_tile_forward(_inputs(means, radii, depths), I, TS, tw, th, sort=sort)
+    assert out["isect_ids"].numel() < 0.85 * aabb["isect_ids"].numel()
+
+
+def test_empty_and_all_culled():
+    g = gsplat()
+    m = np.array([[[24.0, 24.0], [40.0, 8.0]]], np.float32)
+    r = np.array([[[10, 10], [6, 6]]], np.int32)
+    d = np.array([[1.0, 2.0]], np.float32)
+    co = np.array([[[1 / 9, 0.0, 1 / 9]] * 2], np.float32)
+    op = np.array([[0.0, 0.002]], np.float32)  # no pixel can reach alpha 1/255
+    for sort in (True, False):
+        out = g._gsplat_core.intersect_tile_forward(_inputs(m, r, d, co, op), 1, TS, 4, 4, sort=sort)
+        assert host(out["tiles_per_gauss"]).tolist() == [[0, 0]]
+        assert out["isect_ids"].numel() == 0 and out["flatten_ids"].numel() == 0
+    # known answer: the circle drops the four corners of its 3x3 rect
+    out = g._gsplat_core.intersect_tile_forward(_inputs(m[:, :1], r[:, :1], d[:, :1], co[:, :1],
+                                                        np.ones((1, 1), np.float32)), 1, TS, 4, 4)
+    assert ((host(out["isect_ids"]) >> 32) & 0xFF).tolist() == [1, 4, 5, 6, 9]
+    with pytest.raises(RuntimeError, match="needs both conics and opacities"):
+        g._gsplat_core.intersect_tile_forward({"means2d": dev(m), "radii": dev(r), "depths": dev(d),
+                                               "conics": dev(co)}, 1, TS, 4, 4)
+    with pytest.raises(RuntimeError, match="conics"):
+        g._gsplat_core.intersect_tile_forward(_inputs(m, r, d, co[..., :2].copy(), op), 1, TS, 4, 4)
+
+
+def _render(g, means, conics, colors, opac, it, I, W, H, v_rc):
+    import torch
+
+    tw, th = (W + TS - 1) // TS, (H + TS - 1) // TS
+    offs = g._gsplat_core.intersect_offset_forward(it["isect_ids"], I, tw, th)
+    inp = {"means2d": dev(means), "conics": dev(conics), "colors": dev(colors), "opacities": dev(opac),
+           "tile_offsets": offs, "flatten_ids": it["flatten_ids"]}
+    f = g._gsplat_core.rasterize_to_pixels_3dgs_forward(inp, W, H, TS)
+    b = g._gsplat_core.rasterize_to_pixels_3dgs_backward(
+        inp, f, {"v_render_colors": dev(v_rc), "v_render_alphas": torch.ones_like(f["render_alphas"])}, W, H, TS,
+        False)
+    return f, b
+
+
+def test_rendering_identity():
+    rng = np.random.default_rng(7)
+    I, N, W, H, C = 1, 30000, 640, 480, 3
+    means, radii, conics, opac, depths = projected_scene(rng, I, N, W, H)
+    colors = rng.uniform(0, 1, (I, N, C)).astype(np.float32)
+    v_rc = rng.normal(size=(I, H, W, C)).astype(np.float32)
+    g = gsplat()
+    tw, th = (W + TS - 1) // TS, (H + TS - 1) // TS
+    ia = g._gsplat_core.intersect_tile_forward(_inputs(means, radii, depths), I, TS, tw, th)
+    ic = g._gsplat_core.intersect_tile_forward(_inputs(means, radii, depths, conics, opac), I, TS, tw, th)
+    print(f"AABB {ia['isect_ids'].numel()} entries, AccuTile {ic['isect_ids'].numel()}", flush=True)
+    fa, ba = _render(g, means, conics, colors, opac, ia, I, W, H, v_rc)
+    fc, bc = _render(g, means, conics, colors, opac, ic, I, W, H, v_rc)
+    np.testing.assert_array_equal(host(fa["render_colors"]), host(fc["render_colors"]))
+    np.testing.assert_array_equal(host(fa["render_alphas"]), host(fc["render_alphas"]))
+    hit = host(fa["render_alphas"])[..., 0] > 0
+    la, lc = host(fa["last_ids"])[hit], host(fc["last_ids"])[hit]
+    np.testing.assert_array_equal(host(ia["flatten_ids"])[la], host(ic["flatten_ids"])[lc])
+    for k in ("v_means2d", "v_conics", "v_colors", "v_opacities"):
+        assert_close_rel(host(bc[k]), host(ba[k]), 1e-4, k)  # summation order differs
+
+
+def _lib():
+    lib = ctypes.CDLL(LIB)
+    vp, i64, i32, sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t
+    lib.gsplat_hip_last_error.restype = ctypes.c_char_p
+    lib.gsplat_hip_isect_count_scan_workspace_size.restype = sz
+    lib.gsplat_hip_isect_count_scan_workspace_size.argtypes = [i64]
+    lib.gsplat_hip_isect_count_scan_accutile.argtypes = [vp, vp, vp, vp, i64, i32, i32, i32, vp, vp, vp, vp, sz, vp]
+    lib.gsplat_hip_isect_encode_accutile.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, i64, vp, vp,
+                                                     vp]
+    return lib
+
+
+def test_c_abi_count_encode(oracle):
+    import torch
+
+    rng = np.random.default_rng(3)
+    I, N, W, H = 2, 5000, 400, 300
+    means, radii, conics, opac, depths = projected_scene(rng, I, N, W, H)
+    tw, th = (W + TS - 1) // TS, (H + TS - 1) // TS
+    lib = _lib()
+    m, r, co, op, d = dev(means), dev(radii), dev(conics), dev(opac), dev(depths)
+    n = I * N
+    counts = torch.empty(n, dtype=torch.int32, device="cuda")
+    offs = torch.empty(n, dtype=torch.int32, device="cuda")
+    total = torch.empty(1, dtype=torch.int64, device="cuda")
+    ws = torch.empty(lib.gsplat_hip_isect_count_scan_workspace_size(n), dtype=torch.uint8, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.gsplat_hip_isect_count_scan_accutile(m.data_ptr(), r.data_ptr(), co.data_ptr(), op.data_ptr(), n, TS,
+                                                  tw, th, counts.data_ptr(), offs.data_ptr(), total.data_ptr(),
+                                                  ws.data_ptr(), ws.numel(), stream)
+    assert rc == 0, lib.gsplat_hip_last_error()
+    ref = oracle.isect_count_accutile(means, radii, conics, opac, TS, tw, th).reshape(-1)
+    np.testing.assert_array_equal(host(counts), ref)
+    ref_offs, ref_total = oracle.exclusive_scan(ref)
+    np.testing.assert_array_equal(host(offs), ref_offs)
+    assert int(total.item()) == ref_total
+    ids = torch.empty(ref_total, dtype=torch.int64, device="cuda")
+    fl = torch.empty(ref_total, dtype=torch.int32, device="cuda")
+    rc = lib.gsplat_hip_isect_encode_accutile(m.data_ptr(), r.data_ptr(), co.data_ptr(), op.data_ptr(), d.data_ptr(),
+                                              offs.data_ptr(), I, n, TS, tw, th, ref_total, ids.data_ptr(),
+                                              fl.data_ptr(), stream)
+    assert rc == 0, lib.gsplat_hip_last_error()
+    rid, rfl = oracle.isect_encode_accutile(means, radii, conics, opac, depths, ref_offs, I, TS, tw, th, ref_total)
+    np.testing.assert_array_equal(host(ids), rid)
+    np.testing.assert_array_equal(host(fl), rfl)
+    # null opacities: an error, not a fault
+    rc = lib.gsplat_hip_isect_encode_accutile(m.data_ptr(), r.data_ptr(), co.data_ptr(), None, d.data_ptr(),
+                                              offs.data_ptr(), I, n, TS, tw, th, ref_total, ids.data_ptr(),
+                                              fl.data_ptr(), stream)
+    assert rc != 0 and b"null" in lib.gsplat_hip_last_error()
