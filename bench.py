@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--workload", default="sh3_1m",
                     choices=["sh3_1m", "image_fit", "random_forward", "multiview_3m", "heavy_6m"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-accutile", action="store_true", help="skip the ellipse tile list variant")
     ap.add_argument("--cpu-band-rows", type=int, default=0,
                     help="tile rows of the CPU rasterize sample (0: the whole image)")
     ap.add_argument("--cpu-repeats", type=int, default=3, help="CPU baseline runs (median per stage)")
@@ -134,18 +135,18 @@ def main():
     forward_only = target is None
     seed = torch.ones((), device=dev)
 
-    def step():
+    def step(accutile=False):
         for p in params + [viewspace]:
             p.grad = None
         if sh:
             out = R.render_sh_model(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks,
                                     W, H, ts, scene.sh_degree, viewspace_points=viewspace,
-                                    background=scene.background, far_plane=scene.far_plane)
+                                    background=scene.background, far_plane=scene.far_plane, accutile=accutile)
         else:
             out = R.render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, W, H, ts,
                                      background=scene.background,
                                      opacities_in_projection=scene.opacities_in_projection,
-                                     far_plane=scene.far_plane)
+                                     far_plane=scene.far_plane, accutile=accutile)
         if not forward_only:
             loss = R.l1_loss(out["render_colors"], target)
             loss.backward(seed)  # d loss / d loss = 1, allocated once
@@ -270,6 +271,31 @@ def main():
                         "avg_ms": round(avg_ms, 4)}
     log(f"[bench] N={N} M={M} E_fwd(no termination)={e_fwd_max} E_bwd={e_bwd} dominant={dom} {avg_ms:.4f} ms")
 
+    # The same step with ellipse (AccuTile) tile lists: the same images from
+    # fewer intersections. Reported beside the headline (which keeps the
+    # reference's AABB lists), not as it.
+    accutile = None
+    if not args.no_accutile:
+        for _ in range(args.warmup):
+            step(accutile=True)
+        torch.cuda.synchronize()
+        ta = time.perf_counter()
+        for _ in range(args.steps):
+            out_a = step(accutile=True)
+        torch.cuda.synchronize()
+        ms_a = 1000.0 * (time.perf_counter() - ta) / args.steps
+        prof.reset()
+        prof.enable(True)
+        for _ in range(args.steps):
+            out_a = step(accutile=True)
+        torch.cuda.synchronize()
+        prof.enable(False)
+        kern_a = {k: round(ms / args.steps * 1000, 1) for k, (c, ms) in sorted(prof.report().items())}
+        M_a = int(out_a["isect_ids"].numel())
+        accutile = {"ms_per_step": round(ms_a, 4), "value": round(mpix / (ms_a * 1e-3), 2), "unit": "Mpix/s",
+                    "n_isects": M_a, "kernels_us_per_step": kern_a}
+        log(f"[bench] accutile: {ms_a:.3f} ms/step, M={M_a} ({M_a / max(M, 1):.3f} of AABB)")
+
     cpu = None
     if not args.no_cpu_baseline and n_img == 1:
         cpu = cpu_baseline(scene, args.cpu_band_rows, args.cpu_repeats, mpix)
@@ -295,6 +321,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "stages": stages,
+        "accutile": accutile,
         "kernels_us_per_step": {k: round(v[1] * 1000, 1) for k, v in sorted(per_step.items())},
     }
     print(json.dumps(line), flush=True)

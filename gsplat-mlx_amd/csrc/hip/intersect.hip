@@ -130,6 +130,14 @@ __device__ __forceinline__ EllipseTiles ellipse_tiles(const float* __restrict__ 
   e.aR = a * R;
   e.ye = sqrtf(R * a / det);
   e.dyl = b * xe / c;  // dy of the leftmost point; the rightmost is at -dyl
+  // Rows outside [my - ye, my + ye] (with a row of margin either side) are
+  // empty: drop them from the rect so that no loop visits them.
+  const float fts = static_cast<float>(ts);
+  const float ylo = floorf((e.my - e.ye) / fts) - 1.0f;
+  const float yhi = floorf((e.my + e.ye) / fts) + 2.0f;
+  const float fy0 = static_cast<float>(e.r.min_y), fy1 = static_cast<float>(e.r.max_y);
+  e.r.min_y = static_cast<int>(fminf(fmaxf(ylo, fy0), fy1));
+  e.r.max_y = static_cast<int>(fminf(fmaxf(yhi, fy0), fy1));
   return e;
 }
 
@@ -154,24 +162,17 @@ __device__ __forceinline__ void ellipse_row(const EllipseTiles& e, int ty, int t
   const float qr = sqrtf(fmaxf(e.aR - e.det * dr * dr, 0.0f));
   const float xl = e.mx - (e.b * dl + ql) / e.a;
   const float xr = e.mx + (qr - e.b * dr) / e.a;
+  // v / ts; for a power-of-two ts the product with its reciprocal is the
+  // same correctly rounded value, without the division sequence
   const float fts = static_cast<float>(ts);
-  const float lo = floorf((xl + 0.5f) / fts);
-  const float hi = floorf((xr - 0.5f) / fts) + 1.0f;
+  const bool pow2 = (ts & (ts - 1)) == 0;
+  const float inv = 1.0f / fts;
+  const float ul = xl + 0.5f, ur = xr - 0.5f;
+  const float lo = floorf(pow2 ? ul * inv : ul / fts);
+  const float hi = floorf(pow2 ? ur * inv : ur / fts) + 1.0f;
   const float fmin = static_cast<float>(e.r.min_x), fmax = static_cast<float>(e.r.max_x);
   *c0 = static_cast<int>(fminf(fmaxf(lo, fmin), fmax));
   *c1 = static_cast<int>(fminf(fmaxf(hi, fmin), fmax));
-}
-
-__device__ __forceinline__ int32_t ellipse_count(const EllipseTiles& e, int ts) {
-  if (e.mode == 0) return 0;
-  if (e.mode == 1) return (e.r.max_y - e.r.min_y) * (e.r.max_x - e.r.min_x);
-  int32_t n = 0;
-  for (int ty = e.r.min_y; ty < e.r.max_y; ++ty) {
-    int c0, c1;
-    ellipse_row(e, ty, ts, &c0, &c1);
-    n += max(c1 - c0, 0);
-  }
-  return n;
 }
 
 // Tile of the Gaussian's k-th entry (row-major); false when k is past its
@@ -192,13 +193,81 @@ __device__ __forceinline__ bool ellipse_locate(const EllipseTiles& e, int ts, in
   return false;
 }
 
-// Count per Gaussian fused with the block-local exclusive scan; with conics
-// and opacities (ELL) the ellipse count, else the AABB rect's.
-template <bool ELL>
+// Ellipse counts fused with the block-local exclusive scan. The row loops
+// are balanced over the block: in each of kScanItems rounds the block's 256
+// Gaussians put their geometry in LDS, their row counts are scanned, and the
+// threads take the (Gaussian, row) pairs in turn, adding each row's width to
+// its Gaussian's count with an LDS atomic. A wave then waits for the block's
+// mean row count, not for its largest Gaussian.
+__global__ void __launch_bounds__(kScanBlock) count_scan_ellipse_kernel(const float* __restrict__ means2d,
+                                                                        const int32_t* __restrict__ radii,
+                                                                        const float* __restrict__ conics,
+                                                                        const float* __restrict__ opacities,
+                                                                        int64_t n, int ts, int tw, int th,
+                                                                        int32_t* __restrict__ counts,
+                                                                        int32_t* __restrict__ offsets,
+                                                                        int64_t* __restrict__ block_sums) {
+  __shared__ EllipseTiles s_e[kScanBlock];
+  __shared__ int32_t s_pre[kScanBlock];  // exclusive prefix of the row counts
+  __shared__ int32_t s_cnt[kScanTile];
+  const int t = threadIdx.x;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * kScanTile;
+  for (int k = 0; k < kScanItems; ++k) {
+    const int li = k * kScanBlock + t;  // coalesced: consecutive threads, consecutive Gaussians
+    const int64_t i = base + li;
+    EllipseTiles e = {};
+    int rows = 0, direct = 0;
+    if (i < n) {
+      e = ellipse_tiles(means2d, radii, conics, opacities, i, ts, tw, th);
+      if (e.mode == 1) direct = (e.r.max_y - e.r.min_y) * (e.r.max_x - e.r.min_x);
+      if (e.mode == 2) rows = max(e.r.max_y - e.r.min_y, 0);
+    }
+    s_e[t] = e;
+    s_cnt[li] = direct;
+    int64_t total_rows;
+    const int pre = static_cast<int>(block_exclusive_scan(rows, &total_rows));  // syncs
+    s_pre[t] = pre;
+    __syncthreads();
+    for (int u = t; u < static_cast<int>(total_rows); u += kScanBlock) {
+      int lo = 0, hi = kScanBlock - 1;  // last owner o with s_pre[o] <= u
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_pre[mid] <= u)
+          lo = mid;
+        else
+          hi = mid - 1;
+      }
+      const EllipseTiles& eo = s_e[lo];
+      int c0, c1;
+      ellipse_row(eo, eo.r.min_y + (u - s_pre[lo]), ts, &c0, &c1);
+      if (c1 > c0) atomicAdd(&s_cnt[k * kScanBlock + lo], c1 - c0);
+    }
+    __syncthreads();
+  }
+  const int64_t tb = base + static_cast<int64_t>(t) * kScanItems;
+  int32_t v[kScanItems];
+  int64_t sum = 0;
+#pragma unroll
+  for (int k = 0; k < kScanItems; ++k) {
+    v[k] = tb + k < n ? s_cnt[t * kScanItems + k] : 0;
+    if (tb + k < n) counts[tb + k] = v[k];
+    sum += v[k];
+  }
+  int64_t total;
+  int64_t run = block_exclusive_scan(sum, &total);
+  if (offsets) {
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+      if (tb + k < n) offsets[tb + k] = static_cast<int32_t>(run);
+      run += v[k];
+    }
+  }
+  if (t == 0) block_sums[blockIdx.x] = total;
+}
+
+// Count per Gaussian fused with the block-local exclusive scan.
 __global__ void __launch_bounds__(kScanBlock) count_scan_local_kernel(const float* __restrict__ means2d,
                                                                       const int32_t* __restrict__ radii,
-                                                                      const float* __restrict__ conics,
-                                                                      const float* __restrict__ opacities,
                                                                       int64_t n, int ts, int tw, int th,
                                                                       int32_t* __restrict__ counts,
                                                                       int32_t* __restrict__ offsets,
@@ -211,13 +280,8 @@ __global__ void __launch_bounds__(kScanBlock) count_scan_local_kernel(const floa
     const int64_t i = base + k;
     int32_t c = 0;
     if (i < n) {
-      if constexpr (ELL) {
-        c = ellipse_count(ellipse_tiles(means2d, radii, conics, opacities, i, ts, tw, th), ts);
-      } else {
-        const TileRect r =
-            aabb_tile_rect(means2d[i * 2], means2d[i * 2 + 1], radii[i * 2], radii[i * 2 + 1], ts, tw, th);
-        c = (r.max_y - r.min_y) * (r.max_x - r.min_x);
-      }
+      const TileRect r = aabb_tile_rect(means2d[i * 2], means2d[i * 2 + 1], radii[i * 2], radii[i * 2 + 1], ts, tw, th);
+      c = (r.max_y - r.min_y) * (r.max_x - r.min_x);
       counts[i] = c;
     }
     v[k] = c;
@@ -521,21 +585,25 @@ int check_tile_bits(int64_t I, int32_t tile_width, int32_t tile_height, int* til
 // gets the full 64-bit id with the depth bits. Each thread locates its first
 // slot's tile by walking the Gaussian's rows and steps along the row for the
 // next ones.
+constexpr int kEllItems = 512;                     // merged items per block
+constexpr int kEllOuts = kEllItems / kEncodeBlock;  // slots per thread (at most)
+
 __global__ void __launch_bounds__(kEncodeBlock) encode_ellipse_kernel(
     const float* __restrict__ means2d, const int32_t* __restrict__ radii, const float* __restrict__ conics,
     const float* __restrict__ opacities, const float* __restrict__ depths, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, int64_t numel, int64_t n_per_image, int ts, int tw, int th, int tile_bits,
     int64_t n_isects, uint32_t* __restrict__ keys32, int64_t* __restrict__ ids64, int32_t* __restrict__ vals) {
-  constexpr int kRanks = kMergeItems + 1;
+  constexpr int kRanks = kEllItems + 1;
   __shared__ int32_t s_off[kRanks];
   __shared__ int32_t s_g[kRanks];
+  __shared__ EllipseTiles s_e[kRanks];  // each rank's geometry, computed once
   __shared__ int64_t s_split[2];
   const int t = threadIdx.x;
   const int lane = t % kWave;
   const int wave = t / kWave;
   const int64_t total = numel + n_isects;
-  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kMergeItems;
-  const int64_t d1 = min<int64_t>(d0 + kMergeItems, total);
+  const int64_t d0 = static_cast<int64_t>(blockIdx.x) * kEllItems;
+  const int64_t d1 = min<int64_t>(d0 + kEllItems, total);
   if (wave < 2) {
     const int64_t r = merge_split(offsets, numel, n_isects, wave == 0 ? d0 : d1, lane);
     if (lane == 0) s_split[wave] = r;
@@ -546,12 +614,16 @@ __global__ void __launch_bounds__(kEncodeBlock) encode_ellipse_kernel(
   const int64_t rs = r0 > 0 ? r0 - 1 : 0;
   const int nr = static_cast<int>(min<int64_t>(max<int64_t>(r1 - rs, 0), kRanks));
   for (int i = t; i < nr; i += kEncodeBlock) {
+    const int32_t g = perm ? perm[rs + i] : static_cast<int32_t>(rs + i);
     s_off[i] = offsets[rs + i];
-    s_g[i] = perm ? perm[rs + i] : static_cast<int32_t>(rs + i);
+    s_g[i] = g;
+    EllipseTiles e = {};
+    if (g >= 0 && g < numel) e = ellipse_tiles(means2d, radii, conics, opacities, g, ts, tw, th);
+    s_e[i] = e;
   }
   __syncthreads();
   if (nr == 0) return;
-  const int64_t jb = j0 + static_cast<int64_t>(t) * kMergeOuts;
+  const int64_t jb = j0 + static_cast<int64_t>(t) * kEllOuts;
   if (jb >= min<int64_t>(j1, n_isects)) return;
   int lo = 0, hi = nr - 1;  // last i with s_off[i] <= jb
   while (lo < hi) {
@@ -565,7 +637,7 @@ __global__ void __launch_bounds__(kEncodeBlock) encode_ellipse_kernel(
   EllipseTiles e = {};
   bool valid = false, ok = false;
   int ty = 0, tx = 0, row_end = 0;
-  for (int q = 0; q < kMergeOuts; ++q) {
+  for (int q = 0; q < kEllOuts; ++q) {
     const int64_t j = jb + q;
     if (j >= j1 || j >= n_isects) break;
     while (i + 1 < nr && s_off[i + 1] <= j) ++i;
@@ -575,7 +647,7 @@ __global__ void __launch_bounds__(kEncodeBlock) encode_ellipse_kernel(
       valid = g >= 0 && g < numel;
       ok = false;
       if (valid) {
-        e = ellipse_tiles(means2d, radii, conics, opacities, g, ts, tw, th);
+        e = s_e[i];
         ok = ellipse_locate(e, ts, static_cast<int>(j - s_off[i]), &ty, &tx, &row_end);
       }
     } else if (ok && ++tx >= row_end) {
@@ -592,7 +664,7 @@ __global__ void __launch_bounds__(kEncodeBlock) encode_ellipse_kernel(
       }
     }
     // offsets that disagree with the counts still get an in-range tile
-    const int tile = !valid ? 0 : ok ? ty * tw + tx : e.r.min_y * tw + e.r.min_x;
+    const int tile = valid && ok ? ty * tw + tx : 0;
     const uint32_t image = valid ? static_cast<uint32_t>(g / n_per_image) : 0u;
     const uint32_t key = (image << tile_bits) | static_cast<uint32_t>(tile);
     if (keys32) {
@@ -660,8 +732,13 @@ static int count_scan_impl(const float* means2d, const int32_t* radii, const flo
   int64_t* sums = static_cast<int64_t*>(workspace);
   {
     KernelTimer timer("isect_count_scan", s);
-    count_scan_local_kernel<ELL><<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(
-        means2d, radii, conics, opacities, numel, tile_size, tile_width, tile_height, tiles_per_gauss, offsets, sums);
+    if (ELL)
+      count_scan_ellipse_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(
+          means2d, radii, conics, opacities, numel, tile_size, tile_width, tile_height, tiles_per_gauss, offsets,
+          sums);
+    else
+      count_scan_local_kernel<<<static_cast<unsigned>(nb), kScanBlock, 0, s>>>(
+          means2d, radii, numel, tile_size, tile_width, tile_height, tiles_per_gauss, offsets, sums);
   }
   int rc = check_launch("intersect_tile_count");
   if (rc) return rc;
@@ -838,7 +915,7 @@ extern "C" int gsplat_hip_isect_encode_accutile(const float* means2d, const int3
   hipStream_t s = as_stream(stream);
   {
     KernelTimer timer("isect_encode", s);
-    const int64_t nb = (numel + n_isects + kMergeItems - 1) / kMergeItems;
+    const int64_t nb = (numel + n_isects + kEllItems - 1) / kEllItems;
     encode_ellipse_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
         means2d, radii, conics, opacities, depths, nullptr, offsets, numel, numel / I, tile_size, tile_width,
         tile_height, tile_bits, n_isects, nullptr, isect_ids, flatten_ids);
@@ -875,7 +952,7 @@ extern "C" int gsplat_hip_isect_encode_sorted_accutile(const float* means2d, con
   hipStream_t s = as_stream(stream);
   {
     KernelTimer timer("isect_encode", s);
-    const int64_t nb = (numel + n_isects + kMergeItems - 1) / kMergeItems;
+    const int64_t nb = (numel + n_isects + kEllItems - 1) / kEllItems;
     encode_ellipse_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
         means2d, radii, conics, opacities, depths, perm, offsets, numel, numel / I, tile_size, tile_width,
         tile_height, tile_bits, n_isects, l.tkeys, nullptr, l.tvals);

@@ -77,11 +77,15 @@ def tile_grid(width: int, height: int, tile_size: int):
     return (width + tile_size - 1) // tile_size, (height + tile_size - 1) // tile_size
 
 
-def _intersect(proj, width, height, tile_size, images=1):
+def _intersect(proj, width, height, tile_size, images=1, opacities=None):
+    """Sorted tile intersection; with the rasterizer's opacities, the ellipse
+    (AccuTile) tiles, which render the same images from fewer entries."""
     tw, th = tile_grid(width, height, tile_size)
-    isect = _C.intersect_tile_forward(
-        {"means2d": proj["means2d"].detach(), "radii": proj["radii"], "depths": proj["depths"].detach()},
-        images, tile_size, tw, th, True, False)
+    inputs = {"means2d": proj["means2d"].detach(), "radii": proj["radii"], "depths": proj["depths"].detach()}
+    if opacities is not None:
+        inputs["conics"] = proj["conics"].detach()
+        inputs["opacities"] = opacities.detach()
+    isect = _C.intersect_tile_forward(inputs, images, tile_size, tw, th, True, False)
     offsets = _C.intersect_offset_forward(isect["isect_ids"], images, tw, th)
     return isect, offsets
 
@@ -97,19 +101,19 @@ def _per_image(opacities, background, n_images, device):
 
 def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks, width,
                     height, tile_size, sh_degree, viewspace_points=None, background=(0.025, 0.025, 0.025),
-                    far_plane=100.0):
+                    far_plane=100.0, accutile=False):
     """C cameras (viewmats [1, C, 4, 4]) rendered as C images of the same
     Gaussians; returns the render dict ([C, H, W, ...] images) plus radii,
-    tiles_per_gauss and flatten_ids, like the reference."""
+    tiles_per_gauss and flatten_ids, like the reference. accutile: ellipse
+    tile lists (same images, fewer intersections)."""
     C = viewmats.shape[1]
     # the parameter activations run inside the projection kernels
     proj = activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks, width, height,
                                 viewspace_points=viewspace_points, eps2d=0.3, near_plane=0.01,
                                 far_plane=far_plane, radius_clip=0.0, calc_compensations=False, camera_model=0)
-    opac = proj["opacities"]
-    isect, offsets = _intersect(proj, width, height, tile_size, C)
+    opac_img, bg = _per_image(proj["opacities"], background, C, means.device)
+    isect, offsets = _intersect(proj, width, height, tile_size, C, opac_img if accutile else None)
     colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)
-    opac_img, bg = _per_image(opac, background, C, means.device)
     render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, opac_img,
                                       offsets, isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
     return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],
@@ -117,15 +121,15 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
 
 
 def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, width, height, tile_size,
-                     background=(0.0, 0.0, 0.0), opacities_in_projection=False, far_plane=1e10):
-    """RGB colours per Gaussian; C cameras (viewmats [1, C, 4, 4]) as C images."""
+                     background=(0.0, 0.0, 0.0), opacities_in_projection=False, far_plane=1e10, accutile=False):
+    """RGB colours per Gaussian; C cameras (viewmats [1, C, 4, 4]) as C images.
+    accutile: ellipse tile lists (same images, fewer intersections)."""
     C = viewmats.shape[1]
     proj = activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks, width, height, eps2d=0.3,
                                 near_plane=0.01, far_plane=far_plane,
                                 opacities_in_projection=opacities_in_projection)
-    opac = proj["opacities"]
-    isect, offsets = _intersect(proj, width, height, tile_size, C)
-    opac_img, bg = _per_image(opac, background, C, means.device)
+    opac_img, bg = _per_image(proj["opacities"], background, C, means.device)
+    isect, offsets = _intersect(proj, width, height, tile_size, C, opac_img if accutile else None)
     colors_img = colors[:, None] if C == 1 else colors[:, None].expand(-1, C, -1, -1).contiguous()
     render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors_img, opac_img, offsets,
                                       isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
