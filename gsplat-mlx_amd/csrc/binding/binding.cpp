@@ -91,6 +91,72 @@ py::dict projection_ewa_3dgs_fused_backward(const TensorMap& inputs, const Tenso
   return r;
 }
 
+// Packed layout (the reference's intended projection_ewa_3dgs_packed_forward,
+// note/gsplat_cuda_source_map.md:273-315; upstream gsplat's
+// fully_fused_projection(packed=True)).
+py::dict projection_ewa_3dgs_packed_forward(const TensorMap& inputs, int image_width, int image_height, float eps2d,
+                                            float near_plane, float far_plane, float radius_clip,
+                                            bool calc_compensations, int camera_model) {
+  gsplat_core::ProjectionEWA3DGSFusedInput in;
+  in.means = require_key(inputs, "means");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.covars = get_or_empty(inputs, "covars");
+  in.quats = get_or_empty(inputs, "quats");
+  in.scales = get_or_empty(inputs, "scales");
+  in.opacities = get_or_empty(inputs, "opacities");
+  in.params = {image_width, image_height, eps2d, near_plane, far_plane, radius_clip, calc_compensations,
+               camera_model, in.covars.numel() != 0, in.opacities.numel() != 0};
+  auto out = gsplat_core::gsplat_projection_ewa_3dgs_packed(in);
+  py::dict r;
+  r["batch_ids"] = out[gsplat_core::kPackedBatchIds];
+  r["camera_ids"] = out[gsplat_core::kPackedCameraIds];
+  r["gaussian_ids"] = out[gsplat_core::kPackedGaussianIds];
+  r["indptr"] = out[gsplat_core::kPackedIndptr];
+  r["radii"] = out[gsplat_core::kPackedRadii];
+  r["means2d"] = out[gsplat_core::kPackedMeans2D];
+  r["depths"] = out[gsplat_core::kPackedDepths];
+  r["conics"] = out[gsplat_core::kPackedConics];
+  r["compensations"] = out[gsplat_core::kPackedCompensations];
+  return r;
+}
+
+py::dict projection_ewa_3dgs_packed_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
+                                             const TensorMap& cotangents, int image_width, int image_height,
+                                             float eps2d, int camera_model, bool viewmats_requires_grad) {
+  gsplat_core::ProjectionEWA3DGSPackedBackwardInput in;
+  in.means = require_key(inputs, "means");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.covars = get_or_empty(inputs, "covars");
+  in.quats = get_or_empty(inputs, "quats");
+  in.scales = get_or_empty(inputs, "scales");
+  in.batch_ids = get_or_empty(forward_outputs, "batch_ids");
+  in.camera_ids = require_key(forward_outputs, "camera_ids");
+  in.gaussian_ids = require_key(forward_outputs, "gaussian_ids");
+  in.conics = require_key(forward_outputs, "conics");
+  in.compensations = get_or_empty(forward_outputs, "compensations");
+  in.v_means2d = require_key(cotangents, "v_means2d");
+  in.v_depths = get_or_empty(cotangents, "v_depths");  // absent = zeros
+  in.v_conics = require_key(cotangents, "v_conics");
+  in.v_compensations = get_or_empty(cotangents, "v_compensations");
+  const bool use_covars = in.covars.numel() != 0;
+  in.params = {image_width, image_height, eps2d, -1.0e20f, 1.0e20f, 0.0f, in.compensations.numel() != 0,
+               camera_model, use_covars, false};
+  in.viewmats_requires_grad = viewmats_requires_grad;
+  auto out = gsplat_core::gsplat_projection_ewa_3dgs_packed_backward(in);
+  py::dict r;
+  r["v_means"] = out[gsplat_core::kProjectionVMeans];
+  if (use_covars) {
+    r["v_covars"] = out[gsplat_core::kProjectionVCovars];
+  } else {
+    r["v_quats"] = out[gsplat_core::kProjectionVQuats];
+    r["v_scales"] = out[gsplat_core::kProjectionVScales];
+  }
+  if (viewmats_requires_grad) r["v_viewmats"] = out[gsplat_core::kProjectionVViewmats];
+  return r;
+}
+
 py::dict intersect_tile_forward(const TensorMap& inputs, int I, int tile_size, int tile_width, int tile_height,
                                 bool sort, bool segmented) {
   gsplat_core::IntersectTileInput in;
@@ -358,6 +424,13 @@ PYBIND11_MODULE(_gsplat_core, m) {
         py::arg("far_plane") = 1.0e10f, py::arg("radius_clip") = 0.0f, py::arg("calc_compensations") = false,
         py::arg("camera_model") = 0);
   m.def("projection_ewa_3dgs_fused_backward", &projection_ewa_3dgs_fused_backward, py::arg("inputs"),
+        py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
+        py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
+  m.def("projection_ewa_3dgs_packed_forward", &projection_ewa_3dgs_packed_forward, py::arg("inputs"),
+        py::arg("image_width"), py::arg("image_height"), py::arg("eps2d") = 0.3f, py::arg("near_plane") = 0.01f,
+        py::arg("far_plane") = 1.0e10f, py::arg("radius_clip") = 0.0f, py::arg("calc_compensations") = false,
+        py::arg("camera_model") = 0);
+  m.def("projection_ewa_3dgs_packed_backward", &projection_ewa_3dgs_packed_backward, py::arg("inputs"),
         py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
         py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
   m.def("intersect_tile_forward", &intersect_tile_forward, py::arg("inputs"), py::arg("I"), py::arg("tile_size"),

@@ -31,12 +31,31 @@ int bit_length(uint64_t v) {
 }
 
 // gsplat_intersect.cpp:114-148
+// Packed layout (params.packed, rejected by the reference at :115-118):
+// means2d / radii [nnz, 2], depths [nnz], image_ids [nnz] (the image of each
+// row); gaussian_ids are accepted and not needed (flatten ids are rows).
+void validate_packed_input(const IntersectTileInput& input) {
+  if (input.means2d.dim() != 2 || input.means2d.size(-1) != 2)
+    throw std::runtime_error("intersect_tile packed path expects means2d [nnz, 2].");
+  const int64_t nnz = input.means2d.size(0);
+  if (input.radii.dim() != 2 || input.radii.size(0) != nnz || input.radii.size(1) != 2)
+    throw std::runtime_error("intersect_tile packed path expects radii [nnz, 2].");
+  if (input.depths.dim() != 1 || input.depths.size(0) != nnz)
+    throw std::runtime_error("intersect_tile packed path expects depths [nnz].");
+  if (input.image_ids.numel() != nnz)
+    throw std::runtime_error("intersect_tile packed path expects image_ids [nnz].");
+  if (input.image_ids.scalar_type() != at::kInt && input.image_ids.scalar_type() != at::kLong)
+    throw std::runtime_error("intersect_tile packed path expects int32 or int64 image_ids.");
+  if (input.params.I <= 0) throw std::runtime_error("intersect_tile packed path expects I > 0.");
+  require_device(input.image_ids, "image_ids");
+}
+
 void validate_intersect_tile_input(const IntersectTileInput& input) {
-  if (input.params.packed) throw std::runtime_error("intersect_tile packed path is not implemented yet.");
   if (input.params.segmented) throw std::runtime_error("intersect_tile segmented sort is not implemented yet.");
   if (input.params.use_conics != input.params.use_opacities)
     throw std::runtime_error("intersect_tile AccuTile path needs both conics and opacities.");
-  if (input.means2d.dim() < 3 || input.means2d.size(-1) != 2)
+  if (input.params.packed) validate_packed_input(input);
+  if (input.means2d.dim() < (input.params.packed ? 2 : 3) || input.means2d.size(-1) != 2)
     throw std::runtime_error("means2d must have shape [..., N, 2].");
   if (input.radii.dim() != input.means2d.dim() || input.radii.size(-1) != 2)
     throw std::runtime_error("radii must have shape [..., N, 2].");
@@ -61,6 +80,7 @@ void validate_intersect_tile_input(const IntersectTileInput& input) {
 bool accutile(const IntersectTileInput& input) { return input.params.use_conics && input.params.use_opacities; }
 
 void check_dense_size(const IntersectTileInput& input, const char* op) {
+  if (input.params.packed) return;  // validate_packed_input checked the nnz rows
   const int64_t n = input.means2d.size(-2);
   const int64_t numel = input.depths.numel();
   const int64_t I = input.params.I;
@@ -193,6 +213,17 @@ std::vector<array> encode_unsorted(const IntersectTileInput& input, const array&
                                    const array& depths, const array& offsets, int total, void* stream) {
   array ids = at::empty({total}, i64_like(means2d));
   array flat = at::empty({total}, i32_like(means2d));
+  if (input.params.packed) {
+    const array conics = accutile(input) ? contig(input.conics) : array();
+    const array opac = accutile(input) ? contig(input.opacities) : array();
+    const array image_ids = contig(input.image_ids.to(at::kInt));
+    check(gsplat_hip_isect_encode_packed(
+        means2d.data_ptr<float>(), radii.data_ptr<int32_t>(), accutile(input) ? conics.data_ptr<float>() : nullptr,
+        accutile(input) ? opac.data_ptr<float>() : nullptr, image_ids.data_ptr<int32_t>(), depths.data_ptr<float>(),
+        offsets.data_ptr<int32_t>(), input.params.I, depths.numel(), input.params.tile_size, input.params.tile_width,
+        input.params.tile_height, total, ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), stream));
+    return {ids, flat};
+  }
   if (accutile(input)) {
     const array conics = contig(input.conics);
     const array opac = contig(input.opacities);
@@ -310,7 +341,17 @@ std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& in
     array flat = at::empty({total}, i32_like(means2d));
     const size_t ws2_bytes = gsplat_hip_isect_encode_sorted_workspace_size(total);
     array ws2 = workspace(ws2_bytes, means2d);
-    if (accutile(input)) {
+    if (input.params.packed) {
+      const array conics = accutile(input) ? contig(input.conics) : array();
+      const array opac = accutile(input) ? contig(input.opacities) : array();
+      const array image_ids = contig(input.image_ids.to(at::kInt));
+      check(gsplat_hip_isect_encode_sorted_packed(
+          means2d.data_ptr<float>(), radii.data_ptr<int32_t>(),
+          accutile(input) ? conics.data_ptr<float>() : nullptr, accutile(input) ? opac.data_ptr<float>() : nullptr,
+          image_ids.data_ptr<int32_t>(), depths.data_ptr<float>(), perm.data_ptr<int32_t>(), offs.data_ptr<int32_t>(),
+          input.params.I, numel, input.params.tile_size, input.params.tile_width, input.params.tile_height, total,
+          ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), ws2.data_ptr<uint8_t>(), ws2_bytes, stream));
+    } else if (accutile(input)) {
       const array conics = contig(input.conics);
       const array opac = contig(input.opacities);
       check(gsplat_hip_isect_encode_sorted_accutile(

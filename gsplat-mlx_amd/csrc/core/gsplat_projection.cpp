@@ -3,6 +3,8 @@
 // 584-652 of the reference; compute is the HIP C-ABI.
 #include "gsplat_projection.h"
 
+#include <hip/hip_runtime_api.h>
+
 #include "core_util.h"
 #include "gsplat_training_glue.h"
 
@@ -248,7 +250,149 @@ std::vector<array> projection_backward_impl(const ProjectionEWA3DGSFusedBackward
   return {v_means, v_covars, v_quats, v_scales, v_viewmats};
 }
 
+// The packed count, read on the kernels' stream.
+int64_t read_count(const array& dev_count, void* stream) {
+  int64_t host = 0;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err = hipMemcpyAsync(&host, dev_count.data_ptr<int64_t>(), sizeof(int64_t), hipMemcpyDeviceToHost, s);
+  if (err == hipSuccess) err = hipStreamSynchronize(s);
+  if (err != hipSuccess)
+    throw std::runtime_error(std::string("projection_ewa_3dgs_packed_forward: reading the count failed: ") +
+                             hipGetErrorString(err));
+  if (host > static_cast<int64_t>(INT32_MAX))
+    throw std::runtime_error("projection_ewa_3dgs_packed_forward: more than 2^31-1 visible pairs.");
+  return host;
+}
+
+// int32 copy of caller ids (upstream passes int64).
+array ids32(const array& a, const char* name) {
+  require_device(a, name);
+  if (a.scalar_type() != at::kInt && a.scalar_type() != at::kLong)
+    throw std::runtime_error(std::string(name) + " must be int32 or int64.");
+  return contig(a.to(at::kInt));
+}
+
 }  // namespace
+
+std::vector<array> gsplat_projection_ewa_3dgs_packed(const ProjectionEWA3DGSFusedInput& input) {
+  validate_inputs(input);
+  require_device(input.means, "means");
+  require_device(input.viewmats, "viewmats");
+  require_device(input.Ks, "Ks");
+  const Dims d = dims_of(input.means, input.viewmats, input.Ks);
+  const auto& p = input.params;
+  check_gaussian_params(input.means, input.covars, input.quats, input.scales, p.use_covars, d.B * d.N);
+  if (p.use_opacities) {
+    require_device(input.opacities, "opacities");
+    require_dtype(input.opacities, at::kFloat, "projection_ewa_3dgs_packed expects float32 opacities.");
+    if (input.opacities.numel() != d.B * d.N) throw std::runtime_error("opacities must have shape [..., N].");
+  }
+  const c10::DeviceGuard guard(input.means.device());
+  const array means = contig(input.means);
+  const array covars = p.use_covars ? contig(input.covars) : array();
+  const array quats = p.use_covars ? array() : contig(input.quats);
+  const array scales = p.use_covars ? array() : contig(input.scales);
+  const array opac = p.use_opacities ? contig(input.opacities) : array();
+  const array viewmats = contig(input.viewmats.to(at::kFloat));
+  const array Ks = contig(input.Ks.to(at::kFloat));
+  void* stream = stream_for(input.s, means);
+  const gsplat_projection_params cp = to_c(p);
+  const size_t ws_bytes = gsplat_hip_projection_packed_workspace_size(d.B, d.C, d.N, 0);
+  array ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, u8_like(means));
+  array count = at::empty({1}, i64_like(means));
+  const float* cov_p = p.use_covars ? covars.data_ptr<float>() : nullptr;
+  const float* q_p = p.use_covars ? nullptr : quats.data_ptr<float>();
+  const float* s_p = p.use_covars ? nullptr : scales.data_ptr<float>();
+  const float* o_p = p.use_opacities ? opac.data_ptr<float>() : nullptr;
+  check(gsplat_hip_projection_packed_count(means.data_ptr<float>(), cov_p, q_p, s_p, o_p, viewmats.data_ptr<float>(),
+                                           Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, count.data_ptr<int64_t>(),
+                                           ws.data_ptr<uint8_t>(), ws_bytes, stream));
+  const int64_t nnz = d.B * d.C * d.N > 0 ? read_count(count, stream) : 0;
+  auto i32 = [&](std::vector<int64_t> shape) { return at::empty(shape, i32_like(means)); };
+  auto f32 = [&](std::vector<int64_t> shape) { return at::empty(shape, f32_like(means)); };
+  array batch_ids = i32({nnz}), camera_ids = i32({nnz}), gaussian_ids = i32({nnz});
+  array indptr = i32({d.B * d.C + 1});
+  array radii = i32({nnz, 2});
+  array means2d = f32({nnz, 2}), depths = f32({nnz}), conics = f32({nnz, 3});
+  array comps = p.calc_compensations ? f32({nnz}) : f32({0});
+  check(gsplat_hip_projection_packed_fwd(
+      means.data_ptr<float>(), cov_p, q_p, s_p, o_p, viewmats.data_ptr<float>(), Ks.data_ptr<float>(), d.B, d.C, d.N,
+      &cp, nnz, batch_ids.data_ptr<int32_t>(), camera_ids.data_ptr<int32_t>(), gaussian_ids.data_ptr<int32_t>(),
+      indptr.data_ptr<int32_t>(), radii.data_ptr<int32_t>(), means2d.data_ptr<float>(), depths.data_ptr<float>(),
+      conics.data_ptr<float>(), p.calc_compensations ? comps.data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(),
+      ws_bytes, stream));
+  return {batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d, depths, conics, comps};
+}
+
+std::vector<array> gsplat_projection_ewa_3dgs_packed_backward(const ProjectionEWA3DGSPackedBackwardInput& input) {
+  ProjectionEWA3DGSFusedInput fwd;
+  fwd.means = input.means;
+  fwd.covars = input.covars;
+  fwd.quats = input.quats;
+  fwd.scales = input.scales;
+  fwd.viewmats = input.viewmats;
+  fwd.Ks = input.Ks;
+  fwd.params = input.params;
+  validate_inputs(fwd);
+  if (input.params.camera_model != 0)
+    throw std::runtime_error("projection_ewa_3dgs_packed_backward currently supports pinhole only.");
+  require_device(input.means, "means");
+  require_device(input.viewmats, "viewmats");
+  require_device(input.Ks, "Ks");
+  const Dims d = dims_of(input.means, input.viewmats, input.Ks);
+  const auto& p = input.params;
+  check_gaussian_params(input.means, input.covars, input.quats, input.scales, p.use_covars, d.B * d.N);
+  const int64_t nnz = input.camera_ids.numel();
+  const bool use_v_depths = !is_empty(input.v_depths);
+  if (input.gaussian_ids.numel() != nnz || (!is_empty(input.batch_ids) && input.batch_ids.numel() != nnz) ||
+      input.conics.numel() != nnz * 3 || input.v_means2d.numel() != nnz * 2 || input.v_conics.numel() != nnz * 3 ||
+      (use_v_depths && input.v_depths.numel() != nnz))
+    throw std::runtime_error("projection_ewa_3dgs_packed_backward: packed inputs must have nnz rows.");
+  if (d.B > 1 && is_empty(input.batch_ids))
+    throw std::runtime_error("projection_ewa_3dgs_packed_backward: batch_ids are needed with more than one batch.");
+  const bool use_comp = p.calc_compensations && !is_empty(input.compensations) && !is_empty(input.v_compensations);
+  if (use_comp && (input.compensations.numel() != nnz || input.v_compensations.numel() != nnz))
+    throw std::runtime_error("compensations / v_compensations must have nnz rows.");
+  const c10::DeviceGuard guard(input.means.device());
+  const array means = contig(input.means);
+  const array covars = p.use_covars ? contig(input.covars) : array();
+  const array quats = p.use_covars ? array() : contig(input.quats);
+  const array scales = p.use_covars ? array() : contig(input.scales);
+  const array viewmats = contig(input.viewmats.to(at::kFloat));
+  const array Ks = contig(input.Ks.to(at::kFloat));
+  const array bid = is_empty(input.batch_ids) ? array() : ids32(input.batch_ids, "batch_ids");
+  const array cid = ids32(input.camera_ids, "camera_ids");
+  const array gid = ids32(input.gaussian_ids, "gaussian_ids");
+  const array conics = contig(input.conics.to(at::kFloat));
+  const array comps = use_comp ? contig(input.compensations.to(at::kFloat)) : array();
+  const array v_comps = use_comp ? contig(input.v_compensations.to(at::kFloat)) : array();
+  const array v_m2 = contig(input.v_means2d.to(at::kFloat));
+  const array v_dep = use_v_depths ? contig(input.v_depths.to(at::kFloat)) : array();
+  const array v_con = contig(input.v_conics.to(at::kFloat));
+  array v_means = at::empty(means.sizes(), f32_like(means));
+  array v_covars = p.use_covars ? at::empty(covars.sizes(), f32_like(means)) : at::empty({0}, f32_like(means));
+  array v_quats = p.use_covars ? at::empty({0}, f32_like(means)) : at::empty(quats.sizes(), f32_like(means));
+  array v_scales = p.use_covars ? at::empty({0}, f32_like(means)) : at::empty(scales.sizes(), f32_like(means));
+  array v_viewmats = input.viewmats_requires_grad ? at::empty(viewmats.sizes(), f32_like(means))
+                                                  : at::empty({0}, f32_like(means));
+  const size_t ws_bytes =
+      gsplat_hip_projection_packed_workspace_size(d.B, d.C, d.N, input.viewmats_requires_grad ? 1 : 0);
+  array ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, u8_like(means));
+  const gsplat_projection_params cp = to_c(p);
+  check(gsplat_hip_projection_packed_bwd(
+      means.data_ptr<float>(), p.use_covars ? covars.data_ptr<float>() : nullptr,
+      p.use_covars ? nullptr : quats.data_ptr<float>(), p.use_covars ? nullptr : scales.data_ptr<float>(),
+      viewmats.data_ptr<float>(), Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, nnz,
+      is_empty(bid) ? nullptr : bid.data_ptr<int32_t>(), cid.data_ptr<int32_t>(), gid.data_ptr<int32_t>(),
+      conics.data_ptr<float>(), use_comp ? comps.data_ptr<float>() : nullptr, v_m2.data_ptr<float>(),
+      use_v_depths ? v_dep.data_ptr<float>() : nullptr, v_con.data_ptr<float>(),
+      use_comp ? v_comps.data_ptr<float>() : nullptr, v_means.data_ptr<float>(),
+      p.use_covars ? v_covars.data_ptr<float>() : nullptr, p.use_covars ? nullptr : v_quats.data_ptr<float>(),
+      p.use_covars ? nullptr : v_scales.data_ptr<float>(),
+      input.viewmats_requires_grad ? v_viewmats.data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(), ws_bytes,
+      stream_for(input.s, means)));
+  return {v_means, v_covars, v_quats, v_scales, v_viewmats};
+}
 
 std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFusedInput& input) {
   return projection_forward_impl(input, false);

@@ -12,8 +12,23 @@ namespace {
 using namespace detail;
 
 // gsplat_rasterize.cpp:44-88
+// Packed layout (params.packed, rejected by the reference at :48-51): the
+// Gaussian arrays have nnz rows that flatten_ids index directly.
 void validate_rasterize_input(const RasterizeToPixels3DGSInput& in) {
-  if (in.params.packed) throw std::runtime_error("rasterize_to_pixels_3dgs packed path is not implemented yet.");
+  if (in.params.packed) {
+    if (in.means2d.dim() != 2 || in.means2d.size(-1) != 2) throw std::runtime_error("means2d must have shape [nnz, 2].");
+    const int64_t nnz = in.means2d.size(0);
+    if (in.conics.dim() != 2 || in.conics.size(0) != nnz || in.conics.size(1) != 3)
+      throw std::runtime_error("conics must have shape [nnz, 3].");
+    if (in.colors.dim() != 2 || in.colors.size(0) != nnz) throw std::runtime_error("colors must have shape [nnz, channels].");
+    if (in.opacities.dim() != 1 || in.opacities.size(0) != nnz) throw std::runtime_error("opacities must have shape [nnz].");
+    if (in.tile_offsets.dim() < 3)
+      throw std::runtime_error("tile_offsets must have shape [..., tile_height, tile_width].");
+    if (in.flatten_ids.dim() != 1) throw std::runtime_error("flatten_ids must have shape [n_isects].");
+    if (in.params.use_masks && in.masks.sizes() != in.tile_offsets.sizes())
+      throw std::runtime_error("masks must have the same shape as tile_offsets.");
+    return;
+  }
   if (in.means2d.dim() < 3 || in.means2d.size(-1) != 2) throw std::runtime_error("means2d must have shape [..., N, 2].");
   if (in.conics.dim() != in.means2d.dim() || in.conics.size(-1) != 3)
     throw std::runtime_error("conics must have shape [..., N, 3].");
@@ -43,6 +58,11 @@ Layout layout_of(const RasterizeToPixels3DGSInput& in) {
   l.th = static_cast<int>(in.tile_offsets.size(-2));
   l.tw = static_cast<int>(in.tile_offsets.size(-1));
   l.I = (l.th * l.tw) ? in.tile_offsets.numel() / (static_cast<int64_t>(l.th) * l.tw) : 0;
+  if (in.params.packed) {  // N = nnz rows, shapes checked by validate_rasterize_input
+    if (in.params.use_backgrounds && in.backgrounds.numel() != l.I * l.channels)
+      throw std::runtime_error("backgrounds must have shape [..., channels].");
+    return l;
+  }
   if (in.means2d.numel() / 2 != l.I * l.N)
     throw std::runtime_error(
         "rasterize_to_pixels_3dgs dense path expects means2d size to equal I * N * 2.");
@@ -89,7 +109,8 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs(const RasterizeToPixels3DGSIn
   array render_colors = at::empty(rc_shape, f32_like(means2d));
   array render_alphas = at::empty(ra_shape, f32_like(means2d));
   array last_ids = at::empty(li_shape, i32_like(means2d));
-  check(gsplat_hip_rasterize_fwd(means2d.data_ptr<float>(), conics.data_ptr<float>(), colors.data_ptr<float>(),
+  check((p.packed ? gsplat_hip_rasterize_fwd_packed : gsplat_hip_rasterize_fwd)(
+                                 means2d.data_ptr<float>(), conics.data_ptr<float>(), colors.data_ptr<float>(),
                                  opac.data_ptr<float>(), p.use_backgrounds ? bg.data_ptr<float>() : nullptr,
                                  p.use_masks ? masks.data_ptr<uint8_t>() : nullptr, offsets.data_ptr<int32_t>(),
                                  flat.data_ptr<int32_t>(), l.I, l.N, l.channels, p.image_width, p.image_height,
@@ -150,7 +171,7 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
   array v_bg = p.use_backgrounds ? at::empty(bg.sizes(), f32_like(means2d)) : at::empty({0}, f32_like(means2d));
   const size_t ws_bytes = gsplat_hip_rasterize_bwd_workspace_size(l.I, static_cast<int32_t>(l.channels), l.tw, l.th);
   array ws = at::empty({static_cast<int64_t>(std::max<size_t>(ws_bytes, 1))}, u8_like(means2d));
-  check(gsplat_hip_rasterize_bwd(
+  check((p.packed ? gsplat_hip_rasterize_bwd_packed : gsplat_hip_rasterize_bwd)(
       means2d.data_ptr<float>(), conics.data_ptr<float>(), colors.data_ptr<float>(), opac.data_ptr<float>(),
       p.use_backgrounds ? bg.data_ptr<float>() : nullptr, p.use_masks ? masks.data_ptr<uint8_t>() : nullptr,
       offsets.data_ptr<int32_t>(), flat.data_ptr<int32_t>(), l.I, l.N, l.channels, p.image_width, p.image_height,

@@ -71,4 +71,50 @@ std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFused
 
 std::vector<array> gsplat_projection_ewa_3dgs_fused_backward(const ProjectionEWA3DGSFusedBackwardInput& input);
 
+// Packed layout: upstream gsplat's fully_fused_projection(packed=True), the
+// reference's intended projection_ewa_3dgs_packed_forward
+// (note/gsplat_cuda_source_map.md:273-315). Only the visible (camera,
+// Gaussian) pairs, nnz of them, ordered by (batch, camera, gaussian); each row
+// equals the dense output of its pair. ids are int32; indptr [B*C + 1] holds
+// each camera's first row. Reads the count back to the host (one sync).
+enum ProjectionEWA3DGSPackedOutputIndex {
+  kPackedBatchIds = 0,
+  kPackedCameraIds = 1,
+  kPackedGaussianIds = 2,
+  kPackedIndptr = 3,
+  kPackedRadii = 4,
+  kPackedMeans2D = 5,
+  kPackedDepths = 6,
+  kPackedConics = 7,
+  kPackedCompensations = 8,
+};
+
+std::vector<array> gsplat_projection_ewa_3dgs_packed(const ProjectionEWA3DGSFusedInput& input);
+
+// Cotangents v_* [nnz, ...] of the packed outputs; the ids must be the
+// forward's. Outputs as the dense backward (ProjectionEWA3DGSFusedBackward
+// OutputIndex), equal to it with the cotangents scattered to their pairs.
+struct ProjectionEWA3DGSPackedBackwardInput {
+  array means;
+  array covars;
+  array quats;
+  array scales;
+  array viewmats;
+  array Ks;
+  array batch_ids;
+  array camera_ids;
+  array gaussian_ids;
+  array conics;
+  array compensations;
+  array v_means2d;
+  array v_depths;
+  array v_conics;
+  array v_compensations;
+  StreamOrDevice s;
+  ProjectionEWA3DGSFusedParams params;
+  bool viewmats_requires_grad;
+};
+
+std::vector<array> gsplat_projection_ewa_3dgs_packed_backward(const ProjectionEWA3DGSPackedBackwardInput& input);
+
 }  // namespace gsplat_core

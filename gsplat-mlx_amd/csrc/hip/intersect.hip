@@ -7,6 +7,7 @@
 // uses the same float divisions, floor/ceil and clamps.
 #include <algorithm>
 #include <cmath>
+#include <string>
 
 #include "radix_sort.hpp"
 #include "scan.hpp"
@@ -104,6 +105,7 @@ __device__ __forceinline__ EllipseTiles ellipse_tiles(const float* __restrict__ 
     e.mode = 0;
     return e;
   }
+  if (!conics || !opacities) return e;  // AABB lists: the whole rect
   const float o = opacities[g];
   if (o <= 0.0f) {
     e.mode = 0;
@@ -591,8 +593,9 @@ constexpr int kEllOuts = kEllItems / kEncodeBlock;  // slots per thread (at most
 __global__ void __launch_bounds__(kEncodeBlock) encode_ellipse_kernel(
     const float* __restrict__ means2d, const int32_t* __restrict__ radii, const float* __restrict__ conics,
     const float* __restrict__ opacities, const float* __restrict__ depths, const int32_t* __restrict__ perm,
-    const int32_t* __restrict__ offsets, int64_t numel, int64_t n_per_image, int ts, int tw, int th, int tile_bits,
-    int64_t n_isects, uint32_t* __restrict__ keys32, int64_t* __restrict__ ids64, int32_t* __restrict__ vals) {
+    const int32_t* __restrict__ offsets, const int32_t* __restrict__ image_ids, int64_t numel, int64_t n_per_image,
+    int ts, int tw, int th, int tile_bits, int64_t n_isects, uint32_t* __restrict__ keys32,
+    int64_t* __restrict__ ids64, int32_t* __restrict__ vals) {
   constexpr int kRanks = kEllItems + 1;
   __shared__ int32_t s_off[kRanks];
   __shared__ int32_t s_g[kRanks];
@@ -665,7 +668,8 @@ __global__ void __launch_bounds__(kEncodeBlock) encode_ellipse_kernel(
     }
     // offsets that disagree with the counts still get an in-range tile
     const int tile = valid && ok ? ty * tw + tx : 0;
-    const uint32_t image = valid ? static_cast<uint32_t>(g / n_per_image) : 0u;
+    const uint32_t image =
+        !valid ? 0u : static_cast<uint32_t>(image_ids ? static_cast<int64_t>(image_ids[g]) : g / n_per_image);
     const uint32_t key = (image << tile_bits) | static_cast<uint32_t>(tile);
     if (keys32) {
       keys32[j] = key;
@@ -917,7 +921,7 @@ extern "C" int gsplat_hip_isect_encode_accutile(const float* means2d, const int3
     KernelTimer timer("isect_encode", s);
     const int64_t nb = (numel + n_isects + kEllItems - 1) / kEllItems;
     encode_ellipse_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
-        means2d, radii, conics, opacities, depths, nullptr, offsets, numel, numel / I, tile_size, tile_width,
+        means2d, radii, conics, opacities, depths, nullptr, offsets, nullptr, numel, numel / I, tile_size, tile_width,
         tile_height, tile_bits, n_isects, nullptr, isect_ids, flatten_ids);
   }
   return check_launch("intersect_tile_encode");
@@ -954,8 +958,81 @@ extern "C" int gsplat_hip_isect_encode_sorted_accutile(const float* means2d, con
     KernelTimer timer("isect_encode", s);
     const int64_t nb = (numel + n_isects + kEllItems - 1) / kEllItems;
     encode_ellipse_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
-        means2d, radii, conics, opacities, depths, perm, offsets, numel, numel / I, tile_size, tile_width,
+        means2d, radii, conics, opacities, depths, perm, offsets, nullptr, numel, numel / I, tile_size, tile_width,
         tile_height, tile_bits, n_isects, l.tkeys, nullptr, l.tvals);
+  }
+  if ((rc = check_launch(what))) return rc;
+  return radix_sort_pairs<uint32_t>(l.tkeys, l.tvals, n_isects, 0, image_bits + tile_bits, l.tkeys_sorted,
+                                    flatten_ids, l.sort_ws, l.sort_ws_bytes, s, what, depths, isect_ids);
+}
+
+// Packed layout (IntersectTileParams.packed, gsplat_intersect.cpp:115-118):
+// entry i of the nnz rows belongs to image image_ids[i]; flatten ids are
+// row indices. With conics and opacities the ellipse tiles, else the AABB
+// rect. Counts come from gsplat_hip_isect_count_scan(_accutile) over the
+// rows, the sorted path's perm and offsets from gsplat_hip_isect_depth_order.
+static int encode_packed_args(const char* what, const int32_t* image_ids, int64_t I, int64_t nnz, int32_t ts,
+                              int32_t tw, int32_t th, int64_t n_isects, int* tile_bits, int* image_bits) {
+  if (I <= 0 || nnz < 0) return invalid(std::string(what) + " packed path expects I > 0 and nnz >= 0.");
+  if (ts <= 0 || tw <= 0 || th <= 0) return invalid(std::string(what) + ": invalid tiles.");
+  if (n_isects < 0) return invalid(std::string(what) + ": negative intersection count.");
+  if (nnz > INT32_MAX || n_isects > INT32_MAX) return invalid(std::string(what) + ": more than 2^31-1 entries.");
+  if (nnz > 0 && n_isects > 0 && !image_ids) return invalid(std::string(what) + ": null image_ids.");
+  return check_tile_bits(I, tw, th, tile_bits, image_bits);
+}
+
+extern "C" int gsplat_hip_isect_encode_packed(const float* means2d, const int32_t* radii, const float* conics,
+                                              const float* opacities, const int32_t* image_ids, const float* depths,
+                                              const int32_t* offsets, int64_t I, int64_t nnz, int32_t tile_size,
+                                              int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                              int64_t* isect_ids, int32_t* flatten_ids, void* stream) {
+  int tile_bits, image_bits;
+  int rc = encode_packed_args("intersect_tile_encode", image_ids, I, nnz, tile_size, tile_width, tile_height,
+                              n_isects, &tile_bits, &image_bits);
+  if (rc) return rc;
+  if (nnz == 0 || n_isects == 0) return GSPLAT_OK;
+  if (!means2d || !radii || !depths || !offsets || !isect_ids || !flatten_ids)
+    return invalid("intersect_tile_encode: null pointer.");
+  hipStream_t s = as_stream(stream);
+  {
+    KernelTimer timer("isect_encode", s);
+    const int64_t nb = (nnz + n_isects + kEllItems - 1) / kEllItems;
+    encode_ellipse_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
+        means2d, radii, conics && opacities ? conics : nullptr, conics && opacities ? opacities : nullptr, depths,
+        nullptr, offsets, image_ids, nnz, nnz, tile_size, tile_width, tile_height, tile_bits, n_isects, nullptr,
+        isect_ids, flatten_ids);
+  }
+  return check_launch("intersect_tile_encode");
+}
+
+extern "C" int gsplat_hip_isect_encode_sorted_packed(const float* means2d, const int32_t* radii, const float* conics,
+                                                     const float* opacities, const int32_t* image_ids,
+                                                     const float* depths, const int32_t* perm, const int32_t* offsets,
+                                                     int64_t I, int64_t nnz, int32_t tile_size, int32_t tile_width,
+                                                     int32_t tile_height, int64_t n_isects, int64_t* isect_ids,
+                                                     int32_t* flatten_ids, void* workspace, size_t workspace_bytes,
+                                                     void* stream) {
+  const char* what = "intersect_tile";
+  int tile_bits, image_bits;
+  int rc = encode_packed_args(what, image_ids, I, nnz, tile_size, tile_width, tile_height, n_isects, &tile_bits,
+                              &image_bits);
+  if (rc) return rc;
+  if (nnz == 0 || n_isects == 0) return GSPLAT_OK;
+  if (!means2d || !radii || !depths || !perm || !offsets || !isect_ids || !flatten_ids)
+    return invalid("intersect_tile: null pointer.");
+  EncodeSortedLayout l;
+  if (!workspace || workspace_bytes < encode_sorted_layout(n_isects, &l, workspace)) {
+    set_error("intersect_tile: workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  hipStream_t s = as_stream(stream);
+  {
+    KernelTimer timer("isect_encode", s);
+    const int64_t nb = (nnz + n_isects + kEllItems - 1) / kEllItems;
+    encode_ellipse_kernel<<<static_cast<unsigned>(nb), kEncodeBlock, 0, s>>>(
+        means2d, radii, conics && opacities ? conics : nullptr, conics && opacities ? opacities : nullptr, depths,
+        perm, offsets, image_ids, nnz, nnz, tile_size, tile_width, tile_height, tile_bits, n_isects, l.tkeys, nullptr,
+        l.tvals);
   }
   if ((rc = check_launch(what))) return rc;
   return radix_sort_pairs<uint32_t>(l.tkeys, l.tvals, n_isects, 0, image_bits + tile_bits, l.tkeys_sorted,

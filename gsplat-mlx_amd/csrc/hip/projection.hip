@@ -24,6 +24,7 @@
 // the quaternion and scale gradients through the activations and turns the
 // rasterizer's opacity gradient into the logits' gradient.
 #include "projection_common.hpp"
+#include "scan.hpp"
 
 namespace gsplat_hip {
 namespace {
@@ -31,6 +32,84 @@ namespace {
 // ACT: quats, scales and opacities hold the raw parameters (quaternions,
 // log-scales, opacity logits) and opac_out (if non-null) receives the sigmoid
 // opacities, written by the first camera of each batch.
+// One (camera, Gaussian) pair: the culling of gsplat_projection.metal:214-339
+// and the EWA math of gsplat_projection.cpp:446-521, in the same operation
+// order. Shared by the dense kernel and both packed passes, so the packed
+// outputs equal the dense ones bit for bit.
+struct PairOut {
+  bool valid;
+  int32_t rx, ry;
+  float m2x, m2y, depth, c0, c1, c2, comp;
+};
+
+template <bool ACT>
+__device__ __forceinline__ PairOut project_pair(const float* __restrict__ means, const float* __restrict__ covars,
+                                                const float* __restrict__ quats, const float* __restrict__ scales,
+                                                const float* __restrict__ opacities, const CamFrame& f, int64_t g,
+                                                const gsplat_projection_params& p) {
+  PairOut o = {false, 0, 0, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  const float mw[3] = {means[g * 3], means[g * 3 + 1], means[g * 3 + 2]};
+  float mc[3];
+  world_to_cam(f, mw, mc);
+  bool valid = !(mc[2] < p.near_plane || mc[2] > p.far_plane);
+  if (!valid) return o;
+  Mat3 cw;
+  if (p.use_covars) {
+    cw = read_covar(covars + g * 6);
+  } else {
+    float q[4], s[3];
+    load_quat_scale<ACT>(quats, scales, g, q, s);
+    cw = covar_from_quat_scale(q, s);
+  }
+  const Mat3 cc = mat3_mul(mat3_mul(f.R, cw), mat3_tr(f.R));
+  float J[6], m2[2];
+  camera_jacobian(p.camera_model, mc, f, p.image_width, p.image_height, J, m2);
+  float cov2d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int row = 0; row < 2; ++row)
+#pragma unroll
+    for (int col = 0; col < 2; ++col) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int bb = 0; bb < 3; ++bb) acc += J[row * 3 + a] * cc.v[a * 3 + bb] * J[col * 3 + bb];
+      cov2d[row * 2 + col] = acc;
+    }
+  const float det_orig = cov2d[0] * cov2d[3] - cov2d[1] * cov2d[2];
+  cov2d[0] += p.eps2d;
+  cov2d[3] += p.eps2d;
+  const float det = cov2d[0] * cov2d[3] - cov2d[1] * cov2d[2];
+  const float comp = sqrtf(fmaxf(kMinCompensation * kMinCompensation, det_orig / det));
+  valid = det > 0.0f;
+  float extend = kGaussianExtend;
+  if (valid && p.use_opacities) {
+    float op = ACT ? sigmoid_of(opacities[g]) : opacities[g];
+    if (p.calc_compensations) op *= comp;
+    valid = !(op < kAlphaThreshold);
+    if (valid) extend = fminf(kGaussianExtend, sqrtf(2.0f * logf(op / kAlphaThreshold)));
+  }
+  if (!valid) return o;
+  const float rx = ceilf(extend * sqrtf(cov2d[0]));
+  const float ry = ceilf(extend * sqrtf(cov2d[3]));
+  valid = !(rx <= p.radius_clip && ry <= p.radius_clip) &&
+          !(m2[0] + rx <= 0.0f || m2[0] - rx >= static_cast<float>(p.image_width) || m2[1] + ry <= 0.0f ||
+            m2[1] - ry >= static_cast<float>(p.image_height));
+  if (!valid) return o;
+  const float inv_det = 1.0f / det;
+  o.valid = true;
+  o.rx = static_cast<int32_t>(rx);
+  o.ry = static_cast<int32_t>(ry);
+  o.m2x = m2[0];
+  o.m2y = m2[1];
+  o.depth = mc[2];
+  o.c0 = cov2d[3] * inv_det;
+  o.c1 = -cov2d[1] * inv_det;
+  o.c2 = cov2d[0] * inv_det;
+  o.comp = comp;
+  return o;
+}
+
 template <bool ACT>
 __global__ void __launch_bounds__(kProjBlock) projection_fwd_kernel(
     const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
@@ -48,80 +127,113 @@ __global__ void __launch_bounds__(kProjBlock) projection_fwd_kernel(
   if constexpr (ACT) {
     if (opac_out && cam == b * C) opac_out[g] = sigmoid_of(opacities[g]);
   }
+  const PairOut o = project_pair<ACT>(means, covars, quats, scales, opacities, f, g, p);
+  radii[idx * 2] = o.rx;
+  radii[idx * 2 + 1] = o.ry;
+  means2d[idx * 2] = o.m2x;
+  means2d[idx * 2 + 1] = o.m2y;
+  depths[idx] = o.depth;
+  conics[idx * 3] = o.c0;
+  conics[idx * 3 + 1] = o.c1;
+  conics[idx * 3 + 2] = o.c2;
+  if (compensations) compensations[idx] = o.comp;
+}
 
-  int32_t rx_out = 0, ry_out = 0;
-  float m2x = 0.0f, m2y = 0.0f, depth = 0.0f, c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, comp_out = 0.0f;
+// ---------------------------------------------------------------------------
+// Packed layout (upstream gsplat's fully_fused_projection(packed=True),
+// note/gsplat_cuda_source_map.md:273-315): only the visible pairs, in flat
+// order idx = (b * C + c) * N + n. Pass 1 computes every pair's visibility
+// and stores one bit per pair (a 64-bit word per wave of 64 consecutive idx)
+// with the word's popcount; an exclusive scan of the popcounts gives each
+// word's first packed position; pass 2 recomputes the visible pairs and
+// writes them at prefix[word] + popcount(bits below). The same bit words and
+// prefixes ("rank structure", 3/16 byte per pair) let the backward find a
+// pair's packed row without a dense index map.
+__device__ __forceinline__ int64_t packed_rank(const uint64_t* __restrict__ mask, const int32_t* __restrict__ prefix,
+                                               int64_t idx) {
+  const uint64_t w = mask[idx >> 6];
+  const int bit = static_cast<int>(idx & 63);
+  return static_cast<int64_t>(prefix[idx >> 6]) + __popcll(w & ((1ull << bit) - 1ull));
+}
 
-  const float mw[3] = {means[g * 3], means[g * 3 + 1], means[g * 3 + 2]};
-  float mc[3];
-  world_to_cam(f, mw, mc);
-  bool valid = !(mc[2] < p.near_plane || mc[2] > p.far_plane);
-  if (valid) {
-    Mat3 cw;
-    if (p.use_covars) {
-      cw = read_covar(covars + g * 6);
-    } else {
-      float q[4], s[3];
-      load_quat_scale<ACT>(quats, scales, g, q, s);
-      cw = covar_from_quat_scale(q, s);
-    }
-    const Mat3 cc = mat3_mul(mat3_mul(f.R, cw), mat3_tr(f.R));
-    float J[6], m2[2];
-    camera_jacobian(p.camera_model, mc, f, p.image_width, p.image_height, J, m2);
-    float cov2d[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-    for (int row = 0; row < 2; ++row)
-#pragma unroll
-      for (int col = 0; col < 2; ++col) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int a = 0; a < 3; ++a)
-#pragma unroll
-          for (int bb = 0; bb < 3; ++bb) acc += J[row * 3 + a] * cc.v[a * 3 + bb] * J[col * 3 + bb];
-        cov2d[row * 2 + col] = acc;
-      }
-    const float det_orig = cov2d[0] * cov2d[3] - cov2d[1] * cov2d[2];
-    cov2d[0] += p.eps2d;
-    cov2d[3] += p.eps2d;
-    const float det = cov2d[0] * cov2d[3] - cov2d[1] * cov2d[2];
-    const float comp = sqrtf(fmaxf(kMinCompensation * kMinCompensation, det_orig / det));
-    valid = det > 0.0f;
-    float extend = kGaussianExtend;
-    if (valid && p.use_opacities) {
-      float op = ACT ? sigmoid_of(opacities[g]) : opacities[g];
-      if (p.calc_compensations) op *= comp;
-      valid = !(op < kAlphaThreshold);
-      if (valid) extend = fminf(kGaussianExtend, sqrtf(2.0f * logf(op / kAlphaThreshold)));
-    }
-    if (valid) {
-      const float rx = ceilf(extend * sqrtf(cov2d[0]));
-      const float ry = ceilf(extend * sqrtf(cov2d[3]));
-      valid = !(rx <= p.radius_clip && ry <= p.radius_clip) &&
-              !(m2[0] + rx <= 0.0f || m2[0] - rx >= static_cast<float>(p.image_width) || m2[1] + ry <= 0.0f ||
-                m2[1] - ry >= static_cast<float>(p.image_height));
-      if (valid) {
-        const float inv_det = 1.0f / det;
-        rx_out = static_cast<int32_t>(rx);
-        ry_out = static_cast<int32_t>(ry);
-        m2x = m2[0];
-        m2y = m2[1];
-        depth = mc[2];
-        c0 = cov2d[3] * inv_det;
-        c1 = -cov2d[1] * inv_det;
-        c2 = cov2d[0] * inv_det;
-        comp_out = comp;
-      }
-    }
+__global__ void __launch_bounds__(kProjBlock) projection_packed_mask_kernel(
+    const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
+    const float* __restrict__ scales, const float* __restrict__ opacities, const float* __restrict__ viewmats,
+    const float* __restrict__ Ks, int64_t C, int64_t N, int64_t total, gsplat_projection_params p,
+    uint64_t* __restrict__ mask, int32_t* __restrict__ word_counts) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
+  bool valid = false;
+  if (idx < total) {
+    const int64_t cam = idx / N, n = idx - cam * N;
+    const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
+    valid = project_pair<false>(means, covars, quats, scales, opacities, f, (cam / C) * N + n, p).valid;
   }
-  radii[idx * 2] = rx_out;
-  radii[idx * 2 + 1] = ry_out;
-  means2d[idx * 2] = m2x;
-  means2d[idx * 2 + 1] = m2y;
-  depths[idx] = depth;
-  conics[idx * 3] = c0;
-  conics[idx * 3 + 1] = c1;
-  conics[idx * 3 + 2] = c2;
-  if (compensations) compensations[idx] = comp_out;
+  const uint64_t bits = __ballot(valid);
+  if ((threadIdx.x % kWave) == 0 && idx < total) {
+    mask[idx >> 6] = bits;
+    word_counts[idx >> 6] = __popcll(bits);
+  }
+}
+
+__global__ void __launch_bounds__(kProjBlock) projection_packed_write_kernel(
+    const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
+    const float* __restrict__ scales, const float* __restrict__ opacities, const float* __restrict__ viewmats,
+    const float* __restrict__ Ks, int64_t C, int64_t N, int64_t total, gsplat_projection_params p,
+    const uint64_t* __restrict__ mask, const int32_t* __restrict__ prefix, int64_t nnz,
+    int32_t* __restrict__ batch_ids, int32_t* __restrict__ camera_ids, int32_t* __restrict__ gaussian_ids,
+    int32_t* __restrict__ radii, float* __restrict__ means2d, float* __restrict__ depths,
+    float* __restrict__ conics, float* __restrict__ compensations) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
+  if (idx >= total || !((mask[idx >> 6] >> (idx & 63)) & 1ull)) return;
+  const int64_t pos = packed_rank(mask, prefix, idx);
+  if (pos >= nnz) return;  // nnz smaller than the count: keep writes in bounds
+  const int64_t cam = idx / N, n = idx - cam * N;
+  const int64_t b = cam / C;
+  const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
+  const PairOut o = project_pair<false>(means, covars, quats, scales, opacities, f, b * N + n, p);
+  batch_ids[pos] = static_cast<int32_t>(b);
+  camera_ids[pos] = static_cast<int32_t>(cam - b * C);
+  gaussian_ids[pos] = static_cast<int32_t>(n);
+  radii[pos * 2] = o.rx;
+  radii[pos * 2 + 1] = o.ry;
+  means2d[pos * 2] = o.m2x;
+  means2d[pos * 2 + 1] = o.m2y;
+  depths[pos] = o.depth;
+  conics[pos * 3] = o.c0;
+  conics[pos * 3 + 1] = o.c1;
+  conics[pos * 3 + 2] = o.c2;
+  if (compensations) compensations[pos] = o.comp;
+}
+
+// indptr[cam] = packed position of the first pair of camera cam (B*C + 1
+// entries; the last is nnz).
+__global__ void __launch_bounds__(256) projection_packed_indptr_kernel(const uint64_t* __restrict__ mask,
+                                                                       const int32_t* __restrict__ prefix,
+                                                                       int64_t n_cams, int64_t N, int64_t nnz,
+                                                                       int32_t* __restrict__ indptr) {
+  const int64_t cam = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (cam > n_cams) return;
+  indptr[cam] = static_cast<int32_t>(cam == n_cams ? nnz : min<int64_t>(packed_rank(mask, prefix, cam * N), nnz));
+}
+
+// Backward: bit per pair from the packed (batch, camera, gaussian) ids.
+__global__ void __launch_bounds__(256) projection_packed_scatter_kernel(const int32_t* __restrict__ batch_ids,
+                                                                        const int32_t* __restrict__ camera_ids,
+                                                                        const int32_t* __restrict__ gaussian_ids,
+                                                                        int64_t nnz, int64_t B, int64_t C, int64_t N,
+                                                                        uint64_t* __restrict__ mask) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (e >= nnz) return;
+  const int64_t b = batch_ids ? batch_ids[e] : 0, c = camera_ids[e], n = gaussian_ids[e];
+  if (b < 0 || b >= B || c < 0 || c >= C || n < 0 || n >= N) return;  // ignored (the caller's ids are checked)
+  const int64_t idx = (b * C + c) * N + n;
+  atomicOr(reinterpret_cast<unsigned long long*>(mask) + (idx >> 6), 1ull << (idx & 63));
+}
+
+__global__ void __launch_bounds__(256) popcount_words_kernel(const uint64_t* __restrict__ mask, int64_t n_words,
+                                                             int32_t* __restrict__ counts) {
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (w < n_words) counts[w] = __popcll(mask[w]);
 }
 
 // Opacities of an activated projection without cameras.
@@ -295,6 +407,177 @@ extern "C" int gsplat_hip_projection_bwd(const float* means, const float* covars
                                     B, C, N, params, radii, conics, compensations, v_means2d, v_depths, v_conics,
                                     v_compensations, v_means, v_covars, v_quats, v_scales, v_viewmats, nullptr,
                                     nullptr, nullptr, workspace, workspace_bytes, stream);
+}
+
+// Packed layout workspace: [bit words | word prefixes | scan | view-matrix
+// partials (backward with v_viewmats)].
+static size_t align256(size_t b) { return (b + 255) / 256 * 256; }
+
+struct PackedLayout {
+  uint64_t* mask;
+  int32_t* prefix;
+  void* scan_ws;
+  float* partials;
+  int64_t n_words;
+};
+
+static size_t packed_layout(int64_t B, int64_t C, int64_t N, bool vm, PackedLayout* l, void* base) {
+  const int64_t total = B * C * N;
+  const int64_t nw = (total + 63) / 64;
+  const size_t mask_b = align256(static_cast<size_t>(nw) * 8);
+  const size_t pre_b = align256(static_cast<size_t>(nw) * 4);
+  const size_t scan_b = align256(scan_workspace_bytes(nw));
+  const size_t part_b = vm && C > 0 ? static_cast<size_t>(B * C) * grid_for(N, kProjBlock) * 12 * sizeof(float) : 0;
+  if (l && base) {
+    char* p = static_cast<char*>(base);
+    l->mask = reinterpret_cast<uint64_t*>(p);
+    l->prefix = reinterpret_cast<int32_t*>(p + mask_b);
+    l->scan_ws = p + mask_b + pre_b;
+    l->partials = part_b ? reinterpret_cast<float*>(p + mask_b + pre_b + scan_b) : nullptr;
+    l->n_words = nw;
+  }
+  return mask_b + pre_b + scan_b + part_b;
+}
+
+static int packed_args(const std::string& op, const float* means, const float* covars, const float* quats,
+                       const float* scales, const float* viewmats, const float* Ks, int64_t B, int64_t C, int64_t N,
+                       const gsplat_projection_params* params) {
+  if (!params) return invalid(op + ": null params.");
+  if (B < 0 || C < 0 || N < 0) return invalid(op + ": negative size.");
+  if (B * C * N > (static_cast<int64_t>(INT32_MAX) << 6)) return invalid(op + ": too many pairs.");
+  if (B * C * N == 0) return GSPLAT_OK;
+  if (!means || !viewmats || !Ks) return invalid(op + ": null pointer.");
+  if (params->use_covars ? !covars : (!quats || !scales)) return invalid(op + " expects covars or quats+scales.");
+  return GSPLAT_OK;
+}
+
+extern "C" size_t gsplat_hip_projection_packed_workspace_size(int64_t B, int64_t C, int64_t N, int32_t viewmats_grad) {
+  if (B <= 0 || C <= 0 || N <= 0) return 0;
+  return packed_layout(B, C, N, viewmats_grad != 0, nullptr, nullptr);
+}
+
+extern "C" int gsplat_hip_projection_packed_count(const float* means, const float* covars, const float* quats,
+                                                  const float* scales, const float* opacities, const float* viewmats,
+                                                  const float* Ks, int64_t B, int64_t C, int64_t N,
+                                                  const gsplat_projection_params* params, int64_t* nnz_dev,
+                                                  void* workspace, size_t workspace_bytes, void* stream) {
+  const std::string op("projection_ewa_3dgs_packed_forward");
+  int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
+  if (rc) return rc;
+  if (!nnz_dev) return invalid(op + ": null count.");
+  hipStream_t s = as_stream(stream);
+  if (B * C * N == 0) return fill_zero(nnz_dev, sizeof(int64_t), s);
+  if (params->use_opacities && !opacities) return invalid(op + ": null opacities.");
+  PackedLayout l;
+  if (!workspace || workspace_bytes < packed_layout(B, C, N, false, &l, workspace)) {
+    set_error(op + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  const int64_t total = B * C * N;
+  {
+    KernelTimer timer("projection_packed_count", s);
+    projection_packed_mask_kernel<<<grid_for(total, kProjBlock), kProjBlock, 0, s>>>(
+        means, covars, quats, scales, opacities, viewmats, Ks, C, N, total, *params, l.mask, l.prefix);
+  }
+  if ((rc = check_launch(op.c_str()))) return rc;
+  return scan_exclusive_i32(l.prefix, l.prefix, l.n_words, nnz_dev, l.scan_ws, s);
+}
+
+extern "C" int gsplat_hip_projection_packed_fwd(const float* means, const float* covars, const float* quats,
+                                                const float* scales, const float* opacities, const float* viewmats,
+                                                const float* Ks, int64_t B, int64_t C, int64_t N,
+                                                const gsplat_projection_params* params, int64_t nnz,
+                                                int32_t* batch_ids, int32_t* camera_ids, int32_t* gaussian_ids,
+                                                int32_t* indptr, int32_t* radii, float* means2d, float* depths,
+                                                float* conics, float* compensations, const void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+  const std::string op("projection_ewa_3dgs_packed_forward");
+  int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
+  if (rc) return rc;
+  if (nnz < 0) return invalid(op + ": negative nnz.");
+  hipStream_t s = as_stream(stream);
+  const int64_t total = B * C * N;
+  if (!indptr) return invalid(op + ": null indptr.");
+  if (total == 0) return fill_zero(indptr, (B * C + 1) * sizeof(int32_t), s);
+  if (nnz > 0 && (!batch_ids || !camera_ids || !gaussian_ids || !radii || !means2d || !depths || !conics))
+    return invalid(op + ": null pointer.");
+  if (nnz > 0 && params->calc_compensations && !compensations) return invalid(op + ": null compensations.");
+  if (params->use_opacities && !opacities) return invalid(op + ": null opacities.");
+  PackedLayout l;
+  if (!workspace || workspace_bytes < packed_layout(B, C, N, false, &l, const_cast<void*>(workspace))) {
+    set_error(op + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  {
+    KernelTimer timer("projection_packed_fwd", s);
+    if (nnz > 0)
+      projection_packed_write_kernel<<<grid_for(total, kProjBlock), kProjBlock, 0, s>>>(
+          means, covars, quats, scales, opacities, viewmats, Ks, C, N, total, *params, l.mask, l.prefix, nnz,
+          batch_ids, camera_ids, gaussian_ids, radii, means2d, depths, conics,
+          params->calc_compensations ? compensations : nullptr);
+    projection_packed_indptr_kernel<<<grid_for(B * C + 1, 256), 256, 0, s>>>(l.mask, l.prefix, B * C, N, nnz,
+                                                                             indptr);
+  }
+  return check_launch(op.c_str());
+}
+
+extern "C" int gsplat_hip_projection_packed_bwd(const float* means, const float* covars, const float* quats,
+                                                const float* scales, const float* viewmats, const float* Ks,
+                                                int64_t B, int64_t C, int64_t N,
+                                                const gsplat_projection_params* params, int64_t nnz,
+                                                const int32_t* batch_ids, const int32_t* camera_ids,
+                                                const int32_t* gaussian_ids, const float* conics,
+                                                const float* compensations, const float* v_means2d,
+                                                const float* v_depths, const float* v_conics,
+                                                const float* v_compensations, float* v_means, float* v_covars,
+                                                float* v_quats, float* v_scales, float* v_viewmats, void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+  const std::string op("projection_ewa_3dgs_packed_backward");
+  int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
+  if (rc) return rc;
+  const gsplat_projection_params& p = *params;
+  if (p.camera_model != 0) return invalid(op + " currently supports pinhole only.");
+  if (nnz < 0) return invalid(op + ": negative nnz.");
+  hipStream_t s = as_stream(stream);
+  if (B * N == 0) {
+    if (v_viewmats && B * C > 0) return fill_zero(v_viewmats, B * C * 16 * sizeof(float), s);
+    return GSPLAT_OK;
+  }
+  if (!v_means || (p.use_covars ? !v_covars : (!v_quats || !v_scales))) return invalid(op + ": null pointer.");
+  if (nnz > 0 && (!camera_ids || !gaussian_ids || !conics || !v_means2d || !v_conics))
+    return invalid(op + ": null pointer.");
+  if (nnz > 0 && B > 1 && !batch_ids) return invalid(op + ": null batch_ids with more than one batch.");
+  if (v_compensations && !compensations) return invalid(op + ": v_compensations without compensations.");
+  if (B > 65535) return invalid(op + ": batch exceeds 65535.");
+  PackedLayout l;
+  if (!workspace || workspace_bytes < packed_layout(B, C, N, v_viewmats != nullptr, &l, workspace)) {
+    set_error(op + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B));
+  {
+    KernelTimer timer("projection_packed_bwd", s);
+    if ((rc = fill_zero(l.mask, static_cast<size_t>(l.n_words) * 8, s))) return rc;
+    if (nnz > 0)
+      projection_packed_scatter_kernel<<<grid_for(nnz, 256), 256, 0, s>>>(batch_ids, camera_ids, gaussian_ids, nnz,
+                                                                           B, C, N, l.mask);
+    popcount_words_kernel<<<grid_for(l.n_words, 256), 256, 0, s>>>(l.mask, l.n_words, l.prefix);
+  }
+  if ((rc = check_launch(op.c_str()))) return rc;
+  if ((rc = scan_exclusive_i32(l.prefix, l.prefix, l.n_words, nullptr, l.scan_ws, s))) return rc;
+  {
+    KernelTimer timer("projection_packed_bwd", s);
+    launch_projection_bwd(false, grid, s, means, covars, quats, scales, viewmats, Ks, C, N, p, nullptr, conics,
+                          compensations, v_means2d, v_depths, v_conics, v_compensations, v_means, v_covars, v_quats,
+                          v_scales, v_viewmats ? l.partials : nullptr, nullptr, nullptr, nullptr, l.mask, l.prefix);
+  }
+  if ((rc = check_launch(op.c_str())) || !v_viewmats) return rc;
+  {
+    KernelTimer timer("projection_bwd_viewmats", s);
+    viewmat_reduce_kernel<<<static_cast<unsigned>(B * C), 256, 0, s>>>(l.partials, static_cast<int>(grid.x),
+                                                                       v_viewmats);
+  }
+  return check_launch(op.c_str());
 }
 
 extern "C" int gsplat_hip_activated_projection_fwd(const float* means, const float* quats, const float* log_scales,

@@ -155,7 +155,8 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     const float* __restrict__ v_depths, const float* __restrict__ v_conics,
     const float* __restrict__ v_compensations, float* __restrict__ v_means, float* __restrict__ v_covars,
     float* __restrict__ v_quats, float* __restrict__ v_scales, float* __restrict__ vm_partials,
-    const float* __restrict__ logits, const float* __restrict__ v_opac, float* __restrict__ v_logits) {
+    const float* __restrict__ logits, const float* __restrict__ v_opac, float* __restrict__ v_logits,
+    const uint64_t* __restrict__ pmask, const int32_t* __restrict__ pprefix) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
   const int64_t b = blockIdx.y;
   const bool in_range = n < N;
@@ -187,8 +188,21 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
 
   for (int64_t c = 0; c < C; ++c) {
     const int64_t cam = b * C + c;
-    const int64_t idx = cam * N + n;
-    const bool valid = in_range && radii[idx * 2] > 0 && radii[idx * 2 + 1] > 0;
+    int64_t idx = cam * N + n;
+    bool valid;
+    if (pmask) {
+      // packed layout: the pair's bit, and its row among the packed pairs
+      // (prefix of its 64-pair word + set bits below it)
+      valid = false;
+      if (in_range) {
+        const uint64_t w = pmask[idx >> 6];
+        const int bit = static_cast<int>(idx & 63);
+        valid = (w >> bit) & 1ull;
+        idx = static_cast<int64_t>(pprefix[idx >> 6]) + __popcll(w & ((1ull << bit) - 1ull));
+      }
+    } else {
+      valid = in_range && radii[idx * 2] > 0 && radii[idx * 2 + 1] > 0;
+    }
     float vm_part[12];
 #pragma unroll
     for (int i = 0; i < 12; ++i) vm_part[i] = 0.0f;
@@ -277,17 +291,19 @@ void launch_projection_bwd(bool act, dim3 grid, hipStream_t s, const float* mean
                            const float* compensations, const float* v_means2d, const float* v_depths,
                            const float* v_conics, const float* v_compensations, float* v_means, float* v_covars,
                            float* v_quats, float* v_scales, float* vm_partials, const float* logits,
-                           const float* v_opac, float* v_logits) {
+                           const float* v_opac, float* v_logits, const uint64_t* pmask,
+                           const int32_t* pprefix) {
   if (act)
     projection_bwd_kernel<true><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p, radii,
                                                             conics, compensations, v_means2d, v_depths, v_conics,
                                                             v_compensations, v_means, v_covars, v_quats, v_scales,
-                                                            vm_partials, logits, v_opac, v_logits);
+                                                            vm_partials, logits, v_opac, v_logits, pmask, pprefix);
   else
     projection_bwd_kernel<false><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p,
                                                              radii, conics, compensations, v_means2d, v_depths,
                                                              v_conics, v_compensations, v_means, v_covars, v_quats,
-                                                             v_scales, vm_partials, nullptr, nullptr, nullptr);
+                                                             v_scales, vm_partials, nullptr, nullptr, nullptr, pmask,
+                                                             pprefix);
 }
 
 }  // namespace gsplat_hip

@@ -13,14 +13,17 @@ namespace gsplat_hip {
 
 // Launches the projection backward kernel (projection_bwd.hip); arguments as
 // gsplat_hip_projection_bwd, plus the activated projection's opacity logits,
-// opacities' cotangent and logits' gradient (act).
+// opacities' cotangent and logits' gradient (act). With pmask / pprefix (the
+// packed layout's bit per pair and per-word prefix), radii is unused and the
+// per-pair arrays are read at the pair's packed row.
 void launch_projection_bwd(bool act, dim3 grid, hipStream_t s, const float* means, const float* covars,
                            const float* quats, const float* scales, const float* viewmats, const float* Ks, int64_t C,
                            int64_t N, const gsplat_projection_params& p, const int32_t* radii, const float* conics,
                            const float* compensations, const float* v_means2d, const float* v_depths,
                            const float* v_conics, const float* v_compensations, float* v_means, float* v_covars,
                            float* v_quats, float* v_scales, float* vm_partials, const float* logits,
-                           const float* v_opac, float* v_logits);
+                           const float* v_opac, float* v_logits, const uint64_t* pmask = nullptr,
+                           const int32_t* pprefix = nullptr);
 
 namespace {
 

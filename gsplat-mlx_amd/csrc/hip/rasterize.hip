@@ -50,6 +50,7 @@ struct RasterArgs {
   int W, H, ts, tw, th;
   int64_t I;
   int64_t n_isects;
+  int64_t G;  // Gaussian rows: I * N (dense) or nnz (packed)
 };
 
 // Range of the tile's list; the last tile of the last image ends at n_isects
@@ -66,11 +67,11 @@ __device__ __forceinline__ void tile_range(const RasterArgs& a, int64_t image, i
   *end = min(max(e, *start), a.n_isects);
 }
 
-// Gaussian record of list entry j; ids outside [0, I*N) read as a
+// Gaussian record of list entry j; ids outside [0, G) read as a
 // zero-opacity Gaussian (never contributes) instead of reading out of bounds.
 __device__ __forceinline__ int32_t load_gaussian(const RasterArgs& a, int64_t j, float2* xy, float4* co) {
   int32_t g = a.flatten_ids[j];
-  if (g < 0 || static_cast<int64_t>(g) >= a.I * a.N) {
+  if (g < 0 || static_cast<int64_t>(g) >= a.G) {
     *xy = make_float2(0.0f, 0.0f);
     *co = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     return 0;
@@ -1017,14 +1018,15 @@ int check_args(const RasterArgs& a, const char* what) {
 
 using namespace gsplat_hip;
 
-extern "C" int gsplat_hip_rasterize_fwd(const float* means2d, const float* conics, const float* colors,
-                                        const float* opacities, const float* backgrounds, const uint8_t* masks,
-                                        const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I, int64_t N,
-                                        int32_t channels, int32_t image_width, int32_t image_height, int32_t tile_size,
-                                        int32_t tile_width, int32_t tile_height, int64_t n_isects,
-                                        float* render_colors, float* render_alphas, int32_t* last_ids, void* stream) {
+static int rasterize_fwd_impl(const float* means2d, const float* conics, const float* colors,
+                              const float* opacities, const float* backgrounds, const uint8_t* masks,
+                              const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I, int64_t N,
+                              int64_t G, int32_t channels, int32_t image_width, int32_t image_height,
+                              int32_t tile_size, int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                              float* render_colors, float* render_alphas, int32_t* last_ids, void* stream) {
   RasterArgs a{means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, N, channels,
-               image_width, image_height, tile_size, tile_width, tile_height, I, n_isects};
+               image_width, image_height, tile_size, tile_width, tile_height, I, n_isects, G};
+  if (G < 0) return invalid("rasterize_to_pixels_3dgs_forward: invalid sizes.");
   int rc = check_args(a, "rasterize_to_pixels_3dgs_forward");
   if (rc) return rc;
   if (I == 0 || tile_width == 0 || tile_height == 0) return GSPLAT_OK;
@@ -1048,25 +1050,24 @@ extern "C" int gsplat_hip_rasterize_fwd(const float* means2d, const float* conic
   return check_launch("rasterize_to_pixels_3dgs_forward");
 }
 
-extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conics, const float* colors,
-                                        const float* opacities, const float* backgrounds, const uint8_t* masks,
-                                        const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I, int64_t N,
-                                        int32_t channels, int32_t image_width, int32_t image_height, int32_t tile_size,
-                                        int32_t tile_width, int32_t tile_height, int64_t n_isects,
-                                        const float* render_alphas, const int32_t* last_ids,
-                                        const float* v_render_colors, const float* v_render_alphas,
-                                        float* v_means2d_abs, float* v_means2d, float* v_conics, float* v_colors,
-                                        float* v_opacities, float* v_backgrounds, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
+static int rasterize_bwd_impl(const float* means2d, const float* conics, const float* colors,
+                              const float* opacities, const float* backgrounds, const uint8_t* masks,
+                              const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I, int64_t N,
+                              int64_t G, int32_t channels, int32_t image_width, int32_t image_height,
+                              int32_t tile_size, int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                              const float* render_alphas, const int32_t* last_ids, const float* v_render_colors,
+                              const float* v_render_alphas, float* v_means2d_abs, float* v_means2d,
+                              float* v_conics, float* v_colors, float* v_opacities, float* v_backgrounds,
+                              void* workspace, size_t workspace_bytes, void* stream) {
   RasterArgs a{means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, N, channels,
-               image_width, image_height, tile_size, tile_width, tile_height, I, n_isects};
+               image_width, image_height, tile_size, tile_width, tile_height, I, n_isects, G};
   int rc = check_args(a, "rasterize_to_pixels_3dgs_backward");
   if (rc) return rc;
+  if (G < 0) return invalid("rasterize_to_pixels_3dgs_backward: invalid sizes.");
   if (!v_means2d || !v_conics || !v_colors || !v_opacities)
     return invalid("rasterize_to_pixels_3dgs_backward: null pointer.");
   if (backgrounds && !v_backgrounds) return invalid("rasterize_to_pixels_3dgs_backward: null v_backgrounds.");
   hipStream_t s = as_stream(stream);
-  const int64_t G = I * N;
   // outputs are accumulated from zero; the schedule kernel clears them
   // (v_backgrounds is written whole by the order kernel)
   const ZeroSpan spans[] = {{v_means2d, G * 2},
@@ -1140,6 +1141,63 @@ extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conic
 #undef GSPLAT_BWD_ABS
 #undef GSPLAT_BWD_LAUNCH
   return check_launch("rasterize_to_pixels_3dgs_backward");
+}
+
+extern "C" int gsplat_hip_rasterize_fwd(const float* means2d, const float* conics, const float* colors,
+                                        const float* opacities, const float* backgrounds, const uint8_t* masks,
+                                        const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I, int64_t N,
+                                        int32_t channels, int32_t image_width, int32_t image_height, int32_t tile_size,
+                                        int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                        float* render_colors, float* render_alphas, int32_t* last_ids, void* stream) {
+  return rasterize_fwd_impl(means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, I, N,
+                            I * N, channels, image_width, image_height, tile_size, tile_width, tile_height, n_isects,
+                            render_colors, render_alphas, last_ids, stream);
+}
+
+extern "C" int gsplat_hip_rasterize_fwd_packed(const float* means2d, const float* conics, const float* colors,
+                                               const float* opacities, const float* backgrounds,
+                                               const uint8_t* masks, const int32_t* tile_offsets,
+                                               const int32_t* flatten_ids, int64_t I, int64_t nnz, int32_t channels,
+                                               int32_t image_width, int32_t image_height, int32_t tile_size,
+                                               int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                               float* render_colors, float* render_alphas, int32_t* last_ids,
+                                               void* stream) {
+  return rasterize_fwd_impl(means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, I, nnz,
+                            nnz, channels, image_width, image_height, tile_size, tile_width, tile_height, n_isects,
+                            render_colors, render_alphas, last_ids, stream);
+}
+
+extern "C" int gsplat_hip_rasterize_bwd(const float* means2d, const float* conics, const float* colors,
+                                        const float* opacities, const float* backgrounds, const uint8_t* masks,
+                                        const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I, int64_t N,
+                                        int32_t channels, int32_t image_width, int32_t image_height, int32_t tile_size,
+                                        int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                        const float* render_alphas, const int32_t* last_ids,
+                                        const float* v_render_colors, const float* v_render_alphas,
+                                        float* v_means2d_abs, float* v_means2d, float* v_conics, float* v_colors,
+                                        float* v_opacities, float* v_backgrounds, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+  return rasterize_bwd_impl(means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, I, N,
+                            I * N, channels, image_width, image_height, tile_size, tile_width, tile_height, n_isects,
+                            render_alphas, last_ids, v_render_colors, v_render_alphas, v_means2d_abs, v_means2d,
+                            v_conics, v_colors, v_opacities, v_backgrounds, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gsplat_hip_rasterize_bwd_packed(const float* means2d, const float* conics, const float* colors,
+                                               const float* opacities, const float* backgrounds,
+                                               const uint8_t* masks, const int32_t* tile_offsets,
+                                               const int32_t* flatten_ids, int64_t I, int64_t nnz, int32_t channels,
+                                               int32_t image_width, int32_t image_height, int32_t tile_size,
+                                               int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                               const float* render_alphas, const int32_t* last_ids,
+                                               const float* v_render_colors, const float* v_render_alphas,
+                                               float* v_means2d_abs, float* v_means2d, float* v_conics,
+                                               float* v_colors, float* v_opacities, float* v_backgrounds,
+                                               void* workspace, size_t workspace_bytes, void* stream) {
+  return rasterize_bwd_impl(means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, I, nnz,
+                            nnz, channels, image_width, image_height, tile_size, tile_width, tile_height, n_isects,
+                            render_alphas, last_ids, v_render_colors, v_render_alphas, v_means2d_abs, v_means2d,
+                            v_conics, v_colors, v_opacities, v_backgrounds, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t channels, int32_t tile_width,

@@ -128,6 +128,47 @@ int gsplat_hip_projection_bwd(const float* means, const float* covars, const flo
                               float* v_viewmats, void* workspace, size_t workspace_bytes,
                               void* stream);
 
+/* Packed layout: upstream gsplat's fully_fused_projection(packed=True)
+ * (projection_ewa_3dgs_packed_fwd/bwd, note/gsplat_cuda_source_map.md:273-315;
+ * the reference's intended projection_ewa_3dgs_packed_forward). Only the
+ * visible (camera, Gaussian) pairs are written, nnz of them, in the order of
+ * idx = (b * C + c) * N + n; each packed row equals the dense output at idx
+ * bit for bit.
+ *  count: computes every pair's visibility into the workspace and the count
+ *    nnz at *nnz_dev (device int64; the caller reads it to size the outputs).
+ *  fwd: with the same workspace, writes batch_ids, camera_ids, gaussian_ids
+ *    (int32 [nnz]), indptr [B*C + 1] (first packed row of each camera; the
+ *    last is nnz), radii [nnz,2], means2d [nnz,2], depths [nnz], conics
+ *    [nnz,3] and compensations [nnz] (calc_compensations, else NULL).
+ *  bwd: gradients from the packed cotangents (v_* [nnz, ...]); the packed ids
+ *    must be those of the forward (ascending idx, no repeats); batch_ids may
+ *    be NULL when B == 1. Outputs as gsplat_hip_projection_bwd, bit for bit
+ *    the dense backward with the cotangents scattered to their pairs.
+ * Workspace: gsplat_hip_projection_packed_workspace_size (3/16 byte per pair,
+ * plus the view-matrix partials when viewmats_grad). */
+size_t gsplat_hip_projection_packed_workspace_size(int64_t B, int64_t C, int64_t N, int32_t viewmats_grad);
+int gsplat_hip_projection_packed_count(const float* means, const float* covars, const float* quats,
+                                       const float* scales, const float* opacities, const float* viewmats,
+                                       const float* Ks, int64_t B, int64_t C, int64_t N,
+                                       const gsplat_projection_params* params, int64_t* nnz_dev, void* workspace,
+                                       size_t workspace_bytes, void* stream);
+int gsplat_hip_projection_packed_fwd(const float* means, const float* covars, const float* quats,
+                                     const float* scales, const float* opacities, const float* viewmats,
+                                     const float* Ks, int64_t B, int64_t C, int64_t N,
+                                     const gsplat_projection_params* params, int64_t nnz, int32_t* batch_ids,
+                                     int32_t* camera_ids, int32_t* gaussian_ids, int32_t* indptr, int32_t* radii,
+                                     float* means2d, float* depths, float* conics, float* compensations,
+                                     const void* workspace, size_t workspace_bytes, void* stream);
+int gsplat_hip_projection_packed_bwd(const float* means, const float* covars, const float* quats,
+                                     const float* scales, const float* viewmats, const float* Ks, int64_t B,
+                                     int64_t C, int64_t N, const gsplat_projection_params* params, int64_t nnz,
+                                     const int32_t* batch_ids, const int32_t* camera_ids,
+                                     const int32_t* gaussian_ids, const float* conics, const float* compensations,
+                                     const float* v_means2d, const float* v_depths, const float* v_conics,
+                                     const float* v_compensations, float* v_means, float* v_covars,
+                                     float* v_quats, float* v_scales, float* v_viewmats, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Real spherical harmonics, degrees 0..4.
  * Replaces GSPlatSphericalHarmonics(/Backward)::eval_gpu
@@ -278,6 +319,25 @@ int gsplat_hip_isect_encode_sorted_accutile(const float* means2d, const int32_t*
                                             int64_t* isect_ids, int32_t* flatten_ids, void* workspace,
                                             size_t workspace_bytes, void* stream);
 
+/* Packed layout (IntersectTileParams.packed, rejected by the reference at
+ * gsplat_intersect.cpp:115-118): nnz rows, row i in image image_ids[i]
+ * (int32, in [0, I)); flatten ids are row indices. With conics and
+ * opacities the ellipse tiles, else the AABB rect (both may be NULL). Counts
+ * from gsplat_hip_isect_count_scan(_accutile) over the nnz rows; for the
+ * sorted path, perm and offsets from gsplat_hip_isect_depth_order.
+ * Workspace as gsplat_hip_isect_encode_sorted. */
+int gsplat_hip_isect_encode_packed(const float* means2d, const int32_t* radii, const float* conics,
+                                   const float* opacities, const int32_t* image_ids, const float* depths,
+                                   const int32_t* offsets, int64_t I, int64_t nnz, int32_t tile_size,
+                                   int32_t tile_width, int32_t tile_height, int64_t n_isects, int64_t* isect_ids,
+                                   int32_t* flatten_ids, void* stream);
+int gsplat_hip_isect_encode_sorted_packed(const float* means2d, const int32_t* radii, const float* conics,
+                                          const float* opacities, const int32_t* image_ids, const float* depths,
+                                          const int32_t* perm, const int32_t* offsets, int64_t I, int64_t nnz,
+                                          int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                          int64_t n_isects, int64_t* isect_ids, int32_t* flatten_ids,
+                                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* Replaces GSPlatIntersectOffset::eval_gpu (gsplat_intersect.cpp:643-681):
  * offsets [I, tile_height, tile_width] = lower_bound of (image << tile_bits |
  * tile) over the sorted isect_ids >> 32. */
@@ -326,6 +386,29 @@ int gsplat_hip_rasterize_bwd(const float* means2d, const float* conics, const fl
  * reference, whose CPU backward allocates nothing of the kind. */
 size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t channels, int32_t tile_width,
                                                int32_t tile_height);
+
+/* Packed layout (RasterizeToPixels3DGSParams.packed, rejected by the
+ * reference at gsplat_rasterize.cpp:48-51): the Gaussian arrays have nnz rows
+ * (means2d [nnz,2], conics [nnz,3], colors [nnz,channels], opacities [nnz])
+ * and flatten_ids index them; images, backgrounds and masks are as dense
+ * ([I, ...], I from tile_offsets). Gradients have nnz rows. Otherwise as the
+ * dense entry points (same workspace). */
+int gsplat_hip_rasterize_fwd_packed(const float* means2d, const float* conics, const float* colors,
+                                    const float* opacities, const float* backgrounds, const uint8_t* masks,
+                                    const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I,
+                                    int64_t nnz, int32_t channels, int32_t image_width, int32_t image_height,
+                                    int32_t tile_size, int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                    float* render_colors, float* render_alphas, int32_t* last_ids, void* stream);
+int gsplat_hip_rasterize_bwd_packed(const float* means2d, const float* conics, const float* colors,
+                                    const float* opacities, const float* backgrounds, const uint8_t* masks,
+                                    const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I,
+                                    int64_t nnz, int32_t channels, int32_t image_width, int32_t image_height,
+                                    int32_t tile_size, int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                    const float* render_alphas, const int32_t* last_ids,
+                                    const float* v_render_colors, const float* v_render_alphas,
+                                    float* v_means2d_abs, float* v_means2d, float* v_conics, float* v_colors,
+                                    float* v_opacities, float* v_backgrounds, void* workspace,
+                                    size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Training-step glue around the chain, one kernel per direction. No

@@ -1251,6 +1251,41 @@ int oracle_isect_encode_accutile(const float* means2d, const int32_t* radii, con
   return 0;
 }
 
+// Packed-layout encode (IntersectTileParams.packed, which the reference
+// rejects at gsplat_intersect.cpp:115-118; upstream gsplat's isect_tiles with
+// image_ids): row idx of nnz belongs to image image_ids[idx] and its flatten
+// id is idx; tiles are the AABB rect's, or the ellipse rows when conics and
+// opacities are given. Otherwise the dense encode order.
+int oracle_isect_encode_packed(const float* means2d, const int32_t* radii, const float* conics,
+                               const float* opacities, const int32_t* image_ids, const float* depths,
+                               const int32_t* offsets, int64_t nnz, int tile_size, int tile_width, int tile_height,
+                               int64_t total, int64_t* isect_ids, int32_t* flatten_ids) {
+  const int tile_n_bits = floor_log2_plus_one(tile_width * tile_height);
+  for (int64_t idx = 0; idx < nnz; ++idx) {
+    EllipseRows e;
+    if (conics && opacities) {
+      e = ellipse_rows(means2d, radii, conics, opacities, idx, tile_size, tile_width, tile_height);
+    } else {
+      e.r = aabb_tile_rect(means2d[idx * 2], means2d[idx * 2 + 1], radii[idx * 2], radii[idx * 2 + 1], tile_size,
+                           tile_width, tile_height);
+      const int rows = std::max(e.r.max_y - e.r.min_y, 0);
+      e.c0.assign(rows, e.r.min_x);
+      e.c1.assign(rows, e.r.max_x);
+    }
+    int64_t o = offsets[idx];
+    for (size_t k = 0; k < e.c0.size(); ++k) {
+      const int ty = e.r.min_y + static_cast<int>(k);
+      for (int tx = e.c0[k]; tx < e.c1[k]; ++tx) {
+        if (o < 0 || o >= total) return -1;
+        isect_ids[o] = encode_isect_id(image_ids[idx], ty * tile_width + tx, depths[idx], tile_n_bits);
+        flatten_ids[o] = static_cast<int32_t>(idx);
+        ++o;
+      }
+    }
+  }
+  return 0;
+}
+
 // GSPlatIntersectOffset::eval_cpu, gsplat_intersect.cpp:605-641.
 void oracle_isect_offset(const int64_t* isect_ids, int64_t n_isects, int I, int tile_width,
                          int tile_height, int32_t* offsets) {

@@ -318,6 +318,55 @@ def isect_tile(means2d, radii, depths, I, tile_size, tile_width, tile_height, so
     return {"tiles_per_gauss": counts, "isect_ids": ids, "flatten_ids": fl}
 
 
+def isect_tile_packed(means2d, radii, depths, image_ids, I, tile_size, tile_width, tile_height, sort=True,
+                      conics=None, opacities=None):
+    """Packed layout: nnz rows, row i in image image_ids[i], flatten ids = rows; AABB or
+    (conics + opacities) ellipse tiles; count -> scan -> encode -> stable sort."""
+    m = _c(means2d, np.float32)
+    r = _c(radii, np.int32)
+    d = _c(depths, np.float32)
+    img = _c(image_ids, np.int32)
+    if conics is not None:
+        counts = isect_count_accutile(m, r, conics, opacities, tile_size, tile_width, tile_height)
+        co, op = _c(conics, np.float32), _c(opacities, np.float32)
+    else:
+        counts = isect_count(m, r, tile_size, tile_width, tile_height)
+        co = op = None
+    offsets, total = exclusive_scan(counts)
+    ids = np.zeros(total, np.int64)
+    fl = np.zeros(total, np.int32)
+    f = lib().oracle_isect_encode_packed
+    f.restype = ctypes.c_int
+    rc = f(_ptr(m), _ptr(r), _ptr(co), _ptr(op), _ptr(img), _ptr(d), _ptr(_c(offsets, np.int32)), I64(d.size),
+           tile_size, tile_width, tile_height, I64(total), _ptr(ids), _ptr(fl))
+    if rc != 0:
+        raise RuntimeError("intersect_tile_encode tile_offsets write out of bounds.")
+    if sort:
+        ids, fl = isect_sort(ids, fl)
+    return {"tiles_per_gauss": counts, "isect_ids": ids, "flatten_ids": fl}
+
+
+def projection_packed_forward(means, viewmats, Ks, W, H, **kw):
+    """Packed layout of the projection (upstream's fully_fused_projection(packed=True)):
+    the dense oracle's outputs at the visible pairs (both radii > 0), ordered by
+    (batch, camera, gaussian), with their ids and each camera's first row."""
+    e = projection_forward(means, viewmats, Ks, W, H, **kw)
+    radii = e["radii"]
+    vis = np.all(radii > 0, axis=-1)  # [..., C, N]
+    C, N = vis.shape[-2], vis.shape[-1]
+    flat = np.flatnonzero(vis.reshape(-1))
+    cam, n = flat // N, flat % N
+    counts = np.bincount(cam, minlength=vis.size // N)
+    out = {"batch_ids": (cam // C).astype(np.int32), "camera_ids": (cam % C).astype(np.int32),
+           "gaussian_ids": n.astype(np.int32),
+           "indptr": np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)}
+    for k in ("radii", "means2d", "depths", "conics", "compensations"):
+        if k in e and e[k] is not None and np.size(e[k]):
+            v = e[k]
+            out[k] = v.reshape((vis.size,) + v.shape[vis.ndim:])[flat]
+    return out
+
+
 def isect_offset(isect_ids, I, tile_width, tile_height):
     """gsplat_intersect.cpp:586-641."""
     k = _c(isect_ids, np.int64)

@@ -1,0 +1,194 @@
+"""GPU parity for the packed layout (upstream gsplat's packed=True path;
+rejected by the reference at gsplat_intersect.cpp:115-118 and
+gsplat_rasterize.cpp:48-51): the packed projection equals the dense one at
+the visible pairs bit for bit, and its backward equals the dense backward
+with the cotangents scattered (same kernel); the packed intersection is
+bit-exact with the oracle; the packed rasterizer renders what the dense one
+renders; the whole packed chain gives the dense chain's images and
+gradients."""
+import numpy as np
+import pytest
+from scipy.spatial.transform import Rotation
+
+from _helpers import assert_close_rel, dev, gsplat, host, projected_scene
+
+pytestmark = pytest.mark.gpu
+TS = 16
+
+
+def _scene(rng, B, C, N, W=320, H=240):
+    means = (rng.normal(size=(B, N, 3)) * [0.8, 0.6, 0.5] + [0, 0, 4.0]).astype(np.float32)
+    quats = rng.normal(size=(B, N, 4)).astype(np.float32)
+    scales = np.exp(rng.uniform(-4, -1.5, (B, N, 3))).astype(np.float32)
+    opac = rng.uniform(0.01, 1, (B, N)).astype(np.float32)
+    view = np.zeros((B, C, 4, 4), np.float32)
+    for b in range(B):
+        for c in range(C):
+            view[b, c, :3, :3] = Rotation.from_euler("xyz", rng.normal(scale=0.15, size=3)).as_matrix()
+            view[b, c, :3, 3] = rng.normal(scale=0.4, size=3)
+            view[b, c, 3, 3] = 1
+    Ks = np.zeros((B, C, 3, 3), np.float32)
+    Ks[..., 0, 0], Ks[..., 1, 1], Ks[..., 0, 2], Ks[..., 1, 2], Ks[..., 2, 2] = 300, 290, W / 2, H / 2, 1
+    return means, quats, scales, opac, view, Ks
+
+
+@pytest.mark.parametrize("B,C,N,opac,comp", [(1, 1, 1000, False, False), (1, 3, 777, True, False),
+                                             (2, 2, 3001, True, True), (1, 4, 64, False, True)])
+def test_projection_packed_equals_dense(oracle, B, C, N, opac, comp):
+    rng = np.random.default_rng(N)
+    means, quats, scales, op, view, Ks = _scene(rng, B, C, N)
+    g = gsplat()
+    inputs = {"means": dev(means), "quats": dev(quats), "scales": dev(scales), "viewmats": dev(view), "Ks": dev(Ks)}
+    if opac:
+        inputs["opacities"] = dev(op)
+    kw = dict(calc_compensations=comp)
+    print(f"packed projection B={B} C={C} N={N} opac={opac} comp={comp}", flush=True)
+    dn = g.projection_ewa_3dgs_fused_forward(inputs, 320, 240, **kw)
+    pk = g.projection_ewa_3dgs_packed_forward(inputs, 320, 240, **kw)
+    radii = host(dn["radii"])
+    vis = np.all(radii > 0, -1).reshape(-1)
+    flat = np.flatnonzero(vis)
+    nnz = flat.size
+    assert 0 < nnz < vis.size
+    cam = flat // N
+    np.testing.assert_array_equal(host(pk["batch_ids"]), cam // C)
+    np.testing.assert_array_equal(host(pk["camera_ids"]), cam % C)
+    np.testing.assert_array_equal(host(pk["gaussian_ids"]), flat % N)
+    np.testing.assert_array_equal(host(pk["indptr"]), np.concatenate([[0], np.cumsum(np.bincount(cam, minlength=B * C))]))
+    for k, w in (("radii", 2), ("means2d", 2), ("depths", 1), ("conics", 3)) + ((("compensations", 1),) if comp else ()):
+        d = host(dn[k]).reshape(vis.size, -1)[flat]
+        np.testing.assert_array_equal(host(pk[k]).reshape(nnz, -1), d, err_msg=k)
+    # the oracle's packed layout where both see the same visible pairs
+    e = oracle.projection_packed_forward(means, view, Ks, 320, 240, quats=quats, scales=scales,
+                                         opacities=op if opac else None, calc_compensations=comp)
+    if e["gaussian_ids"].size == nnz and (e["camera_ids"] == host(pk["camera_ids"])).all():
+        assert_close_rel(host(pk["conics"]), e["conics"], 1e-5, "conics")
+
+    # backward: the dense backward with the cotangents scattered to their pairs
+    rng2 = np.random.default_rng(1)
+    v_m2 = rng2.normal(size=(nnz, 2)).astype(np.float32)
+    v_d = rng2.normal(size=(nnz,)).astype(np.float32)
+    v_c = rng2.normal(size=(nnz, 3)).astype(np.float32)
+    cot_p = {"v_means2d": dev(v_m2), "v_depths": dev(v_d), "v_conics": dev(v_c)}
+    fwd_p = {"batch_ids": pk["batch_ids"], "camera_ids": pk["camera_ids"], "gaussian_ids": pk["gaussian_ids"],
+             "conics": pk["conics"]}
+    dense_cot = {}
+    for k, v, w in (("v_means2d", v_m2, 2), ("v_depths", v_d, 1), ("v_conics", v_c, 3)):
+        full = np.zeros((vis.size, w), np.float32)
+        full[flat] = v.reshape(nnz, w)
+        dense_cot[k] = dev(full.reshape(host(dn[k[2:]]).shape))
+    fwd_d = {"radii": dn["radii"], "conics": dn["conics"]}
+    if comp:
+        v_comp = rng2.normal(size=(nnz,)).astype(np.float32)
+        cot_p["v_compensations"] = dev(v_comp)
+        fwd_p["compensations"] = pk["compensations"]
+        full = np.zeros(vis.size, np.float32)
+        full[flat] = v_comp
+        dense_cot["v_compensations"] = dev(full.reshape(host(dn["compensations"]).shape))
+        fwd_d["compensations"] = dn["compensations"]
+    bp = g.projection_ewa_3dgs_packed_backward(inputs, fwd_p, cot_p, 320, 240, viewmats_requires_grad=True)
+    bd = g.projection_ewa_3dgs_fused_backward(inputs, fwd_d, dense_cot, 320, 240, viewmats_requires_grad=True)
+    for k in ("v_means", "v_quats", "v_scales", "v_viewmats"):
+        np.testing.assert_array_equal(host(bp[k]), host(bd[k]), err_msg=k)
+
+
+@pytest.mark.parametrize("accutile", [False, True])
+@pytest.mark.parametrize("sort", [False, True])
+def test_isect_packed_vs_oracle(oracle, accutile, sort):
+    rng = np.random.default_rng(17)
+    I, nnz, W, H = 4, 30000, 640, 480
+    means, radii, conics, opac, depths = (a[0] for a in projected_scene(rng, 1, nnz, W, H))
+    img = np.sort(rng.integers(0, I, nnz)).astype(np.int32)
+    tw, th = (W + TS - 1) // TS, (H + TS - 1) // TS
+    g = gsplat()
+    inp = {"means2d": dev(means), "radii": dev(radii), "depths": dev(depths), "image_ids": dev(img)}
+    kw = {}
+    if accutile:
+        inp["conics"], inp["opacities"] = dev(conics), dev(opac)
+        kw = {"conics": conics, "opacities": opac}
+    print(f"packed isect accutile={accutile} sort={sort}", flush=True)
+    out = g.intersect_tile_forward(inp, I, TS, tw, th, sort=sort)
+    ref = oracle.isect_tile_packed(means, radii, depths, img, I, TS, tw, th, sort=sort, **kw)
+    np.testing.assert_array_equal(host(out["tiles_per_gauss"]), ref["tiles_per_gauss"])
+    np.testing.assert_array_equal(host(out["isect_ids"]), ref["isect_ids"])
+    np.testing.assert_array_equal(host(out["flatten_ids"]), ref["flatten_ids"])
+    # int64 image ids (upstream's dtype) give the same lists
+    inp["image_ids"] = dev(img.astype(np.int64))
+    out2 = g.intersect_tile_forward(inp, I, TS, tw, th, sort=sort)
+    np.testing.assert_array_equal(host(out2["isect_ids"]), ref["isect_ids"])
+
+
+def _chain(g, torch, means, quats, scales, op, colors, view, Ks, W, H, packed, cot):
+    B, N = means.shape[0], means.shape[1]
+    C = view.shape[1]
+    params = [torch.from_numpy(a).cuda() for a in (means, quats, scales)]
+    inputs = {"means": params[0], "quats": params[1], "scales": params[2], "viewmats": dev(view), "Ks": dev(Ks)}
+    tw, th = (W + TS - 1) // TS, (H + TS - 1) // TS
+    if packed:
+        pr = g.projection_ewa_3dgs_packed_forward(inputs, W, H)
+        cid = pr["camera_ids"].long()
+        gid = pr["gaussian_ids"].long()
+        rows_op = dev(op)[0][gid]
+        rows_col = dev(colors)[0][gid]
+        it = g.intersect_tile_forward({"means2d": pr["means2d"], "radii": pr["radii"], "depths": pr["depths"],
+                                       "image_ids": pr["camera_ids"], "gaussian_ids": pr["gaussian_ids"]},
+                                      C, TS, tw, th)
+        m2, con, opr, colr = pr["means2d"], pr["conics"], rows_op, rows_col
+    else:
+        pr = g.projection_ewa_3dgs_fused_forward(inputs, W, H)
+        it = g.intersect_tile_forward({"means2d": pr["means2d"], "radii": pr["radii"], "depths": pr["depths"]},
+                                      C, TS, tw, th)
+        m2, con = pr["means2d"], pr["conics"]
+        opr = dev(op)[:, None].expand(-1, C, -1).contiguous()
+        colr = dev(colors)[:, None].expand(-1, C, -1, -1).contiguous()
+    offs = g.intersect_offset_forward(it["isect_ids"], C, tw, th)
+    rin = {"means2d": m2, "conics": con, "colors": colr, "opacities": opr, "tile_offsets": offs,
+           "flatten_ids": it["flatten_ids"]}
+    f = g.rasterize_to_pixels_3dgs_forward(rin, W, H, TS)
+    b = g.rasterize_to_pixels_3dgs_backward(rin, f, {"v_render_colors": dev(cot)}, W, H, TS, False)
+    fo = {"radii": pr["radii"], "conics": pr["conics"]}
+    if packed:
+        fo.update({"batch_ids": pr["batch_ids"], "camera_ids": pr["camera_ids"], "gaussian_ids": pr["gaussian_ids"]})
+        pb = g.projection_ewa_3dgs_packed_backward(inputs, fo, {"v_means2d": b["v_means2d"], "v_conics": b["v_conics"]},
+                                                   W, H)
+        v_op = torch.zeros((N,), device="cuda").index_add_(0, gid, b["v_opacities"])
+        v_col = torch.zeros((N, colors.shape[-1]), device="cuda").index_add_(0, gid, b["v_colors"])
+    else:
+        pb = g.projection_ewa_3dgs_fused_backward(inputs, fo, {"v_means2d": b["v_means2d"], "v_conics": b["v_conics"]},
+                                                  W, H)
+        v_op = b["v_opacities"].sum(1)[0]
+        v_col = b["v_colors"].sum(1)[0]
+    return f, {"v_means": pb["v_means"], "v_quats": pb["v_quats"], "v_scales": pb["v_scales"], "v_opac": v_op,
+               "v_colors": v_col}, it
+
+
+def test_packed_chain_equals_dense():
+    import torch
+
+    rng = np.random.default_rng(5)
+    B, C, N, W, H = 1, 3, 20000, 320, 240
+    means, quats, scales, op, view, Ks = _scene(rng, B, C, N, W, H)
+    colors = rng.uniform(0, 1, (B, N, 3)).astype(np.float32)
+    cot = rng.normal(size=(C, H, W, 3)).astype(np.float32)
+    g = gsplat()
+    fd, gd, itd = _chain(g, torch, means, quats, scales, op, colors, view, Ks, W, H, False, cot)
+    fp, gp, itp = _chain(g, torch, means, quats, scales, op, colors, view, Ks, W, H, True, cot)
+    print(f"dense entries {itd['isect_ids'].numel()}, packed {itp['isect_ids'].numel()}", flush=True)
+    np.testing.assert_array_equal(host(itp["isect_ids"]), host(itd["isect_ids"]))
+    np.testing.assert_array_equal(host(fp["render_colors"]), host(fd["render_colors"]))
+    np.testing.assert_array_equal(host(fp["render_alphas"]), host(fd["render_alphas"]))
+    for k in gd:
+        assert_close_rel(host(gp[k]), host(gd[k]), 1e-4, k)
+
+
+def test_packed_errors():
+    g = gsplat()
+    m = dev(np.zeros((3, 2), np.float32))
+    r = dev(np.ones((3, 2), np.int32))
+    d = dev(np.ones((3,), np.float32))
+    with pytest.raises(RuntimeError, match="image_ids"):
+        g.intersect_tile_forward({"means2d": m, "radii": r, "depths": d, "gaussian_ids": dev(np.arange(3))}, 1, TS, 4,
+                                 4)
+    with pytest.raises(RuntimeError, match="image_ids"):
+        g.intersect_tile_forward({"means2d": m, "radii": r, "depths": d, "image_ids": dev(np.zeros(2, np.int32))}, 1,
+                                 TS, 4, 4)
