@@ -50,6 +50,7 @@ def parse():
                     choices=["sh3_1m", "image_fit", "random_forward", "multiview_3m", "heavy_6m"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-accutile", action="store_true", help="skip the ellipse tile list variant")
+    ap.add_argument("--no-packed", action="store_true", help="skip the packed layout variant")
     ap.add_argument("--cpu-band-rows", type=int, default=0,
                     help="tile rows of the CPU rasterize sample (0: the whole image)")
     ap.add_argument("--cpu-repeats", type=int, default=3, help="CPU baseline runs (median per stage)")
@@ -135,13 +136,14 @@ def main():
     forward_only = target is None
     seed = torch.ones((), device=dev)
 
-    def step(accutile=False):
+    def step(accutile=False, packed=False):
         for p in params + [viewspace]:
             p.grad = None
         if sh:
             out = R.render_sh_model(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks,
                                     W, H, ts, scene.sh_degree, viewspace_points=viewspace,
-                                    background=scene.background, far_plane=scene.far_plane, accutile=accutile)
+                                    background=scene.background, far_plane=scene.far_plane, accutile=accutile,
+                                    packed=packed)
         else:
             out = R.render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, W, H, ts,
                                      background=scene.background,
@@ -296,6 +298,30 @@ def main():
                     "n_isects": M_a, "kernels_us_per_step": kern_a}
         log(f"[bench] accutile: {ms_a:.3f} ms/step, M={M_a} ({M_a / max(M, 1):.3f} of AABB)")
 
+    # The same step over the packed layout (per-pair arrays hold only the
+    # visible pairs; same images). Reported beside the headline.
+    packed = None
+    if sh and not args.no_packed:
+        for _ in range(args.warmup):
+            step(packed=True)
+        torch.cuda.synchronize()
+        tq = time.perf_counter()
+        for _ in range(args.steps):
+            out_p = step(packed=True)
+        torch.cuda.synchronize()
+        ms_p = 1000.0 * (time.perf_counter() - tq) / args.steps
+        prof.reset()
+        prof.enable(True)
+        for _ in range(args.steps):
+            out_p = step(packed=True)
+        torch.cuda.synchronize()
+        prof.enable(False)
+        kern_p = {k: round(ms / args.steps * 1000, 1) for k, (c, ms) in sorted(prof.report().items())}
+        nnz = int(out_p["camera_ids"].numel())
+        packed = {"ms_per_step": round(ms_p, 4), "value": round(mpix / (ms_p * 1e-3), 2), "unit": "Mpix/s",
+                  "nnz": nnz, "dense_pairs": N * n_img, "kernels_us_per_step": kern_p}
+        log(f"[bench] packed: {ms_p:.3f} ms/step, nnz={nnz} of {N * n_img} pairs")
+
     cpu = None
     if not args.no_cpu_baseline and n_img == 1:
         cpu = cpu_baseline(scene, args.cpu_band_rows, args.cpu_repeats, mpix)
@@ -322,6 +348,7 @@ def main():
         "cpu_baseline": cpu,
         "stages": stages,
         "accutile": accutile,
+        "packed": packed,
         "kernels_us_per_step": {k: round(v[1] * 1000, 1) for k, v in sorted(per_step.items())},
     }
     print(json.dumps(line), flush=True)

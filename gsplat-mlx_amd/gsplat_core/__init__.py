@@ -22,7 +22,9 @@ from .autograd import (  # noqa: E402,F401
     activated_projection,
     gaussian_activations,
     l1_loss,
+    packed_viewspace,
     projection_ewa_3dgs_fused,
+    projection_packed,
     quat_scale_to_covar_preci,
     rasterize_to_pixels_3dgs,
     sh_camera_colors,
@@ -50,10 +52,14 @@ __all__ = [
     "activated_projection_backward",
     "l1_loss_forward",
     "l1_loss_backward",
+    "projection_ewa_3dgs_packed_forward",
+    "projection_ewa_3dgs_packed_backward",
     "activated_projection",
     "gaussian_activations",
     "l1_loss",
     "projection_ewa_3dgs_fused",
+    "projection_packed",
+    "packed_viewspace",
     "quat_scale_to_covar_preci",
     "rasterize_to_pixels_3dgs",
     "sh_camera_colors",

@@ -136,6 +136,85 @@ def projection_ewa_3dgs_fused(means, viewmats, Ks, image_width, image_height, qu
             "viewspace_points": viewspace_points}
 
 
+class _ProjectionPacked(torch.autograd.Function):
+    """projection_ewa_3dgs_packed_forward / _backward (upstream gsplat's
+    fully_fused_projection(packed=True)); pinhole backward only."""
+
+    @staticmethod
+    def forward(ctx, means, quats, scales, viewmats, Ks, image_width, image_height, eps2d, near_plane, far_plane,
+                radius_clip, calc_compensations, camera_model):
+        ctx.set_materialize_grads(False)
+        inputs = {"means": means, "quats": quats, "scales": scales, "viewmats": viewmats, "Ks": Ks}
+        out = _C.projection_ewa_3dgs_packed_forward(inputs, image_width, image_height, eps2d, near_plane, far_plane,
+                                                    radius_clip, calc_compensations, camera_model)
+        ctx.save_for_backward(means, quats, scales, viewmats, Ks, out["batch_ids"], out["camera_ids"],
+                              out["gaussian_ids"], out["conics"], out["compensations"])
+        ctx.params = (image_width, image_height, eps2d, calc_compensations, camera_model)
+        for k in ("batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii"):
+            ctx.mark_non_differentiable(out[k])
+        return (out["batch_ids"], out["camera_ids"], out["gaussian_ids"], out["indptr"], out["radii"],
+                out["means2d"], out["depths"], out["conics"], out["compensations"])
+
+    @staticmethod
+    def backward(ctx, _b, _c, _g, _i, _r, v_means2d, v_depths, v_conics, v_compensations):
+        means, quats, scales, viewmats, Ks, bid, cid, gid, conics, comps = ctx.saved_tensors
+        W, H, eps2d, calc_comp, camera_model = ctx.params
+        if camera_model != 0:
+            raise RuntimeError("projection_ewa_3dgs_packed vjp currently supports pinhole only.")
+        nnz = cid.shape[0]
+        v_means2d = means.new_zeros((nnz, 2)) if v_means2d is None else v_means2d.contiguous()
+        v_conics = means.new_zeros((nnz, 3)) if v_conics is None else v_conics.contiguous()
+        inputs = {"means": means, "quats": quats, "scales": scales, "viewmats": viewmats, "Ks": Ks}
+        fwd = {"batch_ids": bid, "camera_ids": cid, "gaussian_ids": gid, "conics": conics}
+        cot = {"v_means2d": v_means2d, "v_conics": v_conics}
+        if v_depths is not None:
+            cot["v_depths"] = v_depths.contiguous()
+        if calc_comp:
+            fwd["compensations"] = comps
+            cot["v_compensations"] = torch.zeros_like(comps) if v_compensations is None else v_compensations.contiguous()
+        needs_viewmats = ctx.needs_input_grad[3]
+        out = _C.projection_ewa_3dgs_packed_backward(inputs, fwd, cot, W, H, eps2d, camera_model, needs_viewmats)
+        return (out["v_means"], out["v_quats"], out["v_scales"], out["v_viewmats"] if needs_viewmats else None,
+                None) + (None,) * 8
+
+
+def projection_packed(means, quats, scales, viewmats, Ks, image_width, image_height, eps2d=0.3, near_plane=0.01,
+                      far_plane=1e10, radius_clip=0.0, calc_compensations=False, camera_model=0):
+    """Packed projection: a dict of the visible pairs' rows (batch_ids,
+    camera_ids, gaussian_ids, indptr, radii, means2d, depths, conics,
+    compensations), differentiable w.r.t. means, quats, scales, viewmats."""
+    keys = ("batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii", "means2d", "depths", "conics",
+            "compensations")
+    out = _ProjectionPacked.apply(means, quats, scales, viewmats, Ks, image_width, image_height, eps2d, near_plane,
+                                  far_plane, radius_clip, calc_compensations, camera_model)
+    return dict(zip(keys, out))
+
+
+class _PackedViewspace(torch.autograd.Function):
+    """Identity on the packed means2d whose backward also scatters their
+    gradient into a dense viewspace_points [1, C, N, 2] proxy (the packed
+    counterpart of the dense projection's proxy gradient)."""
+
+    @staticmethod
+    def forward(ctx, means2d, viewspace_points, camera_ids, gaussian_ids):
+        ctx.save_for_backward(camera_ids, gaussian_ids)
+        ctx.shape = viewspace_points.shape
+        return means2d.view_as(means2d)
+
+    @staticmethod
+    def backward(ctx, g):
+        cid, gid = ctx.saved_tensors
+        vsp = None
+        if ctx.needs_input_grad[1] and g is not None:
+            vsp = g.new_zeros(ctx.shape)
+            vsp[0, cid.long(), gid.long()] = g
+        return g, vsp, None, None
+
+
+def packed_viewspace(means2d, viewspace_points, camera_ids, gaussian_ids):
+    return _PackedViewspace.apply(means2d, viewspace_points, camera_ids, gaussian_ids)
+
+
 class _SphericalHarmonics(torch.autograd.Function):
     @staticmethod
     def forward(ctx, degrees_to_use, dirs, coeffs, masks):

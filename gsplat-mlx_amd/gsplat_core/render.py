@@ -22,8 +22,9 @@ from __future__ import annotations
 import torch
 
 from . import _gsplat_core as _C
-from .autograd import (activated_projection, gaussian_activations, l1_loss as _l1_loss, projection_ewa_3dgs_fused,
-                       rasterize_to_pixels_3dgs, sh_camera_colors, spherical_harmonics)
+from .autograd import (activated_projection, gaussian_activations, l1_loss as _l1_loss, packed_viewspace,
+                       projection_ewa_3dgs_fused, projection_packed, rasterize_to_pixels_3dgs, sh_camera_colors,
+                       spherical_harmonics)
 
 
 def normalize_quats(quats: torch.Tensor) -> torch.Tensor:
@@ -99,13 +100,53 @@ def _per_image(opacities, background, n_images, device):
     return opacities[:, None].expand(-1, n_images, -1).contiguous(), bg.expand(n_images, -1)
 
 
+def _render_sh_packed(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks, width,
+                      height, tile_size, sh_degree, viewspace_points, background, far_plane, accutile):
+    """render_sh_model over the packed layout: only the visible (camera,
+    Gaussian) pairs are projected, intersected and rasterized."""
+    C = viewmats.shape[1]
+    N = means.shape[-2]
+    q, s, o = gaussian_activations(quats, log_scales, opacity_logits)
+    # queued before the projection, whose count read-back then waits on it
+    colors_all = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)  # [1, C, N, 3]
+    pr = projection_packed(means, q, s, viewmats, Ks, width, height, eps2d=0.3, near_plane=0.01, far_plane=far_plane)
+    cid, gid = pr["camera_ids"], pr["gaussian_ids"]
+    m2 = pr["means2d"]
+    if viewspace_points is not None:
+        m2 = packed_viewspace(m2, viewspace_points, cid, gid)
+    # index_select: its backward is an index_add (no sort of the indices)
+    gidl = gid.long()
+    opac = o.reshape(-1).index_select(0, gidl)
+    colors = colors_all.reshape(C * N, -1).index_select(0, cid.long() * N + gidl)
+    tw, th = tile_grid(width, height, tile_size)
+    inputs = {"means2d": m2.detach(), "radii": pr["radii"], "depths": pr["depths"].detach(), "image_ids": cid,
+              "gaussian_ids": gid}
+    if accutile:
+        inputs["conics"] = pr["conics"].detach()
+        inputs["opacities"] = opac.detach()
+    isect = _C.intersect_tile_forward(inputs, C, tile_size, tw, th, True, False)
+    offsets = _C.intersect_offset_forward(isect["isect_ids"], C, tw, th)
+    bg = background_tensor(background, means.device)
+    bg = bg if C == 1 else bg.expand(C, -1)
+    render = rasterize_to_pixels_3dgs(m2, pr["conics"], colors, opac, offsets, isect["flatten_ids"], width, height,
+                                      tile_size, backgrounds=bg)
+    return {**render, "radii": pr["radii"], "camera_ids": cid, "gaussian_ids": gid,
+            "tiles_per_gauss": isect["tiles_per_gauss"], "flatten_ids": isect["flatten_ids"],
+            "isect_ids": isect["isect_ids"], "tile_offsets": offsets}
+
+
 def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks, width,
                     height, tile_size, sh_degree, viewspace_points=None, background=(0.025, 0.025, 0.025),
-                    far_plane=100.0, accutile=False):
+                    far_plane=100.0, accutile=False, packed=False):
     """C cameras (viewmats [1, C, 4, 4]) rendered as C images of the same
     Gaussians; returns the render dict ([C, H, W, ...] images) plus radii,
     tiles_per_gauss and flatten_ids, like the reference. accutile: ellipse
-    tile lists (same images, fewer intersections)."""
+    tile lists (same images, fewer intersections). packed: the packed layout
+    (same images; per-pair arrays hold only the visible pairs)."""
+    if packed:
+        return _render_sh_packed(means, quats, log_scales, features_dc, features_rest, opacity_logits, viewmats, Ks,
+                                 width, height, tile_size, sh_degree, viewspace_points, background, far_plane,
+                                 accutile)
     C = viewmats.shape[1]
     # the parameter activations run inside the projection kernels
     proj = activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks, width, height,
