@@ -21,6 +21,28 @@ __device__ __forceinline__ void add_blur_vjp(float eps2d, const float cb[4], flo
 }
 
 // gsplat_projection.cpp:286-377
+// Orthographic camera: J = [[fx, 0, 0], [0, fy, 0]] is constant, so
+// v_cov3d = J^T v_cov2d J and v_mc += (fx v_mean2d.x, fy v_mean2d.y, 0)
+// (upstream gsplat's ortho_proj_vjp; the reference guards every non-pinhole
+// backward, gsplat_projection.cpp:157-160).
+__device__ __forceinline__ void ortho_proj_vjp(const CamFrame& f, const float v_cov2d[4], const float v_mean2d[2],
+                                               float v_mc[3], Mat3& v_cov3d) {
+  const float J[6] = {f.fx, 0.0f, 0.0f, 0.0f, f.fy, 0.0f};
+#pragma unroll
+  for (int a = 0; a < 3; ++a)
+#pragma unroll
+    for (int b = 0; b < 3; ++b) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc += J[r * 3 + a] * v_cov2d[r * 2 + c] * J[c * 3 + b];
+      v_cov3d.v[a * 3 + b] = acc;
+    }
+  v_mc[0] += f.fx * v_mean2d[0];
+  v_mc[1] += f.fy * v_mean2d[1];
+}
+
 __device__ __forceinline__ void persp_proj_vjp(const float mc[3], const Mat3& cov3d, const CamFrame& f, int width,
                                                int height, const float v_cov2d[4], const float v_mean2d[2],
                                                float v_mc[3], Mat3& v_cov3d) {
@@ -223,7 +245,10 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
       float v_mc[3] = {0.0f, 0.0f, v_depths ? v_depths[idx] : 0.0f};
       const float vm2[2] = {v_means2d[idx * 2], v_means2d[idx * 2 + 1]};
       Mat3 v_cc;
-      persp_proj_vjp(mc, cc, f, p.image_width, p.image_height, v_cov2d, vm2, v_mc, v_cc);
+      if (p.camera_model == 1)
+        ortho_proj_vjp(f, v_cov2d, vm2, v_mc, v_cc);
+      else
+        persp_proj_vjp(mc, cc, f, p.image_width, p.image_height, v_cov2d, vm2, v_mc, v_cc);
       const float* R = f.R.v;
 #pragma unroll
       for (int i = 0; i < 3; ++i) v_mw_total[i] += R[i] * v_mc[0] + R[3 + i] * v_mc[1] + R[6 + i] * v_mc[2];

@@ -408,6 +408,24 @@ void add_blur_vjp(T eps2d, const T* conic_blur, T compensation, T v_compensation
 }
 
 // gsplat_projection.cpp:286-377.
+// Orthographic camera (upstream gsplat's ortho_proj_vjp; the reference has
+// the forward only, its backward is guarded at gsplat_projection.cpp:157-160):
+// J = [[fx, 0, 0], [0, fy, 0]] does not depend on the mean, so
+// v_cov3d = J^T v_cov2d J and v_mean3d += (fx v_mean2d.x, fy v_mean2d.y, 0).
+template <typename T>
+void ortho_proj_vjp(T fx, T fy, const T* v_cov2d, const T* v_mean2d, T* v_mean3d, M3<T>& v_cov3d) {
+  const T J[6] = {fx, T(0), T(0), T(0), fy, T(0)};
+  for (int a = 0; a < 3; ++a)
+    for (int b = 0; b < 3; ++b) {
+      T acc = 0;
+      for (int r = 0; r < 2; ++r)
+        for (int c = 0; c < 2; ++c) acc += J[r * 3 + a] * v_cov2d[r * 2 + c] * J[c * 3 + b];
+      v_cov3d.v[a * 3 + b] = acc;
+    }
+  v_mean3d[0] += fx * v_mean2d[0];
+  v_mean3d[1] += fy * v_mean2d[1];
+}
+
 template <typename T>
 void persp_proj_vjp(const T* mean3d, const M3<T>& cov3d, T fx, T fy, T cx, T cy, int width,
                     int height, const T* v_cov2d, const T* v_mean2d, T* v_mean3d, M3<T>& v_cov3d) {
@@ -544,8 +562,11 @@ void proj_backward(const T* means, const T* covars, const T* quats, const T* sca
         const M3<T> cc = mul(mul(R, cw), tr(R));
         T v_mc[3] = {0, 0, v_depths[idx]};
         M3<T> v_cc = {};
-        persp_proj_vjp(mc, cc, K[0], K[4], K[2], K[5], p.image_width, p.image_height, v_cov2d,
-                       v_means2d + idx * 2, v_mc, v_cc);
+        if (p.camera_model == 1)
+          ortho_proj_vjp(K[0], K[4], v_cov2d, v_means2d + idx * 2, v_mc, v_cc);
+        else
+          persp_proj_vjp(mc, cc, K[0], K[4], K[2], K[5], p.image_width, p.image_height, v_cov2d,
+                         v_means2d + idx * 2, v_mc, v_cc);
         // pos_w2c_vjp / covar_w2c_vjp, gsplat_projection.cpp:379-402
         M3<T> v_R = {};
         T v_t[3] = {};

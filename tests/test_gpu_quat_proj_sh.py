@@ -146,13 +146,17 @@ def test_projection_known_answers_and_culling(oracle):
     np.testing.assert_array_equal(r, e["radii"][0, 0])
 
 
-@pytest.mark.parametrize("use_covars,calc_comp,C", [(False, False, 1), (False, True, 2), (True, True, 3)])
-def test_projection_backward_vs_oracle(oracle, use_covars, calc_comp, C):
+@pytest.mark.parametrize("use_covars,calc_comp,C,camera_model", [(False, False, 1, 0), (False, True, 2, 0),
+                                                                 (True, True, 3, 0), (False, True, 2, 1),
+                                                                 (True, False, 1, 1)])
+def test_projection_backward_vs_oracle(oracle, use_covars, calc_comp, C, camera_model):
     g = gsplat()
     rng = np.random.default_rng(7 + C)
     B, N = 1, 3000
     means, quats, scales, _, view, Ks = _scene(rng, B, C, N)
-    kw = dict(calc_compensations=calc_comp, near_plane=0.01, far_plane=100.0)
+    if camera_model == 1:  # orthographic: keep the means inside the 320x240 view
+        means[..., :2] *= 0.25
+    kw = dict(calc_compensations=calc_comp, near_plane=0.01, far_plane=100.0, camera_model=camera_model)
     cov = None
     if use_covars:
         cov, _ = oracle.quat_scale_to_covar_preci_forward(quats, scales, True, False, True)
@@ -175,18 +179,23 @@ def test_projection_backward_vs_oracle(oracle, use_covars, calc_comp, C):
     if calc_comp:
         fwd["compensations"] = dev(exp["compensations"])
         cot["v_compensations"] = dev(vcomp)
-    out = g.projection_ewa_3dgs_fused_backward(inputs, fwd, cot, 320, 240, viewmats_requires_grad=True)
+    out = g.projection_ewa_3dgs_fused_backward(inputs, fwd, cot, 320, 240, viewmats_requires_grad=True,
+                                               camera_model=camera_model)
     e = oracle.projection_backward(means, view, Ks, 320, 240, radii, exp["conics"], vm2, vd, vc, covars=cov,
                                    quats=None if use_covars else quats, scales=None if use_covars else scales,
                                    compensations=exp["compensations"] if calc_comp else None,
-                                   v_compensations=vcomp if calc_comp else None, viewmats_requires_grad=True)
+                                   v_compensations=vcomp if calc_comp else None, viewmats_requires_grad=True,
+                                   camera_model=camera_model)
+    assert (radii > 0).any(axis=-1).sum() > 1000
     for k in e:
         assert_close_rel(host(out[k]), e[k], GRAD_RTOL, k)
     # an absent v_depths means zeros
     cot0 = dict(cot, v_depths=dev(np.zeros_like(vd)))
     cot_absent = {k: v for k, v in cot.items() if k != "v_depths"}
-    a = g.projection_ewa_3dgs_fused_backward(inputs, fwd, cot0, 320, 240, viewmats_requires_grad=True)
-    b = g.projection_ewa_3dgs_fused_backward(inputs, fwd, cot_absent, 320, 240, viewmats_requires_grad=True)
+    a = g.projection_ewa_3dgs_fused_backward(inputs, fwd, cot0, 320, 240, viewmats_requires_grad=True,
+                                             camera_model=camera_model)
+    b = g.projection_ewa_3dgs_fused_backward(inputs, fwd, cot_absent, 320, 240, viewmats_requires_grad=True,
+                                             camera_model=camera_model)
     for k in a:
         np.testing.assert_allclose(host(b[k]), host(a[k]), rtol=1e-6, atol=1e-30, err_msg=k)
 
