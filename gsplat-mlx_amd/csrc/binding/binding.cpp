@@ -188,6 +188,20 @@ at::Tensor intersect_offset_forward(const at::Tensor& isect_ids, int I, int tile
   return gsplat_core::gsplat_intersect_offset(isect_ids, I, tile_width, tile_height);
 }
 
+// upstream gsplat's rasterize_to_indices_in_range (the reference's planned
+// rasterize_to_indices_3dgs_forward, note/gsplat_cuda_source_map.md:494-545)
+py::dict rasterize_to_indices_3dgs_forward(const TensorMap& inputs, int64_t range_start, int64_t range_end,
+                                           int image_width, int image_height, int tile_size) {
+  auto out = gsplat_core::gsplat_rasterize_to_indices_3dgs(
+      range_start, range_end, get_or_empty(inputs, "transmittances"), require_key(inputs, "means2d"),
+      require_key(inputs, "conics"), require_key(inputs, "opacities"), image_width, image_height, tile_size,
+      require_key(inputs, "tile_offsets"), require_key(inputs, "flatten_ids"));
+  py::dict r;
+  r["gaussian_ids"] = out[0];
+  r["indices"] = out[1];
+  return r;
+}
+
 py::dict rasterize_to_pixels_3dgs_forward(const TensorMap& inputs, int image_width, int image_height, int tile_size) {
   gsplat_core::RasterizeToPixels3DGSInput in;
   in.means2d = require_key(inputs, "means2d");
@@ -433,6 +447,9 @@ PYBIND11_MODULE(_gsplat_core, m) {
   m.def("projection_ewa_3dgs_packed_backward", &projection_ewa_3dgs_packed_backward, py::arg("inputs"),
         py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
         py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
+  m.def("rasterize_to_indices_3dgs_forward", &rasterize_to_indices_3dgs_forward, py::arg("inputs"),
+        py::arg("range_start"), py::arg("range_end"), py::arg("image_width"), py::arg("image_height"),
+        py::arg("tile_size") = 16);
   m.def("intersect_tile_forward", &intersect_tile_forward, py::arg("inputs"), py::arg("I"), py::arg("tile_size"),
         py::arg("tile_width"), py::arg("tile_height"), py::arg("sort") = true, py::arg("segmented") = false);
   m.def("intersect_offset_forward", &intersect_offset_forward, py::arg("isect_ids"), py::arg("I"),

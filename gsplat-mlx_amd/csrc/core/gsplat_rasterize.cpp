@@ -3,6 +3,8 @@
 // HIP C-ABI.
 #include "gsplat_rasterize.h"
 
+#include <hip/hip_runtime_api.h>
+
 #include <algorithm>
 
 #include "core_util.h"
@@ -182,6 +184,66 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPix
       p.use_backgrounds ? v_bg.data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(), ws_bytes,
       stream_for(input.s, means2d)));
   return {v_abs, v_m2, v_con, v_col, v_op, v_bg};
+}
+
+std::vector<array> gsplat_rasterize_to_indices_3dgs(int64_t range_start, int64_t range_end, const array& transmittances,
+                                                    const array& means2d_in, const array& conics_in,
+                                                    const array& opacities_in, int image_width, int image_height,
+                                                    int tile_size, const array& tile_offsets_in,
+                                                    const array& flatten_ids_in, StreamOrDevice s) {
+  for (const auto* a : {&means2d_in, &conics_in, &opacities_in, &tile_offsets_in, &flatten_ids_in})
+    require_device(*a, "rasterize_to_indices_3dgs input");
+  for (const array* a : {&means2d_in, &conics_in, &opacities_in})
+    require_dtype(*a, at::kFloat, "rasterize_to_indices_3dgs expects float32 means2d/conics/opacities.");
+  require_dtype(tile_offsets_in, at::kInt, "tile_offsets must be int32.");
+  require_dtype(flatten_ids_in, at::kInt, "flatten_ids must be int32.");
+  if (tile_offsets_in.dim() < 3) throw std::runtime_error("tile_offsets must have shape [..., tile_height, tile_width].");
+  if (means2d_in.size(-1) != 2 || conics_in.numel() != means2d_in.numel() / 2 * 3 ||
+      opacities_in.numel() != means2d_in.numel() / 2)
+    throw std::runtime_error("rasterize_to_indices_3dgs: means2d/conics/opacities shapes do not match.");
+  const int th = static_cast<int>(tile_offsets_in.size(-2)), tw = static_cast<int>(tile_offsets_in.size(-1));
+  const int64_t I = th * tw ? tile_offsets_in.numel() / (static_cast<int64_t>(th) * tw) : 0;
+  const int64_t n_pix = I * image_width * static_cast<int64_t>(image_height);
+  const bool use_t = !is_empty(transmittances);
+  if (use_t) {
+    require_device(transmittances, "transmittances");
+    if (transmittances.numel() != n_pix)
+      throw std::runtime_error("transmittances must have shape [..., image_height, image_width].");
+  }
+  const c10::DeviceGuard guard(means2d_in.device());
+  const array means2d = contig(means2d_in), conics = contig(conics_in), opac = contig(opacities_in);
+  const array offsets = contig(tile_offsets_in), flat = contig(flatten_ids_in);
+  const array trans = use_t ? contig(transmittances.to(at::kFloat)) : array();
+  void* stream = stream_for(s, means2d);
+  const int64_t n_rows = means2d.numel() / 2;
+  array starts = at::empty({std::max<int64_t>(n_pix, 1)}, i32_like(means2d));
+  array total = at::empty({1}, i64_like(means2d));
+  const size_t ws_bytes = gsplat_hip_rasterize_to_indices_workspace_size(I, image_width, image_height);
+  array ws = at::empty({static_cast<int64_t>(std::max<size_t>(ws_bytes, 1))}, u8_like(means2d));
+  const float* tp = use_t ? trans.data_ptr<float>() : nullptr;
+  check(gsplat_hip_rasterize_to_indices_count(range_start, range_end, tp, means2d.data_ptr<float>(),
+                                              conics.data_ptr<float>(), opac.data_ptr<float>(),
+                                              offsets.data_ptr<int32_t>(), flat.data_ptr<int32_t>(), I, n_rows,
+                                              image_width, image_height, tile_size, tw, th, flat.numel(),
+                                              starts.data_ptr<int32_t>(), total.data_ptr<int64_t>(),
+                                              ws.data_ptr<uint8_t>(), ws_bytes, stream));
+  int64_t m = 0;
+  const hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err = hipMemcpyAsync(&m, total.data_ptr<int64_t>(), sizeof(int64_t), hipMemcpyDeviceToHost, hs);
+  if (err == hipSuccess) err = hipStreamSynchronize(hs);
+  if (err != hipSuccess)
+    throw std::runtime_error(std::string("rasterize_to_indices_3dgs: reading the count failed: ") +
+                             hipGetErrorString(err));
+  if (m > static_cast<int64_t>(INT32_MAX)) throw std::runtime_error("rasterize_to_indices_3dgs: more than 2^31-1 entries.");
+  array gids = at::empty({m}, i32_like(means2d));
+  array idx = at::empty({m}, i64_like(means2d));
+  check(gsplat_hip_rasterize_to_indices_write(range_start, range_end, tp, means2d.data_ptr<float>(),
+                                              conics.data_ptr<float>(), opac.data_ptr<float>(),
+                                              offsets.data_ptr<int32_t>(), flat.data_ptr<int32_t>(), I, n_rows,
+                                              image_width, image_height, tile_size, tw, th, flat.numel(),
+                                              starts.data_ptr<int32_t>(), m, m ? gids.data_ptr<int32_t>() : nullptr,
+                                              m ? idx.data_ptr<int64_t>() : nullptr, stream));
+  return {gids, idx};
 }
 
 }  // namespace gsplat_core

@@ -65,4 +65,16 @@ std::vector<array> gsplat_rasterize_to_pixels_3dgs(const RasterizeToPixels3DGSIn
 
 std::vector<array> gsplat_rasterize_to_pixels_3dgs_backward(const RasterizeToPixels3DGSBackwardInput& input);
 
+// Rasterize to indices (upstream gsplat's rasterize_to_indices_in_range, the
+// reference's planned rasterize_to_indices_3dgs_forward): the (flatten id,
+// pixel index) pairs the forward composites for list positions
+// [range_start, range_end) of each tile, from the given transmittances
+// (empty: 1). Returns {gaussian_ids int32 [M], indices int64 [M]}; dense or
+// packed Gaussian arrays. Reads the count back to the host (one sync).
+std::vector<array> gsplat_rasterize_to_indices_3dgs(int64_t range_start, int64_t range_end, const array& transmittances,
+                                                    const array& means2d, const array& conics,
+                                                    const array& opacities, int image_width, int image_height,
+                                                    int tile_size, const array& tile_offsets,
+                                                    const array& flatten_ids, StreamOrDevice s = {});
+
 }  // namespace gsplat_core

@@ -1013,6 +1013,82 @@ int check_args(const RasterArgs& a, const char* what) {
   return GSPLAT_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Rasterize to indices (upstream gsplat's rasterize_to_indices_in_range,
+// note/gsplat_cuda_source_map.md:494-545; the reference's planned
+// rasterize_to_indices_3dgs_forward). Per pixel, starting from transmittance
+// T0 (1 without a transmittance image), the entries of its tile's list at
+// positions [range_start, range_end) that pass the forward's alpha test, in
+// list order, until the next transmittance would fall to 1e-4 -- the
+// forward's compositing rule with its alpha, threshold and exp, so the
+// entries are exactly those the forward composites. One block per tile, one
+// lane per pixel, records staged through LDS; pass 1 (WRITE false) counts
+// per pixel, pass 2 writes each pixel's entries at its scanned start:
+// gaussian id and the pixel's global index image * H * W + y * W + x.
+template <bool WRITE>
+__global__ void __launch_bounds__(1024) raster_indices_kernel(RasterArgs a, int64_t range_start, int64_t range_end,
+                                                              const float* __restrict__ transmittances,
+                                                              int32_t* __restrict__ counts,
+                                                              const int32_t* __restrict__ starts, int64_t n_out,
+                                                              int32_t* __restrict__ out_gauss,
+                                                              int64_t* __restrict__ out_index) {
+  __shared__ float4 s_co[1024];
+  __shared__ float2 s_xy[1024];
+  __shared__ int32_t s_g[1024];
+  const int tx = blockIdx.x, ty = blockIdx.y;
+  const int64_t image = blockIdx.z;
+  const int t = threadIdx.x;
+  const int bs = blockDim.x;
+  const int x = tx * a.ts + t % a.ts, y = ty * a.ts + t / a.ts;
+  const bool inside = t < a.ts * a.ts && x < a.W && y < a.H;
+  const int64_t pix = image * a.H * a.W + static_cast<int64_t>(y) * a.W + x;
+  int64_t s0, e0;
+  tile_range(a, image, ty * a.tw + tx, &s0, &e0);
+  const int64_t start = min(s0 + max<int64_t>(range_start, 0), e0);
+  const int64_t end = min(s0 + max<int64_t>(range_end, 0), e0);
+  const float px = static_cast<float>(x) + 0.5f, py = static_cast<float>(y) + 0.5f;
+  float T = inside && transmittances ? transmittances[pix] : 1.0f;
+  bool done = !inside;
+  int32_t cnt = 0;
+  int64_t pos = WRITE && inside ? starts[pix] : 0;
+  for (int64_t b = start; b < end; b += bs) {
+    if (__syncthreads_count(!done) == 0) break;
+    const int64_t j = b + t;
+    if (j < end) {
+      float2 xy;
+      float4 co;
+      s_g[t] = load_gaussian(a, j, &xy, &co);
+      s_xy[t] = xy;
+      s_co[t] = co;
+    }
+    __syncthreads();
+    const int n = static_cast<int>(min<int64_t>(bs, end - b));
+    for (int k = 0; k < n && !done; ++k) {
+      const float4 co = s_co[k];
+      const float dx = s_xy[k].x - px;
+      const float dy = s_xy[k].y - py;
+      const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
+      const float alpha = fminf(kMaxAlpha, co.w * exp_alpha(-sigma));
+      if (sigma < 0.0f || alpha < kAlphaThreshold) continue;
+      const float next_T = T * (1.0f - alpha);
+      if (next_T <= kTransmittanceThreshold) {
+        done = true;
+        break;
+      }
+      if constexpr (WRITE) {
+        if (pos < n_out) {
+          out_gauss[pos] = s_g[k];
+          out_index[pos] = pix;
+        }
+        ++pos;
+      }
+      ++cnt;
+      T = next_T;
+    }
+  }
+  if (!WRITE && inside) counts[pix] = cnt;
+}
+
 }  // namespace
 }  // namespace gsplat_hip
 
@@ -1198,6 +1274,82 @@ extern "C" int gsplat_hip_rasterize_bwd_packed(const float* means2d, const float
                             nnz, channels, image_width, image_height, tile_size, tile_width, tile_height, n_isects,
                             render_alphas, last_ids, v_render_colors, v_render_alphas, v_means2d_abs, v_means2d,
                             v_conics, v_colors, v_opacities, v_backgrounds, workspace, workspace_bytes, stream);
+}
+
+static int raster_indices_args(const char* what, const RasterArgs& a) {
+  int rc = check_args(a, what);
+  if (rc) return rc;
+  if (a.ts * a.ts > 1024) return invalid(std::string(what) + ": tile_size must be at most 32.");
+  if (a.I > 0 && a.tw > 0 && a.th > 0 && (!a.tile_offsets || (a.n_isects > 0 && !a.flatten_ids)))
+    return invalid(std::string(what) + ": null pointer.");
+  if (a.n_isects > 0 && (!a.means2d || !a.conics || !a.opacities)) return invalid(std::string(what) + ": null pointer.");
+  return GSPLAT_OK;
+}
+
+extern "C" size_t gsplat_hip_rasterize_to_indices_workspace_size(int64_t I, int32_t image_width,
+                                                                 int32_t image_height) {
+  return scan_workspace_bytes(I * image_width * static_cast<int64_t>(image_height));
+}
+
+extern "C" int gsplat_hip_rasterize_to_indices_count(int64_t range_start, int64_t range_end,
+                                                     const float* transmittances, const float* means2d,
+                                                     const float* conics, const float* opacities,
+                                                     const int32_t* tile_offsets, const int32_t* flatten_ids,
+                                                     int64_t I, int64_t n_rows, int32_t image_width,
+                                                     int32_t image_height, int32_t tile_size, int32_t tile_width,
+                                                     int32_t tile_height, int64_t n_isects, int32_t* starts,
+                                                     int64_t* total_dev, void* workspace, size_t workspace_bytes,
+                                                     void* stream) {
+  const char* what = "rasterize_to_indices_3dgs";
+  RasterArgs a{means2d, conics, nullptr, opacities, nullptr, nullptr, tile_offsets, flatten_ids, n_rows, 1,
+               image_width, image_height, tile_size, tile_width, tile_height, I, n_isects, n_rows};
+  int rc = raster_indices_args(what, a);
+  if (rc) return rc;
+  if (!total_dev) return invalid(std::string(what) + ": null total.");
+  hipStream_t s = as_stream(stream);
+  const int64_t n_pix = I * image_width * static_cast<int64_t>(image_height);
+  if (n_pix == 0 || tile_width == 0 || tile_height == 0) return fill_zero(total_dev, sizeof(int64_t), s);
+  if (!starts) return invalid(std::string(what) + ": null pointer.");
+  if (!workspace || workspace_bytes < scan_workspace_bytes(n_pix)) {
+    set_error(std::string(what) + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  const int bs = (tile_size * tile_size + kWave - 1) / kWave * kWave;
+  {
+    KernelTimer timer("raster_indices", s);
+    raster_indices_kernel<false><<<dim3(tile_width, tile_height, static_cast<unsigned>(I)), bs, 0, s>>>(
+        a, range_start, range_end, transmittances, starts, nullptr, 0, nullptr, nullptr);
+  }
+  if ((rc = check_launch(what))) return rc;
+  return scan_exclusive_i32(starts, starts, n_pix, total_dev, workspace, s);
+}
+
+extern "C" int gsplat_hip_rasterize_to_indices_write(int64_t range_start, int64_t range_end,
+                                                     const float* transmittances, const float* means2d,
+                                                     const float* conics, const float* opacities,
+                                                     const int32_t* tile_offsets, const int32_t* flatten_ids,
+                                                     int64_t I, int64_t n_rows, int32_t image_width,
+                                                     int32_t image_height, int32_t tile_size, int32_t tile_width,
+                                                     int32_t tile_height, int64_t n_isects, const int32_t* starts,
+                                                     int64_t n_out, int32_t* out_gauss_ids, int64_t* out_indices,
+                                                     void* stream) {
+  const char* what = "rasterize_to_indices_3dgs";
+  RasterArgs a{means2d, conics, nullptr, opacities, nullptr, nullptr, tile_offsets, flatten_ids, n_rows, 1,
+               image_width, image_height, tile_size, tile_width, tile_height, I, n_isects, n_rows};
+  int rc = raster_indices_args(what, a);
+  if (rc) return rc;
+  if (n_out < 0) return invalid(std::string(what) + ": negative output size.");
+  const int64_t n_pix = I * image_width * static_cast<int64_t>(image_height);
+  if (n_pix == 0 || tile_width == 0 || tile_height == 0 || n_out == 0) return GSPLAT_OK;
+  if (!starts || !out_gauss_ids || !out_indices) return invalid(std::string(what) + ": null pointer.");
+  hipStream_t s = as_stream(stream);
+  const int bs = (tile_size * tile_size + kWave - 1) / kWave * kWave;
+  {
+    KernelTimer timer("raster_indices", s);
+    raster_indices_kernel<true><<<dim3(tile_width, tile_height, static_cast<unsigned>(I)), bs, 0, s>>>(
+        a, range_start, range_end, transmittances, nullptr, starts, n_out, out_gauss_ids, out_indices);
+  }
+  return check_launch(what);
 }
 
 extern "C" size_t gsplat_hip_rasterize_bwd_workspace_size(int64_t I, int32_t channels, int32_t tile_width,

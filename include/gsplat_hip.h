@@ -410,6 +410,33 @@ int gsplat_hip_rasterize_bwd_packed(const float* means2d, const float* conics, c
                                     float* v_opacities, float* v_backgrounds, void* workspace,
                                     size_t workspace_bytes, void* stream);
 
+/* Rasterize to indices: upstream gsplat's rasterize_to_indices_in_range
+ * (note/gsplat_cuda_source_map.md:494-545; the reference's planned
+ * rasterize_to_indices_3dgs_forward). For each pixel, starting from
+ * transmittances[pixel] (NULL: 1), the entries of its tile's list at
+ * positions [range_start, range_end) that the forward would composite (alpha
+ * test passed, in list order, until the transmittance would fall to 1e-4).
+ * Gaussian arrays have n_rows rows (I * N dense, nnz packed); masks are not
+ * taken. count: per-pixel counts scanned into starts [I*H*W] (exclusive) and
+ * the total at *total_dev (device int64; the caller reads it back); write:
+ * out_gauss_ids [n_out] (flatten ids) and out_indices [n_out] (image * H * W +
+ * y * W + x), pixel-major, list order within a pixel. */
+size_t gsplat_hip_rasterize_to_indices_workspace_size(int64_t I, int32_t image_width, int32_t image_height);
+int gsplat_hip_rasterize_to_indices_count(int64_t range_start, int64_t range_end, const float* transmittances,
+                                          const float* means2d, const float* conics, const float* opacities,
+                                          const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I,
+                                          int64_t n_rows, int32_t image_width, int32_t image_height,
+                                          int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                          int64_t n_isects, int32_t* starts, int64_t* total_dev, void* workspace,
+                                          size_t workspace_bytes, void* stream);
+int gsplat_hip_rasterize_to_indices_write(int64_t range_start, int64_t range_end, const float* transmittances,
+                                          const float* means2d, const float* conics, const float* opacities,
+                                          const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I,
+                                          int64_t n_rows, int32_t image_width, int32_t image_height,
+                                          int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                          int64_t n_isects, const int32_t* starts, int64_t n_out,
+                                          int32_t* out_gauss_ids, int64_t* out_indices, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Training-step glue around the chain, one kernel per direction. No
  * counterpart operator in the reference: these replace the framework

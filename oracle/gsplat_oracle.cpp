@@ -1307,6 +1307,53 @@ int oracle_isect_encode_packed(const float* means2d, const int32_t* radii, const
   return 0;
 }
 
+// rasterize_to_indices (upstream gsplat's rasterize_to_indices_in_range,
+// note/gsplat_cuda_source_map.md:494-545; not in the reference): per pixel,
+// from transmittances[pix] (NULL: 1), the entries at list positions
+// [range_start, range_end) of its tile that the float32 forward loop above
+// composites (same alpha, threshold and stopping rule), in list order.
+// counts (pass 1) or, with starts, gauss_ids / indices (pass 2).
+void oracle_raster_indices(int64_t range_start, int64_t range_end, const float* transmittances,
+                           const float* means2d, const float* conics, const float* opacities,
+                           const int32_t* tile_offsets, const int32_t* flatten_ids, int64_t I, int W, int H,
+                           int tile_size, int tile_width, int tile_height, int64_t n_isects, int32_t* counts,
+                           const int32_t* starts, int32_t* gauss_ids, int64_t* indices) {
+  const int64_t n_tiles = static_cast<int64_t>(tile_width) * tile_height;
+  for (int64_t image = 0; image < I; ++image)
+    for (int y = 0; y < H; ++y)
+      for (int x = 0; x < W; ++x) {
+        const int64_t tile = (y / tile_size) * tile_width + (x / tile_size);
+        const int64_t oi = image * n_tiles + tile;
+        const int64_t t0 = tile_offsets[oi];
+        const int64_t t1 = (oi + 1 == I * n_tiles) ? n_isects : tile_offsets[oi + 1];
+        const int64_t start = std::min(t0 + range_start, t1), end = std::min(t0 + range_end, t1);
+        const int64_t pix = (image * H + y) * W + x;
+        const float px = static_cast<float>(x) + 0.5f, py = static_cast<float>(y) + 0.5f;
+        float Tr = transmittances ? transmittances[pix] : 1.0f;
+        int64_t pos = starts ? starts[pix] : 0;
+        int32_t cnt = 0;
+        for (int64_t idx = start; idx < end; ++idx) {
+          const int64_t g = flatten_ids[idx];
+          const float dx = means2d[g * 2] - px;
+          const float dy = means2d[g * 2 + 1] - py;
+          const float c0 = conics[g * 3], c1 = conics[g * 3 + 1], c2 = conics[g * 3 + 2];
+          const float sigma = 0.5f * (c0 * dx * dx + c2 * dy * dy) + c1 * dx * dy;
+          const float alpha = std::min(kMaxAlpha, opacities[g] * std::exp(-sigma));
+          if (sigma < 0.0f || alpha < kAlphaThreshold) continue;
+          const float next_T = Tr * (1.0f - alpha);
+          if (next_T <= kTransmittanceThreshold) break;
+          if (starts) {
+            gauss_ids[pos] = static_cast<int32_t>(g);
+            indices[pos] = pix;
+            ++pos;
+          }
+          ++cnt;
+          Tr = next_T;
+        }
+        if (counts) counts[pix] = cnt;
+      }
+}
+
 // GSPlatIntersectOffset::eval_cpu, gsplat_intersect.cpp:605-641.
 void oracle_isect_offset(const int64_t* isect_ids, int64_t n_isects, int I, int tile_width,
                          int tile_height, int32_t* offsets) {

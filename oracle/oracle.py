@@ -376,6 +376,28 @@ def isect_offset(isect_ids, I, tile_width, tile_height):
 
 
 # ------------------------------------------------------------- rasterize
+def raster_indices(means2d, conics, opacities, tile_offsets, flatten_ids, image_width, image_height, tile_size,
+                   range_start=0, range_end=2**40, transmittances=None):
+    """rasterize_to_indices: (gaussian_ids int32 [M], indices int64 [M]), pixel-major."""
+    to = _c(tile_offsets, np.int32)
+    th, tw = to.shape[-2], to.shape[-1]
+    I = to.size // (th * tw)
+    m, co, op = _c(means2d, np.float32), _c(conics, np.float32), _c(opacities, np.float32)
+    fl = _c(flatten_ids, np.int32)
+    tr = _c(transmittances, np.float32) if transmittances is not None else None
+    n_pix = I * image_width * image_height
+    counts = np.zeros(n_pix, np.int32)
+    f = lib().oracle_raster_indices
+    args = (I64(range_start), I64(range_end), _ptr(tr), _ptr(m), _ptr(co), _ptr(op), _ptr(to), _ptr(fl), I64(I),
+            image_width, image_height, tile_size, tw, th, I64(fl.size))
+    f(*args, _ptr(counts), None, None, None)
+    starts, total = exclusive_scan(counts)
+    gids = np.zeros(total, np.int32)
+    idx = np.zeros(total, np.int64)
+    f(*args, None, _ptr(starts), _ptr(gids), _ptr(idx))
+    return gids, idx
+
+
 def _raster_dims(means2d, colors, tile_offsets):
     th, tw = tile_offsets.shape[-2], tile_offsets.shape[-1]
     I = tile_offsets.size // (th * tw)

@@ -190,3 +190,28 @@ def test_non_finite_values_stay_local(oracle):
         bad = ~np.isfinite(e)
         assert bad.any() and (~bad).mean() > 0.9, k
         assert_close_rel(np.where(bad, 0, a), np.where(bad, 0, e), GRAD_RTOL, k)
+
+
+@pytest.mark.parametrize("I,N,W,H,ts,chunk", [(1, 2000, 200, 150, 16, None), (2, 3000, 131, 97, 16, 37),
+                                               (1, 1500, 96, 64, 8, None)])
+def test_rasterize_to_indices_vs_oracle(oracle, I, N, W, H, ts, chunk):
+    """rasterize_to_indices_3dgs: the (gaussian, pixel) lists bit-exact with
+    the oracle, for the full range and for a range chunk from carried
+    transmittances."""
+    rng = np.random.default_rng(N)
+    s = make_scene(oracle, rng, I, N, W, H, ts, 3)
+    g = gsplat()
+    inp = {"means2d": dev(s["means2d"]), "conics": dev(s["conics"]), "opacities": dev(s["opacities"]),
+           "tile_offsets": dev(s["tile_offsets"]), "flatten_ids": dev(s["flatten_ids"])}
+    r0, r1 = (0, 2**40) if chunk is None else (chunk, 2 * chunk)
+    trans = None
+    if chunk is not None:
+        trans = rng.uniform(0.2, 1.0, (I, H, W)).astype(np.float32)
+        inp["transmittances"] = dev(trans)
+    print(f"raster indices I={I} N={N} {W}x{H} ts={ts} chunk={chunk}", flush=True)
+    out = g.rasterize_to_indices_3dgs_forward(inp, r0, r1, W, H, ts)
+    eg, ei = oracle.raster_indices(s["means2d"], s["conics"], s["opacities"], s["tile_offsets"], s["flatten_ids"],
+                                   W, H, ts, range_start=r0, range_end=r1, transmittances=trans)
+    assert ei.size > 1000
+    np.testing.assert_array_equal(host(out["indices"]), ei)
+    np.testing.assert_array_equal(host(out["gaussian_ids"]), eg)
