@@ -429,6 +429,12 @@ at::Tensor dummy_array_add(const py::dict& inputs) {
 
 }  // namespace
 
+// upstream gsplat's selective_adam_update (in place)
+void selective_adam_update(at::Tensor param, const at::Tensor& param_grad, at::Tensor exp_avg, at::Tensor exp_avg_sq,
+                           const at::Tensor& valid, double lr, double b1, double b2, double eps, int64_t step) {
+  gsplat_core::gsplat_selective_adam_update(param, param_grad, exp_avg, exp_avg_sq, valid, lr, b1, b2, eps, step);
+}
+
 PYBIND11_MODULE(_gsplat_core, m) {
   m.doc() = "MI355X (gfx950) splatting operator chain with the gsplat_core binding surface.";
   m.def("dummy_add", &dummy_add, py::arg("a"), py::arg("b"));
@@ -450,6 +456,9 @@ PYBIND11_MODULE(_gsplat_core, m) {
   m.def("rasterize_to_indices_3dgs_forward", &rasterize_to_indices_3dgs_forward, py::arg("inputs"),
         py::arg("range_start"), py::arg("range_end"), py::arg("image_width"), py::arg("image_height"),
         py::arg("tile_size") = 16);
+  m.def("selective_adam_update", &selective_adam_update, py::arg("param"), py::arg("param_grad"),
+        py::arg("exp_avg"), py::arg("exp_avg_sq"), py::arg("valid"), py::arg("lr"), py::arg("b1") = 0.9,
+        py::arg("b2") = 0.999, py::arg("eps") = 1e-8, py::arg("step") = 0);
   m.def("intersect_tile_forward", &intersect_tile_forward, py::arg("inputs"), py::arg("I"), py::arg("tile_size"),
         py::arg("tile_width"), py::arg("tile_height"), py::arg("sort") = true, py::arg("segmented") = false);
   m.def("intersect_offset_forward", &intersect_offset_forward, py::arg("isect_ids"), py::arg("I"),

@@ -2,6 +2,8 @@
 // is the HIP C-ABI (training_glue.hip).
 #include "gsplat_training_glue.h"
 
+#include <cmath>
+
 #include "core_util.h"
 
 namespace gsplat_core {
@@ -112,6 +114,34 @@ std::vector<array> gsplat_l1_loss_backward(const array& a_in, const array& b_in,
   check(gsplat_hip_l1_loss_bwd(a.data_ptr<float>(), b.data_ptr<float>(), a.numel(), g.data_ptr<float>(),
                                va.data_ptr<float>(), vb.data_ptr<float>(), stream_for(s, a)));
   return {va, vb};
+}
+
+void gsplat_selective_adam_update(array& param, const array& grad, array& exp_avg, array& exp_avg_sq,
+                                  const array& valid, double lr, double b1, double b2, double eps, int64_t step,
+                                  StreamOrDevice s) {
+  for (const array* a : {static_cast<const array*>(&param), &grad, static_cast<const array*>(&exp_avg),
+                         static_cast<const array*>(&exp_avg_sq)})
+    require_f32(*a, "selective_adam tensor");
+  if (grad.sizes() != param.sizes() || exp_avg.sizes() != param.sizes() || exp_avg_sq.sizes() != param.sizes())
+    throw std::runtime_error("selective_adam: param, grad and moments must have one shape.");
+  if (!param.is_contiguous() || !exp_avg.is_contiguous() || !exp_avg_sq.is_contiguous())
+    throw std::runtime_error("selective_adam: param and moments are updated in place and must be contiguous.");
+  const int64_t n = param.dim() ? param.size(0) : 1;
+  const int64_t D = n ? param.numel() / n : 0;
+  const bool use_valid = !is_empty(valid);
+  if (use_valid) {
+    require_device(valid, "valid");
+    if (valid.numel() != n) throw std::runtime_error("selective_adam: valid must have one flag per row.");
+  }
+  const c10::DeviceGuard guard(param.device());
+  const array g = contig(grad);
+  const array vmask = use_valid ? contig(valid.to(at::kByte)) : array();
+  const double bc1 = step > 0 ? 1.0 - std::pow(b1, static_cast<double>(step)) : 1.0;
+  const double bc2 = step > 0 ? std::sqrt(1.0 - std::pow(b2, static_cast<double>(step))) : 1.0;
+  check(gsplat_hip_selective_adam(param.data_ptr<float>(), g.data_ptr<float>(), exp_avg.data_ptr<float>(),
+                                  exp_avg_sq.data_ptr<float>(), use_valid ? vmask.data_ptr<uint8_t>() : nullptr, n,
+                                  D, lr, b1, b2, eps, bc1, bc2,
+                                  stream_for(s, param)));
 }
 
 }  // namespace gsplat_core

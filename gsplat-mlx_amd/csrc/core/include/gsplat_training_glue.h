@@ -45,4 +45,12 @@ array gsplat_l1_loss_forward(const array& a, const array& b, StreamOrDevice s = 
 // device cotangent g.
 std::vector<array> gsplat_l1_loss_backward(const array& a, const array& b, const array& grad, StreamOrDevice s = {});
 
+// Selective Adam step in place (upstream gsplat's selective_adam_update): the
+// rows (first dimension) of param with valid != 0 (valid empty: all) take
+// torch.optim.Adam's step number `step` (step <= 0: no bias correction, as
+// upstream's kernel); the other rows and their moments are unchanged.
+void gsplat_selective_adam_update(array& param, const array& grad, array& exp_avg, array& exp_avg_sq,
+                                  const array& valid, double lr, double b1, double b2, double eps, int64_t step,
+                                  StreamOrDevice s = {});
+
 }  // namespace gsplat_core

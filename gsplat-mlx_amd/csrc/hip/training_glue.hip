@@ -147,6 +147,32 @@ __global__ void __launch_bounds__(kGlueBlock) l1_bwd_kernel(const float* __restr
   if (v_b) v_b[i] = -v;
 }
 
+// Selective Adam (upstream gsplat's fused selective_adam_update,
+// note/gsplat_cuda_source_map.md:575-577): one lane per value; rows whose
+// valid flag is 0 keep their parameter and moments. Adam in torch's form:
+// m = b1 m + (1 - b1) g, v = b2 v + (1 - b2) g^2,
+// p -= (lr / bc1) m / (sqrt(v) / bc2_sqrt + eps); bc1 = bc2_sqrt = 1 gives
+// upstream's uncorrected update. The host forms 1 - b1, 1 - b2 and lr / bc1
+// in double, as torch does from its Python-float hyperparameters.
+__global__ void __launch_bounds__(kGlueBlock) selective_adam_kernel(float* __restrict__ param,
+                                                                    const float* __restrict__ grad,
+                                                                    float* __restrict__ exp_avg,
+                                                                    float* __restrict__ exp_avg_sq,
+                                                                    const uint8_t* __restrict__ valid, int64_t n,
+                                                                    int64_t D, float step_size, float b1,
+                                                                    float omb1, float b2, float omb2, float eps,
+                                                                    float bc2_sqrt) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kGlueBlock + threadIdx.x;
+  if (i >= n * D) return;
+  if (valid && !valid[i / D]) return;
+  const float g = grad[i];
+  const float m = b1 * exp_avg[i] + omb1 * g;
+  const float v = b2 * exp_avg_sq[i] + omb2 * (g * g);
+  exp_avg[i] = m;
+  exp_avg_sq[i] = v;
+  param[i] = param[i] - step_size * (m / (sqrtf(v) / bc2_sqrt + eps));
+}
+
 }  // namespace
 }  // namespace gsplat_hip
 
@@ -228,4 +254,24 @@ extern "C" int gsplat_hip_l1_loss_bwd(const float* a, const float* b, int64_t n,
     l1_bwd_kernel<<<grid_for(n, kGlueBlock), kGlueBlock, 0, s>>>(a, b, n, grad, v_a, v_b);
   }
   return check_launch("l1_loss_backward");
+}
+
+extern "C" int gsplat_hip_selective_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq,
+                                         const uint8_t* valid, int64_t n, int64_t D, double lr, double b1, double b2,
+                                         double eps, double bias_correction1, double bias_correction2_sqrt,
+                                         void* stream) {
+  if (n < 0 || D < 0) return invalid("selective_adam: negative size.");
+  if (n * D == 0) return GSPLAT_OK;
+  if (!param || !grad || !exp_avg || !exp_avg_sq) return invalid("selective_adam: null pointer.");
+  if (!(bias_correction1 > 0.0) || !(bias_correction2_sqrt > 0.0))
+    return invalid("selective_adam: bias corrections must be positive.");
+  hipStream_t s = as_stream(stream);
+  {
+    KernelTimer timer("selective_adam", s);
+    selective_adam_kernel<<<grid_for(n * D, kGlueBlock), kGlueBlock, 0, s>>>(
+        param, grad, exp_avg, exp_avg_sq, valid, n, D, static_cast<float>(lr / bias_correction1),
+        static_cast<float>(b1), static_cast<float>(1.0 - b1), static_cast<float>(b2), static_cast<float>(1.0 - b2),
+        static_cast<float>(eps), static_cast<float>(bias_correction2_sqrt));
+  }
+  return check_launch("selective_adam");
 }

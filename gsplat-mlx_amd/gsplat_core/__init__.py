@@ -54,6 +54,8 @@ __all__ = [
     "l1_loss_backward",
     "projection_ewa_3dgs_packed_forward",
     "projection_ewa_3dgs_packed_backward",
+    "rasterize_to_indices_3dgs_forward",
+    "selective_adam_update",
     "activated_projection",
     "gaussian_activations",
     "l1_loss",

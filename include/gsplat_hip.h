@@ -497,6 +497,20 @@ int gsplat_hip_l1_loss_fwd(const float* a, const float* b, int64_t n, float* los
 int gsplat_hip_l1_loss_bwd(const float* a, const float* b, int64_t n, const float* grad, float* v_a,
                            float* v_b, void* stream);
 
+/* Selective Adam: upstream gsplat's fused selective_adam_update
+ * (note/gsplat_cuda_source_map.md:575-577), the optimizer step after the
+ * VJPs. In place over n rows of D values (param, grad, exp_avg, exp_avg_sq
+ * [n, D]); rows with valid[row] == 0 are left unchanged (valid NULL: all
+ * rows). m = b1 m + (1 - b1) g; v = b2 v + (1 - b2) g^2;
+ * param -= (lr / bias_correction1) m / (sqrt(v) / bias_correction2_sqrt + eps)
+ * -- torch.optim.Adam's step with bias_correction1 = 1 - b1^t and
+ * bias_correction2_sqrt = sqrt(1 - b2^t); 1 and 1 give upstream's form. The
+ * scalars are double: 1 - b1, 1 - b2 and lr / bias_correction1 are formed in
+ * double and rounded once, as torch forms them from Python floats. */
+int gsplat_hip_selective_adam(float* param, const float* grad, float* exp_avg, float* exp_avg_sq,
+                              const uint8_t* valid, int64_t n, int64_t D, double lr, double b1, double b2,
+                              double eps, double bias_correction1, double bias_correction2_sqrt, void* stream);
+
 #ifdef __cplusplus
 }  /* extern "C" */
 #endif

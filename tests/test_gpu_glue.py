@@ -204,3 +204,51 @@ def test_activated_projection_c_abi_and_errors():
     assert_close_rel(host(opac), 1.0 / (1.0 + np.exp(-lo.astype(np.float64))), 1e-6, "opacities")
     p.use_covars = 1
     assert f(*args) != 0  # covars are not an activated input
+
+
+def test_selective_adam_vs_torch_adam():
+    """selective_adam_update (upstream gsplat's fused selective Adam) against
+    torch.optim.Adam, an independent implementation: three steps with every
+    row valid, then a masked step that must leave invalid rows untouched."""
+    import torch
+
+    g = gsplat()
+    rng = np.random.default_rng(0)
+    n, D = 100003, 3
+    p0 = rng.normal(size=(n, D)).astype(np.float32)
+    grads = [rng.normal(size=(n, D)).astype(np.float32) for _ in range(4)]
+    ref = torch.nn.Parameter(torch.from_numpy(p0.copy()).cuda())
+    opt = torch.optim.Adam([ref], lr=1e-3, betas=(0.9, 0.999), eps=1e-8)
+    p = torch.from_numpy(p0.copy()).cuda()
+    m = torch.zeros_like(p)
+    v = torch.zeros_like(p)
+    for step in range(1, 4):
+        ref.grad = torch.from_numpy(grads[step - 1]).cuda()
+        opt.step()
+        g._gsplat_core.selective_adam_update(p, ref.grad, m, v, torch.empty(0, device="cuda"), 1e-3, 0.9, 0.999, 1e-8,
+                                            step)
+        st = opt.state[ref]
+        # torch updates the first moment as a lerp (m + (1 - b1)(g - m)),
+        # upstream as b1 m + (1 - b1) g: last-bit differences that grow where
+        # g - m cancels, so the bound is relative 2e-5 with an absolute floor
+        for got, exp, name in ((p, ref.detach(), "param"), (m, st["exp_avg"], "exp_avg"),
+                               (v, st["exp_avg_sq"], "exp_avg_sq")):
+            e = host(exp)
+            np.testing.assert_allclose(host(got), e, rtol=2e-5, atol=1e-6 * np.abs(e).max(),
+                                       err_msg=f"{name} step {step}")
+    valid = torch.from_numpy(rng.random(n) < 0.5).cuda()
+    before = [host(t).copy() for t in (p, m, v)]
+    ref.grad = torch.from_numpy(grads[3]).cuda()
+    opt.step()
+    g._gsplat_core.selective_adam_update(p, ref.grad, m, v, valid, 1e-3, 0.9, 0.999, 1e-8, 4)
+    vm = host(valid)
+    for got, old in zip((p, m, v), before):
+        np.testing.assert_array_equal(host(got)[~vm], old[~vm])
+    e = host(ref.detach())[vm]
+    np.testing.assert_allclose(host(p)[vm], e, rtol=2e-5, atol=1e-6 * np.abs(e).max(), err_msg="masked step")
+    # step 0: upstream's uncorrected form p -= lr m / (sqrt(v) + eps)
+    q = torch.zeros((5, 2), device="cuda")
+    gq = torch.ones((5, 2), device="cuda")
+    mq, vq = torch.zeros_like(q), torch.zeros_like(q)
+    g._gsplat_core.selective_adam_update(q, gq, mq, vq, torch.empty(0, device="cuda"), 0.1, 0.9, 0.999, 1e-8, 0)
+    np.testing.assert_allclose(host(q), -0.1 * 0.1 / (np.sqrt(0.001) + 1e-8), rtol=1e-6)
