@@ -163,8 +163,8 @@ std::vector<array> projection_backward_impl(const ProjectionEWA3DGSFusedBackward
   fwd.Ks = input.Ks;
   fwd.params = input.params;
   validate_inputs(fwd);
-  if (input.params.camera_model != 0 && input.params.camera_model != 1)
-    throw std::runtime_error("projection_ewa_3dgs_fused_backward currently supports pinhole and orthographic cameras only.");
+  if (input.params.camera_model < 0 || input.params.camera_model > 2)
+    throw std::runtime_error("projection_ewa_3dgs_fused_backward: unknown camera model.");
   if (input.radii.scalar_type() != at::kInt) throw std::runtime_error("radii must be int32.");
   // an empty v_depths stands for zeros (callers whose loss ignores depths)
   const bool use_v_depths = !is_empty(input.v_depths);
@@ -334,8 +334,8 @@ std::vector<array> gsplat_projection_ewa_3dgs_packed_backward(const ProjectionEW
   fwd.Ks = input.Ks;
   fwd.params = input.params;
   validate_inputs(fwd);
-  if (input.params.camera_model != 0 && input.params.camera_model != 1)
-    throw std::runtime_error("projection_ewa_3dgs_packed_backward currently supports pinhole and orthographic cameras only.");
+  if (input.params.camera_model < 0 || input.params.camera_model > 2)
+    throw std::runtime_error("projection_ewa_3dgs_packed_backward: unknown camera model.");
   require_device(input.means, "means");
   require_device(input.viewmats, "viewmats");
   require_device(input.Ks, "Ks");

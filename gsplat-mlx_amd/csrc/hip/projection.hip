@@ -336,8 +336,7 @@ int projection_bwd_impl(const char* what, const float* means, const float* covar
   const std::string op(what);
   if (!params) return invalid(op + ": null params.");
   const gsplat_projection_params& p = *params;
-  if (p.camera_model != 0 && p.camera_model != 1)
-    return invalid(op + " currently supports pinhole and orthographic cameras only.");
+  if (p.camera_model < 0 || p.camera_model > 2) return invalid(op + ": unknown camera model.");
   if (B < 0 || C < 0 || N < 0) return invalid(op + ": negative size.");
   if (ACT && p.use_covars) return invalid(op + ": the activated projection takes quats and log-scales, not covars.");
   if (ACT && v_logits && !logits) return invalid(op + ": v_opacity_logits requested without opacity logits.");
@@ -537,8 +536,7 @@ extern "C" int gsplat_hip_projection_packed_bwd(const float* means, const float*
   int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
   if (rc) return rc;
   const gsplat_projection_params& p = *params;
-  if (p.camera_model != 0 && p.camera_model != 1)
-    return invalid(op + " currently supports pinhole and orthographic cameras only.");
+  if (p.camera_model < 0 || p.camera_model > 2) return invalid(op + ": unknown camera model.");
   if (nnz < 0) return invalid(op + ": negative nnz.");
   hipStream_t s = as_stream(stream);
   if (B * N == 0) {

@@ -43,6 +43,98 @@ __device__ __forceinline__ void ortho_proj_vjp(const CamFrame& f, const float v_
   v_mc[1] += f.fy * v_mean2d[1];
 }
 
+// Equidistant fisheye (upstream gsplat's fisheye_proj_vjp; the reference has
+// the forward only, camera_jacobian): the mean's image point and the EWA
+// Jacobian J are nonlinear in the camera-space mean, so their derivatives
+// are carried as forward-mode dual numbers through the forward's own
+// formulas (value + d/dx, d/dy, d/dz), which differentiates exactly what the
+// forward computes, eps terms included.
+struct Dual3 {
+  float v, d[3];
+};
+__device__ __forceinline__ Dual3 dconst(float c) { return {c, {0.0f, 0.0f, 0.0f}}; }
+__device__ __forceinline__ Dual3 operator+(const Dual3& a, const Dual3& b) {
+  return {a.v + b.v, {a.d[0] + b.d[0], a.d[1] + b.d[1], a.d[2] + b.d[2]}};
+}
+__device__ __forceinline__ Dual3 operator-(const Dual3& a, const Dual3& b) {
+  return {a.v - b.v, {a.d[0] - b.d[0], a.d[1] - b.d[1], a.d[2] - b.d[2]}};
+}
+__device__ __forceinline__ Dual3 operator*(const Dual3& a, const Dual3& b) {
+  return {a.v * b.v, {a.d[0] * b.v + a.v * b.d[0], a.d[1] * b.v + a.v * b.d[1], a.d[2] * b.v + a.v * b.d[2]}};
+}
+__device__ __forceinline__ Dual3 operator/(const Dual3& a, const Dual3& b) {
+  const float q = a.v / b.v;
+  return {q, {(a.d[0] - q * b.d[0]) / b.v, (a.d[1] - q * b.d[1]) / b.v, (a.d[2] - q * b.d[2]) / b.v}};
+}
+__device__ __forceinline__ Dual3 dsqrt(const Dual3& a) {
+  const float r = sqrtf(a.v);
+  const float k = 0.5f / r;
+  return {r, {a.d[0] * k, a.d[1] * k, a.d[2] * k}};
+}
+// atan2(u, w): d = (w du - u dw) / (u^2 + w^2)
+__device__ __forceinline__ Dual3 datan2(const Dual3& u, const Dual3& w) {
+  const float den = u.v * u.v + w.v * w.v;
+  Dual3 o;
+  o.v = atan2f(u.v, w.v);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) o.d[k] = (w.v * u.d[k] - u.v * w.d[k]) / den;
+  return o;
+}
+
+__device__ __forceinline__ void fisheye_proj_vjp(const float mc[3], const Mat3& cov3d, const CamFrame& f,
+                                                 const float v_cov2d[4], const float v_mean2d[2], float v_mc[3],
+                                                 Mat3& v_cov3d) {
+  const Dual3 x = {mc[0], {1.0f, 0.0f, 0.0f}}, y = {mc[1], {0.0f, 1.0f, 0.0f}}, z = {mc[2], {0.0f, 0.0f, 1.0f}};
+  const Dual3 eps = dconst(0.0000001f), fx = dconst(f.fx), fy = dconst(f.fy);
+  const Dual3 xy_len = dsqrt(x * x + y * y) + eps;
+  const Dual3 theta = datan2(xy_len, z + eps);
+  const Dual3 m2x = x * fx * theta / xy_len;
+  const Dual3 m2y = y * fy * theta / xy_len;
+  const Dual3 x2 = x * x + eps, y2 = y * y, xy = x * y;
+  const Dual3 x2y2 = x2 + y2;
+  const Dual3 inv = dconst(1.0f) / (x2y2 + z * z);
+  const Dual3 b = datan2(xy_len, z) / xy_len / x2y2;
+  const Dual3 a = z * inv / x2y2;
+  const Dual3 Jd[6] = {fx * (x2 * a + y2 * b), fx * xy * (a - b), dconst(0.0f) - fx * x * inv,
+                       fy * xy * (a - b),      fy * (y2 * a + x2 * b), dconst(0.0f) - fy * y * inv};
+  float J[6];
+#pragma unroll
+  for (int i = 0; i < 6; ++i) J[i] = Jd[i].v;
+#pragma unroll
+  for (int ia = 0; ia < 3; ++ia)
+#pragma unroll
+    for (int ib = 0; ib < 3; ++ib) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int c = 0; c < 2; ++c) acc += J[r * 3 + ia] * v_cov2d[r * 2 + c] * J[c * 3 + ib];
+      v_cov3d.v[ia * 3 + ib] = acc;
+    }
+  float v_J[6];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+#pragma unroll
+    for (int ia = 0; ia < 3; ++ia) {
+      float left = 0.0f, right = 0.0f;
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int ib = 0; ib < 3; ++ib) {
+          left += v_cov2d[r * 2 + c] * J[c * 3 + ib] * cov3d.v[ia * 3 + ib];
+          right += v_cov2d[c * 2 + r] * J[c * 3 + ib] * cov3d.v[ib * 3 + ia];
+        }
+      v_J[r * 3 + ia] = left + right;
+    }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    float acc = v_mean2d[0] * m2x.d[k] + v_mean2d[1] * m2y.d[k];
+#pragma unroll
+    for (int i = 0; i < 6; ++i) acc += v_J[i] * Jd[i].d[k];
+    v_mc[k] += acc;
+  }
+}
+
 __device__ __forceinline__ void persp_proj_vjp(const float mc[3], const Mat3& cov3d, const CamFrame& f, int width,
                                                int height, const float v_cov2d[4], const float v_mean2d[2],
                                                float v_mc[3], Mat3& v_cov3d) {
@@ -247,6 +339,8 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
       Mat3 v_cc;
       if (p.camera_model == 1)
         ortho_proj_vjp(f, v_cov2d, vm2, v_mc, v_cc);
+      else if (p.camera_model == 2)
+        fisheye_proj_vjp(mc, cc, f, v_cov2d, vm2, v_mc, v_cc);
       else
         persp_proj_vjp(mc, cc, f, p.image_width, p.image_height, v_cov2d, vm2, v_mc, v_cc);
       const float* R = f.R.v;

@@ -88,9 +88,8 @@ class _ProjectionEWA3DGSFused(torch.autograd.Function):
     def backward(ctx, v_means2d, v_depths, v_conics, v_compensations, _v_radii):
         means, covars, quats, scales, viewmats, Ks, radii, conics, comps = ctx.saved_tensors
         W, H, eps2d, calc_comp, camera_model, use_covars = ctx.params
-        if camera_model not in (0, 1):
-            raise RuntimeError("GSPlatProjectionEWA3DGSFused vjp currently supports pinhole and orthographic "
-                               "cameras only.")
+        if camera_model not in (0, 1, 2):
+            raise RuntimeError("GSPlatProjectionEWA3DGSFused vjp: unknown camera model.")
         shape2 = radii.shape
         v_means2d = torch.zeros(shape2, dtype=torch.float32, device=means.device) if v_means2d is None else v_means2d
         v_depths = _empty(means) if v_depths is None else v_depths  # empty = zeros
@@ -139,7 +138,7 @@ def projection_ewa_3dgs_fused(means, viewmats, Ks, image_width, image_height, qu
 
 class _ProjectionPacked(torch.autograd.Function):
     """projection_ewa_3dgs_packed_forward / _backward (upstream gsplat's
-    fully_fused_projection(packed=True)); pinhole backward only."""
+    fully_fused_projection(packed=True)); backward for all three camera models."""
 
     @staticmethod
     def forward(ctx, means, quats, scales, viewmats, Ks, image_width, image_height, eps2d, near_plane, far_plane,
@@ -160,9 +159,8 @@ class _ProjectionPacked(torch.autograd.Function):
     def backward(ctx, _b, _c, _g, _i, _r, v_means2d, v_depths, v_conics, v_compensations):
         means, quats, scales, viewmats, Ks, bid, cid, gid, conics, comps = ctx.saved_tensors
         W, H, eps2d, calc_comp, camera_model = ctx.params
-        if camera_model not in (0, 1):
-            raise RuntimeError("projection_ewa_3dgs_packed vjp currently supports pinhole and orthographic "
-                               "cameras only.")
+        if camera_model not in (0, 1, 2):
+            raise RuntimeError("projection_ewa_3dgs_packed vjp: unknown camera model.")
         nnz = cid.shape[0]
         v_means2d = means.new_zeros((nnz, 2)) if v_means2d is None else v_means2d.contiguous()
         v_conics = means.new_zeros((nnz, 3)) if v_conics is None else v_conics.contiguous()
@@ -386,9 +384,8 @@ class _ActivatedProjection(torch.autograd.Function):
     def backward(ctx, v_means2d, v_depths, v_conics, v_compensations, _v_radii, v_opacities):
         means, quats, log_scales, logits, viewmats, Ks, radii, conics, comps = ctx.saved_tensors
         W, H, eps2d, calc_comp, camera_model = ctx.params
-        if camera_model not in (0, 1):
-            raise RuntimeError("GSPlatProjectionEWA3DGSFused vjp currently supports pinhole and orthographic "
-                               "cameras only.")
+        if camera_model not in (0, 1, 2):
+            raise RuntimeError("GSPlatProjectionEWA3DGSFused vjp: unknown camera model.")
         dev = means.device
         v_means2d = torch.zeros(radii.shape, dtype=torch.float32, device=dev) if v_means2d is None else v_means2d
         v_conics = torch.zeros(conics.shape, dtype=torch.float32, device=dev) if v_conics is None else v_conics

@@ -426,6 +426,88 @@ void ortho_proj_vjp(T fx, T fy, const T* v_cov2d, const T* v_mean2d, T* v_mean3d
   v_mean3d[1] += fy * v_mean2d[1];
 }
 
+// Equidistant fisheye (upstream gsplat's fisheye_proj_vjp; forward only in
+// the reference): the image point and J are differentiated as forward-mode
+// dual numbers (value and d/dx, d/dy, d/dz) through the forward's formulas
+// (camera_jacobian above), eps terms included. Pinned by float64 finite
+// differences of the fisheye forward.
+template <typename T>
+struct Dual {
+  T v, d[3];
+};
+template <typename T>
+Dual<T> dc(T c) { return {c, {T(0), T(0), T(0)}}; }
+template <typename T>
+Dual<T> operator+(const Dual<T>& a, const Dual<T>& b) {
+  return {a.v + b.v, {a.d[0] + b.d[0], a.d[1] + b.d[1], a.d[2] + b.d[2]}};
+}
+template <typename T>
+Dual<T> operator-(const Dual<T>& a, const Dual<T>& b) {
+  return {a.v - b.v, {a.d[0] - b.d[0], a.d[1] - b.d[1], a.d[2] - b.d[2]}};
+}
+template <typename T>
+Dual<T> operator*(const Dual<T>& a, const Dual<T>& b) {
+  return {a.v * b.v, {a.d[0] * b.v + a.v * b.d[0], a.d[1] * b.v + a.v * b.d[1], a.d[2] * b.v + a.v * b.d[2]}};
+}
+template <typename T>
+Dual<T> operator/(const Dual<T>& a, const Dual<T>& b) {
+  const T q = a.v / b.v;
+  return {q, {(a.d[0] - q * b.d[0]) / b.v, (a.d[1] - q * b.d[1]) / b.v, (a.d[2] - q * b.d[2]) / b.v}};
+}
+template <typename T>
+Dual<T> dsqrt(const Dual<T>& a) {
+  const T r = std::sqrt(a.v);
+  return {r, {a.d[0] / (T(2) * r), a.d[1] / (T(2) * r), a.d[2] / (T(2) * r)}};
+}
+template <typename T>
+Dual<T> datan2(const Dual<T>& u, const Dual<T>& w) {
+  const T den = u.v * u.v + w.v * w.v;
+  Dual<T> o;
+  o.v = std::atan2(u.v, w.v);
+  for (int k = 0; k < 3; ++k) o.d[k] = (w.v * u.d[k] - u.v * w.d[k]) / den;
+  return o;
+}
+
+template <typename T>
+void fisheye_proj_vjp(const T* mc, const M3<T>& cov3d, T fx_, T fy_, const T* v_cov2d, const T* v_mean2d,
+                      T* v_mean3d, M3<T>& v_cov3d) {
+  const Dual<T> x = {mc[0], {T(1), T(0), T(0)}}, y = {mc[1], {T(0), T(1), T(0)}}, z = {mc[2], {T(0), T(0), T(1)}};
+  const Dual<T> eps = dc(T(0.0000001f)), fx = dc(fx_), fy = dc(fy_);
+  const Dual<T> xy_len = dsqrt(x * x + y * y) + eps;
+  const Dual<T> theta = datan2(xy_len, z + eps);
+  const Dual<T> m2[2] = {x * fx * theta / xy_len, y * fy * theta / xy_len};
+  const Dual<T> x2 = x * x + eps, y2 = y * y, xy = x * y;
+  const Dual<T> x2y2 = x2 + y2;
+  const Dual<T> inv = dc(T(1)) / (x2y2 + z * z);
+  const Dual<T> b = datan2(xy_len, z) / xy_len / x2y2;
+  const Dual<T> a = z * inv / x2y2;
+  const Dual<T> J[6] = {fx * (x2 * a + y2 * b), fx * xy * (a - b), dc(T(0)) - fx * x * inv,
+                        fy * xy * (a - b),      fy * (y2 * a + x2 * b), dc(T(0)) - fy * y * inv};
+  for (int ia = 0; ia < 3; ++ia)
+    for (int ib = 0; ib < 3; ++ib) {
+      T acc = 0;
+      for (int r = 0; r < 2; ++r)
+        for (int c = 0; c < 2; ++c) acc += J[r * 3 + ia].v * v_cov2d[r * 2 + c] * J[c * 3 + ib].v;
+      v_cov3d.v[ia * 3 + ib] = acc;
+    }
+  // d/dJ of J cov3d J^T contracted with v_cov2d
+  T v_J[6];
+  for (int r = 0; r < 2; ++r)
+    for (int ia = 0; ia < 3; ++ia) {
+      T acc = 0;
+      for (int c = 0; c < 2; ++c)
+        for (int ib = 0; ib < 3; ++ib)
+          acc += v_cov2d[r * 2 + c] * J[c * 3 + ib].v * cov3d.v[ia * 3 + ib] +
+                 v_cov2d[c * 2 + r] * J[c * 3 + ib].v * cov3d.v[ib * 3 + ia];
+      v_J[r * 3 + ia] = acc;
+    }
+  for (int k = 0; k < 3; ++k) {
+    T acc = v_mean2d[0] * m2[0].d[k] + v_mean2d[1] * m2[1].d[k];
+    for (int i = 0; i < 6; ++i) acc += v_J[i] * J[i].d[k];
+    v_mean3d[k] += acc;
+  }
+}
+
 template <typename T>
 void persp_proj_vjp(const T* mean3d, const M3<T>& cov3d, T fx, T fy, T cx, T cy, int width,
                     int height, const T* v_cov2d, const T* v_mean2d, T* v_mean3d, M3<T>& v_cov3d) {
@@ -564,6 +646,8 @@ void proj_backward(const T* means, const T* covars, const T* quats, const T* sca
         M3<T> v_cc = {};
         if (p.camera_model == 1)
           ortho_proj_vjp(K[0], K[4], v_cov2d, v_means2d + idx * 2, v_mc, v_cc);
+        else if (p.camera_model == 2)
+          fisheye_proj_vjp(mc, cc, K[0], K[4], v_cov2d, v_means2d + idx * 2, v_mc, v_cc);
         else
           persp_proj_vjp(mc, cc, K[0], K[4], K[2], K[5], p.image_width, p.image_height, v_cov2d,
                          v_means2d + idx * 2, v_mc, v_cc);

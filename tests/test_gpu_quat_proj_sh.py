@@ -148,7 +148,8 @@ def test_projection_known_answers_and_culling(oracle):
 
 @pytest.mark.parametrize("use_covars,calc_comp,C,camera_model", [(False, False, 1, 0), (False, True, 2, 0),
                                                                  (True, True, 3, 0), (False, True, 2, 1),
-                                                                 (True, False, 1, 1)])
+                                                                 (True, False, 1, 1), (False, True, 2, 2),
+                                                                 (True, False, 1, 2)])
 def test_projection_backward_vs_oracle(oracle, use_covars, calc_comp, C, camera_model):
     g = gsplat()
     rng = np.random.default_rng(7 + C)

@@ -217,7 +217,7 @@ def _proj_loss(oracle, means, quats, scales, covars, viewmats, Ks, cot, fixed_ra
 
 @pytest.mark.parametrize("use_covars", [False, True])
 @pytest.mark.parametrize("calc_comp", [False, True])
-@pytest.mark.parametrize("camera_model", [0, 1])  # pinhole, orthographic
+@pytest.mark.parametrize("camera_model", [0, 1, 2])  # pinhole, orthographic, fisheye
 def test_backward_finite_differences(oracle, use_covars, calc_comp, camera_model):
     rng = np.random.default_rng(5)
     B, C, N = 1, 2, 6
