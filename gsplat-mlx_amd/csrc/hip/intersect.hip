@@ -1,5 +1,6 @@
-// Dense AABB tile intersection for gfx950: count + exclusive scan, encode,
-// and tile offsets.
+// Tile intersection for gfx950: count + exclusive scan, encode (AABB rect or
+// ellipse tiles; dense or packed layout), depth-presorted sort, and tile
+// offsets.
 //
 // Integer semantics follow gsplat_core/gsplat_intersect.cpp:60-112 (rect and
 // key layout), :309-339 (count), :433-485 (encode order) and :605-641
