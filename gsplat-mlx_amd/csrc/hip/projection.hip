@@ -444,7 +444,8 @@ static int packed_args(const std::string& op, const float* means, const float* c
                        const gsplat_projection_params* params) {
   if (!params) return invalid(op + ": null params.");
   if (B < 0 || C < 0 || N < 0) return invalid(op + ": negative size.");
-  if (B * C * N > (static_cast<int64_t>(INT32_MAX) << 6)) return invalid(op + ": too many pairs.");
+  // packed rows and word prefixes are int32
+  if (B * C * N > static_cast<int64_t>(INT32_MAX)) return invalid(op + ": more than 2^31-1 (camera, Gaussian) pairs.");
   if (B * C * N == 0) return GSPLAT_OK;
   if (!means || !viewmats || !Ks) return invalid(op + ": null pointer.");
   if (params->use_covars ? !covars : (!quats || !scales)) return invalid(op + " expects covars or quats+scales.");
