@@ -223,11 +223,30 @@ __global__ void __launch_bounds__(256) projection_packed_scatter_kernel(const in
                                                                         int64_t nnz, int64_t B, int64_t C, int64_t N,
                                                                         uint64_t* __restrict__ mask) {
   const int64_t e = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (e >= nnz) return;
-  const int64_t b = batch_ids ? batch_ids[e] : 0, c = camera_ids[e], n = gaussian_ids[e];
-  if (b < 0 || b >= B || c < 0 || c >= C || n < 0 || n >= N) return;  // ignored (the caller's ids are checked)
-  const int64_t idx = (b * C + c) * N + n;
-  atomicOr(reinterpret_cast<unsigned long long*>(mask) + (idx >> 6), 1ull << (idx & 63));
+  const int lane = threadIdx.x % kWave;
+  int64_t word = -1;
+  uint64_t bit = 0;
+  if (e < nnz) {
+    const int64_t b = batch_ids ? batch_ids[e] : 0, c = camera_ids[e], n = gaussian_ids[e];
+    if (b >= 0 && b < B && c >= 0 && c < C && n >= 0 && n < N) {  // others are ignored
+      const int64_t idx = (b * C + c) * N + n;
+      word = idx >> 6;
+      bit = 1ull << (idx & 63);
+    }
+  }
+  // Entries in the forward's order put consecutive lanes on the same word:
+  // OR the bits of equal-word lanes together (each lane gathers from the
+  // lanes above it with the same word) so that one lane per word and wave
+  // issues the atomic instead of up to 64.
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) {
+    const uint64_t ob = __shfl_down(bit, off, kWave);
+    const int64_t ow = __shfl_down(word, off, kWave);
+    if (lane + off < kWave && ow == word) bit |= ob;
+  }
+  const int64_t prev = __shfl_up(word, 1, kWave);
+  if (word >= 0 && (lane == 0 || prev != word))
+    atomicOr(reinterpret_cast<unsigned long long*>(mask) + word, bit);
 }
 
 __global__ void __launch_bounds__(256) popcount_words_kernel(const uint64_t* __restrict__ mask, int64_t n_words,
