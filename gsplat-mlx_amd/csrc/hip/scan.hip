@@ -51,6 +51,36 @@ __global__ void __launch_bounds__(kScanBlock) scan_fixup_kernel(int32_t* __restr
   }
 }
 
+// Small inputs (up to kSingleTiles tiles): one block walks the tiles with a
+// carry -- one launch instead of three, which is what a scan of a few
+// thousand values costs.
+constexpr int64_t kSingleTiles = 64;
+
+__global__ void __launch_bounds__(kScanBlock) scan_single_kernel(const int32_t* __restrict__ in,
+                                                                int32_t* __restrict__ out, int64_t n,
+                                                                int64_t* __restrict__ total_dev) {
+  int64_t carry = 0;
+  for (int64_t tile = 0; tile * kScanTile < n; ++tile) {
+    const int64_t base = tile * kScanTile + static_cast<int64_t>(threadIdx.x) * kScanItems;
+    int32_t v[kScanItems];
+    int64_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+      v[k] = base + k < n ? in[base + k] : 0;
+      sum += v[k];
+    }
+    int64_t total;
+    int64_t run = carry + block_exclusive_scan(sum, &total);  // syncs: every read precedes every write
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+      if (base + k < n) out[base + k] = static_cast<int32_t>(run);
+      run += v[k];
+    }
+    carry += total;
+  }
+  if (threadIdx.x == 0 && total_dev) *total_dev = carry;
+}
+
 }  // namespace
 
 int scan_exclusive_i32(const int32_t* in, int32_t* out, int64_t n, int64_t* total_dev, void* workspace,
@@ -61,6 +91,13 @@ int scan_exclusive_i32(const int32_t* in, int32_t* out, int64_t n, int64_t* tota
   }
   const int64_t nb = scan_num_blocks(n);
   if (nb > kMaxGridX) return invalid("scan: too many elements.");
+  if (nb <= kSingleTiles) {
+    {
+      KernelTimer timer("scan_local", stream);
+      scan_single_kernel<<<1, kScanBlock, 0, stream>>>(in, out, n, total_dev);
+    }
+    return check_launch("scan (single block)");
+  }
   int64_t* sums = static_cast<int64_t*>(workspace);
   {
     KernelTimer timer("scan_local", stream);

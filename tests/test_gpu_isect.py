@@ -190,3 +190,27 @@ def test_c_abi_tile_sorted_one_call(oracle):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(ids), exp["isect_ids"])
     np.testing.assert_array_equal(host(flat), exp["flatten_ids"])
+
+
+@pytest.mark.parametrize("n", [1, 1023, 4097, 65536, 65537, 1 << 20])
+def test_c_abi_exclusive_scan(n):
+    """gsplat_hip_exclusive_scan_i32 against numpy, in place, on both sides of
+    the single-block / three-kernel switch (64 tiles of 1024 values)."""
+    import torch
+
+    lib = ctypes.CDLL(LIB)
+    lib.gsplat_hip_last_error.restype = ctypes.c_char_p
+    lib.gsplat_hip_exclusive_scan_i32_workspace_size.restype = ctypes.c_size_t
+    lib.gsplat_hip_exclusive_scan_i32_workspace_size.argtypes = [ctypes.c_int64]
+    lib.gsplat_hip_exclusive_scan_i32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                                  ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    v = np.random.default_rng(n).integers(0, 100, n).astype(np.int32)
+    x = torch.from_numpy(v).cuda()
+    total = torch.zeros(1, dtype=torch.int64, device="cuda")
+    ws = torch.empty(max(lib.gsplat_hip_exclusive_scan_i32_workspace_size(n), 1), dtype=torch.uint8, device="cuda")
+    rc = lib.gsplat_hip_exclusive_scan_i32(x.data_ptr(), x.data_ptr(), n, total.data_ptr(), ws.data_ptr(),
+                                           ws.numel(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.gsplat_hip_last_error()
+    expect = np.concatenate([[0], np.cumsum(v.astype(np.int64))[:-1]])
+    np.testing.assert_array_equal(host(x), expect)
+    assert int(total.item()) == int(v.astype(np.int64).sum())
