@@ -146,7 +146,9 @@ extern "C" int gsplat_hip_valu_probe(float* out, int64_t blocks, int32_t iters, 
 
 extern "C" const char* gsplat_hip_last_error(void) { return gsplat_hip::g_last_error.c_str(); }
 
-extern "C" int gsplat_hip_abi_version(void) { return 100; }
+// 1.01: ellipse tiles, packed layout, rasterize-to-indices and selective Adam
+// entry points added (additive).
+extern "C" int gsplat_hip_abi_version(void) { return 101; }
 
 extern "C" void gsplat_hip_profile_enable(int32_t enable) { gsplat_hip::g_profile = enable != 0; }
 
