@@ -134,6 +134,10 @@ Counted count_and_scan(const IntersectTileInput& input, void* stream, bool with_
   return c;
 }
 
+// Frames with more entries than this that hold a list longer than the LDS
+// tile sort take the depth-presorted path (see intersect_bucketed_finish).
+constexpr int64_t kPresortAboveIsects = int64_t{1} << 26;
+
 // The bucketed intersection path (bucket.hip) is the default for sorted
 // dense intersections, AABB or ellipse tiles, whose tile grid it supports;
 // GSPLAT_ISECT_BUCKETED=0 selects the depth-presorted path instead (read
@@ -333,9 +337,9 @@ std::vector<array> gsplat_intersect_tile_sort(const array& isect_ids, const arra
 }
 
 // Sorted dense intersections (AABB or ellipse tiles) by tile buckets
-// (bucket.hip): counts, then M and the longest list read back together; the
-// bucketed scatter and per-tile sort when every list fits the tile sort, else
-// the depth-presorted encode.
+// (bucket.hip): counts, then M and the longest list read back together (the
+// longest list selects the tile sort launches), then the bucketed scatter and
+// per-tile sorts.
 // The bucketed intersection in two halves around the read-back of M and the
 // longest tile list: the count kernels (queued), then, once the two words are
 // on the host, the M-long outputs and the scatter + tile sort.
@@ -383,7 +387,12 @@ std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, co
   array ids = at::empty({total}, i64_like(b.means2d));
   array flat = at::empty({total}, i32_like(b.means2d));
   if (tile_offsets) *tile_offsets = at::empty({p.I, p.tile_height, p.tile_width}, i32_like(b.means2d));
-  if (longest <= gsplat_hip_isect_bucket_max_list()) {
+  // Lists longer than the LDS tile sort holds are sorted inside the bucket
+  // path (split by their leading depth bits); in frames of many entries that
+  // hold such lists the depth-presorted path is faster (heavy_6m, 247M
+  // entries: 6.97 against 9.98 ms for the intersection, the bucket scatter's
+  // partial-line writes dominating), so those take it.
+  if (longest <= gsplat_hip_isect_bucket_max_list() || total < kPresortAboveIsects) {
     const size_t ws2_bytes = gsplat_hip_isect_bucket_sort_workspace_size(total);
     array ws2 = workspace(ws2_bytes, b.means2d);
     int32_t* offsets_out = tile_offsets ? tile_offsets->data_ptr<int32_t>() : nullptr;
@@ -401,7 +410,7 @@ std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, co
                                          ws2.data_ptr<uint8_t>(), ws2_bytes, stream));
     return {b.tiles_per_gauss, ids, flat};
   }
-  // a list longer than the tile sort holds: depth order, then encode + 32-bit sort
+  // a large frame with a list longer than the LDS tile sort: depth order, then encode + 32-bit sort
   array perm = at::empty({numel}, i32_like(b.means2d));
   array offs = at::empty({numel}, i32_like(b.means2d));
   const size_t ws3_bytes = gsplat_hip_isect_depth_order_workspace_size(numel);

@@ -31,10 +31,11 @@
 //     as the low digits, so the order is the reference's whatever order the
 //     scatter left; the block writes the 64-bit ids and the flatten ids.
 //     Short lists are sorted by one launch over every list, each longer
-//     class by a launch of a larger instantiation.
-// Steps 4-5 need M only to size their outputs. Lists longer than the tile
-// sort's LDS capacity (kBucketMaxList) are left to the caller, which reads
-// the largest count back with M and then takes the depth-presorted pipeline.
+//     class by a launch of a larger instantiation; lists longer than the
+//     LDS holds (kBucketMaxList) are split by their most significant varying
+//     depth byte into runs that the LDS sort takes in turn.
+// Steps 4-5 need M only to size their outputs, and the longest list (read
+// back with M) to launch only the classes present.
 #include <algorithm>
 #include <string>
 
@@ -47,7 +48,7 @@ constexpr int kBucketBlock = 1024;                 // grid and scatter passes
 constexpr int kXcds = 8;                           // MI355X: workgroups are dealt round-robin over 8 XCDs
 constexpr int kBucketMaxGrid = 35072;              // (th + 1)(tw + 1) words of LDS, at most
 constexpr int kColGroup = 64, kColSegs = 16;       // block scan: 64 grid points x 16 block ranges
-constexpr int kBucketMaxList = 16384;              // longest list the tile sort holds in LDS
+constexpr int kBucketMaxList = 16384;              // longest list the LDS tile sort holds
 constexpr int kTilePassBlock = 1024;
 
 inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
@@ -62,17 +63,18 @@ struct BucketDims {
 
 // Tile sort capacities: lists up to kSortCap[0] take the <256, 10> sort in
 // one launch over every list; longer lists are binned by the tile pass into
-// classes 1-3 (up to kSortCap[1..3]: <512, 8>, <512, 16>, <1024, 16>), each
-// sorted by its own launch. At multiview_3m (lists of up to ~10,000) the
-// tile sort takes 2.25 ms this way against 2.78 ms with every list in the
-// instantiation the longest list needs; <512, 5> for the short lists and
-// <1024, 8> for class 2 measured slower.
+// classes 0-2 (up to kSortCap[1..3]: <512, 8>, <512, 16>, <1024, 16>), each
+// sorted by its own launch, and class 3 (longer than LDS holds) by the split
+// sort below. At multiview_3m (lists of up to ~10,000) the tile sort takes
+// 2.25 ms this way against 2.78 ms with every list in the instantiation the
+// longest list needs; <512, 5> for the short lists and <1024, 8> for class 2
+// measured slower.
 constexpr int kSortCap[4] = {256 * 10, 512 * 8, 512 * 16, 1024 * 16};
-constexpr int kSortClasses = 3;
+constexpr int kSortClasses = 4;
 
 // count workspace: per-block grids [I * bpi][G], image total grids [I][G],
-// tile starts [I * n_tiles], the long lists of each class [3][I * n_tiles]
-// and the class sizes [3]
+// tile starts [I * n_tiles], the long lists of each class [4][I * n_tiles]
+// and the class sizes [4] (+ the split sort's fallback count)
 struct CountLayout {
   int32_t* partials;
   int32_t* totals;
@@ -86,7 +88,7 @@ size_t count_layout(const BucketDims& d, CountLayout* l, void* base) {
   const size_t b = align256(static_cast<size_t>(d.I * d.G) * 4);
   const size_t c = align256(static_cast<size_t>(d.I * d.n_tiles) * 4);
   const size_t e = align256(static_cast<size_t>(kSortClasses * d.I * d.n_tiles) * 4);
-  const size_t f = align256(kSortClasses * 4);
+  const size_t f = align256((kSortClasses + 1) * 4);  // class sizes, then the split sort's fallback count
   if (l && base) {
     char* p = static_cast<char*>(base);
     l->partials = reinterpret_cast<int32_t*>(p);
@@ -231,7 +233,12 @@ __device__ __forceinline__ void ell_owners(int c, int pre, int rows, uint32_t* s
 constexpr size_t kEllGridLds = kBucketBlock * sizeof(EllRec) + (kEllRowChunk + kBucketBlock) * 4;
 constexpr size_t kEllScatterLds = kBucketBlock * sizeof(EllRec) + kBucketBlock * 4 + (4 * kEllRowChunk + 1) * 4;
 constexpr size_t kLdsBytes = 160 * 1024;  // MI355X LDS per workgroup
-constexpr int kBucketMaxGridEll = static_cast<int>((kLdsBytes - kEllScatterLds) / 4);
+// static LDS beside the dynamic grid: block_scan_i64's per-wave totals
+constexpr size_t kBlockScanLds = (kBucketBlock / kWave) * sizeof(int64_t);
+constexpr int kBucketMaxGridEll = static_cast<int>((kLdsBytes - kEllScatterLds - kBlockScanLds) / 4);
+static_assert(kEllGridLds <= kEllScatterLds, "the ellipse scatter's LDS bounds the ellipse grid pass's");
+static_assert(kBucketMaxGrid * 4 + (4 * kBucketBlock + 1) * 4 + kBlockScanLds <= kLdsBytes,
+              "the AABB scatter's LDS fits a workgroup");
 
 // ---------------------------------------------------------------------------
 // 1. Difference grid of the block's Gaussians' rects (ELL: of their ellipse
@@ -434,7 +441,7 @@ __global__ void __launch_bounds__(kTilePassBlock) bucket_tile_pass_kernel(Bucket
       const int32_t c = sg[y * W1 + x];
       run += c;
       if (c > kSortCap[0]) {  // rare: a long list goes to its class
-        const int cls = c <= kSortCap[1] ? 0 : (c <= kSortCap[2] ? 1 : 2);
+        const int cls = c <= kSortCap[1] ? 0 : (c <= kSortCap[2] ? 1 : (c <= kSortCap[3] ? 2 : 3));
         class_lists[cls * n_lists + atomicAdd(&s_cls[cls], 1)] = static_cast<int32_t>(image * d.n_tiles + k);
       }
       if (++x == d.tw) {
@@ -456,7 +463,7 @@ __global__ void __launch_bounds__(kTilePassBlock) bucket_tile_pass_kernel(Bucket
     readback[0] = offset;
     readback[1] = largest;
   }
-  if (t < kSortClasses) class_counts[t] = s_cls[t];
+  if (t <= kSortClasses) class_counts[t] = t < kSortClasses ? s_cls[t] : 0;  // + the fallback count
 }
 
 // 4. Scatter of the (depth bits, flatten id) pairs into the tile buckets.
@@ -725,19 +732,15 @@ struct TileSorter {
   }
 };
 
-// One tile list sorted in LDS (the shared arrays of its kernel); a list
-// longer than this instantiation holds is left alone.
+// The n (depth bits, flatten id) pairs at src sorted in LDS (the shared
+// arrays of the calling kernel) and written as ids hi | depth bits and
+// flatten ids at out_ids / out_flat. Every input is read before any output
+// is written, so src may be the bytes of out_ids. n > CAP is left alone.
 template <int B, int ITEMS>
-__device__ __forceinline__ void sort_tile_list(int64_t list, const uint2* __restrict__ pairs,
-                                               const int32_t* __restrict__ tile_start, int64_t n_lists,
-                                               int64_t n_isects, int64_t n_tiles, int tile_bits,
-                                               int64_t* __restrict__ isect_ids, int32_t* __restrict__ flatten_ids,
-                                               uint32_t* s_keys, uint32_t* s_vals, uint32_t* s_wcnt,
-                                               uint32_t* s_dstart, uint32_t* s_bits) {
+__device__ __forceinline__ void sort_range(const uint2* src, int64_t len, uint64_t hi, int64_t* out_ids,
+                                           int32_t* out_flat, uint32_t* s_keys, uint32_t* s_vals,
+                                           uint32_t* s_wcnt, uint32_t* s_dstart, uint32_t* s_bits) {
   using S = TileSorter<B, ITEMS>;
-  const int64_t end = min<int64_t>(list + 1 < n_lists ? tile_start[list + 1] : n_isects, n_isects);
-  const int64_t start = min<int64_t>(max<int64_t>(tile_start[list], 0), end);
-  const int64_t len = end - start;
   if (len <= 0 || len > S::CAP) return;  // block-uniform
   const int n = static_cast<int>(len);
   const int t = threadIdx.x;
@@ -747,7 +750,7 @@ __device__ __forceinline__ void sort_tile_list(int64_t list, const uint2* __rest
   // are skipped
   uint32_t ko = 0u, ka = ~0u, vo = 0u, va = ~0u;
   for (int j = t; j < n; j += B) {
-    const uint2 p = pairs[start + j];
+    const uint2 p = src[j];
     s_keys[j] = p.x;
     s_vals[j] = p.y;
     ko |= p.x;
@@ -776,7 +779,7 @@ __device__ __forceinline__ void sort_tile_list(int64_t list, const uint2* __rest
     for (int shift = 0; shift < 32; shift += 8) srt.pass(false, shift, (kvary >> shift) & 255u);
     // equal depths: their entries go in flatten-id order. A run of up to
     // kShortRun equal keys is insertion-sorted by the thread at its start;
-    // a tile with a longer run is sorted again, ids as the low digits.
+    // a list with a longer run is sorted again, ids as the low digits.
     constexpr int kShortRun = 32;
     auto run_start = [&](int j) {
       return j + 1 < n && s_keys[j + 1] == s_keys[j] && (j == 0 || s_keys[j - 1] != s_keys[j]);
@@ -816,12 +819,39 @@ __device__ __forceinline__ void sort_tile_list(int64_t list, const uint2* __rest
       __syncthreads();
     }
   }
-  const int64_t image = list / n_tiles, tile = list % n_tiles;
-  const uint64_t hi = (static_cast<uint64_t>(image) << (32 + tile_bits)) | (static_cast<uint64_t>(tile) << 32);
+  // every thread read its inputs before the first barrier above
   for (int j = t; j < n; j += B) {
-    isect_ids[start + j] = static_cast<int64_t>(hi | s_keys[j]);
-    flatten_ids[start + j] = static_cast<int32_t>(s_vals[j]);
+    out_ids[j] = static_cast<int64_t>(hi | s_keys[j]);
+    out_flat[j] = static_cast<int32_t>(s_vals[j]);
   }
+}
+
+// The 64-bit id prefix image << (32 + tile_bits) | tile << 32 of list `list`.
+__device__ __forceinline__ uint64_t list_hi(int64_t list, int64_t n_tiles, int tile_bits) {
+  const int64_t image = list / n_tiles, tile = list % n_tiles;
+  return (static_cast<uint64_t>(image) << (32 + tile_bits)) | (static_cast<uint64_t>(tile) << 32);
+}
+
+// [*start, *end) of tile list `list` (clamped to [0, n_isects]).
+__device__ __forceinline__ void list_range(int64_t list, const int32_t* __restrict__ tile_start, int64_t n_lists,
+                                           int64_t n_isects, int64_t* start, int64_t* end) {
+  *end = min<int64_t>(list + 1 < n_lists ? tile_start[list + 1] : n_isects, n_isects);
+  *start = min<int64_t>(max<int64_t>(tile_start[list], 0), *end);
+}
+
+// One tile list sorted in LDS (the shared arrays of its kernel); a list
+// longer than this instantiation holds is left alone.
+template <int B, int ITEMS>
+__device__ __forceinline__ void sort_tile_list(int64_t list, const uint2* __restrict__ pairs,
+                                               const int32_t* __restrict__ tile_start, int64_t n_lists,
+                                               int64_t n_isects, int64_t n_tiles, int tile_bits,
+                                               int64_t* __restrict__ isect_ids, int32_t* __restrict__ flatten_ids,
+                                               uint32_t* s_keys, uint32_t* s_vals, uint32_t* s_wcnt,
+                                               uint32_t* s_dstart, uint32_t* s_bits) {
+  int64_t start, end;
+  list_range(list, tile_start, n_lists, n_isects, &start, &end);
+  sort_range<B, ITEMS>(pairs + start, end - start, list_hi(list, n_tiles, tile_bits), isect_ids + start,
+                       flatten_ids + start, s_keys, s_vals, s_wcnt, s_dstart, s_bits);
 }
 
 template <int B, int ITEMS>
@@ -864,6 +894,309 @@ __global__ void __launch_bounds__(B) bucket_tile_sort_class_kernel(const uint2* 
   if (static_cast<int>(blockIdx.x) >= *class_count) return;
   sort_tile_list<B, ITEMS>(class_list[blockIdx.x], pairs, tile_start, n_lists, n_isects, n_tiles, tile_bits,
                            isect_ids, flatten_ids, sh.keys, sh.vals, sh.wcnt, sh.dstart, sh.bits);
+}
+
+// Lists longer than the LDS sorts hold (class 3). One block per list takes
+// the eight bits of the depth keys below and at their most significant
+// varying bit as a digit (the keys agree on every higher bit, so every key
+// of one digit is smaller than every key of the next) and counts the 256
+// digits; when no digit holds more than kRunCap entries, it scatters the
+// list by digit into the bytes of its isect_ids, groups consecutive digits
+// into runs of at most kRunCap entries, and sorts the runs one after another
+// with the LDS sort, which writes the final ids in place. Otherwise (every
+// depth equal, or one digit too crowded) the list goes to a block that sorts
+// it in global memory: a stable LSD radix sort with the list's pairs and the
+// same bytes of its isect_ids as the two buffers, each pass walking the list
+// in tiles of kHugeTile entries, wave w ranking its contiguous chunk by
+// ballots as TileSorter does; ties of depth are resolved by sorting again on
+// the flatten ids, then on the depth bits.
+constexpr int kHugeBlock = 1024;
+constexpr int kHugeItems = 8;
+constexpr int kHugeTile = kHugeBlock * kHugeItems;
+constexpr int kHugeWaves = kHugeBlock / kWave;
+
+struct HugeRadixLds {
+  uint32_t hist[8][256];  // digit counts: depth bytes 0-3, id bytes 0-3
+  uint32_t run[256];      // running start of each digit in the destination
+  uint32_t wcnt[kHugeWaves][256];
+};
+
+__device__ void huge_hist(const uint2* __restrict__ src, int n, bool ids, HugeRadixLds& sh) {
+  const int t = threadIdx.x;
+  uint32_t(*h)[256] = sh.hist + (ids ? 4 : 0);
+  for (int j = t; j < 4 * 256; j += kHugeBlock) h[j / 256][j % 256] = 0u;
+  __syncthreads();
+  for (int j = t; j < n; j += kHugeBlock) {
+    const uint2 p = src[j];
+    const uint32_t v = ids ? p.y : p.x;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) atomicAdd(&h[q][(v >> (8 * q)) & 255u], 1u);
+  }
+  __syncthreads();
+}
+
+// Exclusive scan of 256 digit counts into `out` by wave 0 (4 digits per
+// lane); returns nothing, callers sync.
+__device__ __forceinline__ void digit_starts(const uint32_t* counts, uint32_t* out) {
+  const int t = threadIdx.x;
+  if (t < kWave) {
+    uint32_t c[4];
+    uint32_t s = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      c[q] = counts[t * 4 + q];
+      s += c[q];
+    }
+    const uint32_t inc = static_cast<uint32_t>(wave_inclusive_scan(static_cast<int>(s)));
+    uint32_t r = inc - s;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      out[t * 4 + q] = r;
+      r += c[q];
+    }
+  }
+}
+
+// One stable pass on byte `shift / 8` of the depth bits (or of the ids) from
+// src to dst; hist: that byte's digit counts over the list.
+__device__ void huge_pass(const uint2* __restrict__ src, uint2* __restrict__ dst, int n, bool by_id, int shift,
+                          const uint32_t* hist, HugeRadixLds& sh) {
+  const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  digit_starts(hist, sh.run);
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (kWave - lane));
+  uint32_t* wc = sh.wcnt[wave];
+  for (int base = 0; base < n; base += kHugeTile) {
+    for (int j = t; j < kHugeWaves * 256; j += kHugeBlock) (&sh.wcnt[0][0])[j] = 0u;
+    __syncthreads();
+    uint2 e[kHugeItems];
+    uint32_t rank[kHugeItems];
+#pragma unroll
+    for (int r = 0; r < kHugeItems; ++r) {
+      const int idx = base + (wave * kHugeItems + r) * kWave + lane;
+      const bool valid = idx < n;
+      e[r] = valid ? src[idx] : make_uint2(0u, 0u);
+      const uint32_t dg = ((by_id ? e[r].y : e[r].x) >> shift) & 255u;
+      const uint64_t vm = __ballot(valid);
+      uint32_t plo = static_cast<uint32_t>(vm), phi = static_cast<uint32_t>(vm >> 32);
+      const uint32_t nd = ~dg;
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const int32_t x = static_cast<int32_t>(nd << (31 - b));
+        const uint32_t z = static_cast<uint32_t>(x >> 31);
+        const uint64_t m = __ballot(x < 0);
+        plo &= ~(static_cast<uint32_t>(m) ^ z);
+        phi &= ~(static_cast<uint32_t>(m >> 32) ^ z);
+      }
+      const uint64_t peers = (static_cast<uint64_t>(phi) << 32) | plo;
+      const uint32_t my = static_cast<uint32_t>(__popcll(peers & below));
+      const uint32_t cur = valid ? wc[dg] : 0u;
+      rank[r] = cur + my;
+      if (valid && my == 0) wc[dg] = cur + static_cast<uint32_t>(__popcll(peers));
+    }
+    __syncthreads();
+    if (t < 256) {  // the tile's digit starts per wave, and the running starts past the tile
+      uint32_t run = sh.run[t];
+      for (int w = 0; w < kHugeWaves; ++w) {
+        const uint32_t c = sh.wcnt[w][t];
+        sh.wcnt[w][t] = run;
+        run += c;
+      }
+      sh.run[t] = run;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kHugeItems; ++r) {
+      const int idx = base + (wave * kHugeItems + r) * kWave + lane;
+      if (idx < n) {
+        const uint32_t dg = ((by_id ? e[r].y : e[r].x) >> shift) & 255u;
+        dst[wc[dg] + rank[r]] = e[r];
+      }
+    }
+    __syncthreads();  // the destination is complete before it is read; wcnt is cleared next tile
+  }
+}
+
+// The radix path for one list (a at the pairs, b at its isect_ids' bytes).
+__device__ void huge_radix(uint2* a, uint2* b, int n, uint32_t kvary, uint32_t ivary, uint64_t hi,
+                           int64_t* out_ids, int32_t* out_flat, HugeRadixLds& sh) {
+  const int t = threadIdx.x;
+  huge_hist(a, n, false, sh);
+  uint2* cur = a;
+  uint2* oth = b;
+  for (int q = 0; q < 4; ++q)
+    if ((kvary >> (8 * q)) & 255u) {
+      huge_pass(cur, oth, n, false, 8 * q, sh.hist[q], sh);
+      uint2* s = cur;
+      cur = oth;
+      oth = s;
+    }
+  bool tie = false;
+  for (int j = t; j + 1 < n; j += kHugeBlock) tie = tie || cur[j].x == cur[j + 1].x;
+  if (__syncthreads_or(tie)) {  // equal depths: ids as the low digits, then the depth bits again
+    huge_hist(cur, n, true, sh);
+    for (int q = 0; q < 4; ++q)
+      if ((ivary >> (8 * q)) & 255u) {
+        huge_pass(cur, oth, n, true, 8 * q, sh.hist[4 + q], sh);
+        uint2* s = cur;
+        cur = oth;
+        oth = s;
+      }
+    for (int q = 0; q < 4; ++q)
+      if ((kvary >> (8 * q)) & 255u) {
+        huge_pass(cur, oth, n, false, 8 * q, sh.hist[q], sh);
+        uint2* s = cur;
+        cur = oth;
+        oth = s;
+      }
+  }
+  // when the result lies in the ids' bytes, each entry is read and then
+  // overwritten by its own thread
+  for (int j = t; j < n; j += kHugeBlock) {
+    const uint2 p = cur[j];
+    out_flat[j] = static_cast<int32_t>(p.y);
+    out_ids[j] = static_cast<int64_t>(hi | p.x);
+  }
+}
+
+// Split path (one block per class-3 list); lists it cannot split are
+// appended to the end of the class-3 array (fallback count class_counts[4]) for
+// bucket_huge_radix_kernel.
+__global__ void __launch_bounds__(kHugeBlock) bucket_huge_sort_kernel(uint2* __restrict__ pairs,
+                                                                      const int32_t* __restrict__ tile_start,
+                                                                      int64_t n_lists, int64_t n_isects,
+                                                                      int64_t n_tiles, int tile_bits,
+                                                                      int64_t* __restrict__ isect_ids,
+                                                                      int32_t* __restrict__ flatten_ids,
+                                                                      int32_t* __restrict__ class_list,
+                                                                      int32_t* __restrict__ class_counts) {
+  constexpr int kRunItems = 8;
+  constexpr int kRunCap = kHugeBlock * kRunItems;
+  __shared__ TileSortLds<kHugeBlock, kRunItems> sh;
+  __shared__ uint32_t s_hist[256], s_cur[256], s_bits[3];
+  __shared__ int32_t s_run[257];
+  __shared__ int s_nrun;
+  const int t = threadIdx.x;
+  const int cnt = class_counts[3];
+  for (int li = blockIdx.x; li < cnt; li += gridDim.x) {
+    const int64_t list = class_list[li];
+    int64_t start, end;
+    list_range(list, tile_start, n_lists, n_isects, &start, &end);
+    const int n = static_cast<int>(end - start);
+    const uint64_t hi = list_hi(list, n_tiles, tile_bits);
+    const uint2* a = pairs + start;
+    uint2* b = reinterpret_cast<uint2*>(isect_ids + start);
+    if (t < 3) s_bits[t] = t == 1 ? ~0u : 0u;
+    if (t < 256) s_hist[t] = 0u;
+    __syncthreads();
+    uint32_t ko = 0u, ka = ~0u;
+    for (int j = t; j < n; j += kHugeBlock) {
+      const uint32_t k = a[j].x;
+      ko |= k;
+      ka &= k;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      ko |= __shfl_xor(ko, off, kWave);
+      ka &= __shfl_xor(ka, off, kWave);
+    }
+    if (t % kWave == 0) {
+      atomicOr(&s_bits[0], ko);
+      atomicAnd(&s_bits[1], ka);
+    }
+    __syncthreads();
+    const uint32_t kvary = s_bits[0] ^ s_bits[1];
+    // the digit: the eight key bits at and below the most significant varying bit
+    const int shift = kvary == 0u ? 0 : max(31 - __builtin_clz(kvary) - 7, 0);
+    for (int j = t; j < n; j += kHugeBlock) atomicAdd(&s_hist[(a[j].x >> shift) & 255u], 1u);
+    __syncthreads();
+    if (t < 256 && s_hist[t] > static_cast<uint32_t>(kRunCap)) atomicOr(&s_bits[2], 1u);
+    digit_starts(s_hist, s_cur);
+    __syncthreads();
+    if (kvary == 0u || s_bits[2] != 0u) {  // block-uniform: the radix kernel takes it
+      if (t == 0) class_list[n_lists - 1 - atomicAdd(&class_counts[4], 1)] = static_cast<int32_t>(list);
+      __syncthreads();  // s_bits and the histogram are reset by the next list
+      continue;
+    }
+    if (t == 0) {  // consecutive digits grouped into runs of at most kRunCap entries
+      int nr = 0;
+      uint32_t acc = 0;
+      s_run[0] = 0;
+      for (int dg = 0; dg < 256; ++dg) {
+        const uint32_t c = s_hist[dg];
+        if (acc + c > static_cast<uint32_t>(kRunCap)) {
+          s_run[++nr] = static_cast<int32_t>(s_cur[dg]);
+          acc = 0;
+        }
+        acc += c;
+      }
+      s_run[++nr] = n;
+      s_nrun = nr;
+    }
+    __syncthreads();
+    for (int j = t; j < n; j += kHugeBlock) {
+      const uint2 p = a[j];
+      b[atomicAdd(&s_cur[(p.x >> shift) & 255u], 1u)] = p;
+    }
+    __syncthreads();
+    const int nrun = s_nrun;
+    for (int r = 0; r < nrun; ++r) {
+      const int r0 = s_run[r], r1 = s_run[r + 1];
+      sort_range<kHugeBlock, kRunItems>(b + r0, r1 - r0, hi, isect_ids + start + r0, flatten_ids + start + r0,
+                                        sh.keys, sh.vals, sh.wcnt, sh.dstart, sh.bits);
+      __syncthreads();  // the sort's LDS is reused by the next run
+    }
+  }
+}
+
+// Radix path for the lists the split path left (every depth equal, or one
+// digit with more entries than a run holds).
+__global__ void __launch_bounds__(kHugeBlock) bucket_huge_radix_kernel(uint2* __restrict__ pairs,
+                                                                       const int32_t* __restrict__ tile_start,
+                                                                       int64_t n_lists, int64_t n_isects,
+                                                                       int64_t n_tiles, int tile_bits,
+                                                                       int64_t* __restrict__ isect_ids,
+                                                                       int32_t* __restrict__ flatten_ids,
+                                                                       const int32_t* __restrict__ class_list,
+                                                                       const int32_t* __restrict__ class_counts) {
+  __shared__ HugeRadixLds sh;
+  __shared__ uint32_t s_bits[4];
+  const int t = threadIdx.x;
+  const int cnt = class_counts[4];
+  for (int li = blockIdx.x; li < cnt; li += gridDim.x) {
+    const int64_t list = class_list[n_lists - 1 - li];
+    int64_t start, end;
+    list_range(list, tile_start, n_lists, n_isects, &start, &end);
+    const int n = static_cast<int>(end - start);
+    uint2* a = pairs + start;
+    uint2* b = reinterpret_cast<uint2*>(isect_ids + start);
+    if (t < 4) s_bits[t] = (t & 1) ? ~0u : 0u;
+    __syncthreads();
+    uint32_t ko = 0u, ka = ~0u, vo = 0u, va = ~0u;
+    for (int j = t; j < n; j += kHugeBlock) {
+      const uint2 p = a[j];
+      ko |= p.x;
+      ka &= p.x;
+      vo |= p.y;
+      va &= p.y;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+      ko |= __shfl_xor(ko, off, kWave);
+      ka &= __shfl_xor(ka, off, kWave);
+      vo |= __shfl_xor(vo, off, kWave);
+      va &= __shfl_xor(va, off, kWave);
+    }
+    if (t % kWave == 0) {
+      atomicOr(&s_bits[0], ko);
+      atomicAnd(&s_bits[1], ka);
+      atomicOr(&s_bits[2], vo);
+      atomicAnd(&s_bits[3], va);
+    }
+    __syncthreads();
+    huge_radix(a, b, n, s_bits[0] ^ s_bits[1], s_bits[2] ^ s_bits[3], list_hi(list, n_tiles, tile_bits),
+               isect_ids + start, flatten_ids + start, sh);
+    __syncthreads();  // LDS is reused by the block's next list
+  }
 }
 
 int bucket_dims(const char* what, int64_t I, int64_t numel, int32_t ts, int32_t tw, int32_t th, bool ell,
@@ -952,9 +1285,7 @@ int bucket_sort(bool ell, const float* means2d, const int32_t* radii, const floa
   int tile_bits = 0;
   if ((rc = tile_bits_of(I, tile_width, tile_height, &tile_bits))) return rc;
   if (n_isects < 0 || n_isects > INT32_MAX) return invalid(std::string(what) + ": invalid intersection count.");
-  if (max_list < 0 || max_list > kBucketMaxList)
-    return invalid(std::string(what) + ": a tile list is longer than the bucketed sort holds (" +
-                   std::to_string(kBucketMaxList) + "); use the depth-presorted path.");
+  if (max_list < 0 || max_list > n_isects) return invalid(std::string(what) + ": invalid longest list.");
   CountLayout l;
   if (!count_workspace || count_workspace_bytes < count_layout(d, &l, const_cast<void*>(count_workspace))) {
     set_error(std::string(what) + ": count workspace too small.");
@@ -990,19 +1321,33 @@ int bucket_sort(bool ell, const float* means2d, const int32_t* radii, const floa
     // longer lists by their class, one launch per class present
     bucket_tile_sort_kernel<256, 10><<<grid, 256, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, d.n_tiles,
                                                            tile_bits, isect_ids, flatten_ids, tile_offsets);
-    const unsigned cgrid = grid;  // a block per list at most; blocks past the class's size exit at once
+    // a block per list of the class at most: every list of class k holds
+    // more than kSortCap[k - 1] entries, so at most n_isects / (kSortCap[k - 1]
+    // + 1) of them exist; blocks past the class's size exit at once
+    auto cgrid = [&](int k) {
+      return static_cast<unsigned>(std::min<int64_t>(n_lists, n_isects / (kSortCap[k - 1] + 1)));
+    };
     if (max_list > kSortCap[0])
-      bucket_tile_sort_class_kernel<512, 8><<<cgrid, 512, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, d.n_tiles,
-                                                                   tile_bits, isect_ids, flatten_ids, l.class_lists,
-                                                                   l.class_counts);
+      bucket_tile_sort_class_kernel<512, 8><<<cgrid(1), 512, 0, s>>>(pairs, l.tile_start, n_lists, n_isects,
+                                                                      d.n_tiles, tile_bits, isect_ids, flatten_ids,
+                                                                      l.class_lists, l.class_counts);
     if (max_list > kSortCap[1])
-      bucket_tile_sort_class_kernel<512, 16><<<cgrid, 512, 0, s>>>(
+      bucket_tile_sort_class_kernel<512, 16><<<cgrid(2), 512, 0, s>>>(
           pairs, l.tile_start, n_lists, n_isects, d.n_tiles, tile_bits, isect_ids, flatten_ids,
           l.class_lists + n_lists, l.class_counts + 1);
     if (max_list > kSortCap[2])
-      bucket_tile_sort_class_kernel<1024, 16><<<cgrid, 1024, 0, s>>>(
+      bucket_tile_sort_class_kernel<1024, 16><<<cgrid(3), 1024, 0, s>>>(
           pairs, l.tile_start, n_lists, n_isects, d.n_tiles, tile_bits, isect_ids, flatten_ids,
           l.class_lists + 2 * n_lists, l.class_counts + 2);
+    if (max_list > kSortCap[3]) {  // lists longer than LDS holds: a block each, taking the lists in turn
+      const unsigned hg = std::min(static_cast<unsigned>(n_isects / (kSortCap[3] + 1)), 2048u);
+      bucket_huge_sort_kernel<<<hg, kHugeBlock, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, d.n_tiles,
+                                                         tile_bits, isect_ids, flatten_ids,
+                                                         l.class_lists + 3 * n_lists, l.class_counts);
+      bucket_huge_radix_kernel<<<hg, kHugeBlock, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, d.n_tiles,
+                                                          tile_bits, isect_ids, flatten_ids,
+                                                          l.class_lists + 3 * n_lists, l.class_counts);
+    }
   }
   return check_launch(what);
 }

@@ -41,7 +41,7 @@ __device__ __forceinline__ TileRect aabb_tile_rect(float mx, float my, int rx, i
 // IntersectTile.cu, Task_Metal.md:95-115). The method is Speedy-Splat's
 // SnugBox + AccuTile (Hanson et al., CVPR 2025): a Gaussian only needs the
 // tiles where some pixel centre can pass the rasterizer's alpha test,
-// alpha = min(0.999, o exp(-sigma)) >= 1/255, sigma = d^T Q d / 2 with Q the
+// alpha = min(0.99, o exp(-sigma)) >= 1/255, sigma = d^T Q d / 2 with Q the
 // conic. That holds inside the ellipse d^T Q d <= 2 ln(255 o); the test below
 // uses the same slack as the rasterizer's per-wave cull, 1.05 ln(255 o) +
 // 1e-4, and the same conditions under which a conic is never culled, so

@@ -354,11 +354,13 @@ int gsplat_hip_isect_encode_sorted(const float* means2d, const int32_t* radii, c
  *    NULL, the tile offsets [I, tile_height, tile_width] (what
  *    gsplat_hip_isect_offset returns for those ids). Needs the count workspace
  *    of the same inputs and a workspace of
- *    gsplat_hip_isect_bucket_sort_workspace_size(M) bytes.
+ *    gsplat_hip_isect_bucket_sort_workspace_size(M) bytes. Lists of up to
+ *    gsplat_hip_isect_bucket_max_list() entries are sorted in LDS, longer ones
+ *    split by their leading depth bits into runs sorted in LDS (or, when the
+ *    split leaves a run too long, sorted in global memory).
  * Supported when gsplat_hip_isect_bucket_supported(I, tile_width, tile_height)
- * (tile grids up to about 35,000 corner points per image) and the longest list
- * is at most gsplat_hip_isect_bucket_max_list() entries; otherwise use the
- * depth-presorted entry points below (bucket_sort rejects a longer max_list). */
+ * (tile grids up to about 35,000 corner points per image); otherwise use the
+ * depth-presorted entry points below. */
 int gsplat_hip_isect_bucket_supported(int64_t I, int32_t tile_width, int32_t tile_height);
 int64_t gsplat_hip_isect_bucket_max_list(void);
 size_t gsplat_hip_isect_bucket_count_workspace_size(int64_t I, int64_t numel, int32_t tile_size,

@@ -1,7 +1,7 @@
 """GPU parity for the ellipse ("AccuTile") tile intersection: counts, keys,
 sorted order and tile offsets bit-exact with the oracle, in both encode
 orders, through the C ABI of both sorted pipelines (tile buckets, the
-default, and the depth-presorted path for long lists and large tile grids); rendering through the AccuTile lists equals
+default, and the depth-presorted path for large tile grids); rendering through the AccuTile lists equals
 rendering through the AABB lists (images bit-exact, gradients to 1e-4: the
 per-Gaussian sums run over fewer tiles, in another order)."""
 import ctypes
@@ -260,11 +260,11 @@ def test_bucket_c_abi(oracle, I, N, W, H, ties, culled):
 
 
 def test_bucket_long_list_and_grid_limit(oracle):
-    """A tile list longer than the tile sort holds (20,000 ellipses on one
-    tile): the C ABI rejects the bucketed sort and intersect_tile_forward
-    takes the depth-presorted ellipse path. A tile grid the ellipse bucket
-    path does not support (201 x 131 corner points) takes the same path. Both
-    give the oracle's lists; supported() marks the grid limit."""
+    """A tile list longer than the LDS tile sort holds (20,000 ellipses on one
+    tile, a quarter at one depth): the bucketed C ABI sorts it (split by the
+    leading depth bits into LDS-sorted runs). A tile grid the ellipse bucket
+    path does not support (201 x 131 corner points) takes the depth-presorted
+    path. Both give the oracle's lists; supported() marks the grid limit."""
     lib = _bucket_lib()
     assert lib.gsplat_hip_isect_bucket_accutile_supported(1, 160, 90)      # 2560x1440 at 16 px
     assert not lib.gsplat_hip_isect_bucket_accutile_supported(1, 200, 130)
@@ -277,19 +277,47 @@ def test_bucket_long_list_and_grid_limit(oracle):
     op = rng.uniform(0.2, 1.0, (1, n)).astype(np.float32)
     d = rng.uniform(1, 9, (1, n)).astype(np.float32)
     d[:, ::4] = 3.0
-    rc, M, longest, *_ = _bucket(lib, m, r, co, op, d, 1, 4, 4)
-    assert longest > 16384 and rc == 1 and b"longer" in lib.gsplat_hip_last_error()
+    rc, M, longest, tpg, ids, flat, offs = _bucket(lib, m, r, co, op, d, 1, 4, 4)
+    assert rc == 0, lib.gsplat_hip_last_error()
+    assert longest > 16384
+    ref = oracle.isect_tile(m, r, d, 1, TS, 4, 4, sort=True, conics=co, opacities=op)
+    np.testing.assert_array_equal(ids, ref["isect_ids"])
+    np.testing.assert_array_equal(flat, ref["flatten_ids"])
+    np.testing.assert_array_equal(offs, oracle.isect_offset(ref["isect_ids"], 1, 4, 4))
     cases = [(m, r, co, op, d, 4, 4)]
     sm, sr, sc, so, sd = projected_scene(rng, 1, 3000, 3200, 2080)
     cases.append((sm, sr, sc, so, sd, 200, 130))
     for cm, cr, cc, cop, cd, tw, th in cases:
-        print(f"accutile presorted fallback n={cd.size} grid {tw}x{th}", flush=True)
+        print(f"accutile intersect_tile_offsets n={cd.size} grid {tw}x{th}", flush=True)
         out = g._gsplat_core.intersect_tile_offsets_forward(_inputs(cm, cr, cd, cc, cop), 1, TS, tw, th)
         ref = oracle.isect_tile(cm, cr, cd, 1, TS, tw, th, sort=True, conics=cc, opacities=cop)
         np.testing.assert_array_equal(host(out["tiles_per_gauss"]), ref["tiles_per_gauss"])
         np.testing.assert_array_equal(host(out["isect_ids"]), ref["isect_ids"])
         np.testing.assert_array_equal(host(out["flatten_ids"]), ref["flatten_ids"])
         np.testing.assert_array_equal(host(out["tile_offsets"]), oracle.isect_offset(ref["isect_ids"], 1, tw, th))
+
+
+def test_bucket_largest_ellipse_grid(oracle):
+    """The largest tile grid the ellipse bucket path accepts (37 x 691 =
+    25,567 corner points: the scatter's dynamic LDS plus its static block-scan
+    words fill the 160 KiB workgroup LDS) runs count and sort through the C
+    ABI and gives the oracle's lists; one more tile row is refused."""
+    lib = _bucket_lib()
+    tw, th = 36, 690
+    assert lib.gsplat_hip_isect_bucket_accutile_supported(1, tw, th)
+    assert not lib.gsplat_hip_isect_bucket_accutile_supported(1, tw, th + 1)
+    rng = np.random.default_rng(25567)
+    W, H = tw * TS, th * TS
+    means, radii, conics, opac, depths = projected_scene(rng, 1, 4000, W, H)
+    print(f"bucket accutile largest grid {tw}x{th}", flush=True)
+    rc, M, longest, tpg, ids, flat, offs = _bucket(lib, means, radii, conics, opac, depths, 1, tw, th)
+    assert rc == 0, lib.gsplat_hip_last_error()
+    ref = oracle.isect_tile(means, radii, depths, 1, TS, tw, th, sort=True, conics=conics, opacities=opac)
+    assert M == ref["isect_ids"].size
+    np.testing.assert_array_equal(tpg, ref["tiles_per_gauss"].ravel())
+    np.testing.assert_array_equal(ids, ref["isect_ids"])
+    np.testing.assert_array_equal(flat, ref["flatten_ids"])
+    np.testing.assert_array_equal(offs, oracle.isect_offset(ref["isect_ids"], 1, tw, th))
 
 
 @pytest.mark.parametrize("name", ["sh3_1m", "multiview_3m"])

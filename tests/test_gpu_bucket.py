@@ -2,11 +2,11 @@
 against the oracle, bit for bit: tiles_per_gauss, the sorted isect_ids and
 flatten_ids, the tile offsets, the count M and the longest tile list. Scenes
 cover several images, 8x8 tiles, depth ties (the tile sort's (depth, id)
-re-sort), negative and signed-zero depths, empty input, and every capacity of
+re-sort), negative and signed-zero depths, empty input, every capacity of
 the per-tile LDS sort (lists up to 2560, 4096, 8192 and 16384 entries, one
-class at a time and all in one call); a
-list longer than 16384 is rejected by the C ABI and sorted by the
-depth-presorted path in intersect_tile_forward."""
+class at a time and all in one call), and lists longer than 16384 (split by
+their leading depth bits into LDS-sorted runs, or sorted in global memory
+when one digit is too crowded) beside short ones in one frame."""
 import ctypes
 import os
 
@@ -164,27 +164,63 @@ def test_bucket_empty_and_limits(oracle):
 
 
 def test_list_longer_than_the_tile_sort(oracle):
-    """20000 Gaussians on one tile: the C ABI rejects the bucketed sort, and
-    intersect_tile_forward sorts by the depth-presorted path instead, with
-    the oracle's result."""
-    import torch
-
+    """20000 Gaussians on one tile, a quarter of them at one depth: the
+    bucketed sort splits the list by its leading depth bits and sorts the
+    runs in LDS (the quarter at one depth exceeds no run: the (id, depth)
+    re-sort of a run); the same list with every depth equal goes to the
+    global-memory radix sort (ids only). Both through the C ABI and
+    intersect_tile_forward, against the oracle."""
     lib = _lib()
+    g = gsplat()
     rng = np.random.default_rng(4)
     n = 20000
     m = np.stack([rng.uniform(17, 31, n), rng.uniform(17, 31, n)], -1).astype(np.float32)[None]
     r = np.full((1, n, 2), 2, np.int32)
     d = rng.uniform(1, 9, (1, n)).astype(np.float32)
     d[:, ::4] = 3.0
-    rc, M, longest, *_ = bucket(lib, m, r, d, 1, 16, 4, 4)
-    assert longest > 16384 and rc == 1 and b"longer" in lib.gsplat_hip_last_error()
-    g = gsplat()
-    out = g.intersect_tile_forward({"means2d": dev(m), "radii": dev(r), "depths": dev(d)}, 1, 16, 4, 4)
-    exp = oracle.isect_tile(m, r, d, 1, 16, 4, 4, sort=True)
-    np.testing.assert_array_equal(host(out["isect_ids"]), exp["isect_ids"])
-    np.testing.assert_array_equal(host(out["flatten_ids"]), exp["flatten_ids"])
-    np.testing.assert_array_equal(host(out["tiles_per_gauss"]), exp["tiles_per_gauss"])
-    del torch
+    for depths in (d, np.full_like(d, 5.0)):
+        print(f"bucket long list, {np.unique(depths).size} distinct depths", flush=True)
+        M, longest = _check(oracle, lib, m, r, depths, 1, 16, 4, 4)
+        assert longest > 16384
+        out = g.intersect_tile_forward({"means2d": dev(m), "radii": dev(r), "depths": dev(depths)}, 1, 16, 4, 4)
+        exp = oracle.isect_tile(m, r, depths, 1, 16, 4, 4, sort=True)
+        np.testing.assert_array_equal(host(out["isect_ids"]), exp["isect_ids"])
+        np.testing.assert_array_equal(host(out["flatten_ids"]), exp["flatten_ids"])
+        np.testing.assert_array_equal(host(out["tiles_per_gauss"]), exp["tiles_per_gauss"])
+
+
+def test_short_and_long_lists_in_one_frame(oracle):
+    """Lists longer than the LDS tile sorts hold beside short lists and lists
+    of every LDS class in one frame of two images: 20000 Gaussians on one
+    tile (a quarter at one depth: split into LDS-sorted runs), 40000 on
+    another (half of them at one depth, so one digit of the leading bits
+    holds more than a run: the global-memory radix sort with its id
+    re-sort), crowds of 3500 and 12000, and a random background; bit for bit
+    against the oracle."""
+    from test_gpu_isect import random_projected
+
+    lib = _lib()
+    rng = np.random.default_rng(40)
+    I, W, H, ts = 2, 256, 192, 16
+    tw, th = W // ts, H // ts
+    m, r, d = random_projected(rng, I, 5000, W, H, ties=False)
+    parts = [(m, r, d)]
+    for n, cx, cy, kind in [(20000, 24, 24, "tie"), (40000, 200, 120, "crowded"), (3500, 120, 40, "flat"),
+                            (12000, 72, 168, "tie")]:
+        cm = np.stack([rng.uniform(cx - 6, cx + 6, (I, n)), rng.uniform(cy - 6, cy + 6, (I, n))], -1)
+        cr = rng.integers(1, 3, (I, n, 2))
+        cd = rng.uniform(1, 90, (I, n)) if kind == "crowded" else rng.uniform(1, 9, (I, n))
+        if kind == "tie":
+            cd[:, ::4] = 3.0
+        if kind == "crowded":
+            cd[:, ::2] = 30.0
+        parts.append((cm.astype(np.float32), cr.astype(np.int32), cd.astype(np.float32)))
+    m = np.concatenate([p[0] for p in parts], 1)
+    r = np.concatenate([p[1] for p in parts], 1)
+    d = np.concatenate([p[2] for p in parts], 1)
+    print(f"bucket short and long lists N={d.shape[1]}", flush=True)
+    M, longest = _check(oracle, lib, m, r, d, I, ts, tw, th)
+    assert longest > 2 * 16384
 
 
 @pytest.mark.parametrize("step", [0.25, 2.0])
