@@ -212,6 +212,8 @@ def main():
     last = out["last_ids"].reshape(n_img, H, W).long()
     e_fwd_max = int(torch.sum(end_p - start_p))  # entries examined without early termination
     e_bwd = int(torch.clamp(torch.minimum(last, end_p - 1) - start_p + 1, min=0).sum())
+    e_fwd = count_forward_evals(prof.lib, torch, R, scene, means, quats, log_scales, opacity_logits, viewmats, Ks,
+                                out, W, H, ts)
     K = (scene.sh_degree + 1) ** 2 if sh else 0
     NC = N * n_img  # projected (Gaussian, camera) pairs
     P = n_img * W * H
@@ -219,9 +221,23 @@ def main():
     # bytes read once + written once, or FP32 flops for the rasterizer (the
     # reference's per-evaluation operation counts x the evaluations up to
     # each pixel's last contributor).
+    blocks, grid_words = bucket_blocks(NC, N, n_img, tw, th)
+    n_tiles = n_img * tw * th
     units = {
         "raster_bwd": ("flops", BWD_FLOPS_PER_EVAL * e_bwd),
-        "raster_fwd": ("flops", FWD_FLOPS_PER_EVAL * e_bwd),
+        "raster_fwd": ("flops", FWD_FLOPS_PER_EVAL * e_fwd),
+        # tile buckets: per (camera, Gaussian) pair 16 B of means2d and radii
+        # in and 4 B of tiles_per_gauss out, plus each grid / scatter block's
+        # difference grid of (tw + 1)(th + 1) words (written, scanned in place,
+        # read); the tile pass reads each image's total grid and writes the
+        # tile starts; the scatter also reads the depths and writes an 8-byte
+        # (depth bits, flatten id) pair per entry; the tile sort reads the pairs
+        # and the tile starts and writes the 64-bit ids, the flatten ids and
+        # the tile offsets
+        "isect_bucket_grid": ("bytes", 20 * NC + 4 * blocks * grid_words),
+        "isect_bucket_scan": ("bytes", 8 * blocks * grid_words + 4 * n_img * grid_words + 4 * n_tiles),
+        "isect_bucket_scatter": ("bytes", 20 * NC + 4 * blocks * grid_words + 8 * M),
+        "isect_bucket_tile_sort": ("bytes", 20 * M + 8 * n_tiles),
         # the activated projection also reads the opacity logits and writes
         # the opacities (forward), reads them and the opacity cotangent and
         # writes the logits' gradient (backward)
@@ -281,16 +297,20 @@ def main():
                         "lds_broadcast_attainable": lds}
             if "raster_fwd" in per_step and "raster_bwd" in per_step:
                 t_fb = (per_step["raster_fwd"][1] + per_step["raster_bwd"][1]) * 1e-3
-                fb = (FWD_FLOPS_PER_EVAL + BWD_FLOPS_PER_EVAL) * e_bwd / t_fb / 1e12
+                fb = (FWD_FLOPS_PER_EVAL * e_fwd + BWD_FLOPS_PER_EVAL * e_bwd) / t_fb / 1e12
+                fw = FWD_FLOPS_PER_EVAL * e_fwd / (per_step["raster_fwd"][1] * 1e-3) / 1e12
                 roofline["raster_fwd_bwd"] = {"achieved": round(fb, 3), "frac_of_attainable": round(fb / att, 4),
                                               "ms": round(t_fb * 1e3, 4)}
+                roofline["raster_fwd"] = {"achieved": round(fw, 3), "frac_of_attainable": round(fw / att, 4),
+                                          "ms": round(per_step["raster_fwd"][1], 4), "e_fwd": e_fwd}
         else:
             achieved = per_launch / (avg_ms * 1e-3) / 1e9
             roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                         "frac": round(achieved / HBM_PEAK_GBS, 4),
                         "traffic": measured_traffic(args.workload, dom), "kernel": dom,
                         "avg_ms": round(avg_ms, 4)}
-    log(f"[bench] N={N} M={M} E_fwd(no termination)={e_fwd_max} E_bwd={e_bwd} dominant={dom} {avg_ms:.4f} ms")
+    log(f"[bench] N={N} M={M} E_fwd={e_fwd} (without termination {e_fwd_max}) E_bwd={e_bwd} dominant={dom} "
+        f"{avg_ms:.4f} ms")
 
     # The same step with ellipse (AccuTile) tile lists: the same images from
     # fewer intersections. Reported beside the headline (which keeps the
@@ -373,10 +393,19 @@ def main():
         log(f"[bench] l1_dssim: {ms_d:.3f} ms/step {loss_stages}")
 
     cpu = None
-    if not args.no_cpu_baseline and n_img == 1:
-        cpu = cpu_baseline(scene, args.cpu_band_rows, args.cpu_repeats, mpix)
-    elif not args.no_cpu_baseline:
-        log("[bench] cpu baseline: single-camera workloads only")
+    if not args.no_cpu_baseline:
+        if n_img == 1:
+            cpu = cpu_baseline(scene, args.cpu_band_rows, args.cpu_repeats, mpix)
+        else:
+            # the oracle renders one camera at a time (the reference's CPU
+            # loops do): camera 0 of the batch, whose rate is the batch's
+            import dataclasses
+
+            one = dataclasses.replace(scene, viewmats=scene.viewmats[:, :1], Ks=scene.Ks[:, :1],
+                                      target=None if scene.target is None else scene.target[:1])
+            cpu = cpu_baseline(one, args.cpu_band_rows, args.cpu_repeats, W * H / 1e6)
+            cpu["sample"] = (f"camera 0 of the {n_img} (the CPU loops render one camera at a time, so this camera's "
+                             f"rate is the batch's): " + cpu["sample"])
 
     line = {
         "metric": "fwd+bwd ms/frame & Mpix/s, 1M Gaussians SH3 1297x840; % of HBM/VALU roofline",
@@ -404,6 +433,43 @@ def main():
         "kernels_us_per_step": {k: round(v[1] * 1000, 1) for k, v in sorted(per_step.items())},
     }
     print(json.dumps(line), flush=True)
+
+
+def bucket_blocks(pairs, n, images, tw, th):
+    """Grid / scatter blocks of the tile-bucket intersection and the words of
+    one difference grid, as the library sizes them (bucket.hip bucket_dims)."""
+    want = (pairs + 511) // 512
+    gpb = min(16, max(1, (want + 1023) // 1024)) * 1024
+    return images * max(1, (n + gpb - 1) // gpb), (tw + 1) * (th + 1)
+
+
+def count_forward_evals(lib, torch, R, scene, means, quats, log_scales, opacity_logits, viewmats, Ks, out, W, H,
+                        ts):
+    """E_f, the (pixel, list entry) evaluations of the reference's forward loop
+    up to each pixel's termination, counted exactly on the GPU by the
+    library's counting kernel over the step's lists (the projection is
+    recomputed: it is deterministic)."""
+    C = viewmats.shape[1]
+    with torch.no_grad():
+        proj = R.activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks, W, H, eps2d=0.3,
+                                      near_plane=0.01, far_plane=scene.far_plane,
+                                      opacities_in_projection=scene.opacities_in_projection)
+        opac = proj["opacities"][:, None].expand(-1, C, -1).contiguous()
+    th, tw = out["tile_offsets"].shape[-2:]
+    evals = torch.zeros(C * th * tw, dtype=torch.int64, device="cuda")
+    lib.gsplat_hip_rasterize_count_evals.restype = ctypes.c_int
+    P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    lib.gsplat_hip_rasterize_count_evals.argtypes = [P, P, P, P, P, P, I64, I64, I32, I32, I32, I32, I32, I64, P, P]
+    m2 = proj["means2d"].contiguous()
+    co = proj["conics"].contiguous()
+    to = out["tile_offsets"].contiguous()
+    fl = out["flatten_ids"].contiguous()
+    rc = lib.gsplat_hip_rasterize_count_evals(m2.data_ptr(), co.data_ptr(), opac.data_ptr(), None, to.data_ptr(),
+                                              fl.data_ptr(), C, C * scene.n, W, H, ts, tw, th, fl.numel(),
+                                              evals.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    if rc != 0:
+        raise RuntimeError("rasterize_count_evals failed")
+    return int(evals.sum())
 
 
 def valu_attainable_tflops(lib, torch):

@@ -1330,6 +1330,69 @@ __global__ void __launch_bounds__(1024) raster_indices_kernel(RasterArgs a, int6
   if (!WRITE && inside) counts[pix] = cnt;
 }
 
+// E_f of the forward, per tile: the (pixel, list entry) evaluations of the
+// reference's per-pixel loop (gsplat_rasterize.cpp:291-368) -- every entry of
+// the pixel's tile list up to and including the one whose alpha would take
+// the transmittance to 1e-4 -- summed over the tile's pixels into
+// tile_evals[image, tile] (0 for a masked tile). The falloff, exp and
+// thresholds are the forward's. This measures the work the rasterizer's
+// roofline is priced on; the forward itself skips records that cannot touch a
+// wave's pixels and stops at the block's last saturated pixel.
+__global__ void __launch_bounds__(1024) raster_count_kernel(RasterArgs a, int64_t* __restrict__ tile_evals) {
+  __shared__ float4 s_co[1024];
+  __shared__ float2 s_xy[1024];
+  __shared__ int64_t s_sum[1024 / kWave];
+  const int tx = blockIdx.x, ty = blockIdx.y;
+  const int64_t image = blockIdx.z;
+  const int t = threadIdx.x;
+  const int bs = blockDim.x;
+  const int tile = ty * a.tw + tx;
+  const int64_t n_tiles = static_cast<int64_t>(a.tw) * a.th;
+  const int x = tx * a.ts + t % a.ts, y = ty * a.ts + t / a.ts;
+  const bool inside = t < a.ts * a.ts && x < a.W && y < a.H;
+  const bool masked = a.masks && !a.masks[image * n_tiles + tile];
+  int64_t start, end;
+  tile_range(a, image, tile, &start, &end);
+  const float px = static_cast<float>(x) + 0.5f, py = static_cast<float>(y) + 0.5f;
+  float T = 1.0f;
+  bool done = !inside || masked;
+  int64_t cnt = 0;
+  for (int64_t b = start; b < end; b += bs) {
+    if (__syncthreads_count(!done) == 0) break;
+    const int64_t j = b + t;
+    if (j < end) {
+      float2 xy;
+      float4 co;
+      load_gaussian(a, j, &xy, &co);
+      s_xy[t] = xy;
+      s_co[t] = co;
+    }
+    __syncthreads();
+    const int n = static_cast<int>(min<int64_t>(bs, end - b));
+    for (int k = 0; k < n && !done; ++k) {
+      ++cnt;
+      const float4 co = s_co[k];
+      const float dx = s_xy[k].x - px;
+      const float dy = s_xy[k].y - py;
+      const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
+      const float alpha = fminf(kMaxAlpha, co.w * exp_alpha(-sigma));
+      if (sigma < 0.0f || alpha < kAlphaThreshold) continue;
+      const float next_T = T * (1.0f - alpha);
+      if (next_T <= kTransmittanceThreshold) done = true;
+      T = next_T;
+    }
+  }
+#pragma unroll
+  for (int off = 1; off < kWave; off <<= 1) cnt += __shfl_xor(cnt, off, kWave);
+  if (t % kWave == 0) s_sum[t / kWave] = cnt;
+  __syncthreads();
+  if (t == 0) {
+    int64_t sum = 0;
+    for (int w = 0; w < bs / kWave; ++w) sum += s_sum[w];
+    tile_evals[image * n_tiles + tile] = sum;
+  }
+}
+
 // out[i] = exp_alpha(y[i]) (the rasterizer's exp, for unit tests).
 __global__ void __launch_bounds__(256) exp_alpha_kernel(const float* __restrict__ y, int64_t n,
                                                         float* __restrict__ out) {
@@ -1341,6 +1404,26 @@ __global__ void __launch_bounds__(256) exp_alpha_kernel(const float* __restrict_
 }  // namespace gsplat_hip
 
 using namespace gsplat_hip;
+
+extern "C" int gsplat_hip_rasterize_count_evals(const float* means2d, const float* conics, const float* opacities,
+                                                const uint8_t* masks, const int32_t* tile_offsets,
+                                                const int32_t* flatten_ids, int64_t I, int64_t G,
+                                                int32_t image_width, int32_t image_height, int32_t tile_size,
+                                                int32_t tile_width, int32_t tile_height, int64_t n_isects,
+                                                int64_t* tile_evals, void* stream) {
+  RasterArgs a{means2d, conics, nullptr, opacities, nullptr, masks, tile_offsets, flatten_ids, G, 1,
+               image_width, image_height, tile_size, tile_width, tile_height, I, n_isects, G};
+  int rc = check_args(a, "rasterize_count_evals");
+  if (rc) return rc;
+  if (G < 0) return invalid("rasterize_count_evals: invalid sizes.");
+  if (I == 0 || tile_width == 0 || tile_height == 0) return GSPLAT_OK;
+  if (!tile_offsets || !tile_evals || (n_isects > 0 && (!flatten_ids || !means2d || !conics || !opacities)))
+    return invalid("rasterize_count_evals: null pointer.");
+  const dim3 grid(tile_width, tile_height, static_cast<unsigned>(I));
+  const int bs = (tile_size * tile_size + kWave - 1) / kWave * kWave;
+  raster_count_kernel<<<grid, bs, 0, as_stream(stream)>>>(a, tile_evals);
+  return check_launch("rasterize_count_evals");
+}
 
 extern "C" int gsplat_hip_exp_alpha_eval(const float* y, int64_t n, float* out, void* stream) {
   if (n < 0) return invalid("exp_alpha_eval: negative size.");

@@ -474,6 +474,18 @@ int gsplat_hip_rasterize_fwd(const float* means2d, const float* conics, const fl
                              int32_t tile_width, int32_t tile_height, int64_t n_isects,
                              float* render_colors, float* render_alphas, int32_t* last_ids,
                              void* stream);
+/* Measurement, no counterpart in the reference: E_f, the (pixel, list entry)
+ * evaluations of the reference's forward loop (gsplat_rasterize.cpp:291-368:
+ * every entry of a pixel's tile list up to and including the one that takes
+ * its transmittance to 1e-4), per tile into tile_evals [I, tile_height,
+ * tile_width] (int64). Inputs as gsplat_hip_rasterize_fwd (G Gaussian rows;
+ * colours are not needed). The unit of work the rasterizer's roofline is
+ * priced on. */
+int gsplat_hip_rasterize_count_evals(const float* means2d, const float* conics, const float* opacities,
+                                     const uint8_t* masks, const int32_t* tile_offsets,
+                                     const int32_t* flatten_ids, int64_t I, int64_t G, int32_t image_width,
+                                     int32_t image_height, int32_t tile_size, int32_t tile_width,
+                                     int32_t tile_height, int64_t n_isects, int64_t* tile_evals, void* stream);
 int gsplat_hip_rasterize_bwd(const float* means2d, const float* conics, const float* colors,
                              const float* opacities, const float* backgrounds,
                              const uint8_t* masks, const int32_t* tile_offsets,

@@ -964,12 +964,15 @@ int64_t encode_isect_id(int image_id, int tile_id, float depth, int tile_n_bits)
 // ---------------------------------------------------------------------------
 // Rasterization, gsplat_rasterize.cpp:249-369 (forward), 371-569 (backward).
 
+// tile_evals (optional, [I, tile_height, tile_width]): per tile, the loop
+// iterations of its pixels -- each entry evaluated before a pixel's
+// termination, the terminating entry included (E_f).
 template <typename T>
 void raster_forward(const T* means2d, const T* conics, const T* colors, const T* opacities,
                     const T* backgrounds, const uint8_t* masks, const int32_t* tile_offsets,
                     const int32_t* flatten_ids, int64_t I, int64_t channels, int W, int H,
                     int tile_size, int tile_width, int tile_height, int64_t n_isects,
-                    T* render_colors, T* render_alphas, int32_t* last_ids) {
+                    T* render_colors, T* render_alphas, int32_t* last_ids, int64_t* tile_evals = nullptr) {
   std::memset(render_colors, 0, sizeof(T) * I * H * W * channels);
   ORACLE_PARALLEL_TILES
   for (int64_t image = 0; image < I; ++image)
@@ -980,6 +983,7 @@ void raster_forward(const T* means2d, const T* conics, const T* colors, const T*
         const int64_t start = tile_offsets[oi];
         const int64_t end = (image == I - 1 && tile == tile_width * tile_height - 1) ? n_isects : tile_offsets[oi + 1];
         const bool skip = masks && !masks[oi];
+        int64_t evals = 0;
         for (int ly = 0; ly < tile_size; ++ly) {
           const int y = ty * tile_size + ly;
           if (y >= H) continue;
@@ -992,6 +996,7 @@ void raster_forward(const T* means2d, const T* conics, const T* colors, const T*
             int32_t cur = 0;
             T* out = render_colors + pix * channels;
             for (int64_t idx = start; !skip && idx < end; ++idx) {
+              ++evals;
               const int64_t g = flatten_ids[idx];
               const T dx = means2d[g * 2] - px;
               const T dy = means2d[g * 2 + 1] - py;
@@ -1012,6 +1017,7 @@ void raster_forward(const T* means2d, const T* conics, const T* colors, const T*
             last_ids[pix] = cur;
           }
         }
+        if (tile_evals) tile_evals[oi] = evals;
       }
 }
 
@@ -1180,10 +1186,10 @@ void raster_backward(const T* means2d, const T* conics, const T* colors, const T
       const T* backgrounds, const uint8_t* masks, const int32_t* tile_offsets,                   \
       const int32_t* flatten_ids, int64_t I, int64_t channels, int W, int H, int tile_size,      \
       int tile_width, int tile_height, int64_t n_isects, T* render_colors, T* render_alphas,     \
-      int32_t* last_ids) {                                                                       \
+      int32_t* last_ids, int64_t* tile_evals) {                                                  \
     raster_forward<T>(means2d, conics, colors, opacities, backgrounds, masks, tile_offsets,      \
                       flatten_ids, I, channels, W, H, tile_size, tile_width, tile_height,        \
-                      n_isects, render_colors, render_alphas, last_ids);                         \
+                      n_isects, render_colors, render_alphas, last_ids, tile_evals);             \
   }                                                                                              \
   extern "C" void oracle_raster_bwd_##SFX(                                                       \
       const T* means2d, const T* conics, const T* colors, const T* opacities,                   \

@@ -469,11 +469,14 @@ def raster_forward(means2d, conics, colors, opacities, tile_offsets, flatten_ids
     bg = _c(backgrounds, dt) if backgrounds is not None and np.size(backgrounds) else None
     mk = np.ascontiguousarray(masks, dtype=np.uint8) if masks is not None and np.size(masks) else None
     fl = _c(flatten_ids, np.int32)
+    ev = np.zeros(to.shape, np.int64)
     _fn(f"oracle_raster_fwd_{_sfx(dt)}")(
         _ptr(_c(means2d, dt)), _ptr(_c(conics, dt)), _ptr(_c(colors, dt)), _ptr(_c(opacities, dt)), _ptr(bg),
         _ptr(mk), _ptr(to), _ptr(fl), I64(I), I64(ch), image_width, image_height, tile_size, tw, th,
-        I64(fl.size), _ptr(rc), _ptr(ra), _ptr(li))
-    return {"render_colors": rc, "render_alphas": ra, "last_ids": li}
+        I64(fl.size), _ptr(rc), _ptr(ra), _ptr(li), _ptr(ev))
+    # tile_evals: per tile, the forward loop's iterations over its pixels
+    # (entries evaluated up to each pixel's termination, E_f)
+    return {"render_colors": rc, "render_alphas": ra, "last_ids": li, "tile_evals": ev}
 
 
 def raster_backward(means2d, conics, colors, opacities, tile_offsets, flatten_ids, image_width, image_height,

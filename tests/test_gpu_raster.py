@@ -306,3 +306,40 @@ def test_ill_conditioned_records_far_from_the_mean(oracle):
         a, e = host(bwd[k]), eb[k]
         np.testing.assert_array_equal(np.isfinite(a), np.isfinite(e), err_msg=k)
         assert_close_rel(np.where(np.isfinite(e), a, 0), np.where(np.isfinite(e), e, 0), GRAD_RTOL, k)
+
+
+@pytest.mark.parametrize("I,N,W,H,ts,masks,opac", [(1, 3000, 256, 256, 16, False, (0.05, 0.95)),
+                                                   (2, 1500, 200, 120, 16, True, (0.05, 0.95)),
+                                                   (1, 4000, 128, 128, 16, False, (0.9, 0.99)),
+                                                   (1, 2000, 100, 90, 8, False, (0.5, 0.99))])
+def test_count_evals_vs_oracle(oracle, I, N, W, H, ts, masks, opac):
+    """gsplat_hip_rasterize_count_evals (E_f, the forward loop's evaluations up
+    to each pixel's termination, per tile) equals the oracle's count of its
+    own forward loop, tile for tile, with masks, several images, saturating
+    scenes and 8-pixel tiles."""
+    import ctypes
+    import os
+
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "gsplat-mlx_amd",
+                                   "gsplat_core", "libgsplat_hip.so"))
+    lib.gsplat_hip_last_error.restype = ctypes.c_char_p
+    P, I64, I32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+    lib.gsplat_hip_rasterize_count_evals.argtypes = [P, P, P, P, P, P, I64, I64, I32, I32, I32, I32, I32, I64, P, P]
+    rng = np.random.default_rng(N + 7)
+    s = make_scene(oracle, rng, I, N, W, H, ts, 3, opac=opac, masks=masks)
+    exp = _oracle_fwd(oracle, s, W, H, ts)
+    th, tw = s["tile_offsets"].shape[-2:]
+    t = {k: dev(v) for k, v in s.items() if k in ("means2d", "conics", "opacities", "tile_offsets", "flatten_ids")}
+    mk = dev(s["masks"].astype(np.uint8)) if masks else None
+    out = torch.zeros(I * th * tw, dtype=torch.int64, device="cuda")
+    print(f"count evals I={I} N={N} {W}x{H} ts={ts}", flush=True)
+    rc = lib.gsplat_hip_rasterize_count_evals(
+        t["means2d"].data_ptr(), t["conics"].data_ptr(), t["opacities"].data_ptr(), mk.data_ptr() if masks else None,
+        t["tile_offsets"].data_ptr(), t["flatten_ids"].data_ptr(), I, I * N, W, H, ts, tw, th,
+        s["flatten_ids"].size, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.gsplat_hip_last_error()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(out).reshape(I, th, tw), exp["tile_evals"])
+    assert exp["tile_evals"].sum() > 0

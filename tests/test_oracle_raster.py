@@ -154,3 +154,53 @@ def test_backward_finite_differences(oracle, seed):
     T_final = 1 - fwd["render_alphas"]
     np.testing.assert_allclose(bwd["v_backgrounds"], np.sum(T_final * v_rc, axis=(1, 2)), rtol=1e-12)
     assert np.all(bwd["v_means2d_abs"] >= np.abs(bwd["v_means2d"]) - 1e-12)
+
+
+def test_tile_evals_pins(oracle):
+    """The oracle's per-tile E_f (the forward loop's iterations up to each
+    pixel's termination) on known answers: a lone Gaussian never saturates a
+    pixel, so every pixel evaluates the whole list; two opaque flat Gaussians
+    saturate every pixel at the second entry (T = (1 - 0.99)^2 < 1e-4), so
+    each pixel evaluates 2 of 4; a masked tile evaluates nothing. On a random
+    scene: a tile whose pixels all end with transmittance above 1e-2 (none can
+    have stopped: alpha <= 0.99) evaluates pixels x list length, and every
+    tile lies between its pixels' replayed prefixes (last_id - start + 1) and
+    pixels x list length."""
+    flat = np.array([[[1.0e-6, 0.0, 1.0e-6]]], np.float32)
+    for n, per_pixel in ((1, 1), (4, 2)):
+        s = dict(means2d=np.full((1, n, 2), 8.0, np.float32), conics=np.repeat(flat, n, 1),
+                 colors=np.ones((1, n, 3), np.float32), opacities=np.ones((1, n), np.float32))
+        offs = np.array([[[0, n]]], np.int32)
+        out = oracle.raster_forward(s["means2d"], s["conics"], s["colors"], s["opacities"], offs,
+                                    np.arange(n, dtype=np.int32), 32, 16, 16,
+                                    masks=np.array([[[True, False]]]))
+        assert out["tile_evals"].tolist() == [[[256 * per_pixel, 0]]]
+    rng = np.random.default_rng(3)
+    from test_gpu_raster import make_scene
+
+    I, W, H, ts = 1, 160, 96, 16
+    s = make_scene(oracle, rng, I, 300, W, H, ts, 3, opac=(0.3, 0.99))
+    out = oracle.raster_forward(s["means2d"], s["conics"], s["colors"], s["opacities"], s["tile_offsets"],
+                                s["flatten_ids"], W, H, ts)
+    th, tw = s["tile_offsets"].shape[-2:]
+    offs = s["tile_offsets"].ravel().astype(np.int64)
+    ends = np.append(offs[1:], s["flatten_ids"].size)
+    alphas = out["render_alphas"][0, :, :, 0]
+    last = out["last_ids"][0]
+    saturated = unsaturated = 0
+    for ty in range(th):
+        for tx in range(tw):
+            k = ty * tw + tx
+            n = ends[k] - offs[k]
+            a = alphas[ty * ts:(ty + 1) * ts, tx * ts:(tx + 1) * ts]
+            li = last[ty * ts:(ty + 1) * ts, tx * ts:(tx + 1) * ts]
+            ev = out["tile_evals"][0, ty, tx]
+            replayed = np.where(a > 0, li - offs[k] + 1, 0).sum()
+            assert replayed <= ev <= a.size * n
+            # a pixel that stops at an entry of alpha <= 0.99 ends with T <= 1e-4 / 0.01
+            if (1.0 - a).min() > 0.0101:
+                assert ev == a.size * n
+                unsaturated += 1
+            else:
+                saturated += 1
+    assert saturated > 0 and unsaturated > 0
