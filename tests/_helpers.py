@@ -29,17 +29,29 @@ def host(t):
     return t.detach().cpu().numpy()
 
 
-def assert_close_rel(actual, expected, rtol, name="", scale_floor=0.0):
-    """|a - e| <= rtol * max(|e|, s) elementwise with s = rtol-scaled norm floor:
-    relative to each element, but elements much smaller than the tensor's
-    largest magnitude are held to rtol * max|e| * 1e-2 (cancellation-prone
-    values carry no relative information)."""
+# Radii are ceil() of float expressions that the kernels evaluate in the
+# oracle's order; a last-ulp difference (sqrt, log of the opacity-aware
+# extent) can still move one across an integer. The parity tests count such
+# Gaussians, print the count and allow at most this many per check.
+MAX_RADIUS_FLIPS = 2
+
+FLOOR_ATOMIC = 1e-2  # sums whose float order differs from the oracle's (atomics, chained stages)
+FLOOR_ORDERED = 1e-4  # per-element results computed without atomics (projection, SH, activations)
+
+
+def assert_close_rel(actual, expected, rtol, name="", scale_floor=0.0, floor_rel=FLOOR_ATOMIC):
+    """|a - e| <= rtol * max(|e|, s) elementwise with s = max(floor_rel *
+    max|e|, scale_floor): relative to each element, but elements much smaller
+    than the tensor's largest magnitude are held to rtol * s absolute
+    (cancellation-prone values carry no relative information). Prints how
+    many elements meet the bar only through that floor (off by more than
+    rtol * |e|) and returns the count."""
     a = np.asarray(actual, np.float64)
     e = np.asarray(expected, np.float64)
     assert a.shape == e.shape, f"{name}: shape {a.shape} != {e.shape}"
     if e.size == 0:
-        return
-    floor = max(np.abs(e).max() * 1e-2, scale_floor)
+        return 0
+    floor = max(np.abs(e).max() * floor_rel, scale_floor)
     err = np.abs(a - e)
     tol = rtol * np.maximum(np.abs(e), floor)
     bad = err > tol
@@ -47,6 +59,10 @@ def assert_close_rel(actual, expected, rtol, name="", scale_floor=0.0):
         i = np.unravel_index(np.argmax(err - tol), e.shape)
         raise AssertionError(f"{name}: {bad.sum()} / {e.size} elements off; worst at {i}: got {a[i]!r}, "
                              f"expected {e[i]!r} (tol {tol[i]:.3g})")
+    via_floor = int(np.count_nonzero(err > rtol * np.abs(e)))
+    print(f"[parity] {name or 'tensor'}: rtol {rtol:g}, floor {floor_rel:g}*max; {via_floor} of {e.size} "
+          f"elements pass only through the floor", flush=True)
+    return via_floor
 
 
 def assert_close_rel_summation(actual, expected, rtol, name="", outlier_rtol=1e-2, outliers_per_million=1.0):

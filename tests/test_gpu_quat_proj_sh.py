@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 from scipy.spatial.transform import Rotation
 
-from _helpers import assert_close_rel, dev, gsplat, host
+from _helpers import FLOOR_ATOMIC, FLOOR_ORDERED, MAX_RADIUS_FLIPS, assert_close_rel, dev, gsplat, host
 
 pytestmark = pytest.mark.gpu
 
@@ -18,6 +18,21 @@ GRAD_RTOL = 1e-3
 
 
 # ------------------------------------------------------------------ quat/scale
+def _floor(camera_model, grad=False):
+    """The small-element floor of a projection check: 1e-4 of the largest
+    magnitude for the pinhole camera. The equidistant fisheye (camera model 2)
+    takes atan2 and sqrt from the device math library, which differ from the
+    host libm's in the last ulp; cancellation in near-zero means2d and
+    gradient elements turns that into ~1e-3 relative differences below 1e-2
+    of the largest magnitude. Orthographic gradients (camera model 1) are
+    sums of terms of the tensor's largest magnitude: measured differences
+    reach 1.8e-7 of that magnitude (about 3 float32 ulps), so elements below
+    1e-3 of it are held to 1e-6 of it."""
+    if camera_model == 2:
+        return FLOOR_ATOMIC
+    return 1e-3 if grad and camera_model == 1 else FLOOR_ORDERED
+
+
 def test_quat_known_answers():
     g = gsplat()
     quats = np.array([[1, 0, 0, 0], [2, 0, 0, 0]], np.float32)
@@ -39,22 +54,22 @@ def test_quat_random_vs_oracle(oracle, triu):
     scales = np.exp(rng.uniform(-3, 1, (n, 3))).astype(np.float32)
     out = g.quat_scale_to_covar_preci_forward({"quats": dev(quats), "scales": dev(scales)}, True, True, triu)
     ec, ep = oracle.quat_scale_to_covar_preci_forward(quats, scales, True, True, triu)
-    assert_close_rel(host(out["covars"]), ec, FWD_RTOL, "covars")
-    assert_close_rel(host(out["precis"]), ep, FWD_RTOL, "precis")
+    assert_close_rel(host(out["covars"]), ec, FWD_RTOL, "covars", floor_rel=FLOOR_ORDERED)
+    assert_close_rel(host(out["precis"]), ep, FWD_RTOL, "precis", floor_rel=FLOOR_ORDERED)
     shape = (n, 6) if triu else (n, 3, 3)
     vc = rng.normal(size=shape).astype(np.float32)
     vp = rng.normal(size=shape).astype(np.float32)
     bwd = g.quat_scale_to_covar_preci_backward({"quats": dev(quats), "scales": dev(scales)},
                                                {"v_covars": dev(vc), "v_precis": dev(vp)}, triu)
     eq, es = oracle.quat_scale_to_covar_preci_backward(quats, scales, vc, vp, triu)
-    assert_close_rel(host(bwd["v_quats"]), eq, GRAD_RTOL, "v_quats")
-    assert_close_rel(host(bwd["v_scales"]), es, GRAD_RTOL, "v_scales")
+    assert_close_rel(host(bwd["v_quats"]), eq, GRAD_RTOL, "v_quats", floor_rel=FLOOR_ORDERED)
+    assert_close_rel(host(bwd["v_scales"]), es, GRAD_RTOL, "v_scales", floor_rel=FLOOR_ORDERED)
     # only one cotangent
     bwd1 = g.quat_scale_to_covar_preci_backward({"quats": dev(quats), "scales": dev(scales)}, {"v_precis": dev(vp)},
                                                 triu)
     eq1, es1 = oracle.quat_scale_to_covar_preci_backward(quats, scales, None, vp, triu)
-    assert_close_rel(host(bwd1["v_quats"]), eq1, GRAD_RTOL, "v_quats precis-only")
-    assert_close_rel(host(bwd1["v_scales"]), es1, GRAD_RTOL, "v_scales precis-only")
+    assert_close_rel(host(bwd1["v_quats"]), eq1, GRAD_RTOL, "v_quats precis-only", floor_rel=FLOOR_ORDERED)
+    assert_close_rel(host(bwd1["v_scales"]), es1, GRAD_RTOL, "v_scales precis-only", floor_rel=FLOOR_ORDERED)
 
 
 def test_quat_errors():
@@ -115,13 +130,15 @@ def test_projection_forward_vs_oracle(oracle, B, C, use_covars, use_opac, calc_c
     # radii are ceil() of float expressions evaluated in the same order; a
     # log() ulp (opacity-aware extent) may flip one at an integer boundary
     flips = np.sum(np.any(r_got != r_exp, axis=-1))
-    assert flips <= max(1, r_exp.shape[-2] // 2000), f"{flips} radius mismatches"
+    print(f"[projection] radius flips: {flips} of {r_exp.shape[-2]}", flush=True)
+    assert flips <= MAX_RADIUS_FLIPS, f"{flips} radius mismatches"
     both = np.all(r_got > 0, -1) & np.all(r_exp > 0, -1)
     assert both.sum() > 100
     for k in ("means2d", "conics", "depths"):
-        assert_close_rel(host(got[k])[both], exp[k][both], FWD_RTOL, k)
+        assert_close_rel(host(got[k])[both], exp[k][both], FWD_RTOL, k, floor_rel=_floor(camera_model))
     if calc_comp:
-        assert_close_rel(host(got["compensations"])[both], exp["compensations"][both], FWD_RTOL, "compensations")
+        assert_close_rel(host(got["compensations"])[both], exp["compensations"][both], FWD_RTOL, "compensations",
+                         floor_rel=_floor(camera_model))
     else:
         assert tuple(got["compensations"].shape) == (0,)
     culled = np.all(r_got == 0, -1)
@@ -189,7 +206,7 @@ def test_projection_backward_vs_oracle(oracle, use_covars, calc_comp, C, camera_
                                    camera_model=camera_model)
     assert (radii > 0).any(axis=-1).sum() > 1000
     for k in e:
-        assert_close_rel(host(out[k]), e[k], GRAD_RTOL, k)
+        assert_close_rel(host(out[k]), e[k], GRAD_RTOL, k, floor_rel=_floor(camera_model, grad=True))
     # an absent v_depths means zeros
     cot0 = dict(cot, v_depths=dev(np.zeros_like(vd)))
     cot_absent = {k: v for k, v in cot.items() if k != "v_depths"}
@@ -236,14 +253,14 @@ def test_sh_vs_oracle(oracle, degree, K, use_masks):
         inputs["masks"] = dev(masks)
     got = host(g.spherical_harmonics_forward(degree, inputs))
     exp = oracle.sh_forward(degree, dirs, coeffs, masks)
-    assert_close_rel(got, exp, FWD_RTOL, "colors")
+    assert_close_rel(got, exp, FWD_RTOL, "colors", floor_rel=FLOOR_ORDERED)
     b = g.spherical_harmonics_backward(degree, inputs, {"v_colors": dev(v_colors)})
     ed, ec = oracle.sh_backward(degree, dirs, coeffs, v_colors, masks)
-    assert_close_rel(host(b["v_coeffs"]), ec, GRAD_RTOL, "v_coeffs")
-    assert_close_rel(host(b["v_dirs"]), ed, GRAD_RTOL, "v_dirs")
+    assert_close_rel(host(b["v_coeffs"]), ec, GRAD_RTOL, "v_coeffs", floor_rel=FLOOR_ORDERED)
+    assert_close_rel(host(b["v_dirs"]), ed, GRAD_RTOL, "v_dirs", floor_rel=FLOOR_ORDERED)
     nb = g.spherical_harmonics_backward(degree, inputs, {"v_colors": dev(v_colors)}, compute_v_dirs=False)
     assert "v_dirs" not in nb
-    assert_close_rel(host(nb["v_coeffs"]), ec, GRAD_RTOL, "v_coeffs (no dirs)")
+    assert_close_rel(host(nb["v_coeffs"]), ec, GRAD_RTOL, "v_coeffs (no dirs)", floor_rel=FLOOR_ORDERED)
 
 
 def test_sh_errors():

@@ -11,7 +11,7 @@ the clip masks cannot differ by rounding."""
 import numpy as np
 import pytest
 
-from _helpers import assert_close_rel, dev, gsplat, host
+from _helpers import FLOOR_ORDERED, assert_close_rel, dev, gsplat, host
 
 pytestmark = pytest.mark.gpu
 
@@ -108,13 +108,13 @@ def test_fused_vs_oracle(oracle, degree, B, C, R):
     inputs = {"means": dev(means), "viewmats": dev(vm), "features_dc": dev(dc), "features_rest": dev(rest)}
     colors = host(g._gsplat_core.sh_camera_colors_forward(degree, inputs))
     assert colors.shape == (B, C, N, 3)
-    assert_close_rel(colors, np.clip(raw + 0.5, 0, 1), FWD_RTOL, "colors")
+    assert_close_rel(colors, np.clip(raw + 0.5, 0, 1), FWD_RTOL, "colors", floor_rel=FLOOR_ORDERED)
     v_colors = rng.normal(size=(B, C, N, 3)).astype(np.float32)
     out = g._gsplat_core.sh_camera_colors_backward(degree, inputs, {"v_colors": dev(v_colors)})
     ev_means, ev_dc, ev_rest = _oracle_backward(oracle, degree, means, campos, coeffs, raw, dirs, norms, v_colors, R)
-    assert_close_rel(host(out["v_features_dc"]), ev_dc, GRAD_RTOL, "v_features_dc")
-    assert_close_rel(host(out["v_features_rest"]), ev_rest, GRAD_RTOL, "v_features_rest")
-    assert_close_rel(host(out["v_means"]), ev_means, GRAD_RTOL, "v_means")
+    assert_close_rel(host(out["v_features_dc"]), ev_dc, GRAD_RTOL, "v_features_dc", floor_rel=FLOOR_ORDERED)
+    assert_close_rel(host(out["v_features_rest"]), ev_rest, GRAD_RTOL, "v_features_rest", floor_rel=FLOOR_ORDERED)
+    assert_close_rel(host(out["v_means"]), ev_means, GRAD_RTOL, "v_means", floor_rel=FLOOR_ORDERED)
 
 
 def test_fused_matches_unfused_torch_autograd(oracle):
@@ -142,7 +142,7 @@ def test_fused_matches_unfused_torch_autograd(oracle):
     fused = run(Rn.sh_colors_for_camera)
     plain = run(Rn.sh_colors_for_camera_unfused)
     for a, e, name in zip(fused, plain, ["colors", "v_means", "v_dc", "v_rest"]):
-        assert_close_rel(a, e, FWD_RTOL if name == "colors" else GRAD_RTOL, name)
+        assert_close_rel(a, e, FWD_RTOL if name == "colors" else GRAD_RTOL, name, floor_rel=FLOOR_ORDERED)
     del torch
 
 

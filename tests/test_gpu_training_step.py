@@ -18,18 +18,20 @@ either loss.
 
 Bars: the parameter activations within 1e-6 relative of float64; projection
 outputs within 1e-5 relative of the oracle's on those activations (radius flips
-counted and printed, at most N/2000; the oracle's later stages take the
+counted and printed, at most MAX_RADIUS_FLIPS; the oracle's later stages take the
 GPU's radii), SH colours within 1e-5; tile counts, sorted ids, flatten ids
 and tile offsets bit-exact with the oracle's intersection of the GPU's
 projection; images within 1e-4 max-abs, last_ids exact; the loss within
 1e-6 (L1 + DSSIM: 1e-5 relative); every parameter gradient (means, quaternions, log-scales, opacity
 logits, SH features or colours, and the viewspace proxy) within 1e-3
-relative (floor 1e-2 of the tensor's largest magnitude)."""
+relative (floor 1e-2 of the tensor's largest magnitude: the rasterizer's float
+atomics sum in another order); activations and projection outputs with the
+1e-4 floor."""
 import numpy as np
 import pytest
 
 import _oracle_chain as ch
-from _helpers import assert_close_rel, dev, host
+from _helpers import FLOOR_ORDERED, MAX_RADIUS_FLIPS, assert_close_rel, dev, host
 from oracle import image_loss as il
 
 pytestmark = pytest.mark.gpu
@@ -103,17 +105,17 @@ def _check_forward(oracle, sc, fwd, C, sh):
     q32, s32, o32 = fwd["act"]
     for got, want, k in zip(fwd["act"], ch.activations(sc.quats, sc.log_scales, sc.opacity_logits),
                             ("quats", "scales", "opacities")):
-        assert_close_rel(got, want, 1e-6, k)
+        assert_close_rel(got, want, 1e-6, k, floor_rel=FLOOR_ORDERED)
     np.testing.assert_array_equal(fwd["opacities"], o32)
     pr = oracle.projection_forward(sc.means, sc.viewmats[:, :C], sc.Ks[:, :C], W, H, quats=q32, scales=s32,
                                    opacities=o32 if sc.opacities_in_projection else None, far_plane=sc.far_plane)
     on_g, on_o = (fwd["radii"] > 0).all(-1), (pr["radii"] > 0).all(-1)
     flips = int(np.sum(np.any(fwd["radii"] != pr["radii"], -1)))
     print(f"{sc.name}: N={N} C={C} visible={int(on_g.sum())} radius flips={flips}", flush=True)
-    assert flips <= max(1, N * C // 2000)
+    assert flips <= MAX_RADIUS_FLIPS, flips
     both = on_g & on_o
     for k in ("means2d", "depths", "conics"):
-        assert_close_rel(fwd[k][both], pr[k][both], 1e-5, k)
+        assert_close_rel(fwd[k][both], pr[k][both], 1e-5, k, floor_rel=FLOOR_ORDERED)
     if sh:
         col, _ = ch.sh_colours(oracle, sc.means, sc.features_dc, sc.features_rest, sc.viewmats[:, :C], sc.sh_degree)
         assert np.abs(fwd["colors"] - col).max() <= 1e-5
@@ -153,7 +155,8 @@ def _check_gradients(oracle, sc, fwd, grads, loss, C, sh, loss_mode="l1"):
 
 
 @pytest.mark.parametrize("loss_mode", ["l1", "l1_dssim"])
-@pytest.mark.parametrize("name,C,n,W,H", [("sh3_1m", 1, 8000, 320, 208), ("multiview_3m", 3, 6000, 240, 136)])
+@pytest.mark.parametrize("name,C,n,W,H", [("sh3_1m", 1, 8000, 320, 208), ("multiview_3m", 3, 6000, 240, 136),
+                                         ("multiview_3m", 8, 6000, 240, 136)])
 def test_sh_training_step_vs_oracle_chain(oracle, name, C, n, W, H, loss_mode):
     from gsplat_core.scenes import make_scene
 

@@ -12,7 +12,12 @@ def test_relative_bar_and_floor():
     with pytest.raises(AssertionError):
         assert_close_rel(e * (1 + 2e-3), e, 1e-3)
     # elements below 1e-2 of the largest magnitude are held to rtol * (1e-2 * 100)
-    assert_close_rel(e + np.array([0.0, 0.0, 5e-4]), e, 1e-3)
+    assert assert_close_rel(e + np.array([0.0, 0.0, 5e-4]), e, 1e-3) == 1
+    # the ordered-results floor, 1e-4 of the largest, holds them to 1e-5 absolute
+    with pytest.raises(AssertionError):
+        assert_close_rel(e + np.array([0.0, 0.0, 5e-4]), e, 1e-3, floor_rel=1e-4)
+    assert assert_close_rel(e + np.array([0.0, 0.0, 5e-6]), e, 1e-3, floor_rel=1e-4) == 1
+    assert assert_close_rel(e * (1 + 9e-4), e, 1e-3, floor_rel=1e-4) == 0
 
 
 def test_summation_outlier_budget():
