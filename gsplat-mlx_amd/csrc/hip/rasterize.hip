@@ -191,10 +191,12 @@ __device__ __forceinline__ float quad_form(float c0, float c1, float c2, float d
 
 // A record's cull constants, formed once for all the rectangles it is tested
 // against: the bound 1.05 ln(255 o) + 1e-4 on the minimum of sigma, and the
-// conic's reciprocal diagonal for the clamped edge minimisers (the products
-// differ from quotients by an ulp or two, far inside the slack). `always`:
-// never culled (ill-conditioned or non-finite values, NaN opacity); `never`:
-// always culled (opacity <= 0).
+// conic's reciprocal diagonal for the clamped edge minimisers. Both come from
+// the hardware approximations (v_log_f32, v_rcp_f32: about 1 ulp), far inside
+// the slack; a denormal 255 o that v_log_f32 flushes gives ln = -inf, which
+// culls the record as the exact logarithm (about -90) does. `always`: never
+// culled (ill-conditioned or non-finite values, NaN opacity); `never`: always
+// culled (opacity <= 0).
 struct CullRec {
   float mx, my, c0, c1, c2, ic0, ic2, bound;
   bool always, never;
@@ -209,12 +211,12 @@ __device__ __forceinline__ CullRec cull_rec(float2 m, float4 co) {
   r.c2 = co.z;
   const float o = co.w;
   r.never = o <= 0.0f;
-  const float t = logf(255.0f * o);
+  const float t = __builtin_amdgcn_logf(255.0f * o) * 0.69314718055994531f;  // log2 -> ln
   r.always = !r.never && (!(t < 1.0e30f) || !(r.c0 > 0.0f && r.c2 > 0.0f && r.c0 < 1.0e30f && r.c2 < 1.0e30f) ||
                           !(r.c0 * r.c2 - r.c1 * r.c1 > 1.0e-4f * r.c0 * r.c2) || !(fabsf(m.x) < 1.0e30f) ||
                           !(fabsf(m.y) < 1.0e30f));
-  r.ic0 = 1.0f / r.c0;
-  r.ic2 = 1.0f / r.c2;
+  r.ic0 = __builtin_amdgcn_rcpf(r.c0);
+  r.ic2 = __builtin_amdgcn_rcpf(r.c2);
   r.bound = 1.05f * t + 1.0e-4f;
   return r;
 }
@@ -238,11 +240,25 @@ __device__ __forceinline__ bool may_touch(const CullRec& c, const PixRect& r) {
   return !(best > c.bound);
 }
 
-__device__ __forceinline__ uint32_t touch_mask(float2 m, float4 co, int n_waves, int ts, int tx, int ty) {
+// The block's wave rectangles (x0, x1, y0, y1 per wave), formed once per
+// block into LDS so that the staging lanes read them instead of converting
+// the integer bounds for every record; visible after the block's next
+// barrier.
+__device__ __forceinline__ void store_wave_rects(float4* s_rect, int n_waves, int ts, int tx, int ty) {
+  const int w = threadIdx.x;
+  if (w < n_waves) {
+    const PixRect r = wave_rect(w, ts, tx, ty);
+    s_rect[w] = make_float4(r.x0, r.x1, r.y0, r.y1);
+  }
+}
+
+__device__ __forceinline__ uint32_t touch_mask(float2 m, float4 co, int n_waves, const float4* s_rect) {
   const CullRec c = cull_rec(m, co);
   uint32_t mask = 0;
-  for (int w = 0; w < n_waves; ++w)
-    if (may_touch(c, wave_rect(w, ts, tx, ty))) mask |= 1u << w;
+  for (int w = 0; w < n_waves; ++w) {
+    const float4 r = s_rect[w];
+    if (may_touch(c, PixRect{r.x, r.y, r.z, r.w})) mask |= 1u << w;
+  }
   return mask;
 }
 
@@ -272,6 +288,7 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
   const int BS = blockDim.x;
   float* s_rec = smem;                                               // [BS][FW]
   uint32_t* s_mask = reinterpret_cast<uint32_t*>(smem + FW * BS);   // [BS] per-wave touch bits
+  float4* s_rect = reinterpret_cast<float4*>(smem + (FW + 1) * BS);  // [n_waves] wave pixel rects
 
   const int channels = CH > 0 ? CH : a.channels;
   const int tx = blockIdx.x, ty = blockIdx.y;
@@ -301,6 +318,7 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
   }
   int64_t start, end;
   tile_range(a, image, tile, &start, &end);
+  store_wave_rects(s_rect, n_waves, a.ts, tx, ty);
   const float px = static_cast<float>(x) + 0.5f;
   const float py = static_cast<float>(y) + 0.5f;
   float T = 1.0f;
@@ -318,13 +336,16 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
       float4 co;
       const int32_t g = load_gaussian(a, j, &xy, &co);
       float* rec = s_rec + t * FW;
-      *reinterpret_cast<float4*>(rec) = co;
+      // conic diagonal pre-halved: (0.5 c0 dx) dx + (0.5 c2 dy) dy equals
+      // 0.5 ((c0 dx) dx + (c2 dy) dy) bit for bit (scaling by 2 commutes with
+      // rounding away from the subnormal range), one multiply less per visit
+      *reinterpret_cast<float4*>(rec) = make_float4(0.5f * co.x, co.y, 0.5f * co.z, co.w);
       float tail[FW - 4];
 #pragma unroll
       for (int i = 0; i < FW - 4; ++i) tail[i] = 0.0f;
       tail[0] = xy.x;
       tail[1] = xy.y;
-      uint32_t mask = touch_mask(xy, co, n_waves, a.ts, tx, ty);
+      uint32_t mask = touch_mask(xy, co, n_waves, s_rect);
       if constexpr (CH > 0) {
         bool finite = true;
 #pragma unroll
@@ -351,9 +372,11 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
       // (without this record) when T would fall to the threshold
       const bool pass = !done && pass_in;
       const float next_T = T * (1.0f - alpha);
-      const bool sat = pass && next_T <= kTransmittanceThreshold;
-      const bool take = pass && !sat;
-      done = done || sat;
+      // next_T is never NaN (alpha = min(0.99, .) is not, and T only takes
+      // values above the threshold), so one comparison decides both ways
+      const bool live = next_T > kTransmittanceThreshold;
+      const bool take = pass && live;
+      done = done || (pass && !live);
       const float vis = take ? alpha * T : 0.0f;
       if constexpr (CH > 0) {
         float col[4] = {xc.z, xc.w, ex.x, ex.y};
@@ -379,7 +402,7 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
     auto falloff = [&](const float4& co, const float4& xc, bool* pass, float* alpha) {
       const float dx = xc.x - px;
       const float dy = xc.y - py;
-      const float sigma = 0.5f * (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;
+      const float sigma = (co.x * dx * dx + co.z * dy * dy) + co.y * dx * dy;  // co.x, co.z pre-halved
       *alpha = fminf(kMaxAlpha, co.w * exp_alpha(-sigma));
       *pass = !(sigma < 0.0f || *alpha < kAlphaThreshold);
     };
@@ -573,6 +596,7 @@ raster_bwd_kernel(
   constexpr int GW = 6 + o;  // word of the Gaussian id; the touch mask follows
   float* s_rec = smem;                  // [BB][RW]
   float* s_acc = smem + RW * BB;        // [n_waves][BB][NS]
+  float4* s_rect = reinterpret_cast<float4*>(s_acc + n_waves * BB * NS);  // [n_waves] wave pixel rects
   auto s_g = [&](int k) { return __float_as_int(s_rec[k * RW + GW]); };
   auto s_mask = [&](int k) { return __float_as_uint(s_rec[k * RW + GW + 1]); };
 
@@ -675,6 +699,7 @@ raster_bwd_kernel(
       if (lo0 > start) load_ids(lo0, max<int64_t>(start, lo0 - BB));
     }
 
+    store_wave_rects(s_rect, n_waves, a.ts, tx, ty);  // read after the batch loop's first barrier
     int qx, qy;
     lane_pixel(t, a.ts, &qx, &qy);
     const int x = tx * a.ts + qx;
@@ -717,7 +742,7 @@ raster_bwd_kernel(
       const int64_t b0 = max<int64_t>(start, b1 - BB);
       __syncthreads();  // previous batch fully consumed and flushed
       if (t < BB && b1 - 1 - t >= b0) {
-        const uint32_t r_mask = touch_mask(r_xy, r_co, n_waves, a.ts, tx, ty);
+        const uint32_t r_mask = touch_mask(r_xy, r_co, n_waves, s_rect);
         float* rec = s_rec + t * RW;
         *reinterpret_cast<float4*>(rec) = r_co;
         float tail[RW - 4];
@@ -1223,7 +1248,10 @@ size_t bwd_workspace_bytes(int64_t n_tiles_total, int channels) {
 }
 
 // records: mean 2, conic+opacity 4, colours (CH > 0), Gaussian id, touch mask
-size_t fwd_smem(int ch, int bs) { return static_cast<size_t>(bs) * (fwd_record_words(ch) + 1) * 4; }
+// plus one float4 wave rectangle per wave
+size_t fwd_smem(int ch, int bs) {
+  return static_cast<size_t>(bs) * (fwd_record_words(ch) + 1) * 4 + static_cast<size_t>(bs / kWave) * 16;
+}
 // Backward block: one pixel per lane, the whole tile in one block (measured
 // fastest on gfx950 for 16x16 tiles against 2 or 4 pixels per lane and
 // against splitting a tile over several blocks: the lower register count
@@ -1238,7 +1266,7 @@ int bwd_batch(int bs) { return bs <= 128 ? bs : (bs <= 256 ? 128 : 64); }
 size_t bwd_smem(int ch, int bs, int bb, bool absgrad) {
   const int cc = ch > 0 ? ch : 0;
   const int ns = cc + (absgrad ? 8 : 6) + 1;
-  return static_cast<size_t>(bb) * (bwd_record_words(ch) + (bs / kWave) * ns) * 4;
+  return static_cast<size_t>(bb) * (bwd_record_words(ch) + (bs / kWave) * ns) * 4 + static_cast<size_t>(bs / kWave) * 16;
 }
 
 int check_args(const RasterArgs& a, const char* what) {
