@@ -265,20 +265,17 @@ __device__ __forceinline__ uint32_t touch_mask(float2 m, float4 co, int n_waves,
 // Words of one forward batch record in LDS: conic xyz + opacity, then mean xy
 // and the CH staged colours (CH == 0: the Gaussian id), padded to 16 bytes.
 __host__ __device__ constexpr int fwd_record_words(int ch) { return 4 + (2 + (ch > 0 ? ch : 1) + 3) / 4 * 4; }
-// Touch-mask bit of a record whose staged colours (forward) / mean or staged
-// colours (backward) are not all finite.
-constexpr uint32_t kNonFiniteColour = 1u << 31;
+// Touch-mask bit of a backward record whose mean or staged colours are not
+// all finite.
 constexpr uint32_t kNonFiniteRecord = 1u << 31;
 
 // CH in 1..4: colors staged in LDS; CH == 0: runtime channel count (<= 64),
 // colors read from global memory.
 //
-// Records are visited in pairs of straight-line code (the two falloffs and
-// alpha tests overlap; compositing stays in list order, an odd count ends
-// with an inert second visit). A chunk of 64 records whose staged colours
-// are all finite accumulates colour * vis with FMAs and no select, since vis
-// is 0 for a record the pixel does not take; a chunk holding a non-finite
-// colour selects instead, so a record the pixel skips never adds a NaN.
+// Records are visited in pairs (the two falloffs and alpha tests are
+// straight-line code that overlaps; compositing stays in list order, an odd
+// count ends with an inert second visit). Each composite is an exec-masked
+// branch taken by the lanes that keep the record.
 template <int CH>
 __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* __restrict__ render_colors,
                                                           float* __restrict__ render_alphas,
@@ -345,15 +342,10 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
       for (int i = 0; i < FW - 4; ++i) tail[i] = 0.0f;
       tail[0] = xy.x;
       tail[1] = xy.y;
-      uint32_t mask = touch_mask(xy, co, n_waves, s_rect);
+      const uint32_t mask = touch_mask(xy, co, n_waves, s_rect);
       if constexpr (CH > 0) {
-        bool finite = true;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) {
-          tail[2 + c] = a.colors[static_cast<int64_t>(g) * CH + c];
-          finite = finite && fabsf(tail[2 + c]) <= 3.402823466e38f;
-        }
-        if (!finite) mask |= kNonFiniteColour;
+        for (int c = 0; c < CH; ++c) tail[2 + c] = a.colors[static_cast<int64_t>(g) * CH + c];
       } else {
         tail[2] = __int_as_float(g);
       }
@@ -365,39 +357,32 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
     __syncthreads();
     const int cnt = static_cast<int>(min<int64_t>(BS, end - b0));
 
-    // Compositing of one visit after its falloff (list order). `careful`:
-    // the chunk holds a non-finite colour (select the colour terms).
-    auto composite = [&](int k, const float4& xc, const float4& ex, bool pass_in, float alpha, bool careful) {
-      // branch-free form of: skip when sigma < 0 or alpha < 1/255; stop
-      // (without this record) when T would fall to the threshold
+    // Compositing of one visit after its falloff (list order): skip when
+    // sigma < 0 or alpha < 1/255; stop (without this record) when T would
+    // fall to the threshold. The update is a branch, so the lanes that do not
+    // take the record run it with their exec bit clear: they add nothing,
+    // not even a non-finite colour, and a record no lane takes costs no
+    // update at all.
+    auto composite = [&](int k, const float4& xc, const float4& ex, bool pass_in, float alpha) {
       const bool pass = !done && pass_in;
       const float next_T = T * (1.0f - alpha);
       // next_T is never NaN (alpha = min(0.99, .) is not, and T only takes
       // values above the threshold), so one comparison decides both ways
       const bool live = next_T > kTransmittanceThreshold;
-      const bool take = pass && live;
       done = done || (pass && !live);
-      const float vis = take ? alpha * T : 0.0f;
-      if constexpr (CH > 0) {
-        float col[4] = {xc.z, xc.w, ex.x, ex.y};
-        if (careful) {
-#pragma unroll
-          for (int c = 0; c < CH; ++c) {
-            const float add = col[c] * vis;
-            acc[c] += take ? add : 0.0f;  // a skipped record adds nothing, even a non-finite colour
-          }
-        } else {
+      if (pass && live) {
+        const float vis = alpha * T;
+        if constexpr (CH > 0) {
+          const float col[4] = {xc.z, xc.w, ex.x, ex.y};
 #pragma unroll
           for (int c = 0; c < CH; ++c) acc[c] = __builtin_fmaf(col[c], vis, acc[c]);
-        }
-      } else {
-        if (take) {
+        } else {
           const float* colp = a.colors + static_cast<int64_t>(__float_as_int(xc.z)) * channels;
           for (int c = 0; c < channels; ++c) acc[c] += colp[c] * vis;
         }
+        cur = static_cast<int32_t>(b0 + k);
+        T = next_T;
       }
-      cur = take ? static_cast<int32_t>(b0 + k) : cur;
-      T = take ? next_T : T;
     };
     auto falloff = [&](const float4& co, const float4& xc, bool* pass, float* alpha) {
       const float dx = xc.x - px;
@@ -419,7 +404,6 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
       const bool mine = (mk >> wave) & 1u;
       uint64_t bits = __ballot(mine);
       if (__ballot(!done) == 0) bits = 0;  // every pixel of the wave has saturated
-      const bool careful = CH > 0 && __ballot(mine && (mk & kNonFiniteColour)) != 0;
       while (bits) {
         const int k1 = c0 + __builtin_ctzll(bits);
         bits &= bits - 1;
@@ -434,13 +418,8 @@ __global__ void __launch_bounds__(1024) raster_fwd_kernel(RasterArgs a, float* _
         float al1, al2;
         falloff(co1, xc1, &p1, &al1);
         falloff(co2, xc2, &p2, &al2);
-        if (careful) {
-          composite(k1, xc1, ex1, p1, al1, true);
-          composite(k2, xc2, ex2, p2 && two, al2, true);
-        } else {
-          composite(k1, xc1, ex1, p1, al1, false);
-          composite(k2, xc2, ex2, p2 && two, al2, false);
-        }
+        composite(k1, xc1, ex1, p1, al1);
+        composite(k2, xc2, ex2, p2 && two, al2);
       }
     }
   }
