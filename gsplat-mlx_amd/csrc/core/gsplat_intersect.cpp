@@ -212,19 +212,6 @@ int read_total(const array& total_dev, void* stream) {
   return finish_read_total(r);
 }
 
-std::vector<array> sort_pairs(const array& keys, const array& vals, int key_bits, void* stream) {
-  const int64_t n = keys.numel();
-  array ko = at::empty({n}, keys.options());
-  array vo = at::empty({n}, vals.options());
-  if (n == 0) return {ko, vo};
-  const size_t ws_bytes = gsplat_hip_isect_sort_workspace_size(n);
-  array ws = workspace(ws_bytes, keys);
-  check(gsplat_hip_isect_sort(keys.data_ptr<int64_t>(), vals.data_ptr<int32_t>(), n, key_bits,
-                              ko.data_ptr<int64_t>(), vo.data_ptr<int32_t>(), ws.data_ptr<uint8_t>(), ws_bytes,
-                              stream));
-  return {ko, vo};
-}
-
 // Largest key the encoder can produce for I images of n_tiles tiles: the sort
 // only needs that many low bits (higher bits are zero for every key).
 int encoded_key_bits(int64_t I, int64_t n_tiles) {
@@ -322,18 +309,16 @@ std::vector<array> gsplat_intersect_tile_sort(const array& isect_ids, const arra
   const array keys = contig(isect_ids);
   const array vals = contig(flatten_ids);
   if (keys.numel() == 0) return {keys.clone(), vals.clone()};
-  void* stream = stream_for(s, keys);
-  // Arbitrary int64 keys: flip the sign bit so the unsigned order equals the
-  // signed order, sort the significant bits, flip back.
-  const int64_t kmin = keys.min().item<int64_t>();
-  if (kmin >= 0) {
-    const int64_t kmax = keys.max().item<int64_t>();
-    return sort_pairs(keys, vals, bit_length(static_cast<uint64_t>(kmax)), stream);
-  }
-  const array flipped = at::bitwise_xor(keys, std::numeric_limits<int64_t>::min());
-  auto out = sort_pairs(flipped, vals, 64, stream);
-  out[0] = at::bitwise_xor(out[0], std::numeric_limits<int64_t>::min());
-  return out;
+  // Arbitrary int64 keys, in signed order; the passes over digits that every
+  // key shares are skipped on the device, so nothing is read back.
+  const int64_t n = keys.numel();
+  array ko = at::empty({n}, keys.options());
+  array vo = at::empty({n}, vals.options());
+  const size_t ws_bytes = gsplat_hip_isect_sort_workspace_size(n);
+  array ws = workspace(ws_bytes, keys);
+  check(gsplat_hip_isect_sort_i64(keys.data_ptr<int64_t>(), vals.data_ptr<int32_t>(), n, ko.data_ptr<int64_t>(),
+                                  vo.data_ptr<int32_t>(), ws.data_ptr<uint8_t>(), ws_bytes, stream_for(s, keys)));
+  return {ko, vo};
 }
 
 // Sorted dense intersections (AABB or ellipse tiles) by tile buckets

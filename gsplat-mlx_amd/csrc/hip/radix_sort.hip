@@ -64,7 +64,8 @@ __device__ __forceinline__ uint32_t digit_of(K key, int shift) {
 
 template <typename K>
 __global__ void __launch_bounds__(kSortBlock) hist_kernel(const K* __restrict__ keys, int64_t n, int shift,
-                                                          int64_t num_blocks, int32_t* __restrict__ block_hist) {
+                                                          int64_t num_blocks, int32_t* __restrict__ block_hist,
+                                                          uint32_t dxor) {
   __shared__ int32_t h[kRadix];
   h[threadIdx.x] = 0;
   __syncthreads();
@@ -72,7 +73,7 @@ __global__ void __launch_bounds__(kSortBlock) hist_kernel(const K* __restrict__ 
 #pragma unroll 4
   for (int r = 0; r < kSortItems; ++r) {
     const int64_t i = base + r * kSortBlock + threadIdx.x;
-    if (i < n) atomicAdd(&h[digit_of(keys[i], shift)], 1);
+    if (i < n) atomicAdd(&h[digit_of(keys[i], shift) ^ dxor], 1);
   }
   __syncthreads();
   block_hist[static_cast<int64_t>(threadIdx.x) * num_blocks + blockIdx.x] = h[threadIdx.x];
@@ -84,7 +85,7 @@ __global__ void __launch_bounds__(kSortBlock) scatter_kernel(const K* __restrict
                                                              int64_t num_blocks,
                                                              const int32_t* __restrict__ digit_block_start,
                                                              K* __restrict__ keys_out,
-                                                             int32_t* __restrict__ vals_out) {
+                                                             int32_t* __restrict__ vals_out, uint32_t dxor) {
   __shared__ K s_keys[kTile];
   __shared__ int32_t s_vals[kTile];
   // per-wave digit counts -> per-wave digit bases; double-buffered by round
@@ -125,7 +126,7 @@ __global__ void __launch_bounds__(kSortBlock) scatter_kernel(const K* __restrict
     for (int w = 0; w < kWaves; ++w) wc[w][t] = 0;
     __syncthreads();
     const bool valid = r * kSortBlock + t < cnt;
-    const uint32_t d = digit_of(k[r], shift);
+    const uint32_t d = digit_of(k[r], shift) ^ dxor;
     uint64_t peers = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -169,7 +170,7 @@ __global__ void __launch_bounds__(kSortBlock) scatter_kernel(const K* __restrict
 #pragma unroll
   for (int r = 0; r < kSortItems; ++r) {
     if (r * kSortBlock + t < cnt) {
-      const int pos = s_tile_start[digit_of(k[r], shift)] + rank[r];
+      const int pos = s_tile_start[digit_of(k[r], shift) ^ dxor] + rank[r];
       s_keys[pos] = k[r];
       s_vals[pos] = v[r];
     }
@@ -177,7 +178,7 @@ __global__ void __launch_bounds__(kSortBlock) scatter_kernel(const K* __restrict
   __syncthreads();
   for (int j = t; j < cnt; j += kSortBlock) {
     const K key = s_keys[j];
-    const uint32_t d = digit_of(key, shift);
+    const uint32_t d = digit_of(key, shift) ^ dxor;
     const int64_t dst = static_cast<int64_t>(s_global[d]) + (j - s_tile_start[d]);
     keys_out[dst] = key;
     vals_out[dst] = s_vals[j];
@@ -189,6 +190,20 @@ __global__ void copy_kernel(const K* __restrict__ k_in, const int32_t* __restric
                             K* __restrict__ k_out, int32_t* __restrict__ v_out) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < n) {
+    k_out[i] = k_in[i];
+    v_out[i] = v_in[i];
+  }
+}
+
+// copy_kernel when *flag is set (a device-planned sort with no pass to run:
+// every key is equal, so the stable order is the input order); a grid-stride
+// loop, as the grid is sized before the flag is known.
+template <typename K>
+__global__ void copy_if_kernel(const K* __restrict__ k_in, const int32_t* __restrict__ v_in, int64_t n,
+                               K* __restrict__ k_out, int32_t* __restrict__ v_out, const uint32_t* __restrict__ flag) {
+  if (*flag == 0u) return;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
     k_out[i] = k_in[i];
     v_out[i] = v_in[i];
   }
@@ -216,7 +231,7 @@ constexpr int kHistRowsPerAdd = 32;
 
 template <typename K>
 __global__ void __launch_bounds__(kSortBlock) hist_partial_kernel(const K* __restrict__ keys, int64_t n,
-                                                                  int bit_lo, int passes,
+                                                                  int bit_lo, int passes, int flip_pass,
                                                                   uint32_t* __restrict__ partial,
                                                                   uint32_t* __restrict__ clear, int64_t clear_words) {
   __shared__ uint32_t h[kMaxPasses][kRadix];
@@ -241,7 +256,8 @@ __global__ void __launch_bounds__(kSortBlock) hist_partial_kernel(const K* __res
 #pragma unroll
     for (int r = 0; r < kOsItems; ++r) {
       if (base + r * kSortBlock + t >= n) continue;
-      for (int p = 0; p < passes; ++p) atomicAdd(&h[p][digit_of(k[r], bit_lo + 8 * p)], 1u);
+      for (int p = 0; p < passes; ++p)
+        atomicAdd(&h[p][digit_of(k[r], bit_lo + 8 * p) ^ (p == flip_pass ? 0x80u : 0u)], 1u);
     }
   }
   __syncthreads();
@@ -259,6 +275,43 @@ __global__ void __launch_bounds__(kSortBlock) hist_add_kernel(const uint32_t* __
   if (sum) atomicAdd(&hist[p * kRadix + t], sum);
 }
 
+// Pass plan of a sort whose constant digits are found on the device (one
+// thread): a digit is constant when the pass histogram counts all n keys in
+// the digit of the first key; such a pass would be the identity and is
+// skipped. plan[p] = 1 for a skipped pass, else src << 1 | dst << 3 with
+// buffers 0 = the input, 1 = the workspace copy, 2 = the output, chosen so
+// that the last pass run writes the output; plan[passes] = 1 when no pass
+// runs (the output is then a copy of the input).
+template <typename K>
+__global__ void sort_plan_kernel(const K* __restrict__ keys, int64_t n, int bit_lo, int passes, int flip_pass,
+                                 const uint32_t* __restrict__ hist, uint32_t* __restrict__ plan) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  const K k0 = keys[0];
+  uint32_t skip = 0;
+  int runs = 0;
+  for (int p = 0; p < passes; ++p) {
+    const uint32_t d = digit_of(k0, bit_lo + 8 * p) ^ (p == flip_pass ? 0x80u : 0u);
+    if (static_cast<int64_t>(hist[p * kRadix + d]) == n) {
+      skip |= 1u << p;
+    } else {
+      ++runs;
+    }
+  }
+  uint32_t src = 0;
+  int j = 0;
+  for (int p = 0; p < passes; ++p) {
+    if ((skip >> p) & 1u) {
+      plan[p] = 1u;
+      continue;
+    }
+    const uint32_t dst = ((runs - 1 - j) % 2 == 0) ? 2u : 1u;
+    plan[p] = (src << 1) | (dst << 3);
+    src = dst;
+    ++j;
+  }
+  plan[passes] = runs == 0 ? 1u : 0u;
+}
+
 // Where a pass writes: keys and values; or (ASM, 32-bit keys, last pass of
 // the intersection sort) 64-bit ids key << 32 | depth bits of the value's
 // pair plus the values; GATHER adds gather[value] at the same position. With
@@ -273,6 +326,12 @@ struct OsOut {
   const int32_t* gather;  // GATHER: gathered = gather[value] beside the keys
   int32_t* gathered;
   uint32_t* v2;           // V2, not ASM: the second value's output
+  // device-planned passes (sort_plan_kernel; plain passes only): this pass's
+  // plan entry picks the source among the input, keys_alt / vals_alt and
+  // keys / vals, and the destination among the last two, or skips the pass
+  const uint32_t* plan;
+  K* keys_alt;
+  int32_t* vals_alt;
 };
 
 template <typename K, bool ASM, bool GATHER, bool V2>
@@ -281,7 +340,7 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
                                                               const uint32_t* __restrict__ v2_in, int64_t n,
                                                               int shift, const uint32_t* __restrict__ hist,
                                                               uint32_t* __restrict__ lookback, int spin_limit,
-                                                              OsOut<K> out) {
+                                                              OsOut<K> out, uint32_t dxor) {
   __shared__ K s_keys[kOsTile];
   __shared__ int32_t s_vals[kOsTile];
   __shared__ uint32_t s_v2[V2 ? kOsTile : 1];
@@ -296,6 +355,19 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
   const int64_t part = blockIdx.x;
   const int64_t base = part * kOsTile;
   const int cnt = static_cast<int>(min<int64_t>(kOsTile, n - base));
+  const K* kin = keys_in;
+  const int32_t* vin = vals_in;
+  K* kout = out.keys;
+  int32_t* vout = out.vals;
+  if (out.plan) {  // block-uniform
+    const uint32_t e = *out.plan;
+    if (e & 1u) return;  // constant digit: the pass is skipped
+    const uint32_t src = (e >> 1) & 3u, dst = (e >> 3) & 3u;
+    kin = src == 0u ? keys_in : (src == 1u ? out.keys_alt : out.keys);
+    vin = src == 0u ? vals_in : (src == 1u ? out.vals_alt : out.vals);
+    kout = dst == 1u ? out.keys_alt : out.keys;
+    vout = dst == 1u ? out.vals_alt : out.vals;
+  }
 
   // load: wave w owns tile keys [w * 1024, (w + 1) * 1024), round r covers
   // w * 1024 + r * 64 + lane, so (wave, round, lane) is input order
@@ -307,8 +379,8 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
   for (int r = 0; r < kOsItems; ++r) {
     const int idx = wave * kOsWaveKeys + r * kWave + lane;
     if (idx < cnt) {
-      k[r] = keys_in[base + idx];
-      v[r] = vals_in[base + idx];
+      k[r] = kin[base + idx];
+      v[r] = vin[base + idx];
       if constexpr (V2) w2[r] = v2_in[base + idx];
     } else {
       k[r] = 0;
@@ -334,7 +406,7 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
 #pragma unroll
   for (int r = 0; r < kOsItems; ++r) {
     const bool valid = wave * kOsWaveKeys + r * kWave + lane < cnt;
-    const uint32_t d = digit_of(k[r], shift);
+    const uint32_t d = digit_of(k[r], shift) ^ dxor;
     uint64_t peers = __ballot(valid);
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
@@ -379,7 +451,7 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
 #pragma unroll
   for (int r = 0; r < kOsItems; ++r) {
     if (wave * kOsWaveKeys + r * kWave + lane < cnt) {
-      const uint32_t d = digit_of(k[r], shift);
+      const uint32_t d = digit_of(k[r], shift) ^ dxor;
       const uint32_t pos = s_tile_start[d] + wc[d] + rank[r];
       s_keys[pos] = k[r];
       s_vals[pos] = v[r];
@@ -437,7 +509,7 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
     __syncthreads();
-    for (int64_t i = t; i < base; i += kSortBlock) atomicAdd(&wc[digit_of(keys_in[i], shift)], 1u);
+    for (int64_t i = t; i < base; i += kSortBlock) atomicAdd(&wc[digit_of(kin[i], shift) ^ dxor], 1u);
     __syncthreads();
     if (gave_up) {
       prefix = 0;
@@ -451,7 +523,7 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
   }
   for (int j = t; j < cnt; j += kSortBlock) {
     const K key = s_keys[j];
-    const uint32_t d = digit_of(key, shift);
+    const uint32_t d = digit_of(key, shift) ^ dxor;
     const int64_t dst = static_cast<int64_t>(s_gbase[d]) + (j - static_cast<int64_t>(s_tile_start[d]));
     const int32_t val = s_vals[j];
     if constexpr (ASM && V2) {
@@ -459,11 +531,11 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
     } else if constexpr (ASM) {
       out.ids[dst] = static_cast<int64_t>((static_cast<uint64_t>(key) << 32) | __float_as_uint(out.depths[val]));
     } else {
-      out.keys[dst] = key;
+      kout[dst] = key;
       if constexpr (V2) out.v2[dst] = s_v2[j];
     }
     if constexpr (GATHER) out.gathered[dst] = out.gather[val];
-    out.vals[dst] = val;
+    vout[dst] = val;
   }
 }
 
@@ -477,6 +549,7 @@ struct SortWorkspace {
   uint32_t* os_hist;      // [kMaxPasses][256]
   uint32_t* os_lookback;  // [passes][n_parts][256]
   uint32_t* os_partial;   // [kHistBlocks][kMaxPasses][256] per-block histogram rows
+  uint32_t* plan;         // [kMaxPasses + 1] device pass plan (sort_plan_kernel)
 };
 
 inline size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
@@ -502,6 +575,7 @@ size_t layout(int64_t n, SortWorkspace<K>* ws, void* base) {
   const size_t oh_b = onesweep ? align_up(kMaxPasses * kRadix * sizeof(uint32_t)) : 0;
   const size_t ol_b = onesweep ? align_up(static_cast<size_t>(max_passes) * n_parts * kRadix * sizeof(uint32_t)) : 0;
   const size_t op_b = onesweep ? align_up(static_cast<size_t>(kHistBlocks) * kMaxPasses * kRadix * sizeof(uint32_t)) : 0;
+  const size_t plan_b = align_up((kMaxPasses + 1) * sizeof(uint32_t));
   if (ws && base) {
     char* p = static_cast<char*>(base);
     ws->keys_alt = reinterpret_cast<K*>(p);
@@ -512,8 +586,9 @@ size_t layout(int64_t n, SortWorkspace<K>* ws, void* base) {
     ws->os_hist = reinterpret_cast<uint32_t*>(q);
     ws->os_lookback = reinterpret_cast<uint32_t*>(q + oh_b);
     ws->os_partial = reinterpret_cast<uint32_t*>(q + oh_b + ol_b);
+    ws->plan = reinterpret_cast<uint32_t*>(q + oh_b + ol_b + op_b);
   }
-  return keys_b + vals_b + hist_b + scan_b + oh_b + ol_b + op_b;
+  return keys_b + vals_b + hist_b + scan_b + oh_b + ol_b + op_b + plan_b;
 }
 
 // ids[i] = keys[i] << 32 | bits of depths[vals[i]] (32-bit keys).
@@ -600,7 +675,7 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
       KernelTimer timer("sort_histogram", s);
       const int hb = static_cast<int>(std::min<int64_t>(n_parts, kHistBlocks));
       hist_partial_kernel<K><<<static_cast<unsigned>(hb), kSortBlock, 0, s>>>(
-          keys_in, n, bit_lo, passes, ws.os_partial, ws.os_hist, clear_words);
+          keys_in, n, bit_lo, passes, -1, ws.os_partial, ws.os_hist, clear_words);
       const dim3 add_grid((hb + kHistRowsPerAdd - 1) / kHistRowsPerAdd, passes);
       hist_add_kernel<<<add_grid, kSortBlock, 0, s>>>(ws.os_partial, hb, ws.os_hist);
     }
@@ -626,26 +701,26 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
         if constexpr (sizeof(K) == 4) {
           if (last && asm_ids && asm_bits) {
             onesweep_kernel<K, true, false, true><<<grid, kSortBlock, 0, s>>>(src_k, src_v, src_b, n, shift, hist_p,
-                                                                              look_p, spin, o);
+                                                                              look_p, spin, o, 0u);
             launched = true;
           } else if (last && asm_ids) {
             onesweep_kernel<K, true, false, false><<<grid, kSortBlock, 0, s>>>(src_k, src_v, nullptr, n, shift,
-                                                                               hist_p, look_p, spin, o);
+                                                                               hist_p, look_p, spin, o, 0u);
             launched = true;
           } else if (asm_bits) {
             onesweep_kernel<K, false, false, true><<<grid, kSortBlock, 0, s>>>(src_k, src_v, src_b, n, shift, hist_p,
-                                                                               look_p, spin, o);
+                                                                               look_p, spin, o, 0u);
             launched = true;
           }
         }
         if (!launched && last && gather_dst) {
           onesweep_kernel<K, false, true, false><<<grid, kSortBlock, 0, s>>>(src_k, src_v, nullptr, n, shift, hist_p,
-                                                                             look_p, spin, o);
+                                                                             look_p, spin, o, 0u);
           launched = true;
         }
         if (!launched)
           onesweep_kernel<K, false, false, false><<<grid, kSortBlock, 0, s>>>(src_k, src_v, nullptr, n, shift,
-                                                                              hist_p, look_p, spin, o);
+                                                                              hist_p, look_p, spin, o, 0u);
       }
       if ((rc = check_launch(what))) return rc;
       src_k = dst_k;
@@ -665,7 +740,7 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
     const int shift = bit_lo + 8 * p;
     {
       KernelTimer timer("sort_histogram", s);
-      hist_kernel<K><<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, n, shift, nb, ws.hist);
+      hist_kernel<K><<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, n, shift, nb, ws.hist, 0u);
     }
     int rc = check_launch(what);
     if (rc) return rc;
@@ -674,7 +749,7 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
     {
       KernelTimer timer("sort_scatter", s);
       scatter_kernel<K><<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, src_v, n, shift, nb, ws.hist, dst_k,
-                                                                         dst_v);
+                                                                         dst_v, 0u);
     }
     rc = check_launch(what);
     if (rc) return rc;
@@ -683,6 +758,93 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
   }
   if (asm_ids) return assemble(keys_out, vals_out, asm_depths, n, asm_ids, s, what);
   if (gather_dst) return gather(vals_out, gather_src, n, gather_dst, s, what);
+  return GSPLAT_OK;
+}
+
+// Stable sort of signed 64-bit keys (two's complement order: the top digit's
+// sign bit is flipped when digits are formed, the keys themselves are moved
+// unchanged) over all eight digits, with the passes on digits that every key
+// shares found and skipped on the device (sort_plan_kernel): nothing is read
+// back to the host. Inputs of 2^30 keys or more take the block-scan passes,
+// all eight of them.
+int radix_sort_pairs_i64_planned(const int64_t* keys_in_s, const int32_t* vals_in, int64_t n, int64_t* keys_out_s,
+                                 int32_t* vals_out, void* workspace, size_t workspace_bytes, hipStream_t s,
+                                 const char* what) {
+  using K = uint64_t;
+  const std::string w(what);
+  if (n < 0) return invalid(w + ": invalid sort arguments.");
+  if (n == 0) return GSPLAT_OK;
+  if (!keys_in_s || !vals_in || !keys_out_s || !vals_out) return invalid(w + ": null pointer.");
+  if (n > (static_cast<int64_t>(1) << 31) - 1) return invalid(w + ": more than 2^31-1 keys.");
+  const K* keys_in = reinterpret_cast<const K*>(keys_in_s);
+  K* keys_out = reinterpret_cast<K*>(keys_out_s);
+  constexpr int passes = 8;
+  constexpr int flip_pass = passes - 1;
+  SortWorkspace<K> ws;
+  if (!workspace || workspace_bytes < layout<K>(n, &ws, workspace)) {
+    set_error(w + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  int rc;
+  if (n < g_onesweep_max_keys.load(std::memory_order_relaxed)) {
+    const int64_t n_parts = (n + kOsTile - 1) / kOsTile;
+    const int spin = g_spin_limit.load(std::memory_order_relaxed);
+    const int64_t clear_words = (reinterpret_cast<char*>(ws.os_lookback + passes * n_parts * kRadix) -
+                                 reinterpret_cast<char*>(ws.os_hist)) / 4;
+    {
+      KernelTimer timer("sort_histogram", s);
+      const int hb = static_cast<int>(std::min<int64_t>(n_parts, kHistBlocks));
+      hist_partial_kernel<K><<<static_cast<unsigned>(hb), kSortBlock, 0, s>>>(
+          keys_in, n, 0, passes, flip_pass, ws.os_partial, ws.os_hist, clear_words);
+      const dim3 add_grid((hb + kHistRowsPerAdd - 1) / kHistRowsPerAdd, passes);
+      hist_add_kernel<<<add_grid, kSortBlock, 0, s>>>(ws.os_partial, hb, ws.os_hist);
+      sort_plan_kernel<K><<<1, 64, 0, s>>>(keys_in, n, 0, passes, flip_pass, ws.os_hist, ws.plan);
+    }
+    if ((rc = check_launch(what))) return rc;
+    for (int p = 0; p < passes; ++p) {
+      KernelTimer timer("sort_onesweep", s);
+      OsOut<K> o{};
+      o.keys = keys_out;
+      o.vals = vals_out;
+      o.plan = ws.plan + p;
+      o.keys_alt = ws.keys_alt;
+      o.vals_alt = ws.vals_alt;
+      onesweep_kernel<K, false, false, false><<<static_cast<unsigned>(n_parts), kSortBlock, 0, s>>>(
+          keys_in, vals_in, nullptr, n, 8 * p, ws.os_hist + p * kRadix, ws.os_lookback + p * n_parts * kRadix, spin,
+          o, p == flip_pass ? 0x80u : 0u);
+      if ((rc = check_launch(what))) return rc;
+    }
+    {
+      KernelTimer timer("sort_copy", s);
+      const unsigned cg = static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 2048));
+      copy_if_kernel<K><<<cg, 256, 0, s>>>(keys_in, vals_in, n, keys_out, vals_out, ws.plan + passes);
+    }
+    return check_launch(what);
+  }
+  const int64_t nb = (n + kTile - 1) / kTile;
+  const K* src_k = keys_in;
+  const int32_t* src_v = vals_in;
+  for (int p = 0; p < passes; ++p) {
+    const bool to_out = ((passes - 1 - p) % 2) == 0;
+    K* dst_k = to_out ? keys_out : ws.keys_alt;
+    int32_t* dst_v = to_out ? vals_out : ws.vals_alt;
+    const int shift = 8 * p;
+    const uint32_t dxor = p == flip_pass ? 0x80u : 0u;
+    {
+      KernelTimer timer("sort_histogram", s);
+      hist_kernel<K><<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, n, shift, nb, ws.hist, dxor);
+    }
+    if ((rc = check_launch(what))) return rc;
+    if ((rc = scan_exclusive_i32(ws.hist, ws.hist, nb * kRadix, nullptr, ws.scan_ws, s))) return rc;
+    {
+      KernelTimer timer("sort_scatter", s);
+      scatter_kernel<K><<<static_cast<unsigned>(nb), kSortBlock, 0, s>>>(src_k, src_v, n, shift, nb, ws.hist, dst_k,
+                                                                         dst_v, dxor);
+    }
+    if ((rc = check_launch(what))) return rc;
+    src_k = dst_k;
+    src_v = dst_v;
+  }
   return GSPLAT_OK;
 }
 
@@ -710,6 +872,13 @@ extern "C" int gsplat_hip_isect_sort(const int64_t* keys_in, const int32_t* vals
   return radix_sort_pairs<uint64_t>(reinterpret_cast<const uint64_t*>(keys_in), vals_in, n, 0, key_bits,
                                     reinterpret_cast<uint64_t*>(keys_out), vals_out, workspace, workspace_bytes,
                                     as_stream(stream), "intersect_tile_sort");
+}
+
+extern "C" int gsplat_hip_isect_sort_i64(const int64_t* keys_in, const int32_t* vals_in, int64_t n,
+                                         int64_t* keys_out, int32_t* vals_out, void* workspace,
+                                         size_t workspace_bytes, void* stream) {
+  return radix_sort_pairs_i64_planned(keys_in, vals_in, n, keys_out, vals_out, workspace, workspace_bytes,
+                                      as_stream(stream), "intersect_tile_sort");
 }
 
 extern "C" void gsplat_hip_sort_debug_set(int32_t spin_limit, int64_t onesweep_max_keys) {

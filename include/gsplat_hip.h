@@ -271,6 +271,17 @@ int gsplat_hip_isect_sort(const int64_t* keys_in, const int32_t* vals_in, int64_
                           int32_t key_bits, int64_t* keys_out, int32_t* vals_out,
                           void* workspace, size_t workspace_bytes, void* stream);
 
+/* Stable ascending sort of arbitrary (signed) int64 keys carrying int32
+ * values, all 64 bits compared, with nothing read back to the host: the
+ * digits that every key shares are found on the device from the pass
+ * histograms and their passes skipped. Replaces the same mx::argsort +
+ * 2x mx::take (gsplat_intersect.cpp:266-286), which takes any int64 key.
+ * Workspace: gsplat_hip_isect_sort_workspace_size(n). Inputs are left
+ * unchanged. */
+int gsplat_hip_isect_sort_i64(const int64_t* keys_in, const int32_t* vals_in, int64_t n,
+                              int64_t* keys_out, int32_t* vals_out, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
 /* Radix sort diagnostics and test hooks (no counterpart in the reference,
  * whose sort is MLX's). Every sort of this library (the standalone sort and
  * the two sorts of the intersection pipeline) runs, below 2^30 keys, one

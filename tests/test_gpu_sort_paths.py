@@ -8,6 +8,8 @@ the oracle's intersection lists:
   poll finds an unpublished predecessor (a run-dependent mix of both ways);
 - the reduce-then-scan path that sorts of 2^30 keys or more take (histogram,
   scan, scatter per pass), forced by lowering the onesweep key limit;
+- the signed sort that skips constant digits on the device (every key shape
+  of digits constant and varying, all keys equal), on all three paths;
 - in the depth-presorted intersection, the tile-key sort carrying each
   entry's depth bits (taken above 2^21 pairs) and the encode blocks' rank
   ranges from the up-front split kernel (taken from 65536 blocks), forced on
@@ -43,6 +45,8 @@ def _lib():
     lib.gsplat_hip_isect_sort_workspace_size.argtypes = [i64]
     lib.gsplat_hip_isect_sort.restype = ctypes.c_int
     lib.gsplat_hip_isect_sort.argtypes = [p, p, i64, i32, p, p, p, ctypes.c_size_t, p]
+    lib.gsplat_hip_isect_sort_i64.restype = ctypes.c_int
+    lib.gsplat_hip_isect_sort_i64.argtypes = [p, p, i64, p, p, p, ctypes.c_size_t, p]
     lib.gsplat_hip_isect_debug_set.restype = None
     lib.gsplat_hip_isect_debug_set.argtypes = [i64, i64]
     lib.gsplat_hip_isect_debug_reset.restype = None
@@ -82,6 +86,64 @@ def _sort(lib, keys, vals, bits):
     assert rc == 0, lib.gsplat_hip_last_error()
     torch.cuda.synchronize()
     return host(ko), host(vo)
+
+
+def _sort_i64(lib, keys, vals):
+    """The device-planned signed sort (all 64 bits, constant digits skipped
+    on the device)."""
+    import torch
+
+    n = keys.size
+    kd, vd = dev(keys), dev(vals)
+    ws_bytes = lib.gsplat_hip_isect_sort_workspace_size(n)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device="cuda")
+    ko, vo = torch.empty_like(kd), torch.empty_like(vd)
+    rc = lib.gsplat_hip_isect_sort_i64(kd.data_ptr(), vd.data_ptr(), n, ko.data_ptr(), vo.data_ptr(),
+                                       ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.gsplat_hip_last_error()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(kd), keys)  # inputs unchanged
+    return host(ko), host(vo)
+
+
+def _signed_keys(kind, n, seed):
+    rng = np.random.default_rng(seed)
+    if kind == "full":  # every digit varies, both signs, extremes
+        keys = rng.integers(np.iinfo(np.int64).min, np.iinfo(np.int64).max, size=n, dtype=np.int64)
+        keys[: min(n, 4)] = np.array([np.iinfo(np.int64).min, -1, 0, np.iinfo(np.int64).max])[: min(n, 4)]
+    elif kind == "ids":  # intersection-shaped: image | tile | depth bits, high digits constant
+        keys = (rng.integers(0, 3, n) << 46) | (rng.integers(0, 4346, n) << 32) | rng.integers(0, 1 << 32, n)
+    elif kind == "middle":  # digits 2, 3 and 5 constant (0xAB, 0x00, 0x7F), the rest varying, some negative
+        keys = rng.integers(0, 1 << 62, size=n, dtype=np.int64)
+        keys &= ~np.int64((0xFF << 16) | (0xFF << 24) | (0xFF << 40))
+        keys |= np.int64((0xAB << 16) | (0x7F << 40))
+        keys[rng.random(n) < 0.5] *= -1
+    elif kind == "negative":  # all negative, one varying digit in the middle
+        keys = -(np.int64(1) << 50) + (rng.integers(0, 256, n).astype(np.int64) << 24)
+    else:  # "equal": no pass runs, the output is the input
+        keys = np.full(n, -12345678901, np.int64)
+    keys = keys.astype(np.int64)
+    keys[rng.random(n) < 0.3] = keys[0]  # ties: stability matters
+    return keys, rng.permutation(n).astype(np.int32)
+
+
+@pytest.mark.parametrize("kind", ["full", "ids", "middle", "negative", "equal"])
+@pytest.mark.parametrize("n", [1, 4096, 100_003])
+@pytest.mark.parametrize("path", ["onesweep", "recount", "reduce_then_scan"])
+def test_signed_planned_sort(lib, kind, n, path):
+    """gsplat_hip_isect_sort_i64 against numpy's stable argsort of the int64
+    keys: signed order, all 64 bits, on each sort path."""
+    keys, vals = _signed_keys(kind, n, n + len(kind))
+    order = np.argsort(keys, kind="stable")
+    print(f"signed planned sort kind={kind} n={n} path={path}", flush=True)
+    if path == "recount":
+        lib.gsplat_hip_sort_debug_set(-1, 0)
+    elif path == "reduce_then_scan":
+        lib.gsplat_hip_sort_debug_set(1 << 18, 1)
+    for _ in range(2):  # the second run reuses the plan words of the first
+        ko, vo = _sort_i64(lib, keys, vals)
+        np.testing.assert_array_equal(ko, keys[order])
+        np.testing.assert_array_equal(vo, vals[order])
 
 
 def _keys(n, bits, seed):
