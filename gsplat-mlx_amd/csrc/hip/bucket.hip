@@ -634,12 +634,13 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_scatter_kernel(const floa
 // chunk (ballots, as the device-wide sort), the per-digit counts are scanned
 // over waves and digits, and the elements are written back to LDS in digit
 // order. A pass whose digit is one value for the whole list is skipped.
+// Each element is one 8-byte LDS word (depth bits, flatten id), so a pass
+// reads and scatters it with one instruction.
 template <int B, int ITEMS>
 struct TileSorter {
   static constexpr int W = B / kWave;
   static constexpr int CAP = B * ITEMS;
-  uint32_t* keys;     // [CAP] depth bits
-  uint32_t* vals;     // [CAP] flatten ids
+  uint2* kv;          // [CAP] (depth bits, flatten id)
   uint32_t* wcnt;     // [W][256]
   uint32_t* dstart;   // [256]
   int n, R;
@@ -662,8 +663,9 @@ struct TileSorter {
       if (r >= R) break;  // wave-uniform
       const int idx = (wave * R + r) * kWave + lane;
       const bool valid = idx < n;
-      k[r] = valid ? keys[idx] : 0u;
-      v[r] = valid ? vals[idx] : 0u;
+      const uint2 e = valid ? kv[idx] : make_uint2(0u, 0u);
+      k[r] = e.x;
+      v[r] = e.y;
       const uint32_t dg = ((by_id ? v[r] : k[r]) >> shift) & 255u;
       // lanes with the same digit: for each bit, ballot the lanes whose bit is
       // clear and keep the ballot (or its complement) that contains this lane;
@@ -724,8 +726,7 @@ struct TileSorter {
       if (idx < n) {
         const uint32_t dg = ((by_id ? v[r] : k[r]) >> shift) & 255u;
         const uint32_t pos = dstart[dg] + wcnt[wave * 256 + dg] + rank[r];
-        keys[pos] = k[r];
-        vals[pos] = v[r];
+        kv[pos] = make_uint2(k[r], v[r]);
       }
     }
     __syncthreads();
@@ -738,7 +739,7 @@ struct TileSorter {
 // is written, so src may be the bytes of out_ids. n > CAP is left alone.
 template <int B, int ITEMS>
 __device__ __forceinline__ void sort_range(const uint2* src, int64_t len, uint64_t hi, int64_t* out_ids,
-                                           int32_t* out_flat, uint32_t* s_keys, uint32_t* s_vals,
+                                           int32_t* out_flat, uint2* s_kv,
                                            uint32_t* s_wcnt, uint32_t* s_dstart, uint32_t* s_bits) {
   using S = TileSorter<B, ITEMS>;
   if (len <= 0 || len > S::CAP) return;  // block-uniform
@@ -747,16 +748,28 @@ __device__ __forceinline__ void sort_range(const uint2* src, int64_t len, uint64
   if (t < 4) s_bits[t] = (t & 1) ? ~0u : 0u;
   __syncthreads();
   // the bits that vary over the list: passes on digits every element shares
-  // are skipped
+  // are skipped. The list is loaded ITEMS elements per thread, all loads in
+  // flight before the first LDS store (lists this sort holds have at most
+  // B * ITEMS elements).
   uint32_t ko = 0u, ka = ~0u, vo = 0u, va = ~0u;
-  for (int j = t; j < n; j += B) {
-    const uint2 p = src[j];
-    s_keys[j] = p.x;
-    s_vals[j] = p.y;
-    ko |= p.x;
-    ka &= p.x;
-    vo |= p.y;
-    va &= p.y;
+  {
+    uint2 e[ITEMS];
+#pragma unroll
+    for (int r = 0; r < ITEMS; ++r) {
+      const int j = r * B + t;
+      e[r] = j < n ? src[j] : make_uint2(0u, ~0u);
+    }
+#pragma unroll
+    for (int r = 0; r < ITEMS; ++r) {
+      const int j = r * B + t;
+      if (j < n) {
+        s_kv[j] = e[r];
+        ko |= e[r].x;
+        ka &= e[r].x;
+        vo |= e[r].y;
+        va &= e[r].y;
+      }
+    }
   }
 #pragma unroll
   for (int off = kWave / 2; off > 0; off >>= 1) {
@@ -773,7 +786,7 @@ __device__ __forceinline__ void sort_range(const uint2* src, int64_t len, uint64
   }
   __syncthreads();
   const uint32_t kvary = s_bits[0] ^ s_bits[1], ivary = s_bits[2] ^ s_bits[3];
-  S srt{s_keys, s_vals, s_wcnt, s_dstart, n, (n + S::W * kWave - 1) / (S::W * kWave)};
+  S srt{s_kv, s_wcnt, s_dstart, n, (n + S::W * kWave - 1) / (S::W * kWave)};
   if (n > 1) {
 #pragma unroll 1
     for (int shift = 0; shift < 32; shift += 8) srt.pass(false, shift, (kvary >> shift) & 255u);
@@ -782,11 +795,11 @@ __device__ __forceinline__ void sort_range(const uint2* src, int64_t len, uint64
     // a list with a longer run is sorted again, ids as the low digits.
     constexpr int kShortRun = 32;
     auto run_start = [&](int j) {
-      return j + 1 < n && s_keys[j + 1] == s_keys[j] && (j == 0 || s_keys[j - 1] != s_keys[j]);
+      return j + 1 < n && s_kv[j + 1].x == s_kv[j].x && (j == 0 || s_kv[j - 1].x != s_kv[j].x);
     };
     auto run_end = [&](int j) {
       int e = j + 1;
-      while (e < n && s_keys[e] == s_keys[j] && e - j <= kShortRun) ++e;
+      while (e < n && s_kv[e].x == s_kv[j].x && e - j <= kShortRun) ++e;
       return e;
     };
     bool tie = false, long_run = false;
@@ -806,14 +819,14 @@ __device__ __forceinline__ void sort_range(const uint2* src, int64_t len, uint64
       for (int j = t; j < n; j += B) {
         if (!run_start(j)) continue;
         const int e = run_end(j);
-        for (int a = j + 1; a < e; ++a) {  // insertion sort of s_vals[j, e)
-          const uint32_t v = s_vals[a];
+        for (int a = j + 1; a < e; ++a) {  // insertion sort of the ids of [j, e)
+          const uint32_t v = s_kv[a].y;
           int b = a - 1;
-          while (b >= j && s_vals[b] > v) {
-            s_vals[b + 1] = s_vals[b];
+          while (b >= j && s_kv[b].y > v) {
+            s_kv[b + 1].y = s_kv[b].y;
             --b;
           }
-          s_vals[b + 1] = v;
+          s_kv[b + 1].y = v;
         }
       }
       __syncthreads();
@@ -821,8 +834,9 @@ __device__ __forceinline__ void sort_range(const uint2* src, int64_t len, uint64
   }
   // every thread read its inputs before the first barrier above
   for (int j = t; j < n; j += B) {
-    out_ids[j] = static_cast<int64_t>(hi | s_keys[j]);
-    out_flat[j] = static_cast<int32_t>(s_vals[j]);
+    const uint2 e = s_kv[j];
+    out_ids[j] = static_cast<int64_t>(hi | e.x);
+    out_flat[j] = static_cast<int32_t>(e.y);
   }
 }
 
@@ -846,19 +860,18 @@ __device__ __forceinline__ void sort_tile_list(int64_t list, const uint2* __rest
                                                const int32_t* __restrict__ tile_start, int64_t n_lists,
                                                int64_t n_isects, int64_t n_tiles, int tile_bits,
                                                int64_t* __restrict__ isect_ids, int32_t* __restrict__ flatten_ids,
-                                               uint32_t* s_keys, uint32_t* s_vals, uint32_t* s_wcnt,
+                                               uint2* s_kv, uint32_t* s_wcnt,
                                                uint32_t* s_dstart, uint32_t* s_bits) {
   int64_t start, end;
   list_range(list, tile_start, n_lists, n_isects, &start, &end);
   sort_range<B, ITEMS>(pairs + start, end - start, list_hi(list, n_tiles, tile_bits), isect_ids + start,
-                       flatten_ids + start, s_keys, s_vals, s_wcnt, s_dstart, s_bits);
+                       flatten_ids + start, s_kv, s_wcnt, s_dstart, s_bits);
 }
 
 template <int B, int ITEMS>
 struct TileSortLds {
   using S = TileSorter<B, ITEMS>;
-  uint32_t keys[S::CAP];
-  uint32_t vals[S::CAP];
+  uint2 kv[S::CAP];
   uint32_t wcnt[S::W * 256];
   uint32_t dstart[256];
   uint32_t bits[4];  // OR and AND of the keys, OR and AND of the ids
@@ -877,7 +890,7 @@ __global__ void __launch_bounds__(B) bucket_tile_sort_kernel(const uint2* __rest
   const int64_t list = blockIdx.x;
   if (tile_offsets && threadIdx.x == 0) tile_offsets[list] = tile_start[list];
   sort_tile_list<B, ITEMS>(list, pairs, tile_start, n_lists, n_isects, n_tiles, tile_bits, isect_ids, flatten_ids,
-                           sh.keys, sh.vals, sh.wcnt, sh.dstart, sh.bits);
+                           sh.kv, sh.wcnt, sh.dstart, sh.bits);
 }
 
 // Block b sorts list b of one long class (the tile pass's binning); blocks
@@ -893,7 +906,7 @@ __global__ void __launch_bounds__(B) bucket_tile_sort_class_kernel(const uint2* 
   __shared__ TileSortLds<B, ITEMS> sh;
   if (static_cast<int>(blockIdx.x) >= *class_count) return;
   sort_tile_list<B, ITEMS>(class_list[blockIdx.x], pairs, tile_start, n_lists, n_isects, n_tiles, tile_bits,
-                           isect_ids, flatten_ids, sh.keys, sh.vals, sh.wcnt, sh.dstart, sh.bits);
+                           isect_ids, flatten_ids, sh.kv, sh.wcnt, sh.dstart, sh.bits);
 }
 
 // Lists longer than the LDS sorts hold (class 3). One block per list takes
@@ -1142,7 +1155,7 @@ __global__ void __launch_bounds__(kHugeBlock) bucket_huge_sort_kernel(uint2* __r
     for (int r = 0; r < nrun; ++r) {
       const int r0 = s_run[r], r1 = s_run[r + 1];
       sort_range<kHugeBlock, kRunItems>(b + r0, r1 - r0, hi, isect_ids + start + r0, flatten_ids + start + r0,
-                                        sh.keys, sh.vals, sh.wcnt, sh.dstart, sh.bits);
+                                        sh.kv, sh.wcnt, sh.dstart, sh.bits);
       __syncthreads();  // the sort's LDS is reused by the next run
     }
   }
