@@ -150,9 +150,12 @@ bool bucketed_enabled() {
   return on;
 }
 
+// Packed inputs take it too when their rows are grouped by image (the packed
+// projection's order), which the count step checks on the device; otherwise
+// they fall back to the depth-presorted path after the read-back.
 bool use_bucketed(const IntersectTileInput& input) {
   const auto& p = input.params;
-  if (!p.sort || p.packed || !bucketed_enabled()) return false;
+  if (!p.sort || !bucketed_enabled()) return false;
   return accutile(input) ? gsplat_hip_isect_bucket_accutile_supported(p.I, p.tile_width, p.tile_height)
                          : gsplat_hip_isect_bucket_supported(p.I, p.tile_width, p.tile_height);
 }
@@ -163,7 +166,9 @@ bool use_bucketed(const IntersectTileInput& input) {
 // the wait: the copy lands in a pinned host word and an event marks it, so
 // the wait ends when the copy is done rather than when the stream drains.
 struct CountReadback {
-  int64_t* host = nullptr;  // [2]: the count and, for the bucketed path, the longest tile list
+  // [3]: the count and, for the bucketed path, the longest tile list and
+  // (packed rows) the ungrouped flag
+  int64_t* host = nullptr;
   hipEvent_t done = nullptr;
 };
 
@@ -176,7 +181,7 @@ CountReadback& readback_slot() {
   CountReadback& r = slots[dev];
   if (!r.host) {
     void* p = nullptr;
-    if (hipHostMalloc(&p, 2 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess)
+    if (hipHostMalloc(&p, 4 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess)
       throw std::runtime_error("intersect_tile: pinned host allocation for the count failed.");
     r.host = static_cast<int64_t*>(p);
   }
@@ -329,10 +334,12 @@ std::vector<array> gsplat_intersect_tile_sort(const array& isect_ids, const arra
 // longest tile list: the count kernels (queued), then, once the two words are
 // on the host, the M-long outputs and the scatter + tile sort.
 struct BucketState {
-  array means2d, radii, depths, conics, opacities, tiles_per_gauss, totals, ws1;
+  array means2d, radii, depths, conics, opacities, image_ids, tiles_per_gauss, totals, ws1;
   size_t ws1_bytes = 0;
-  bool ell = false;  // ellipse tiles (conics and opacities held)
+  bool ell = false;     // ellipse tiles (conics and opacities held)
+  bool packed = false;  // packed rows (image_ids held)
   void* stream = nullptr;
+  int readback_words() const { return packed ? 3 : 2; }
 };
 
 BucketState intersect_bucketed_count(const IntersectTileInput& input, void* stream) {
@@ -344,10 +351,27 @@ BucketState intersect_bucketed_count(const IntersectTileInput& input, void* stre
   const auto& p = input.params;
   const int64_t numel = b.depths.numel();
   b.tiles_per_gauss = at::empty(input.depths.sizes(), i32_like(b.means2d));
-  b.totals = at::empty({2}, i64_like(b.means2d));
+  b.totals = at::empty({3}, i64_like(b.means2d));
+  b.ell = accutile(input);
+  b.packed = p.packed;
+  if (b.packed) {
+    b.image_ids = contig(input.image_ids.to(at::kInt));
+    if (b.ell) {
+      b.conics = contig(input.conics);
+      b.opacities = contig(input.opacities);
+    }
+    b.ws1_bytes =
+        gsplat_hip_isect_bucket_count_packed_workspace_size(p.I, numel, p.tile_size, p.tile_width, p.tile_height);
+    b.ws1 = workspace(b.ws1_bytes, b.means2d);
+    check(gsplat_hip_isect_bucket_count_packed(
+        b.means2d.data_ptr<float>(), b.radii.data_ptr<int32_t>(), b.ell ? b.conics.data_ptr<float>() : nullptr,
+        b.ell ? b.opacities.data_ptr<float>() : nullptr, b.image_ids.data_ptr<int32_t>(), p.I, numel, p.tile_size,
+        p.tile_width, p.tile_height, b.tiles_per_gauss.data_ptr<int32_t>(), b.totals.data_ptr<int64_t>(),
+        b.ws1.data_ptr<uint8_t>(), b.ws1_bytes, stream));
+    return b;
+  }
   b.ws1_bytes = gsplat_hip_isect_bucket_count_workspace_size(p.I, numel, p.tile_size, p.tile_width, p.tile_height);
   b.ws1 = workspace(b.ws1_bytes, b.means2d);
-  b.ell = accutile(input);
   if (b.ell) {
     b.conics = contig(input.conics);
     b.opacities = contig(input.opacities);
@@ -364,11 +388,21 @@ BucketState intersect_bucketed_count(const IntersectTileInput& input, void* stre
   return b;
 }
 
+std::vector<array> intersect_presorted(const IntersectTileInput& input, void* stream);
+
 std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, const BucketState& b, int total,
-                                             int64_t longest, array* tile_offsets) {
+                                             int64_t longest, bool ungrouped, array* tile_offsets) {
   const auto& p = input.params;
   const int64_t numel = b.depths.numel();
   void* stream = b.stream;
+  if (ungrouped) {
+    // packed rows not grouped by image: the counts are not valid; the
+    // depth-presorted path recounts
+    auto out = intersect_presorted(input, stream);
+    if (tile_offsets)
+      *tile_offsets = gsplat_intersect_offset(out[kIsectIds], p.I, p.tile_width, p.tile_height, input.s);
+    return out;
+  }
   array ids = at::empty({total}, i64_like(b.means2d));
   array flat = at::empty({total}, i32_like(b.means2d));
   if (tile_offsets) *tile_offsets = at::empty({p.I, p.tile_height, p.tile_width}, i32_like(b.means2d));
@@ -381,7 +415,14 @@ std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, co
     const size_t ws2_bytes = gsplat_hip_isect_bucket_sort_workspace_size(total);
     array ws2 = workspace(ws2_bytes, b.means2d);
     int32_t* offsets_out = tile_offsets ? tile_offsets->data_ptr<int32_t>() : nullptr;
-    if (b.ell)
+    if (b.packed)
+      check(gsplat_hip_isect_bucket_sort_packed(
+          b.means2d.data_ptr<float>(), b.radii.data_ptr<int32_t>(), b.ell ? b.conics.data_ptr<float>() : nullptr,
+          b.ell ? b.opacities.data_ptr<float>() : nullptr, b.depths.data_ptr<float>(),
+          b.image_ids.data_ptr<int32_t>(), p.I, numel, p.tile_size, p.tile_width, p.tile_height, total, longest,
+          ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), offsets_out, b.ws1.data_ptr<uint8_t>(), b.ws1_bytes,
+          ws2.data_ptr<uint8_t>(), ws2_bytes, stream));
+    else if (b.ell)
       check(gsplat_hip_isect_bucket_sort_accutile(
           b.means2d.data_ptr<float>(), b.radii.data_ptr<int32_t>(), b.conics.data_ptr<float>(),
           b.opacities.data_ptr<float>(), b.depths.data_ptr<float>(), p.I, numel, p.tile_size, p.tile_width,
@@ -405,7 +446,13 @@ std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, co
                                      ws3_bytes, stream));
   const size_t ws4_bytes = gsplat_hip_isect_encode_sorted_workspace_size(total);
   array ws4 = workspace(ws4_bytes, b.means2d);
-  if (b.ell)
+  if (b.packed)
+    check(gsplat_hip_isect_encode_sorted_packed(
+        b.means2d.data_ptr<float>(), b.radii.data_ptr<int32_t>(), b.ell ? b.conics.data_ptr<float>() : nullptr,
+        b.ell ? b.opacities.data_ptr<float>() : nullptr, b.image_ids.data_ptr<int32_t>(), b.depths.data_ptr<float>(),
+        perm.data_ptr<int32_t>(), offs.data_ptr<int32_t>(), p.I, numel, p.tile_size, p.tile_width, p.tile_height,
+        total, ids.data_ptr<int64_t>(), flat.data_ptr<int32_t>(), ws4.data_ptr<uint8_t>(), ws4_bytes, stream));
+  else if (b.ell)
     check(gsplat_hip_isect_encode_sorted_accutile(
         b.means2d.data_ptr<float>(), b.radii.data_ptr<int32_t>(), b.conics.data_ptr<float>(),
         b.opacities.data_ptr<float>(), b.depths.data_ptr<float>(), perm.data_ptr<int32_t>(), offs.data_ptr<int32_t>(),
@@ -426,9 +473,9 @@ std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, co
 std::vector<array> intersect_bucketed(const IntersectTileInput& input, void* stream, array* tile_offsets = nullptr) {
   const BucketState b = intersect_bucketed_count(input, stream);
   CountReadback& r = readback_slot();
-  start_read_total(b.totals, stream, r, 2);
+  start_read_total(b.totals, stream, r, b.readback_words());
   const int total = finish_read_total(r);
-  return intersect_bucketed_finish(input, b, total, r.host[1], tile_offsets);
+  return intersect_bucketed_finish(input, b, total, r.host[1], b.packed && r.host[2] != 0, tile_offsets);
 }
 
 // Read-back slots of split intersections, one per pending call: pinned words
@@ -455,7 +502,7 @@ CountReadback acquire_readback(int dev) {
   }
   CountReadback r;
   void* p = nullptr;
-  if (hipHostMalloc(&p, 2 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess)
+  if (hipHostMalloc(&p, 4 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess)
     throw std::runtime_error("intersect_tile: pinned host allocation for the count failed.");
   r.host = static_cast<int64_t*>(p);
   if (hipEventCreateWithFlags(&r.done, hipEventDisableTiming) != hipSuccess)
@@ -477,6 +524,12 @@ std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& in
   const c10::DeviceGuard guard(input.means2d.device());
   void* stream = stream_for(input.s, input.means2d);
   if (use_bucketed(input)) return intersect_bucketed(input, stream);
+  return intersect_presorted(input, stream);
+}
+
+// Counts, then (sort) the depth-presorted encode and 32-bit tile-key sort, or
+// (no sort) the pair-major encode.
+std::vector<array> intersect_presorted(const IntersectTileInput& input, void* stream) {
   Counted c = count_and_scan(input, stream, !input.params.sort);
   const array means2d = contig(input.means2d);
   const array radii = contig(input.radii);
@@ -595,7 +648,7 @@ std::shared_ptr<PendingIntersect> gsplat_intersect_tile_offsets_begin(const Inte
   if (hipGetDevice(&pending->dev) != hipSuccess) throw std::runtime_error("intersect_tile: no current HIP device.");
   pending->rb = acquire_readback(pending->dev);
   pending->bucketed = true;
-  start_read_total(pending->state.totals, stream, pending->rb, 2);
+  start_read_total(pending->state.totals, stream, pending->rb, pending->state.readback_words());
   return pending;
 }
 
@@ -605,10 +658,11 @@ std::vector<array> gsplat_intersect_tile_offsets_end(const std::shared_ptr<Pendi
   const c10::DeviceGuard guard(pending->input.means2d.device());
   const int total = finish_read_total(pending->rb);
   const int64_t longest = pending->rb.host[1];
+  const bool ungrouped = pending->state.packed && pending->rb.host[2] != 0;
   pending->finished = true;
   release_readback(pending->dev, pending->rb);
   array offsets;
-  auto out = intersect_bucketed_finish(pending->input, pending->state, total, longest, &offsets);
+  auto out = intersect_bucketed_finish(pending->input, pending->state, total, longest, ungrouped, &offsets);
   out.push_back(offsets);
   pending->result = out;
   pending->state = BucketState();  // the count workspace goes back to the allocator

@@ -36,6 +36,13 @@
 //     depth byte into runs that the LDS sort takes in turn.
 // Steps 4-5 need M only to size their outputs, and the longest list (read
 // back with M) to launch only the classes present.
+//
+// Rows: dense inputs hold N Gaussians per image, row image * N + n. Packed
+// inputs (one row per visible (image, Gaussian) pair, grouped by image as the
+// packed projection writes them) hold the rows of image i at [row_start[i],
+// row_start[i + 1]), found on the device from the rows' image ids. Either
+// way an image's rows are cut into segments of at most gpb rows, one grid /
+// scatter block each, and a row's flatten id is its row index.
 #include <algorithm>
 #include <string>
 
@@ -54,12 +61,46 @@ constexpr int kTilePassBlock = 1024;
 inline size_t align256(size_t b) { return (b + 255) / 256 * 256; }
 
 struct BucketDims {
-  int64_t I, N, bpi;  // images, Gaussians per image, grid blocks per image
+  int64_t I, N, bpi;  // images, Gaussians per image, grid blocks per image (dense)
   int64_t gpb;        // Gaussians per grid / scatter block (a multiple of kBucketBlock)
   int tw, th, ts;
   int64_t G;          // grid words per image, (th + 1)(tw + 1)
   int64_t n_tiles;    // tw * th
+  int64_t n_seg;      // grid / scatter blocks: I * bpi (dense), ceil(rows / gpb) + I at most (packed)
+  // packed rows (nullptr: dense): [I + 1] first segment and first row of each
+  // image, the rows' image ids, and a word set when a row's image id is not
+  // its segment's (rows not grouped by image, or ids outside [0, I))
+  const int32_t* seg_start;
+  const int32_t* row_start;
+  const int32_t* image_ids;
+  int32_t* ungrouped;
 };
+
+// The rows of grid / scatter block lb: image, first row and row count (0 for
+// the packed layout's spare blocks past the last segment).
+struct Segment {
+  int64_t image, row0, rows;
+};
+
+__device__ __forceinline__ Segment segment_of(const BucketDims& d, int64_t lb) {
+  Segment s;
+  if (!d.seg_start) {
+    s.image = lb / d.bpi;
+    const int64_t n0 = (lb % d.bpi) * d.gpb;
+    s.row0 = s.image * d.N + n0;
+    s.rows = max<int64_t>(0, min<int64_t>(d.gpb, d.N - n0));
+    return s;
+  }
+  int lo = 0, hi = static_cast<int>(d.I) - 1;  // the last image whose first segment is <= lb
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (d.seg_start[mid] <= lb) lo = mid; else hi = mid - 1;
+  }
+  s.image = lo;
+  s.row0 = d.row_start[lo] + (lb - d.seg_start[lo]) * d.gpb;
+  s.rows = max<int64_t>(0, min<int64_t>(d.gpb, d.row_start[lo + 1] - s.row0));
+  return s;
+}
 
 // Tile sort capacities: lists up to kSortCap[0] take the <256, 10> sort in
 // one launch over every list; longer lists are binned by the tile pass into
@@ -72,23 +113,29 @@ struct BucketDims {
 constexpr int kSortCap[4] = {256 * 10, 512 * 8, 512 * 16, 1024 * 16};
 constexpr int kSortClasses = 4;
 
-// count workspace: per-block grids [I * bpi][G], image total grids [I][G],
-// tile starts [I * n_tiles], the long lists of each class [4][I * n_tiles]
-// and the class sizes [4] (+ the split sort's fallback count)
+// count workspace: per-block grids [n_seg][G], image total grids [I][G],
+// tile starts [I * n_tiles], the long lists of each class [4][I * n_tiles],
+// the class sizes [4] (+ the split sort's fallback count), and for packed
+// rows the segment and row starts [I + 1] each and the ungrouped word
 struct CountLayout {
   int32_t* partials;
   int32_t* totals;
   int32_t* tile_start;
   int32_t* class_lists;
   int32_t* class_counts;
+  int32_t* seg_start;
+  int32_t* row_start;
+  int32_t* ungrouped;
 };
 
 size_t count_layout(const BucketDims& d, CountLayout* l, void* base) {
-  const size_t a = align256(static_cast<size_t>(d.I * d.bpi * d.G) * 4);
+  const size_t a = align256(static_cast<size_t>(d.n_seg * d.G) * 4);
   const size_t b = align256(static_cast<size_t>(d.I * d.G) * 4);
   const size_t c = align256(static_cast<size_t>(d.I * d.n_tiles) * 4);
   const size_t e = align256(static_cast<size_t>(kSortClasses * d.I * d.n_tiles) * 4);
   const size_t f = align256((kSortClasses + 1) * 4);  // class sizes, then the split sort's fallback count
+  const size_t r = align256(static_cast<size_t>(d.I + 1) * 4);  // packed: segment / row starts
+  const size_t rows_b = d.bpi == 0 ? 2 * r + align256(4) : 0;
   if (l && base) {
     char* p = static_cast<char*>(base);
     l->partials = reinterpret_cast<int32_t*>(p);
@@ -96,8 +143,46 @@ size_t count_layout(const BucketDims& d, CountLayout* l, void* base) {
     l->tile_start = reinterpret_cast<int32_t*>(p + a + b);
     l->class_lists = reinterpret_cast<int32_t*>(p + a + b + c);
     l->class_counts = reinterpret_cast<int32_t*>(p + a + b + c + e);
+    l->seg_start = rows_b ? reinterpret_cast<int32_t*>(p + a + b + c + e + f) : nullptr;
+    l->row_start = rows_b ? reinterpret_cast<int32_t*>(p + a + b + c + e + f + r) : nullptr;
+    l->ungrouped = rows_b ? reinterpret_cast<int32_t*>(p + a + b + c + e + f + 2 * r) : nullptr;
   }
-  return a + b + c + e + f;
+  return a + b + c + e + f + rows_b;
+}
+
+// Packed rows (one block of kRowsBlock threads): each image's first row as
+// the lower bound of its id in the rows' ids (made non-decreasing, so the
+// segments stay inside [0, rows) whatever the ids), its segments of at most
+// gpb rows, and the ungrouped word cleared -- or set at once when the ids do
+// not start at image 0 or end below I.
+constexpr int kRowsBlock = 256;
+
+__global__ void __launch_bounds__(kRowsBlock) bucket_rows_kernel(const int32_t* __restrict__ image_ids, int64_t rows,
+                                                                 int64_t I, int64_t gpb, int32_t* __restrict__ row_start,
+                                                                 int32_t* __restrict__ seg_start,
+                                                                 int32_t* __restrict__ ungrouped) {
+  const int t = threadIdx.x;
+  for (int64_t i = t; i <= I; i += kRowsBlock) {
+    int64_t lo = 0, hi = rows;
+    while (lo < hi) {
+      const int64_t mid = (lo + hi) >> 1;
+      if (image_ids[mid] < i) lo = mid + 1; else hi = mid;
+    }
+    row_start[i] = static_cast<int32_t>(lo);
+  }
+  __syncthreads();
+  if (t != 0) return;
+  const bool bad = row_start[0] != 0 || row_start[I] != rows;
+  int32_t prev = 0;
+  int64_t seg = 0;
+  for (int64_t i = 0; i <= I; ++i) {
+    const int32_t r = max(row_start[i], prev);
+    row_start[i] = r;
+    if (i > 0) seg += (r - prev + gpb - 1) / gpb;
+    seg_start[i] = static_cast<int32_t>(seg);
+    prev = r;
+  }
+  *ungrouped = bad ? 1 : 0;
 }
 
 // The grid and scatter passes' block b (in dispatch order) takes the
@@ -210,16 +295,22 @@ __device__ __forceinline__ int ell_round(const GaussTileIn& in, bool valid, cons
   return static_cast<int>(tot);
 }
 
-// Thread t's Gaussian of the round starting at i0 (zeros past N): loaded one
-// round ahead, so the loads are in flight while the previous round's rows
+// Thread t's Gaussian of the round (row idx; zeros past the segment): loaded
+// one round ahead, so the loads are in flight while the previous round's rows
 // are dealt.
 __device__ __forceinline__ GaussTileIn ell_load(const float* __restrict__ means2d, const int32_t* __restrict__ radii,
                                                 const float* __restrict__ conics,
-                                                const float* __restrict__ opacities, const BucketDims& d,
-                                                int64_t image, int64_t n) {
+                                                const float* __restrict__ opacities, int64_t idx, bool valid) {
   GaussTileIn in = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0, 0};
-  if (n < d.N) in = load_gauss_tile_in(means2d, radii, conics, opacities, image * d.N + n);
+  if (valid) in = load_gauss_tile_in(means2d, radii, conics, opacities, idx);
   return in;
+}
+
+// Packed rows: a row whose image id is not its segment's marks the input
+// ungrouped (the caller then takes another path; nothing here reads out of
+// bounds either way).
+__device__ __forceinline__ void check_row_image(const BucketDims& d, int64_t idx, int64_t image) {
+  if (d.image_ids && d.image_ids[idx] != image) atomicOr(d.ungrouped, 1);
 }
 
 // Slots of chunk [c, c + kEllRowChunk) held by this thread's rows
@@ -252,17 +343,17 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_grid_kernel(const float* 
                                                                    int32_t* __restrict__ partials) {
   extern __shared__ int32_t sg[];  // [G]; ELL: then the round's records, row prefix and counts
   const int t = threadIdx.x;
-  const int64_t lb = logical_block(blockIdx.x, d.I * d.bpi);
-  const int64_t image = lb / d.bpi;
-  const int64_t n0 = (lb % d.bpi) * d.gpb;
+  const int64_t lb = logical_block(blockIdx.x, d.n_seg);
+  const Segment seg = segment_of(d, lb);
+  if (d.seg_start && seg.rows == 0) return;  // a packed spare block: its grid is never read
+  const int64_t image = seg.image;
   const int W1 = d.tw + 1;
   for (int j = t; j < d.G; j += kBucketBlock) sg[j] = 0;
   __syncthreads();
   if constexpr (!ELL) {
-    for (int64_t i = t; i < d.gpb; i += kBucketBlock) {
-      const int64_t n = n0 + i;
-      if (n >= d.N) break;
-      const int64_t idx = image * d.N + n;
+    for (int64_t i = t; i < seg.rows; i += kBucketBlock) {
+      const int64_t idx = seg.row0 + i;
+      check_row_image(d, idx, image);
       const TileRect r = aabb_tile_rect(means2d[idx * 2], means2d[idx * 2 + 1], radii[idx * 2], radii[idx * 2 + 1],
                                         d.ts, d.tw, d.th);
       const int area = (r.max_y - r.min_y) * (r.max_x - r.min_x);
@@ -278,13 +369,16 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_grid_kernel(const float* 
     EllRec* s_r = reinterpret_cast<EllRec*>(sg + d.G);
     uint32_t* s_own = reinterpret_cast<uint32_t*>(s_r + kBucketBlock);  // [kEllRowChunk] chunk slots
     int32_t* s_cnt = reinterpret_cast<int32_t*>(s_own + kEllRowChunk);  // entries per Gaussian
-    GaussTileIn next = ell_load(means2d, radii, conics, opacities, d, image, n0 + t);
-    for (int64_t i0 = 0; i0 < d.gpb; i0 += kBucketBlock) {
-      const int64_t n = n0 + i0 + t;
+    GaussTileIn next = ell_load(means2d, radii, conics, opacities, seg.row0 + t, t < seg.rows);
+    for (int64_t i0 = 0; i0 < seg.rows; i0 += kBucketBlock) {
+      const bool valid = i0 + t < seg.rows;
+      const int64_t idx = seg.row0 + i0 + t;
+      if (valid) check_row_image(d, idx, image);
       s_cnt[t] = 0;
       int pre, my_rows;
-      const int rows = ell_round(next, n < d.N, d, s_r, &pre, &my_rows);  // syncs
-      if (i0 + kBucketBlock < d.gpb) next = ell_load(means2d, radii, conics, opacities, d, image, n + kBucketBlock);
+      const int rows = ell_round(next, valid, d, s_r, &pre, &my_rows);  // syncs
+      if (i0 + kBucketBlock < seg.rows)
+        next = ell_load(means2d, radii, conics, opacities, idx + kBucketBlock, i0 + kBucketBlock + t < seg.rows);
       for (int c = 0; c < rows; c += kEllRowChunk) {
         ell_owners(c, pre, my_rows, s_own);
         __syncthreads();
@@ -306,7 +400,7 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_grid_kernel(const float* 
       // the last chunk's barrier ordered every count of this round; the next
       // round's block scan orders this read before its slots and counts are
       // written by other threads
-      if (n < d.N) tiles_per_gauss[image * d.N + n] = s_cnt[t];
+      if (valid) tiles_per_gauss[idx] = s_cnt[t];
     }
   }
   __syncthreads();
@@ -318,9 +412,9 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_grid_kernel(const float* 
 // the image total. Thread (seg, col) sums a contiguous range of blocks for
 // grid point col of its group (a wave reads 64 consecutive grid words of one
 // block grid); the 16 range sums are scanned in LDS. A range of up to
-// kScanRegs blocks (bpi <= 512) is loaded once, all loads in flight
-// together, and kept in registers for the write-back.
-constexpr int kScanRegs = 32;
+// kScanRegs blocks (768 blocks per image) is loaded once, all loads in
+// flight together, and kept in registers for the write-back.
+constexpr int kScanRegs = 48;
 
 __global__ void __launch_bounds__(kColGroup* kColSegs) bucket_block_scan_kernel(BucketDims d,
                                                                                   int32_t* __restrict__ partials,
@@ -329,10 +423,13 @@ __global__ void __launch_bounds__(kColGroup* kColSegs) bucket_block_scan_kernel(
   const int col = threadIdx.x % kColGroup, seg = threadIdx.x / kColGroup;
   const int64_t g = static_cast<int64_t>(blockIdx.x) * kColGroup + col;
   const int64_t image = blockIdx.y;
-  const int64_t per = (d.bpi + kColSegs - 1) / kColSegs;
+  // the image's blocks: [s0, s0 + nb)
+  const int64_t s0 = d.seg_start ? d.seg_start[image] : image * d.bpi;
+  const int64_t nb = d.seg_start ? d.seg_start[image + 1] - s0 : d.bpi;
+  const int64_t per = (nb + kColSegs - 1) / kColSegs;
   const bool in_regs = per <= kScanRegs;  // uniform
-  const int64_t b0 = min<int64_t>(d.bpi, seg * per), b1 = min<int64_t>(d.bpi, b0 + per);
-  int32_t* base = partials + image * d.bpi * d.G + g;
+  const int64_t b0 = min<int64_t>(nb, seg * per), b1 = min<int64_t>(nb, b0 + per);
+  int32_t* base = partials + s0 * d.G + g;
   int32_t v[kScanRegs];
   int32_t s = 0;
   if (g < d.G) {
@@ -462,6 +559,7 @@ __global__ void __launch_bounds__(kTilePassBlock) bucket_tile_pass_kernel(Bucket
     for (int w = 1; w < kTilePassBlock / kWave; ++w) largest = max(largest, s_max[w]);
     readback[0] = offset;
     readback[1] = largest;
+    if (d.ungrouped) readback[2] = *d.ungrouped;
   }
   if (t <= kSortClasses) class_counts[t] = t < kSortClasses ? s_cls[t] : 0;  // + the fallback count
 }
@@ -544,9 +642,10 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_scatter_kernel(const floa
                                                                       int64_t n_isects, uint2* __restrict__ pairs) {
   extern __shared__ int32_t sg[];  // [G] per-tile cursors, then the round's records
   const int t = threadIdx.x;
-  const int64_t lb = logical_block(blockIdx.x, d.I * d.bpi);
-  const int64_t image = lb / d.bpi;
-  const int64_t n0 = (lb % d.bpi) * d.gpb;
+  const int64_t lb = logical_block(blockIdx.x, d.n_seg);
+  const Segment seg = segment_of(d, lb);
+  if (d.seg_start && seg.rows == 0) return;  // a packed spare block
+  const int64_t image = seg.image;
   const int W1 = d.tw + 1;
   const int32_t* ex = partials + lb * d.G;
   for (int j = t; j < d.G; j += kBucketBlock) sg[j] = ex[j];
@@ -563,11 +662,10 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_scatter_kernel(const floa
     uint32_t* s_xy = reinterpret_cast<uint32_t*>(s_pre + kBucketBlock + 1);  // rect min x | min y << 16
     int32_t* s_w = reinterpret_cast<int32_t*>(s_xy + kBucketBlock);          // rect width
     uint32_t* s_d = reinterpret_cast<uint32_t*>(s_w + kBucketBlock);         // depth bits
-    for (int64_t i0 = 0; i0 < d.gpb; i0 += kBucketBlock) {
-      const int64_t n = n0 + i0 + t;
+    for (int64_t i0 = 0; i0 < seg.rows; i0 += kBucketBlock) {
       int area = 0;
-      if (n < d.N) {
-        const int64_t idx = image * d.N + n;
+      if (i0 + t < seg.rows) {
+        const int64_t idx = seg.row0 + i0 + t;
         const TileRect r = aabb_tile_rect(means2d[idx * 2], means2d[idx * 2 + 1], radii[idx * 2],
                                           radii[idx * 2 + 1], d.ts, d.tw, d.th);
         area = (r.max_y - r.min_y) * (r.max_x - r.min_x);
@@ -580,7 +678,7 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_scatter_kernel(const floa
       s_pre[t] = static_cast<int32_t>(pre);
       if (t == 0) s_pre[kBucketBlock] = static_cast<int32_t>(tot);
       __syncthreads();
-      const uint32_t id0 = static_cast<uint32_t>(image * d.N + n0 + i0);
+      const uint32_t id0 = static_cast<uint32_t>(seg.row0 + i0);
       scatter_units<false>(tot, kBucketBlock, s_pre, s_xy, s_w, s_d, id0, W1, sg, n_isects, pairs);
       __syncthreads();  // the round's LDS records are rewritten next round
     }
@@ -591,14 +689,16 @@ __global__ void __launch_bounds__(kBucketBlock) bucket_scatter_kernel(const floa
     int32_t* s_epre = reinterpret_cast<int32_t*>(s_own + kEllRowChunk);      // [kEllRowChunk + 1] entry prefix
     uint32_t* s_xy = reinterpret_cast<uint32_t*>(s_epre + kEllRowChunk + 1);  // row c0 | y << 16
     int32_t* s_w = reinterpret_cast<int32_t*>(s_xy + kEllRowChunk);          // row width | Gaussian << 16
-    GaussTileIn next = ell_load(means2d, radii, conics, opacities, d, image, n0 + t);
-    for (int64_t i0 = 0; i0 < d.gpb; i0 += kBucketBlock) {
-      const int64_t n = n0 + i0 + t;
-      if (n < d.N) s_d[t] = __float_as_uint(depths[image * d.N + n]);
+    GaussTileIn next = ell_load(means2d, radii, conics, opacities, seg.row0 + t, t < seg.rows);
+    for (int64_t i0 = 0; i0 < seg.rows; i0 += kBucketBlock) {
+      const bool valid = i0 + t < seg.rows;
+      const int64_t idx = seg.row0 + i0 + t;
+      if (valid) s_d[t] = __float_as_uint(depths[idx]);
       int pre, my_rows;
-      const int rows = ell_round(next, n < d.N, d, s_r, &pre, &my_rows);  // syncs
-      if (i0 + kBucketBlock < d.gpb) next = ell_load(means2d, radii, conics, opacities, d, image, n + kBucketBlock);
-      const uint32_t id0 = static_cast<uint32_t>(image * d.N + n0 + i0);
+      const int rows = ell_round(next, valid, d, s_r, &pre, &my_rows);  // syncs
+      if (i0 + kBucketBlock < seg.rows)
+        next = ell_load(means2d, radii, conics, opacities, idx + kBucketBlock, i0 + kBucketBlock + t < seg.rows);
+      const uint32_t id0 = static_cast<uint32_t>(seg.row0 + i0);
       for (int c = 0; c < rows; c += kEllRowChunk) {
         const int nr = min(kEllRowChunk, rows - c);
         ell_owners(c, pre, my_rows, s_own);
@@ -1212,18 +1312,24 @@ __global__ void __launch_bounds__(kHugeBlock) bucket_huge_radix_kernel(uint2* __
   }
 }
 
+// packed: numel rows of I images (grouped by image), segments found on the
+// device; otherwise numel = I * N.
 int bucket_dims(const char* what, int64_t I, int64_t numel, int32_t ts, int32_t tw, int32_t th, bool ell,
-                BucketDims* d) {
-  if (I <= 0 || numel < 0 || ts <= 0 || tw <= 0 || th <= 0 || numel % I != 0)
+                BucketDims* d, bool packed = false) {
+  if (I <= 0 || numel < 0 || ts <= 0 || tw <= 0 || th <= 0 || (!packed && numel % I != 0))
     return invalid(std::string(what) + ": invalid sizes.");
+  if (packed && (numel > INT32_MAX || I > INT32_MAX - 1)) return invalid(std::string(what) + ": invalid sizes.");
   if (tw >= 65535 || th >= 65535) return invalid(std::string(what) + ": tile grid too large.");
+  *d = BucketDims{};
   d->I = I;
-  d->N = numel / I;
-  // about two grid / scatter blocks per CU of a 256-CU MI355X (at least one
-  // round of kBucketBlock Gaussians per block, at most 16 rounds)
+  d->N = packed ? 0 : numel / I;
+  // about two grid / scatter blocks per CU of a 256-CU MI355X: the nearest
+  // whole number of rounds of kBucketBlock Gaussians (at least one, at most
+  // 16); rounding up would leave 1.2 blocks per CU at 640K rows
   const int64_t want = (numel + 511) / 512;
-  d->gpb = std::min<int64_t>(16, std::max<int64_t>(1, (want + kBucketBlock - 1) / kBucketBlock)) * kBucketBlock;
-  d->bpi = std::max<int64_t>(1, (d->N + d->gpb - 1) / d->gpb);
+  d->gpb = std::min<int64_t>(16, std::max<int64_t>(1, (want + kBucketBlock / 2) / kBucketBlock)) * kBucketBlock;
+  d->bpi = packed ? 0 : std::max<int64_t>(1, (d->N + d->gpb - 1) / d->gpb);
+  d->n_seg = packed ? (numel + d->gpb - 1) / d->gpb + I : I * d->bpi;
   d->tw = tw;
   d->th = th;
   d->ts = ts;
@@ -1231,8 +1337,16 @@ int bucket_dims(const char* what, int64_t I, int64_t numel, int32_t ts, int32_t 
   d->n_tiles = static_cast<int64_t>(tw) * th;
   if (d->G > (ell ? kBucketMaxGridEll : kBucketMaxGrid))
     return invalid(std::string(what) + ": tile grid larger than the bucketed intersection supports.");
-  if (I * d->bpi > kMaxGridX || I * d->n_tiles > INT32_MAX) return invalid(std::string(what) + ": too many tiles.");
+  if (d->n_seg > kMaxGridX || I * d->n_tiles > INT32_MAX) return invalid(std::string(what) + ": too many tiles.");
   return GSPLAT_OK;
+}
+
+// The packed rows' tables in the count workspace (after count_layout).
+void attach_rows(BucketDims* d, const CountLayout& l, const int32_t* image_ids) {
+  d->seg_start = l.seg_start;
+  d->row_start = l.row_start;
+  d->image_ids = image_ids;
+  d->ungrouped = l.ungrouped;
 }
 
 int tile_bits_of(int64_t I, int tw, int th, int* tile_bits) {
@@ -1246,24 +1360,33 @@ bool grid_supported(int64_t I, int32_t tw, int32_t th, int64_t max_grid) {
   return I > 0 && tw > 0 && th > 0 && tw < 65535 && th < 65535 && static_cast<int64_t>(tw + 1) * (th + 1) <= max_grid;
 }
 
-// Counts (steps 1-3); ell: ellipse tiles of conics / opacities.
+// Counts (steps 1-3); ell: ellipse tiles of conics / opacities; packed:
+// numel rows with their image_ids (totals_dev then takes a third word, the
+// ungrouped flag).
 int bucket_count(bool ell, const float* means2d, const int32_t* radii, const float* conics, const float* opacities,
-                 int64_t I, int64_t numel, int32_t tile_size, int32_t tile_width, int32_t tile_height,
-                 int32_t* tiles_per_gauss, int64_t* totals_dev, void* workspace, size_t workspace_bytes, void* stream) {
+                 bool packed, const int32_t* image_ids, int64_t I, int64_t numel, int32_t tile_size,
+                 int32_t tile_width, int32_t tile_height, int32_t* tiles_per_gauss, int64_t* totals_dev,
+                 void* workspace, size_t workspace_bytes, void* stream) {
   const char* what = "intersect_tile";
   BucketDims d;
-  int rc = bucket_dims(what, I, numel, tile_size, tile_width, tile_height, ell, &d);
+  int rc = bucket_dims(what, I, numel, tile_size, tile_width, tile_height, ell, &d, packed);
   if (rc) return rc;
   CountLayout l;
   if (!workspace || workspace_bytes < count_layout(d, &l, workspace)) {
     set_error(std::string(what) + ": workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
   }
-  if (!totals_dev || (numel > 0 && (!means2d || !radii || !tiles_per_gauss || (ell && (!conics || !opacities)))))
+  if (!totals_dev || (numel > 0 && (!means2d || !radii || !tiles_per_gauss || (ell && (!conics || !opacities)) ||
+                                    (packed && !image_ids))))
     return invalid(std::string(what) + ": null pointer.");
   hipStream_t s = as_stream(stream);
   const size_t grid_lds = static_cast<size_t>(d.G) * 4;
-  const unsigned blocks = static_cast<unsigned>(I * d.bpi);
+  const unsigned blocks = static_cast<unsigned>(d.n_seg);
+  if (packed) {
+    attach_rows(&d, l, image_ids);
+    KernelTimer timer("isect_bucket_grid", s);
+    bucket_rows_kernel<<<1, kRowsBlock, 0, s>>>(image_ids, numel, I, d.gpb, l.row_start, l.seg_start, l.ungrouped);
+  }
   {
     KernelTimer timer("isect_bucket_grid", s);
     if (ell)
@@ -1285,15 +1408,15 @@ int bucket_count(bool ell, const float* means2d, const int32_t* radii, const flo
   return check_launch(what);
 }
 
-// Scatter + tile sort (steps 4-5); ell as bucket_count's.
+// Scatter + tile sort (steps 4-5); ell, packed and image_ids as bucket_count's.
 int bucket_sort(bool ell, const float* means2d, const int32_t* radii, const float* conics, const float* opacities,
-                const float* depths, int64_t I, int64_t numel, int32_t tile_size, int32_t tile_width,
-                int32_t tile_height, int64_t n_isects, int64_t max_list, int64_t* isect_ids, int32_t* flatten_ids,
-                int32_t* tile_offsets, const void* count_workspace, size_t count_workspace_bytes, void* workspace,
-                size_t workspace_bytes, void* stream) {
+                const float* depths, bool packed, const int32_t* image_ids, int64_t I, int64_t numel, int32_t tile_size,
+                int32_t tile_width, int32_t tile_height, int64_t n_isects, int64_t max_list, int64_t* isect_ids,
+                int32_t* flatten_ids, int32_t* tile_offsets, const void* count_workspace, size_t count_workspace_bytes,
+                void* workspace, size_t workspace_bytes, void* stream) {
   const char* what = "intersect_tile";
   BucketDims d;
-  int rc = bucket_dims(what, I, numel, tile_size, tile_width, tile_height, ell, &d);
+  int rc = bucket_dims(what, I, numel, tile_size, tile_width, tile_height, ell, &d, packed);
   if (rc) return rc;
   int tile_bits = 0;
   if ((rc = tile_bits_of(I, tile_width, tile_height, &tile_bits))) return rc;
@@ -1304,18 +1427,20 @@ int bucket_sort(bool ell, const float* means2d, const int32_t* radii, const floa
     set_error(std::string(what) + ": count workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
   }
+  if (packed) attach_rows(&d, l, image_ids);
   hipStream_t s = as_stream(stream);
   if (n_isects == 0 && !tile_offsets) return GSPLAT_OK;
   if (n_isects > 0 && (!workspace || workspace_bytes < gsplat_hip_isect_bucket_sort_workspace_size(n_isects))) {
     set_error(std::string(what) + ": workspace too small.");
     return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
   }
-  if (n_isects > 0 && (!means2d || !radii || !depths || !isect_ids || !flatten_ids || (ell && (!conics || !opacities))))
+  if (n_isects > 0 && (!means2d || !radii || !depths || !isect_ids || !flatten_ids || (ell && (!conics || !opacities)) ||
+                       (packed && !image_ids)))
     return invalid(std::string(what) + ": null pointer.");
   uint2* pairs = static_cast<uint2*>(workspace);
   if (n_isects > 0) {
     KernelTimer timer("isect_bucket_scatter", s);
-    const unsigned blocks = static_cast<unsigned>(I * d.bpi);
+    const unsigned blocks = static_cast<unsigned>(d.n_seg);
     const size_t grid_lds = static_cast<size_t>(d.G) * 4;
     const size_t lds = grid_lds + (kBucketBlock + 1 + 3 * kBucketBlock) * 4;
     if (ell)
@@ -1391,7 +1516,7 @@ extern "C" int gsplat_hip_isect_bucket_count(const float* means2d, const int32_t
                                              int32_t tile_size, int32_t tile_width, int32_t tile_height,
                                              int32_t* tiles_per_gauss, int64_t* totals_dev, void* workspace,
                                              size_t workspace_bytes, void* stream) {
-  return bucket_count(false, means2d, radii, nullptr, nullptr, I, numel, tile_size, tile_width, tile_height,
+  return bucket_count(false, means2d, radii, nullptr, nullptr, false, nullptr, I, numel, tile_size, tile_width, tile_height,
                       tiles_per_gauss, totals_dev, workspace, workspace_bytes, stream);
 }
 
@@ -1401,7 +1526,7 @@ extern "C" int gsplat_hip_isect_bucket_count_accutile(const float* means2d, cons
                                                       int32_t tile_height, int32_t* tiles_per_gauss,
                                                       int64_t* totals_dev, void* workspace, size_t workspace_bytes,
                                                       void* stream) {
-  return bucket_count(true, means2d, radii, conics, opacities, I, numel, tile_size, tile_width, tile_height,
+  return bucket_count(true, means2d, radii, conics, opacities, false, nullptr, I, numel, tile_size, tile_width, tile_height,
                       tiles_per_gauss, totals_dev, workspace, workspace_bytes, stream);
 }
 
@@ -1415,8 +1540,8 @@ extern "C" int gsplat_hip_isect_bucket_sort(const float* means2d, const int32_t*
                                             int64_t* isect_ids, int32_t* flatten_ids, int32_t* tile_offsets,
                                             const void* count_workspace, size_t count_workspace_bytes,
                                             void* workspace, size_t workspace_bytes, void* stream) {
-  return bucket_sort(false, means2d, radii, nullptr, nullptr, depths, I, numel, tile_size, tile_width, tile_height,
-                     n_isects, max_list, isect_ids, flatten_ids, tile_offsets, count_workspace,
+  return bucket_sort(false, means2d, radii, nullptr, nullptr, depths, false, nullptr, I, numel, tile_size, tile_width,
+                     tile_height, n_isects, max_list, isect_ids, flatten_ids, tile_offsets, count_workspace,
                      count_workspace_bytes, workspace, workspace_bytes, stream);
 }
 
@@ -1427,7 +1552,36 @@ extern "C" int gsplat_hip_isect_bucket_sort_accutile(const float* means2d, const
                                                      int64_t* isect_ids, int32_t* flatten_ids, int32_t* tile_offsets,
                                                      const void* count_workspace, size_t count_workspace_bytes,
                                                      void* workspace, size_t workspace_bytes, void* stream) {
-  return bucket_sort(true, means2d, radii, conics, opacities, depths, I, numel, tile_size, tile_width, tile_height,
-                     n_isects, max_list, isect_ids, flatten_ids, tile_offsets, count_workspace,
+  return bucket_sort(true, means2d, radii, conics, opacities, depths, false, nullptr, I, numel, tile_size, tile_width,
+                     tile_height, n_isects, max_list, isect_ids, flatten_ids, tile_offsets, count_workspace,
                      count_workspace_bytes, workspace, workspace_bytes, stream);
+}
+
+extern "C" size_t gsplat_hip_isect_bucket_count_packed_workspace_size(int64_t I, int64_t nnz, int32_t tile_size,
+                                                                      int32_t tile_width, int32_t tile_height) {
+  BucketDims d;
+  if (bucket_dims("intersect_tile", I, nnz, tile_size, tile_width, tile_height, false, &d, true)) return 0;
+  return count_layout(d, nullptr, nullptr);
+}
+
+extern "C" int gsplat_hip_isect_bucket_count_packed(const float* means2d, const int32_t* radii, const float* conics,
+                                                    const float* opacities, const int32_t* image_ids, int64_t I,
+                                                    int64_t nnz, int32_t tile_size, int32_t tile_width,
+                                                    int32_t tile_height, int32_t* tiles_per_gauss,
+                                                    int64_t* totals_dev, void* workspace, size_t workspace_bytes,
+                                                    void* stream) {
+  return bucket_count(conics != nullptr, means2d, radii, conics, opacities, true, image_ids, I, nnz, tile_size, tile_width,
+                      tile_height, tiles_per_gauss, totals_dev, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gsplat_hip_isect_bucket_sort_packed(const float* means2d, const int32_t* radii, const float* conics,
+                                                   const float* opacities, const float* depths,
+                                                   const int32_t* image_ids, int64_t I, int64_t nnz,
+                                                   int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                                   int64_t n_isects, int64_t max_list, int64_t* isect_ids,
+                                                   int32_t* flatten_ids, int32_t* tile_offsets,
+                                                   const void* count_workspace, size_t count_workspace_bytes,
+                                                   void* workspace, size_t workspace_bytes, void* stream) {
+  return bucket_sort(conics != nullptr, means2d, radii, conics, opacities, depths, true, image_ids, I, nnz, tile_size, tile_width, tile_height, n_isects, max_list, isect_ids, flatten_ids, tile_offsets,
+                     count_workspace, count_workspace_bytes, workspace, workspace_bytes, stream);
 }

@@ -51,34 +51,42 @@ __global__ void __launch_bounds__(kScanBlock) scan_fixup_kernel(int32_t* __restr
   }
 }
 
-// Small inputs (up to kSingleTiles tiles): one block walks the tiles with a
-// carry -- one launch instead of three, which is what a scan of a few
-// thousand values costs.
-constexpr int64_t kSingleTiles = 64;
+// Small inputs (up to kSingleBlock * kSingleItems values): one block of
+// 1024 threads, each scanning kSingleItems consecutive values with every load
+// in flight together -- one launch instead of three.
+constexpr int kSingleBlock = 1024;
+constexpr int kSingleItems = 16;
+constexpr int64_t kSingleMax = static_cast<int64_t>(kSingleBlock) * kSingleItems;
 
-__global__ void __launch_bounds__(kScanBlock) scan_single_kernel(const int32_t* __restrict__ in,
-                                                                int32_t* __restrict__ out, int64_t n,
-                                                                int64_t* __restrict__ total_dev) {
-  int64_t carry = 0;
-  for (int64_t tile = 0; tile * kScanTile < n; ++tile) {
-    const int64_t base = tile * kScanTile + static_cast<int64_t>(threadIdx.x) * kScanItems;
-    int32_t v[kScanItems];
-    int64_t sum = 0;
+__global__ void __launch_bounds__(kSingleBlock) scan_single_kernel(const int32_t* __restrict__ in,
+                                                                  int32_t* __restrict__ out, int64_t n,
+                                                                  int64_t* __restrict__ total_dev) {
+  __shared__ int64_t s_wave[kSingleBlock / kWave];
+  const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  const int64_t base = static_cast<int64_t>(t) * kSingleItems;
+  int32_t v[kSingleItems];
+  int64_t sum = 0;
 #pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
-      v[k] = base + k < n ? in[base + k] : 0;
-      sum += v[k];
-    }
-    int64_t total;
-    int64_t run = carry + block_exclusive_scan(sum, &total);  // syncs: every read precedes every write
-#pragma unroll
-    for (int k = 0; k < kScanItems; ++k) {
-      if (base + k < n) out[base + k] = static_cast<int32_t>(run);
-      run += v[k];
-    }
-    carry += total;
+  for (int k = 0; k < kSingleItems; ++k) {
+    v[k] = base + k < n ? in[base + k] : 0;
+    sum += v[k];
   }
-  if (threadIdx.x == 0 && total_dev) *total_dev = carry;
+  const int64_t inc = wave_inclusive_scan_i64(sum);
+  if (lane == kWave - 1) s_wave[wave] = inc;
+  __syncthreads();  // every read of in precedes every write of out (they may alias)
+  int64_t run = inc - sum, tot = 0;
+#pragma unroll
+  for (int w = 0; w < kSingleBlock / kWave; ++w) {
+    const int64_t x = s_wave[w];
+    run += w < wave ? x : 0;
+    tot += x;
+  }
+#pragma unroll
+  for (int k = 0; k < kSingleItems; ++k) {
+    if (base + k < n) out[base + k] = static_cast<int32_t>(run);
+    run += v[k];
+  }
+  if (t == 0 && total_dev) *total_dev = tot;
 }
 
 }  // namespace
@@ -91,10 +99,10 @@ int scan_exclusive_i32(const int32_t* in, int32_t* out, int64_t n, int64_t* tota
   }
   const int64_t nb = scan_num_blocks(n);
   if (nb > kMaxGridX) return invalid("scan: too many elements.");
-  if (nb <= kSingleTiles) {
+  if (n <= kSingleMax) {
     {
       KernelTimer timer("scan_local", stream);
-      scan_single_kernel<<<1, kScanBlock, 0, stream>>>(in, out, n, total_dev);
+      scan_single_kernel<<<1, kSingleBlock, 0, stream>>>(in, out, n, total_dev);
     }
     return check_launch("scan (single block)");
   }

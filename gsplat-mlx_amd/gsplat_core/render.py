@@ -133,8 +133,10 @@ def _render_sh_packed(means, quats, log_scales, features_dc, features_rest, opac
     if accutile:
         inputs["conics"] = pr["conics"].detach()
         inputs["opacities"] = opac.detach()
-    isect = _C.intersect_tile_forward(inputs, C, tile_size, tw, th, True, False)
-    offsets = _C.intersect_offset_forward(isect["isect_ids"], C, tw, th)
+    # sorted lists and tile offsets in one call (the tile-bucket path writes
+    # the offsets itself)
+    isect = _C.intersect_tile_offsets_forward(inputs, C, tile_size, tw, th)
+    offsets = isect["tile_offsets"]
     bg = background_tensor(background, means.device)
     bg = bg if C == 1 else bg.expand(C, -1)
     render = rasterize_to_pixels_3dgs(m2, pr["conics"], colors, opac, offsets, isect["flatten_ids"], width, height,

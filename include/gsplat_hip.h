@@ -407,6 +407,32 @@ int gsplat_hip_isect_bucket_sort_accutile(const float* means2d, const int32_t* r
                                           int32_t* flatten_ids, int32_t* tile_offsets, const void* count_workspace,
                                           size_t count_workspace_bytes, void* workspace, size_t workspace_bytes,
                                           void* stream);
+/* The same two steps for the packed layout (nnz rows, row r of image
+ * image_ids[r]; the reference rejects packed at gsplat_intersect.cpp:115-118,
+ * upstream gsplat's packed isect_tiles takes it): AABB tiles, or ellipse
+ * tiles when conics and opacities are given. Flatten ids are row indices.
+ * The rows must be grouped by image in ascending order, as the packed
+ * projection writes them: totals_dev then holds three words, M, the longest
+ * list and 0; a nonzero third word means the rows are not so grouped (or an
+ * id lies outside [0, I)), and the first two words and the count workspace
+ * are then not valid (use the depth-presorted packed entry points). Count
+ * workspace: gsplat_hip_isect_bucket_count_packed_workspace_size(I, nnz, ...);
+ * supported grids as the dense entry points (accutile_supported for ellipse
+ * tiles). */
+size_t gsplat_hip_isect_bucket_count_packed_workspace_size(int64_t I, int64_t nnz, int32_t tile_size,
+                                                           int32_t tile_width, int32_t tile_height);
+int gsplat_hip_isect_bucket_count_packed(const float* means2d, const int32_t* radii, const float* conics,
+                                         const float* opacities, const int32_t* image_ids, int64_t I, int64_t nnz,
+                                         int32_t tile_size, int32_t tile_width, int32_t tile_height,
+                                         int32_t* tiles_per_gauss, int64_t* totals_dev, void* workspace,
+                                         size_t workspace_bytes, void* stream);
+int gsplat_hip_isect_bucket_sort_packed(const float* means2d, const int32_t* radii, const float* conics,
+                                        const float* opacities, const float* depths, const int32_t* image_ids,
+                                        int64_t I, int64_t nnz, int32_t tile_size, int32_t tile_width,
+                                        int32_t tile_height, int64_t n_isects, int64_t max_list,
+                                        int64_t* isect_ids, int32_t* flatten_ids, int32_t* tile_offsets,
+                                        const void* count_workspace, size_t count_workspace_bytes,
+                                        void* workspace, size_t workspace_bytes, void* stream);
 
 /* Ellipse ("AccuTile") tile intersection: the use_conics / use_opacities
  * path of IntersectTileParams (gsplat_core/include/gsplat_intersect.h),

@@ -192,10 +192,10 @@ def test_c_abi_tile_sorted_one_call(oracle):
     np.testing.assert_array_equal(host(flat), exp["flatten_ids"])
 
 
-@pytest.mark.parametrize("n", [1, 1023, 4097, 65536, 65537, 1 << 20])
+@pytest.mark.parametrize("n", [1, 1023, 4097, 16383, 16384, 16385, 65536, 65537, 1 << 20])
 def test_c_abi_exclusive_scan(n):
     """gsplat_hip_exclusive_scan_i32 against numpy, in place, on both sides of
-    the single-block / three-kernel switch (64 tiles of 1024 values)."""
+    the single-block / three-kernel switch (16384 values)."""
     import torch
 
     lib = ctypes.CDLL(LIB)

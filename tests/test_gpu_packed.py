@@ -92,13 +92,25 @@ def test_projection_packed_equals_dense(oracle, B, C, N, opac, comp):
         np.testing.assert_array_equal(host(bp[k]), host(bd[k]), err_msg=k)
 
 
+def _packed_image_ids(rng, layout, I, nnz):
+    """Row image ids: grouped by image (the packed projection's order), grouped
+    with empty images (first, inner and last), or not grouped (the sorted
+    intersection then takes the depth-presorted path after the read-back)."""
+    if layout == "grouped":
+        return np.sort(rng.integers(0, I, nnz)).astype(np.int32)
+    if layout == "gaps":
+        return np.sort(rng.choice(np.array([1, 3], np.int32), nnz)).astype(np.int32)
+    return rng.integers(0, I, nnz).astype(np.int32)
+
+
+@pytest.mark.parametrize("layout", ["grouped", "gaps", "shuffled"])
 @pytest.mark.parametrize("accutile", [False, True])
 @pytest.mark.parametrize("sort", [False, True])
-def test_isect_packed_vs_oracle(oracle, accutile, sort):
+def test_isect_packed_vs_oracle(oracle, accutile, sort, layout):
     rng = np.random.default_rng(17)
-    I, nnz, W, H = 4, 30000, 640, 480
+    I, nnz, W, H = 5 if layout == "gaps" else 4, 30000, 640, 480
     means, radii, conics, opac, depths = (a[0] for a in projected_scene(rng, 1, nnz, W, H))
-    img = np.sort(rng.integers(0, I, nnz)).astype(np.int32)
+    img = _packed_image_ids(rng, layout, I, nnz)
     tw, th = (W + TS - 1) // TS, (H + TS - 1) // TS
     g = gsplat()
     inp = {"means2d": dev(means), "radii": dev(radii), "depths": dev(depths), "image_ids": dev(img)}
@@ -106,7 +118,7 @@ def test_isect_packed_vs_oracle(oracle, accutile, sort):
     if accutile:
         inp["conics"], inp["opacities"] = dev(conics), dev(opac)
         kw = {"conics": conics, "opacities": opac}
-    print(f"packed isect accutile={accutile} sort={sort}", flush=True)
+    print(f"packed isect accutile={accutile} sort={sort} layout={layout}", flush=True)
     out = g.intersect_tile_forward(inp, I, TS, tw, th, sort=sort)
     ref = oracle.isect_tile_packed(means, radii, depths, img, I, TS, tw, th, sort=sort, **kw)
     np.testing.assert_array_equal(host(out["tiles_per_gauss"]), ref["tiles_per_gauss"])
@@ -116,6 +128,38 @@ def test_isect_packed_vs_oracle(oracle, accutile, sort):
     inp["image_ids"] = dev(img.astype(np.int64))
     out2 = g.intersect_tile_forward(inp, I, TS, tw, th, sort=sort)
     np.testing.assert_array_equal(host(out2["isect_ids"]), ref["isect_ids"])
+    if sort:  # the lists with their tile offsets, in one call and split around the read-back
+        offs = oracle.isect_offset(ref["isect_ids"], I, tw, th)
+        from gsplat_core import _gsplat_core as _C
+
+        for o in (_C.intersect_tile_offsets_forward(inp, I, TS, tw, th),
+                  _C.intersect_tile_offsets_end(_C.intersect_tile_offsets_begin(inp, I, TS, tw, th))):
+            np.testing.assert_array_equal(host(o["isect_ids"]), ref["isect_ids"])
+            np.testing.assert_array_equal(host(o["flatten_ids"]), ref["flatten_ids"])
+            np.testing.assert_array_equal(host(o["tiles_per_gauss"]), ref["tiles_per_gauss"])
+            np.testing.assert_array_equal(host(o["tile_offsets"]), offs)
+
+
+@pytest.mark.parametrize("nnz", [1, 2047])
+def test_isect_packed_small(oracle, nnz):
+    """Packed sorted intersections of 1 and 2047 rows over three images (the
+    tile-bucket path with images that hold no segment, and one segment; the
+    binding takes inputs without rows as the dense layout)."""
+    rng = np.random.default_rng(nnz + 3)
+    I, W, H = 3, 200, 150
+    tw, th = (W + TS - 1) // TS, (H + TS - 1) // TS
+    means, radii, conics, opac, depths = (a[0] for a in projected_scene(rng, 1, max(nnz, 1), W, H))
+    means, radii, depths = means[:nnz], radii[:nnz], depths[:nnz]
+    img = np.sort(rng.integers(0, I, nnz)).astype(np.int32)
+    from gsplat_core import _gsplat_core as _C
+
+    inp = {"means2d": dev(means), "radii": dev(radii), "depths": dev(depths), "image_ids": dev(img)}
+    print(f"packed isect small nnz={nnz}", flush=True)
+    o = _C.intersect_tile_offsets_forward(inp, I, TS, tw, th)
+    ref = oracle.isect_tile_packed(means, radii, depths, img, I, TS, tw, th, sort=True)
+    np.testing.assert_array_equal(host(o["isect_ids"]), ref["isect_ids"])
+    np.testing.assert_array_equal(host(o["flatten_ids"]), ref["flatten_ids"])
+    np.testing.assert_array_equal(host(o["tile_offsets"]), oracle.isect_offset(ref["isect_ids"], I, tw, th))
 
 
 def _chain(g, torch, means, quats, scales, op, colors, view, Ks, W, H, packed, cot):
