@@ -52,8 +52,11 @@ __global__ void __launch_bounds__(kScanBlock) scan_fixup_kernel(int32_t* __restr
 }
 
 // Small inputs (up to kSingleBlock * kSingleItems values): one block of
-// 1024 threads, each scanning kSingleItems consecutive values with every load
-// in flight together -- one launch instead of three.
+// 1024 threads -- one launch instead of three. The values pass through LDS so
+// that global loads and stores are coalesced (wave w moves 64 consecutive
+// values per instruction) while each thread scans kSingleItems consecutive
+// values; a thread-strided global layout would turn every store into 64
+// partial-line writes from one CU.
 constexpr int kSingleBlock = 1024;
 constexpr int kSingleItems = 16;
 constexpr int64_t kSingleMax = static_cast<int64_t>(kSingleBlock) * kSingleItems;
@@ -61,19 +64,26 @@ constexpr int64_t kSingleMax = static_cast<int64_t>(kSingleBlock) * kSingleItems
 __global__ void __launch_bounds__(kSingleBlock) scan_single_kernel(const int32_t* __restrict__ in,
                                                                   int32_t* __restrict__ out, int64_t n,
                                                                   int64_t* __restrict__ total_dev) {
+  __shared__ int32_t s_v[kSingleMax];
   __shared__ int64_t s_wave[kSingleBlock / kWave];
   const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
-  const int64_t base = static_cast<int64_t>(t) * kSingleItems;
+  const int cnt = static_cast<int>(n);  // n <= kSingleMax
+#pragma unroll
+  for (int k = 0; k < kSingleItems; ++k) {
+    const int i = k * kSingleBlock + t;
+    s_v[i] = i < cnt ? in[i] : 0;
+  }
+  __syncthreads();  // every read of in precedes every write of out (they may alias)
   int32_t v[kSingleItems];
   int64_t sum = 0;
 #pragma unroll
   for (int k = 0; k < kSingleItems; ++k) {
-    v[k] = base + k < n ? in[base + k] : 0;
+    v[k] = s_v[t * kSingleItems + k];
     sum += v[k];
   }
   const int64_t inc = wave_inclusive_scan_i64(sum);
   if (lane == kWave - 1) s_wave[wave] = inc;
-  __syncthreads();  // every read of in precedes every write of out (they may alias)
+  __syncthreads();
   int64_t run = inc - sum, tot = 0;
 #pragma unroll
   for (int w = 0; w < kSingleBlock / kWave; ++w) {
@@ -83,8 +93,14 @@ __global__ void __launch_bounds__(kSingleBlock) scan_single_kernel(const int32_t
   }
 #pragma unroll
   for (int k = 0; k < kSingleItems; ++k) {
-    if (base + k < n) out[base + k] = static_cast<int32_t>(run);
+    s_v[t * kSingleItems + k] = static_cast<int32_t>(run);
     run += v[k];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < kSingleItems; ++k) {
+    const int i = k * kSingleBlock + t;
+    if (i < cnt) out[i] = s_v[i];
   }
   if (t == 0 && total_dev) *total_dev = tot;
 }

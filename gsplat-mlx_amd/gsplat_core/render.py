@@ -125,17 +125,26 @@ def _render_sh_packed(means, quats, log_scales, features_dc, features_rest, opac
         m2 = packed_viewspace(m2, viewspace_points, cid, gid)
     # index_select: its backward is an index_add (no sort of the indices)
     gidl = gid.long()
-    opac = o.reshape(-1).index_select(0, gidl)
-    colors = colors_all.reshape(C * N, -1).index_select(0, cid.long() * N + gidl)
+
+    def gather_opacities():
+        return o.reshape(-1).index_select(0, gidl)
+
     tw, th = tile_grid(width, height, tile_size)
     inputs = {"means2d": m2.detach(), "radii": pr["radii"], "depths": pr["depths"].detach(), "image_ids": cid,
               "gaussian_ids": gid}
+    opac = None
     if accutile:
+        opac = gather_opacities()
         inputs["conics"] = pr["conics"].detach()
         inputs["opacities"] = opac.detach()
-    # sorted lists and tile offsets in one call (the tile-bucket path writes
-    # the offsets itself)
-    isect = _C.intersect_tile_offsets_forward(inputs, C, tile_size, tw, th)
+    # sorted lists and tile offsets (the tile-bucket path writes the offsets
+    # itself) in two calls around the count read-back: the per-row gathers
+    # are queued in between, so their host work overlaps the count kernels
+    pending = _C.intersect_tile_offsets_begin(inputs, C, tile_size, tw, th)
+    if opac is None:
+        opac = gather_opacities()
+    colors = colors_all.reshape(C * N, -1).index_select(0, cid.long() * N + gidl)
+    isect = _C.intersect_tile_offsets_end(pending)
     offsets = isect["tile_offsets"]
     bg = background_tensor(background, means.device)
     bg = bg if C == 1 else bg.expand(C, -1)
