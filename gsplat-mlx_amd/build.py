@@ -35,7 +35,7 @@ HIP_SOURCES = ["common", "quat_scale_to_covar", "projection", "projection_bwd", 
                "intersect", "bucket", "radix_sort", "rasterize", "training_glue", "image_loss"]
 GRADIENT_ONLY = {"projection_bwd"}
 CORE_SOURCES = ["gsplat_quat_scale_to_covar", "gsplat_projection", "gsplat_spherical_harmonics",
-                "gsplat_intersect", "gsplat_rasterize", "gsplat_training_glue"]
+                "gsplat_intersect", "gsplat_rasterize", "gsplat_training_glue", "gsplat_render"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-ffp-contract=off",

@@ -471,6 +471,64 @@ at::Tensor image_loss_backward(const at::Tensor& image, const at::Tensor& target
   return gsplat_core::gsplat_image_loss_backward(image, target, maps, window_size, g_l1, g_ssim);
 }
 
+// The RGB render step in one call per direction (gsplat_render.h; no
+// counterpart in the reference binding): inputs means, quats, log_scales,
+// opacity_logits, colors, viewmats, Ks and optional backgrounds; the forward
+// returns the images, the intersections and what the backward reads back.
+gsplat_core::RenderRGBInput render_rgb_input(const TensorMap& inputs, int image_width, int image_height,
+                                             int tile_size, float eps2d, float near_plane, float far_plane,
+                                             bool opacities_in_projection, bool accutile) {
+  gsplat_core::RenderRGBInput in;
+  in.means = require_key(inputs, "means");
+  in.quats = require_key(inputs, "quats");
+  in.log_scales = require_key(inputs, "log_scales");
+  in.opacity_logits = require_key(inputs, "opacity_logits");
+  in.colors = require_key(inputs, "colors");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.backgrounds = get_or_empty(inputs, "backgrounds");
+  in.image_width = image_width;
+  in.image_height = image_height;
+  in.tile_size = tile_size;
+  in.eps2d = eps2d;
+  in.near_plane = near_plane;
+  in.far_plane = far_plane;
+  in.opacities_in_projection = opacities_in_projection;
+  in.accutile = accutile;
+  return in;
+}
+
+const char* const kRenderRGBKeys[] = {"render_colors", "render_alphas", "last_ids", "radii", "means2d", "conics",
+                                      "opacities", "tiles_per_gauss", "isect_ids", "flatten_ids", "tile_offsets"};
+
+py::dict render_rgb_forward(const TensorMap& inputs, int image_width, int image_height, int tile_size, float eps2d,
+                            float near_plane, float far_plane, bool opacities_in_projection, bool accutile) {
+  auto out = gsplat_core::gsplat_render_rgb_forward(render_rgb_input(
+      inputs, image_width, image_height, tile_size, eps2d, near_plane, far_plane, opacities_in_projection, accutile));
+  py::dict r;
+  for (size_t i = 0; i < out.size(); ++i) r[kRenderRGBKeys[i]] = out[i];
+  return r;
+}
+
+py::dict render_rgb_backward(const TensorMap& inputs, const TensorMap& forward_outputs, const TensorMap& cotangents,
+                             int image_width, int image_height, int tile_size, float eps2d, bool accutile,
+                             bool viewmats_requires_grad) {
+  const auto in = render_rgb_input(inputs, image_width, image_height, tile_size, eps2d, 0.01f, 1e10f, false, accutile);
+  std::vector<at::Tensor> fwd;
+  for (const char* k : kRenderRGBKeys) fwd.push_back(require_key(forward_outputs, k));
+  auto out = gsplat_core::gsplat_render_rgb_backward(in, fwd, require_key(cotangents, "v_render_colors"),
+                                                     get_or_empty(cotangents, "v_render_alphas"),
+                                                     viewmats_requires_grad);
+  py::dict r;
+  r["v_means"] = out[0];
+  r["v_quats"] = out[1];
+  r["v_log_scales"] = out[2];
+  r["v_opacity_logits"] = out[3];
+  r["v_colors"] = out[4];
+  if (viewmats_requires_grad) r["v_viewmats"] = out[5];
+  return r;
+}
+
 // Template smoke entries of the reference (gsplat_core/dummy.cpp:7-13).
 int dummy_add(int a, int b) { return a + b; }
 
@@ -543,6 +601,12 @@ PYBIND11_MODULE(_gsplat_core, m) {
   m.def("activated_projection_backward", &activated_projection_backward, py::arg("inputs"),
         py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
         py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
+  m.def("render_rgb_forward", &render_rgb_forward, py::arg("inputs"), py::arg("image_width"),
+        py::arg("image_height"), py::arg("tile_size"), py::arg("eps2d") = 0.3f, py::arg("near_plane") = 0.01f,
+        py::arg("far_plane") = 1.0e10f, py::arg("opacities_in_projection") = false, py::arg("accutile") = false);
+  m.def("render_rgb_backward", &render_rgb_backward, py::arg("inputs"), py::arg("forward_outputs"),
+        py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"), py::arg("tile_size"),
+        py::arg("eps2d") = 0.3f, py::arg("accutile") = false, py::arg("viewmats_requires_grad") = false);
   m.def("l1_loss_forward", &l1_loss_forward, py::arg("image"), py::arg("target"));
   m.def("l1_loss_backward", &l1_loss_backward, py::arg("image"), py::arg("target"), py::arg("grad"));
   m.def("image_loss_forward", &image_loss_forward, py::arg("image"), py::arg("target"), py::arg("window_size") = 11,

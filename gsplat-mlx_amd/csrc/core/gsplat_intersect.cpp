@@ -390,6 +390,81 @@ BucketState intersect_bucketed_count(const IntersectTileInput& input, void* stre
 
 std::vector<array> intersect_presorted(const IntersectTileInput& input, void* stream);
 
+// Speculative scatter + tile sort: with the count kernels queued, the second
+// step is launched at once into outputs sized by the M of the previous call
+// on the same inputs' shape (plus an eighth), reading the new M on the
+// device; the host then waits for M while the GPU sorts. The result is kept
+// when M fits and the tile sort classes launched cover the longest list
+// (otherwise the exact step runs after the read-back). Hints are per host
+// thread and shape key.
+struct SpecHint {
+  int64_t capacity = 0, longest = 0;
+};
+
+SpecHint& spec_hint(const IntersectTileInput& input, int64_t numel) {
+  thread_local std::map<std::vector<int64_t>, SpecHint> hints;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const auto& p = input.params;
+  return hints[{dev, p.I, p.tile_size, p.tile_width, p.tile_height, accutile(input), p.packed, numel}];
+}
+
+struct Speculation {
+  bool active = false;
+  int64_t capacity = 0, max_list = 0;
+  array ids, flat, offsets, ws2;
+};
+
+// Frames whose long lists take the depth-presorted path (see
+// intersect_bucketed_finish) are not speculated.
+bool presorted_policy(int64_t longest, int64_t total) {
+  return longest > gsplat_hip_isect_bucket_max_list() && total >= kPresortAboveIsects;
+}
+
+Speculation speculate(const IntersectTileInput& input, const BucketState& b, bool with_offsets) {
+  Speculation sp;
+  const auto& p = input.params;
+  const SpecHint& h = spec_hint(input, b.depths.numel());
+  if (h.capacity <= 0 || presorted_policy(h.longest, h.capacity)) return sp;
+  sp.active = true;
+  sp.capacity = h.capacity;
+  sp.max_list = h.longest;
+  sp.ids = at::empty({sp.capacity}, i64_like(b.means2d));
+  sp.flat = at::empty({sp.capacity}, i32_like(b.means2d));
+  if (with_offsets) sp.offsets = at::empty({p.I, p.tile_height, p.tile_width}, i32_like(b.means2d));
+  const size_t ws2_bytes = gsplat_hip_isect_bucket_sort_workspace_size(sp.capacity);
+  sp.ws2 = workspace(ws2_bytes, b.means2d);
+  check(gsplat_hip_isect_bucket_sort_speculative(
+      b.means2d.data_ptr<float>(), b.radii.data_ptr<int32_t>(), b.ell ? b.conics.data_ptr<float>() : nullptr,
+      b.ell ? b.opacities.data_ptr<float>() : nullptr, b.depths.data_ptr<float>(), b.packed ? 1 : 0,
+      b.packed ? b.image_ids.data_ptr<int32_t>() : nullptr, p.I, b.depths.numel(), p.tile_size, p.tile_width,
+      p.tile_height, sp.capacity, sp.max_list, b.totals.data_ptr<int64_t>(), sp.ids.data_ptr<int64_t>(),
+      sp.flat.data_ptr<int32_t>(), with_offsets ? sp.offsets.data_ptr<int32_t>() : nullptr,
+      b.ws1.data_ptr<uint8_t>(), b.ws1_bytes, sp.ws2.data_ptr<uint8_t>(), ws2_bytes, b.stream));
+  return sp;
+}
+
+// After the read-back: the speculative result when it holds, else the exact
+// step; the hint follows this call's M and longest list.
+std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, const BucketState& b, int total,
+                                             int64_t longest, bool ungrouped, array* tile_offsets);
+
+std::vector<array> intersect_bucketed_settle(const IntersectTileInput& input, const BucketState& b,
+                                             const Speculation& sp, int total, int64_t longest, bool ungrouped,
+                                             array* tile_offsets) {
+  if (!ungrouped) {
+    SpecHint& h = spec_hint(input, b.depths.numel());
+    h.capacity = total + std::max<int64_t>(total / 8, 4096);
+    h.longest = longest;
+  }
+  if (sp.active && !ungrouped && total <= sp.capacity && gsplat_hip_isect_bucket_sort_covers(sp.max_list, longest) &&
+      !presorted_policy(longest, total)) {
+    if (tile_offsets) *tile_offsets = sp.offsets;
+    return {b.tiles_per_gauss, sp.ids.narrow(0, 0, total), sp.flat.narrow(0, 0, total)};
+  }
+  return intersect_bucketed_finish(input, b, total, longest, ungrouped, tile_offsets);
+}
+
 std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, const BucketState& b, int total,
                                              int64_t longest, bool ungrouped, array* tile_offsets) {
   const auto& p = input.params;
@@ -474,8 +549,9 @@ std::vector<array> intersect_bucketed(const IntersectTileInput& input, void* str
   const BucketState b = intersect_bucketed_count(input, stream);
   CountReadback& r = readback_slot();
   start_read_total(b.totals, stream, r, b.readback_words());
+  const Speculation sp = speculate(input, b, tile_offsets != nullptr);
   const int total = finish_read_total(r);
-  return intersect_bucketed_finish(input, b, total, r.host[1], b.packed && r.host[2] != 0, tile_offsets);
+  return intersect_bucketed_settle(input, b, sp, total, r.host[1], b.packed && r.host[2] != 0, tile_offsets);
 }
 
 // Read-back slots of split intersections, one per pending call: pinned words
@@ -616,6 +692,7 @@ struct PendingIntersect {
   bool bucketed = false, finished = false;
   int dev = 0;
   BucketState state;
+  Speculation spec;
   CountReadback rb;
   std::vector<array> result;
   ~PendingIntersect() {
@@ -649,6 +726,7 @@ std::shared_ptr<PendingIntersect> gsplat_intersect_tile_offsets_begin(const Inte
   pending->rb = acquire_readback(pending->dev);
   pending->bucketed = true;
   start_read_total(pending->state.totals, stream, pending->rb, pending->state.readback_words());
+  pending->spec = speculate(input, pending->state, true);
   return pending;
 }
 
@@ -662,10 +740,12 @@ std::vector<array> gsplat_intersect_tile_offsets_end(const std::shared_ptr<Pendi
   pending->finished = true;
   release_readback(pending->dev, pending->rb);
   array offsets;
-  auto out = intersect_bucketed_finish(pending->input, pending->state, total, longest, ungrouped, &offsets);
+  auto out = intersect_bucketed_settle(pending->input, pending->state, pending->spec, total, longest, ungrouped,
+                                       &offsets);
   out.push_back(offsets);
   pending->result = out;
   pending->state = BucketState();  // the count workspace goes back to the allocator
+  pending->spec = Speculation();
   return out;
 }
 

@@ -5,5 +5,6 @@
 #include "gsplat_projection.h"
 #include "gsplat_quat_scale_to_covar.h"
 #include "gsplat_rasterize.h"
+#include "gsplat_render.h"
 #include "gsplat_spherical_harmonics.h"
 #include "gsplat_training_glue.h"

@@ -982,11 +982,13 @@ struct TileSortLds {
 template <int B, int ITEMS>
 __global__ void __launch_bounds__(B) bucket_tile_sort_kernel(const uint2* __restrict__ pairs,
                                                              const int32_t* __restrict__ tile_start, int64_t n_lists,
-                                                             int64_t n_isects, int64_t n_tiles, int tile_bits,
+                                                             int64_t n_isects, const int64_t* __restrict__ m_dev,
+                                                             int64_t n_tiles, int tile_bits,
                                                              int64_t* __restrict__ isect_ids,
                                                              int32_t* __restrict__ flatten_ids,
                                                              int32_t* __restrict__ tile_offsets) {
   __shared__ TileSortLds<B, ITEMS> sh;
+  if (m_dev) n_isects = min(n_isects, *m_dev);
   const int64_t list = blockIdx.x;
   if (tile_offsets && threadIdx.x == 0) tile_offsets[list] = tile_start[list];
   sort_tile_list<B, ITEMS>(list, pairs, tile_start, n_lists, n_isects, n_tiles, tile_bits, isect_ids, flatten_ids,
@@ -998,13 +1000,15 @@ __global__ void __launch_bounds__(B) bucket_tile_sort_kernel(const uint2* __rest
 template <int B, int ITEMS>
 __global__ void __launch_bounds__(B) bucket_tile_sort_class_kernel(const uint2* __restrict__ pairs,
                                                                    const int32_t* __restrict__ tile_start,
-                                                                   int64_t n_lists, int64_t n_isects, int64_t n_tiles,
+                                                                   int64_t n_lists, int64_t n_isects,
+                                                                   const int64_t* __restrict__ m_dev, int64_t n_tiles,
                                                                    int tile_bits, int64_t* __restrict__ isect_ids,
                                                                    int32_t* __restrict__ flatten_ids,
                                                                    const int32_t* __restrict__ class_list,
                                                                    const int32_t* __restrict__ class_count) {
   __shared__ TileSortLds<B, ITEMS> sh;
   if (static_cast<int>(blockIdx.x) >= *class_count) return;
+  if (m_dev) n_isects = min(n_isects, *m_dev);
   sort_tile_list<B, ITEMS>(class_list[blockIdx.x], pairs, tile_start, n_lists, n_isects, n_tiles, tile_bits,
                            isect_ids, flatten_ids, sh.kv, sh.wcnt, sh.dstart, sh.bits);
 }
@@ -1177,6 +1181,7 @@ __device__ void huge_radix(uint2* a, uint2* b, int n, uint32_t kvary, uint32_t i
 __global__ void __launch_bounds__(kHugeBlock) bucket_huge_sort_kernel(uint2* __restrict__ pairs,
                                                                       const int32_t* __restrict__ tile_start,
                                                                       int64_t n_lists, int64_t n_isects,
+                                                                      const int64_t* __restrict__ m_dev,
                                                                       int64_t n_tiles, int tile_bits,
                                                                       int64_t* __restrict__ isect_ids,
                                                                       int32_t* __restrict__ flatten_ids,
@@ -1188,6 +1193,7 @@ __global__ void __launch_bounds__(kHugeBlock) bucket_huge_sort_kernel(uint2* __r
   __shared__ uint32_t s_hist[256], s_cur[256], s_bits[3];
   __shared__ int32_t s_run[257];
   __shared__ int s_nrun;
+  if (m_dev) n_isects = min(n_isects, *m_dev);
   const int t = threadIdx.x;
   const int cnt = class_counts[3];
   for (int li = blockIdx.x; li < cnt; li += gridDim.x) {
@@ -1266,6 +1272,7 @@ __global__ void __launch_bounds__(kHugeBlock) bucket_huge_sort_kernel(uint2* __r
 __global__ void __launch_bounds__(kHugeBlock) bucket_huge_radix_kernel(uint2* __restrict__ pairs,
                                                                        const int32_t* __restrict__ tile_start,
                                                                        int64_t n_lists, int64_t n_isects,
+                                                                       const int64_t* __restrict__ m_dev,
                                                                        int64_t n_tiles, int tile_bits,
                                                                        int64_t* __restrict__ isect_ids,
                                                                        int32_t* __restrict__ flatten_ids,
@@ -1273,6 +1280,7 @@ __global__ void __launch_bounds__(kHugeBlock) bucket_huge_radix_kernel(uint2* __
                                                                        const int32_t* __restrict__ class_counts) {
   __shared__ HugeRadixLds sh;
   __shared__ uint32_t s_bits[4];
+  if (m_dev) n_isects = min(n_isects, *m_dev);
   const int t = threadIdx.x;
   const int cnt = class_counts[4];
   for (int li = blockIdx.x; li < cnt; li += gridDim.x) {
@@ -1409,11 +1417,14 @@ int bucket_count(bool ell, const float* means2d, const int32_t* radii, const flo
 }
 
 // Scatter + tile sort (steps 4-5); ell, packed and image_ids as bucket_count's.
+// m_dev (nullable): the device word of the count step's M; n_isects is then
+// the outputs' capacity (launched before M is on the host), and every write
+// stays below it.
 int bucket_sort(bool ell, const float* means2d, const int32_t* radii, const float* conics, const float* opacities,
                 const float* depths, bool packed, const int32_t* image_ids, int64_t I, int64_t numel, int32_t tile_size,
                 int32_t tile_width, int32_t tile_height, int64_t n_isects, int64_t max_list, int64_t* isect_ids,
                 int32_t* flatten_ids, int32_t* tile_offsets, const void* count_workspace, size_t count_workspace_bytes,
-                void* workspace, size_t workspace_bytes, void* stream) {
+                void* workspace, size_t workspace_bytes, void* stream, const int64_t* m_dev = nullptr) {
   const char* what = "intersect_tile";
   BucketDims d;
   int rc = bucket_dims(what, I, numel, tile_size, tile_width, tile_height, ell, &d, packed);
@@ -1457,8 +1468,8 @@ int bucket_sort(bool ell, const float* means2d, const int32_t* radii, const floa
     const unsigned grid = static_cast<unsigned>(n_lists);
     // every list up to kSortCap[0] (and every tile offset) in one launch;
     // longer lists by their class, one launch per class present
-    bucket_tile_sort_kernel<256, 10><<<grid, 256, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, d.n_tiles,
-                                                           tile_bits, isect_ids, flatten_ids, tile_offsets);
+    bucket_tile_sort_kernel<256, 10><<<grid, 256, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, m_dev,
+                                                           d.n_tiles, tile_bits, isect_ids, flatten_ids, tile_offsets);
     // a block per list of the class at most: every list of class k holds
     // more than kSortCap[k - 1] entries, so at most n_isects / (kSortCap[k - 1]
     // + 1) of them exist; blocks past the class's size exit at once
@@ -1466,23 +1477,23 @@ int bucket_sort(bool ell, const float* means2d, const int32_t* radii, const floa
       return static_cast<unsigned>(std::min<int64_t>(n_lists, n_isects / (kSortCap[k - 1] + 1)));
     };
     if (max_list > kSortCap[0])
-      bucket_tile_sort_class_kernel<512, 8><<<cgrid(1), 512, 0, s>>>(pairs, l.tile_start, n_lists, n_isects,
+      bucket_tile_sort_class_kernel<512, 8><<<cgrid(1), 512, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, m_dev,
                                                                       d.n_tiles, tile_bits, isect_ids, flatten_ids,
                                                                       l.class_lists, l.class_counts);
     if (max_list > kSortCap[1])
       bucket_tile_sort_class_kernel<512, 16><<<cgrid(2), 512, 0, s>>>(
-          pairs, l.tile_start, n_lists, n_isects, d.n_tiles, tile_bits, isect_ids, flatten_ids,
+          pairs, l.tile_start, n_lists, n_isects, m_dev, d.n_tiles, tile_bits, isect_ids, flatten_ids,
           l.class_lists + n_lists, l.class_counts + 1);
     if (max_list > kSortCap[2])
       bucket_tile_sort_class_kernel<1024, 16><<<cgrid(3), 1024, 0, s>>>(
-          pairs, l.tile_start, n_lists, n_isects, d.n_tiles, tile_bits, isect_ids, flatten_ids,
+          pairs, l.tile_start, n_lists, n_isects, m_dev, d.n_tiles, tile_bits, isect_ids, flatten_ids,
           l.class_lists + 2 * n_lists, l.class_counts + 2);
     if (max_list > kSortCap[3]) {  // lists longer than LDS holds: a block each, taking the lists in turn
       const unsigned hg = std::min(static_cast<unsigned>(n_isects / (kSortCap[3] + 1)), 2048u);
-      bucket_huge_sort_kernel<<<hg, kHugeBlock, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, d.n_tiles,
+      bucket_huge_sort_kernel<<<hg, kHugeBlock, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, m_dev, d.n_tiles,
                                                          tile_bits, isect_ids, flatten_ids,
                                                          l.class_lists + 3 * n_lists, l.class_counts);
-      bucket_huge_radix_kernel<<<hg, kHugeBlock, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, d.n_tiles,
+      bucket_huge_radix_kernel<<<hg, kHugeBlock, 0, s>>>(pairs, l.tile_start, n_lists, n_isects, m_dev, d.n_tiles,
                                                           tile_bits, isect_ids, flatten_ids,
                                                           l.class_lists + 3 * n_lists, l.class_counts);
     }
@@ -1584,4 +1595,28 @@ extern "C" int gsplat_hip_isect_bucket_sort_packed(const float* means2d, const i
                                                    void* workspace, size_t workspace_bytes, void* stream) {
   return bucket_sort(conics != nullptr, means2d, radii, conics, opacities, depths, true, image_ids, I, nnz, tile_size, tile_width, tile_height, n_isects, max_list, isect_ids, flatten_ids, tile_offsets,
                      count_workspace, count_workspace_bytes, workspace, workspace_bytes, stream);
+}
+
+// 0, 1, 2, 3 or 4: the tile sort classes beyond the short-list sort that a
+// bucket sort launched with this longest list runs.
+int class_launches(int64_t max_list) {
+  int k = 0;
+  while (k < kSortClasses && max_list > kSortCap[k]) ++k;
+  return k;
+}
+
+extern "C" int gsplat_hip_isect_bucket_sort_covers(int64_t max_list_launched, int64_t longest) {
+  return class_launches(longest) <= class_launches(max_list_launched);
+}
+
+extern "C" int gsplat_hip_isect_bucket_sort_speculative(
+    const float* means2d, const int32_t* radii, const float* conics, const float* opacities, const float* depths,
+    int32_t packed, const int32_t* image_ids, int64_t I, int64_t numel, int32_t tile_size, int32_t tile_width,
+    int32_t tile_height, int64_t capacity, int64_t max_list, const int64_t* totals_dev, int64_t* isect_ids,
+    int32_t* flatten_ids, int32_t* tile_offsets, const void* count_workspace, size_t count_workspace_bytes,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  if (!totals_dev || capacity <= 0) return invalid("intersect_tile: invalid speculative sort arguments.");
+  return bucket_sort(conics != nullptr, means2d, radii, conics, opacities, depths, packed != 0, image_ids, I, numel,
+                     tile_size, tile_width, tile_height, capacity, max_list, isect_ids, flatten_ids, tile_offsets,
+                     count_workspace, count_workspace_bytes, workspace, workspace_bytes, stream, totals_dev);
 }

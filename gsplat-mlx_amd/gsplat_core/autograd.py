@@ -429,6 +429,66 @@ def activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks,
             "viewspace_points": viewspace_points, "opacities": opac}
 
 
+_RENDER_RGB_SAVED = ("render_colors", "render_alphas", "last_ids", "radii", "means2d", "conics", "opacities",
+                     "tiles_per_gauss", "isect_ids", "flatten_ids", "tile_offsets")
+
+
+class _RenderRGB(torch.autograd.Function):
+    """The RGB render step (activated projection, sorted tile intersection,
+    rasterization) as one C++ call per direction: the same operators as the
+    composed path, without the interpreter between them."""
+
+    @staticmethod
+    def forward(ctx, means, quats, log_scales, colors, opacity_logits, viewmats, Ks, backgrounds, image_width,
+                image_height, tile_size, far_plane, opacities_in_projection, accutile):
+        ctx.set_materialize_grads(False)
+        inputs = {"means": means, "quats": quats, "log_scales": log_scales, "opacity_logits": opacity_logits,
+                  "colors": colors, "viewmats": viewmats, "Ks": Ks}
+        if _nonempty(backgrounds):
+            inputs["backgrounds"] = backgrounds
+        out = _C.render_rgb_forward(inputs, image_width, image_height, tile_size, 0.3, 0.01, far_plane,
+                                    opacities_in_projection, accutile)
+        ctx.save_for_backward(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, backgrounds,
+                              *(out[k] for k in _RENDER_RGB_SAVED))
+        ctx.dims = (image_width, image_height, tile_size, accutile)
+        nd = [out[k] for k in ("last_ids", "radii", "tiles_per_gauss", "isect_ids", "flatten_ids", "tile_offsets")]
+        ctx.mark_non_differentiable(*nd)
+        return (out["render_colors"], out["render_alphas"], out["last_ids"], out["radii"], out["tiles_per_gauss"],
+                out["flatten_ids"], out["isect_ids"], out["tile_offsets"])
+
+    @staticmethod
+    def backward(ctx, v_render_colors, v_render_alphas, *_):
+        saved = ctx.saved_tensors
+        means, quats, log_scales, colors, logits, viewmats, Ks, backgrounds = saved[:8]
+        fwd = dict(zip(_RENDER_RGB_SAVED, saved[8:]))
+        W, H, ts, accutile = ctx.dims
+        inputs = {"means": means, "quats": quats, "log_scales": log_scales, "opacity_logits": logits,
+                  "colors": colors, "viewmats": viewmats, "Ks": Ks}
+        if _nonempty(backgrounds):
+            inputs["backgrounds"] = backgrounds
+        if v_render_colors is None:
+            v_render_colors = torch.zeros_like(fwd["render_colors"])
+        cot = {"v_render_colors": v_render_colors.contiguous()}
+        if v_render_alphas is not None:  # absent = zeros
+            cot["v_render_alphas"] = v_render_alphas.contiguous()
+        needs_viewmats = ctx.needs_input_grad[5]
+        out = _C.render_rgb_backward(inputs, fwd, cot, W, H, ts, 0.3, accutile, needs_viewmats)
+        return (out["v_means"], out["v_quats"], out["v_log_scales"], out["v_colors"], out["v_opacity_logits"],
+                out["v_viewmats"] if needs_viewmats else None) + (None,) * 8
+
+
+def render_rgb(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, backgrounds, image_width,
+               image_height, tile_size, far_plane=1e10, opacities_in_projection=False, accutile=False):
+    """Differentiable RGB render step in one C++ call per direction."""
+    e = _empty(means)
+    rc, ra, li, radii, tpg, flat, ids, offs = _RenderRGB.apply(
+        means, quats, log_scales, colors, opacity_logits, viewmats, Ks,
+        backgrounds if backgrounds is not None else e, image_width, image_height, tile_size, far_plane,
+        opacities_in_projection, accutile)
+    return {"render_colors": rc, "render_alphas": ra, "last_ids": li, "radii": radii, "tiles_per_gauss": tpg,
+            "flatten_ids": flat, "isect_ids": ids, "tile_offsets": offs}
+
+
 class _L1Loss(torch.autograd.Function):
     @staticmethod
     def forward(ctx, image, target):

@@ -27,8 +27,8 @@ import torch
 
 from . import _gsplat_core as _C
 from .autograd import (activated_projection, gaussian_activations, image_loss, l1_loss as _l1_loss, packed_viewspace,
-                       projection_ewa_3dgs_fused, projection_packed, rasterize_to_pixels_3dgs, sh_camera_colors,
-                       spherical_harmonics)
+                       projection_ewa_3dgs_fused, projection_packed, rasterize_to_pixels_3dgs, render_rgb,
+                       sh_camera_colors, spherical_harmonics)
 
 
 def normalize_quats(quats: torch.Tensor) -> torch.Tensor:
@@ -185,10 +185,19 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
 
 
 def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, width, height, tile_size,
-                     background=(0.0, 0.0, 0.0), opacities_in_projection=False, far_plane=1e10, accutile=False):
+                     background=(0.0, 0.0, 0.0), opacities_in_projection=False, far_plane=1e10, accutile=False,
+                     fused=True):
     """RGB colours per Gaussian; C cameras (viewmats [1, C, 4, 4]) as C images.
-    accutile: ellipse tile lists (same images, fewer intersections)."""
+    accutile: ellipse tile lists (same images, fewer intersections). fused:
+    the whole step as one C++ call per direction (the same operators; fused
+    False composes them here, one autograd node each)."""
     C = viewmats.shape[1]
+    if fused:
+        bg = background_tensor(background, means.device)
+        bg = bg if C == 1 else bg.expand(C, -1)
+        return render_rgb(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, bg, width, height,
+                          tile_size, far_plane=far_plane, opacities_in_projection=opacities_in_projection,
+                          accutile=accutile)
     proj = activated_projection(means, quats, log_scales, opacity_logits, viewmats, Ks, width, height, eps2d=0.3,
                                 near_plane=0.01, far_plane=far_plane,
                                 opacities_in_projection=opacities_in_projection)

@@ -434,6 +434,25 @@ int gsplat_hip_isect_bucket_sort_packed(const float* means2d, const int32_t* rad
                                         const void* count_workspace, size_t count_workspace_bytes,
                                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* Speculative second step (no counterpart in the reference; for callers
+ * that know a likely M, e.g. from the previous frame): the bucket sort of
+ * any of the layouts above (ellipse tiles when conics is not NULL, packed
+ * rows when packed != 0) launched before M is on the host. The kernels read
+ * M from totals_dev[0] (the count step's output); capacity bounds every
+ * write (isect_ids and flatten_ids hold capacity entries, the workspace
+ * gsplat_hip_isect_bucket_sort_workspace_size(capacity) bytes) and max_list
+ * selects the tile sort launches. The result equals the exact call's when
+ * M <= capacity and gsplat_hip_isect_bucket_sort_covers(max_list, longest)
+ * for the longest list read back with M; otherwise it must be discarded and
+ * the exact step run. */
+int gsplat_hip_isect_bucket_sort_covers(int64_t max_list_launched, int64_t longest);
+int gsplat_hip_isect_bucket_sort_speculative(
+    const float* means2d, const int32_t* radii, const float* conics, const float* opacities, const float* depths,
+    int32_t packed, const int32_t* image_ids, int64_t I, int64_t numel, int32_t tile_size, int32_t tile_width,
+    int32_t tile_height, int64_t capacity, int64_t max_list, const int64_t* totals_dev, int64_t* isect_ids,
+    int32_t* flatten_ids, int32_t* tile_offsets, const void* count_workspace, size_t count_workspace_bytes,
+    void* workspace, size_t workspace_bytes, void* stream);
+
 /* Ellipse ("AccuTile") tile intersection: the use_conics / use_opacities
  * path of IntersectTileParams (gsplat_core/include/gsplat_intersect.h),
  * which the reference rejects at gsplat_intersect.cpp:123-126 and leaves to
