@@ -398,7 +398,8 @@ std::vector<array> intersect_presorted(const IntersectTileInput& input, void* st
 // (otherwise the exact step runs after the read-back). Hints are per host
 // thread and shape key.
 struct SpecHint {
-  int64_t capacity = 0, longest = 0;
+  int64_t capacity = 0, longest = 0, total = 0;
+  int presorted_calls = 0;  // consecutive calls sent straight to the presorted path
 };
 
 SpecHint& spec_hint(const IntersectTileInput& input, int64_t numel) {
@@ -444,6 +445,20 @@ Speculation speculate(const IntersectTileInput& input, const BucketState& b, boo
   return sp;
 }
 
+// Shapes whose last bucket count chose the presorted path go there directly
+// (the bucket count would be thrown away); every 32nd such call takes the
+// bucket path again, so a frame that no longer needs the presorted path
+// returns to the tile buckets.
+bool presorted_by_hint(const IntersectTileInput& input) {
+  SpecHint& h = spec_hint(input, input.depths.numel());
+  if (h.capacity <= 0 || !presorted_policy(h.longest, h.total)) return false;
+  if (++h.presorted_calls >= 32) {
+    h.presorted_calls = 0;
+    return false;
+  }
+  return true;
+}
+
 // After the read-back: the speculative result when it holds, else the exact
 // step; the hint follows this call's M and longest list.
 std::vector<array> intersect_bucketed_finish(const IntersectTileInput& input, const BucketState& b, int total,
@@ -456,6 +471,8 @@ std::vector<array> intersect_bucketed_settle(const IntersectTileInput& input, co
     SpecHint& h = spec_hint(input, b.depths.numel());
     h.capacity = total + std::max<int64_t>(total / 8, 4096);
     h.longest = longest;
+    h.total = total;
+    h.presorted_calls = 0;
   }
   if (sp.active && !ungrouped && total <= sp.capacity && gsplat_hip_isect_bucket_sort_covers(sp.max_list, longest) &&
       !presorted_policy(longest, total)) {
@@ -599,7 +616,7 @@ std::vector<array> gsplat_intersect_tile_gpu_staged(const IntersectTileInput& in
     throw std::runtime_error("intersect_tile_encode image id and tile id require more than 32 bits.");
   const c10::DeviceGuard guard(input.means2d.device());
   void* stream = stream_for(input.s, input.means2d);
-  if (use_bucketed(input)) return intersect_bucketed(input, stream);
+  if (use_bucketed(input) && !presorted_by_hint(input)) return intersect_bucketed(input, stream);
   return intersect_presorted(input, stream);
 }
 
@@ -667,11 +684,24 @@ std::vector<array> gsplat_intersect_tile(const IntersectTileInput& input) {
   return gsplat_intersect_tile_gpu_staged(input);
 }
 
+// The sorted lists and their offsets by the depth-presorted path.
+std::vector<array> gsplat_intersect_tile_with_offsets_unbucketed(const IntersectTileInput& input) {
+  const auto& p = input.params;
+  check_dense_size(input, "intersect_tile");
+  const int64_t n_tiles = static_cast<int64_t>(p.tile_width) * p.tile_height;
+  if (floor_log2_plus_one(p.I) + floor_log2_plus_one(n_tiles) > 32)
+    throw std::runtime_error("intersect_tile_encode image id and tile id require more than 32 bits.");
+  const c10::DeviceGuard guard(input.means2d.device());
+  auto out = intersect_presorted(input, stream_for(input.s, input.means2d));
+  out.push_back(gsplat_intersect_offset(out[kIsectIds], p.I, p.tile_width, p.tile_height, input.s));
+  return out;
+}
+
 std::vector<array> gsplat_intersect_tile_with_offsets(const IntersectTileInput& input) {
   validate_intersect_tile_input(input);
   if (!input.params.sort) throw std::runtime_error("intersect_tile_with_offsets needs sort = true.");
   const auto& p = input.params;
-  if (use_bucketed(input)) {
+  if (use_bucketed(input) && !presorted_by_hint(input)) {
     check_dense_size(input, "intersect_tile");
     const int64_t n_tiles = static_cast<int64_t>(p.tile_width) * p.tile_height;
     if (floor_log2_plus_one(p.I) + floor_log2_plus_one(n_tiles) > 32)
@@ -682,9 +712,7 @@ std::vector<array> gsplat_intersect_tile_with_offsets(const IntersectTileInput& 
     out.push_back(offsets);
     return out;
   }
-  auto out = gsplat_intersect_tile(input);
-  out.push_back(gsplat_intersect_offset(out[kIsectIds], p.I, p.tile_width, p.tile_height, input.s));
-  return out;
+  return gsplat_intersect_tile_with_offsets_unbucketed(input);
 }
 
 struct PendingIntersect {
@@ -710,8 +738,8 @@ std::shared_ptr<PendingIntersect> gsplat_intersect_tile_offsets_begin(const Inte
   const auto& p = input.params;
   auto pending = std::make_shared<PendingIntersect>();
   pending->input = input;
-  if (!use_bucketed(input)) {
-    pending->result = gsplat_intersect_tile_with_offsets(input);
+  if (!use_bucketed(input) || presorted_by_hint(input)) {
+    pending->result = gsplat_intersect_tile_with_offsets_unbucketed(input);
     pending->finished = true;
     return pending;
   }

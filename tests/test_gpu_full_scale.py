@@ -137,7 +137,21 @@ def _run(name, oracle, n_sub=3000, n_heavy=3, n_random=3):
     counts = torch.bincount(flat.long(), minlength=C * N)
     assert torch.equal(counts.to(torch.int32), tpg)
     del counts
+    # the same frame again, with the offsets: the second call of a shape
+    # speculates the scatter and tile sort from the first's M (or, for a
+    # frame whose long lists chose the depth-presorted path, goes there
+    # without the bucket count); the lists must not change
+    from gsplat_core import _gsplat_core as _C
+
+    again = _C.intersect_tile_offsets_forward({"means2d": proj["means2d"], "radii": proj["radii"],
+                                               "depths": proj["depths"]}, C, ts, tw, th)
+    assert torch.equal(again["isect_ids"], keys) and torch.equal(again["flatten_ids"], flat)
+    assert torch.equal(again["tiles_per_gauss"].reshape(-1), tpg)
+    offs_again = again["tile_offsets"]
+    del again
     offs_t = g.intersect_offset_forward(keys, C, tw, th)  # [C, th, tw]
+    assert torch.equal(offs_again, offs_t)
+    del offs_again
     tile_bits = int(np.floor(np.log2(tw * th))) + 1
     img = torch.arange(C, device="cuda", dtype=torch.int64)[:, None]
     tl = torch.arange(tw * th, device="cuda", dtype=torch.int64)[None, :]
