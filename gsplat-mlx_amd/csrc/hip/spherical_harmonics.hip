@@ -629,29 +629,14 @@ __device__ __forceinline__ void slab_rows(const float* __restrict__ means, const
   m[2] = s_m[t * 3 + 2];
 }
 
-// The forward stages per wave: wave w copies the rows of its own 64
-// Gaussians into its part of the slab and reads them back a row per lane,
-// with no block barrier, so a block's waves load and compute independently
-// (one wave's loads are in flight while another computes).
-template <int W>
-__device__ __forceinline__ void stage_rows_wave(float* __restrict__ dst, const float* __restrict__ src, int rows) {
-  const int lane = threadIdx.x % kWave;
-  if (rows == kWave && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
-    static_assert((kWave * W) % 4 == 0, "whole float4s per wave's rows");
-    constexpr int T4 = kWave * W / 4;
-    constexpr int PER = (T4 + kWave - 1) / kWave;
-    const float4* s4 = reinterpret_cast<const float4*>(src);
-    float4* d4 = reinterpret_cast<float4*>(dst);
-#pragma clang loop unroll(full)
-    for (int i = 0; i < PER; ++i) {
-      const int idx = lane + i * kWave;
-      if (idx < T4) d4[idx] = s4[idx];
-    }
-  } else {
-    for (int idx = lane; idx < rows * W; idx += kWave) dst[idx] = src[idx];
-  }
-}
-
+// The forward is a resident grid: each wave walks groups of 64 Gaussians
+// (group g, g + stride, ...) and keeps the next group's rest rows in flight
+// in registers (16-byte loads of the group's contiguous span) while it
+// computes the current one, so the memory system always holds every wave's
+// next loads; the LDS of a wave holds one group (the transposition to a row
+// per lane), and no block barrier is taken (the waves are independent).
+// Groups that are partial or whose span is not 16-byte aligned read their
+// rows per lane instead.
 template <int DEG>
 __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* __restrict__ means,
                                                                   const float* __restrict__ viewmats,
@@ -660,44 +645,116 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
                                                                   int64_t N, float* __restrict__ colors) {
   constexpr int A = (DEG + 1) * (DEG + 1);
   constexpr int R3 = (A - 1) * 3;
+  constexpr int T4 = R3 > 0 ? kWave * R3 / 4 : 1;  // float4s of a group's rest span
+  constexpr int PER = (T4 + kWave - 1) / kWave;
+  static_assert((kWave * R3) % 4 == 0, "whole float4s per group");
   __shared__ __align__(16) float s_rest[R3 > 0 ? kShSlab * R3 : 4];
-  __shared__ __align__(16) float s_dc[kShSlab * 3];
-  __shared__ __align__(16) float s_m[kShSlab * 3];
   const int64_t b = blockIdx.y;
-  const int t = threadIdx.x;
-  const int wave = t / kWave;
-  const int64_t w0 = static_cast<int64_t>(blockIdx.x) * kShSlab + wave * kWave;  // the wave's first Gaussian
-  const int rows = static_cast<int>(min<int64_t>(kWave, N - w0));
-  if (rows <= 0) return;  // wave-uniform; no block barrier follows
-  const int64_t row0 = b * N + w0;
-  if constexpr (R3 > 0) stage_rows_wave<R3>(s_rest + wave * kWave * R3, rest + row0 * R3, rows);
-  stage_rows_wave<3>(s_dc + wave * kWave * 3, dc + row0 * 3, rows);
-  stage_rows_wave<3>(s_m + wave * kWave * 3, means + row0 * 3, rows);
-  // the wave's LDS writes before its reads of other lanes' rows
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  if (t % kWave >= rows) return;
-  float co[A * 3], m[3];
-  co[0] = s_dc[t * 3];
-  co[1] = s_dc[t * 3 + 1];
-  co[2] = s_dc[t * 3 + 2];
+  const int lane = threadIdx.x % kWave;
+  const int wave = threadIdx.x / kWave;
+  const int64_t n_groups = (N + kWave - 1) / kWave;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * (kShSlab / kWave);
+  float* sw = s_rest + wave * kWave * R3;
+  auto span = [&](int64_t grp) { return rest + (b * N + grp * kWave) * R3; };
+  auto vec_ok = [&](int64_t grp) {
+    return R3 > 0 && N - grp * kWave >= kWave && (reinterpret_cast<uintptr_t>(span(grp)) & 15) == 0;
+  };
+  // the group's rest span (clamped: every lane loads PER float4s of it)
+  auto fetch = [&](int64_t grp, int i) {
+    return reinterpret_cast<const float4*>(span(grp))[min(lane + i * kWave, T4 - 1)];
+  };
+  // dc and mean of this lane's Gaussian of the group (12 bytes each)
+  auto fetch_row = [&](int64_t grp, float (&p)[6]) {
+    const int64_t g = b * N + grp * kWave + lane;
+    const bool active = grp * kWave + lane < N;
 #pragma clang loop unroll(full)
-  for (int i = 0; i < R3; ++i) co[3 + i] = s_rest[t * R3 + i];
-  m[0] = s_m[t * 3];
-  m[1] = s_m[t * 3 + 1];
-  m[2] = s_m[t * 3 + 2];
-  for (int64_t c = 0; c < C; ++c) {
-    float cp[3];
-    camera_centre(viewmats + (b * C + c) * 16, cp);
-    float d[3], n[3], raw[3];
-    view_dir(m, cp, d, n);
-    sh_eval<DEG>(n, co, raw);
-    float* out = colors + ((b * C + c) * N + w0 + t % kWave) * 3;
-    out[0] = clamp01(raw[0] + 0.5f);
-    out[1] = clamp01(raw[1] + 0.5f);
-    out[2] = clamp01(raw[2] + 0.5f);
+    for (int k = 0; k < 3; ++k) {
+      p[k] = active ? dc[g * 3 + k] : 0.0f;
+      p[3 + k] = active ? means[g * 3 + k] : 0.0f;
+    }
+  };
+  float4 r[PER];
+  float p[6];
+  int64_t grp = static_cast<int64_t>(blockIdx.x) * (kShSlab / kWave) + wave;
+  if (grp < n_groups) {
+    fetch_row(grp, p);
+    if (vec_ok(grp)) {
+#pragma clang loop unroll(full)
+      for (int i = 0; i < PER; ++i) r[i] = fetch(grp, i);
+    }
   }
+  for (; grp < n_groups; grp += stride) {
+    const int64_t w0 = grp * kWave;
+    const int rows = static_cast<int>(min<int64_t>(kWave, N - w0));
+    const bool active = lane < rows;
+    float co[A * 3], m[3];
+#pragma clang loop unroll(full)
+    for (int k = 0; k < 3; ++k) {
+      co[k] = p[k];
+      m[k] = p[3 + k];
+    }
+    if constexpr (R3 > 0) {
+      if (vec_ok(grp)) {  // wave-uniform
+        float4* d4 = reinterpret_cast<float4*>(sw);
+#pragma clang loop unroll(full)
+        for (int i = 0; i < PER; ++i)
+          if (lane + i * kWave < T4) d4[lane + i * kWave] = r[i];
+        // the wave's LDS writes before its reads of other lanes' rows
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma clang loop unroll(full)
+        for (int i = 0; i < R3; ++i) co[3 + i] = sw[lane * R3 + i];
+        // the reads before the next group's writes
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      } else {
+        const float* src = span(grp);
+#pragma clang loop unroll(full)
+        for (int i = 0; i < R3; ++i) co[3 + i] = active ? src[lane * R3 + i] : 0.0f;
+      }
+    }
+    if (grp + stride < n_groups) {  // the next group's loads, in flight during the compute
+      fetch_row(grp + stride, p);
+      if (vec_ok(grp + stride)) {
+#pragma clang loop unroll(full)
+        for (int i = 0; i < PER; ++i) r[i] = fetch(grp + stride, i);
+      }
+    }
+    if (active) {
+      for (int64_t c = 0; c < C; ++c) {
+        float cp[3];
+        camera_centre(viewmats + (b * C + c) * 16, cp);
+        float d[3], n[3], raw[3];
+        view_dir(m, cp, d, n);
+        sh_eval<DEG>(n, co, raw);
+        float* out = colors + ((b * C + c) * N + w0 + lane) * 3;
+        out[0] = clamp01(raw[0] + 0.5f);
+        out[1] = clamp01(raw[1] + 0.5f);
+        out[2] = clamp01(raw[2] + 0.5f);
+      }
+    }
+  }
+}
+
+// Workgroups of `kernel` resident on the current device at once (the
+// occupancy calculator's blocks per CU x CUs), computed once per device;
+// 0 when the runtime cannot tell.
+template <typename Kernel>
+int resident_blocks(Kernel kernel, int block) {
+  constexpr int kMaxDevices = 64;
+  static int cached[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  if (cached[dev] == 0) {
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      return 0;
+    cached[dev] = std::max(1, per_cu * cus);
+  }
+  return cached[dev];
 }
 
 template <int DEG>
@@ -784,7 +841,11 @@ int launch_cam_fwd(const float* means, const float* viewmats, const float* dc, c
     bool slab = false;
     if constexpr (slab_degree(DEG)) {
       if (R == (DEG + 1) * (DEG + 1) - 1) {
-        const dim3 grid(grid_for(N, kShSlab), static_cast<unsigned>(B));
+        // a resident grid (each wave walks several groups), at most one wave per group
+        const int64_t blocks = grid_for(grid_for(N, kWave), kShSlab / kWave);
+        const int res = resident_blocks(sh_cam_fwd_slab_kernel<DEG>, kShSlab);
+        const int64_t per_batch = res > 0 ? std::max<int64_t>(1, res / B) : blocks;
+        const dim3 grid(static_cast<unsigned>(std::min<int64_t>(blocks, per_batch)), static_cast<unsigned>(B));
         sh_cam_fwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, C, N, colors);
         slab = true;
       }
