@@ -460,6 +460,18 @@ std::atomic<int64_t> g_carry_min_pairs{kCarryBitsMinPairs};
 
 inline bool carry_depth_bits(int64_t numel) { return numel > g_carry_min_pairs.load(std::memory_order_relaxed); }
 
+// Whether the carrying sorts generate their first pass's keys instead of
+// encoding them (radix_sort_tiles_generated; test hook
+// gsplat_hip_isect_debug_generated). It needs room for two 16-byte records
+// per Gaussian in the encode's key and value buffers, so at least four
+// entries per Gaussian.
+std::atomic<int32_t> g_generated{1};
+
+inline bool generate_keys(int64_t numel, int64_t n_isects, int tw, int th, int bit_hi) {
+  return g_generated.load(std::memory_order_relaxed) != 0 && 4 * numel <= n_isects &&
+         tiles_generated_supported(n_isects, tw, th, bit_hi);
+}
+
 int check_tile_bits(int64_t I, int32_t tile_width, int32_t tile_height, int* tile_bits, int* image_bits) {
   const int64_t n_tiles = static_cast<int64_t>(tile_width) * tile_height;
   *tile_bits = floor_log2_plus_one(n_tiles);
@@ -780,6 +792,12 @@ extern "C" int gsplat_hip_isect_encode_sorted(const float* means2d, const int32_
   }
   hipStream_t s = as_stream(stream);
   const bool carry = carry_depth_bits(numel);
+  if (carry && generate_keys(numel, n_isects, tile_width, tile_height, image_bits + tile_bits))
+    return radix_sort_tiles_generated(means2d, radii, depths, perm, offsets, numel, numel / I, tile_size, tile_width,
+                                      tile_height, tile_bits, n_isects, image_bits + tile_bits,
+                                      reinterpret_cast<uint4*>(l.tkeys), reinterpret_cast<int32_t*>(l.tbits),
+                                      l.tkeys_sorted, flatten_ids, isect_ids, l.tbits, l.tbits_alt, l.sort_ws,
+                                      l.sort_ws_bytes, s, what);
   {
     KernelTimer timer("isect_encode", s);
     const int64_t nb = (numel + n_isects + kMergeItems - 1) / kMergeItems;
@@ -994,4 +1012,11 @@ extern "C" void gsplat_hip_isect_debug_set(int64_t carry_min_pairs, int64_t spli
   g_split_min_blocks.store(split_min_blocks < 0 ? kSplitMinBlocks : split_min_blocks, std::memory_order_relaxed);
 }
 
-extern "C" void gsplat_hip_isect_debug_reset(void) { gsplat_hip_isect_debug_set(-1, -1); }
+extern "C" void gsplat_hip_isect_debug_generated(int32_t enable) {
+  g_generated.store(enable != 0 ? 1 : 0, std::memory_order_relaxed);
+}
+
+extern "C" void gsplat_hip_isect_debug_reset(void) {
+  gsplat_hip_isect_debug_set(-1, -1);
+  gsplat_hip_isect_debug_generated(1);
+}

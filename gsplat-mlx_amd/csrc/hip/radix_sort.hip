@@ -42,6 +42,7 @@
 
 #include "radix_sort.hpp"
 #include "scan.hpp"
+#include "tiles.hpp"
 
 namespace gsplat_hip {
 
@@ -317,6 +318,75 @@ __global__ void sort_plan_kernel(const K* __restrict__ keys, int64_t n, int bit_
 // pair plus the values; GATHER adds gather[value] at the same position. With
 // V2 a second 32-bit value rides along (v2 in, out.v2 out); ASM then takes
 // the depth bits from it instead of gathering depths[value].
+// Generated first pass (radix_sort_tiles_generated): the keys of the
+// depth-presorted tile lists are formed inside the first onesweep pass
+// instead of being written by an encode kernel and read back. Partition p
+// holds entries [4096 p, 4096 p + 4096) of the lists in depth order; entry j
+// belongs to the last depth rank r with offsets[r] <= j, whose Gaussian
+// g = perm[r] covers the tiles of its rect row by row: local index
+// k = j - offsets[r] is tile (min_y + k / w, min_x + k % w). The entry's key
+// is image << tile_bits | tile id, its value g and its carried bits the
+// depth bits of g.
+struct TileGenArgs {
+  const int32_t* offsets;    // [numel] first entry of each rank
+  const uint4* ranked;       // [numel] per rank: min_x | min_y << 16, width | height << 16 (the rect of its
+                             // Gaussian in tile units), depth bits, Gaussian
+  const int32_t* part_rank;  // [n_parts + 1] rank holding each partition's first entry, then numel - 1
+  int64_t numel;
+  int64_t n_per_image;
+  int32_t tw, tile_bits;
+};
+
+// Ranks staged in LDS per chunk of a generated partition of `items` keys
+// per thread (six words each: first entry, Gaussian, min corner, width,
+// depth bits, image bits, in the space the partition's reorder uses
+// afterwards).
+constexpr int gen_ranks(int items) { return (3 * kSortBlock * items - 1) / 6; }
+// Keys per thread of a generated pass: 3072 per partition, whose 42 KB of
+// LDS let three blocks share a CU (two at 4096); measured faster at
+// heavy_6m's sizes (2.60 against 2.90 ms) although its runs per digit are
+// shorter.
+constexpr int kGenItems = 12;
+constexpr int kGenTile = kSortBlock * kGenItems;
+
+// Adds the low-digit counts of the contiguous keys [a, a + len) to a
+// difference array over the 256 digits (diff[d] - diff[d - 1] adds to digit
+// d) plus a count added to every digit (all).
+__device__ __forceinline__ void add_low_digits(uint32_t* diff, uint32_t& all, uint32_t a, uint32_t len) {
+  all += len >> 8;
+  const uint32_t rem = len & 255u;
+  if (rem == 0u) return;
+  const uint32_t s = a & 255u, e = s + rem;
+  atomicAdd(&diff[s], 1u);
+  if (e < 256u) {
+    atomicAdd(&diff[e], ~0u);
+  } else if (e > 256u) {
+    atomicAdd(&diff[0], 1u);
+    atomicAdd(&diff[e - 256u], ~0u);
+  }
+}
+
+// floor(k / w), k - w floor(k / w) for 0 <= k, 1 <= w: the float quotient is
+// within one of the exact one while k < 2^24, then corrected.
+__device__ __forceinline__ void div_rect(int32_t k, int32_t w, int32_t* q, int32_t* r) {
+  if (k < (1 << 24)) {
+    int32_t qq = static_cast<int32_t>(floorf(static_cast<float>(k) * __builtin_amdgcn_rcpf(static_cast<float>(w))));
+    int32_t rr = k - qq * w;
+    if (rr < 0) {
+      --qq;
+      rr += w;
+    } else if (rr >= w) {
+      ++qq;
+      rr -= w;
+    }
+    *q = qq;
+    *r = rr;
+  } else {
+    *q = k / w;
+    *r = k - *q * w;
+  }
+}
+
 template <typename K>
 struct OsOut {
   K* keys;
@@ -334,16 +404,26 @@ struct OsOut {
   int32_t* vals_alt;
 };
 
-template <typename K, bool ASM, bool GATHER, bool V2>
+// GEN: the partition's keys, values and carried bits are generated from
+// `gen` (TileGenArgs; 32-bit keys with carried bits, first pass only)
+// instead of read from keys_in / vals_in / v2_in.
+template <typename K, bool ASM, bool GATHER, bool V2, bool GEN = false, int ITEMS = kOsItems>
 __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restrict__ keys_in,
                                                               const int32_t* __restrict__ vals_in,
                                                               const uint32_t* __restrict__ v2_in, int64_t n,
                                                               int shift, const uint32_t* __restrict__ hist,
                                                               uint32_t* __restrict__ lookback, int spin_limit,
-                                                              OsOut<K> out, uint32_t dxor) {
-  __shared__ K s_keys[kOsTile];
-  __shared__ int32_t s_vals[kOsTile];
-  __shared__ uint32_t s_v2[V2 ? kOsTile : 1];
+                                                              OsOut<K> out, uint32_t dxor, TileGenArgs gen = {}) {
+  static_assert(!GEN || (sizeof(K) == 4 && V2 && !GATHER), "generated passes carry bits beside 32-bit keys");
+  constexpr int kTileT = kSortBlock * ITEMS;  // keys per partition
+  constexpr int kWaveKeysT = kWave * ITEMS;   // keys ranked by one wave
+  constexpr int kPoolWords = (static_cast<int>(sizeof(K)) / 4 + 1 + (V2 ? 1 : 0)) * kTileT;
+  constexpr int kGenRanksT = gen_ranks(ITEMS);
+  static_assert(!GEN || kPoolWords >= 6 * kGenRanksT + 1, "generated ranks fit the reorder space");
+  __shared__ __align__(16) uint32_t s_pool[kPoolWords];  // the reorder: keys, values, carried bits
+  K* s_keys = reinterpret_cast<K*>(s_pool);
+  int32_t* s_vals = reinterpret_cast<int32_t*>(s_pool + kTileT * sizeof(K) / 4);
+  uint32_t* s_v2 = s_pool + kTileT * (sizeof(K) / 4 + 1);
   __shared__ uint32_t s_wcnt[kWaves][kRadix];  // per-wave running counts, then per-wave bases
   __shared__ uint32_t s_tile_start[kRadix];
   __shared__ uint32_t s_gbase[kRadix];
@@ -353,8 +433,8 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
   const int lane = t % kWave;
   const int wave = t / kWave;
   const int64_t part = blockIdx.x;
-  const int64_t base = part * kOsTile;
-  const int cnt = static_cast<int>(min<int64_t>(kOsTile, n - base));
+  const int64_t base = part * kTileT;
+  const int cnt = static_cast<int>(min<int64_t>(kTileT, n - base));
   const K* kin = keys_in;
   const int32_t* vin = vals_in;
   K* kout = out.keys;
@@ -371,21 +451,83 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
 
   // load: wave w owns tile keys [w * 1024, (w + 1) * 1024), round r covers
   // w * 1024 + r * 64 + lane, so (wave, round, lane) is input order
-  K k[kOsItems];
-  int32_t v[kOsItems];
-  uint32_t w2[V2 ? kOsItems : 1];
-  uint32_t rank[kOsItems];
+  K k[ITEMS];
+  int32_t v[ITEMS];
+  uint32_t w2[V2 ? ITEMS : 1];
+  uint32_t rank[ITEMS];
+  if constexpr (GEN) {
 #pragma unroll
-  for (int r = 0; r < kOsItems; ++r) {
-    const int idx = wave * kOsWaveKeys + r * kWave + lane;
-    if (idx < cnt) {
-      k[r] = kin[base + idx];
-      v[r] = vin[base + idx];
-      if constexpr (V2) w2[r] = v2_in[base + idx];
-    } else {
+    for (int r = 0; r < ITEMS; ++r) {
       k[r] = 0;
       v[r] = 0;
-      if constexpr (V2) w2[r] = 0;
+      w2[r] = 0;
+    }
+    // the partition's ranks [r0, r1], staged kGenRanksT at a time
+    int32_t* g_off = reinterpret_cast<int32_t*>(s_pool);  // [kGenRanksT + 1]
+    int32_t* g_g = g_off + kGenRanksT + 1;
+    uint32_t* g_xy = reinterpret_cast<uint32_t*>(g_g + kGenRanksT);
+    int32_t* g_w = reinterpret_cast<int32_t*>(g_xy + kGenRanksT);
+    uint32_t* g_d = reinterpret_cast<uint32_t*>(g_w + kGenRanksT);
+    uint32_t* g_hi = g_d + kGenRanksT;
+    const int64_t r0 = gen.part_rank[part], r1 = gen.part_rank[part + 1];
+    for (int64_t c0 = r0; c0 <= r1; c0 += kGenRanksT) {
+      const int nc = static_cast<int>(min<int64_t>(kGenRanksT, r1 + 1 - c0));
+      __syncthreads();  // the previous chunk's reads are done
+      for (int i = t; i < nc; i += kSortBlock) {
+        const uint4 rec = gen.ranked[c0 + i];
+        g_off[i] = gen.offsets[c0 + i];
+        g_g[i] = static_cast<int32_t>(rec.w);
+        g_xy[i] = rec.x;
+        g_w[i] = static_cast<int32_t>(max(rec.y & 0xffffu, 1u));
+        g_d[i] = rec.z;
+        g_hi[i] = static_cast<uint32_t>(static_cast<int64_t>(rec.w) / gen.n_per_image) << gen.tile_bits;
+      }
+      if (t == 0) g_off[nc] = c0 + nc < gen.numel ? gen.offsets[c0 + nc] : INT32_MAX;
+      __syncthreads();
+      const int32_t lo = g_off[0], hi = g_off[nc];
+      // each item's rank, the last staged one whose first entry is <= j, by
+      // binary lifting: the same uniform steps for all items, so the sixteen
+      // items' LDS reads of a step are in flight together
+      int at[ITEMS];
+#pragma unroll
+      for (int r = 0; r < ITEMS; ++r) at[r] = 0;
+      for (int step = nc > 1 ? 1 << (31 - __builtin_clz(nc - 1)) : 0; step > 0; step >>= 1) {
+#pragma unroll
+        for (int r = 0; r < ITEMS; ++r) {
+          const int32_t j = static_cast<int32_t>(base + wave * kWaveKeysT + r * kWave + lane);
+          const int c = at[r] + step;
+          if (c < nc && g_off[c] <= j) at[r] = c;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < ITEMS; ++r) {
+        const int idx = wave * kWaveKeysT + r * kWave + lane;
+        const int32_t j = static_cast<int32_t>(base + idx);
+        if (idx < cnt && j >= lo && j < hi) {
+          const int a = at[r];
+          int32_t row, col;
+          div_rect(j - g_off[a], g_w[a], &row, &col);
+          const uint32_t xy = g_xy[a];
+          k[r] = g_hi[a] | static_cast<uint32_t>((static_cast<int32_t>(xy >> 16) + row) * gen.tw +
+                                                 static_cast<int32_t>(xy & 0xffffu) + col);
+          v[r] = g_g[a];
+          w2[r] = g_d[a];
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int r = 0; r < ITEMS; ++r) {
+      const int idx = wave * kWaveKeysT + r * kWave + lane;
+      if (idx < cnt) {
+        k[r] = kin[base + idx];
+        v[r] = vin[base + idx];
+        if constexpr (V2) w2[r] = v2_in[base + idx];
+      } else {
+        k[r] = 0;
+        v[r] = 0;
+        if constexpr (V2) w2[r] = 0;
+      }
     }
   }
   // thread t owns digit t: start of digit t over the whole pass (scan of the
@@ -404,8 +546,8 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
   const uint64_t lanes_below = (lane == 0) ? 0ull : (~0ull >> (kWave - lane));
   uint32_t* wc = s_wcnt[wave];
 #pragma unroll
-  for (int r = 0; r < kOsItems; ++r) {
-    const bool valid = wave * kOsWaveKeys + r * kWave + lane < cnt;
+  for (int r = 0; r < ITEMS; ++r) {
+    const bool valid = wave * kWaveKeysT + r * kWave + lane < cnt;
     const uint32_t d = digit_of(k[r], shift) ^ dxor;
     uint64_t peers = __ballot(valid);
 #pragma unroll
@@ -449,8 +591,8 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
   // reorder the partition by digit in LDS before looking back, so the keys
   // leave registers while earlier partitions publish
 #pragma unroll
-  for (int r = 0; r < kOsItems; ++r) {
-    if (wave * kOsWaveKeys + r * kWave + lane < cnt) {
+  for (int r = 0; r < ITEMS; ++r) {
+    if (wave * kWaveKeysT + r * kWave + lane < cnt) {
       const uint32_t d = digit_of(k[r], shift) ^ dxor;
       const uint32_t pos = s_tile_start[d] + wc[d] + rank[r];
       s_keys[pos] = k[r];
@@ -509,7 +651,45 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) s_wcnt[w][t] = 0;
     __syncthreads();
-    for (int64_t i = t; i < base; i += kSortBlock) atomicAdd(&wc[digit_of(kin[i], shift) ^ dxor], 1u);
+    if constexpr (GEN) {
+      // the low key digits of entries [0, base) from the ranks' rects: every
+      // rank before the partition's first whole, that one up to base, row by
+      // row (consecutive keys) into a difference array in row 1 and a count
+      // for every digit in row 2
+      uint32_t* diff = s_wcnt[1];
+      uint32_t all = 0;
+      const int64_t r0 = gen.part_rank[part];
+      for (int64_t r = t; r <= r0; r += kSortBlock) {
+        const uint4 rec = gen.ranked[r];
+        const uint32_t hi_bits = static_cast<uint32_t>(static_cast<int64_t>(rec.w) / gen.n_per_image) << gen.tile_bits;
+        const int32_t w = static_cast<int32_t>(rec.y & 0xffffu), h = static_cast<int32_t>(rec.y >> 16);
+        const int64_t e = min<int64_t>(static_cast<int64_t>(w) * h, base - gen.offsets[r]);
+        if (e <= 0) continue;
+        const int32_t full = static_cast<int32_t>(e / w), rem = static_cast<int32_t>(e - static_cast<int64_t>(full) * w);
+        const int32_t x0 = static_cast<int32_t>(rec.x & 0xffffu), y0 = static_cast<int32_t>(rec.x >> 16);
+        for (int32_t y = 0; y <= full; ++y) {
+          const int32_t len = y < full ? w : rem;
+          if (len > 0)
+            add_low_digits(diff, all, hi_bits | static_cast<uint32_t>((y0 + y) * gen.tw + x0),
+                           static_cast<uint32_t>(len));
+        }
+      }
+      atomicAdd(&s_wcnt[2][0], all);
+      __syncthreads();
+      const uint32_t all_tot = s_wcnt[2][0];
+      const int inc = wave_inclusive_scan(static_cast<int>(diff[t]));
+      if (lane == kWave - 1) s_wsum[wave] = static_cast<uint32_t>(inc);
+      __syncthreads();
+      uint32_t wb = 0;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w)
+        if (w < wave) wb += s_wsum[w];
+      s_wcnt[0][t] = all_tot + wb + static_cast<uint32_t>(inc);
+      s_wcnt[1][t] = 0;
+      s_wcnt[2][t] = 0;
+    } else {
+      for (int64_t i = t; i < base; i += kSortBlock) atomicAdd(&wc[digit_of(kin[i], shift) ^ dxor], 1u);
+    }
     __syncthreads();
     if (gave_up) {
       prefix = 0;
@@ -525,6 +705,11 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
     const K key = s_keys[j];
     const uint32_t d = digit_of(key, shift) ^ dxor;
     const int64_t dst = static_cast<int64_t>(s_gbase[d]) + (j - static_cast<int64_t>(s_tile_start[d]));
+    // generated keys whose digits disagree with the histogram (offsets not
+    // from these rects) land out of place but never out of bounds
+    if constexpr (GEN) {
+      if (dst < 0 || dst >= n) continue;
+    }
     const int32_t val = s_vals[j];
     if constexpr (ASM && V2) {
       out.ids[dst] = static_cast<int64_t>((static_cast<uint64_t>(key) << 32) | s_v2[j]);
@@ -537,6 +722,98 @@ __global__ void __launch_bounds__(kSortBlock) onesweep_kernel(const K* __restric
     if constexpr (GATHER) out.gathered[dst] = out.gather[val];
     vout[dst] = val;
   }
+}
+
+// Records and digit histograms of the generated tile lists, one pass over
+// the Gaussians in their own order: recs[g] = (min_x | min_y << 16,
+// width | height << 16, depth bits, image << tile_bits) of g's AABB tile
+// rect (aabb_tile_rect, the rect the counts were taken from), and per block
+// one row of partial counts per pass (as hist_partial_kernel) of g's keys:
+// each rect row is a run of consecutive keys, added to the low digit through
+// a difference array and to the higher digits run by run. Also clears the
+// totals and look-back words, as hist_partial_kernel does.
+__global__ void __launch_bounds__(kSortBlock) tile_records_kernel(
+    const float* __restrict__ means2d, const int32_t* __restrict__ radii, const float* __restrict__ depths,
+    int64_t numel, int64_t n_per_image, int ts, int tw, int th, int tile_bits, int passes, uint4* __restrict__ recs,
+    uint32_t* __restrict__ partial, uint32_t* __restrict__ clear, int64_t clear_words) {
+  __shared__ uint32_t h[kMaxPasses][kRadix];  // pass 0: the difference array
+  __shared__ uint32_t s_all;
+  __shared__ uint32_t s_wsum[kWaves];
+  const int t = threadIdx.x;
+  const int lane = t % kWave, wave = t / kWave;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kSortBlock + t; i < clear_words;
+       i += static_cast<int64_t>(gridDim.x) * kSortBlock)
+    clear[i] = 0u;
+  for (int p = 0; p < passes; ++p) h[p][t] = 0;
+  if (t == 0) s_all = 0;
+  __syncthreads();
+  uint32_t all = 0;
+  for (int64_t g = static_cast<int64_t>(blockIdx.x) * kSortBlock + t; g < numel;
+       g += static_cast<int64_t>(gridDim.x) * kSortBlock) {
+    const TileRect r = aabb_tile_rect(means2d[g * 2], means2d[g * 2 + 1], radii[g * 2], radii[g * 2 + 1], ts, tw, th);
+    const int w = max(r.max_x - r.min_x, 0), hh = max(r.max_y - r.min_y, 0);
+    const uint32_t hi = static_cast<uint32_t>(g / n_per_image) << tile_bits;
+    recs[g] = make_uint4(static_cast<uint32_t>(r.min_x) | (static_cast<uint32_t>(r.min_y) << 16),
+                         static_cast<uint32_t>(w) | (static_cast<uint32_t>(hh) << 16), __float_as_uint(depths[g]), hi);
+    if (w == 0) continue;
+    for (int y = 0; y < hh; ++y) {
+      const uint32_t a = hi | static_cast<uint32_t>((r.min_y + y) * tw + r.min_x);
+      add_low_digits(h[0], all, a, static_cast<uint32_t>(w));
+      for (int p = 1; p < passes; ++p) {
+        const int sh = 8 * p;
+        const uint64_t end = static_cast<uint64_t>(a) + static_cast<uint64_t>(w);
+        for (uint64_t v = a >> sh; v <= (end - 1) >> sh; ++v) {
+          const uint64_t lo = max<uint64_t>(a, v << sh), up = min<uint64_t>(end, (v + 1) << sh);
+          atomicAdd(&h[p][v & (kRadix - 1)], static_cast<uint32_t>(up - lo));
+        }
+      }
+    }
+  }
+  atomicAdd(&s_all, all);
+  __syncthreads();
+  const int inc = wave_inclusive_scan(static_cast<int>(h[0][t]));
+  if (lane == kWave - 1) s_wsum[wave] = static_cast<uint32_t>(inc);
+  __syncthreads();
+  uint32_t wb = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w)
+    if (w < wave) wb += s_wsum[w];
+  partial[static_cast<int64_t>(blockIdx.x) * kMaxPasses * kRadix + t] = s_all + wb + static_cast<uint32_t>(inc);
+  for (int p = 1; p < passes; ++p) partial[(static_cast<int64_t>(blockIdx.x) * kMaxPasses + p) * kRadix + t] = h[p][t];
+}
+
+// ranked[r] = recs[perm[r]] with the Gaussian perm[r] in place of the image
+// bits: the records in depth order, so that a generated partition reads
+// its ranks' records coalesced.
+__global__ void __launch_bounds__(256) rank_records_kernel(const int32_t* __restrict__ perm,
+                                                           const uint4* __restrict__ recs, int64_t numel,
+                                                           uint4* __restrict__ ranked) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (r >= numel) return;
+  const int32_t g = perm[r];
+  const uint4 rec = recs[g];
+  ranked[r] = make_uint4(rec.x, rec.y, rec.z, static_cast<uint32_t>(g));
+}
+
+// part_rank[p] = the last depth rank whose first entry is <= tile p (the rank
+// holding partition p's first entry), for p < n_parts; part_rank[n_parts] =
+// numel - 1.
+__global__ void __launch_bounds__(256) partition_ranks_kernel(const int32_t* __restrict__ offsets, int64_t numel,
+                                                              int64_t n_parts, int64_t tile,
+                                                              int32_t* __restrict__ part_rank) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (p > n_parts) return;
+  if (p == n_parts) {
+    part_rank[p] = static_cast<int32_t>(numel - 1);
+    return;
+  }
+  const int64_t x = p * tile;
+  int64_t lo = 0, hi = numel - 1;
+  while (lo < hi) {
+    const int64_t mid = (lo + hi + 1) >> 1;
+    if (offsets[mid] <= x) lo = mid; else hi = mid - 1;
+  }
+  part_rank[p] = static_cast<int32_t>(lo);
 }
 
 template <typename K>
@@ -844,6 +1121,90 @@ int radix_sort_pairs_i64_planned(const int64_t* keys_in_s, const int32_t* vals_i
     if ((rc = check_launch(what))) return rc;
     src_k = dst_k;
     src_v = dst_v;
+  }
+  return GSPLAT_OK;
+}
+
+// At most three passes: the generated pass's look-back words (a third more
+// partitions than a pass of 4096 keys) and the others' fit the four passes'
+// words of the workspace.
+bool tiles_generated_supported(int64_t n, int tw, int th, int bit_hi) {
+  return n > 0 && n < g_onesweep_max_keys.load(std::memory_order_relaxed) && tw > 0 && th > 0 && tw < 65536 &&
+         th < 65536 && bit_hi >= 1 && bit_hi <= 24;
+}
+
+int radix_sort_tiles_generated(const float* means2d, const int32_t* radii, const float* depths, const int32_t* perm,
+                               const int32_t* offsets, int64_t numel, int64_t n_per_image, int ts, int tw, int th,
+                               int tile_bits, int64_t n, int bit_hi, uint4* recs, int32_t* part_rank,
+                               uint32_t* keys_out, int32_t* vals_out, int64_t* ids, uint32_t* bits,
+                               uint32_t* bits_alt, void* workspace, size_t workspace_bytes, hipStream_t s,
+                               const char* what) {
+  using K = uint32_t;
+  const std::string w(what);
+  if (!tiles_generated_supported(n, tw, th, bit_hi) || numel <= 0 || numel > INT32_MAX || n_per_image <= 0)
+    return invalid(w + ": invalid sort arguments.");
+  if (!means2d || !radii || !depths || !perm || !offsets || !recs || !part_rank || !keys_out || !vals_out || !ids ||
+      !bits || !bits_alt)
+    return invalid(w + ": null pointer.");
+  SortWorkspace<K> ws;
+  if (!workspace || workspace_bytes < layout<K>(n, &ws, workspace)) {
+    set_error(w + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  const int passes = (bit_hi + 7) / 8;
+  const int64_t n_parts = (n + kOsTile - 1) / kOsTile;
+  const int64_t n_gen = (n + kGenTile - 1) / kGenTile;  // partitions of the generated pass
+  const int spin = g_spin_limit.load(std::memory_order_relaxed);
+  // look-back words: the generated pass's, then each later pass's
+  auto look = [&](int p) { return ws.os_lookback + (p == 0 ? 0 : (n_gen + (p - 1) * n_parts) * kRadix); };
+  const int64_t clear_words = (reinterpret_cast<char*>(look(passes)) - reinterpret_cast<char*>(ws.os_hist)) / 4;
+  int rc;
+  {
+    KernelTimer timer("sort_histogram", s);
+    const int hb = static_cast<int>(std::min<int64_t>((numel + kSortBlock - 1) / kSortBlock, kHistBlocks));
+    tile_records_kernel<<<static_cast<unsigned>(hb), kSortBlock, 0, s>>>(
+        means2d, radii, depths, numel, n_per_image, ts, tw, th, tile_bits, passes, recs, ws.os_partial, ws.os_hist,
+        clear_words);
+    const dim3 add_grid((hb + kHistRowsPerAdd - 1) / kHistRowsPerAdd, passes);
+    hist_add_kernel<<<add_grid, kSortBlock, 0, s>>>(ws.os_partial, hb, ws.os_hist);
+    partition_ranks_kernel<<<grid_for(n_gen + 1, 256), 256, 0, s>>>(offsets, numel, n_gen, kGenTile, part_rank);
+    rank_records_kernel<<<grid_for(numel, 256), 256, 0, s>>>(perm, recs, numel, recs + numel);
+  }
+  if ((rc = check_launch(what))) return rc;
+  const TileGenArgs gen{offsets, recs + numel, part_rank, numel, n_per_image, tw, tile_bits};
+  const K* src_k = nullptr;
+  const int32_t* src_v = nullptr;
+  const uint32_t* src_b = nullptr;
+  for (int p = 0; p < passes; ++p) {
+    const bool to_out = ((passes - 1 - p) % 2) == 0;
+    K* dst_k = to_out ? keys_out : ws.keys_alt;
+    int32_t* dst_v = to_out ? vals_out : ws.vals_alt;
+    uint32_t* dst_b = p % 2 == 0 ? bits_alt : bits;
+    {
+      KernelTimer timer("sort_onesweep", s);
+      const bool last = p == passes - 1;
+      const OsOut<K> o{dst_k, dst_v, depths, ids, nullptr, nullptr, dst_b};
+      const unsigned grid = static_cast<unsigned>(p == 0 ? n_gen : n_parts);
+      const uint32_t* hist_p = ws.os_hist + p * kRadix;
+      uint32_t* look_p = look(p);
+      const int shift = 8 * p;
+      if (p == 0 && last)
+        onesweep_kernel<K, true, false, true, true, kGenItems><<<grid, kSortBlock, 0, s>>>(
+            nullptr, nullptr, nullptr, n, shift, hist_p, look_p, spin, o, 0u, gen);
+      else if (p == 0)
+        onesweep_kernel<K, false, false, true, true, kGenItems><<<grid, kSortBlock, 0, s>>>(
+            nullptr, nullptr, nullptr, n, shift, hist_p, look_p, spin, o, 0u, gen);
+      else if (last)
+        onesweep_kernel<K, true, false, true><<<grid, kSortBlock, 0, s>>>(src_k, src_v, src_b, n, shift, hist_p,
+                                                                          look_p, spin, o, 0u);
+      else
+        onesweep_kernel<K, false, false, true><<<grid, kSortBlock, 0, s>>>(src_k, src_v, src_b, n, shift, hist_p,
+                                                                           look_p, spin, o, 0u);
+    }
+    if ((rc = check_launch(what))) return rc;
+    src_k = dst_k;
+    src_v = dst_v;
+    src_b = dst_b;
   }
   return GSPLAT_OK;
 }

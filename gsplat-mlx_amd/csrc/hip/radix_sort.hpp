@@ -31,4 +31,27 @@ int radix_sort_pairs(const K* keys_in, const int32_t* vals_in, int64_t n, int bi
                      const int32_t* gather_src = nullptr, int32_t* gather_dst = nullptr, uint32_t* asm_bits = nullptr,
                      uint32_t* asm_bits_alt = nullptr);
 
+// Whether radix_sort_tiles_generated takes n entries on a tw x th tile grid
+// with keys of bit_hi bits.
+bool tiles_generated_supported(int64_t n, int tw, int th, int bit_hi);
+
+// The depth-presorted tile lists sorted by (image, tile) with the encode
+// folded into the first pass: the same output as encoding the lists of the
+// Gaussians in depth order (entry j of rank r: Gaussian perm[r], tile k =
+// j - offsets[r] of its AABB rect in row-major order, key image << tile_bits
+// | tile, carried depth bits) and sorting bits [0, bit_hi) of the keys with
+// radix_sort_pairs into ids (key << 32 | depth bits) and vals_out (Gaussian),
+// without the encoded keys ever being stored. n entries in all (offsets:
+// exclusive scan of the rect sizes in rank order); numel Gaussians,
+// n_per_image per image. Scratch: recs [2 numel] (16 bytes each), part_rank
+// [n / 3072 + 2], keys_out, bits and bits_alt [n] each, and the
+// radix_sort_workspace_bytes<uint32_t>(n) workspace. Requires
+// tiles_generated_supported(n, tw, th).
+int radix_sort_tiles_generated(const float* means2d, const int32_t* radii, const float* depths, const int32_t* perm,
+                               const int32_t* offsets, int64_t numel, int64_t n_per_image, int ts, int tw, int th,
+                               int tile_bits, int64_t n, int bit_hi, uint4* recs, int32_t* part_rank,
+                               uint32_t* keys_out, int32_t* vals_out, int64_t* ids, uint32_t* bits,
+                               uint32_t* bits_alt, void* workspace, size_t workspace_bytes, hipStream_t stream,
+                               const char* what);
+
 }  // namespace gsplat_hip

@@ -311,9 +311,12 @@ int gsplat_hip_sort_lookback_recounts(uint64_t* count);
  * carry_min_pairs pairs (default 2^21), and take every encode block's rank
  * range from one up-front search kernel (rather than searching in each block)
  * from split_min_blocks blocks on (default 65536). Negative values restore the
- * defaults; the outputs are the same either way. isect_debug_reset restores
- * both. */
+ * defaults. A carrying AABB sort with at least four entries per Gaussian forms
+ * its first pass's keys inside that pass instead of encoding and re-reading
+ * them; isect_debug_generated(0) turns that off (1, the default, on). The
+ * outputs are the same either way. isect_debug_reset restores all three. */
 void gsplat_hip_isect_debug_set(int64_t carry_min_pairs, int64_t split_min_blocks);
+void gsplat_hip_isect_debug_generated(int32_t enable);
 void gsplat_hip_isect_debug_reset(void);
 
 /* Sorted intersections in one call: replaces the encode + sort of

@@ -13,7 +13,12 @@ the oracle's intersection lists:
 - in the depth-presorted intersection, the tile-key sort carrying each
   entry's depth bits (taken above 2^21 pairs) and the encode blocks' rank
   ranges from the up-front split kernel (taken from 65536 blocks), forced on
-  at small sizes for the AABB, ellipse and packed encodes.
+  at small sizes for the AABB, ellipse and packed encodes;
+- the carrying AABB sort's generated first pass (keys formed inside the pass
+  from the depth ranks' rects instead of encoded; taken with at least four
+  entries per Gaussian) against the encoded one, with one, two and three
+  passes, several images, partitions spanning more ranks than one LDS chunk
+  holds, and the recount of its look-back prefix from the rects.
 
 Every kernel runs to completion in these tests: the hooks only change which
 of two correct ways a partition obtains its prefix, or which sort runs."""
@@ -50,6 +55,8 @@ def _lib():
     lib.gsplat_hip_isect_debug_set.restype = None
     lib.gsplat_hip_isect_debug_set.argtypes = [i64, i64]
     lib.gsplat_hip_isect_debug_reset.restype = None
+    lib.gsplat_hip_isect_debug_generated.restype = None
+    lib.gsplat_hip_isect_debug_generated.argtypes = [i32]
     lib.gsplat_hip_isect_tile_sorted_workspace_size.restype = ctypes.c_size_t
     lib.gsplat_hip_isect_tile_sorted_workspace_size.argtypes = [i64, i64]
     lib.gsplat_hip_isect_tile_sorted.restype = ctypes.c_int
@@ -199,10 +206,11 @@ def test_reduce_then_scan_path_is_exact(lib, n, bits):
     np.testing.assert_array_equal(vo, vals[order])
 
 
-@pytest.mark.parametrize("splits", [False, True])
-@pytest.mark.parametrize("carry", [False, True])
+@pytest.mark.parametrize("carry,splits,generated", [(False, False, False), (False, True, False),
+                                                     (True, False, False), (True, True, False),
+                                                     (True, False, True)])
 @pytest.mark.parametrize("mode", ["onesweep", "recount", "reduce_then_scan"])
-def test_intersection_pipeline_on_forced_paths(lib, oracle, mode, carry, splits):
+def test_intersection_pipeline_on_forced_paths(lib, oracle, mode, carry, splits, generated):
     """The two sorts of the depth-presorted intersection pipeline (32-bit
     depth keys gathering the counts; 32-bit tile keys assembling the 64-bit
     ids, with the depth bits gathered or carried), through the C ABI's one-call
@@ -219,12 +227,15 @@ def test_intersection_pipeline_on_forced_paths(lib, oracle, mode, carry, splits)
     exp = oracle.isect_tile(m, r, d, I, ts, tw, th, sort=True)
     counts = oracle.isect_count(m, r, ts, tw, th).astype(np.int32)
     n_isects = int(counts.sum())
-    print(f"intersection pipeline, {mode} carry={carry} splits={splits}, {n_isects} intersections", flush=True)
+    print(f"intersection pipeline, {mode} carry={carry} splits={splits} generated={generated}, "
+          f"{n_isects} intersections", flush=True)
+    assert n_isects >= 4 * I * N  # the generated pass's condition
     if mode == "recount":
         lib.gsplat_hip_sort_debug_set(-1, 0)
     elif mode == "reduce_then_scan":
         lib.gsplat_hip_sort_debug_set(1 << 18, 1)
     lib.gsplat_hip_isect_debug_set(0 if carry else 1 << 40, 1 if splits else 1 << 40)
+    lib.gsplat_hip_isect_debug_generated(1 if generated else 0)
     ws_bytes = lib.gsplat_hip_isect_tile_sorted_workspace_size(I * N, n_isects)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
     md, rd, dd, cd = dev(m), dev(r), dev(d), dev(counts)
@@ -271,3 +282,62 @@ def test_sorted_encodes_with_carried_bits_and_splits(lib, oracle, layout):
         ref = oracle.isect_tile_packed(means, radii, depths, img, I, TS, tw, th, sort=True, **kw)
     np.testing.assert_array_equal(host(out["isect_ids"]), ref["isect_ids"])
     np.testing.assert_array_equal(host(out["flatten_ids"]), ref["flatten_ids"])
+
+
+@pytest.mark.parametrize("case", ["mixed", "three_passes", "one_pass", "images"])
+@pytest.mark.parametrize("recount", [False, True])
+def test_generated_first_pass(lib, oracle, case, recount):
+    """The generated first pass (carried bits, keys formed in the pass) gives
+    the oracle's sorted lists bit for bit: mixed has a depth range of
+    one-tile and invisible Gaussians before large ones, so partitions there
+    hold more ranks than one LDS chunk (1535); three_passes a 65536-tile grid
+    (17 key bits); one_pass an 8 x 8 tile grid (7 bits: the generated pass is
+    also the last); images four images. recount: every partition recounts its
+    look-back prefix from the rects."""
+    import torch
+
+    from test_gpu_isect import random_projected
+
+    rng = np.random.default_rng({"mixed": 1, "three_passes": 2, "one_pass": 3, "images": 4}[case])
+    I, ts = 1, 16
+    if case == "mixed":
+        N, W, H = 40_000, 640, 480
+        m = np.stack([rng.uniform(0, W, (I, N)), rng.uniform(0, H, (I, N))], -1).astype(np.float32)
+        d = rng.uniform(0.1, 50, (I, N)).astype(np.float32)
+        near = d < 25  # the near half: one-tile Gaussians, a third of them invisible
+        r = np.where(near[..., None], 3, rng.integers(40, 120, (I, N, 2))).astype(np.int32)
+        r[near & (rng.random((I, N)) < 0.33)] = 0
+    elif case == "three_passes":
+        N, W, H = 30_000, 4096, 4096
+        m, r, d = random_projected(rng, I, N, W, H, ties=True)
+    elif case == "one_pass":
+        N, W, H = 5_000, 128, 128
+        m, r, d = random_projected(rng, I, N, W, H, ties=True, signed=True)
+    else:
+        I, N, W, H = 4, 8_000, 320, 240
+        m, r, d = random_projected(rng, I, N, W, H, ties=True)
+    tw, th = (W + ts - 1) // ts, (H + ts - 1) // ts
+    exp = oracle.isect_tile(m, r, d, I, ts, tw, th, sort=True)
+    counts = oracle.isect_count(m, r, ts, tw, th).astype(np.int32)
+    n_isects = int(counts.sum())
+    print(f"generated first pass {case} recount={recount}: {I}x{N} Gaussians, {tw}x{th} tiles, "
+          f"{n_isects} intersections", flush=True)
+    assert n_isects >= 4 * I * N
+    if recount:
+        lib.gsplat_hip_sort_debug_set(-1, 0)
+    lib.gsplat_hip_isect_debug_set(0, 1 << 40)  # carry the depth bits
+    before = _recounts(lib)
+    ws_bytes = lib.gsplat_hip_isect_tile_sorted_workspace_size(I * N, n_isects)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    md, rd, dd, cd = dev(m), dev(r), dev(d), dev(counts)
+    ids = torch.empty(n_isects, dtype=torch.int64, device="cuda")
+    flat = torch.empty(n_isects, dtype=torch.int32, device="cuda")
+    rc = lib.gsplat_hip_isect_tile_sorted(md.data_ptr(), rd.data_ptr(), dd.data_ptr(), cd.data_ptr(), I, I * N, ts,
+                                          tw, th, n_isects, ids.data_ptr(), flat.data_ptr(), ws.data_ptr(), ws_bytes,
+                                          torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.gsplat_hip_last_error()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(ids), exp["isect_ids"])
+    np.testing.assert_array_equal(host(flat), exp["flatten_ids"])
+    if recount:  # every partition after the first of every pass (the depth sort's too) recounted
+        assert _recounts(lib) - before > (n_isects + PART - 1) // PART - 1
