@@ -409,6 +409,61 @@ py::dict activated_projection_forward(const TensorMap& inputs, int image_width, 
   return r;
 }
 
+// Activated packed projection: inputs as activated_projection_forward; the
+// packed rows plus per-row "opacities" and the "rank" the backward reads.
+py::dict activated_projection_packed_forward(const TensorMap& inputs, int image_width, int image_height,
+                                             float eps2d, float near_plane, float far_plane, float radius_clip,
+                                             bool calc_compensations, int camera_model,
+                                             bool opacities_in_projection) {
+  gsplat_core::ProjectionEWA3DGSFusedInput in;
+  in.means = require_key(inputs, "means");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.quats = require_key(inputs, "quats");
+  in.scales = require_key(inputs, "log_scales");
+  in.opacities = get_or_empty(inputs, "opacity_logits");
+  in.params = {image_width, image_height, eps2d, near_plane, far_plane, radius_clip, calc_compensations,
+               camera_model, false, opacities_in_projection && in.opacities.numel() != 0};
+  auto out = gsplat_core::gsplat_activated_projection_packed_forward(in);
+  py::dict r;
+  const char* keys[] = {"batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii", "means2d",
+                        "depths",    "conics",     "compensations", "opacities", "rank"};
+  for (size_t i = 0; i < out.size(); ++i) r[keys[i]] = out[i];
+  return r;
+}
+
+// forward_outputs: conics, rank (compensations optional); cotangents per row
+// (v_depths, v_compensations, v_opacities optional).
+py::dict activated_projection_packed_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
+                                              const TensorMap& cotangents, int image_width, int image_height,
+                                              float eps2d, int camera_model, bool viewmats_requires_grad) {
+  gsplat_core::ProjectionEWA3DGSPackedBackwardInput in;
+  in.means = require_key(inputs, "means");
+  in.viewmats = require_key(inputs, "viewmats");
+  in.Ks = require_key(inputs, "Ks");
+  in.quats = require_key(inputs, "quats");
+  in.scales = require_key(inputs, "log_scales");
+  in.conics = require_key(forward_outputs, "conics");
+  in.compensations = get_or_empty(forward_outputs, "compensations");
+  in.v_means2d = require_key(cotangents, "v_means2d");
+  in.v_depths = get_or_empty(cotangents, "v_depths");
+  in.v_conics = require_key(cotangents, "v_conics");
+  in.v_compensations = get_or_empty(cotangents, "v_compensations");
+  in.params = {image_width, image_height, eps2d, -1.0e20f, 1.0e20f, 0.0f, in.compensations.numel() != 0,
+               camera_model, false, false};
+  in.viewmats_requires_grad = viewmats_requires_grad;
+  auto out = gsplat_core::gsplat_activated_projection_packed_backward(
+      in, require_key(forward_outputs, "rank"), get_or_empty(inputs, "opacity_logits"),
+      get_or_empty(cotangents, "v_opacities"));
+  py::dict r;
+  r["v_means"] = out[0];
+  r["v_quats"] = out[1];
+  r["v_log_scales"] = out[2];
+  r["v_opacity_logits"] = out[3];
+  if (viewmats_requires_grad) r["v_viewmats"] = out[4];
+  return r;
+}
+
 py::dict activated_projection_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
                                        const TensorMap& cotangents, int image_width, int image_height, float eps2d,
                                        int camera_model, bool viewmats_requires_grad) {
@@ -599,6 +654,13 @@ PYBIND11_MODULE(_gsplat_core, m) {
         py::arg("far_plane") = 1.0e10f, py::arg("radius_clip") = 0.0f, py::arg("calc_compensations") = false,
         py::arg("camera_model") = 0, py::arg("opacities_in_projection") = false);
   m.def("activated_projection_backward", &activated_projection_backward, py::arg("inputs"),
+        py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
+        py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
+  m.def("activated_projection_packed_forward", &activated_projection_packed_forward, py::arg("inputs"),
+        py::arg("image_width"), py::arg("image_height"), py::arg("eps2d") = 0.3f, py::arg("near_plane") = 0.01f,
+        py::arg("far_plane") = 1.0e10f, py::arg("radius_clip") = 0.0f, py::arg("calc_compensations") = false,
+        py::arg("camera_model") = 0, py::arg("opacities_in_projection") = false);
+  m.def("activated_projection_packed_backward", &activated_projection_packed_backward, py::arg("inputs"),
         py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
         py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
   m.def("render_rgb_forward", &render_rgb_forward, py::arg("inputs"), py::arg("image_width"),

@@ -394,6 +394,139 @@ std::vector<array> gsplat_projection_ewa_3dgs_packed_backward(const ProjectionEW
   return {v_means, v_covars, v_quats, v_scales, v_viewmats};
 }
 
+std::vector<array> gsplat_activated_projection_packed_forward(const ProjectionEWA3DGSFusedInput& input) {
+  const char* op = "activated_projection_packed_forward";
+  if (input.params.use_covars) throw std::runtime_error(std::string(op) + " takes quats and log_scales, not covars.");
+  validate_inputs(input);
+  require_device(input.means, "means");
+  require_device(input.viewmats, "viewmats");
+  require_device(input.Ks, "Ks");
+  const Dims d = dims_of(input.means, input.viewmats, input.Ks);
+  const auto& p = input.params;
+  check_gaussian_params(input.means, input.covars, input.quats, input.scales, false, d.B * d.N);
+  const bool have_logits = !is_empty(input.opacities);
+  if (p.use_opacities && !have_logits) throw std::runtime_error(std::string(op) + ": use_opacities without logits.");
+  if (have_logits) {
+    require_device(input.opacities, "opacity_logits");
+    require_dtype(input.opacities, at::kFloat, "activated_projection_packed expects float32 opacity_logits.");
+    if (input.opacities.numel() != d.B * d.N) throw std::runtime_error("opacity_logits must have shape [..., N].");
+  }
+  const c10::DeviceGuard guard(input.means.device());
+  const array means = contig(input.means);
+  const array quats = contig(input.quats);
+  const array scales = contig(input.scales);
+  const array logits = have_logits ? contig(input.opacities) : array();
+  const array viewmats = contig(input.viewmats.to(at::kFloat));
+  const array Ks = contig(input.Ks.to(at::kFloat));
+  void* stream = stream_for(input.s, means);
+  const gsplat_projection_params cp = to_c(p);
+  const size_t ws_bytes = gsplat_hip_projection_packed_workspace_size(d.B, d.C, d.N, 0);
+  array ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, u8_like(means));
+  array count = at::empty({1}, i64_like(means));
+  const float* l_p = have_logits ? logits.data_ptr<float>() : nullptr;
+  check(gsplat_hip_activated_projection_packed_count(means.data_ptr<float>(), quats.data_ptr<float>(),
+                                                     scales.data_ptr<float>(), l_p, viewmats.data_ptr<float>(),
+                                                     Ks.data_ptr<float>(), d.B, d.C, d.N, &cp,
+                                                     count.data_ptr<int64_t>(), ws.data_ptr<uint8_t>(), ws_bytes,
+                                                     stream));
+  const int64_t nnz = d.B * d.C * d.N > 0 ? read_count(count, stream) : 0;
+  auto i32 = [&](std::vector<int64_t> shape) { return at::empty(shape, i32_like(means)); };
+  auto f32 = [&](std::vector<int64_t> shape) { return at::empty(shape, f32_like(means)); };
+  array batch_ids = i32({nnz}), camera_ids = i32({nnz}), gaussian_ids = i32({nnz});
+  array indptr = i32({d.B * d.C + 1});
+  array radii = i32({nnz, 2});
+  array means2d = f32({nnz, 2}), depths = f32({nnz}), conics = f32({nnz, 3});
+  array comps = p.calc_compensations ? f32({nnz}) : f32({0});
+  array opac = have_logits ? f32({nnz}) : f32({0});
+  check(gsplat_hip_activated_projection_packed_fwd(
+      means.data_ptr<float>(), quats.data_ptr<float>(), scales.data_ptr<float>(), l_p, viewmats.data_ptr<float>(),
+      Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, nnz, batch_ids.data_ptr<int32_t>(), camera_ids.data_ptr<int32_t>(),
+      gaussian_ids.data_ptr<int32_t>(), indptr.data_ptr<int32_t>(), radii.data_ptr<int32_t>(),
+      means2d.data_ptr<float>(), depths.data_ptr<float>(), conics.data_ptr<float>(),
+      p.calc_compensations ? comps.data_ptr<float>() : nullptr, have_logits ? opac.data_ptr<float>() : nullptr,
+      ws.data_ptr<uint8_t>(), ws_bytes, stream));
+  return {batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d, depths, conics, comps, opac, ws};
+}
+
+std::vector<array> gsplat_activated_projection_packed_backward(const ProjectionEWA3DGSPackedBackwardInput& input,
+                                                               const array& rank, const array& opacity_logits,
+                                                               const array& v_opacities) {
+  const char* op = "activated_projection_packed_backward";
+  if (input.params.use_covars) throw std::runtime_error(std::string(op) + " takes quats and log_scales, not covars.");
+  ProjectionEWA3DGSFusedInput fwd;
+  fwd.means = input.means;
+  fwd.quats = input.quats;
+  fwd.scales = input.scales;
+  fwd.viewmats = input.viewmats;
+  fwd.Ks = input.Ks;
+  fwd.params = input.params;
+  validate_inputs(fwd);
+  if (input.params.camera_model < 0 || input.params.camera_model > 2)
+    throw std::runtime_error(std::string(op) + ": unknown camera model.");
+  require_device(input.means, "means");
+  require_device(input.viewmats, "viewmats");
+  require_device(input.Ks, "Ks");
+  const Dims d = dims_of(input.means, input.viewmats, input.Ks);
+  const auto& p = input.params;
+  check_gaussian_params(input.means, input.covars, input.quats, input.scales, false, d.B * d.N);
+  const int64_t nnz = input.conics.numel() / 3;
+  const bool use_v_depths = !is_empty(input.v_depths);
+  const bool have_logits = !is_empty(opacity_logits);
+  const bool have_v_opac = have_logits && !is_empty(v_opacities);
+  if (input.conics.numel() != nnz * 3 || input.v_means2d.numel() != nnz * 2 || input.v_conics.numel() != nnz * 3 ||
+      (use_v_depths && input.v_depths.numel() != nnz) || (have_v_opac && v_opacities.numel() != nnz))
+    throw std::runtime_error(std::string(op) + ": packed inputs must have nnz rows.");
+  const size_t rank_bytes = gsplat_hip_projection_packed_workspace_size(d.B, d.C, d.N, 0);
+  require_device(rank, "rank");
+  if (rank.scalar_type() != at::kByte || static_cast<size_t>(rank.numel()) < rank_bytes)
+    throw std::runtime_error(std::string(op) + ": rank must be the forward's uint8 workspace.");
+  const bool use_comp = p.calc_compensations && !is_empty(input.compensations) && !is_empty(input.v_compensations);
+  if (use_comp && (input.compensations.numel() != nnz || input.v_compensations.numel() != nnz))
+    throw std::runtime_error("compensations / v_compensations must have nnz rows.");
+  if (have_logits) {
+    require_device(opacity_logits, "opacity_logits");
+    require_dtype(opacity_logits, at::kFloat, "activated_projection_packed expects float32 opacity_logits.");
+    if (opacity_logits.numel() != d.B * d.N) throw std::runtime_error("opacity_logits must have shape [..., N].");
+  }
+  const c10::DeviceGuard guard(input.means.device());
+  const array means = contig(input.means);
+  const array quats = contig(input.quats);
+  const array scales = contig(input.scales);
+  const array viewmats = contig(input.viewmats.to(at::kFloat));
+  const array Ks = contig(input.Ks.to(at::kFloat));
+  const array conics = contig(input.conics.to(at::kFloat));
+  const array comps = use_comp ? contig(input.compensations.to(at::kFloat)) : array();
+  const array v_comps = use_comp ? contig(input.v_compensations.to(at::kFloat)) : array();
+  const array v_m2 = contig(input.v_means2d.to(at::kFloat));
+  const array v_dep = use_v_depths ? contig(input.v_depths.to(at::kFloat)) : array();
+  const array v_con = contig(input.v_conics.to(at::kFloat));
+  const array logits = have_logits ? contig(opacity_logits) : array();
+  const array v_opac = have_v_opac ? contig(v_opacities.to(at::kFloat)) : array();
+  const array rk = contig(rank);
+  array v_means = at::empty(means.sizes(), f32_like(means));
+  array v_quats = at::empty(quats.sizes(), f32_like(means));
+  array v_scales = at::empty(scales.sizes(), f32_like(means));
+  array v_logits = have_logits ? at::empty(logits.sizes(), f32_like(means)) : at::empty({0}, f32_like(means));
+  array v_viewmats = input.viewmats_requires_grad ? at::empty(viewmats.sizes(), f32_like(means))
+                                                  : at::empty({0}, f32_like(means));
+  const size_t ws_bytes =
+      gsplat_hip_projection_packed_workspace_size(d.B, d.C, d.N, input.viewmats_requires_grad ? 1 : 0);
+  array ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, u8_like(means));
+  const gsplat_projection_params cp = to_c(p);
+  check(gsplat_hip_activated_projection_packed_bwd(
+      means.data_ptr<float>(), quats.data_ptr<float>(), scales.data_ptr<float>(),
+      have_logits ? logits.data_ptr<float>() : nullptr, viewmats.data_ptr<float>(), Ks.data_ptr<float>(), d.B, d.C,
+      d.N, &cp, nnz, rk.data_ptr<uint8_t>(), static_cast<size_t>(rk.numel()), conics.data_ptr<float>(),
+      use_comp ? comps.data_ptr<float>() : nullptr, v_m2.data_ptr<float>(),
+      use_v_depths ? v_dep.data_ptr<float>() : nullptr, v_con.data_ptr<float>(),
+      use_comp ? v_comps.data_ptr<float>() : nullptr, have_v_opac ? v_opac.data_ptr<float>() : nullptr,
+      v_means.data_ptr<float>(), v_quats.data_ptr<float>(), v_scales.data_ptr<float>(),
+      have_logits ? v_logits.data_ptr<float>() : nullptr,
+      input.viewmats_requires_grad ? v_viewmats.data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(), ws_bytes,
+      stream_for(input.s, means)));
+  return {v_means, v_quats, v_scales, v_logits, v_viewmats};
+}
+
 std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFusedInput& input) {
   return projection_forward_impl(input, false);
 }

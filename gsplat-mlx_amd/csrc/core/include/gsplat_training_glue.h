@@ -25,6 +25,22 @@ std::vector<array> gsplat_activated_projection_forward(const ProjectionEWA3DGSFu
 std::vector<array> gsplat_activated_projection_backward(const ProjectionEWA3DGSFusedBackwardInput& input,
                                                         const array& opacity_logits, const array& v_opacities);
 
+// Activated packed projection: the activations fused into the packed
+// projection (gsplat_projection_ewa_3dgs_packed), fields as
+// gsplat_activated_projection_forward's. Returns {batch_ids, camera_ids,
+// gaussian_ids, indptr, radii, means2d, depths, conics, compensations,
+// opacities, rank}: the packed rows, each row's sigmoid opacity (empty
+// without logits) and the uint8 rank structure the backward reads.
+std::vector<array> gsplat_activated_projection_packed_forward(const ProjectionEWA3DGSFusedInput& input);
+
+// {v_means, v_quats, v_log_scales, v_opacity_logits, v_viewmats} of the
+// activated packed projection: `input` as the packed backward's with raw
+// quats and log-scales (the ids are not read), the forward's rank, the
+// opacity logits and the per-row cotangent of the opacities (empty: zeros).
+std::vector<array> gsplat_activated_projection_packed_backward(const ProjectionEWA3DGSPackedBackwardInput& input,
+                                                               const array& rank, const array& opacity_logits,
+                                                               const array& v_opacities);
+
 // {quats / max(|quats|, 1e-8), exp(log_scales), sigmoid(opacity_logits)};
 // each input may be undefined / empty (its output is then empty).
 std::vector<array> gsplat_gaussian_activations_forward(const array& quats, const array& log_scales,

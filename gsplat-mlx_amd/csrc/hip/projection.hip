@@ -156,6 +156,8 @@ __device__ __forceinline__ int64_t packed_rank(const uint64_t* __restrict__ mask
   return static_cast<int64_t>(prefix[idx >> 6]) + __popcll(w & ((1ull << bit) - 1ull));
 }
 
+// ACT: raw parameters, as the activated projection (project_pair<true>).
+template <bool ACT>
 __global__ void __launch_bounds__(kProjBlock) projection_packed_mask_kernel(
     const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities, const float* __restrict__ viewmats,
@@ -166,7 +168,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_packed_mask_kernel(
   if (idx < total) {
     const int64_t cam = idx / N, n = idx - cam * N;
     const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
-    valid = project_pair<false>(means, covars, quats, scales, opacities, f, (cam / C) * N + n, p).valid;
+    valid = project_pair<ACT>(means, covars, quats, scales, opacities, f, (cam / C) * N + n, p).valid;
   }
   const uint64_t bits = __ballot(valid);
   if ((threadIdx.x % kWave) == 0 && idx < total) {
@@ -175,6 +177,9 @@ __global__ void __launch_bounds__(kProjBlock) projection_packed_mask_kernel(
   }
 }
 
+// ACT: raw parameters; opac_rows (if non-null) receives each visible pair's
+// sigmoid opacity (the rasterizer's per-row opacities).
+template <bool ACT>
 __global__ void __launch_bounds__(kProjBlock) projection_packed_write_kernel(
     const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ opacities, const float* __restrict__ viewmats,
@@ -182,7 +187,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_packed_write_kernel(
     const uint64_t* __restrict__ mask, const int32_t* __restrict__ prefix, int64_t nnz,
     int32_t* __restrict__ batch_ids, int32_t* __restrict__ camera_ids, int32_t* __restrict__ gaussian_ids,
     int32_t* __restrict__ radii, float* __restrict__ means2d, float* __restrict__ depths,
-    float* __restrict__ conics, float* __restrict__ compensations) {
+    float* __restrict__ conics, float* __restrict__ compensations, float* __restrict__ opac_rows) {
   const int64_t idx = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
   if (idx >= total || !((mask[idx >> 6] >> (idx & 63)) & 1ull)) return;
   const int64_t pos = packed_rank(mask, prefix, idx);
@@ -190,7 +195,10 @@ __global__ void __launch_bounds__(kProjBlock) projection_packed_write_kernel(
   const int64_t cam = idx / N, n = idx - cam * N;
   const int64_t b = cam / C;
   const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
-  const PairOut o = project_pair<false>(means, covars, quats, scales, opacities, f, b * N + n, p);
+  const PairOut o = project_pair<ACT>(means, covars, quats, scales, opacities, f, b * N + n, p);
+  if constexpr (ACT) {
+    if (opac_rows) opac_rows[pos] = sigmoid_of(opacities[b * N + n]);
+  }
   batch_ids[pos] = static_cast<int32_t>(b);
   camera_ids[pos] = static_cast<int32_t>(cam - b * C);
   gaussian_ids[pos] = static_cast<int32_t>(n);
@@ -476,14 +484,20 @@ extern "C" size_t gsplat_hip_projection_packed_workspace_size(int64_t B, int64_t
   return packed_layout(B, C, N, viewmats_grad != 0, nullptr, nullptr);
 }
 
-extern "C" int gsplat_hip_projection_packed_count(const float* means, const float* covars, const float* quats,
-                                                  const float* scales, const float* opacities, const float* viewmats,
-                                                  const float* Ks, int64_t B, int64_t C, int64_t N,
-                                                  const gsplat_projection_params* params, int64_t* nnz_dev,
-                                                  void* workspace, size_t workspace_bytes, void* stream) {
-  const std::string op("projection_ewa_3dgs_packed_forward");
+// The packed passes of the operator (ACT false) and of the activated
+// projection (ACT true: quats, scales, opacities hold raw quaternions,
+// log-scales and opacity logits; the forward also writes the per-row sigmoid
+// opacities, the backward reads the count pass's rank structure from
+// rank_ws instead of rebuilding it from the ids, and its opacity cotangent
+// is per row).
+template <bool ACT>
+int packed_count_impl(const std::string& op, const float* means, const float* covars, const float* quats,
+                      const float* scales, const float* opacities, const float* viewmats, const float* Ks, int64_t B,
+                      int64_t C, int64_t N, const gsplat_projection_params* params, int64_t* nnz_dev,
+                      void* workspace, size_t workspace_bytes, void* stream) {
   int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
   if (rc) return rc;
+  if (ACT && params->use_covars) return invalid(op + " takes quats and log_scales, not covars.");
   if (!nnz_dev) return invalid(op + ": null count.");
   hipStream_t s = as_stream(stream);
   if (B * C * N == 0) return fill_zero(nnz_dev, sizeof(int64_t), s);
@@ -496,11 +510,131 @@ extern "C" int gsplat_hip_projection_packed_count(const float* means, const floa
   const int64_t total = B * C * N;
   {
     KernelTimer timer("projection_packed_count", s);
-    projection_packed_mask_kernel<<<grid_for(total, kProjBlock), kProjBlock, 0, s>>>(
+    projection_packed_mask_kernel<ACT><<<grid_for(total, kProjBlock), kProjBlock, 0, s>>>(
         means, covars, quats, scales, opacities, viewmats, Ks, C, N, total, *params, l.mask, l.prefix);
   }
   if ((rc = check_launch(op.c_str()))) return rc;
   return scan_exclusive_i32(l.prefix, l.prefix, l.n_words, nnz_dev, l.scan_ws, s);
+}
+
+template <bool ACT>
+int packed_fwd_impl(const std::string& op, const float* means, const float* covars, const float* quats,
+                    const float* scales, const float* opacities, const float* viewmats, const float* Ks, int64_t B,
+                    int64_t C, int64_t N, const gsplat_projection_params* params, int64_t nnz, int32_t* batch_ids,
+                    int32_t* camera_ids, int32_t* gaussian_ids, int32_t* indptr, int32_t* radii, float* means2d,
+                    float* depths, float* conics, float* compensations, float* opac_rows, const void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
+  if (rc) return rc;
+  if (ACT && params->use_covars) return invalid(op + " takes quats and log_scales, not covars.");
+  if (nnz < 0) return invalid(op + ": negative nnz.");
+  hipStream_t s = as_stream(stream);
+  const int64_t total = B * C * N;
+  if (!indptr) return invalid(op + ": null indptr.");
+  if (total == 0) return fill_zero(indptr, (B * C + 1) * sizeof(int32_t), s);
+  if (nnz > 0 && (!batch_ids || !camera_ids || !gaussian_ids || !radii || !means2d || !depths || !conics))
+    return invalid(op + ": null pointer.");
+  if (nnz > 0 && params->calc_compensations && !compensations) return invalid(op + ": null compensations.");
+  if (params->use_opacities && !opacities) return invalid(op + ": null opacities.");
+  if (ACT && nnz > 0 && opac_rows && !opacities) return invalid(op + ": opacities out without opacity logits.");
+  PackedLayout l;
+  if (!workspace || workspace_bytes < packed_layout(B, C, N, false, &l, const_cast<void*>(workspace))) {
+    set_error(op + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  {
+    KernelTimer timer("projection_packed_fwd", s);
+    if (nnz > 0)
+      projection_packed_write_kernel<ACT><<<grid_for(total, kProjBlock), kProjBlock, 0, s>>>(
+          means, covars, quats, scales, opacities, viewmats, Ks, C, N, total, *params, l.mask, l.prefix, nnz,
+          batch_ids, camera_ids, gaussian_ids, radii, means2d, depths, conics,
+          params->calc_compensations ? compensations : nullptr, ACT ? opac_rows : nullptr);
+    projection_packed_indptr_kernel<<<grid_for(B * C + 1, 256), 256, 0, s>>>(l.mask, l.prefix, B * C, N, nnz,
+                                                                             indptr);
+  }
+  return check_launch(op.c_str());
+}
+
+template <bool ACT>
+int packed_bwd_impl(const std::string& op, const float* means, const float* covars, const float* quats,
+                    const float* scales, const float* viewmats, const float* Ks, int64_t B, int64_t C, int64_t N,
+                    const gsplat_projection_params* params, int64_t nnz, const int32_t* batch_ids,
+                    const int32_t* camera_ids, const int32_t* gaussian_ids, const void* rank_ws,
+                    size_t rank_ws_bytes, const float* conics, const float* compensations, const float* v_means2d,
+                    const float* v_depths, const float* v_conics, const float* v_compensations,
+                    const float* logits, const float* v_opac_rows, float* v_means, float* v_covars, float* v_quats,
+                    float* v_scales, float* v_logits, float* v_viewmats, void* workspace, size_t workspace_bytes,
+                    void* stream) {
+  int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
+  if (rc) return rc;
+  const gsplat_projection_params& p = *params;
+  if (ACT && p.use_covars) return invalid(op + " takes quats and log_scales, not covars.");
+  if (p.camera_model < 0 || p.camera_model > 2) return invalid(op + ": unknown camera model.");
+  if (nnz < 0) return invalid(op + ": negative nnz.");
+  hipStream_t s = as_stream(stream);
+  if (B * N == 0) {
+    if (v_viewmats && B * C > 0) return fill_zero(v_viewmats, B * C * 16 * sizeof(float), s);
+    return GSPLAT_OK;
+  }
+  if (!v_means || (p.use_covars ? !v_covars : (!v_quats || !v_scales))) return invalid(op + ": null pointer.");
+  if (nnz > 0 && (!conics || !v_means2d || !v_conics)) return invalid(op + ": null pointer.");
+  if (!ACT && nnz > 0 && (!camera_ids || !gaussian_ids)) return invalid(op + ": null pointer.");
+  if (!ACT && nnz > 0 && B > 1 && !batch_ids) return invalid(op + ": null batch_ids with more than one batch.");
+  if (v_compensations && !compensations) return invalid(op + ": v_compensations without compensations.");
+  if (ACT && v_logits && !logits) return invalid(op + ": v_opacity_logits without opacity logits.");
+  if (B > 65535) return invalid(op + ": batch exceeds 65535.");
+  PackedLayout l;
+  if (!workspace || workspace_bytes < packed_layout(B, C, N, v_viewmats != nullptr, &l, workspace)) {
+    set_error(op + ": workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  const uint64_t* mask = l.mask;
+  const int32_t* prefix = l.prefix;
+  if constexpr (ACT) {  // the count pass's rank structure
+    PackedLayout r;
+    if (!rank_ws || rank_ws_bytes < packed_layout(B, C, N, false, &r, const_cast<void*>(rank_ws))) {
+      set_error(op + ": count workspace too small.");
+      return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+    }
+    mask = r.mask;
+    prefix = r.prefix;
+  }
+  const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B));
+  if constexpr (!ACT) {
+    {
+      KernelTimer timer("projection_packed_bwd", s);
+      if ((rc = fill_zero(l.mask, static_cast<size_t>(l.n_words) * 8, s))) return rc;
+      if (nnz > 0)
+        projection_packed_scatter_kernel<<<grid_for(nnz, 256), 256, 0, s>>>(batch_ids, camera_ids, gaussian_ids,
+                                                                             nnz, B, C, N, l.mask);
+      popcount_words_kernel<<<grid_for(l.n_words, 256), 256, 0, s>>>(l.mask, l.n_words, l.prefix);
+    }
+    if ((rc = check_launch(op.c_str()))) return rc;
+    if ((rc = scan_exclusive_i32(l.prefix, l.prefix, l.n_words, nullptr, l.scan_ws, s))) return rc;
+  }
+  {
+    KernelTimer timer("projection_packed_bwd", s);
+    launch_projection_bwd(ACT, grid, s, means, covars, quats, scales, viewmats, Ks, C, N, p, nullptr, conics,
+                          compensations, v_means2d, v_depths, v_conics, v_compensations, v_means, v_covars, v_quats,
+                          v_scales, v_viewmats ? l.partials : nullptr, ACT ? logits : nullptr, nullptr,
+                          ACT ? v_logits : nullptr, mask, prefix, ACT ? v_opac_rows : nullptr);
+  }
+  if ((rc = check_launch(op.c_str())) || !v_viewmats) return rc;
+  {
+    KernelTimer timer("projection_bwd_viewmats", s);
+    viewmat_reduce_kernel<<<static_cast<unsigned>(B * C), 256, 0, s>>>(l.partials, static_cast<int>(grid.x),
+                                                                       v_viewmats);
+  }
+  return check_launch(op.c_str());
+}
+
+extern "C" int gsplat_hip_projection_packed_count(const float* means, const float* covars, const float* quats,
+                                                  const float* scales, const float* opacities, const float* viewmats,
+                                                  const float* Ks, int64_t B, int64_t C, int64_t N,
+                                                  const gsplat_projection_params* params, int64_t* nnz_dev,
+                                                  void* workspace, size_t workspace_bytes, void* stream) {
+  return packed_count_impl<false>("projection_ewa_3dgs_packed_forward", means, covars, quats, scales, opacities,
+                                  viewmats, Ks, B, C, N, params, nnz_dev, workspace, workspace_bytes, stream);
 }
 
 extern "C" int gsplat_hip_projection_packed_fwd(const float* means, const float* covars, const float* quats,
@@ -511,34 +645,10 @@ extern "C" int gsplat_hip_projection_packed_fwd(const float* means, const float*
                                                 int32_t* indptr, int32_t* radii, float* means2d, float* depths,
                                                 float* conics, float* compensations, const void* workspace,
                                                 size_t workspace_bytes, void* stream) {
-  const std::string op("projection_ewa_3dgs_packed_forward");
-  int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
-  if (rc) return rc;
-  if (nnz < 0) return invalid(op + ": negative nnz.");
-  hipStream_t s = as_stream(stream);
-  const int64_t total = B * C * N;
-  if (!indptr) return invalid(op + ": null indptr.");
-  if (total == 0) return fill_zero(indptr, (B * C + 1) * sizeof(int32_t), s);
-  if (nnz > 0 && (!batch_ids || !camera_ids || !gaussian_ids || !radii || !means2d || !depths || !conics))
-    return invalid(op + ": null pointer.");
-  if (nnz > 0 && params->calc_compensations && !compensations) return invalid(op + ": null compensations.");
-  if (params->use_opacities && !opacities) return invalid(op + ": null opacities.");
-  PackedLayout l;
-  if (!workspace || workspace_bytes < packed_layout(B, C, N, false, &l, const_cast<void*>(workspace))) {
-    set_error(op + ": workspace too small.");
-    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
-  }
-  {
-    KernelTimer timer("projection_packed_fwd", s);
-    if (nnz > 0)
-      projection_packed_write_kernel<<<grid_for(total, kProjBlock), kProjBlock, 0, s>>>(
-          means, covars, quats, scales, opacities, viewmats, Ks, C, N, total, *params, l.mask, l.prefix, nnz,
-          batch_ids, camera_ids, gaussian_ids, radii, means2d, depths, conics,
-          params->calc_compensations ? compensations : nullptr);
-    projection_packed_indptr_kernel<<<grid_for(B * C + 1, 256), 256, 0, s>>>(l.mask, l.prefix, B * C, N, nnz,
-                                                                             indptr);
-  }
-  return check_launch(op.c_str());
+  return packed_fwd_impl<false>("projection_ewa_3dgs_packed_forward", means, covars, quats, scales, opacities,
+                                viewmats, Ks, B, C, N, params, nnz, batch_ids, camera_ids, gaussian_ids, indptr,
+                                radii, means2d, depths, conics, compensations, nullptr, workspace, workspace_bytes,
+                                stream);
 }
 
 extern "C" int gsplat_hip_projection_packed_bwd(const float* means, const float* covars, const float* quats,
@@ -552,52 +662,48 @@ extern "C" int gsplat_hip_projection_packed_bwd(const float* means, const float*
                                                 const float* v_compensations, float* v_means, float* v_covars,
                                                 float* v_quats, float* v_scales, float* v_viewmats, void* workspace,
                                                 size_t workspace_bytes, void* stream) {
-  const std::string op("projection_ewa_3dgs_packed_backward");
-  int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
-  if (rc) return rc;
-  const gsplat_projection_params& p = *params;
-  if (p.camera_model < 0 || p.camera_model > 2) return invalid(op + ": unknown camera model.");
-  if (nnz < 0) return invalid(op + ": negative nnz.");
-  hipStream_t s = as_stream(stream);
-  if (B * N == 0) {
-    if (v_viewmats && B * C > 0) return fill_zero(v_viewmats, B * C * 16 * sizeof(float), s);
-    return GSPLAT_OK;
-  }
-  if (!v_means || (p.use_covars ? !v_covars : (!v_quats || !v_scales))) return invalid(op + ": null pointer.");
-  if (nnz > 0 && (!camera_ids || !gaussian_ids || !conics || !v_means2d || !v_conics))
-    return invalid(op + ": null pointer.");
-  if (nnz > 0 && B > 1 && !batch_ids) return invalid(op + ": null batch_ids with more than one batch.");
-  if (v_compensations && !compensations) return invalid(op + ": v_compensations without compensations.");
-  if (B > 65535) return invalid(op + ": batch exceeds 65535.");
-  PackedLayout l;
-  if (!workspace || workspace_bytes < packed_layout(B, C, N, v_viewmats != nullptr, &l, workspace)) {
-    set_error(op + ": workspace too small.");
-    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
-  }
-  const dim3 grid(grid_for(N, kProjBlock), static_cast<unsigned>(B));
-  {
-    KernelTimer timer("projection_packed_bwd", s);
-    if ((rc = fill_zero(l.mask, static_cast<size_t>(l.n_words) * 8, s))) return rc;
-    if (nnz > 0)
-      projection_packed_scatter_kernel<<<grid_for(nnz, 256), 256, 0, s>>>(batch_ids, camera_ids, gaussian_ids, nnz,
-                                                                           B, C, N, l.mask);
-    popcount_words_kernel<<<grid_for(l.n_words, 256), 256, 0, s>>>(l.mask, l.n_words, l.prefix);
-  }
-  if ((rc = check_launch(op.c_str()))) return rc;
-  if ((rc = scan_exclusive_i32(l.prefix, l.prefix, l.n_words, nullptr, l.scan_ws, s))) return rc;
-  {
-    KernelTimer timer("projection_packed_bwd", s);
-    launch_projection_bwd(false, grid, s, means, covars, quats, scales, viewmats, Ks, C, N, p, nullptr, conics,
-                          compensations, v_means2d, v_depths, v_conics, v_compensations, v_means, v_covars, v_quats,
-                          v_scales, v_viewmats ? l.partials : nullptr, nullptr, nullptr, nullptr, l.mask, l.prefix);
-  }
-  if ((rc = check_launch(op.c_str())) || !v_viewmats) return rc;
-  {
-    KernelTimer timer("projection_bwd_viewmats", s);
-    viewmat_reduce_kernel<<<static_cast<unsigned>(B * C), 256, 0, s>>>(l.partials, static_cast<int>(grid.x),
-                                                                       v_viewmats);
-  }
-  return check_launch(op.c_str());
+  return packed_bwd_impl<false>("projection_ewa_3dgs_packed_backward", means, covars, quats, scales, viewmats, Ks, B,
+                                C, N, params, nnz, batch_ids, camera_ids, gaussian_ids, nullptr, 0, conics,
+                                compensations, v_means2d, v_depths, v_conics, v_compensations, nullptr, nullptr,
+                                v_means, v_covars, v_quats, v_scales, nullptr, v_viewmats, workspace,
+                                workspace_bytes, stream);
+}
+
+extern "C" int gsplat_hip_activated_projection_packed_count(const float* means, const float* quats,
+                                                            const float* log_scales, const float* opacity_logits,
+                                                            const float* viewmats, const float* Ks, int64_t B,
+                                                            int64_t C, int64_t N,
+                                                            const gsplat_projection_params* params, int64_t* nnz_dev,
+                                                            void* workspace, size_t workspace_bytes, void* stream) {
+  return packed_count_impl<true>("activated_projection_packed_forward", means, nullptr, quats, log_scales,
+                                 opacity_logits, viewmats, Ks, B, C, N, params, nnz_dev, workspace, workspace_bytes,
+                                 stream);
+}
+
+extern "C" int gsplat_hip_activated_projection_packed_fwd(
+    const float* means, const float* quats, const float* log_scales, const float* opacity_logits,
+    const float* viewmats, const float* Ks, int64_t B, int64_t C, int64_t N, const gsplat_projection_params* params,
+    int64_t nnz, int32_t* batch_ids, int32_t* camera_ids, int32_t* gaussian_ids, int32_t* indptr, int32_t* radii,
+    float* means2d, float* depths, float* conics, float* compensations, float* opacities, const void* workspace,
+    size_t workspace_bytes, void* stream) {
+  return packed_fwd_impl<true>("activated_projection_packed_forward", means, nullptr, quats, log_scales,
+                               opacity_logits, viewmats, Ks, B, C, N, params, nnz, batch_ids, camera_ids,
+                               gaussian_ids, indptr, radii, means2d, depths, conics, compensations, opacities,
+                               workspace, workspace_bytes, stream);
+}
+
+extern "C" int gsplat_hip_activated_projection_packed_bwd(
+    const float* means, const float* quats, const float* log_scales, const float* opacity_logits,
+    const float* viewmats, const float* Ks, int64_t B, int64_t C, int64_t N, const gsplat_projection_params* params,
+    int64_t nnz, const void* count_workspace, size_t count_workspace_bytes, const float* conics,
+    const float* compensations, const float* v_means2d, const float* v_depths, const float* v_conics,
+    const float* v_compensations, const float* v_opacities, float* v_means, float* v_quats, float* v_log_scales,
+    float* v_opacity_logits, float* v_viewmats, void* workspace, size_t workspace_bytes, void* stream) {
+  return packed_bwd_impl<true>("activated_projection_packed_backward", means, nullptr, quats, log_scales, viewmats,
+                               Ks, B, C, N, params, nnz, nullptr, nullptr, nullptr, count_workspace,
+                               count_workspace_bytes, conics, compensations, v_means2d, v_depths, v_conics,
+                               v_compensations, opacity_logits, v_opacities, v_means, nullptr, v_quats, v_log_scales,
+                               v_opacity_logits, v_viewmats, workspace, workspace_bytes, stream);
 }
 
 extern "C" int gsplat_hip_activated_projection_fwd(const float* means, const float* quats, const float* log_scales,

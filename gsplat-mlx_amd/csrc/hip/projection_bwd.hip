@@ -259,7 +259,9 @@ __device__ __forceinline__ void block_sum12_store(float vals[12], float* __restr
 
 // ACT: quats / scales hold quaternions / log-scales (raw), v_quats / v_scales
 // receive their gradients, and v_logits (if non-null) = v_opac * o (1 - o)
-// with o = sigmoid(logits) (v_opac null: zeros).
+// with o = sigmoid(logits) (v_opac null: zeros). With v_opac_rows (packed
+// layout) the opacity cotangent is per visible pair instead: its sum over
+// the Gaussian's pairs (in camera order) takes v_opac's place.
 template <bool ACT>
 __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
@@ -270,7 +272,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     const float* __restrict__ v_compensations, float* __restrict__ v_means, float* __restrict__ v_covars,
     float* __restrict__ v_quats, float* __restrict__ v_scales, float* __restrict__ vm_partials,
     const float* __restrict__ logits, const float* __restrict__ v_opac, float* __restrict__ v_logits,
-    const uint64_t* __restrict__ pmask, const int32_t* __restrict__ pprefix) {
+    const uint64_t* __restrict__ pmask, const int32_t* __restrict__ pprefix, const float* __restrict__ v_opac_rows) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
   const int64_t b = blockIdx.y;
   const bool in_range = n < N;
@@ -296,6 +298,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
   }
 
   float v_mw_total[3] = {0.0f, 0.0f, 0.0f};
+  float v_opac_sum = 0.0f;  // v_opac_rows over the Gaussian's pairs
   Mat3 v_cw_total;
 #pragma unroll
   for (int i = 0; i < 9; ++i) v_cw_total.v[i] = 0.0f;
@@ -321,6 +324,9 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
 #pragma unroll
     for (int i = 0; i < 12; ++i) vm_part[i] = 0.0f;
     if (valid) {
+      if constexpr (ACT) {
+        if (v_opac_rows) v_opac_sum += v_opac_rows[idx];
+      }
       const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
       const float cn[3] = {conics[idx * 3], conics[idx * 3 + 1], conics[idx * 3 + 2]};
       const float vc[3] = {v_conics[idx * 3], v_conics[idx * 3 + 1], v_conics[idx * 3 + 2]};
@@ -392,7 +398,10 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
       for (int i = 0; i < 3; ++i) vs[i] = vs[i] * s[i];  // d exp(x) / dx = exp(x)
       if (v_logits) {
         const float o = sigmoid_of(logits[g]);
-        v_logits[g] = v_opac ? (v_opac[g] * (1.0f - o)) * o : 0.0f;
+        if (v_opac_rows)
+          v_logits[g] = (v_opac_sum * (1.0f - o)) * o;
+        else
+          v_logits[g] = v_opac ? (v_opac[g] * (1.0f - o)) * o : 0.0f;
       }
     }
 #pragma unroll
@@ -411,18 +420,19 @@ void launch_projection_bwd(bool act, dim3 grid, hipStream_t s, const float* mean
                            const float* v_conics, const float* v_compensations, float* v_means, float* v_covars,
                            float* v_quats, float* v_scales, float* vm_partials, const float* logits,
                            const float* v_opac, float* v_logits, const uint64_t* pmask,
-                           const int32_t* pprefix) {
+                           const int32_t* pprefix, const float* v_opac_rows) {
   if (act)
     projection_bwd_kernel<true><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p, radii,
                                                             conics, compensations, v_means2d, v_depths, v_conics,
                                                             v_compensations, v_means, v_covars, v_quats, v_scales,
-                                                            vm_partials, logits, v_opac, v_logits, pmask, pprefix);
+                                                            vm_partials, logits, v_opac, v_logits, pmask, pprefix,
+                                                            v_opac_rows);
   else
     projection_bwd_kernel<false><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p,
                                                              radii, conics, compensations, v_means2d, v_depths,
                                                              v_conics, v_compensations, v_means, v_covars, v_quats,
                                                              v_scales, vm_partials, nullptr, nullptr, nullptr, pmask,
-                                                             pprefix);
+                                                             pprefix, nullptr);
 }
 
 }  // namespace gsplat_hip

@@ -20,6 +20,7 @@ except ImportError as exc:  # pragma: no cover - exercised only on broken instal
 
 from .autograd import (  # noqa: E402,F401
     activated_projection,
+    activated_projection_packed,
     gaussian_activations,
     image_loss,
     l1_loss,
@@ -54,6 +55,8 @@ __all__ = [
     "gaussian_activations_backward",
     "activated_projection_forward",
     "activated_projection_backward",
+    "activated_projection_packed_forward",
+    "activated_projection_packed_backward",
     "l1_loss_forward",
     "l1_loss_backward",
     "image_loss_forward",
@@ -63,6 +66,7 @@ __all__ = [
     "rasterize_to_indices_3dgs_forward",
     "selective_adam_update",
     "activated_projection",
+    "activated_projection_packed",
     "gaussian_activations",
     "image_loss",
     "l1_loss",

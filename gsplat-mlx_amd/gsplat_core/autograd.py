@@ -191,6 +191,73 @@ def projection_packed(means, quats, scales, viewmats, Ks, image_width, image_hei
     return dict(zip(keys, out))
 
 
+class _ActivatedProjectionPacked(torch.autograd.Function):
+    """activated_projection_packed_forward / _backward: the packed projection
+    with the parameter activations fused in (raw quaternions, log-scales,
+    opacity logits), plus each visible pair's sigmoid opacity. The backward
+    reads the forward's rank structure (no ids) and takes the opacities'
+    cotangent per row."""
+
+    @staticmethod
+    def forward(ctx, means, quats, log_scales, opacity_logits, viewmats, Ks, image_width, image_height, eps2d,
+                near_plane, far_plane, radius_clip, calc_compensations, camera_model):
+        ctx.set_materialize_grads(False)
+        inputs = {"means": means, "quats": quats, "log_scales": log_scales, "viewmats": viewmats, "Ks": Ks}
+        if _nonempty(opacity_logits):
+            inputs["opacity_logits"] = opacity_logits
+        out = _C.activated_projection_packed_forward(inputs, image_width, image_height, eps2d, near_plane,
+                                                     far_plane, radius_clip, calc_compensations, camera_model)
+        ctx.save_for_backward(means, quats, log_scales, opacity_logits, viewmats, Ks, out["conics"],
+                              out["compensations"], out["rank"])
+        ctx.params = (image_width, image_height, eps2d, calc_compensations, camera_model)
+        for k in ("batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii"):
+            ctx.mark_non_differentiable(out[k])
+        return (out["batch_ids"], out["camera_ids"], out["gaussian_ids"], out["indptr"], out["radii"],
+                out["means2d"], out["depths"], out["conics"], out["compensations"], out["opacities"])
+
+    @staticmethod
+    def backward(ctx, _b, _c, _g, _i, _r, v_means2d, v_depths, v_conics, v_compensations, v_opacities):
+        means, quats, log_scales, logits, viewmats, Ks, conics, comps, rank = ctx.saved_tensors
+        W, H, eps2d, calc_comp, camera_model = ctx.params
+        nnz = conics.shape[0]
+        v_means2d = means.new_zeros((nnz, 2)) if v_means2d is None else v_means2d.contiguous()
+        v_conics = means.new_zeros((nnz, 3)) if v_conics is None else v_conics.contiguous()
+        inputs = {"means": means, "quats": quats, "log_scales": log_scales, "viewmats": viewmats, "Ks": Ks}
+        if _nonempty(logits):
+            inputs["opacity_logits"] = logits
+        fwd = {"conics": conics, "rank": rank}
+        cot = {"v_means2d": v_means2d, "v_conics": v_conics}
+        if v_depths is not None:
+            cot["v_depths"] = v_depths.contiguous()
+        if calc_comp:
+            fwd["compensations"] = comps
+            cot["v_compensations"] = torch.zeros_like(comps) if v_compensations is None else v_compensations.contiguous()
+        if v_opacities is not None:
+            cot["v_opacities"] = v_opacities.contiguous()
+        needs_viewmats = ctx.needs_input_grad[4]
+        out = _C.activated_projection_packed_backward(inputs, fwd, cot, W, H, eps2d, camera_model, needs_viewmats)
+        g_logits = out["v_opacity_logits"] if ctx.needs_input_grad[3] else None
+        return (out["v_means"], out["v_quats"], out["v_log_scales"], g_logits,
+                out["v_viewmats"] if needs_viewmats else None) + (None,) * 9
+
+
+def activated_projection_packed(means, quats, log_scales, opacity_logits, viewmats, Ks, image_width, image_height,
+                                eps2d=0.3, near_plane=0.01, far_plane=1e10, radius_clip=0.0, calc_compensations=False,
+                                camera_model=0):
+    """gaussian_activations followed by projection_packed, in the packed
+    projection's kernels: a dict of the visible pairs' rows as
+    projection_packed's plus "opacities", each row's sigmoid opacity (the
+    rasterizer's), differentiable w.r.t. means, the raw parameters and
+    viewmats."""
+    keys = ("batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii", "means2d", "depths", "conics",
+            "compensations", "opacities")
+    out = _ActivatedProjectionPacked.apply(means, quats, log_scales,
+                                           opacity_logits if opacity_logits is not None else _empty(means), viewmats,
+                                           Ks, image_width, image_height, eps2d, near_plane, far_plane, radius_clip,
+                                           calc_compensations, camera_model)
+    return dict(zip(keys, out))
+
+
 class _PackedViewspace(torch.autograd.Function):
     """Identity on the packed means2d whose backward also scatters their
     gradient into a dense viewspace_points [1, C, N, 2] proxy (the packed

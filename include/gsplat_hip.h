@@ -691,6 +691,47 @@ int gsplat_hip_activated_projection_bwd(const float* means, const float* quats,
                                         float* v_opacity_logits, float* v_viewmats, void* workspace,
                                         size_t workspace_bytes, void* stream);
 
+/* Activated packed projection (no reference counterpart): the activations
+ * fused into the packed projection (gsplat_hip_projection_packed_count /
+ * _fwd / _bwd), for the packed training step of a model with raw
+ * parameters. Inputs as gsplat_hip_activated_projection_fwd; the count and
+ * forward take the workspace of gsplat_hip_projection_packed_workspace_size(
+ * B, C, N, 0) and give the same rows as gsplat_hip_gaussian_activations_fwd
+ * followed by the packed projection, bit for bit, plus opacities [nnz] (when
+ * non-NULL; needs opacity_logits), each visible pair's sigmoid opacity. The
+ * caller keeps the count's workspace for the backward (count_workspace): it
+ * holds the rank structure that maps a pair to its row, so the backward takes
+ * no ids. The backward's cotangents are per row, v_opacities [nnz] included
+ * (NULL: zeros; it is summed over a Gaussian's pairs in camera order), and it
+ * writes the raw parameters' gradients as gsplat_hip_activated_projection_bwd,
+ * with its own workspace of gsplat_hip_projection_packed_workspace_size(B, C,
+ * N, v_viewmats != NULL). */
+int gsplat_hip_activated_projection_packed_count(const float* means, const float* quats,
+                                                 const float* log_scales, const float* opacity_logits,
+                                                 const float* viewmats, const float* Ks, int64_t B,
+                                                 int64_t C, int64_t N, const gsplat_projection_params* params,
+                                                 int64_t* nnz_dev, void* workspace, size_t workspace_bytes,
+                                                 void* stream);
+int gsplat_hip_activated_projection_packed_fwd(const float* means, const float* quats,
+                                               const float* log_scales, const float* opacity_logits,
+                                               const float* viewmats, const float* Ks, int64_t B, int64_t C,
+                                               int64_t N, const gsplat_projection_params* params, int64_t nnz,
+                                               int32_t* batch_ids, int32_t* camera_ids, int32_t* gaussian_ids,
+                                               int32_t* indptr, int32_t* radii, float* means2d, float* depths,
+                                               float* conics, float* compensations, float* opacities,
+                                               const void* workspace, size_t workspace_bytes, void* stream);
+int gsplat_hip_activated_projection_packed_bwd(const float* means, const float* quats,
+                                               const float* log_scales, const float* opacity_logits,
+                                               const float* viewmats, const float* Ks, int64_t B, int64_t C,
+                                               int64_t N, const gsplat_projection_params* params, int64_t nnz,
+                                               const void* count_workspace, size_t count_workspace_bytes,
+                                               const float* conics, const float* compensations,
+                                               const float* v_means2d, const float* v_depths,
+                                               const float* v_conics, const float* v_compensations,
+                                               const float* v_opacities, float* v_means, float* v_quats,
+                                               float* v_log_scales, float* v_opacity_logits, float* v_viewmats,
+                                               void* workspace, size_t workspace_bytes, void* stream);
+
 /* Image L1 term mean(|a - b|) over n values into the device scalar *loss
  * (nn.losses.l1_loss in image_loss_components,
  * scanner_points_training_utils.py:1147-1160). The backward reads the device scalar cotangent

@@ -92,6 +92,64 @@ def test_projection_packed_equals_dense(oracle, B, C, N, opac, comp):
         np.testing.assert_array_equal(host(bp[k]), host(bd[k]), err_msg=k)
 
 
+@pytest.mark.parametrize("B,C,N,logits,viewgrad", [(1, 1, 2000, True, False), (1, 3, 3001, True, True),
+                                                     (2, 2, 777, True, True), (1, 2, 500, False, False)])
+def test_activated_projection_packed(B, C, N, logits, viewgrad):
+    """The activated packed projection (activations in the packed kernels,
+    per-row opacities, the backward reading the forward's rank structure)
+    against its composition from the separate operators: gaussian_activations,
+    projection_packed and a gather of the opacities by Gaussian id. Rows and
+    opacities bit for bit; gradients w.r.t. means, raw quaternions,
+    log-scales, opacity logits and view matrices within 1e-4 relative (the
+    opacity gradient sums a Gaussian's rows in another order)."""
+    import torch
+
+    from gsplat_core.autograd import activated_projection_packed, gaussian_activations, projection_packed
+
+    rng = np.random.default_rng(N + C)
+    means, quats, scales, op, view, Ks = _scene(rng, B, C, N)
+    log_scales = np.log(scales).astype(np.float32)
+    lg = rng.normal(size=(B, N)).astype(np.float32)
+    print(f"activated packed projection B={B} C={C} N={N} logits={logits} viewgrad={viewgrad}", flush=True)
+
+    def run(fused):
+        m, q, ls, vm = (dev(a).requires_grad_(True) for a in (means, quats, log_scales, view))
+        lo = dev(lg).requires_grad_(True) if logits else None
+        K = dev(Ks)
+        if fused:
+            out = activated_projection_packed(m, q, ls, lo, vm if viewgrad else vm.detach(), K, 320, 240)
+        else:
+            qa, sa, oa = gaussian_activations(q, ls, lo if logits else torch.zeros((B, N), device="cuda"))
+            out = projection_packed(m, qa, sa, vm if viewgrad else vm.detach(), K, 320, 240)
+            if logits:
+                out["opacities"] = oa.reshape(-1).index_select(0, (out["batch_ids"].long() * N +
+                                                                   out["gaussian_ids"].long()))
+        g = torch.Generator(device="cuda").manual_seed(7)
+        loss = 0
+        for k in ("means2d", "depths", "conics") + (("opacities",) if logits else ()):
+            loss = loss + (out[k] * torch.randn(out[k].shape, device="cuda", generator=g)).sum()
+        loss.backward()
+        torch.cuda.synchronize()
+        res = {k: host(v) for k, v in out.items() if k != "compensations"}
+        res.update({"v_means": host(m.grad), "v_quats": host(q.grad), "v_log_scales": host(ls.grad)})
+        if logits:
+            res["v_logits"] = host(lo.grad)
+        if viewgrad:
+            res["v_viewmats"] = host(vm.grad)
+        return res
+
+    a, b = run(True), run(False)
+    assert a["means2d"].shape[0] > 0
+    if not logits:
+        assert a.pop("opacities").size == 0
+    for k in a:
+        if k.startswith("v_"):
+            assert np.abs(b[k]).max() > 0, k
+            assert_close_rel_summation(a[k], b[k], 1e-4, k)
+        else:
+            np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+
+
 def _packed_image_ids(rng, layout, I, nnz):
     """Row image ids: grouped by image (the packed projection's order), grouped
     with empty images (first, inner and last), or not grouped (the sorted
