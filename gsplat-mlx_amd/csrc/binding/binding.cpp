@@ -436,7 +436,8 @@ py::dict activated_projection_packed_forward(const TensorMap& inputs, int image_
 // (v_depths, v_compensations, v_opacities optional).
 py::dict activated_projection_packed_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
                                               const TensorMap& cotangents, int image_width, int image_height,
-                                              float eps2d, int camera_model, bool viewmats_requires_grad) {
+                                              float eps2d, int camera_model, bool viewmats_requires_grad,
+                                              bool viewspace_requires_grad) {
   gsplat_core::ProjectionEWA3DGSPackedBackwardInput in;
   in.means = require_key(inputs, "means");
   in.viewmats = require_key(inputs, "viewmats");
@@ -454,14 +455,27 @@ py::dict activated_projection_packed_backward(const TensorMap& inputs, const Ten
   in.viewmats_requires_grad = viewmats_requires_grad;
   auto out = gsplat_core::gsplat_activated_projection_packed_backward(
       in, require_key(forward_outputs, "rank"), get_or_empty(inputs, "opacity_logits"),
-      get_or_empty(cotangents, "v_opacities"));
+      get_or_empty(cotangents, "v_opacities"), viewspace_requires_grad);
   py::dict r;
   r["v_means"] = out[0];
   r["v_quats"] = out[1];
   r["v_log_scales"] = out[2];
   r["v_opacity_logits"] = out[3];
   if (viewmats_requires_grad) r["v_viewmats"] = out[4];
+  if (viewspace_requires_grad) r["v_viewspace"] = out[5];
   return r;
+}
+
+// Packed rows of dense [B, C, N, K] values (batch_ids optional with B = 1).
+at::Tensor packed_rows_gather(const at::Tensor& dense, const TensorMap& ids) {
+  return gsplat_core::gsplat_packed_rows_gather(dense, get_or_empty(ids, "batch_ids"), require_key(ids, "camera_ids"),
+                                                require_key(ids, "gaussian_ids"));
+}
+
+// The adjoint: rows at their slots of a dense [B, C, N, K] array, zeros
+// elsewhere (rank: the activated packed forward's).
+at::Tensor packed_rows_scatter(const at::Tensor& rows, const at::Tensor& rank, int64_t B, int64_t C, int64_t N) {
+  return gsplat_core::gsplat_packed_rows_scatter(rows, rank, B, C, N);
 }
 
 py::dict activated_projection_backward(const TensorMap& inputs, const TensorMap& forward_outputs,
@@ -662,7 +676,11 @@ PYBIND11_MODULE(_gsplat_core, m) {
         py::arg("camera_model") = 0, py::arg("opacities_in_projection") = false);
   m.def("activated_projection_packed_backward", &activated_projection_packed_backward, py::arg("inputs"),
         py::arg("forward_outputs"), py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"),
-        py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false);
+        py::arg("eps2d") = 0.3f, py::arg("camera_model") = 0, py::arg("viewmats_requires_grad") = false,
+        py::arg("viewspace_requires_grad") = false);
+  m.def("packed_rows_gather", &packed_rows_gather, py::arg("dense"), py::arg("ids"));
+  m.def("packed_rows_scatter", &packed_rows_scatter, py::arg("rows"), py::arg("rank"), py::arg("B"), py::arg("C"),
+        py::arg("N"));
   m.def("render_rgb_forward", &render_rgb_forward, py::arg("inputs"), py::arg("image_width"),
         py::arg("image_height"), py::arg("tile_size"), py::arg("eps2d") = 0.3f, py::arg("near_plane") = 0.01f,
         py::arg("far_plane") = 1.0e10f, py::arg("opacities_in_projection") = false, py::arg("accutile") = false);

@@ -5,6 +5,9 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <map>
+#include <vector>
+
 #include "core_util.h"
 #include "gsplat_training_glue.h"
 
@@ -394,6 +397,24 @@ std::vector<array> gsplat_projection_ewa_3dgs_packed_backward(const ProjectionEW
   return {v_means, v_covars, v_quats, v_scales, v_viewmats};
 }
 
+namespace {
+
+// Speculative packed forward: a call whose shape (device, B, C, N) was seen
+// before writes its rows into outputs sized by the previous count plus an
+// eighth, queued behind the count pass before the count reaches the host
+// (the kernels bound every write by that capacity and take indptr's total
+// from the device). The rows are then narrowed to the count; a count over
+// the capacity runs the forward again into exact outputs. Hints are per host
+// thread.
+int64_t& packed_hint(int64_t B, int64_t C, int64_t N) {
+  thread_local std::map<std::vector<int64_t>, int64_t> hints;
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  return hints[{dev, B, C, N}];
+}
+
+}  // namespace
+
 std::vector<array> gsplat_activated_projection_packed_forward(const ProjectionEWA3DGSFusedInput& input) {
   const char* op = "activated_projection_packed_forward";
   if (input.params.use_covars) throw std::runtime_error(std::string(op) + " takes quats and log_scales, not covars.");
@@ -429,28 +450,54 @@ std::vector<array> gsplat_activated_projection_packed_forward(const ProjectionEW
                                                      Ks.data_ptr<float>(), d.B, d.C, d.N, &cp,
                                                      count.data_ptr<int64_t>(), ws.data_ptr<uint8_t>(), ws_bytes,
                                                      stream));
-  const int64_t nnz = d.B * d.C * d.N > 0 ? read_count(count, stream) : 0;
   auto i32 = [&](std::vector<int64_t> shape) { return at::empty(shape, i32_like(means)); };
   auto f32 = [&](std::vector<int64_t> shape) { return at::empty(shape, f32_like(means)); };
-  array batch_ids = i32({nnz}), camera_ids = i32({nnz}), gaussian_ids = i32({nnz});
   array indptr = i32({d.B * d.C + 1});
-  array radii = i32({nnz, 2});
-  array means2d = f32({nnz, 2}), depths = f32({nnz}), conics = f32({nnz, 3});
-  array comps = p.calc_compensations ? f32({nnz}) : f32({0});
-  array opac = have_logits ? f32({nnz}) : f32({0});
-  check(gsplat_hip_activated_projection_packed_fwd(
-      means.data_ptr<float>(), quats.data_ptr<float>(), scales.data_ptr<float>(), l_p, viewmats.data_ptr<float>(),
-      Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, nnz, batch_ids.data_ptr<int32_t>(), camera_ids.data_ptr<int32_t>(),
-      gaussian_ids.data_ptr<int32_t>(), indptr.data_ptr<int32_t>(), radii.data_ptr<int32_t>(),
-      means2d.data_ptr<float>(), depths.data_ptr<float>(), conics.data_ptr<float>(),
-      p.calc_compensations ? comps.data_ptr<float>() : nullptr, have_logits ? opac.data_ptr<float>() : nullptr,
-      ws.data_ptr<uint8_t>(), ws_bytes, stream));
-  return {batch_ids, camera_ids, gaussian_ids, indptr, radii, means2d, depths, conics, comps, opac, ws};
+  // rows of `rows` capacity; nnz_dev: the count on the device (speculative)
+  auto run = [&](int64_t rows, const int64_t* nnz_dev) {
+    std::vector<array> o = {i32({rows}),    i32({rows}),    i32({rows}),
+                            indptr,         i32({rows, 2}), f32({rows, 2}),
+                            f32({rows}),    f32({rows, 3}), p.calc_compensations ? f32({rows}) : f32({0}),
+                            have_logits ? f32({rows}) : f32({0})};
+    check(gsplat_hip_activated_projection_packed_fwd(
+        means.data_ptr<float>(), quats.data_ptr<float>(), scales.data_ptr<float>(), l_p, viewmats.data_ptr<float>(),
+        Ks.data_ptr<float>(), d.B, d.C, d.N, &cp, rows, nnz_dev, o[0].data_ptr<int32_t>(), o[1].data_ptr<int32_t>(),
+        o[2].data_ptr<int32_t>(), indptr.data_ptr<int32_t>(), o[4].data_ptr<int32_t>(), o[5].data_ptr<float>(),
+        o[6].data_ptr<float>(), o[7].data_ptr<float>(), p.calc_compensations ? o[8].data_ptr<float>() : nullptr,
+        have_logits ? o[9].data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(), ws_bytes, stream));
+    return o;
+  };
+  if (d.B * d.C * d.N == 0) {
+    auto o = run(0, nullptr);
+    o.push_back(ws);
+    return o;
+  }
+  int64_t& hint = packed_hint(d.B, d.C, d.N);
+  std::vector<array> out;
+  int64_t nnz = -1;
+  if (hint > 0) {
+    const int64_t cap = std::min(d.B * d.C * d.N, hint + hint / 8 + 1024);
+    out = run(cap, count.data_ptr<int64_t>());
+    nnz = read_count(count, stream);
+    if (nnz <= cap) {
+      for (size_t i = 0; i < out.size(); ++i)
+        if (i != 3 && out[i].numel() > 0) out[i] = out[i].narrow(0, 0, nnz);
+    } else {
+      out.clear();
+    }
+  }
+  if (out.empty()) {
+    if (nnz < 0) nnz = read_count(count, stream);
+    out = run(nnz, nullptr);
+  }
+  hint = nnz;
+  out.push_back(ws);
+  return out;
 }
 
 std::vector<array> gsplat_activated_projection_packed_backward(const ProjectionEWA3DGSPackedBackwardInput& input,
                                                                const array& rank, const array& opacity_logits,
-                                                               const array& v_opacities) {
+                                                               const array& v_opacities, bool viewspace_grad) {
   const char* op = "activated_projection_packed_backward";
   if (input.params.use_covars) throw std::runtime_error(std::string(op) + " takes quats and log_scales, not covars.");
   ProjectionEWA3DGSFusedInput fwd;
@@ -509,6 +556,8 @@ std::vector<array> gsplat_activated_projection_packed_backward(const ProjectionE
   array v_logits = have_logits ? at::empty(logits.sizes(), f32_like(means)) : at::empty({0}, f32_like(means));
   array v_viewmats = input.viewmats_requires_grad ? at::empty(viewmats.sizes(), f32_like(means))
                                                   : at::empty({0}, f32_like(means));
+  array v_viewspace = viewspace_grad ? at::empty(projection_shape(means, viewmats, 2), f32_like(means))
+                                     : at::empty({0}, f32_like(means));
   const size_t ws_bytes =
       gsplat_hip_projection_packed_workspace_size(d.B, d.C, d.N, input.viewmats_requires_grad ? 1 : 0);
   array ws = at::empty({static_cast<int64_t>(ws_bytes > 0 ? ws_bytes : 1)}, u8_like(means));
@@ -522,9 +571,50 @@ std::vector<array> gsplat_activated_projection_packed_backward(const ProjectionE
       use_comp ? v_comps.data_ptr<float>() : nullptr, have_v_opac ? v_opac.data_ptr<float>() : nullptr,
       v_means.data_ptr<float>(), v_quats.data_ptr<float>(), v_scales.data_ptr<float>(),
       have_logits ? v_logits.data_ptr<float>() : nullptr,
-      input.viewmats_requires_grad ? v_viewmats.data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(), ws_bytes,
+      input.viewmats_requires_grad ? v_viewmats.data_ptr<float>() : nullptr,
+      viewspace_grad ? v_viewspace.data_ptr<float>() : nullptr, ws.data_ptr<uint8_t>(), ws_bytes,
       stream_for(input.s, means)));
-  return {v_means, v_quats, v_scales, v_logits, v_viewmats};
+  return {v_means, v_quats, v_scales, v_logits, v_viewmats, v_viewspace};
+}
+
+array gsplat_packed_rows_gather(const array& dense, const array& batch_ids, const array& camera_ids,
+                                const array& gaussian_ids, StreamOrDevice s) {
+  require_device(dense, "dense");
+  require_dtype(dense, at::kFloat, "packed_rows_gather expects float32 values.");
+  if (dense.dim() != 4) throw std::runtime_error("packed_rows_gather: dense must have shape [B, C, N, K].");
+  const int64_t B = dense.size(0), C = dense.size(1), N = dense.size(2), K = dense.size(3);
+  const int64_t nnz = camera_ids.numel();
+  if (gaussian_ids.numel() != nnz || (!is_empty(batch_ids) && batch_ids.numel() != nnz))
+    throw std::runtime_error("packed_rows_gather: ids must have nnz entries.");
+  if (B > 1 && is_empty(batch_ids)) throw std::runtime_error("packed_rows_gather: batch_ids needed with B > 1.");
+  const c10::DeviceGuard guard(dense.device());
+  const array d = contig(dense);
+  const array bid = is_empty(batch_ids) ? array() : ids32(batch_ids, "batch_ids");
+  const array cid = ids32(camera_ids, "camera_ids");
+  const array gid = ids32(gaussian_ids, "gaussian_ids");
+  array rows = at::empty({nnz, K}, f32_like(d));
+  check(gsplat_hip_packed_rows_gather(d.data_ptr<float>(), is_empty(bid) ? nullptr : bid.data_ptr<int32_t>(),
+                                      cid.data_ptr<int32_t>(), gid.data_ptr<int32_t>(), nnz, B, C, N,
+                                      static_cast<int32_t>(K), rows.data_ptr<float>(), stream_for(s, d)));
+  return rows;
+}
+
+array gsplat_packed_rows_scatter(const array& rows, const array& rank, int64_t B, int64_t C, int64_t N,
+                                 StreamOrDevice s) {
+  require_device(rows, "rows");
+  require_dtype(rows, at::kFloat, "packed_rows_scatter expects float32 values.");
+  if (rows.dim() != 2) throw std::runtime_error("packed_rows_scatter: rows must have shape [nnz, K].");
+  require_device(rank, "rank");
+  if (rank.scalar_type() != at::kByte) throw std::runtime_error("packed_rows_scatter: rank must be uint8.");
+  const int64_t nnz = rows.size(0), K = rows.size(1);
+  const c10::DeviceGuard guard(rows.device());
+  const array r = contig(rows);
+  const array rk = contig(rank);
+  array dense = at::empty({B, C, N, K}, f32_like(r));
+  check(gsplat_hip_packed_rows_scatter(r.data_ptr<float>(), rk.data_ptr<uint8_t>(), static_cast<size_t>(rk.numel()),
+                                       nnz, B, C, N, static_cast<int32_t>(K), dense.data_ptr<float>(),
+                                       stream_for(s, r)));
+  return dense;
 }
 
 std::vector<array> gsplat_projection_ewa_3dgs_fused(const ProjectionEWA3DGSFusedInput& input) {

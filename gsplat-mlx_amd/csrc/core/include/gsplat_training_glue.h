@@ -33,13 +33,27 @@ std::vector<array> gsplat_activated_projection_backward(const ProjectionEWA3DGSF
 // without logits) and the uint8 rank structure the backward reads.
 std::vector<array> gsplat_activated_projection_packed_forward(const ProjectionEWA3DGSFusedInput& input);
 
-// {v_means, v_quats, v_log_scales, v_opacity_logits, v_viewmats} of the
-// activated packed projection: `input` as the packed backward's with raw
-// quats and log-scales (the ids are not read), the forward's rank, the
-// opacity logits and the per-row cotangent of the opacities (empty: zeros).
+// {v_means, v_quats, v_log_scales, v_opacity_logits, v_viewmats,
+// v_viewspace} of the activated packed projection: `input` as the packed
+// backward's with raw quats and log-scales (the ids are not read), the
+// forward's rank, the opacity logits and the per-row cotangent of the
+// opacities (empty: zeros). v_viewspace ([..., C, N, 2], empty unless
+// viewspace_grad): the means2d rows' cotangent at their dense (camera,
+// Gaussian) slots, zeros elsewhere -- the gradient of a dense viewspace
+// proxy.
 std::vector<array> gsplat_activated_projection_packed_backward(const ProjectionEWA3DGSPackedBackwardInput& input,
                                                                const array& rank, const array& opacity_logits,
-                                                               const array& v_opacities);
+                                                               const array& v_opacities, bool viewspace_grad = false);
+
+// Packed rows [nnz, K] of dense [B, C, N, K] values at the rows' (batch,
+// camera, Gaussian) ids (batch_ids may be empty with B = 1).
+array gsplat_packed_rows_gather(const array& dense, const array& batch_ids, const array& camera_ids,
+                                const array& gaussian_ids, StreamOrDevice s = {});
+
+// Its adjoint: dense [B, C, N, K] holding each row at its pair's slot (the
+// activated packed forward's rank) and zeros elsewhere.
+array gsplat_packed_rows_scatter(const array& rows, const array& rank, int64_t B, int64_t C, int64_t N,
+                                 StreamOrDevice s = {});
 
 // {quats / max(|quats|, 1e-8), exp(log_scales), sigmoid(opacity_logits)};
 // each input may be undefined / empty (its output is then empty).

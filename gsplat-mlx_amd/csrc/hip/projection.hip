@@ -214,14 +214,16 @@ __global__ void __launch_bounds__(kProjBlock) projection_packed_write_kernel(
 }
 
 // indptr[cam] = packed position of the first pair of camera cam (B*C + 1
-// entries; the last is nnz).
+// entries; the last is nnz, read from nnz_dev when that is non-null).
 __global__ void __launch_bounds__(256) projection_packed_indptr_kernel(const uint64_t* __restrict__ mask,
                                                                        const int32_t* __restrict__ prefix,
                                                                        int64_t n_cams, int64_t N, int64_t nnz,
+                                                                       const int64_t* __restrict__ nnz_dev,
                                                                        int32_t* __restrict__ indptr) {
   const int64_t cam = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (cam > n_cams) return;
-  indptr[cam] = static_cast<int32_t>(cam == n_cams ? nnz : min<int64_t>(packed_rank(mask, prefix, cam * N), nnz));
+  const int64_t nn = nnz_dev ? *nnz_dev : nnz;
+  indptr[cam] = static_cast<int32_t>(cam == n_cams ? nn : min<int64_t>(packed_rank(mask, prefix, cam * N), nn));
 }
 
 // Backward: bit per pair from the packed (batch, camera, gaussian) ids.
@@ -520,10 +522,11 @@ int packed_count_impl(const std::string& op, const float* means, const float* co
 template <bool ACT>
 int packed_fwd_impl(const std::string& op, const float* means, const float* covars, const float* quats,
                     const float* scales, const float* opacities, const float* viewmats, const float* Ks, int64_t B,
-                    int64_t C, int64_t N, const gsplat_projection_params* params, int64_t nnz, int32_t* batch_ids,
-                    int32_t* camera_ids, int32_t* gaussian_ids, int32_t* indptr, int32_t* radii, float* means2d,
-                    float* depths, float* conics, float* compensations, float* opac_rows, const void* workspace,
-                    size_t workspace_bytes, void* stream) {
+                    int64_t C, int64_t N, const gsplat_projection_params* params, int64_t nnz,
+                    const int64_t* nnz_dev, int32_t* batch_ids, int32_t* camera_ids, int32_t* gaussian_ids,
+                    int32_t* indptr, int32_t* radii, float* means2d, float* depths, float* conics,
+                    float* compensations, float* opac_rows, const void* workspace, size_t workspace_bytes,
+                    void* stream) {
   int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
   if (rc) return rc;
   if (ACT && params->use_covars) return invalid(op + " takes quats and log_scales, not covars.");
@@ -550,7 +553,7 @@ int packed_fwd_impl(const std::string& op, const float* means, const float* cova
           batch_ids, camera_ids, gaussian_ids, radii, means2d, depths, conics,
           params->calc_compensations ? compensations : nullptr, ACT ? opac_rows : nullptr);
     projection_packed_indptr_kernel<<<grid_for(B * C + 1, 256), 256, 0, s>>>(l.mask, l.prefix, B * C, N, nnz,
-                                                                             indptr);
+                                                                             nnz_dev, indptr);
   }
   return check_launch(op.c_str());
 }
@@ -563,8 +566,8 @@ int packed_bwd_impl(const std::string& op, const float* means, const float* cova
                     size_t rank_ws_bytes, const float* conics, const float* compensations, const float* v_means2d,
                     const float* v_depths, const float* v_conics, const float* v_compensations,
                     const float* logits, const float* v_opac_rows, float* v_means, float* v_covars, float* v_quats,
-                    float* v_scales, float* v_logits, float* v_viewmats, void* workspace, size_t workspace_bytes,
-                    void* stream) {
+                    float* v_scales, float* v_logits, float* v_viewmats, float* v_viewspace, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   int rc = packed_args(op, means, covars, quats, scales, viewmats, Ks, B, C, N, params);
   if (rc) return rc;
   const gsplat_projection_params& p = *params;
@@ -578,6 +581,7 @@ int packed_bwd_impl(const std::string& op, const float* means, const float* cova
   }
   if (!v_means || (p.use_covars ? !v_covars : (!v_quats || !v_scales))) return invalid(op + ": null pointer.");
   if (nnz > 0 && (!conics || !v_means2d || !v_conics)) return invalid(op + ": null pointer.");
+  if (!ACT && v_viewspace) return invalid(op + ": no viewspace gradient here.");
   if (!ACT && nnz > 0 && (!camera_ids || !gaussian_ids)) return invalid(op + ": null pointer.");
   if (!ACT && nnz > 0 && B > 1 && !batch_ids) return invalid(op + ": null batch_ids with more than one batch.");
   if (v_compensations && !compensations) return invalid(op + ": v_compensations without compensations.");
@@ -617,7 +621,8 @@ int packed_bwd_impl(const std::string& op, const float* means, const float* cova
     launch_projection_bwd(ACT, grid, s, means, covars, quats, scales, viewmats, Ks, C, N, p, nullptr, conics,
                           compensations, v_means2d, v_depths, v_conics, v_compensations, v_means, v_covars, v_quats,
                           v_scales, v_viewmats ? l.partials : nullptr, ACT ? logits : nullptr, nullptr,
-                          ACT ? v_logits : nullptr, mask, prefix, ACT ? v_opac_rows : nullptr);
+                          ACT ? v_logits : nullptr, mask, prefix, ACT ? v_opac_rows : nullptr,
+                          ACT ? v_viewspace : nullptr);
   }
   if ((rc = check_launch(op.c_str())) || !v_viewmats) return rc;
   {
@@ -646,9 +651,9 @@ extern "C" int gsplat_hip_projection_packed_fwd(const float* means, const float*
                                                 float* conics, float* compensations, const void* workspace,
                                                 size_t workspace_bytes, void* stream) {
   return packed_fwd_impl<false>("projection_ewa_3dgs_packed_forward", means, covars, quats, scales, opacities,
-                                viewmats, Ks, B, C, N, params, nnz, batch_ids, camera_ids, gaussian_ids, indptr,
-                                radii, means2d, depths, conics, compensations, nullptr, workspace, workspace_bytes,
-                                stream);
+                                viewmats, Ks, B, C, N, params, nnz, nullptr, batch_ids, camera_ids, gaussian_ids,
+                                indptr, radii, means2d, depths, conics, compensations, nullptr, workspace,
+                                workspace_bytes, stream);
 }
 
 extern "C" int gsplat_hip_projection_packed_bwd(const float* means, const float* covars, const float* quats,
@@ -665,7 +670,7 @@ extern "C" int gsplat_hip_projection_packed_bwd(const float* means, const float*
   return packed_bwd_impl<false>("projection_ewa_3dgs_packed_backward", means, covars, quats, scales, viewmats, Ks, B,
                                 C, N, params, nnz, batch_ids, camera_ids, gaussian_ids, nullptr, 0, conics,
                                 compensations, v_means2d, v_depths, v_conics, v_compensations, nullptr, nullptr,
-                                v_means, v_covars, v_quats, v_scales, nullptr, v_viewmats, workspace,
+                                v_means, v_covars, v_quats, v_scales, nullptr, v_viewmats, nullptr, workspace,
                                 workspace_bytes, stream);
 }
 
@@ -683,11 +688,11 @@ extern "C" int gsplat_hip_activated_projection_packed_count(const float* means, 
 extern "C" int gsplat_hip_activated_projection_packed_fwd(
     const float* means, const float* quats, const float* log_scales, const float* opacity_logits,
     const float* viewmats, const float* Ks, int64_t B, int64_t C, int64_t N, const gsplat_projection_params* params,
-    int64_t nnz, int32_t* batch_ids, int32_t* camera_ids, int32_t* gaussian_ids, int32_t* indptr, int32_t* radii,
-    float* means2d, float* depths, float* conics, float* compensations, float* opacities, const void* workspace,
-    size_t workspace_bytes, void* stream) {
+    int64_t nnz, const int64_t* nnz_dev, int32_t* batch_ids, int32_t* camera_ids, int32_t* gaussian_ids,
+    int32_t* indptr, int32_t* radii, float* means2d, float* depths, float* conics, float* compensations,
+    float* opacities, const void* workspace, size_t workspace_bytes, void* stream) {
   return packed_fwd_impl<true>("activated_projection_packed_forward", means, nullptr, quats, log_scales,
-                               opacity_logits, viewmats, Ks, B, C, N, params, nnz, batch_ids, camera_ids,
+                               opacity_logits, viewmats, Ks, B, C, N, params, nnz, nnz_dev, batch_ids, camera_ids,
                                gaussian_ids, indptr, radii, means2d, depths, conics, compensations, opacities,
                                workspace, workspace_bytes, stream);
 }
@@ -698,12 +703,81 @@ extern "C" int gsplat_hip_activated_projection_packed_bwd(
     int64_t nnz, const void* count_workspace, size_t count_workspace_bytes, const float* conics,
     const float* compensations, const float* v_means2d, const float* v_depths, const float* v_conics,
     const float* v_compensations, const float* v_opacities, float* v_means, float* v_quats, float* v_log_scales,
-    float* v_opacity_logits, float* v_viewmats, void* workspace, size_t workspace_bytes, void* stream) {
+    float* v_opacity_logits, float* v_viewmats, float* v_viewspace, void* workspace, size_t workspace_bytes,
+    void* stream) {
   return packed_bwd_impl<true>("activated_projection_packed_backward", means, nullptr, quats, log_scales, viewmats,
                                Ks, B, C, N, params, nnz, nullptr, nullptr, nullptr, count_workspace,
                                count_workspace_bytes, conics, compensations, v_means2d, v_depths, v_conics,
                                v_compensations, opacity_logits, v_opacities, v_means, nullptr, v_quats, v_log_scales,
-                               v_opacity_logits, v_viewmats, workspace, workspace_bytes, stream);
+                               v_opacity_logits, v_viewmats, v_viewspace, workspace, workspace_bytes, stream);
+}
+
+// Rows of the packed layout <-> dense (batch, camera, Gaussian) slots of K
+// floats each: the gather reads each row's slot; the scatter writes every
+// slot, the row's values where the pair has one (rank structure of the
+// count pass) and zeros elsewhere.
+__global__ void __launch_bounds__(256) packed_rows_gather_kernel(const float* __restrict__ dense,
+                                                                 const int32_t* __restrict__ batch_ids,
+                                                                 const int32_t* __restrict__ camera_ids,
+                                                                 const int32_t* __restrict__ gaussian_ids,
+                                                                 int64_t nnz, int64_t B, int64_t C, int64_t N,
+                                                                 int K, float* __restrict__ rows) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (r >= nnz) return;
+  const int64_t b = batch_ids ? batch_ids[r] : 0, c = camera_ids[r], g = gaussian_ids[r];
+  const bool ok = b >= 0 && b < B && c >= 0 && c < C && g >= 0 && g < N;
+  const float* src = dense + ((ok ? (b * C + c) * N + g : 0)) * K;
+  for (int k = 0; k < K; ++k) rows[r * K + k] = ok ? src[k] : 0.0f;
+}
+
+__global__ void __launch_bounds__(256) packed_rows_scatter_kernel(const float* __restrict__ rows,
+                                                                  const uint64_t* __restrict__ mask,
+                                                                  const int32_t* __restrict__ prefix, int64_t nnz,
+                                                                  int64_t total, int K, float* __restrict__ dense) {
+  const int64_t pair = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (pair >= total) return;
+  int64_t r = -1;
+  if ((mask[pair >> 6] >> (pair & 63)) & 1ull) {
+    r = packed_rank(mask, prefix, pair);
+    if (r >= nnz) r = -1;
+  }
+  for (int k = 0; k < K; ++k) dense[pair * K + k] = r >= 0 ? rows[r * K + k] : 0.0f;
+}
+
+extern "C" int gsplat_hip_packed_rows_gather(const float* dense, const int32_t* batch_ids, const int32_t* camera_ids,
+                                             const int32_t* gaussian_ids, int64_t nnz, int64_t B, int64_t C,
+                                             int64_t N, int32_t K, float* rows, void* stream) {
+  if (nnz < 0 || B < 0 || C < 0 || N < 0 || K <= 0) return invalid("packed_rows_gather: invalid sizes.");
+  if (nnz == 0) return GSPLAT_OK;
+  if (!dense || !camera_ids || !gaussian_ids || !rows) return invalid("packed_rows_gather: null pointer.");
+  if (B > 1 && !batch_ids) return invalid("packed_rows_gather: null batch_ids with more than one batch.");
+  hipStream_t s = as_stream(stream);
+  {
+    KernelTimer timer("packed_rows", s);
+    packed_rows_gather_kernel<<<grid_for(nnz, 256), 256, 0, s>>>(dense, batch_ids, camera_ids, gaussian_ids, nnz, B,
+                                                                  C, N, K, rows);
+  }
+  return check_launch("packed_rows_gather");
+}
+
+extern "C" int gsplat_hip_packed_rows_scatter(const float* rows, const void* count_workspace,
+                                              size_t count_workspace_bytes, int64_t nnz, int64_t B, int64_t C,
+                                              int64_t N, int32_t K, float* dense, void* stream) {
+  if (nnz < 0 || B < 0 || C < 0 || N < 0 || K <= 0) return invalid("packed_rows_scatter: invalid sizes.");
+  const int64_t total = B * C * N;
+  if (total == 0) return GSPLAT_OK;
+  if (!dense || (nnz > 0 && !rows)) return invalid("packed_rows_scatter: null pointer.");
+  PackedLayout l;
+  if (!count_workspace || count_workspace_bytes < packed_layout(B, C, N, false, &l, const_cast<void*>(count_workspace))) {
+    set_error("packed_rows_scatter: count workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  hipStream_t s = as_stream(stream);
+  {
+    KernelTimer timer("packed_rows", s);
+    packed_rows_scatter_kernel<<<grid_for(total, 256), 256, 0, s>>>(rows, l.mask, l.prefix, nnz, total, K, dense);
+  }
+  return check_launch("packed_rows_scatter");
 }
 
 extern "C" int gsplat_hip_activated_projection_fwd(const float* means, const float* quats, const float* log_scales,

@@ -261,7 +261,9 @@ __device__ __forceinline__ void block_sum12_store(float vals[12], float* __restr
 // receive their gradients, and v_logits (if non-null) = v_opac * o (1 - o)
 // with o = sigmoid(logits) (v_opac null: zeros). With v_opac_rows (packed
 // layout) the opacity cotangent is per visible pair instead: its sum over
-// the Gaussian's pairs (in camera order) takes v_opac's place.
+// the Gaussian's pairs (in camera order) takes v_opac's place, and
+// v_viewspace (packed layout, if non-null) receives each (camera, Gaussian)
+// pair's means2d cotangent densely, zero where the pair has no row.
 template <bool ACT>
 __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
@@ -272,7 +274,8 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     const float* __restrict__ v_compensations, float* __restrict__ v_means, float* __restrict__ v_covars,
     float* __restrict__ v_quats, float* __restrict__ v_scales, float* __restrict__ vm_partials,
     const float* __restrict__ logits, const float* __restrict__ v_opac, float* __restrict__ v_logits,
-    const uint64_t* __restrict__ pmask, const int32_t* __restrict__ pprefix, const float* __restrict__ v_opac_rows) {
+    const uint64_t* __restrict__ pmask, const int32_t* __restrict__ pprefix, const float* __restrict__ v_opac_rows,
+    float* __restrict__ v_viewspace) {
   const int64_t n = static_cast<int64_t>(blockIdx.x) * kProjBlock + threadIdx.x;
   const int64_t b = blockIdx.y;
   const bool in_range = n < N;
@@ -316,6 +319,18 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
         const int bit = static_cast<int>(idx & 63);
         valid = (w >> bit) & 1ull;
         idx = static_cast<int64_t>(pprefix[idx >> 6]) + __popcll(w & ((1ull << bit) - 1ull));
+      }
+      // the dense viewspace proxy's gradient: this pair's means2d cotangent,
+      // zero for a pair without a row
+      if (v_viewspace && in_range) {
+        float vx = 0.0f, vy = 0.0f;
+        if (valid) {
+          vx = v_means2d[idx * 2];
+          vy = v_means2d[idx * 2 + 1];
+        }
+        const int64_t slot = cam * N + n;
+        v_viewspace[slot * 2] = vx;
+        v_viewspace[slot * 2 + 1] = vy;
       }
     } else {
       valid = in_range && radii[idx * 2] > 0 && radii[idx * 2 + 1] > 0;
@@ -420,19 +435,19 @@ void launch_projection_bwd(bool act, dim3 grid, hipStream_t s, const float* mean
                            const float* v_conics, const float* v_compensations, float* v_means, float* v_covars,
                            float* v_quats, float* v_scales, float* vm_partials, const float* logits,
                            const float* v_opac, float* v_logits, const uint64_t* pmask,
-                           const int32_t* pprefix, const float* v_opac_rows) {
+                           const int32_t* pprefix, const float* v_opac_rows, float* v_viewspace) {
   if (act)
     projection_bwd_kernel<true><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p, radii,
                                                             conics, compensations, v_means2d, v_depths, v_conics,
                                                             v_compensations, v_means, v_covars, v_quats, v_scales,
                                                             vm_partials, logits, v_opac, v_logits, pmask, pprefix,
-                                                            v_opac_rows);
+                                                            v_opac_rows, v_viewspace);
   else
     projection_bwd_kernel<false><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p,
                                                              radii, conics, compensations, v_means2d, v_depths,
                                                              v_conics, v_compensations, v_means, v_covars, v_quats,
                                                              v_scales, vm_partials, nullptr, nullptr, nullptr, pmask,
-                                                             pprefix, nullptr);
+                                                             pprefix, nullptr, nullptr);
 }
 
 }  // namespace gsplat_hip

@@ -23,7 +23,8 @@ void launch_projection_bwd(bool act, dim3 grid, hipStream_t s, const float* mean
                            const float* v_conics, const float* v_compensations, float* v_means, float* v_covars,
                            float* v_quats, float* v_scales, float* vm_partials, const float* logits,
                            const float* v_opac, float* v_logits, const uint64_t* pmask = nullptr,
-                           const int32_t* pprefix = nullptr, const float* v_opac_rows = nullptr);
+                           const int32_t* pprefix = nullptr, const float* v_opac_rows = nullptr,
+                           float* v_viewspace = nullptr);
 
 namespace {
 

@@ -24,6 +24,7 @@ from .autograd import (  # noqa: E402,F401
     gaussian_activations,
     image_loss,
     l1_loss,
+    packed_rows,
     packed_viewspace,
     projection_ewa_3dgs_fused,
     projection_packed,
@@ -57,6 +58,8 @@ __all__ = [
     "activated_projection_backward",
     "activated_projection_packed_forward",
     "activated_projection_packed_backward",
+    "packed_rows_gather",
+    "packed_rows_scatter",
     "l1_loss_forward",
     "l1_loss_backward",
     "image_loss_forward",
@@ -72,6 +75,7 @@ __all__ = [
     "l1_loss",
     "projection_ewa_3dgs_fused",
     "projection_packed",
+    "packed_rows",
     "packed_viewspace",
     "quat_scale_to_covar_preci",
     "rasterize_to_pixels_3dgs",

@@ -199,8 +199,8 @@ class _ActivatedProjectionPacked(torch.autograd.Function):
     cotangent per row."""
 
     @staticmethod
-    def forward(ctx, means, quats, log_scales, opacity_logits, viewmats, Ks, image_width, image_height, eps2d,
-                near_plane, far_plane, radius_clip, calc_compensations, camera_model):
+    def forward(ctx, means, quats, log_scales, opacity_logits, viewmats, Ks, viewspace_points, image_width,
+                image_height, eps2d, near_plane, far_plane, radius_clip, calc_compensations, camera_model):
         ctx.set_materialize_grads(False)
         inputs = {"means": means, "quats": quats, "log_scales": log_scales, "viewmats": viewmats, "Ks": Ks}
         if _nonempty(opacity_logits):
@@ -210,13 +210,14 @@ class _ActivatedProjectionPacked(torch.autograd.Function):
         ctx.save_for_backward(means, quats, log_scales, opacity_logits, viewmats, Ks, out["conics"],
                               out["compensations"], out["rank"])
         ctx.params = (image_width, image_height, eps2d, calc_compensations, camera_model)
-        for k in ("batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii"):
+        ctx.vsp_shape = viewspace_points.shape
+        for k in ("batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii", "rank"):
             ctx.mark_non_differentiable(out[k])
         return (out["batch_ids"], out["camera_ids"], out["gaussian_ids"], out["indptr"], out["radii"],
-                out["means2d"], out["depths"], out["conics"], out["compensations"], out["opacities"])
+                out["means2d"], out["depths"], out["conics"], out["compensations"], out["opacities"], out["rank"])
 
     @staticmethod
-    def backward(ctx, _b, _c, _g, _i, _r, v_means2d, v_depths, v_conics, v_compensations, v_opacities):
+    def backward(ctx, _b, _c, _g, _i, _r, v_means2d, v_depths, v_conics, v_compensations, v_opacities, _rank):
         means, quats, log_scales, logits, viewmats, Ks, conics, comps, rank = ctx.saved_tensors
         W, H, eps2d, calc_comp, camera_model = ctx.params
         nnz = conics.shape[0]
@@ -235,27 +236,63 @@ class _ActivatedProjectionPacked(torch.autograd.Function):
         if v_opacities is not None:
             cot["v_opacities"] = v_opacities.contiguous()
         needs_viewmats = ctx.needs_input_grad[4]
-        out = _C.activated_projection_packed_backward(inputs, fwd, cot, W, H, eps2d, camera_model, needs_viewmats)
+        needs_vsp = ctx.needs_input_grad[6]
+        out = _C.activated_projection_packed_backward(inputs, fwd, cot, W, H, eps2d, camera_model, needs_viewmats,
+                                                      needs_vsp)
         g_logits = out["v_opacity_logits"] if ctx.needs_input_grad[3] else None
+        g_vsp = out["v_viewspace"].reshape(ctx.vsp_shape) if needs_vsp else None
         return (out["v_means"], out["v_quats"], out["v_log_scales"], g_logits,
-                out["v_viewmats"] if needs_viewmats else None) + (None,) * 9
+                out["v_viewmats"] if needs_viewmats else None, None, g_vsp) + (None,) * 8
 
 
 def activated_projection_packed(means, quats, log_scales, opacity_logits, viewmats, Ks, image_width, image_height,
-                                eps2d=0.3, near_plane=0.01, far_plane=1e10, radius_clip=0.0, calc_compensations=False,
-                                camera_model=0):
+                                viewspace_points=None, eps2d=0.3, near_plane=0.01, far_plane=1e10, radius_clip=0.0,
+                                calc_compensations=False, camera_model=0):
     """gaussian_activations followed by projection_packed, in the packed
     projection's kernels: a dict of the visible pairs' rows as
     projection_packed's plus "opacities", each row's sigmoid opacity (the
-    rasterizer's), differentiable w.r.t. means, the raw parameters and
-    viewmats."""
+    rasterizer's), and "rank", the rank structure packed_rows scatters by;
+    differentiable w.r.t. means, the raw parameters and viewmats.
+    viewspace_points (dense [..., C, N, 2], optional) receives the means2d
+    rows' gradient at their (camera, Gaussian) slots, as the dense
+    projection's proxy does."""
     keys = ("batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii", "means2d", "depths", "conics",
-            "compensations", "opacities")
+            "compensations", "opacities", "rank")
+    e = _empty(means)
     out = _ActivatedProjectionPacked.apply(means, quats, log_scales,
-                                           opacity_logits if opacity_logits is not None else _empty(means), viewmats,
-                                           Ks, image_width, image_height, eps2d, near_plane, far_plane, radius_clip,
+                                           opacity_logits if opacity_logits is not None else e, viewmats, Ks,
+                                           viewspace_points if viewspace_points is not None else e, image_width,
+                                           image_height, eps2d, near_plane, far_plane, radius_clip,
                                            calc_compensations, camera_model)
     return dict(zip(keys, out))
+
+
+class _PackedRows(torch.autograd.Function):
+    """Packed rows [nnz, K] of dense [B, C, N, K] values at the rows'
+    (batch, camera, Gaussian) ids; the backward scatters the rows' gradient
+    to their slots by the activated packed projection's rank (zeros
+    elsewhere)."""
+
+    @staticmethod
+    def forward(ctx, dense, batch_ids, camera_ids, gaussian_ids, rank):
+        ctx.save_for_backward(rank)
+        ctx.shape = dense.shape
+        ids = {"camera_ids": camera_ids, "gaussian_ids": gaussian_ids}
+        if dense.shape[0] > 1:
+            ids["batch_ids"] = batch_ids
+        return _C.packed_rows_gather(dense.contiguous(), ids)
+
+    @staticmethod
+    def backward(ctx, g):
+        (rank,) = ctx.saved_tensors
+        B, C, N, _K = ctx.shape
+        return _C.packed_rows_scatter(g.contiguous(), rank, B, C, N), None, None, None, None
+
+
+def packed_rows(dense, batch_ids, camera_ids, gaussian_ids, rank):
+    """dense [B, C, N, K] at the packed rows' pairs, differentiable w.r.t.
+    dense (rank: activated_projection_packed's)."""
+    return _PackedRows.apply(dense, batch_ids, camera_ids, gaussian_ids, rank)
 
 
 class _PackedViewspace(torch.autograd.Function):

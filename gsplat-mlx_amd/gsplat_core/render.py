@@ -27,7 +27,7 @@ import torch
 
 from . import _gsplat_core as _C
 from .autograd import (activated_projection, activated_projection_packed, image_loss, l1_loss as _l1_loss,
-                       packed_viewspace, projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs, render_rgb,
+                       packed_rows, projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs, render_rgb,
                        sh_camera_colors, spherical_harmonics)
 
 
@@ -114,17 +114,15 @@ def _render_sh_packed(means, quats, log_scales, features_dc, features_rest, opac
     """render_sh_model over the packed layout: only the visible (camera,
     Gaussian) pairs are projected, intersected and rasterized."""
     C = viewmats.shape[1]
-    N = means.shape[-2]
     # queued before the projection, whose count read-back then waits on it
     colors_all = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)  # [1, C, N, 3]
     # the parameter activations run inside the packed projection's kernels,
     # which also write each row's opacity
     pr = activated_projection_packed(means, quats, log_scales, opacity_logits, viewmats, Ks, width, height,
-                                     eps2d=0.3, near_plane=0.01, far_plane=far_plane)
+                                     viewspace_points=viewspace_points, eps2d=0.3, near_plane=0.01,
+                                     far_plane=far_plane)
     cid, gid = pr["camera_ids"], pr["gaussian_ids"]
     m2 = pr["means2d"]
-    if viewspace_points is not None:
-        m2 = packed_viewspace(m2, viewspace_points, cid, gid)
     opac = pr["opacities"]
     tw, th = tile_grid(width, height, tile_size)
     inputs = {"means2d": m2.detach(), "radii": pr["radii"], "depths": pr["depths"].detach(), "image_ids": cid,
@@ -135,9 +133,9 @@ def _render_sh_packed(means, quats, log_scales, features_dc, features_rest, opac
     # sorted lists and tile offsets (the tile-bucket path writes the offsets
     # itself) in two calls around the count read-back: the per-row colour
     # gather is queued in between, so its host work overlaps the count
-    # kernels (index_select: its backward is an index_add, no sort)
+    # kernels
     pending = _C.intersect_tile_offsets_begin(inputs, C, tile_size, tw, th)
-    colors = colors_all.reshape(C * N, -1).index_select(0, cid.long() * N + gid.long())
+    colors = packed_rows(colors_all, pr["batch_ids"], cid, gid, pr["rank"])
     isect = _C.intersect_tile_offsets_end(pending)
     offsets = isect["tile_offsets"]
     bg = background_tensor(background, means.device)

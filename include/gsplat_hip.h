@@ -698,14 +698,20 @@ int gsplat_hip_activated_projection_bwd(const float* means, const float* quats,
  * forward take the workspace of gsplat_hip_projection_packed_workspace_size(
  * B, C, N, 0) and give the same rows as gsplat_hip_gaussian_activations_fwd
  * followed by the packed projection, bit for bit, plus opacities [nnz] (when
- * non-NULL; needs opacity_logits), each visible pair's sigmoid opacity. The
+ * non-NULL; needs opacity_logits), each visible pair's sigmoid opacity. With
+ * nnz_dev (the count's device total) the forward may run before the count is
+ * on the host: nnz is then the outputs' capacity (rows past it are not
+ * written; the result is whole when the count is at most nnz) and indptr
+ * ends with the device total. The
  * caller keeps the count's workspace for the backward (count_workspace): it
  * holds the rank structure that maps a pair to its row, so the backward takes
  * no ids. The backward's cotangents are per row, v_opacities [nnz] included
  * (NULL: zeros; it is summed over a Gaussian's pairs in camera order), and it
  * writes the raw parameters' gradients as gsplat_hip_activated_projection_bwd,
  * with its own workspace of gsplat_hip_projection_packed_workspace_size(B, C,
- * N, v_viewmats != NULL). */
+ * N, v_viewmats != NULL), plus v_viewspace [B, C, N, 2] when non-NULL: each
+ * pair's v_means2d row, zeros for pairs without a row (the gradient of a
+ * dense viewspace proxy of the means2d). */
 int gsplat_hip_activated_projection_packed_count(const float* means, const float* quats,
                                                  const float* log_scales, const float* opacity_logits,
                                                  const float* viewmats, const float* Ks, int64_t B,
@@ -716,10 +722,11 @@ int gsplat_hip_activated_projection_packed_fwd(const float* means, const float* 
                                                const float* log_scales, const float* opacity_logits,
                                                const float* viewmats, const float* Ks, int64_t B, int64_t C,
                                                int64_t N, const gsplat_projection_params* params, int64_t nnz,
-                                               int32_t* batch_ids, int32_t* camera_ids, int32_t* gaussian_ids,
-                                               int32_t* indptr, int32_t* radii, float* means2d, float* depths,
-                                               float* conics, float* compensations, float* opacities,
-                                               const void* workspace, size_t workspace_bytes, void* stream);
+                                               const int64_t* nnz_dev, int32_t* batch_ids, int32_t* camera_ids,
+                                               int32_t* gaussian_ids, int32_t* indptr, int32_t* radii,
+                                               float* means2d, float* depths, float* conics, float* compensations,
+                                               float* opacities, const void* workspace, size_t workspace_bytes,
+                                               void* stream);
 int gsplat_hip_activated_projection_packed_bwd(const float* means, const float* quats,
                                                const float* log_scales, const float* opacity_logits,
                                                const float* viewmats, const float* Ks, int64_t B, int64_t C,
@@ -730,7 +737,21 @@ int gsplat_hip_activated_projection_packed_bwd(const float* means, const float* 
                                                const float* v_conics, const float* v_compensations,
                                                const float* v_opacities, float* v_means, float* v_quats,
                                                float* v_log_scales, float* v_opacity_logits, float* v_viewmats,
-                                               void* workspace, size_t workspace_bytes, void* stream);
+                                               float* v_viewspace, void* workspace, size_t workspace_bytes,
+                                               void* stream);
+
+/* Packed rows <-> dense slots (no reference counterpart; the packed
+ * training step's per-row colours): gather rows [nnz, K] = dense [B, C, N, K]
+ * at each row's (batch, camera, Gaussian) (batch_ids may be NULL with B = 1;
+ * ids outside the grid give zeros); scatter, its adjoint, writes every dense
+ * slot: the row's values where the pair has a row (the count pass's rank
+ * structure, as the activated packed backward reads it), zeros elsewhere. */
+int gsplat_hip_packed_rows_gather(const float* dense, const int32_t* batch_ids, const int32_t* camera_ids,
+                                  const int32_t* gaussian_ids, int64_t nnz, int64_t B, int64_t C, int64_t N,
+                                  int32_t K, float* rows, void* stream);
+int gsplat_hip_packed_rows_scatter(const float* rows, const void* count_workspace, size_t count_workspace_bytes,
+                                   int64_t nnz, int64_t B, int64_t C, int64_t N, int32_t K, float* dense,
+                                   void* stream);
 
 /* Image L1 term mean(|a - b|) over n values into the device scalar *loss
  * (nn.losses.l1_loss in image_loss_components,

@@ -118,6 +118,7 @@ def test_activated_projection_packed(B, C, N, logits, viewgrad):
         K = dev(Ks)
         if fused:
             out = activated_projection_packed(m, q, ls, lo, vm if viewgrad else vm.detach(), K, 320, 240)
+            out = {k: v for k, v in out.items()}
         else:
             qa, sa, oa = gaussian_activations(q, ls, lo if logits else torch.zeros((B, N), device="cuda"))
             out = projection_packed(m, qa, sa, vm if viewgrad else vm.detach(), K, 320, 240)
@@ -140,6 +141,7 @@ def test_activated_projection_packed(B, C, N, logits, viewgrad):
 
     a, b = run(True), run(False)
     assert a["means2d"].shape[0] > 0
+    a.pop("rank")
     if not logits:
         assert a.pop("opacities").size == 0
     for k in a:
@@ -148,6 +150,77 @@ def test_activated_projection_packed(B, C, N, logits, viewgrad):
             assert_close_rel_summation(a[k], b[k], 1e-4, k)
         else:
             np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+
+
+def test_activated_packed_speculation():
+    """A repeated shape writes its rows speculatively (outputs sized by the
+    previous count, filled before the count reaches the host): kept when the
+    count fits, redone when it does not. Four calls of one shape -- few
+    visible pairs, then many (over the capacity), many again (kept), few
+    again (kept) -- each give the rows, indptr and opacities of the exact
+    composition (gaussian_activations + projection_packed)."""
+    import torch
+
+    from gsplat_core.autograd import activated_projection_packed, gaussian_activations, projection_packed
+
+    B, C, N = 1, 2, 4001  # a shape of its own
+    rng = np.random.default_rng(99)
+    means, quats, scales, op, view, Ks = _scene(rng, B, C, N)
+    few = means.copy()
+    few[:, : N * 3 // 4, 2] = -5.0  # three quarters behind the cameras
+    lg = rng.normal(size=(B, N)).astype(np.float32)
+    for name, m in (("few", few), ("many", means), ("many again", means), ("few again", few)):
+        out = activated_projection_packed(dev(m), dev(quats), dev(np.log(scales)), dev(lg), dev(view), dev(Ks), 320,
+                                          240)
+        qa, sa, oa = gaussian_activations(dev(quats), dev(np.log(scales)), dev(lg))
+        ref = projection_packed(dev(m), qa, sa, dev(view), dev(Ks), 320, 240)
+        torch.cuda.synchronize()
+        print(f"speculation {name}: nnz {out['camera_ids'].numel()}", flush=True)
+        for k in ("batch_ids", "camera_ids", "gaussian_ids", "indptr", "radii", "means2d", "depths", "conics"):
+            np.testing.assert_array_equal(host(out[k]), host(ref[k]), err_msg=f"{name} {k}")
+        np.testing.assert_array_equal(host(out["opacities"]), host(oa).reshape(-1)[host(ref["gaussian_ids"])],
+                                      err_msg=name)
+
+
+@pytest.mark.parametrize("B,C,K", [(1, 1, 3), (1, 3, 3), (2, 2, 5)])
+def test_packed_rows(B, C, K):
+    """packed_rows_gather takes each row's (batch, camera, Gaussian) slot of a
+    dense array; packed_rows_scatter puts rows back at their slots by the rank
+    structure, zeros elsewhere (the gather's adjoint), and the viewspace
+    gradient of the activated packed backward is the same scatter of the
+    means2d rows' cotangent."""
+    import torch
+
+    from gsplat_core.autograd import activated_projection_packed
+
+    rng = np.random.default_rng(B * 10 + C)
+    N = 2500
+    means, quats, scales, op, view, Ks = _scene(rng, B, C, N)
+    g = gsplat()
+    m = dev(means)
+    vsp = torch.zeros((B, C, N, 2), device="cuda", requires_grad=True)
+    out = activated_projection_packed(m, dev(quats), dev(np.log(scales)), None, dev(view), dev(Ks), 320, 240,
+                                      viewspace_points=vsp)
+    bid, cid, gid = (host(out[k]) for k in ("batch_ids", "camera_ids", "gaussian_ids"))
+    nnz = cid.size
+    assert 0 < nnz < B * C * N
+    dense = rng.normal(size=(B, C, N, K)).astype(np.float32)
+    ids = {"camera_ids": out["camera_ids"], "gaussian_ids": out["gaussian_ids"]}
+    if B > 1:
+        ids["batch_ids"] = out["batch_ids"]
+    rows = host(g._gsplat_core.packed_rows_gather(dev(dense), ids))
+    np.testing.assert_array_equal(rows, dense[bid, cid, gid])
+    v = rng.normal(size=(nnz, K)).astype(np.float32)
+    back = host(g._gsplat_core.packed_rows_scatter(dev(v), out["rank"], B, C, N))
+    exp = np.zeros_like(dense)
+    exp[bid, cid, gid] = v
+    np.testing.assert_array_equal(back, exp)
+    # the viewspace proxy's gradient: the means2d rows' cotangent at their slots
+    w = torch.from_numpy(rng.normal(size=(nnz, 2)).astype(np.float32)).cuda()
+    (out["means2d"] * w).sum().backward()
+    exp2 = np.zeros((B, C, N, 2), np.float32)
+    exp2[bid, cid, gid] = host(w)
+    np.testing.assert_array_equal(host(vsp.grad), exp2)
 
 
 def _packed_image_ids(rng, layout, I, nnz):
