@@ -264,7 +264,10 @@ __device__ __forceinline__ void block_sum12_store(float vals[12], float* __restr
 // the Gaussian's pairs (in camera order) takes v_opac's place, and
 // v_viewspace (packed layout, if non-null) receives each (camera, Gaussian)
 // pair's means2d cotangent densely, zero where the pair has no row.
-template <bool ACT>
+// PK: the packed layout's per-row opacity cotangent and dense viewspace
+// gradient are read / written (a separate instantiation: the two extra
+// arguments' registers would cost the others a wave per SIMD).
+template <bool ACT, bool PK = false>
 __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
     const float* __restrict__ means, const float* __restrict__ covars, const float* __restrict__ quats,
     const float* __restrict__ scales, const float* __restrict__ viewmats, const float* __restrict__ Ks, int64_t C,
@@ -322,7 +325,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
       }
       // the dense viewspace proxy's gradient: this pair's means2d cotangent,
       // zero for a pair without a row
-      if (v_viewspace && in_range) {
+      if (PK && v_viewspace && in_range) {
         float vx = 0.0f, vy = 0.0f;
         if (valid) {
           vx = v_means2d[idx * 2];
@@ -339,7 +342,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
 #pragma unroll
     for (int i = 0; i < 12; ++i) vm_part[i] = 0.0f;
     if (valid) {
-      if constexpr (ACT) {
+      if constexpr (ACT && PK) {
         if (v_opac_rows) v_opac_sum += v_opac_rows[idx];
       }
       const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
@@ -413,7 +416,7 @@ __global__ void __launch_bounds__(kProjBlock) projection_bwd_kernel(
       for (int i = 0; i < 3; ++i) vs[i] = vs[i] * s[i];  // d exp(x) / dx = exp(x)
       if (v_logits) {
         const float o = sigmoid_of(logits[g]);
-        if (v_opac_rows)
+        if (PK && v_opac_rows)
           v_logits[g] = (v_opac_sum * (1.0f - o)) * o;
         else
           v_logits[g] = v_opac ? (v_opac[g] * (1.0f - o)) * o : 0.0f;
@@ -436,12 +439,17 @@ void launch_projection_bwd(bool act, dim3 grid, hipStream_t s, const float* mean
                            float* v_quats, float* v_scales, float* vm_partials, const float* logits,
                            const float* v_opac, float* v_logits, const uint64_t* pmask,
                            const int32_t* pprefix, const float* v_opac_rows, float* v_viewspace) {
-  if (act)
+  if (act && (v_opac_rows || v_viewspace))
+    projection_bwd_kernel<true, true><<<grid, kProjBlock, 0, s>>>(
+        means, covars, quats, scales, viewmats, Ks, C, N, p, radii, conics, compensations, v_means2d, v_depths,
+        v_conics, v_compensations, v_means, v_covars, v_quats, v_scales, vm_partials, logits, v_opac, v_logits, pmask,
+        pprefix, v_opac_rows, v_viewspace);
+  else if (act)
     projection_bwd_kernel<true><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p, radii,
                                                             conics, compensations, v_means2d, v_depths, v_conics,
                                                             v_compensations, v_means, v_covars, v_quats, v_scales,
                                                             vm_partials, logits, v_opac, v_logits, pmask, pprefix,
-                                                            v_opac_rows, v_viewspace);
+                                                            nullptr, nullptr);
   else
     projection_bwd_kernel<false><<<grid, kProjBlock, 0, s>>>(means, covars, quats, scales, viewmats, Ks, C, N, p,
                                                              radii, conics, compensations, v_means2d, v_depths,
