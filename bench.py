@@ -152,6 +152,14 @@ def main():
                                     W, H, ts, scene.sh_degree, viewspace_points=viewspace,
                                     background=scene.background, far_plane=scene.far_plane, accutile=accutile,
                                     packed=packed)
+        elif not forward_only and loss_mode == "l1":
+            # the trainer's value_and_grad: loss and gradients in one call
+            # (the same kernels as the render, loss and backward below)
+            _, out, _ = R.render_rgb_model_l1_value_and_grad(
+                means, quats, log_scales, colors, opacity_logits, viewmats, Ks, target, W, H, ts,
+                background=scene.background, opacities_in_projection=scene.opacities_in_projection,
+                far_plane=scene.far_plane, accutile=accutile)
+            return out
         else:
             out = R.render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, W, H, ts,
                                      background=scene.background,
@@ -222,6 +230,8 @@ def main():
     # reference's per-evaluation operation counts x the evaluations up to
     # each pixel's last contributor).
     blocks, grid_words = bucket_blocks(NC, N, n_img, tw, th)
+    rad = out["radii"].reshape(n_img, N, 2)
+    n_seen = int(((rad[..., 0] > 0) & (rad[..., 1] > 0)).any(dim=0).sum())
     n_tiles = n_img * tw * th
     units = {
         "raster_bwd": ("flops", BWD_FLOPS_PER_EVAL * e_bwd),
@@ -243,7 +253,12 @@ def main():
         # writes the logits' gradient (backward)
         "projection_fwd": ("bytes", (72 + (4 if scene.opacities_in_projection else 0)) * NC + 8 * N),
         "projection_bwd": ("bytes", (80 + 40 * n_img) * N + 12 * N),
-        "sh_camera_fwd": ("bytes", (12 + 12 * K + 12 * n_img) * N),
+        # the camera colours' forward reads the radii (8 B per pair) and the
+        # means and coefficients of the N_s rows some camera sees (the other
+        # rows are in no tile list: colour 0), and writes every colour; the
+        # backward reads every row and colour cotangent and writes every
+        # gradient row
+        "sh_camera_fwd": ("bytes", 8 * NC + (12 + 12 * K) * n_seen + 12 * NC),
         "sh_camera_bwd": ("bytes", (24 + 24 * K + 12 * n_img) * N),
         "isect_count_scan": ("bytes", 20 * NC),
         "isect_depth_keys": ("bytes", 12 * NC),

@@ -23,6 +23,12 @@ const at::Tensor& require_key(const TensorMap& inputs, const char* key) {
   return it->second;
 }
 
+// absent optional input -> undefined tensor
+at::Tensor get_or_undefined(const TensorMap& inputs, const char* key) {
+  auto it = inputs.find(key);
+  return it == inputs.end() ? at::Tensor() : it->second;
+}
+
 // binding.cpp:37-45: absent optional input -> empty float32 array
 at::Tensor get_or_empty(const TensorMap& inputs, const char* key) {
   auto it = inputs.find(key);
@@ -355,10 +361,12 @@ py::dict quat_scale_to_covar_preci_backward(const TensorMap& inputs, const Tenso
 
 // Caller-side SH glue fused into the kernels (addition to the reference
 // surface; see gsplat_sh_camera_colors_forward).
+// Optional forward input "radii" (the projection's): rows no camera sees
+// are skipped (colour 0).
 at::Tensor sh_camera_colors_forward(int degrees_to_use, const TensorMap& inputs) {
   return gsplat_core::gsplat_sh_camera_colors_forward(
       degrees_to_use, require_key(inputs, "means"), require_key(inputs, "viewmats"), require_key(inputs, "features_dc"),
-      require_key(inputs, "features_rest"));
+      require_key(inputs, "features_rest"), get_or_undefined(inputs, "radii"));
 }
 
 py::dict sh_camera_colors_backward(int degrees_to_use, const TensorMap& inputs, const TensorMap& cotangents) {
@@ -598,6 +606,25 @@ py::dict render_rgb_backward(const TensorMap& inputs, const TensorMap& forward_o
   return r;
 }
 
+// Loss and gradients of the RGB step with the L1 image loss in one call
+// (gsplat_render_rgb_l1_value_and_grad): {"loss", the forward's keys,
+// "v_means", "v_quats", "v_log_scales", "v_opacity_logits", "v_colors"}.
+py::dict render_rgb_l1_value_and_grad(const TensorMap& inputs, const at::Tensor& target, int image_width,
+                                      int image_height, int tile_size, float eps2d, float near_plane, float far_plane,
+                                      bool opacities_in_projection, bool accutile) {
+  auto out = gsplat_core::gsplat_render_rgb_l1_value_and_grad(
+      render_rgb_input(inputs, image_width, image_height, tile_size, eps2d, near_plane, far_plane,
+                       opacities_in_projection, accutile),
+      target);
+  py::dict r;
+  r["loss"] = out[0];
+  const size_t nf = sizeof(kRenderRGBKeys) / sizeof(kRenderRGBKeys[0]);
+  for (size_t i = 0; i < nf; ++i) r[kRenderRGBKeys[i]] = out[1 + i];
+  const char* const grads[] = {"v_means", "v_quats", "v_log_scales", "v_opacity_logits", "v_colors"};
+  for (size_t i = 0; i < 5; ++i) r[grads[i]] = out[1 + nf + i];
+  return r;
+}
+
 // Template smoke entries of the reference (gsplat_core/dummy.cpp:7-13).
 int dummy_add(int a, int b) { return a + b; }
 
@@ -687,6 +714,10 @@ PYBIND11_MODULE(_gsplat_core, m) {
   m.def("render_rgb_backward", &render_rgb_backward, py::arg("inputs"), py::arg("forward_outputs"),
         py::arg("cotangents"), py::arg("image_width"), py::arg("image_height"), py::arg("tile_size"),
         py::arg("eps2d") = 0.3f, py::arg("accutile") = false, py::arg("viewmats_requires_grad") = false);
+  m.def("render_rgb_l1_value_and_grad", &render_rgb_l1_value_and_grad, py::arg("inputs"), py::arg("target"),
+        py::arg("image_width"), py::arg("image_height"), py::arg("tile_size"), py::arg("eps2d") = 0.3f,
+        py::arg("near_plane") = 0.01f, py::arg("far_plane") = 1.0e10f, py::arg("opacities_in_projection") = false,
+        py::arg("accutile") = false);
   m.def("l1_loss_forward", &l1_loss_forward, py::arg("image"), py::arg("target"));
   m.def("l1_loss_backward", &l1_loss_backward, py::arg("image"), py::arg("target"), py::arg("grad"));
   m.def("image_loss_forward", &image_loss_forward, py::arg("image"), py::arg("target"), py::arg("window_size") = 11,

@@ -4,6 +4,9 @@
 // order with the same inputs.
 #include "gsplat_render.h"
 
+#include <map>
+#include <mutex>
+
 #include "core_util.h"
 #include "gsplat_intersect.h"
 #include "gsplat_projection.h"
@@ -144,6 +147,47 @@ std::vector<array> gsplat_render_rgb_backward(const RenderRGBInput& in, const st
   const auto pg = gsplat_activated_projection_backward(pb, in.opacity_logits, v_opac);
   return {pg[0], pg[1], pg[2], pg[3], sum_images(g[kRasterVColors], C, in.colors),
           viewmats_requires_grad ? pg[4] : empty_f32()};
+}
+
+namespace {
+
+// A device scalar 1.0 (the loss's own cotangent) per device, created once
+// and never written.
+const array& device_one(const array& like) {
+  static std::mutex mu;
+  static std::map<int, array> ones;
+  const std::lock_guard<std::mutex> lock(mu);
+  const int dev = like.device().index();
+  auto it = ones.find(dev);
+  if (it == ones.end()) it = ones.emplace(dev, at::ones({}, f32_like(like))).first;
+  return it->second;
+}
+
+}  // namespace
+
+std::vector<array> gsplat_render_rgb_l1_value_and_grad(const RenderRGBInput& in, const array& target_in) {
+  std::vector<array> fwd = gsplat_render_rgb_forward(in);
+  const array& image = fwd[kRenderRGBColors];
+  if (target_in.scalar_type() != at::kFloat || target_in.numel() != image.numel() ||
+      target_in.device() != image.device())
+    throw std::runtime_error("render_rgb_l1_value_and_grad: target must be float32 with one value per rendered "
+                             "colour, on the render's device.");
+  const c10::DeviceGuard guard(image.device());
+  const array target = contig(target_in).view(image.sizes());
+  array loss = gsplat_l1_loss_forward(image, target, in.s);
+  // d loss / d image with d loss / d loss = 1; no target gradient
+  array v_image = at::empty(image.sizes(), f32_like(image));
+  if (image.numel() > 0)
+    check(gsplat_hip_l1_loss_bwd(image.data_ptr<float>(), target.data_ptr<float>(), image.numel(),
+                                 device_one(image).data_ptr<float>(), v_image.data_ptr<float>(), nullptr,
+                                 stream_for(in.s, image)));
+  std::vector<array> grads = gsplat_render_rgb_backward(in, fwd, v_image, array(), false);
+  std::vector<array> out;
+  out.reserve(1 + fwd.size() + 5);
+  out.push_back(loss);
+  out.insert(out.end(), fwd.begin(), fwd.end());
+  out.insert(out.end(), grads.begin(), grads.begin() + 5);
+  return out;
 }
 
 }  // namespace gsplat_core

@@ -55,19 +55,34 @@ CamDims validate_camera(const char* op, int degree, const array& means, const ar
   return d;
 }
 
+// The optional radii of the camera colour functions: [..., C, N, 2] int32 on
+// the means' device, or none (undefined or empty).
+const int32_t* camera_radii(const array& radii, const CamDims& d, const array& means, array& keep, const char* what) {
+  if (!radii.defined() || radii.numel() == 0) return nullptr;
+  const std::string o(what);
+  if (radii.scalar_type() != at::kInt) throw std::runtime_error(o + ": radii must be int32.");
+  if (radii.numel() != d.B * d.C * d.N * 2 || radii.size(-1) != 2)
+    throw std::runtime_error(o + ": radii must have shape [..., C, N, 2].");
+  if (radii.device() != means.device()) throw std::runtime_error(o + ": radii must be on the means' device.");
+  keep = contig(radii);
+  return keep.data_ptr<int32_t>();
+}
+
 }  // namespace
 
 array gsplat_sh_camera_colors_forward(int degree, const array& means_in, const array& viewmats_in, const array& dc_in,
-                                      const array& rest_in, StreamOrDevice s) {
+                                      const array& rest_in, const array& radii_in, StreamOrDevice s) {
   const CamDims d = validate_camera("sh_camera_colors_forward", degree, means_in, viewmats_in, dc_in, rest_in);
   const c10::DeviceGuard guard(means_in.device());
   const array means = contig(means_in), viewmats = contig(viewmats_in), dc = contig(dc_in), rest = contig(rest_in);
+  array radii;
+  const int32_t* rp = camera_radii(radii_in, d, means, radii, "sh_camera_colors_forward");
   std::vector<int64_t> shape(means.sizes().begin(), means.sizes().end() - 2);
   shape.insert(shape.end(), {d.C, d.N, 3});
   array colors = at::empty(shape, f32_like(means));
   check(gsplat_hip_sh_camera_colors_fwd(degree, means.data_ptr<float>(), viewmats.data_ptr<float>(),
-                                        dc.data_ptr<float>(), d.R > 0 ? rest.data_ptr<float>() : nullptr, d.B, d.C,
-                                        d.N, d.R, colors.data_ptr<float>(), stream_for(s, means)));
+                                        dc.data_ptr<float>(), d.R > 0 ? rest.data_ptr<float>() : nullptr, rp, d.B,
+                                        d.C, d.N, d.R, colors.data_ptr<float>(), stream_for(s, means)));
   return colors;
 }
 

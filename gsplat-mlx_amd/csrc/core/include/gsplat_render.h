@@ -55,4 +55,14 @@ std::vector<array> gsplat_render_rgb_backward(const RenderRGBInput& input, const
                                               const array& v_render_colors, const array& v_render_alphas,
                                               bool viewmats_requires_grad);
 
+// The step's loss and gradients in one call, as the reference trainer's
+// value_and_grad of the L1 image loss (train_image_fitting_3dgs_mlx.py:
+// 165-237): the forward above, loss = mean |render_colors - target|, its
+// image cotangent (sign(render - target) / count, the L1 backward with
+// d loss / d loss = 1) and the backward above. Returns {loss, the forward's
+// outputs in RenderRGBOutputIndex order, v_means, v_quats, v_log_scales,
+// v_opacity_logits, v_colors}. target: float32, one value per rendered
+// colour (viewed as render_colors' shape).
+std::vector<array> gsplat_render_rgb_l1_value_and_grad(const RenderRGBInput& input, const array& target);
+
 }  // namespace gsplat_core

@@ -41,9 +41,13 @@ std::vector<array> gsplat_spherical_harmonics_backward(const SphericalHarmonicsB
 // clamp(SH(normalize(means - campos[c]); [dc, rest]) + 0.5, 0, 1) with
 // campos[c] = -R^T t of viewmats[c] = [R | t], for means [B, N, 3], viewmats
 // [B, C, 4, 4], features_dc [B, N, 3], features_rest [B, N, R, 3]
-// (R >= (degree + 1)^2 - 1).
+// (R >= (degree + 1)^2 - 1). radii (optional: undefined or empty for none):
+// the projection's [B, C, N, 2]; rows whose radii are not both positive in
+// any camera (no tile, so no render reads them) are then skipped and get
+// colour 0.
 array gsplat_sh_camera_colors_forward(int degree, const array& means, const array& viewmats, const array& features_dc,
-                                      const array& features_rest, StreamOrDevice s = {});
+                                      const array& features_rest, const array& radii = array(),
+                                      StreamOrDevice s = {});
 
 // Gradients {v_means, v_features_dc, v_features_rest} of the above, summed
 // over cameras (viewmats get none).

@@ -11,6 +11,8 @@
 //
 // Math follows gsplat_core/gsplat_spherical_harmonics.cpp:112-425 in the same
 // operation order (FMA contraction off for this file).
+#include <atomic>
+
 #include "common.hpp"
 
 namespace gsplat_hip {
@@ -445,11 +447,27 @@ __device__ __forceinline__ void view_dir_vjp(const float vn[3], const float n[3]
 
 __device__ __forceinline__ float clamp01(float x) { return x < 0.0f ? 0.0f : (x > 1.0f ? 1.0f : x); }
 
+// Whether some camera sees Gaussian n of batch b: both radii positive in at
+// least one of the C cameras (radii [B, C, N, 2], the projection's output).
+// A Gaussian no camera sees has no tile (gsplat_intersect.cpp:74-76 gives it
+// none), so the rasterizer never reads its colour and its colour gradient
+// is zero.
+__device__ __forceinline__ bool seen_by_any(const int32_t* __restrict__ radii, int64_t b, int64_t C, int64_t N,
+                                            int64_t n) {
+  bool seen = false;
+  for (int64_t c = 0; c < C; ++c) {
+    const int2 r = *reinterpret_cast<const int2*>(radii + ((b * C + c) * N + n) * 2);
+    seen = seen | ((r.x > 0) & (r.y > 0));
+  }
+  return seen;
+}
+
 template <int DEG>
 __global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __restrict__ means,
                                                               const float* __restrict__ viewmats,
                                                               const float* __restrict__ dc,
-                                                              const float* __restrict__ rest, int64_t C, int64_t N,
+                                                              const float* __restrict__ rest,
+                                                              const int32_t* __restrict__ radii, int64_t C, int64_t N,
                                                               int64_t R, uint32_t r3_magic,
                                                               float* __restrict__ colors) {
   constexpr int A = (DEG + 1) * (DEG + 1);
@@ -471,13 +489,19 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __res
   if (t >= cnt) return;
   const int64_t g = b * N + e0 + t;
   const float* co = sc + t * PW;
+  // rows no camera sees (with radii) get colour 0
+  const bool live = !radii || seen_by_any(radii, b, C, N, e0 + t);
   for (int64_t c = 0; c < C; ++c) {
+    float* out = colors + ((b * C + c) * N + e0 + t) * 3;
+    if (!live) {
+      out[0] = out[1] = out[2] = 0.0f;
+      continue;
+    }
     float cp[3];
     camera_centre(viewmats + (b * C + c) * 16, cp);
     float d[3], n[3], raw[3];
     view_dir(means + g * 3, cp, d, n);
     sh_eval<DEG>(n, co, raw);
-    float* out = colors + ((b * C + c) * N + e0 + t) * 3;
     out[0] = clamp01(raw[0] + 0.5f);
     out[1] = clamp01(raw[1] + 0.5f);
     out[2] = clamp01(raw[2] + 0.5f);
@@ -637,11 +661,19 @@ __device__ __forceinline__ void slab_rows(const float* __restrict__ means, const
 // per lane), and no block barrier is taken (the waves are independent).
 // Groups that are partial or whose span is not 16-byte aligned read their
 // rows per lane instead.
+//
+// With radii (the projection's [B, C, N, 2]), rows that no camera sees
+// (seen_by_any) are neither read nor evaluated: their colours are written as
+// 0, and a float4 of the rest span is loaded only when it holds a float of
+// a seen row. The rasterizer reads no such row, so the render is unchanged.
+// With one camera the radii are loaded one group ahead of the rows they
+// select.
 template <int DEG>
 __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* __restrict__ means,
                                                                   const float* __restrict__ viewmats,
                                                                   const float* __restrict__ dc,
-                                                                  const float* __restrict__ rest, int64_t C,
+                                                                  const float* __restrict__ rest,
+                                                                  const int32_t* __restrict__ radii, int64_t C,
                                                                   int64_t N, float* __restrict__ colors) {
   constexpr int A = (DEG + 1) * (DEG + 1);
   constexpr int R3 = (A - 1) * 3;
@@ -659,14 +691,36 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
   auto vec_ok = [&](int64_t grp) {
     return R3 > 0 && N - grp * kWave >= kWave && (reinterpret_cast<uintptr_t>(span(grp)) & 15) == 0;
   };
-  // the group's rest span (clamped: every lane loads PER float4s of it)
-  auto fetch = [&](int64_t grp, int i) {
-    return reinterpret_cast<const float4*>(span(grp))[min(lane + i * kWave, T4 - 1)];
+  // radii of this lane's row of a group (one camera: held one group ahead)
+  int2 rad = make_int2(0, 0);
+  auto fetch_rad = [&](int64_t grp) {
+    const int64_t n = grp * kWave + lane;
+    if (radii && C == 1 && n < N) rad = *reinterpret_cast<const int2*>(radii + (b * N + n) * 2);
+  };
+  // the group's rows that some camera sees, as a wave mask (every row
+  // without radii); one camera reads the radii fetch_rad loaded
+  auto seen_rows = [&](int64_t grp) -> uint64_t {
+    if (!radii) return ~0ull;
+    const int64_t n = grp * kWave + lane;
+    const bool seen = n < N && (C == 1 ? (rad.x > 0) & (rad.y > 0) : seen_by_any(radii, b, C, N, n));
+    return __ballot(seen);
+  };
+  // the group's rest span (clamped: every lane loads PER float4s of it);
+  // float4 j holds floats 4j..4j+3, i.e. rows 4j / R3 and (4j + 3) / R3. A
+  // float4 of unseen rows only is read from the span's first float4 instead
+  // (the loads stay unconditional; the lanes so redirected share one line)
+  // and lands in LDS words no seen row reads.
+  auto fetch = [&](int64_t grp, int i, uint64_t seen, int ln) {
+    constexpr int RD = R3 > 0 ? R3 : 1;
+    const int j = min(ln + i * kWave, T4 - 1);
+    const int r0 = (4 * j) / RD, r1 = (4 * j + 3) / RD;
+    const bool need = ((seen >> r0) | (seen >> r1)) & 1ull;
+    return reinterpret_cast<const float4*>(span(grp))[need ? j : 0];
   };
   // dc and mean of this lane's Gaussian of the group (12 bytes each)
-  auto fetch_row = [&](int64_t grp, float (&p)[6]) {
+  auto fetch_row = [&](int64_t grp, uint64_t seen, float (&p)[6]) {
     const int64_t g = b * N + grp * kWave + lane;
-    const bool active = grp * kWave + lane < N;
+    const bool active = grp * kWave + lane < N && ((seen >> lane) & 1ull);
 #pragma clang loop unroll(full)
     for (int k = 0; k < 3; ++k) {
       p[k] = active ? dc[g * 3 + k] : 0.0f;
@@ -675,18 +729,24 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
   };
   float4 r[PER];
   float p[6];
+  uint64_t seen_next = 0;
   int64_t grp = static_cast<int64_t>(blockIdx.x) * (kShSlab / kWave) + wave;
   if (grp < n_groups) {
-    fetch_row(grp, p);
+    fetch_rad(grp);
+    seen_next = seen_rows(grp);
+    fetch_row(grp, seen_next, p);
     if (vec_ok(grp)) {
 #pragma clang loop unroll(full)
-      for (int i = 0; i < PER; ++i) r[i] = fetch(grp, i);
+      for (int i = 0; i < PER; ++i) r[i] = fetch(grp, i, seen_next, lane);
     }
+    if (grp + stride < n_groups) fetch_rad(grp + stride);
   }
   for (; grp < n_groups; grp += stride) {
     const int64_t w0 = grp * kWave;
     const int rows = static_cast<int>(min<int64_t>(kWave, N - w0));
+    const uint64_t seen = seen_next;
     const bool active = lane < rows;
+    const bool live = (seen >> lane) & 1ull;
     float co[A * 3], m[3];
 #pragma clang loop unroll(full)
     for (int k = 0; k < 3; ++k) {
@@ -712,24 +772,34 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
       } else {
         const float* src = span(grp);
 #pragma clang loop unroll(full)
-        for (int i = 0; i < R3; ++i) co[3 + i] = active ? src[lane * R3 + i] : 0.0f;
+        for (int i = 0; i < R3; ++i) co[3 + i] = active && live ? src[lane * R3 + i] : 0.0f;
       }
     }
     if (grp + stride < n_groups) {  // the next group's loads, in flight during the compute
-      fetch_row(grp + stride, p);
+      seen_next = seen_rows(grp + stride);
+      fetch_row(grp + stride, seen_next, p);
       if (vec_ok(grp + stride)) {
+        // the lane index is opaque here, so the loop does not hoist the
+        // float4 indices and their rows (registers held across it)
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
 #pragma clang loop unroll(full)
-        for (int i = 0; i < PER; ++i) r[i] = fetch(grp + stride, i);
+        for (int i = 0; i < PER; ++i) r[i] = fetch(grp + stride, i, seen_next, ln);
       }
+      if (grp + 2 * stride < n_groups) fetch_rad(grp + 2 * stride);
     }
     if (active) {
       for (int64_t c = 0; c < C; ++c) {
+        float* out = colors + ((b * C + c) * N + w0 + lane) * 3;
+        if (!live) {
+          out[0] = out[1] = out[2] = 0.0f;
+          continue;
+        }
         float cp[3];
         camera_centre(viewmats + (b * C + c) * 16, cp);
         float d[3], n[3], raw[3];
         view_dir(m, cp, d, n);
         sh_eval<DEG>(n, co, raw);
-        float* out = colors + ((b * C + c) * N + w0 + lane) * 3;
         out[0] = clamp01(raw[0] + 0.5f);
         out[1] = clamp01(raw[1] + 0.5f);
         out[2] = clamp01(raw[2] + 0.5f);
@@ -738,23 +808,23 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
   }
 }
 
-// Workgroups of `kernel` resident on the current device at once (the
-// occupancy calculator's blocks per CU x CUs), computed once per device;
-// 0 when the runtime cannot tell.
-template <typename Kernel>
-int resident_blocks(Kernel kernel, int block) {
+// Workgroups of kernel KernelFn (blocks of `block` threads) resident on the
+// current device at once (the occupancy calculator's blocks per CU x CUs),
+// computed once per kernel and device; 0 when the runtime cannot tell.
+template <auto KernelFn>
+int resident_blocks(int block) {
   constexpr int kMaxDevices = 64;
-  static int cached[kMaxDevices] = {};
+  static std::atomic<int> cached[kMaxDevices];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
-  if (cached[dev] == 0) {
+  if (cached[dev].load(std::memory_order_relaxed) == 0) {
     int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, 0) != hipSuccess ||
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, KernelFn, block, 0) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
       return 0;
-    cached[dev] = std::max(1, per_cu * cus);
+    cached[dev].store(std::max(1, per_cu * cus), std::memory_order_relaxed);
   }
-  return cached[dev];
+  return cached[dev].load(std::memory_order_relaxed);
 }
 
 template <int DEG>
@@ -834,8 +904,8 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
 constexpr bool slab_degree(int deg) { return deg == 0 || deg == 1 || deg == 3; }
 
 template <int DEG>
-int launch_cam_fwd(const float* means, const float* viewmats, const float* dc, const float* rest, int64_t B, int64_t C,
-                   int64_t N, int64_t R, float* colors, hipStream_t s) {
+int launch_cam_fwd(const float* means, const float* viewmats, const float* dc, const float* rest, const int32_t* radii,
+                   int64_t B, int64_t C, int64_t N, int64_t R, float* colors, hipStream_t s) {
   {
     KernelTimer timer("sh_camera_fwd", s);
     bool slab = false;
@@ -843,16 +913,16 @@ int launch_cam_fwd(const float* means, const float* viewmats, const float* dc, c
       if (R == (DEG + 1) * (DEG + 1) - 1) {
         // a resident grid (each wave walks several groups), at most one wave per group
         const int64_t blocks = grid_for(grid_for(N, kWave), kShSlab / kWave);
-        const int res = resident_blocks(sh_cam_fwd_slab_kernel<DEG>, kShSlab);
+        const int res = resident_blocks<sh_cam_fwd_slab_kernel<DEG>>(kShSlab);
         const int64_t per_batch = res > 0 ? std::max<int64_t>(1, res / B) : blocks;
         const dim3 grid(static_cast<unsigned>(std::min<int64_t>(blocks, per_batch)), static_cast<unsigned>(B));
-        sh_cam_fwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, C, N, colors);
+        sh_cam_fwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, radii, C, N, colors);
         slab = true;
       }
     }
     if (!slab) {
       const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
-      sh_cam_fwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, viewmats, dc, rest, C, N, R,
+      sh_cam_fwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, viewmats, dc, rest, radii, C, N, R,
                                                         magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), colors);
     }
   }
@@ -963,8 +1033,9 @@ static int check_cam_args(int32_t degree, int64_t B, int64_t C, int64_t N, int64
 }
 
 extern "C" int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* viewmats,
-                                               const float* features_dc, const float* features_rest, int64_t B,
-                                               int64_t C, int64_t N, int64_t R, float* colors, void* stream) {
+                                               const float* features_dc, const float* features_rest,
+                                               const int32_t* radii, int64_t B, int64_t C, int64_t N, int64_t R,
+                                               float* colors, void* stream) {
   const char* what = "sh_camera_colors_forward";
   int rc = check_cam_args(degree, B, C, N, R, what);
   if (rc) return rc;
@@ -973,11 +1044,11 @@ extern "C" int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* mean
     return invalid(std::string(what) + ": null pointer.");
   hipStream_t s = as_stream(stream);
   switch (degree) {
-    case 0: return launch_cam_fwd<0>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
-    case 1: return launch_cam_fwd<1>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
-    case 2: return launch_cam_fwd<2>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
-    case 3: return launch_cam_fwd<3>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
-    default: return launch_cam_fwd<4>(means, viewmats, features_dc, features_rest, B, C, N, R, colors, s);
+    case 0: return launch_cam_fwd<0>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
+    case 1: return launch_cam_fwd<1>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
+    case 2: return launch_cam_fwd<2>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
+    case 3: return launch_cam_fwd<3>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
+    default: return launch_cam_fwd<4>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
   }
 }
 

@@ -352,12 +352,18 @@ class _ShCameraColors(torch.autograd.Function):
     """colors [B, C, N, 3] = clamp(SH(normalize(means - campos[c])) + 0.5, 0, 1)
     with campos[c] = -R^T t of viewmats[c] and the coefficient concat /
     broadcast of the reference caller (scanner_points_training_utils.py:
-    1005-1034) fused into the kernels. The view matrices carry no gradient."""
+    1005-1034) fused into the kernels. The view matrices carry no gradient.
+    With radii (the projection's [B, C, N, 2]), the forward skips the rows
+    that no camera sees (radii not both positive in any camera: no tile, so
+    no render reads them and the rasterizer gives them no colour gradient)
+    and writes their colours as 0."""
 
     @staticmethod
-    def forward(ctx, degrees_to_use, means, viewmats, features_dc, features_rest):
+    def forward(ctx, degrees_to_use, means, viewmats, features_dc, features_rest, radii):
         ctx.set_materialize_grads(False)  # unused outputs get no zero-filled cotangent
         inputs = {"means": means, "viewmats": viewmats, "features_dc": features_dc, "features_rest": features_rest}
+        if radii is not None:
+            inputs["radii"] = radii
         colors = _C.sh_camera_colors_forward(degrees_to_use, inputs)
         ctx.save_for_backward(means, viewmats, features_dc, features_rest)
         ctx.degree = degrees_to_use
@@ -368,14 +374,15 @@ class _ShCameraColors(torch.autograd.Function):
         means, viewmats, features_dc, features_rest = ctx.saved_tensors
         inputs = {"means": means, "viewmats": viewmats, "features_dc": features_dc, "features_rest": features_rest}
         out = _C.sh_camera_colors_backward(ctx.degree, inputs, {"v_colors": v_colors.contiguous()})
-        return None, out["v_means"], None, out["v_features_dc"], out["v_features_rest"]
+        return None, out["v_means"], None, out["v_features_dc"], out["v_features_rest"], None
 
 
-def sh_camera_colors(degrees_to_use, means, viewmats, features_dc, features_rest):
-    """Fused camera colours; viewmats must not require grad."""
+def sh_camera_colors(degrees_to_use, means, viewmats, features_dc, features_rest, radii=None):
+    """Fused camera colours; viewmats must not require grad. radii (optional,
+    the projection's): the forward skips the rows no camera sees (colour 0)."""
     if viewmats.requires_grad:
         raise ValueError("sh_camera_colors: view-matrix gradients are not supported; detach viewmats.")
-    return _ShCameraColors.apply(degrees_to_use, means, viewmats, features_dc, features_rest)
+    return _ShCameraColors.apply(degrees_to_use, means, viewmats, features_dc, features_rest, radii)
 
 
 class _RasterizeToPixels3DGS(torch.autograd.Function):
@@ -591,6 +598,28 @@ def render_rgb(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, b
         opacities_in_projection, accutile)
     return {"render_colors": rc, "render_alphas": ra, "last_ids": li, "radii": radii, "tiles_per_gauss": tpg,
             "flatten_ids": flat, "isect_ids": ids, "tile_offsets": offs}
+
+
+def render_rgb_l1_value_and_grad(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, target, backgrounds,
+                                 image_width, image_height, tile_size, far_plane=1e10, opacities_in_projection=False,
+                                 accutile=False):
+    """Loss, render outputs and parameter gradients of the RGB step with the
+    L1 image loss in one C++ call, as the reference trainer's value_and_grad
+    (train_image_fitting_3dgs_mlx.py:165-237): the forward of render_rgb,
+    loss = mean |render_colors - target|, and the backward with d loss /
+    d loss = 1, without an autograd graph. Returns (loss, render dict, grads
+    dict with v_means, v_quats, v_log_scales, v_colors, v_opacity_logits)."""
+    inputs = {"means": means.detach(), "quats": quats.detach(), "log_scales": log_scales.detach(),
+              "opacity_logits": opacity_logits.detach(), "colors": colors.detach(), "viewmats": viewmats.detach(),
+              "Ks": Ks.detach()}
+    if _nonempty(backgrounds):
+        inputs["backgrounds"] = backgrounds.detach()
+    out = _C.render_rgb_l1_value_and_grad(inputs, target.detach(), image_width, image_height, tile_size, 0.3, 0.01,
+                                          far_plane, opacities_in_projection, accutile)
+    grads = {k: out[k] for k in ("v_means", "v_quats", "v_log_scales", "v_colors", "v_opacity_logits")}
+    render = {k: out[k] for k in ("render_colors", "render_alphas", "last_ids", "radii", "tiles_per_gauss",
+                                  "flatten_ids", "isect_ids", "tile_offsets")}
+    return out["loss"], render, grads
 
 
 class _L1Loss(torch.autograd.Function):

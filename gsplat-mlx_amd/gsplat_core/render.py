@@ -28,6 +28,7 @@ import torch
 from . import _gsplat_core as _C
 from .autograd import (activated_projection, activated_projection_packed, image_loss, l1_loss as _l1_loss,
                        packed_rows, projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs, render_rgb,
+                       render_rgb_l1_value_and_grad,
                        sh_camera_colors, spherical_harmonics)
 
 
@@ -43,13 +44,15 @@ def camera_center_from_viewmat(viewmats: torch.Tensor) -> torch.Tensor:
     return -torch.matmul(rot.transpose(-1, -2), trans[..., None])[..., 0]
 
 
-def sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree):
+def sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree, radii=None):
     """scanner_points_training_utils.py:1011-1034. The normalisation, the
     coefficient concat / broadcast and the clip run inside the fused SH
     kernels when the camera centres need no gradient; otherwise the
-    reference's composition of elementwise ops and the SH operator runs."""
+    reference's composition of elementwise ops and the SH operator runs.
+    radii (the projection's, fused path only): the rows no camera sees, which
+    no render reads, are skipped in the forward (colour 0)."""
     if not viewmats.requires_grad:
-        return sh_camera_colors(sh_degree, means, viewmats.contiguous(), features_dc, features_rest)
+        return sh_camera_colors(sh_degree, means, viewmats.contiguous(), features_dc, features_rest, radii)
     return sh_colors_for_camera_unfused(means, features_dc, features_rest, viewmats, sh_degree)
 
 
@@ -168,7 +171,8 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
     pending = _intersect_begin(proj, width, height, tile_size, C, opac_img if accutile else None)
     # queued behind the intersection's count read-back: the GPU evaluates the
     # SH colours while the host waits for the count
-    colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)
+    # rows no camera sees are in no tile list: their colours are skipped
+    colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree, radii=proj["radii"])
     isect, offsets = _intersect_end(pending)
     render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, opac_img,
                                       offsets, isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
@@ -201,6 +205,22 @@ def render_rgb_model(means, quats, log_scales, colors, opacity_logits, viewmats,
                                       isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
     return {**render, "radii": proj["radii"], "tiles_per_gauss": isect["tiles_per_gauss"],
             "flatten_ids": isect["flatten_ids"], "isect_ids": isect["isect_ids"], "tile_offsets": offsets}
+
+
+def render_rgb_model_l1_value_and_grad(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, target, width,
+                                       height, tile_size, background=(0.0, 0.0, 0.0), opacities_in_projection=False,
+                                       far_plane=1e10, accutile=False):
+    """render_rgb_model's step with the L1 image loss as one value_and_grad
+    call (train_image_fitting_3dgs_mlx.py:165-237): returns (loss, the render
+    dict, {"v_means", "v_quats", "v_log_scales", "v_colors",
+    "v_opacity_logits"}); the same kernels as render_rgb_model followed by
+    l1_loss and backward, with no autograd graph in between."""
+    C = viewmats.shape[1]
+    bg = background_tensor(background, means.device)
+    bg = bg if C == 1 else bg.expand(C, -1)
+    return render_rgb_l1_value_and_grad(means, quats, log_scales, colors, opacity_logits, viewmats, Ks, target, bg,
+                                        width, height, tile_size, far_plane=far_plane,
+                                        opacities_in_projection=opacities_in_projection, accutile=accutile)
 
 
 def l1_loss(image: torch.Tensor, target: torch.Tensor) -> torch.Tensor:

@@ -216,10 +216,16 @@ int gsplat_hip_spherical_harmonics_bwd(int32_t degree, const float* dirs, const 
  * 0 < colour + 0.5 < 1 (the VJP of the reference's mx.clip, i.e. of
  * minimum(maximum(x, 0), 1): ties go to the bounds) and writes v_means, v_features_dc,
  * v_features_rest summed over the C cameras (inactive bases get 0); the view
- * matrices get no gradient. */
+ * matrices get no gradient.
+ * radii (forward; the projection's [B,C,N,2], or NULL): a Gaussian whose
+ * radii are not both positive in any camera has no tile
+ * (gsplat_intersect.cpp:74-76), so a render never reads its colour and the
+ * rasterizer gives it no colour gradient; given radii, the forward does not
+ * read such rows and writes their colours as 0. */
 int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* viewmats,
-                                    const float* features_dc, const float* features_rest, int64_t B,
-                                    int64_t C, int64_t N, int64_t R, float* colors, void* stream);
+                                    const float* features_dc, const float* features_rest,
+                                    const int32_t* radii, int64_t B, int64_t C, int64_t N, int64_t R,
+                                    float* colors, void* stream);
 int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const float* viewmats,
                                     const float* features_dc, const float* features_rest,
                                     const float* v_colors, int64_t B, int64_t C, int64_t N, int64_t R,

@@ -73,3 +73,52 @@ def test_fused_equals_composed(name, C, accutile, alphas_loss):
             assert_close_rel_summation(a[k], b[k], 1e-4, k)
         else:
             np.testing.assert_array_equal(a[k], b[k], err_msg=k)
+
+
+# The step's loss and gradients in one call (render_rgb_model_l1_value_and_grad,
+# the reference trainer's value_and_grad) against the same step through
+# autograd (render_rgb_model, l1_loss, backward): the same kernels, so the
+# loss, images and lists agree bit for bit and the gradients up to the order
+# of the rasterizer's float atomics.
+@pytest.mark.parametrize("C,accutile", [(1, False), (1, True), (3, False)])
+def test_l1_value_and_grad_equals_autograd(C, accutile):
+    import torch
+
+    from gsplat_core import render as R
+    from gsplat_core.scenes import make_scene
+
+    sc = make_scene("image_fit", seed=5, n=20000, width=200, height=152)
+    if C > 1:
+        from scipy.spatial.transform import Rotation
+
+        v0 = sc.viewmats[:, :1]
+        extra = []
+        for k in range(1, C):
+            v = v0.copy()
+            v[0, 0, :3, :3] = Rotation.from_euler("x", 0.04 * k).as_matrix().astype(np.float32) @ v[0, 0, :3, :3]
+            extra.append(v)
+        sc.viewmats = np.concatenate([v0] + extra, axis=1).astype(np.float32)
+        sc.Ks = np.repeat(sc.Ks[:, :1], C, axis=1)
+    rng = np.random.default_rng(C)
+    target = dev(rng.uniform(0, 1, (C, sc.height, sc.width, 3)).astype(np.float32))
+    names = ("means", "quats", "log_scales", "colors", "opacity_logits")
+    p = {k: dev(getattr(sc, k)).requires_grad_(True) for k in names}
+    args = (p["means"], p["quats"], p["log_scales"], p["colors"], p["opacity_logits"], dev(sc.viewmats[:, :C]),
+            dev(sc.Ks[:, :C]))
+    kw = dict(background=sc.background, opacities_in_projection=sc.opacities_in_projection,
+              far_plane=sc.far_plane, accutile=accutile)
+    print(f"l1 value_and_grad C={C} accutile={accutile}", flush=True)
+    out = R.render_rgb_model(*args, sc.width, sc.height, sc.tile_size, **kw)
+    loss = R.l1_loss(out["render_colors"], target.reshape(out["render_colors"].shape))
+    loss.backward()
+    loss2, render2, grads2 = R.render_rgb_model_l1_value_and_grad(*args, target, sc.width, sc.height, sc.tile_size,
+                                                                   **kw)
+    torch.cuda.synchronize()
+    assert render2["isect_ids"].numel() > 0
+    np.testing.assert_array_equal(host(loss2), host(loss))
+    for k in render2:
+        np.testing.assert_array_equal(host(render2[k]), host(out[k]), err_msg=k)
+    for k in names:
+        e = host(p[k].grad)
+        assert np.abs(e).max() > 0, k
+        assert_close_rel_summation(host(grads2["v_" + k]), e, 1e-4, k)

@@ -179,3 +179,44 @@ def test_errors():
     with pytest.raises(RuntimeError, match="features_dc"):
         g._gsplat_core.sh_camera_colors_forward(1, {"means": z(1, 4, 3), "viewmats": z(1, 1, 4, 4),
                                                     "features_dc": z(1, 5, 3), "features_rest": z(1, 4, 3, 3)})
+
+
+# With the projection's radii, the forward skips the rows that no camera
+# sees (radii not both positive in any camera: no tile, so no render reads
+# them): colour 0. Every other row runs the same arithmetic as without radii,
+# so its colours agree bit for bit with the unmasked kernel's. Slab and
+# general kernels, one and three cameras, partial and unaligned groups, and
+# the resident-grid walk.
+@pytest.mark.parametrize("degree,B,C,R,N", [(3, 1, 1, 15, 3001), (3, 2, 1, 15, 200001), (3, 1, 3, 15, 3001),
+                                            (1, 2, 2, 3, 3001), (0, 1, 1, 0, 777), (2, 1, 1, 8, 3001),
+                                            (4, 2, 3, 24, 1500), (3, 1, 1, 15, 64)])
+@pytest.mark.parametrize("unseen", [0.37, 0.0, 1.0])
+def test_radii_skip_unseen_rows(degree, B, C, R, N, unseen):
+    g = gsplat()
+    rng = np.random.default_rng(degree * 1000 + B * 100 + C * 10 + int(unseen * 10))
+    means = (rng.normal(size=(B, N, 3)) * 2 + [0, 0, 6]).astype(np.float32)
+    vm, _ = _views(rng, B, C)
+    dc = rng.normal(scale=0.3, size=(B, N, 3)).astype(np.float32)
+    rest = rng.normal(scale=0.1, size=(B, N, R, 3)).astype(np.float32)
+    # radii [B, C, N, 2]: unseen rows get zero or one-sided radii in every
+    # camera; seen rows are seen by one random camera at least
+    radii = rng.integers(1, 30, size=(B, C, N, 2)).astype(np.int32)
+    seen_any = rng.random((B, N)) >= unseen
+    for c in range(C):
+        off = ~seen_any | (rng.random((B, N)) < 0.5)
+        kind = rng.integers(0, 3, size=(B, N))
+        radii[:, c, :, 0] = np.where(off & (kind != 1), 0, radii[:, c, :, 0])
+        radii[:, c, :, 1] = np.where(off & (kind != 2), -1 * (kind == 0), radii[:, c, :, 1])
+    first = rng.integers(0, C, size=(B, N))
+    for c in range(C):
+        pick = seen_any & (first == c)
+        radii[:, c][pick] = np.maximum(radii[:, c][pick], 1)
+    seen = ((radii[..., 0] > 0) & (radii[..., 1] > 0)).any(axis=1)  # [B, N]
+    assert (seen == seen_any).all()
+    base = {"means": dev(means), "viewmats": dev(vm), "features_dc": dev(dc), "features_rest": dev(rest)}
+    masked = dict(base, radii=dev(radii))
+    print(f"sh camera radii skip: degree={degree} B={B} C={C} R={R} N={N} unseen={unseen}", flush=True)
+    full = host(g._gsplat_core.sh_camera_colors_forward(degree, base))
+    part = host(g._gsplat_core.sh_camera_colors_forward(degree, masked))
+    exp = np.where(seen[:, None, :, None], full, 0.0)
+    np.testing.assert_array_equal(part, exp)
