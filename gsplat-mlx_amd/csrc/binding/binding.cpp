@@ -380,6 +380,25 @@ py::dict sh_camera_colors_backward(int degrees_to_use, const TensorMap& inputs, 
   return r;
 }
 
+// The packed layout's camera colours: inputs as above plus "rank" (the
+// packed projection's count workspace); the forward returns [nnz, 3] rows.
+at::Tensor sh_camera_colors_packed_forward(int degrees_to_use, const TensorMap& inputs, int64_t nnz) {
+  return gsplat_core::gsplat_sh_camera_colors_packed_forward(
+      degrees_to_use, require_key(inputs, "means"), require_key(inputs, "viewmats"), require_key(inputs, "features_dc"),
+      require_key(inputs, "features_rest"), require_key(inputs, "rank"), nnz);
+}
+
+py::dict sh_camera_colors_packed_backward(int degrees_to_use, const TensorMap& inputs, const TensorMap& cotangents) {
+  auto out = gsplat_core::gsplat_sh_camera_colors_packed_backward(
+      degrees_to_use, require_key(inputs, "means"), require_key(inputs, "viewmats"), require_key(inputs, "features_dc"),
+      require_key(inputs, "features_rest"), require_key(inputs, "rank"), require_key(cotangents, "v_colors"));
+  py::dict r;
+  r["v_means"] = out[0];
+  r["v_features_dc"] = out[1];
+  r["v_features_rest"] = out[2];
+  return r;
+}
+
 // Training-step glue fused into kernels (additions to the reference surface;
 // see gsplat_training_glue.h).
 py::dict gaussian_activations_forward(const TensorMap& inputs) {
@@ -685,6 +704,10 @@ PYBIND11_MODULE(_gsplat_core, m) {
   m.def("spherical_harmonics_backward", &spherical_harmonics_backward, py::arg("degrees_to_use"), py::arg("inputs"),
         py::arg("cotangents"), py::arg("compute_v_dirs") = true);
   m.def("sh_camera_colors_forward", &sh_camera_colors_forward, py::arg("degrees_to_use"), py::arg("inputs"));
+  m.def("sh_camera_colors_packed_forward", &sh_camera_colors_packed_forward, py::arg("degrees_to_use"),
+        py::arg("inputs"), py::arg("nnz"));
+  m.def("sh_camera_colors_packed_backward", &sh_camera_colors_packed_backward, py::arg("degrees_to_use"),
+        py::arg("inputs"), py::arg("cotangents"));
   m.def("sh_camera_colors_backward", &sh_camera_colors_backward, py::arg("degrees_to_use"), py::arg("inputs"),
         py::arg("cotangents"));
   m.def("gaussian_activations_forward", &gaussian_activations_forward, py::arg("inputs"));

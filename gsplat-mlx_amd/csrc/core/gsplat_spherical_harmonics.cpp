@@ -107,6 +107,63 @@ std::vector<array> gsplat_sh_camera_colors_backward(int degree, const array& mea
   return {v_means, v_dc, v_rest};
 }
 
+namespace {
+
+// The packed count workspace (uint8, the packed projection's "rank" output)
+// and the packed row count of the packed camera colour functions.
+void check_packed_rank(const array& rank, int64_t nnz, const CamDims& d, const array& means, const char* what) {
+  const std::string o(what);
+  if (rank.scalar_type() != at::kByte || rank.dim() != 1)
+    throw std::runtime_error(o + ": rank must be the packed projection's uint8 workspace.");
+  if (rank.device() != means.device()) throw std::runtime_error(o + ": rank must be on the means' device.");
+  if (nnz < 0 || nnz > d.B * d.C * d.N) throw std::runtime_error(o + ": invalid packed row count.");
+}
+
+}  // namespace
+
+array gsplat_sh_camera_colors_packed_forward(int degree, const array& means_in, const array& viewmats_in,
+                                             const array& dc_in, const array& rest_in, const array& rank_in,
+                                             int64_t nnz, StreamOrDevice s) {
+  const char* what = "sh_camera_colors_packed_forward";
+  const CamDims d = validate_camera(what, degree, means_in, viewmats_in, dc_in, rest_in);
+  check_packed_rank(rank_in, nnz, d, means_in, what);
+  const c10::DeviceGuard guard(means_in.device());
+  const array means = contig(means_in), viewmats = contig(viewmats_in), dc = contig(dc_in), rest = contig(rest_in);
+  const array rank = contig(rank_in);
+  array rows = at::empty({nnz, 3}, f32_like(means));
+  check(gsplat_hip_sh_camera_colors_packed_fwd(
+      degree, means.data_ptr<float>(), viewmats.data_ptr<float>(), dc.data_ptr<float>(),
+      d.R > 0 ? rest.data_ptr<float>() : nullptr, rank.numel() ? rank.data_ptr<uint8_t>() : nullptr,
+      static_cast<size_t>(rank.numel()), nnz, d.B, d.C, d.N, d.R, rows.data_ptr<float>(), stream_for(s, means)));
+  return rows;
+}
+
+std::vector<array> gsplat_sh_camera_colors_packed_backward(int degree, const array& means_in,
+                                                           const array& viewmats_in, const array& dc_in,
+                                                           const array& rest_in, const array& rank_in,
+                                                           const array& v_rows_in, StreamOrDevice s) {
+  const char* what = "sh_camera_colors_packed_backward";
+  const CamDims d = validate_camera(what, degree, means_in, viewmats_in, dc_in, rest_in);
+  const int64_t nnz = v_rows_in.dim() == 2 ? v_rows_in.size(0) : -1;
+  if (nnz < 0 || v_rows_in.size(1) != 3 || v_rows_in.scalar_type() != at::kFloat)
+    throw std::runtime_error(std::string(what) + ": v_colors must have shape [nnz, 3] (float32).");
+  require_device(v_rows_in, "v_colors");
+  check_packed_rank(rank_in, nnz, d, means_in, what);
+  const c10::DeviceGuard guard(means_in.device());
+  const array means = contig(means_in), viewmats = contig(viewmats_in), dc = contig(dc_in), rest = contig(rest_in);
+  const array rank = contig(rank_in), v_rows = contig(v_rows_in);
+  array v_means = at::empty(means.sizes(), f32_like(means));
+  array v_dc = at::empty(dc.sizes(), f32_like(means));
+  array v_rest = at::empty(rest.sizes(), f32_like(means));
+  check(gsplat_hip_sh_camera_colors_packed_bwd(
+      degree, means.data_ptr<float>(), viewmats.data_ptr<float>(), dc.data_ptr<float>(),
+      d.R > 0 ? rest.data_ptr<float>() : nullptr, rank.numel() ? rank.data_ptr<uint8_t>() : nullptr,
+      static_cast<size_t>(rank.numel()), nnz ? v_rows.data_ptr<float>() : nullptr, nnz, d.B, d.C, d.N, d.R,
+      v_means.data_ptr<float>(), v_dc.data_ptr<float>(), d.R > 0 ? v_rest.data_ptr<float>() : nullptr,
+      stream_for(s, means)));
+  return {v_means, v_dc, v_rest};
+}
+
 array gsplat_spherical_harmonics_forward(const SphericalHarmonicsInput& input) {
   if (input.dirs.scalar_type() != at::kFloat || input.coeffs.scalar_type() != at::kFloat)
     throw std::runtime_error("spherical_harmonics_forward currently supports float32 dirs and coeffs.");

@@ -55,4 +55,19 @@ std::vector<array> gsplat_sh_camera_colors_backward(int degree, const array& mea
                                                     const array& features_dc, const array& features_rest,
                                                     const array& v_colors, StreamOrDevice s = {});
 
+// The camera colours of the packed layout's pairs: rank is the packed
+// projection's count workspace (its "rank" output: one bit per (b, c, n)
+// pair and per-word packed-row prefixes) and nnz its row count. The forward
+// returns [nnz, 3], each visible pair's colour as above at its packed row;
+// the backward takes the rows' cotangents [nnz, 3] and returns {v_means,
+// v_features_dc, v_features_rest} as above for the dense cotangents with
+// zeros at the pairs without a row.
+array gsplat_sh_camera_colors_packed_forward(int degree, const array& means, const array& viewmats,
+                                             const array& features_dc, const array& features_rest,
+                                             const array& rank, int64_t nnz, StreamOrDevice s = {});
+std::vector<array> gsplat_sh_camera_colors_packed_backward(int degree, const array& means, const array& viewmats,
+                                                           const array& features_dc, const array& features_rest,
+                                                           const array& rank, const array& v_rows,
+                                                           StreamOrDevice s = {});
+
 }  // namespace gsplat_core

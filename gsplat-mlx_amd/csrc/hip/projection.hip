@@ -23,6 +23,7 @@
 // also writes the sigmoid opacities the rasterizer takes; the backward maps
 // the quaternion and scale gradients through the activations and turns the
 // rasterizer's opacity gradient into the logits' gradient.
+#include "packed_ranks.hpp"
 #include "projection_common.hpp"
 #include "scan.hpp"
 
@@ -149,12 +150,6 @@ __global__ void __launch_bounds__(kProjBlock) projection_fwd_kernel(
 // writes them at prefix[word] + popcount(bits below). The same bit words and
 // prefixes ("rank structure", 3/16 byte per pair) let the backward find a
 // pair's packed row without a dense index map.
-__device__ __forceinline__ int64_t packed_rank(const uint64_t* __restrict__ mask, const int32_t* __restrict__ prefix,
-                                               int64_t idx) {
-  const uint64_t w = mask[idx >> 6];
-  const int bit = static_cast<int>(idx & 63);
-  return static_cast<int64_t>(prefix[idx >> 6]) + __popcll(w & ((1ull << bit) - 1ull));
-}
 
 // ACT: raw parameters, as the activated projection (project_pair<true>).
 template <bool ACT>
@@ -450,11 +445,13 @@ struct PackedLayout {
   int64_t n_words;
 };
 
+// The rank structure (packed_ranks.hpp: words, then prefixes) first, then
+// the scan's workspace and the view-matrix partials.
 static size_t packed_layout(int64_t B, int64_t C, int64_t N, bool vm, PackedLayout* l, void* base) {
   const int64_t total = B * C * N;
   const int64_t nw = (total + 63) / 64;
-  const size_t mask_b = align256(static_cast<size_t>(nw) * 8);
-  const size_t pre_b = align256(static_cast<size_t>(nw) * 4);
+  const size_t mask_b = packed_ranks_align(static_cast<size_t>(nw) * 8);
+  const size_t pre_b = packed_ranks_align(static_cast<size_t>(nw) * 4);
   const size_t scan_b = align256(scan_workspace_bytes(nw));
   const size_t part_b = vm && C > 0 ? static_cast<size_t>(B * C) * grid_for(N, kProjBlock) * 12 * sizeof(float) : 0;
   if (l && base) {

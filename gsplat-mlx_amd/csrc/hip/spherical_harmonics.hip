@@ -14,6 +14,7 @@
 #include <atomic>
 
 #include "common.hpp"
+#include "packed_ranks.hpp"
 
 namespace gsplat_hip {
 namespace {
@@ -462,14 +463,16 @@ __device__ __forceinline__ bool seen_by_any(const int32_t* __restrict__ radii, i
   return seen;
 }
 
-template <int DEG>
+// radii: rows no camera sees get colour 0; PK: colours go to the pairs'
+// packed rows (packed_ranks.hpp), pairs without one write nothing.
+template <int DEG, bool PK>
 __global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __restrict__ means,
                                                               const float* __restrict__ viewmats,
                                                               const float* __restrict__ dc,
                                                               const float* __restrict__ rest,
-                                                              const int32_t* __restrict__ radii, int64_t C, int64_t N,
-                                                              int64_t R, uint32_t r3_magic,
-                                                              float* __restrict__ colors) {
+                                                              const int32_t* __restrict__ radii, PackedRanks pk,
+                                                              int64_t nnz, int64_t C, int64_t N, int64_t R,
+                                                              uint32_t r3_magic, float* __restrict__ colors) {
   constexpr int A = (DEG + 1) * (DEG + 1);
   constexpr int PW = padded(A * 3);
   __shared__ float sc[kShBlock * PW];
@@ -489,10 +492,14 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __res
   if (t >= cnt) return;
   const int64_t g = b * N + e0 + t;
   const float* co = sc + t * PW;
-  // rows no camera sees (with radii) get colour 0
-  const bool live = !radii || seen_by_any(radii, b, C, N, e0 + t);
+  const bool live = PK || !radii || seen_by_any(radii, b, C, N, e0 + t);
   for (int64_t c = 0; c < C; ++c) {
     float* out = colors + ((b * C + c) * N + e0 + t) * 3;
+    if constexpr (PK) {
+      const int64_t rc = packed_row(pk.mask, pk.prefix, (b * C + c) * N + e0 + t, nnz);
+      if (rc < 0) continue;
+      out = colors + rc * 3;
+    }
     if (!live) {
       out[0] = out[1] = out[2] = 0.0f;
       continue;
@@ -508,12 +515,15 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_fwd_kernel(const float* __res
   }
 }
 
-template <int DEG>
+// PK: v_colors holds the packed rows, read at each pair's row (pairs
+// without one have a zero cotangent).
+template <int DEG, bool PK>
 __global__ void __launch_bounds__(kShBlock) sh_cam_bwd_kernel(const float* __restrict__ means,
                                                               const float* __restrict__ viewmats,
                                                               const float* __restrict__ dc,
                                                               const float* __restrict__ rest,
-                                                              const float* __restrict__ v_colors, int64_t C, int64_t N,
+                                                              const float* __restrict__ v_colors, PackedRanks pk,
+                                                              int64_t nnz, int64_t C, int64_t N,
                                                               int64_t R, uint32_t r3_magic,
                                                               float* __restrict__ v_means, float* __restrict__ v_dc,
                                                               float* __restrict__ v_rest) {
@@ -547,11 +557,16 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_bwd_kernel(const float* __res
       const float norm = view_dir(means + g * 3, cp, d, n);
       sh_eval<DEG>(n, co, raw);
       const float* vc = v_colors + ((b * C + c) * N + e0 + t) * 3;
+      if constexpr (PK) {
+        const int64_t rc = packed_row(pk.mask, pk.prefix, (b * C + c) * N + e0 + t, nnz);
+        vc = rc >= 0 ? v_colors + rc * 3 : nullptr;
+      }
       float gcol[3];
 #pragma unroll
       for (int ch = 0; ch < 3; ++ch) {
         const float x = raw[ch] + 0.5f;
-        gcol[ch] = (x > 0.0f && x < 1.0f) ? vc[ch] : 0.0f;
+        gcol[ch] = 0.0f;
+        if (x > 0.0f && x < 1.0f && (!PK || vc)) gcol[ch] = vc[ch];
       }
       float basis[A];
       sh_basis<DEG>(n[0], n[1], n[2], basis);
@@ -666,14 +681,18 @@ __device__ __forceinline__ void slab_rows(const float* __restrict__ means, const
 // (seen_by_any) are neither read nor evaluated: their colours are written as
 // 0, and a float4 of the rest span is loaded only when it holds a float of
 // a seen row. The rasterizer reads no such row, so the render is unchanged.
-// With one camera the radii are loaded one group ahead of the rows they
-// select.
-template <int DEG>
+// PK (the packed layout): the rank structure (packed_ranks.hpp) selects the
+// pairs instead, and each pair's colour is written at its packed row of
+// `colors` ([nnz, 3]); pairs without a row write nothing. With one camera
+// the selection (radii, or the pair's rank word and prefix) is loaded one
+// group ahead of the rows it selects.
+template <int DEG, bool PK>
 __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* __restrict__ means,
                                                                   const float* __restrict__ viewmats,
                                                                   const float* __restrict__ dc,
                                                                   const float* __restrict__ rest,
-                                                                  const int32_t* __restrict__ radii, int64_t C,
+                                                                  const int32_t* __restrict__ radii,
+                                                                  PackedRanks pk, int64_t nnz, int64_t C,
                                                                   int64_t N, float* __restrict__ colors) {
   constexpr int A = (DEG + 1) * (DEG + 1);
   constexpr int R3 = (A - 1) * 3;
@@ -686,23 +705,48 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
   const int wave = threadIdx.x / kWave;
   const int64_t n_groups = (N + kWave - 1) / kWave;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * (kShSlab / kWave);
+  const bool select = PK || radii != nullptr;
   float* sw = s_rest + wave * kWave * R3;
   auto span = [&](int64_t grp) { return rest + (b * N + grp * kWave) * R3; };
   auto vec_ok = [&](int64_t grp) {
     return R3 > 0 && N - grp * kWave >= kWave && (reinterpret_cast<uintptr_t>(span(grp)) & 15) == 0;
   };
-  // radii of this lane's row of a group (one camera: held one group ahead)
+  // one camera: the selection of this lane's row of a group, held a group
+  // ahead (radii, or the rank word and prefix of the pair)
   int2 rad = make_int2(0, 0);
-  auto fetch_rad = [&](int64_t grp) {
+  uint64_t pw = 0;
+  int32_t pp = 0;
+  auto fetch_sel = [&](int64_t grp) {
     const int64_t n = grp * kWave + lane;
-    if (radii && C == 1 && n < N) rad = *reinterpret_cast<const int2*>(radii + (b * N + n) * 2);
+    if (C != 1 || n >= N) return;
+    if constexpr (PK) {
+      pw = pk.mask[(b * N + n) >> 6];
+      pp = pk.prefix[(b * N + n) >> 6];
+    } else {
+      if (radii) rad = *reinterpret_cast<const int2*>(radii + (b * N + n) * 2);
+    }
   };
   // the group's rows that some camera sees, as a wave mask (every row
-  // without radii); one camera reads the radii fetch_rad loaded
-  auto seen_rows = [&](int64_t grp) -> uint64_t {
-    if (!radii) return ~0ull;
+  // without a selection); with one camera it reads what fetch_sel loaded
+  // and (PK) leaves the lane's packed row in *row
+  auto seen_rows = [&](int64_t grp, int64_t* row) -> uint64_t {
+    if (!select) return ~0ull;
     const int64_t n = grp * kWave + lane;
-    const bool seen = n < N && (C == 1 ? (rad.x > 0) & (rad.y > 0) : seen_by_any(radii, b, C, N, n));
+    bool seen = false;
+    if (n < N) {
+      if constexpr (PK) {
+        if (C == 1) {
+          const int bit = static_cast<int>((b * N + n) & 63);
+          const int64_t r = static_cast<int64_t>(pp) + __popcll(pw & ((1ull << bit) - 1ull));
+          seen = ((pw >> bit) & 1ull) && r < nnz;
+          *row = seen ? r : -1;
+        } else {
+          for (int64_t c = 0; c < C; ++c) seen = seen | (packed_row(pk.mask, pk.prefix, (b * C + c) * N + n, nnz) >= 0);
+        }
+      } else {
+        seen = C == 1 ? (rad.x > 0) & (rad.y > 0) : seen_by_any(radii, b, C, N, n);
+      }
+    }
     return __ballot(seen);
   };
   // the group's rest span (clamped: every lane loads PER float4s of it);
@@ -730,21 +774,23 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
   float4 r[PER];
   float p[6];
   uint64_t seen_next = 0;
+  int64_t row_next = -1;  // PK, one camera: the lane's packed row
   int64_t grp = static_cast<int64_t>(blockIdx.x) * (kShSlab / kWave) + wave;
   if (grp < n_groups) {
-    fetch_rad(grp);
-    seen_next = seen_rows(grp);
+    fetch_sel(grp);
+    seen_next = seen_rows(grp, &row_next);
     fetch_row(grp, seen_next, p);
     if (vec_ok(grp)) {
 #pragma clang loop unroll(full)
       for (int i = 0; i < PER; ++i) r[i] = fetch(grp, i, seen_next, lane);
     }
-    if (grp + stride < n_groups) fetch_rad(grp + stride);
+    if (grp + stride < n_groups) fetch_sel(grp + stride);
   }
   for (; grp < n_groups; grp += stride) {
     const int64_t w0 = grp * kWave;
     const int rows = static_cast<int>(min<int64_t>(kWave, N - w0));
     const uint64_t seen = seen_next;
+    const int64_t row = row_next;
     const bool active = lane < rows;
     const bool live = (seen >> lane) & 1ull;
     float co[A * 3], m[3];
@@ -776,7 +822,7 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
       }
     }
     if (grp + stride < n_groups) {  // the next group's loads, in flight during the compute
-      seen_next = seen_rows(grp + stride);
+      seen_next = seen_rows(grp + stride, &row_next);
       fetch_row(grp + stride, seen_next, p);
       if (vec_ok(grp + stride)) {
         // the lane index is opaque here, so the loop does not hoist the
@@ -786,14 +832,21 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
 #pragma clang loop unroll(full)
         for (int i = 0; i < PER; ++i) r[i] = fetch(grp + stride, i, seen_next, ln);
       }
-      if (grp + 2 * stride < n_groups) fetch_rad(grp + 2 * stride);
+      if (grp + 2 * stride < n_groups) fetch_sel(grp + 2 * stride);
     }
-    if (active) {
+    if (active && (PK ? live : true)) {
       for (int64_t c = 0; c < C; ++c) {
-        float* out = colors + ((b * C + c) * N + w0 + lane) * 3;
-        if (!live) {
-          out[0] = out[1] = out[2] = 0.0f;
-          continue;
+        float* out;
+        if constexpr (PK) {
+          const int64_t rc = C == 1 ? row : packed_row(pk.mask, pk.prefix, (b * C + c) * N + w0 + lane, nnz);
+          if (rc < 0) continue;
+          out = colors + rc * 3;
+        } else {
+          out = colors + ((b * C + c) * N + w0 + lane) * 3;
+          if (!live) {
+            out[0] = out[1] = out[2] = 0.0f;
+            continue;
+          }
         }
         float cp[3];
         camera_centre(viewmats + (b * C + c) * 16, cp);
@@ -827,11 +880,14 @@ int resident_blocks(int block) {
   return cached[dev].load(std::memory_order_relaxed);
 }
 
-template <int DEG>
+// PK (the packed layout): v_colors holds the packed rows ([nnz, 3]), read
+// at each pair's row through the rank structure; pairs without a row have a
+// zero cotangent.
+template <int DEG, bool PK>
 __global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
     const float* __restrict__ means, const float* __restrict__ viewmats, const float* __restrict__ dc,
-    const float* __restrict__ rest, const float* __restrict__ v_colors, int64_t C, int64_t N,
-    float* __restrict__ v_means, float* __restrict__ v_dc, float* __restrict__ v_rest) {
+    const float* __restrict__ rest, const float* __restrict__ v_colors, PackedRanks pk, int64_t nnz, int64_t C,
+    int64_t N, float* __restrict__ v_means, float* __restrict__ v_dc, float* __restrict__ v_rest) {
   constexpr int A = (DEG + 1) * (DEG + 1);
   constexpr int R3 = (A - 1) * 3;
   __shared__ __align__(16) float s_rest[R3 > 0 ? kShSlab * R3 : 4];
@@ -856,11 +912,16 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
       const float norm = view_dir(m, cp, d, n);
       sh_eval<DEG>(n, co, raw);
       const float* vc = v_colors + ((b * C + c) * N + e0 + t) * 3;
+      if constexpr (PK) {
+        const int64_t rc = packed_row(pk.mask, pk.prefix, (b * C + c) * N + e0 + t, nnz);
+        vc = rc >= 0 ? v_colors + rc * 3 : nullptr;
+      }
       float gcol[3];
 #pragma clang loop unroll(full)
       for (int ch = 0; ch < 3; ++ch) {
         const float x = raw[ch] + 0.5f;
-        gcol[ch] = (x > 0.0f && x < 1.0f) ? vc[ch] : 0.0f;
+        gcol[ch] = 0.0f;
+        if (x > 0.0f && x < 1.0f && (!PK || vc)) gcol[ch] = vc[ch];
       }
       float basis[A];
       sh_basis<DEG>(n[0], n[1], n[2], basis);
@@ -903,55 +964,74 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
 // float count (degrees 0, 1, 3); other layouts take the general kernels.
 constexpr bool slab_degree(int deg) { return deg == 0 || deg == 1 || deg == 3; }
 
-template <int DEG>
-int launch_cam_fwd(const float* means, const float* viewmats, const float* dc, const float* rest, const int32_t* radii,
-                   int64_t B, int64_t C, int64_t N, int64_t R, float* colors, hipStream_t s) {
-  {
-    KernelTimer timer("sh_camera_fwd", s);
-    bool slab = false;
-    if constexpr (slab_degree(DEG)) {
-      if (R == (DEG + 1) * (DEG + 1) - 1) {
-        // a resident grid (each wave walks several groups), at most one wave per group
-        const int64_t blocks = grid_for(grid_for(N, kWave), kShSlab / kWave);
-        const int res = resident_blocks<sh_cam_fwd_slab_kernel<DEG>>(kShSlab);
-        const int64_t per_batch = res > 0 ? std::max<int64_t>(1, res / B) : blocks;
-        const dim3 grid(static_cast<unsigned>(std::min<int64_t>(blocks, per_batch)), static_cast<unsigned>(B));
-        sh_cam_fwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, radii, C, N, colors);
-        slab = true;
-      }
+// pk.mask set: the packed layout (PK kernels; colors / v_colors are the
+// nnz packed rows).
+template <int DEG, bool PK>
+int launch_cam_fwd_t(const float* means, const float* viewmats, const float* dc, const float* rest,
+                     const int32_t* radii, PackedRanks pk, int64_t nnz, int64_t B, int64_t C, int64_t N, int64_t R,
+                     float* colors, hipStream_t s) {
+  bool slab = false;
+  if constexpr (slab_degree(DEG)) {
+    if (R == (DEG + 1) * (DEG + 1) - 1) {
+      // a resident grid (each wave walks several groups), at most one wave per group
+      const int64_t blocks = grid_for(grid_for(N, kWave), kShSlab / kWave);
+      const int res = resident_blocks<sh_cam_fwd_slab_kernel<DEG, PK>>(kShSlab);
+      const int64_t per_batch = res > 0 ? std::max<int64_t>(1, res / B) : blocks;
+      const dim3 grid(static_cast<unsigned>(std::min<int64_t>(blocks, per_batch)), static_cast<unsigned>(B));
+      sh_cam_fwd_slab_kernel<DEG, PK><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, radii, pk, nnz, C, N,
+                                                               colors);
+      slab = true;
     }
-    if (!slab) {
-      const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
-      sh_cam_fwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, viewmats, dc, rest, radii, C, N, R,
-                                                        magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), colors);
-    }
+  }
+  if (!slab) {
+    const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
+    sh_cam_fwd_kernel<DEG, PK><<<grid, kShBlock, 0, s>>>(means, viewmats, dc, rest, radii, pk, nnz, C, N, R,
+                                                         magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), colors);
   }
   return check_launch("sh_camera_colors_forward");
 }
 
 template <int DEG>
-int launch_cam_bwd(const float* means, const float* viewmats, const float* dc, const float* rest, const float* v_colors,
-                   int64_t B, int64_t C, int64_t N, int64_t R, float* v_means, float* v_dc, float* v_rest,
+int launch_cam_fwd(const float* means, const float* viewmats, const float* dc, const float* rest, const int32_t* radii,
+                   PackedRanks pk, int64_t nnz, int64_t B, int64_t C, int64_t N, int64_t R, float* colors,
                    hipStream_t s) {
-  {
-    KernelTimer timer("sh_camera_bwd", s);
-    bool slab = false;
-    if constexpr (slab_degree(DEG)) {
-      if (R == (DEG + 1) * (DEG + 1) - 1) {
-        const dim3 grid(grid_for(N, kShSlab), static_cast<unsigned>(B));
-        sh_cam_bwd_slab_kernel<DEG><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, v_colors, C, N, v_means, v_dc,
-                                                              v_rest);
-        slab = true;
-      }
-    }
-    if (!slab) {
-      const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
-      sh_cam_bwd_kernel<DEG><<<grid, kShBlock, 0, s>>>(means, viewmats, dc, rest, v_colors, C, N, R,
-                                                        magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), v_means,
-                                                        v_dc, v_rest);
+  KernelTimer timer("sh_camera_fwd", s);
+  if (pk.mask) return launch_cam_fwd_t<DEG, true>(means, viewmats, dc, rest, nullptr, pk, nnz, B, C, N, R, colors, s);
+  return launch_cam_fwd_t<DEG, false>(means, viewmats, dc, rest, radii, pk, nnz, B, C, N, R, colors, s);
+}
+
+template <int DEG, bool PK>
+int launch_cam_bwd_t(const float* means, const float* viewmats, const float* dc, const float* rest,
+                     const float* v_colors, PackedRanks pk, int64_t nnz, int64_t B, int64_t C, int64_t N, int64_t R,
+                     float* v_means, float* v_dc, float* v_rest, hipStream_t s) {
+  bool slab = false;
+  if constexpr (slab_degree(DEG)) {
+    if (R == (DEG + 1) * (DEG + 1) - 1) {
+      const dim3 grid(grid_for(N, kShSlab), static_cast<unsigned>(B));
+      sh_cam_bwd_slab_kernel<DEG, PK><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, v_colors, pk, nnz, C, N,
+                                                               v_means, v_dc, v_rest);
+      slab = true;
     }
   }
+  if (!slab) {
+    const dim3 grid(grid_for(N, kShBlock), static_cast<unsigned>(B));
+    sh_cam_bwd_kernel<DEG, PK><<<grid, kShBlock, 0, s>>>(means, viewmats, dc, rest, v_colors, pk, nnz, C, N, R,
+                                                         magic_for(static_cast<uint32_t>(R > 0 ? R * 3 : 1)), v_means,
+                                                         v_dc, v_rest);
+  }
   return check_launch("sh_camera_colors_backward");
+}
+
+template <int DEG>
+int launch_cam_bwd(const float* means, const float* viewmats, const float* dc, const float* rest, const float* v_colors,
+                   PackedRanks pk, int64_t nnz, int64_t B, int64_t C, int64_t N, int64_t R, float* v_means,
+                   float* v_dc, float* v_rest, hipStream_t s) {
+  KernelTimer timer("sh_camera_bwd", s);
+  if (pk.mask)
+    return launch_cam_bwd_t<DEG, true>(means, viewmats, dc, rest, v_colors, pk, nnz, B, C, N, R, v_means, v_dc,
+                                       v_rest, s);
+  return launch_cam_bwd_t<DEG, false>(means, viewmats, dc, rest, v_colors, pk, nnz, B, C, N, R, v_means, v_dc, v_rest,
+                                      s);
 }
 
 template <int DEG>
@@ -1032,24 +1112,73 @@ static int check_cam_args(int32_t degree, int64_t B, int64_t C, int64_t N, int64
   return GSPLAT_OK;
 }
 
-extern "C" int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* viewmats,
-                                               const float* features_dc, const float* features_rest,
-                                               const int32_t* radii, int64_t B, int64_t C, int64_t N, int64_t R,
-                                               float* colors, void* stream) {
-  const char* what = "sh_camera_colors_forward";
+static int cam_fwd_impl(const char* what, int32_t degree, const float* means, const float* viewmats,
+                        const float* features_dc, const float* features_rest, const int32_t* radii, PackedRanks pk,
+                        int64_t nnz, int64_t B, int64_t C, int64_t N, int64_t R, float* colors, void* stream) {
   int rc = check_cam_args(degree, B, C, N, R, what);
   if (rc) return rc;
-  if (B == 0 || C == 0 || N == 0) return GSPLAT_OK;
+  if (B == 0 || C == 0 || N == 0 || (pk.mask && nnz == 0)) return GSPLAT_OK;
   if (!means || !viewmats || !features_dc || (R > 0 && !features_rest) || !colors)
     return invalid(std::string(what) + ": null pointer.");
   hipStream_t s = as_stream(stream);
   switch (degree) {
-    case 0: return launch_cam_fwd<0>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
-    case 1: return launch_cam_fwd<1>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
-    case 2: return launch_cam_fwd<2>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
-    case 3: return launch_cam_fwd<3>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
-    default: return launch_cam_fwd<4>(means, viewmats, features_dc, features_rest, radii, B, C, N, R, colors, s);
+    case 0: return launch_cam_fwd<0>(means, viewmats, features_dc, features_rest, radii, pk, nnz, B, C, N, R, colors, s);
+    case 1: return launch_cam_fwd<1>(means, viewmats, features_dc, features_rest, radii, pk, nnz, B, C, N, R, colors, s);
+    case 2: return launch_cam_fwd<2>(means, viewmats, features_dc, features_rest, radii, pk, nnz, B, C, N, R, colors, s);
+    case 3: return launch_cam_fwd<3>(means, viewmats, features_dc, features_rest, radii, pk, nnz, B, C, N, R, colors, s);
+    default:
+      return launch_cam_fwd<4>(means, viewmats, features_dc, features_rest, radii, pk, nnz, B, C, N, R, colors, s);
   }
+}
+
+static int cam_bwd_impl(const char* what, int32_t degree, const float* means, const float* viewmats,
+                        const float* features_dc, const float* features_rest, const float* v_colors, PackedRanks pk,
+                        int64_t nnz, int64_t B, int64_t C, int64_t N, int64_t R, float* v_means, float* v_features_dc,
+                        float* v_features_rest, void* stream) {
+  int rc = check_cam_args(degree, B, C, N, R, what);
+  if (rc) return rc;
+  if (B == 0 || N == 0) return GSPLAT_OK;
+  if (!means || !features_dc || (R > 0 && (!features_rest || !v_features_rest)) || !v_means || !v_features_dc ||
+      (C > 0 && (!viewmats || (!v_colors && !(pk.mask && nnz == 0)))))
+    return invalid(std::string(what) + ": null pointer.");
+  hipStream_t s = as_stream(stream);
+  switch (degree) {
+    case 0: return launch_cam_bwd<0>(means, viewmats, features_dc, features_rest, v_colors, pk, nnz, B, C, N, R,
+                                     v_means, v_features_dc, v_features_rest, s);
+    case 1: return launch_cam_bwd<1>(means, viewmats, features_dc, features_rest, v_colors, pk, nnz, B, C, N, R,
+                                     v_means, v_features_dc, v_features_rest, s);
+    case 2: return launch_cam_bwd<2>(means, viewmats, features_dc, features_rest, v_colors, pk, nnz, B, C, N, R,
+                                     v_means, v_features_dc, v_features_rest, s);
+    case 3: return launch_cam_bwd<3>(means, viewmats, features_dc, features_rest, v_colors, pk, nnz, B, C, N, R,
+                                     v_means, v_features_dc, v_features_rest, s);
+    default: return launch_cam_bwd<4>(means, viewmats, features_dc, features_rest, v_colors, pk, nnz, B, C, N, R,
+                                      v_means, v_features_dc, v_features_rest, s);
+  }
+}
+
+// The rank structure at the start of a packed count workspace for B * C * N
+// pairs, or an error (mask left null).
+static int cam_packed_ranks(const char* what, const void* count_workspace, size_t count_workspace_bytes, int64_t nnz,
+                            int64_t B, int64_t C, int64_t N, PackedRanks* pk) {
+  *pk = PackedRanks{nullptr, nullptr};
+  if (nnz < 0 || B < 0 || C < 0 || N < 0) return invalid(std::string(what) + ": negative size.");
+  const int64_t total = B * C * N;
+  if (nnz > total) return invalid(std::string(what) + ": more packed rows than pairs.");
+  if (total == 0) return GSPLAT_OK;
+  if (!count_workspace || count_workspace_bytes < packed_ranks_bytes(total)) {
+    set_error(std::string(what) + ": count workspace too small.");
+    return GSPLAT_ERR_WORKSPACE_TOO_SMALL;
+  }
+  *pk = packed_ranks_at(count_workspace, total);
+  return GSPLAT_OK;
+}
+
+extern "C" int gsplat_hip_sh_camera_colors_fwd(int32_t degree, const float* means, const float* viewmats,
+                                               const float* features_dc, const float* features_rest,
+                                               const int32_t* radii, int64_t B, int64_t C, int64_t N, int64_t R,
+                                               float* colors, void* stream) {
+  return cam_fwd_impl("sh_camera_colors_forward", degree, means, viewmats, features_dc, features_rest, radii,
+                      PackedRanks{nullptr, nullptr}, 0, B, C, N, R, colors, stream);
 }
 
 extern "C" int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const float* viewmats,
@@ -1057,24 +1186,34 @@ extern "C" int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* mean
                                                const float* v_colors, int64_t B, int64_t C, int64_t N, int64_t R,
                                                float* v_means, float* v_features_dc, float* v_features_rest,
                                                void* stream) {
-  const char* what = "sh_camera_colors_backward";
-  int rc = check_cam_args(degree, B, C, N, R, what);
+  return cam_bwd_impl("sh_camera_colors_backward", degree, means, viewmats, features_dc, features_rest, v_colors,
+                      PackedRanks{nullptr, nullptr}, 0, B, C, N, R, v_means, v_features_dc, v_features_rest, stream);
+}
+
+extern "C" int gsplat_hip_sh_camera_colors_packed_fwd(int32_t degree, const float* means, const float* viewmats,
+                                                      const float* features_dc, const float* features_rest,
+                                                      const void* count_workspace, size_t count_workspace_bytes,
+                                                      int64_t nnz, int64_t B, int64_t C, int64_t N, int64_t R,
+                                                      float* rows, void* stream) {
+  const char* what = "sh_camera_colors_packed_forward";
+  PackedRanks pk;
+  const int rc = cam_packed_ranks(what, count_workspace, count_workspace_bytes, nnz, B, C, N, &pk);
+  if (rc || !pk.mask) return rc;
+  return cam_fwd_impl(what, degree, means, viewmats, features_dc, features_rest, nullptr, pk, nnz, B, C, N, R, rows,
+                      stream);
+}
+
+extern "C" int gsplat_hip_sh_camera_colors_packed_bwd(int32_t degree, const float* means, const float* viewmats,
+                                                      const float* features_dc, const float* features_rest,
+                                                      const void* count_workspace, size_t count_workspace_bytes,
+                                                      const float* v_rows, int64_t nnz, int64_t B, int64_t C,
+                                                      int64_t N, int64_t R, float* v_means, float* v_features_dc,
+                                                      float* v_features_rest, void* stream) {
+  const char* what = "sh_camera_colors_packed_backward";
+  PackedRanks pk;
+  const int rc = cam_packed_ranks(what, count_workspace, count_workspace_bytes, nnz, B, C, N, &pk);
   if (rc) return rc;
-  if (B == 0 || N == 0) return GSPLAT_OK;
-  if (!means || !features_dc || (R > 0 && (!features_rest || !v_features_rest)) || !v_means || !v_features_dc ||
-      (C > 0 && (!viewmats || !v_colors)))
-    return invalid(std::string(what) + ": null pointer.");
-  hipStream_t s = as_stream(stream);
-  switch (degree) {
-    case 0: return launch_cam_bwd<0>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
-                                     v_features_dc, v_features_rest, s);
-    case 1: return launch_cam_bwd<1>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
-                                     v_features_dc, v_features_rest, s);
-    case 2: return launch_cam_bwd<2>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
-                                     v_features_dc, v_features_rest, s);
-    case 3: return launch_cam_bwd<3>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
-                                     v_features_dc, v_features_rest, s);
-    default: return launch_cam_bwd<4>(means, viewmats, features_dc, features_rest, v_colors, B, C, N, R, v_means,
-                                      v_features_dc, v_features_rest, s);
-  }
+  // without pairs (no cameras) the kernels read no rows: every gradient is 0
+  return cam_bwd_impl(what, degree, means, viewmats, features_dc, features_rest, v_rows, pk, nnz, B, C, N, R, v_means,
+                      v_features_dc, v_features_rest, stream);
 }

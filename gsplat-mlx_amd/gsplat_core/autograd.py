@@ -385,6 +385,41 @@ def sh_camera_colors(degrees_to_use, means, viewmats, features_dc, features_rest
     return _ShCameraColors.apply(degrees_to_use, means, viewmats, features_dc, features_rest, radii)
 
 
+class _ShCameraColorsPacked(torch.autograd.Function):
+    """The camera colours of the packed layout's visible pairs: [nnz, 3], row
+    r the colour of pair r (camera_ids / gaussian_ids of the packed
+    projection), as _ShCameraColors computes it. rank is the packed
+    projection's "rank" output (its count workspace), nnz its row count. The
+    colours are written and their cotangents read at the pairs' packed rows,
+    so no dense [B, C, N, 3] colours are formed."""
+
+    @staticmethod
+    def forward(ctx, degrees_to_use, means, viewmats, features_dc, features_rest, rank, nnz):
+        ctx.set_materialize_grads(False)
+        inputs = {"means": means, "viewmats": viewmats, "features_dc": features_dc, "features_rest": features_rest,
+                  "rank": rank}
+        rows = _C.sh_camera_colors_packed_forward(degrees_to_use, inputs, nnz)
+        ctx.save_for_backward(means, viewmats, features_dc, features_rest, rank)
+        ctx.degree = degrees_to_use
+        return rows
+
+    @staticmethod
+    def backward(ctx, v_rows):
+        means, viewmats, features_dc, features_rest, rank = ctx.saved_tensors
+        inputs = {"means": means, "viewmats": viewmats, "features_dc": features_dc, "features_rest": features_rest,
+                  "rank": rank}
+        out = _C.sh_camera_colors_packed_backward(ctx.degree, inputs, {"v_colors": v_rows.contiguous()})
+        return None, out["v_means"], None, out["v_features_dc"], out["v_features_rest"], None, None
+
+
+def sh_camera_colors_packed(degrees_to_use, means, viewmats, features_dc, features_rest, rank, nnz):
+    """Fused camera colours of the packed pairs ([nnz, 3]); viewmats must not
+    require grad."""
+    if viewmats.requires_grad:
+        raise ValueError("sh_camera_colors_packed: view-matrix gradients are not supported; detach viewmats.")
+    return _ShCameraColorsPacked.apply(degrees_to_use, means, viewmats, features_dc, features_rest, rank, int(nnz))
+
+
 class _RasterizeToPixels3DGS(torch.autograd.Function):
     @staticmethod
     def forward(ctx, means2d, conics, colors, opacities, backgrounds, masks, tile_offsets, flatten_ids, image_width,

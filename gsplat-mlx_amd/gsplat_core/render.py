@@ -29,7 +29,7 @@ from . import _gsplat_core as _C
 from .autograd import (activated_projection, activated_projection_packed, image_loss, l1_loss as _l1_loss,
                        packed_rows, projection_ewa_3dgs_fused, rasterize_to_pixels_3dgs, render_rgb,
                        render_rgb_l1_value_and_grad,
-                       sh_camera_colors, spherical_harmonics)
+                       sh_camera_colors, sh_camera_colors_packed, spherical_harmonics)
 
 
 def normalize_quats(quats: torch.Tensor) -> torch.Tensor:
@@ -117,8 +117,10 @@ def _render_sh_packed(means, quats, log_scales, features_dc, features_rest, opac
     """render_sh_model over the packed layout: only the visible (camera,
     Gaussian) pairs are projected, intersected and rasterized."""
     C = viewmats.shape[1]
-    # queued before the projection, whose count read-back then waits on it
-    colors_all = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)  # [1, C, N, 3]
+    fused_colors = not viewmats.requires_grad
+    if not fused_colors:
+        # the reference composition (view-matrix gradients), gathered per row below
+        colors_all = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree)  # [1, C, N, 3]
     # the parameter activations run inside the packed projection's kernels,
     # which also write each row's opacity
     pr = activated_projection_packed(means, quats, log_scales, opacity_logits, viewmats, Ks, width, height,
@@ -134,11 +136,16 @@ def _render_sh_packed(means, quats, log_scales, features_dc, features_rest, opac
         inputs["conics"] = pr["conics"].detach()
         inputs["opacities"] = opac.detach()
     # sorted lists and tile offsets (the tile-bucket path writes the offsets
-    # itself) in two calls around the count read-back: the per-row colour
-    # gather is queued in between, so its host work overlaps the count
-    # kernels
+    # itself) in two calls around the count read-back: the rows' colours are
+    # queued in between, so the GPU evaluates them while the host waits for
+    # the count (written and, in the backward, read at the packed rows
+    # through the projection's rank structure)
     pending = _C.intersect_tile_offsets_begin(inputs, C, tile_size, tw, th)
-    colors = packed_rows(colors_all, pr["batch_ids"], cid, gid, pr["rank"])
+    if fused_colors:
+        colors = sh_camera_colors_packed(sh_degree, means, viewmats.contiguous(), features_dc, features_rest,
+                                         pr["rank"], cid.numel())
+    else:
+        colors = packed_rows(colors_all, pr["batch_ids"], cid, gid, pr["rank"])
     isect = _C.intersect_tile_offsets_end(pending)
     offsets = isect["tile_offsets"]
     bg = background_tensor(background, means.device)

@@ -232,6 +232,30 @@ int gsplat_hip_sh_camera_colors_bwd(int32_t degree, const float* means, const fl
                                     float* v_means, float* v_features_dc, float* v_features_rest,
                                     void* stream);
 
+/* The camera colours of the packed layout's pairs (no counterpart in the
+ * reference; the packed render's SH colours, in place of the dense colours
+ * followed by gsplat_hip_packed_rows_gather / _scatter). count_workspace is
+ * the packed projection count's workspace (its rank structure: one bit per
+ * pair (b, c, n) and per-word packed-row prefixes) and nnz its row count.
+ * The forward writes each visible pair's colour, as
+ * gsplat_hip_sh_camera_colors_fwd computes it, at the pair's packed row of
+ * rows [nnz, 3], and reads only the Gaussians that some camera sees; the
+ * backward reads each pair's colour cotangent at its packed row of v_rows
+ * [nnz, 3] (pairs without a row: zero) and writes v_means, v_features_dc,
+ * v_features_rest as gsplat_hip_sh_camera_colors_bwd does for the dense
+ * cotangents with zeros at the pairs without a row. */
+int gsplat_hip_sh_camera_colors_packed_fwd(int32_t degree, const float* means, const float* viewmats,
+                                           const float* features_dc, const float* features_rest,
+                                           const void* count_workspace, size_t count_workspace_bytes,
+                                           int64_t nnz, int64_t B, int64_t C, int64_t N, int64_t R,
+                                           float* rows, void* stream);
+int gsplat_hip_sh_camera_colors_packed_bwd(int32_t degree, const float* means, const float* viewmats,
+                                           const float* features_dc, const float* features_rest,
+                                           const void* count_workspace, size_t count_workspace_bytes,
+                                           const float* v_rows, int64_t nnz, int64_t B, int64_t C, int64_t N,
+                                           int64_t R, float* v_means, float* v_features_dc,
+                                           float* v_features_rest, void* stream);
+
 /* ---------------------------------------------------------------------------
  * Tile intersection (dense AABB binning).
  * count + exclusive scan: replaces GSPlatIntersectTileCount::eval_gpu

@@ -223,6 +223,43 @@ def test_packed_rows(B, C, K):
     np.testing.assert_array_equal(host(vsp.grad), exp2)
 
 
+@pytest.mark.parametrize("B,C,degree,R,N", [(1, 1, 3, 15, 2500), (1, 3, 3, 15, 2500), (2, 2, 1, 3, 2501),
+                                            (1, 1, 3, 15, 130001), (1, 2, 2, 8, 1500), (2, 1, 0, 0, 777)])
+def test_sh_camera_colors_packed(B, C, degree, R, N):
+    """The packed layout's camera colours (written and read at the pairs'
+    packed rows through the rank structure) equal the dense camera colours
+    gathered at the rows, bit for bit, and their backward equals the dense
+    backward of the rows' cotangents scattered to their slots (zeros
+    elsewhere). Slab and general kernels, one to three cameras, two batches,
+    and the slab forward's resident-grid walk."""
+    import torch
+
+    from gsplat_core.autograd import activated_projection_packed
+
+    rng = np.random.default_rng(B * 100 + C * 10 + degree)
+    means, quats, scales, op, view, Ks = _scene(rng, B, C, N)
+    g = gsplat()
+    out = activated_projection_packed(dev(means), dev(quats), dev(np.log(scales)), None, dev(view), dev(Ks), 320, 240)
+    bid, cid, gid = (host(out[k]) for k in ("batch_ids", "camera_ids", "gaussian_ids"))
+    nnz = cid.size
+    assert 0 < nnz < B * C * N
+    dc = rng.normal(scale=0.3, size=(B, N, 3)).astype(np.float32)
+    rest = rng.normal(scale=0.1, size=(B, N, R, 3)).astype(np.float32)
+    base = {"means": dev(means), "viewmats": dev(view), "features_dc": dev(dc), "features_rest": dev(rest)}
+    print(f"packed sh colours: B={B} C={C} degree={degree} R={R} N={N} nnz={nnz}", flush=True)
+    dense = host(g._gsplat_core.sh_camera_colors_forward(degree, base))
+    rows = host(g._gsplat_core.sh_camera_colors_packed_forward(degree, dict(base, rank=out["rank"]), nnz))
+    np.testing.assert_array_equal(rows, dense[bid, cid, gid])
+    v = rng.normal(size=(nnz, 3)).astype(np.float32)
+    vd = np.zeros((B, C, N, 3), np.float32)
+    vd[bid, cid, gid] = v
+    e = g._gsplat_core.sh_camera_colors_backward(degree, base, {"v_colors": dev(vd)})
+    a = g._gsplat_core.sh_camera_colors_packed_backward(degree, dict(base, rank=out["rank"]), {"v_colors": dev(v)})
+    for k in ("v_means", "v_features_dc", "v_features_rest"):
+        np.testing.assert_array_equal(host(a[k]), host(e[k]), err_msg=k)
+    torch.cuda.synchronize()
+
+
 def _packed_image_ids(rng, layout, I, nnz):
     """Row image ids: grouped by image (the packed projection's order), grouped
     with empty images (first, inner and last), or not grouped (the sorted
