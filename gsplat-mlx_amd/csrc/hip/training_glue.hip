@@ -122,8 +122,13 @@ __global__ void __launch_bounds__(kGlueBlock) l1_final_kernel(const float* __res
                                                               float* __restrict__ loss) {
   __shared__ float s_w[kGlueBlock / kWave];
   const int t = threadIdx.x;
+  constexpr int kPer = kL1Blocks / kGlueBlock;
+  float pv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) pv[j] = t + j * kGlueBlock < parts ? partial[t + j * kGlueBlock] : 0.0f;
   float acc = 0.0f;
-  for (int i = t; i < parts; i += kGlueBlock) acc += partial[i];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) acc += pv[j];
   const float w = wave_sum_uniform(acc);
   if (t % kWave == 0) s_w[t / kWave] = w;
   __syncthreads();
@@ -136,15 +141,29 @@ __global__ void __launch_bounds__(kGlueBlock) l1_final_kernel(const float* __res
 
 __device__ __forceinline__ float sign_of(float x) { return x > 0.0f ? 1.0f : (x < 0.0f ? -1.0f : (x == x ? 0.0f : x)); }
 
+// One float4 of the operands per thread (16-byte accesses when every
+// pointer is aligned; 4-byte ones otherwise).
 __global__ void __launch_bounds__(kGlueBlock) l1_bwd_kernel(const float* __restrict__ a, const float* __restrict__ b,
                                                             int64_t n, const float* __restrict__ grad,
-                                                            float* __restrict__ v_a, float* __restrict__ v_b) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kGlueBlock + threadIdx.x;
-  if (i >= n) return;
+                                                            float* __restrict__ v_a, float* __restrict__ v_b,
+                                                            bool vec) {
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kGlueBlock + threadIdx.x) * 4;
+  if (i0 >= n) return;
   const float g = *grad / static_cast<float>(n);
-  const float v = g * sign_of(a[i] - b[i]);
-  if (v_a) v_a[i] = v;
-  if (v_b) v_b[i] = -v;
+  if (vec && i0 + 4 <= n) {
+    const float4 x = *reinterpret_cast<const float4*>(a + i0);
+    const float4 y = *reinterpret_cast<const float4*>(b + i0);
+    const float4 v = make_float4(g * sign_of(x.x - y.x), g * sign_of(x.y - y.y), g * sign_of(x.z - y.z),
+                                 g * sign_of(x.w - y.w));
+    if (v_a) *reinterpret_cast<float4*>(v_a + i0) = v;
+    if (v_b) *reinterpret_cast<float4*>(v_b + i0) = make_float4(-v.x, -v.y, -v.z, -v.w);
+    return;
+  }
+  for (int64_t i = i0; i < min<int64_t>(n, i0 + 4); ++i) {
+    const float v = g * sign_of(a[i] - b[i]);
+    if (v_a) v_a[i] = v;
+    if (v_b) v_b[i] = -v;
+  }
 }
 
 // Selective Adam (upstream gsplat's fused selective_adam_update,
@@ -247,11 +266,14 @@ extern "C" int gsplat_hip_l1_loss_bwd(const float* a, const float* b, int64_t n,
   if (n < 0) return invalid("l1_loss_backward: negative size.");
   if (n == 0) return GSPLAT_OK;
   if (!a || !b || !grad) return invalid("l1_loss_backward: null input.");
-  if (n > kMaxGridX / 2 * kGlueBlock) return invalid("l1_loss_backward: too many values.");
+  if ((n + 3) / 4 > static_cast<int64_t>(kMaxGridX / 2) * kGlueBlock)
+    return invalid("l1_loss_backward: too many values.");
   hipStream_t s = as_stream(stream);
+  const auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  const bool vec = aligned(a) && aligned(b) && (!v_a || aligned(v_a)) && (!v_b || aligned(v_b));
   {
     KernelTimer timer("l1_loss_bwd", s);
-    l1_bwd_kernel<<<grid_for(n, kGlueBlock), kGlueBlock, 0, s>>>(a, b, n, grad, v_a, v_b);
+    l1_bwd_kernel<<<grid_for((n + 3) / 4, kGlueBlock), kGlueBlock, 0, s>>>(a, b, n, grad, v_a, v_b, vec);
   }
   return check_launch("l1_loss_backward");
 }

@@ -71,8 +71,13 @@ def test_activations_partial_grads():
     del torch
 
 
-@pytest.mark.parametrize("shape", [(1, 840, 1297, 3), (2, 33, 17, 3), (5,)])
-def test_l1_vs_torch(shape):
+# Whole 4096-float tiles of the partial sums with and without a ragged last
+# one, more tiles than partial blocks (35M values: blocks walk several
+# tiles), a tiny input, and operands 4 bytes off 16-byte alignment (the
+# 4-byte paths of both kernels).
+@pytest.mark.parametrize("shape,offset", [((1, 840, 1297, 3), 0), ((2, 33, 17, 3), 0), ((5,), 0),
+                                          ((3, 1001, 17), 0), ((35_000_001,), 0), ((3, 1001, 17), 1)])
+def test_l1_vs_torch(shape, offset):
     import torch
 
     g = gsplat()
@@ -85,6 +90,13 @@ def test_l1_vs_torch(shape):
 
     def run(fn):
         ta, tb = dev(a).requires_grad_(True), dev(b).requires_grad_(True)
+        if offset:  # views one float into a larger buffer: 4-byte aligned only
+            pa, pb = torch.zeros(a.size + offset, device="cuda"), torch.zeros(b.size + offset, device="cuda")
+            pa[offset:] = ta.detach().reshape(-1)
+            pb[offset:] = tb.detach().reshape(-1)
+            ta = pa[offset:].reshape(shape).requires_grad_(True)
+            tb = pb[offset:].reshape(shape).requires_grad_(True)
+            assert ta.data_ptr() % 16 != 0
         loss = fn(ta, tb)
         (loss * 3.0).backward()
         return host(loss), host(ta.grad), host(tb.grad)
