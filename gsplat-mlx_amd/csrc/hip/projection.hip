@@ -49,17 +49,33 @@ __device__ __forceinline__ PairOut project_pair(const float* __restrict__ means,
                                                 const float* __restrict__ opacities, const CamFrame& f, int64_t g,
                                                 const gsplat_projection_params& p) {
   PairOut o = {false, 0, 0, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  // Every input of the pair is loaded before the first test: a culled
+  // pair's later loads are wasted, but the tests no longer wait for a
+  // second and a third round trip to memory.
   const float mw[3] = {means[g * 3], means[g * 3 + 1], means[g * 3 + 2]};
+  float qr[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sr[3] = {0.0f, 0.0f, 0.0f}, cv[6] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  // the activated projection takes quaternions and log-scales only
+  const bool use_covars = !ACT && p.use_covars;
+  if (use_covars) {
+#pragma unroll
+    for (int k = 0; k < 6; ++k) cv[k] = covars[g * 6 + k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) qr[k] = quats[g * 4 + k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) sr[k] = scales[g * 3 + k];
+  }
+  const float op_in = p.use_opacities ? opacities[g] : 0.0f;
   float mc[3];
   world_to_cam(f, mw, mc);
   bool valid = !(mc[2] < p.near_plane || mc[2] > p.far_plane);
   if (!valid) return o;
   Mat3 cw;
-  if (p.use_covars) {
-    cw = read_covar(covars + g * 6);
+  if (use_covars) {
+    cw = read_covar(cv);
   } else {
     float q[4], s[3];
-    load_quat_scale<ACT>(quats, scales, g, q, s);
+    quat_scale_of<ACT>(qr, sr, q, s);
     cw = covar_from_quat_scale(q, s);
   }
   const Mat3 cc = mat3_mul(mat3_mul(f.R, cw), mat3_tr(f.R));
@@ -85,7 +101,7 @@ __device__ __forceinline__ PairOut project_pair(const float* __restrict__ means,
   valid = det > 0.0f;
   float extend = kGaussianExtend;
   if (valid && p.use_opacities) {
-    float op = ACT ? sigmoid_of(opacities[g]) : opacities[g];
+    float op = ACT ? sigmoid_of(op_in) : op_in;
     if (p.calc_compensations) op *= comp;
     valid = !(op < kAlphaThreshold);
     if (valid) extend = fminf(kGaussianExtend, sqrtf(2.0f * logf(op / kAlphaThreshold)));
@@ -125,10 +141,11 @@ __global__ void __launch_bounds__(kProjBlock) projection_fwd_kernel(
   const int64_t g = b * N + n;
   const int64_t idx = cam * N + n;
   const CamFrame f = load_camera(viewmats + cam * 16, Ks + cam * 9);
-  if constexpr (ACT) {
-    if (opac_out && cam == b * C) opac_out[g] = sigmoid_of(opacities[g]);
-  }
+  // the logit is loaded with the pair's inputs, its sigmoid stored after
+  const bool write_opac = ACT && opac_out && cam == b * C;
+  const float logit = write_opac ? opacities[g] : 0.0f;
   const PairOut o = project_pair<ACT>(means, covars, quats, scales, opacities, f, g, p);
+  if (write_opac) opac_out[g] = sigmoid_of(logit);
   radii[idx * 2] = o.rx;
   radii[idx * 2 + 1] = o.ry;
   means2d[idx * 2] = o.m2x;

@@ -74,6 +74,22 @@ __device__ __forceinline__ void load_quat_scale(const float* __restrict__ quats,
   }
 }
 
+// The same from values already loaded (raw quaternion qr, scales or
+// log-scales sr).
+template <bool ACT>
+__device__ __forceinline__ void quat_scale_of(const float qr[4], const float sr[3], float q[4], float s[3]) {
+  if constexpr (ACT) {
+    activate_quat(qr, q);
+#pragma unroll
+    for (int k = 0; k < 3; ++k) s[k] = expf(sr[k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q[k] = qr[k];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) s[k] = sr[k];
+  }
+}
+
 struct CamFrame {
   Mat3 R;
   float t[3];
