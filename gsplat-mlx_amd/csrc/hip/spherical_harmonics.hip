@@ -457,8 +457,8 @@ __device__ __forceinline__ bool seen_by_any(const int32_t* __restrict__ radii, i
                                             int64_t n) {
   bool seen = false;
   for (int64_t c = 0; c < C; ++c) {
-    const int2 r = *reinterpret_cast<const int2*>(radii + ((b * C + c) * N + n) * 2);
-    seen = seen | ((r.x > 0) & (r.y > 0));
+    const int32_t* r = radii + ((b * C + c) * N + n) * 2;  // 4-byte aligned only
+    seen = seen | ((r[0] > 0) & (r[1] > 0));
   }
   return seen;
 }
@@ -723,7 +723,7 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
       pw = pk.mask[(b * N + n) >> 6];
       pp = pk.prefix[(b * N + n) >> 6];
     } else {
-      if (radii) rad = *reinterpret_cast<const int2*>(radii + (b * N + n) * 2);
+      if (radii) rad = make_int2(radii[(b * N + n) * 2], radii[(b * N + n) * 2 + 1]);
     }
   };
   // the group's rows that some camera sees, as a wave mask (every row
