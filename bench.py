@@ -231,7 +231,8 @@ def main():
     # each pixel's last contributor).
     blocks, grid_words = bucket_blocks(NC, N, n_img, tw, th)
     rad = out["radii"].reshape(n_img, N, 2)
-    n_seen = int(((rad[..., 0] > 0) & (rad[..., 1] > 0)).any(dim=0).sum())
+    # the render skips unseen rows' SH colours with one camera only
+    n_seen = int(((rad[..., 0] > 0) & (rad[..., 1] > 0)).any(dim=0).sum()) if n_img == 1 else N
     n_tiles = n_img * tw * th
     units = {
         "raster_bwd": ("flops", BWD_FLOPS_PER_EVAL * e_bwd),
@@ -258,7 +259,7 @@ def main():
         # rows are in no tile list: colour 0), and writes every colour; the
         # backward reads every row and colour cotangent and writes every
         # gradient row
-        "sh_camera_fwd": ("bytes", 8 * NC + (12 + 12 * K) * n_seen + 12 * NC),
+        "sh_camera_fwd": ("bytes", (8 * NC if n_img == 1 else 0) + (12 + 12 * K) * n_seen + 12 * NC),
         "sh_camera_bwd": ("bytes", (24 + 24 * K + 12 * n_img) * N),
         "isect_count_scan": ("bytes", 20 * NC),
         "isect_depth_keys": ("bytes", 12 * NC),

@@ -178,8 +178,11 @@ def render_sh_model(means, quats, log_scales, features_dc, features_rest, opacit
     pending = _intersect_begin(proj, width, height, tile_size, C, opac_img if accutile else None)
     # queued behind the intersection's count read-back: the GPU evaluates the
     # SH colours while the host waits for the count
-    # rows no camera sees are in no tile list: their colours are skipped
-    colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree, radii=proj["radii"])
+    # rows no camera sees are in no tile list: with one camera their colours
+    # are skipped (a prefetched 8-byte test per Gaussian; with C cameras the
+    # test reads C radii per Gaussian and costs more than it saves)
+    colors = sh_colors_for_camera(means, features_dc, features_rest, viewmats, sh_degree,
+                                  radii=proj["radii"] if C == 1 else None)
     isect, offsets = _intersect_end(pending)
     render = rasterize_to_pixels_3dgs(proj["means2d"], proj["conics"], colors, opac_img,
                                       offsets, isect["flatten_ids"], width, height, tile_size, backgrounds=bg)
