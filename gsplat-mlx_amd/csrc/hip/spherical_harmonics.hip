@@ -623,23 +623,26 @@ __global__ void __launch_bounds__(kShBlock) sh_cam_bwd_kernel(const float* __res
 // arithmetic as sh_cam_fwd_kernel / sh_cam_bwd_kernel, so results are
 // identical.
 constexpr int kShSlab = 256;
+// rows (and threads) of a backward slab block (128 and 64 measured slower:
+// 92.6 and 94.9 against 82 us at a million Gaussians, degree 3)
+constexpr int kShBwdRows = 256;
 
 template <int W>
 __device__ __forceinline__ void stage_slab(float* __restrict__ dst, const float* __restrict__ src, int cnt) {
-  if (cnt == kShSlab && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
-    static_assert((kShSlab * W) % 4 == 0, "whole float4s per slab");
-    constexpr int T4 = kShSlab * W / 4;
-    constexpr int PER = (T4 + kShSlab - 1) / kShSlab;
+  if (cnt == kShBwdRows && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    static_assert((kShBwdRows * W) % 4 == 0, "whole float4s per slab");
+    constexpr int T4 = kShBwdRows * W / 4;
+    constexpr int PER = (T4 + kShBwdRows - 1) / kShBwdRows;
     const float4* s4 = reinterpret_cast<const float4*>(src);
     float4* d4 = reinterpret_cast<float4*>(dst);
     // global and LDS do not alias: the compiler hoists every load above the stores
 #pragma clang loop unroll(full)
     for (int i = 0; i < PER; ++i) {
-      const int idx = threadIdx.x + i * kShSlab;
+      const int idx = threadIdx.x + i * kShBwdRows;
       if (idx < T4) d4[idx] = s4[idx];
     }
   } else {
-    for (int idx = threadIdx.x; idx < cnt * W; idx += kShSlab) dst[idx] = src[idx];
+    for (int idx = threadIdx.x; idx < cnt * W; idx += kShBwdRows) dst[idx] = src[idx];
   }
 }
 
@@ -865,18 +868,18 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_fwd_slab_kernel(const float* _
 // at each pair's row through the rank structure; pairs without a row have a
 // zero cotangent.
 template <int DEG, bool PK>
-__global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
+__global__ void __launch_bounds__(kShBwdRows) sh_cam_bwd_slab_kernel(
     const float* __restrict__ means, const float* __restrict__ viewmats, const float* __restrict__ dc,
     const float* __restrict__ rest, const float* __restrict__ v_colors, PackedRanks pk, int64_t nnz, int64_t C,
     int64_t N, float* __restrict__ v_means, float* __restrict__ v_dc, float* __restrict__ v_rest) {
   constexpr int A = (DEG + 1) * (DEG + 1);
   constexpr int R3 = (A - 1) * 3;
-  __shared__ __align__(16) float s_rest[R3 > 0 ? kShSlab * R3 : 4];
-  __shared__ __align__(16) float s_dc[kShSlab * 3];
-  __shared__ __align__(16) float s_m[kShSlab * 3];
+  __shared__ __align__(16) float s_rest[R3 > 0 ? kShBwdRows * R3 : 4];
+  __shared__ __align__(16) float s_dc[kShBwdRows * 3];
+  __shared__ __align__(16) float s_m[kShBwdRows * 3];
   const int64_t b = blockIdx.y;
-  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShSlab;
-  const int cnt = static_cast<int>(min<int64_t>(kShSlab, N - e0));
+  const int64_t e0 = static_cast<int64_t>(blockIdx.x) * kShBwdRows;
+  const int cnt = static_cast<int>(min<int64_t>(kShBwdRows, N - e0));
   const int t = threadIdx.x;
   float co[A * 3], m[3];
   slab_rows<DEG>(means, dc, rest, b * N + e0, cnt, s_rest, s_dc, s_m, co, m);
@@ -931,12 +934,12 @@ __global__ void __launch_bounds__(kShSlab) sh_cam_bwd_slab_kernel(
   if constexpr (R3 > 0) {
     __syncthreads();
     float* out = v_rest + (b * N + e0) * R3;
-    if (cnt == kShSlab && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
+    if (cnt == kShBwdRows && (reinterpret_cast<uintptr_t>(out) & 15) == 0) {
       float4* o4 = reinterpret_cast<float4*>(out);
       const float4* s4 = reinterpret_cast<const float4*>(s_rest);
-      for (int idx = t; idx < kShSlab * R3 / 4; idx += kShSlab) o4[idx] = s4[idx];
+      for (int idx = t; idx < kShBwdRows * R3 / 4; idx += kShBwdRows) o4[idx] = s4[idx];
     } else {
-      for (int idx = t; idx < cnt * R3; idx += kShSlab) out[idx] = s_rest[idx];
+      for (int idx = t; idx < cnt * R3; idx += kShBwdRows) out[idx] = s_rest[idx];
     }
   }
 }
@@ -987,8 +990,8 @@ int launch_cam_bwd_t(const float* means, const float* viewmats, const float* dc,
   bool slab = false;
   if constexpr (slab_degree(DEG)) {
     if (R == (DEG + 1) * (DEG + 1) - 1) {
-      const dim3 grid(grid_for(N, kShSlab), static_cast<unsigned>(B));
-      sh_cam_bwd_slab_kernel<DEG, PK><<<grid, kShSlab, 0, s>>>(means, viewmats, dc, rest, v_colors, pk, nnz, C, N,
+      const dim3 grid(grid_for(N, kShBwdRows), static_cast<unsigned>(B));
+      sh_cam_bwd_slab_kernel<DEG, PK><<<grid, kShBwdRows, 0, s>>>(means, viewmats, dc, rest, v_colors, pk, nnz, C, N,
                                                                v_means, v_dc, v_rest);
       slab = true;
     }
