@@ -184,7 +184,9 @@ extern "C" const char* gsplat_hip_last_error(void) { return gsplat_hip::g_last_e
 // 1.01: ellipse tiles, packed layout, rasterize-to-indices and selective Adam
 // entry points added (additive). 1.02: allocation-free rasterize backward,
 // sort diagnostics and test hooks, exp and LDS probes (additive).
-extern "C" int gsplat_hip_abi_version(void) { return 102; }
+// 200: gsplat_hip_sh_camera_colors_fwd takes the projection's radii (an
+// argument more), the packed camera colours and the packed row kernels added
+extern "C" int gsplat_hip_abi_version(void) { return 200; }
 
 extern "C" void gsplat_hip_profile_enable(int32_t enable) { gsplat_hip::g_profile = enable != 0; }
 

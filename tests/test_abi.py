@@ -41,7 +41,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 def test_version_and_error_plumbing(lib):
     lib.gsplat_hip_abi_version.restype = ctypes.c_int
-    assert lib.gsplat_hip_abi_version() >= 100
+    assert lib.gsplat_hip_abi_version() >= 200  # the SH camera forward takes radii
     lib.gsplat_hip_last_error.restype = ctypes.c_char_p
     lib.gsplat_hip_isect_sort.restype = ctypes.c_int
     lib.gsplat_hip_isect_sort.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
