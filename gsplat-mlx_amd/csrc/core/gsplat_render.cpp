@@ -152,14 +152,15 @@ std::vector<array> gsplat_render_rgb_backward(const RenderRGBInput& in, const st
 namespace {
 
 // A device scalar 1.0 (the loss's own cotangent) per device, created once
-// and never written.
+// and never written. The map is never destroyed: its tensors must not be
+// freed at process exit, after the device runtime may have shut down.
 const array& device_one(const array& like) {
   static std::mutex mu;
-  static std::map<int, array> ones;
+  static auto* ones = new std::map<int, array>();
   const std::lock_guard<std::mutex> lock(mu);
   const int dev = like.device().index();
-  auto it = ones.find(dev);
-  if (it == ones.end()) it = ones.emplace(dev, at::ones({}, f32_like(like))).first;
+  auto it = ones->find(dev);
+  if (it == ones->end()) it = ones->emplace(dev, at::ones({}, f32_like(like))).first;
   return it->second;
 }
 
