@@ -723,7 +723,9 @@ raster_bwd_kernel(
       if (t < BB && b1 - 1 - t >= b0) {
         const uint32_t r_mask = touch_mask(r_xy, r_co, n_waves, s_rect);
         float* rec = s_rec + t * RW;
-        *reinterpret_cast<float4*>(rec) = r_co;
+        // conic diagonal pre-halved, as in the forward (the same sigma bit for
+        // bit); the flush and the absolute gradients double it back exactly
+        *reinterpret_cast<float4*>(rec) = make_float4(0.5f * r_co.x, r_co.y, 0.5f * r_co.z, r_co.w);
         float tail[RW - 4];
 #pragma unroll
         for (int i = 0; i < RW - 4; ++i) tail[i] = 0.0f;
@@ -774,7 +776,7 @@ raster_bwd_kernel(
         const int k_rel = k_rel0 - k;
         f.dx = xc.x - px;
         f.dy = xc.y - py;
-        const float sigma = 0.5f * (co.x * f.dx * f.dx + co.z * f.dy * f.dy) + co.y * f.dx * f.dy;
+        const float sigma = (co.x * f.dx * f.dx + co.z * f.dy * f.dy) + co.y * f.dx * f.dy;  // co.x, co.z pre-halved
         f.vis = exp_alpha(-sigma);
         f.a_raw = co.w * f.vis;
         f.alpha = fminf(kMaxAlpha, f.a_raw);
@@ -834,8 +836,8 @@ raster_bwd_kernel(
         // vis v_alpha = -v_sigma / opacity: the flush divides the sum once
         v[o + 5] = v_sigma;
         if constexpr (ABS) {
-          v[o + 6] = geo ? fabsf(__builtin_fmaf(co.x, hx, co.y * hy)) : 0.0f;
-          v[o + 7] = geo ? fabsf(__builtin_fmaf(co.y, hx, co.z * hy)) : 0.0f;
+          v[o + 6] = geo ? fabsf(__builtin_fmaf(co.x + co.x, hx, co.y * hy)) : 0.0f;
+          v[o + 7] = geo ? fabsf(__builtin_fmaf(co.y, hx, (co.z + co.z) * hy)) : 0.0f;
         }
       };
       auto load = [&](int k, float4& co, float4& xc, float4& ex) {
@@ -917,7 +919,7 @@ raster_bwd_kernel(
           // reach the mean's gradient)
           if (v == 0.0f && v2 == 0.0f) continue;
           const float4 co = *reinterpret_cast<const float4*>(s_rec + slot * RW);
-          v = fl_comp == 0 ? co.x * v + co.y * v2 : co.y * v + co.z * v2;
+          v = fl_comp == 0 ? (co.x + co.x) * v + co.y * v2 : co.y * v + (co.z + co.z) * v2;
         } else if (fl_kind == kFlushOpacity) {
           // sum of v_sigma = -opacity vis v_alpha: the opacity is at least
           // 1/255 wherever a pixel contributed (alpha passed the threshold)
