@@ -91,7 +91,7 @@ class Profiler:
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (every box here has one GPU); "
+        print("bench.py measures one GPU: the library has no multi-GPU path; "
               "run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
@@ -306,7 +306,7 @@ def main():
                         "traffic": measured_traffic(args.workload, dom),
                         "kernel": dom, "avg_ms": round(avg_ms, 4),
                         "note": "compute roofline: FP32 VALU (no MFMA on this path), peak = MI355X FP32 "
-                                "(counts packed FP32, which this build does not use)",
+                                "(counts packed FP32, which these kernels do not use)",
                         "attainable": {"peak": round(att, 2), "frac": round(achieved / att, 4),
                                        "note": "measured FP32 FMA-chain probe (single, not packed, VALU "
                                                "instructions) on this GPU in this run"},

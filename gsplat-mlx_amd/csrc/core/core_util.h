@@ -22,7 +22,7 @@ inline array empty_f32() { return at::empty({0}, at::TensorOptions().dtype(at::k
 inline void require_device(const array& a, const char* name) {
   if (!a.defined() || !a.is_cuda()) {
     throw std::runtime_error(std::string("gsplat_core: ") + name +
-                             " must be a tensor on a ROCm GPU device (this build has no CPU path).");
+                             " must be a tensor on a ROCm GPU device (the library has no CPU path).");
   }
 }
 

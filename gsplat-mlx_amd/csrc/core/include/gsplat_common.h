@@ -1,7 +1,7 @@
 // Common types of the gsplat_core C++ operator API (MI355X build).
 //
 // The reference API (a1091150/gsplat-mlx, gsplat_core/include/*.h) passes
-// mx::array values and an mx::StreamOrDevice. This build keeps the same
+// mx::array values and an mx::StreamOrDevice. This library keeps the same
 // structs, field names and order, with at::Tensor (ROCm device tensors) as
 // the array type and StreamOrDevice naming the HIP stream to enqueue on
 // (default: the caller's current torch stream on the tensors' device).

@@ -7,7 +7,8 @@
 // bench.py does and the tests' build does not). It exists
 // to check the HIP implementation; nothing on the product path may link,
 // load or call it. Only tests/, __graft_entry__.smoke() and bench.py's
-// CPU-baseline leg use it, always as the checker.
+// CPU-baseline leg use it, always as the reference the GPU results are
+// compared with.
 //
 // Every routine is a template over the scalar type so that the float32
 // instantiation reproduces the reference's fp32 arithmetic and the float64
@@ -1516,7 +1517,7 @@ int oracle_set_threads(int n) {
 #endif
 }
 
-// CPU baseline only (never the checker): flush denormal results and inputs
+// CPU baseline only (never for comparisons): flush denormal results and inputs
 // to zero on the calling thread and every OpenMP thread, as a tuned CPU run
 // would; tiny cotangents otherwise make x86 take its slow denormal path in
 // whole stages. Returns 1 where the control exists (x86-64), else 0.

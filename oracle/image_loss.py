@@ -31,7 +31,8 @@ reference's own image_loss_debug.py assertions, and the VJP against central
 finite differences.
 
 Only tests/, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
-``bench.py`` may import this module, and only as the checker.
+``bench.py`` may import this module, and only as the reference that
+results are compared with.
 """
 from __future__ import annotations
 

@@ -8,7 +8,8 @@ empty-output conventions follow the reference binding
 projection culling taken from gsplat_projection.metal:249-326.
 
 Only tests/, ``__graft_entry__.smoke()`` and the CPU-baseline leg of
-``bench.py`` may import this module, and only as the checker.
+``bench.py`` may import this module, and only as the reference that
+results are compared with.
 
 Every function accepts float32 or float64 arrays; float64 inputs select the
 float64 instantiation of the same C++ templates (used by finite-difference
@@ -43,7 +44,7 @@ def lib() -> ctypes.CDLL:
 
 
 def build_native(openmp: bool = False) -> str:
-    """A CPU-baseline build (bench.py only, never a checker): the same
+    """A CPU-baseline build (bench.py only, never for comparisons): the same
     source at -O3 -march=native, with its OpenMP loops when `openmp`,
     compiled on the host that runs it into a file named for that host's CPU
     and the source (a build for another CPU's instruction set, or of another
